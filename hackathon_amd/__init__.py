@@ -1,0 +1,36 @@
+"""MI355X (gfx950) QLoRA training-step kernel set with the reference's Python interface.
+
+Drop-in for the reference's `solution` package (solution/__init__.py:1-34): the same module
+names and function signatures, with every Triton kernel and every torch GEMM of the path
+replaced by hand-written HIP kernels for gfx950 in `libqlora_gfx950.so` (C-ABI declared in
+include/qlora_gfx950.h, bound through ctypes in `_lib`).
+
+  nf4.py            NF4 dequant (+ double-quantised absmax) and the 4-bit linear
+  rmsnorm.py        Qwen2RMSNorm.forward                      fwd + bwd
+  rope.py           modeling_qwen2.apply_rotary_pos_emb        fwd + bwd (q and k in one launch)
+  swiglu.py         Qwen2MLP.forward's silu(gate) * up         fwd + bwd
+  lora.py           4-bit LoRA layer: dropout+cast, adapter GEMMs, scaled add
+  fused_ce.py       chunked lm_head + CE with row selection (fused_head_loss)
+  cross_entropy.py  chunked lm_head + CE installed on Qwen2ForCausalLM.forward
+  quant.py          NF4 storage format: codebook, QuantState, quantizer, Linear4bit
+  gemm.py           the MFMA GEMM behind every contraction of the path
+"""
+
+PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora")
+
+_applied = set()
+
+
+def apply(include_example=True):
+    """Install every patch (idempotent), as solution/__init__.py:22-34 does."""
+    from importlib import import_module
+
+    for name in PATCHES:
+        if name not in _applied:
+            import_module(f"{__name__}.{name}").patch()
+            _applied.add(name)
+    if include_example and "swiglu" not in _applied:
+        from .swiglu import patch_qwen2_mlp
+
+        patch_qwen2_mlp()
+        _applied.add("swiglu")

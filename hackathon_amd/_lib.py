@@ -1,0 +1,123 @@
+"""ctypes binding of libqlora_gfx950.so (the C-ABI declared in include/qlora_gfx950.h).
+
+The library is loaded once, from this package directory only. There is no fallback: if the
+library is missing, every kernel call raises, naming the build command. Each wrapper takes
+torch tensors, checks what the C side cannot (device, dtype tags), and passes raw device
+pointers plus the current HIP stream of the tensor's device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libqlora_gfx950.so"
+
+F32, F16, BF16 = 0, 1, 2
+_DTYPE_TAG = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_ptr = ctypes.c_void_p
+_c_f32 = ctypes.c_float
+_c_u64 = ctypes.c_uint64
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> argtypes; every function returns int (QL_OK = 0)
+_SIGNATURES = {
+    "qlora_nf4_dequant": [_c_ptr, _c_i64, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_f32, _c_int, _c_int,
+                          _c_ptr, _c_ptr, _c_int, _c_ptr],
+    "qlora_rmsnorm_fwd": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_ptr, _c_int, _c_i64, _c_ptr,
+                          _c_i64, _c_i64, _c_f32, _c_ptr],
+    "qlora_rmsnorm_bwd": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_ptr,
+                          _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr],
+    "qlora_rope_qk": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
+                      _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64p,
+                      _c_i64, _c_i64, _c_int, _c_ptr],
+    "qlora_swiglu_fwd": [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_ptr],
+    "qlora_swiglu_bwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_ptr],
+    "qlora_lora_dropout_scale": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64,
+                                 _c_u64, _c_f32, _c_f32, _c_ptr],
+    "qlora_lora_scaled_add": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,
+                              _c_i64, _c_i64, _c_i64, _c_f32, _c_ptr],
+    "qlora_gemm": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int,
+                   _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32, _c_f32, _c_ptr],
+    "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                      _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class KernelLibraryMissing(RuntimeError):
+    pass
+
+
+def load():
+    """The loaded ctypes library (loads it on first use; raises if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise KernelLibraryMissing(
+                f"{LIB_PATH.name} is not built: run `python -m hackathon_amd.build` "
+                f"(expected at {LIB_PATH})")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        lib.qlora_strerror.argtypes = [ctypes.c_int]
+        lib.qlora_strerror.restype = ctypes.c_char_p
+        lib.qlora_abi_version.argtypes = []
+        lib.qlora_abi_version.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def exported_symbols():
+    """Names the binding expects the library to export (used by the ABI tests)."""
+    return sorted(list(_SIGNATURES) + ["qlora_strerror", "qlora_abi_version"])
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().qlora_strerror(status).decode()
+        raise RuntimeError(f"{what} failed with status {status}: {msg}")
+
+
+def tag(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_TAG[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}") from None
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("HIP kernels need tensors on a GPU device")
+
+
+def i64_array(values) -> ctypes.Array:
+    return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+
+
+def call(name: str, *args) -> None:
+    """Call a C-ABI entry point and raise RuntimeError on a non-zero status."""
+    check(getattr(load(), name)(*args), name)

@@ -1,0 +1,183 @@
+// LoRA elementwise kernels around the adapter GEMMs, for gfx950.
+//
+// Reference semantics:
+//   solution/lora.py:29-46  OUT = IN * keep * scale (keep from a counter-based RNG), or a
+//                           plain scale-and-cast when dropout is off;
+//   solution/lora.py:49-60  OUT = BASE + LO * scaling in fp32.
+//
+// The dropout mask is regenerated (never stored): keep = U(seed, row*N + col) > p, with U the
+// uniform of Philox4x32-10 (Salmon et al., "Parallel Random Numbers: As Easy as 1, 2, 3",
+// SC'11) on counter {flat index, 0, 0, 0} and key {seed_lo, seed_hi}; word 0 is folded to a
+// non-negative int32 (x < 0 -> -x-1) and scaled by 4.6566127342e-10f. That is the uniform
+// Triton's tl.rand(seed, int32 offset) draws, so a seed gives the reference's mask.
+//
+// HBM-bound. One workgroup per row; each thread moves 8 consecutive elements per step.
+#include "ql_vec.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+QL_DEV uint32_t philox_word0(uint32_t ctr, uint64_t seed) {
+  uint32_t c0 = ctr, c1 = 0u, c2 = 0u, c3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+    c0 = hi1 ^ c1 ^ k0;
+    c1 = lo1;
+    c2 = hi0 ^ c3 ^ k1;
+    c3 = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+
+QL_DEV float uniform_from_word(uint32_t w) {
+  int32_t x = (int32_t)w;
+  x = x < 0 ? ~x : x;  // -x - 1 in two's complement, also for INT32_MIN
+  return (float)x * 4.6566127342e-10f;
+}
+
+template <int IT, int OT, bool DROPOUT, bool VEC>
+__global__ __launch_bounds__(kThreads) void dropout_scale_kernel(
+    const typename Elem<IT>::T* __restrict__ in, int64_t in_rs, typename Elem<OT>::T* __restrict__ out,
+    int64_t out_rs, int64_t n_cols, uint64_t seed, float p, float scale) {
+  const int64_t row = blockIdx.x;
+  const auto* src = in + row * in_rs;
+  auto* dst = out + row * out_rs;
+  if constexpr (VEC) {
+    for (int64_t c = 8 * (int64_t)threadIdx.x; c < n_cols; c += 8 * kThreads) {
+      float v[8];
+      Vec8<IT>::load(src + c, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if constexpr (DROPOUT) {
+          const uint32_t flat = (uint32_t)(row * n_cols + c + j);
+          const bool keep = uniform_from_word(philox_word0(flat, seed)) > p;
+          v[j] = keep ? v[j] * scale : 0.0f;
+        } else {
+          v[j] = v[j] * scale;
+        }
+      }
+      Vec8<OT>::store(dst + c, v);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < n_cols; c += kThreads) {
+      float v = Elem<IT>::to_f32(src[c]);
+      if constexpr (DROPOUT) {
+        const uint32_t flat = (uint32_t)(row * n_cols + c);
+        v = uniform_from_word(philox_word0(flat, seed)) > p ? v * scale : 0.0f;
+      } else {
+        v = v * scale;
+      }
+      dst[c] = Elem<OT>::from_f32(v);
+    }
+  }
+}
+
+template <int BT, int LT, int OT, bool VEC>
+__global__ __launch_bounds__(kThreads) void scaled_add_kernel(
+    const typename Elem<BT>::T* __restrict__ base, int64_t b_rs, const typename Elem<LT>::T* __restrict__ lo,
+    int64_t l_rs, typename Elem<OT>::T* __restrict__ out, int64_t o_rs, int64_t n_cols, float scaling) {
+  const int64_t row = blockIdx.x;
+  const auto* b = base + row * b_rs;
+  const auto* l = lo + row * l_rs;
+  auto* o = out + row * o_rs;
+  if constexpr (VEC) {
+    for (int64_t c = 8 * (int64_t)threadIdx.x; c < n_cols; c += 8 * kThreads) {
+      float bv[8], lv[8], ov[8];
+      Vec8<BT>::load(b + c, bv);
+      Vec8<LT>::load(l + c, lv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ov[j] = bv[j] + lv[j] * scaling;
+      Vec8<OT>::store(o + c, ov);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < n_cols; c += kThreads)
+      o[c] = Elem<OT>::from_f32(Elem<BT>::to_f32(b[c]) + Elem<LT>::to_f32(l[c]) * scaling);
+  }
+}
+
+bool rows_vec_ok(const void* p, int64_t rs, int dt, int64_t n_cols) {
+  return (n_cols % 8) == 0 && ql_aligned(p, 16) && ((rs * ql_elem_size(dt)) % 16) == 0;
+}
+
+template <int IT, int OT>
+int launch_dropout(const void* in, int64_t in_rs, void* out, int64_t out_rs, int64_t n_rows,
+                   int64_t n_cols, uint64_t seed, float p, float scale, bool vec, hipStream_t s) {
+  using I = typename Elem<IT>::T;
+  using O = typename Elem<OT>::T;
+  const dim3 grid((unsigned)n_rows);
+  const bool drop = p > 0.0f;
+#define QL_DROP(D, V)                                                                        \
+  hipLaunchKernelGGL((dropout_scale_kernel<IT, OT, D, V>), grid, dim3(kThreads), 0, s,       \
+                     (const I*)in, in_rs, (O*)out, out_rs, n_cols, seed, p, scale)
+  if (drop) {
+    if (vec) QL_DROP(true, true); else QL_DROP(true, false);
+  } else {
+    if (vec) QL_DROP(false, true); else QL_DROP(false, false);
+  }
+#undef QL_DROP
+  return ql_launch_status();
+}
+
+template <int BT, int LT>
+int launch_add(const void* base, int64_t b_rs, const void* lo, int64_t l_rs, void* out,
+               int64_t o_rs, int64_t n_rows, int64_t n_cols, float scaling, bool vec,
+               hipStream_t s) {
+  constexpr int OT = (BT == LT) ? BT : QL_F32;
+  using Bt = typename Elem<BT>::T;
+  using Lt = typename Elem<LT>::T;
+  using Ot = typename Elem<OT>::T;
+  const dim3 grid((unsigned)n_rows);
+  if (vec)
+    hipLaunchKernelGGL((scaled_add_kernel<BT, LT, OT, true>), grid, dim3(kThreads), 0, s,
+                       (const Bt*)base, b_rs, (const Lt*)lo, l_rs, (Ot*)out, o_rs, n_cols, scaling);
+  else
+    hipLaunchKernelGGL((scaled_add_kernel<BT, LT, OT, false>), grid, dim3(kThreads), 0, s,
+                       (const Bt*)base, b_rs, (const Lt*)lo, l_rs, (Ot*)out, o_rs, n_cols, scaling);
+  return ql_launch_status();
+}
+
+}  // namespace
+
+extern "C" int qlora_lora_dropout_scale(const void* in, int in_dtype, int64_t in_row_stride,
+                                        void* out, int out_dtype, int64_t out_row_stride,
+                                        int64_t n_rows, int64_t n_cols, uint64_t seed, float p,
+                                        float scale, ql_stream_t stream) {
+  if (n_rows < 0 || n_cols < 0 || n_rows > UINT32_MAX) return QL_EINVAL;
+  if (!ql_valid_dtype(in_dtype) || !ql_valid_dtype(out_dtype)) return QL_EDTYPE;
+  if (n_rows == 0 || n_cols == 0) return QL_OK;
+  if (!in || !out) return QL_EINVAL;
+  const bool vec = rows_vec_ok(in, in_row_stride, in_dtype, n_cols) &&
+                   rows_vec_ok(out, out_row_stride, out_dtype, n_cols);
+  QL_DISPATCH_DTYPE2(in_dtype, out_dtype, IT, OT,
+                     return launch_dropout<IT, OT>(in, in_row_stride, out, out_row_stride, n_rows,
+                                                   n_cols, seed, p, scale, vec,
+                                                   static_cast<hipStream_t>(stream)));
+  return QL_EDTYPE;
+}
+
+extern "C" int qlora_lora_scaled_add(const void* base, int base_dtype, int64_t base_row_stride,
+                                     const void* lo, int lo_dtype, int64_t lo_row_stride,
+                                     void* out, int out_dtype, int64_t out_row_stride,
+                                     int64_t n_rows, int64_t n_cols, float scaling,
+                                     ql_stream_t stream) {
+  if (n_rows < 0 || n_cols < 0 || n_rows > UINT32_MAX) return QL_EINVAL;
+  if (!ql_valid_dtype(base_dtype) || !ql_valid_dtype(lo_dtype) ||
+      out_dtype != ql_promote(base_dtype, lo_dtype))
+    return QL_EDTYPE;
+  if (n_rows == 0 || n_cols == 0) return QL_OK;
+  if (!base || !lo || !out) return QL_EINVAL;
+  const bool vec = rows_vec_ok(base, base_row_stride, base_dtype, n_cols) &&
+                   rows_vec_ok(lo, lo_row_stride, lo_dtype, n_cols) &&
+                   rows_vec_ok(out, out_row_stride, out_dtype, n_cols);
+  QL_DISPATCH_DTYPE2(base_dtype, lo_dtype, BT, LT,
+                     return launch_add<BT, LT>(base, base_row_stride, lo, lo_row_stride, out,
+                                               out_row_stride, n_rows, n_cols, scaling, vec,
+                                               static_cast<hipStream_t>(stream)));
+  return QL_EDTYPE;
+}

@@ -1,0 +1,192 @@
+// NF4 dequantisation with a double-quantised absmax, for gfx950.
+//
+// Reference semantics: solution/nf4.py:25-49 (nf4_dequant_kernel) and :71-92
+// (dequantize_nf4). Weight j lives in packed byte j/2 (high nibble first); its block scale
+// is, with double quantisation,
+//     s = code2[absmax_q[j / bs]] * absmax2[(j / bs) / bs2];   s = s + offset
+// (two fp32 roundings, never an FMA), otherwise s = absmax[j / bs]. The weight is the fp32
+// product nf4[nibble] * s, rounded once to the output dtype.
+//
+// HBM-bound: 0.5 B of nibbles + 1/bs B of absmax codes in, 2 B of bf16 out per weight.
+// Fast path: one lane turns one 32-bit word (4 packed bytes = 8 weights) into one 16-byte
+// bf16 store. Lanes of a wave take consecutive words, so each global load instruction reads
+// 256 contiguous bytes and each store instruction writes 1 KiB contiguous; a workgroup
+// covers UNROLL such spans with all loads issued before the first store. The 16-entry
+// codebook and the 256-entry code2 table sit in LDS.
+#include "ql_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int OUT_DT> struct Group8;  // 8 dequantised weights -> one vector store
+template <> struct Group8<QL_BF16> {
+  static QL_DEV void store(uint16_t* out, int64_t g, const float* w) {
+    uint4 v;
+    v.x = pack_bf16x2(w[0], w[1]);
+    v.y = pack_bf16x2(w[2], w[3]);
+    v.z = pack_bf16x2(w[4], w[5]);
+    v.w = pack_bf16x2(w[6], w[7]);
+    reinterpret_cast<uint4*>(out)[g] = v;
+  }
+};
+template <> struct Group8<QL_F16> {
+  static QL_DEV void store(uint16_t* out, int64_t g, const float* w) {
+    uint4 v;
+    v.x = pack_f16x2(w[0], w[1]);
+    v.y = pack_f16x2(w[2], w[3]);
+    v.z = pack_f16x2(w[4], w[5]);
+    v.w = pack_f16x2(w[6], w[7]);
+    reinterpret_cast<uint4*>(out)[g] = v;
+  }
+};
+template <> struct Group8<QL_F32> {
+  static QL_DEV void store(float* out, int64_t g, const float* w) {
+    float4* o = reinterpret_cast<float4*>(out) + 2 * g;
+    o[0] = make_float4(w[0], w[1], w[2], w[3]);
+    o[1] = make_float4(w[4], w[5], w[6], w[7]);
+  }
+};
+
+// Block scale of block `blk`, exactly as the reference orders the fp32 operations.
+template <bool NESTED>
+QL_DEV float block_scale(int64_t blk, const uint8_t* __restrict__ absmax_q,
+                         const float* __restrict__ absmax_f, const float* code2_lds,
+                         const float* __restrict__ absmax2, float offset, int log2_bs2) {
+#pragma clang fp contract(off)
+  if constexpr (NESTED) {
+    float s = code2_lds[absmax_q[blk]] * absmax2[blk >> log2_bs2];
+    return s + offset;
+  } else {
+    return absmax_f[blk];
+  }
+}
+
+template <int OUT_DT, bool NESTED, int UNROLL>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
+    const uint32_t* __restrict__ packed4, int64_t n_groups, const uint8_t* __restrict__ absmax_q,
+    const float* __restrict__ absmax_f, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, float offset, int log2_bs, int log2_bs2,
+    const float* __restrict__ nf4_table, typename Elem<OUT_DT>::T* __restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ float table[16];
+  __shared__ float code2_lds[NESTED ? 256 : 1];
+  if (threadIdx.x < 16) table[threadIdx.x] = nf4_table[threadIdx.x];
+  if constexpr (NESTED) code2_lds[threadIdx.x] = code2[threadIdx.x];  // kThreads == 256
+  __syncthreads();
+
+  const int64_t base = (int64_t)blockIdx.x * (kThreads * UNROLL) + threadIdx.x;
+  uint32_t word[UNROLL];
+  int64_t blk[UNROLL];
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t g = base + (int64_t)u * kThreads;
+    word[u] = g < n_groups ? packed4[g] : 0u;
+    blk[u] = (g * 8) >> log2_bs;  // all 8 weights of a group share one block (bs >= 8)
+  }
+#pragma unroll
+  for (int u = 0; u < UNROLL; ++u) {
+    const int64_t g = base + (int64_t)u * kThreads;
+    if (g >= n_groups) continue;
+    const float s =
+        block_scale<NESTED>(blk[u], absmax_q, absmax_f, code2_lds, absmax2, offset, log2_bs2);
+    float w[8];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (word[u] >> (8 * b)) & 0xffu;
+      w[2 * b] = table[byte >> 4] * s;      // high nibble: the first weight of the byte
+      w[2 * b + 1] = table[byte & 15u] * s;  // low nibble: the second
+    }
+    Group8<OUT_DT>::store(out, g, w);
+  }
+}
+
+// Any even blocksize, any alignment: one thread per packed byte.
+template <int OUT_DT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_scalar(
+    const uint8_t* __restrict__ packed, int64_t byte_begin, int64_t byte_end,
+    const uint8_t* __restrict__ absmax_q, const float* __restrict__ absmax_f,
+    const float* __restrict__ code2, const float* __restrict__ absmax2, float offset,
+    int64_t blocksize, int64_t blocksize2, const float* __restrict__ nf4_table,
+    typename Elem<OUT_DT>::T* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int64_t i = byte_begin + (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= byte_end) return;
+  const int64_t blk = (2 * i) / blocksize;
+  float s;
+  if constexpr (NESTED) {
+    s = code2[absmax_q[blk]] * absmax2[blk / blocksize2];
+    s = s + offset;
+  } else {
+    s = absmax_f[blk];
+  }
+  const uint32_t byte = packed[i];
+  Elem<OUT_DT>::store(out, 2 * i, nf4_table[byte >> 4] * s);
+  Elem<OUT_DT>::store(out, 2 * i + 1, nf4_table[byte & 15u] * s);
+}
+
+int ilog2_exact(int64_t v) {  // log2 of a power of two, else -1
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((int64_t(1) << l) < v) ++l;
+  return l;
+}
+
+template <int OUT_DT, bool NESTED>
+int launch_dequant(const uint8_t* packed, int64_t n_weights, const void* absmax,
+                   const float* code2, const float* absmax2, float offset, int blocksize,
+                   int blocksize2, const float* table, void* out_v, hipStream_t stream) {
+  using T = typename Elem<OUT_DT>::T;
+  T* out = static_cast<T*>(out_v);
+  const uint8_t* aq = NESTED ? static_cast<const uint8_t*>(absmax) : nullptr;
+  const float* af = NESTED ? nullptr : static_cast<const float*>(absmax);
+  const int64_t n_bytes = n_weights / 2;
+  const int lbs = ilog2_exact(blocksize);
+  const int lbs2 = NESTED ? ilog2_exact(blocksize2) : 0;
+  const bool fast = lbs >= 3 && lbs2 >= 0 && ql_aligned(packed, 4) && ql_aligned(out, 16);
+  int64_t done = 0;
+  if (fast) {
+    constexpr int kUnroll = 2;
+    const int64_t n_groups = n_bytes / 4;
+    if (n_groups > 0) {
+      const int64_t grid = (n_groups + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+      hipLaunchKernelGGL((nf4_dequant_vec<OUT_DT, NESTED, kUnroll>), dim3((unsigned)grid),
+                         dim3(kThreads), 0, stream, reinterpret_cast<const uint32_t*>(packed),
+                         n_groups, aq, af, code2, absmax2, offset, lbs, lbs2, table, out);
+    }
+    done = n_groups * 4;
+  }
+  if (done < n_bytes) {
+    const int64_t grid = (n_bytes - done + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL((nf4_dequant_scalar<OUT_DT, NESTED>), dim3((unsigned)grid), dim3(kThreads),
+                       0, stream, packed, done, n_bytes, aq, af, code2, absmax2, offset,
+                       (int64_t)blocksize, (int64_t)(NESTED ? blocksize2 : 1), table, out);
+  }
+  return ql_launch_status();
+}
+
+}  // namespace
+
+extern "C" int qlora_nf4_dequant(const uint8_t* packed, int64_t n_weights, const void* absmax,
+                                 int nested, const float* code2, const float* absmax2,
+                                 float offset, int blocksize, int blocksize2,
+                                 const float* nf4_table, void* out, int out_dtype,
+                                 ql_stream_t stream) {
+  if (n_weights < 0 || (n_weights & 1) || blocksize < 2 || (blocksize & 1)) return QL_EINVAL;
+  if (n_weights == 0) return QL_OK;
+  if (!packed || !absmax || !nf4_table || !out) return QL_EINVAL;
+  if (nested && (!code2 || !absmax2 || blocksize2 < 2 || (blocksize2 & 1))) return QL_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nested) {
+    QL_DISPATCH_DTYPE(out_dtype, DT,
+                      return launch_dequant<DT, true>(packed, n_weights, absmax, code2, absmax2,
+                                                      offset, blocksize, blocksize2, nf4_table,
+                                                      out, s));
+  } else {
+    QL_DISPATCH_DTYPE(out_dtype, DT,
+                      return launch_dequant<DT, false>(packed, n_weights, absmax, nullptr,
+                                                       nullptr, 0.f, blocksize, 1, nf4_table, out,
+                                                       s));
+  }
+  return QL_EDTYPE;
+}

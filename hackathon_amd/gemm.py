@@ -1,0 +1,72 @@
+"""Host wrappers of the library's MFMA GEMM (`qlora_gemm`).
+
+These stand in for the torch GEMM calls of the reference's path (F.linear and torch.matmul
+in solution/nf4.py:102,111, the LoRA nn.Linear pair of solution/lora.py:172 and the chunk
+GEMMs of solution/cross_entropy.py:117,123 / solution/fused_ce.py:135,143). Inputs must be
+bf16 or fp16 on a GPU; they are made unit-stride along their contiguous dimension if needed.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """A 2-D view with unit stride along the last dim (any row stride: the kernel takes it)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < t2.shape[1]):
+        t2 = t2.contiguous()
+    return t2
+
+
+def padded_rows(n_rows: int, n_cols: int, dtype, device) -> torch.Tensor:
+    """An [n_rows, n_cols] buffer whose rows start 16-B aligned (row stride rounded up to a
+    multiple of 8 elements), so the GEMM and row kernels take their vector paths."""
+    stride = (n_cols + 7) // 8 * 8
+    return torch.empty((n_rows, stride), dtype=dtype, device=device)[:, :n_cols]
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, *, a_km: bool = False, b_kn: bool = False,
+         out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+         bias: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
+    """C = alpha * A @ B^T (+ beta C) (+ bias) with A [M,K] (or stored [K,M] when a_km) and
+    B [N,K] (or stored [K,N] when b_kn), both 2-D, unit stride along their last dim."""
+    _lib.require_device(a, b)
+    if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"GEMM operands must share dtype bf16/fp16, got {a.dtype}, {b.dtype}")
+    a, b = _rows(a), _rows(b)
+    M, K = (a.shape[1], a.shape[0]) if a_km else (a.shape[0], a.shape[1])
+    N, Kb = (b.shape[1], b.shape[0]) if b_kn else (b.shape[0], b.shape[1])
+    if K != Kb:
+        raise ValueError(f"GEMM inner sizes differ: {K} vs {Kb}")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or a.dtype, device=a.device)
+    elif out.shape != (M, N) or out.stride(-1) != 1:
+        raise ValueError("out must be [M, N] with unit stride along N")
+    if bias is not None:
+        bias = bias.to(a.dtype).contiguous()
+    _lib.call("qlora_gemm", int(a_km), int(b_kn), M, N, K, a.data_ptr(), a.stride(0),
+              b.data_ptr(), b.stride(0), _lib.tag(a.dtype), out.data_ptr(), out.stride(0),
+              _lib.tag(out.dtype), _lib.ptr(bias), float(alpha), float(beta), _lib.stream_of(out))
+    return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x, weight, bias) for x [..., K] and weight [N, K] (output in x.dtype)."""
+    x2 = _rows(x)
+    y = gemm(x2, weight, bias=bias)
+    return y.view(*x.shape[:-1], weight.shape[0])
+
+
+def matmul_nn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a @ b for a [..., K] and b [K, N] (output in a.dtype)."""
+    a2 = _rows(a)
+    y = gemm(a2, b, b_kn=True)
+    return y.view(*a.shape[:-1], b.shape[1])
+
+
+def matmul_tn(a: torch.Tensor, b: torch.Tensor, out_dtype=None) -> torch.Tensor:
+    """a^T @ b for a [K, M] and b [K, N], both stored row-major (reduction over rows)."""
+    return gemm(_rows(a), _rows(b), a_km=True, b_kn=True, out_dtype=out_dtype)

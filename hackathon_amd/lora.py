@@ -1,0 +1,240 @@
+"""LoRA dropout + cast and scaled add around a 4-bit LoRA layer (drop-in for solution/lora.py).
+
+A peft 4-bit LoRA layer's forward under autocast (solution/lora.py:5-7):
+    result = base_layer(x)
+    out    = lora_B(lora_A(dropout(x))) * scaling
+    result = result + out
+Here (solution/lora.py:8-17):
+    xd  = DropoutCast(x)   one pass: counter-based mask (regenerated in backward, never stored),
+                           1/(1-p) scale, cast to the compute dtype  -> qlora_lora_dropout_scale
+    lo  = lora_B(lora_A(xd))                                        -> qlora_gemm (x2)
+    out = ScaledAdd(result, lo, scaling) in fp32                    -> qlora_lora_scaled_add
+peft is not installed in this environment, so `LoraLinear4bit` below carries the attribute
+surface the patched forward reads (base_layer, lora_A/lora_B/lora_dropout ModuleDicts,
+scaling, active_adapters, disable_adapters, merged) and always runs the patched forward.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _common, _lib
+from . import gemm as _gemm
+
+TORCH_DROPOUT_RNG = False
+
+
+def _rows(t):
+    t2 = t.reshape(-1, t.shape[-1])
+    return t2 if t2.stride(-1) == 1 else t2.contiguous()
+
+
+def _block(n):
+    """The reference's per-row column block (solution/lora.py:68-71); the HIP kernels move 8
+    elements per thread per step and do not need it."""
+    return 1024
+
+
+def _dropout_scale(src, out_dtype, seed, p, scale):
+    """OUT = SRC * keep * scale, cast (solution/lora.py:74-81)."""
+    _lib.require_device(src)
+    s2 = _rows(src)
+    out = torch.empty(s2.shape, dtype=out_dtype, device=src.device)
+    M, N = s2.shape
+    _lib.call("qlora_lora_dropout_scale", s2.data_ptr(), _lib.tag(s2.dtype), s2.stride(0),
+              out.data_ptr(), _lib.tag(out_dtype), out.stride(0), M, N,
+              int(seed) & 0xFFFF_FFFF_FFFF_FFFF, float(p), float(scale), _lib.stream_of(s2))
+    return out.view(src.shape)
+
+
+class DropoutCast(torch.autograd.Function):
+    """solution/lora.py:84-93: the backward regenerates the same mask from the same seed."""
+
+    @staticmethod
+    def forward(ctx, x, p, seed, out_dtype):
+        scale = 1.0 / (1.0 - p) if p > 0 else 1.0
+        ctx.p, ctx.seed, ctx.scale, ctx.x_dtype = p, seed, scale, x.dtype
+        return _dropout_scale(x, out_dtype, seed, p, scale)
+
+    @staticmethod
+    def backward(ctx, g):
+        return _dropout_scale(g, ctx.x_dtype, ctx.seed, ctx.p, ctx.scale), None, None, None
+
+
+class ScaledAdd(torch.autograd.Function):
+    """out = base + lo * scaling in fp32 (solution/lora.py:96-112)."""
+
+    @staticmethod
+    def forward(ctx, base, lo, scaling):
+        _lib.require_device(base, lo)
+        b2, l2 = _rows(base), _rows(lo)
+        out_dtype = torch.promote_types(base.dtype, lo.dtype)
+        out = torch.empty(b2.shape, dtype=out_dtype, device=base.device)
+        M, N = b2.shape
+        _lib.call("qlora_lora_scaled_add", b2.data_ptr(), _lib.tag(b2.dtype), b2.stride(0),
+                  l2.data_ptr(), _lib.tag(l2.dtype), l2.stride(0), out.data_ptr(),
+                  _lib.tag(out_dtype), out.stride(0), M, N, float(scaling), _lib.stream_of(b2))
+        ctx.scaling, ctx.base_dtype, ctx.lo_dtype = scaling, base.dtype, lo.dtype
+        return out.view(base.shape)
+
+    @staticmethod
+    def backward(ctx, g):
+        d_base = g if g.dtype == ctx.base_dtype else g.to(ctx.base_dtype)
+        d_lo = _dropout_scale(g, ctx.lo_dtype, 0, 0.0, ctx.scaling)  # g * scaling, cast
+        return d_base, d_lo, None
+
+
+class _Seeds:
+    """Dropout seeds from a private generator seeded from the run's torch seed, so the run is
+    reproducible and no other random stream is disturbed (solution/lora.py:115-124)."""
+    gen = None
+
+    @classmethod
+    def next(cls):
+        if cls.gen is None:
+            cls.gen = torch.Generator().manual_seed(torch.initial_seed() & 0xFFFF_FFFF)
+        return int(torch.randint(0, 2**31 - 1, (1,), generator=cls.gen))
+
+
+class LoRALinearFn(torch.autograd.Function):
+    """lo = (xd @ A^T) @ B^T on the MFMA GEMM, with the adapter weight gradients:
+        u = xd A^T;  lo = u B^T;   dB = dlo^T u;  du = dlo B;  dA = du^T xd;  dxd = du A
+    (the nn.Linear pair of solution/lora.py:172 and what autograd computes for it)."""
+
+    @staticmethod
+    def forward(ctx, xd, a_weight, b_weight):
+        x2 = _rows(xd)
+        a = a_weight.to(x2.dtype)
+        b = b_weight.to(x2.dtype)
+        u = _gemm.gemm(x2, a)
+        lo = _gemm.gemm(u, b)
+        ctx.save_for_backward(x2, u, a, b)
+        ctx.shape, ctx.wdtypes = xd.shape, (a_weight.dtype, b_weight.dtype)
+        return lo.view(*xd.shape[:-1], b.shape[0])
+
+    @staticmethod
+    def backward(ctx, dlo):
+        x2, u, a, b = ctx.saved_tensors
+        d2 = _rows(dlo).to(x2.dtype)
+        da = db = dx = None
+        du = _gemm.gemm(d2, b, b_kn=True)                               # [M, r]
+        if ctx.needs_input_grad[2]:
+            db = _gemm.matmul_tn(d2, u, out_dtype=torch.float32).to(ctx.wdtypes[1])
+        if ctx.needs_input_grad[1]:
+            da = _gemm.matmul_tn(du, x2, out_dtype=torch.float32).to(ctx.wdtypes[0])
+        if ctx.needs_input_grad[0]:
+            dx = _gemm.gemm(du, a, b_kn=True).view(ctx.shape)
+        return dx, da, db
+
+
+def _single_adapter(layer):
+    """The one active plain-Linear adapter, or None (solution/lora.py:127-142)."""
+    if layer.disable_adapters or layer.merged:
+        return None
+    active = [a for a in layer.active_adapters if a in layer.lora_A.keys()]
+    if len(active) != 1:
+        return None
+    a = active[0]
+    if a in getattr(layer, "lora_variant", {}):
+        return None
+    lora_a, lora_b = layer.lora_A[a], layer.lora_B[a]
+    if not (type(lora_a) is torch.nn.Linear and type(lora_b) is torch.nn.Linear
+            and lora_a.bias is None and lora_b.bias is None):
+        return None
+    if not isinstance(layer.lora_dropout[a], (torch.nn.Dropout, torch.nn.Identity)):
+        return None
+    return a
+
+
+def lora_forward(self, x, *args, **kwargs):
+    """The patched 4-bit LoRA forward (solution/lora.py:157-173), or None when this call must
+    take the layer's original path."""
+    compute_dtype = _common.autocast_dtype() or getattr(self, "compute_dtype", None)
+    adapter = None
+    if not args and not kwargs and compute_dtype is not None and _common.on_gpu(x) \
+            and x.dtype in (torch.float32, torch.float16, torch.bfloat16):
+        adapter = _single_adapter(self)
+    if adapter is None:
+        return None
+    result = self.base_layer(x)
+    drop = self.lora_dropout[adapter]
+    p = float(drop.p) if isinstance(drop, torch.nn.Dropout) and drop.training else 0.0
+    if TORCH_DROPOUT_RNG and p > 0:
+        xd = DropoutCast.apply(drop(x), 0.0, 0, compute_dtype)
+    else:
+        xd = DropoutCast.apply(x, p, _Seeds.next() if p > 0 else 0, compute_dtype)
+    with torch.autocast("cuda", enabled=False):
+        lo = LoRALinearFn.apply(xd, self.lora_A[adapter].weight, self.lora_B[adapter].weight)
+    return ScaledAdd.apply(result, lo, self.scaling[adapter])
+
+
+class LoraLinear4bit(torch.nn.Module):
+    """A 4-bit base layer with one LoRA adapter, with peft's LoRA-layer attribute surface.
+
+    `compute_dtype` is the adapters' matmul dtype when autocast is off (under autocast the
+    autocast dtype wins, as in solution/lora.py:158)."""
+
+    def __init__(self, base_layer, r=16, lora_alpha=32, lora_dropout=0.0, adapter="default",
+                 compute_dtype=None, init_b_std=0.0):
+        super().__init__()
+        self.base_layer = base_layer
+        in_f, out_f = base_layer.in_features, base_layer.out_features
+        dev = base_layer.bias.device if base_layer.bias is not None else (
+            base_layer.weight.device if base_layer.weight is not None else None)
+        self.lora_A = torch.nn.ModuleDict(
+            {adapter: torch.nn.Linear(in_f, r, bias=False, device=dev)})
+        self.lora_B = torch.nn.ModuleDict(
+            {adapter: torch.nn.Linear(r, out_f, bias=False, device=dev)})
+        torch.nn.init.kaiming_uniform_(self.lora_A[adapter].weight, a=math.sqrt(5))
+        if init_b_std:
+            torch.nn.init.normal_(self.lora_B[adapter].weight, std=init_b_std)
+        else:
+            torch.nn.init.zeros_(self.lora_B[adapter].weight)
+        self.lora_dropout = torch.nn.ModuleDict(
+            {adapter: torch.nn.Dropout(lora_dropout) if lora_dropout > 0 else torch.nn.Identity()})
+        self.scaling = {adapter: lora_alpha / r}
+        self.r = {adapter: r}
+        self.active_adapters = [adapter]
+        self.disable_adapters = False
+        self.merged = False
+        self.compute_dtype = compute_dtype
+
+    @property
+    def in_features(self):
+        return self.base_layer.in_features
+
+    @property
+    def out_features(self):
+        return self.base_layer.out_features
+
+    def forward(self, x, *args, **kwargs):
+        out = lora_forward(self, x, *args, **kwargs)
+        if out is None:
+            from . import eager
+
+            return eager.lora_forward_eager(self, x)
+        return out
+
+
+def patch():
+    """Route peft's 4-bit LoRA layer through `lora_forward` when peft is importable
+    (solution/lora.py:145-176). This package's LoraLinear4bit needs no patch."""
+    try:
+        from peft.tuners.lora import bnb as lora_bnb
+    except ImportError:
+        return
+    cls = getattr(lora_bnb, "Linear4bit", None)
+    if cls is None:
+        return
+    original = cls.forward
+    if getattr(original, "_solution_patch", False):
+        return
+
+    def forward(self, x, *args, **kwargs):
+        out = lora_forward(self, x, *args, **kwargs)
+        return original(self, x, *args, **kwargs) if out is None else out
+
+    forward._solution_patch = True
+    cls.forward = forward

@@ -1,0 +1,172 @@
+"""NF4 dequantisation and the 4-bit linear layers that use it (drop-in for solution/nf4.py).
+
+Every 4-bit layer call rebuilds the weight from the packed NF4 nibbles and the
+double-quantised block scales (solution/nf4.py:1-16); here that rebuild is the gfx950 kernel
+`qlora_nf4_dequant`, with the scale dequantisation `code2[q] * absmax2 + offset` folded in and
+evaluated with the same fp32 operation order, so the weights come out bit-identical to the
+reference's formula. The contraction runs in the library's bf16/fp16 MFMA GEMM
+(`qlora_gemm`), and the backward re-dequantises (nothing dense is kept between forward and
+backward, solution/nf4.py:95-112).
+
+Signatures kept from the reference: `dequantize_nf4(packed, quant_state, dtype)`,
+`supported(qs)`, `NF4Linear.apply(x, packed, quant_state, bias)`, `_prepare(module, x)`,
+`linear4bit(module, x, keep_compute_dtype)`, `patch_linear4bit()`, `project(layer, x)`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from . import gemm as _gemm
+from . import quant
+
+DEQUANT_BLOCK = 1024  # packed bytes per workgroup step in the reference (solution/nf4.py:22)
+
+_NF4_TABLES = {}
+
+
+def _nf4_table(device):
+    """The 16-entry fp32 NF4 codebook on `device`, cached per device (solution/nf4.py:52-62)."""
+    table = _NF4_TABLES.get(device)
+    if table is None:
+        table = quant.nf4_code(device).contiguous()
+        _NF4_TABLES[device] = table
+    return table
+
+
+def supported(quant_state):
+    """NF4, 2-D, even blocksizes (solution/nf4.py:65-68)."""
+    return (quant_state is not None and quant_state.quant_type == "nf4"
+            and len(quant_state.shape) == 2 and quant_state.blocksize % 2 == 0
+            and (not quant_state.nested or quant_state.state2.blocksize % 2 == 0))
+
+
+def _scale_args(quant_state):
+    """(absmax, nested, code2, absmax2, offset, blocksize2) for the C-ABI (solution/nf4.py:77-86)."""
+    if quant_state.nested:
+        s2 = quant_state.state2
+        absmax = quant_state.absmax
+        if absmax.dtype != torch.uint8:
+            raise TypeError("double-quantised absmax must be uint8 codes")
+        code2 = s2.code if s2.code.dtype == torch.float32 else s2.code.float()
+        absmax2 = s2.absmax if s2.absmax.dtype == torch.float32 else s2.absmax.float()
+        if code2.numel() != 256:
+            raise ValueError("the double-quant code map must have 256 entries")
+        return (absmax.contiguous(), 1, code2.contiguous(), absmax2.contiguous(),
+                float(quant_state.offset), int(s2.blocksize))
+    absmax = quant_state.absmax
+    absmax = (absmax if absmax.dtype == torch.float32 else absmax.float()).contiguous()
+    return absmax, 0, None, None, 0.0, 1
+
+
+def dequantize_nf4(packed, quant_state, dtype=torch.float16, out=None):
+    """The weight [out_features, in_features] in `dtype`, from the packed NF4 bytes
+    (solution/nf4.py:71-92)."""
+    shape = tuple(quant_state.shape)
+    _lib.require_device(packed)
+    if out is None:
+        out = torch.empty(shape, dtype=dtype, device=packed.device)
+    n = out.numel()
+    packed = packed.reshape(-1)
+    if packed.numel() * 2 < n:
+        raise ValueError("packed buffer is smaller than the quantised shape")
+    absmax, nested, code2, absmax2, offset, blocksize2 = _scale_args(quant_state)
+    _lib.call("qlora_nf4_dequant", packed.data_ptr(), n, absmax.data_ptr(), nested,
+              _lib.ptr(code2), _lib.ptr(absmax2), offset, int(quant_state.blocksize),
+              blocksize2, _nf4_table(packed.device).data_ptr(), out.data_ptr(),
+              _lib.tag(out.dtype), _lib.stream_of(out))
+    return out
+
+
+class NF4Linear(torch.autograd.Function):
+    """y = x @ W.T + b with W rebuilt by the dequant kernel in forward and again in backward
+    (solution/nf4.py:95-112). Weight and bias are frozen."""
+
+    @staticmethod
+    def forward(ctx, x, packed, quant_state, bias):
+        weight = dequantize_nf4(packed, quant_state, x.dtype)
+        out = _gemm.linear(x, weight, bias)
+        ctx.packed, ctx.quant_state = packed, quant_state
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            weight = dequantize_nf4(ctx.packed, ctx.quant_state, grad_out.dtype)
+            grad_x = _gemm.matmul_nn(grad_out, weight)
+        return grad_x, None, None, None
+
+
+def _prepare(module, x):
+    """The part of a 4-bit layer's forward before the matmul (solution/nf4.py:115-138):
+    returns (x, bias, input dtype), or None when this layer should take the original path.
+    bf16 compute is accepted here (the reference accepted fp16/fp32 only, :131-132)."""
+    quant_state = getattr(module.weight, "quant_state", None)
+    if (not x.is_cuda or not supported(quant_state) or module.weight.requires_grad
+            or (module.bias is not None and module.bias.requires_grad)):
+        return None
+    if not module.compute_type_is_set:
+        module.set_compute_type(x)
+        module.compute_type_is_set = True
+    inp_dtype = x.dtype
+    if module.compute_dtype is not None:
+        x = x.to(module.compute_dtype)
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return None
+    bias = module.bias
+    if bias is not None:
+        if bias.dtype != x.dtype:
+            bias.data = bias.data.to(x.dtype)
+        bias = bias.to(x.dtype)
+    return x, bias, inp_dtype
+
+
+def _original_forward(module, x):
+    """The unpatched 4-bit forward: torch-op dequantisation + F.linear in the compute dtype
+    (what bitsandbytes' Linear4bit.forward computes). Used for inputs the kernels do not take
+    (CPU or meta tensors) and as the eager baseline."""
+    from . import eager
+
+    return eager.linear4bit_eager(module, x)
+
+
+_ORIGINAL = {}
+
+
+def linear4bit(module, x, keep_compute_dtype=False):
+    """A 4-bit layer's forward with the dequant kernel (solution/nf4.py:141-149). With
+    keep_compute_dtype the output stays in the compute dtype instead of the input dtype."""
+    prepared = _prepare(module, x)
+    if prepared is None:
+        return _ORIGINAL.get("forward", _original_forward)(module, x)
+    x, bias, inp_dtype = prepared
+    out = NF4Linear.apply(x, module.weight, module.weight.quant_state, bias)
+    return out if keep_compute_dtype else out.to(inp_dtype)
+
+
+def patch_linear4bit():
+    """Route bitsandbytes' Linear4bit.forward through `linear4bit` when bitsandbytes is
+    importable (solution/nf4.py:155-166); this package's own Linear4bit always does."""
+    try:
+        import bitsandbytes.nn.modules as bnb_modules
+    except ImportError:
+        return
+    cls = bnb_modules.Linear4bit
+    if "forward" in _ORIGINAL:
+        return
+    _ORIGINAL["forward"] = cls.forward
+
+    def forward(self, x):
+        return linear4bit(self, x)
+
+    cls.forward = forward
+
+
+def project(layer, x):
+    """An MLP projection that keeps its output in the compute dtype when it is a plain 4-bit
+    layer (solution/nf4.py:169-175). Anything else runs as it is."""
+    if type(layer) is quant.Linear4bit:
+        return linear4bit(layer, x, keep_compute_dtype=True)
+    return layer(x)

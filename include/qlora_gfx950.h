@@ -1,0 +1,179 @@
+/*
+ * libqlora_gfx950 — C-ABI of the MI355X (gfx950) QLoRA training-step kernel set.
+ *
+ * Each entry point replaces one Triton kernel (or torch GEMM call site) of the reference's
+ * `solution/` package together with its host-side launch; the reference file:line it
+ * replaces is cited on each declaration. The Python façades in `hackathon_amd/` keep the
+ * reference's function signatures and call these through ctypes.
+ *
+ * Conventions
+ *   - All tensor arguments are raw DEVICE pointers; sizes and strides are in ELEMENTS.
+ *   - `stream` is a hipStream_t (NULL = the legacy null stream). Every call only enqueues
+ *     work on `stream`; nothing synchronises the host, nothing allocates device memory.
+ *   - Return value: QL_OK (0) on success; a negative QL_E* code for a rejected argument
+ *     (nothing was launched); a positive hipError_t code if the launch itself failed.
+ *     No entry point throws across the ABI.
+ *   - dtype tags: QL_F32 / QL_F16 / QL_BF16 (storage of fp16/bf16 is IEEE binary16 /
+ *     bfloat16 bits). All arithmetic is fp32; every store to a 16-bit type is RNE.
+ */
+#ifndef QLORA_GFX950_H
+#define QLORA_GFX950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { QL_F32 = 0, QL_F16 = 1, QL_BF16 = 2 };
+
+enum {
+  QL_OK = 0,
+  QL_EINVAL = -1, /* null pointer, negative size, unsupported blocksize/flag */
+  QL_EDTYPE = -2, /* dtype tag or dtype combination not supported */
+  QL_EALIGN = -3, /* pointer/stride alignment a kernel requires is not met */
+  QL_ESHAPE = -4  /* inconsistent sizes */
+};
+
+typedef void* ql_stream_t; /* hipStream_t */
+
+/* Library identification and error text. */
+int qlora_abi_version(void);
+const char* qlora_strerror(int status);
+
+/*
+ * NF4 dequantisation with optional double-quantised absmax.
+ * Replaces: solution/nf4.py:25-49 (nf4_dequant_kernel) + solution/nf4.py:71-92
+ * (dequantize_nf4's unpacking of QuantState and launch).
+ *
+ *   packed   uint8[n_weights/2]; byte i holds weight 2i in its HIGH nibble and weight
+ *            2i+1 in its LOW nibble (solution/nf4.py:30,45-47).
+ *   nested=1 absmax is uint8[ceil(n/blocksize)] codes; the block scale is
+ *              s = code2[absmax[blk]] * absmax2[blk / blocksize2] ; s = s + offset
+ *            with two separate fp32 roundings (no FMA contraction).
+ *   nested=0 absmax is float32[ceil(n/blocksize)] and s = absmax[blk].
+ *   out[j] = round_to(out_dtype, nf4_table[nibble_j] * s),  blk = j / blocksize.
+ * n_weights must be even; blocksize (and blocksize2 when nested) even and >= 2.
+ * out_dtype: QL_BF16, QL_F16 or QL_F32.
+ */
+int qlora_nf4_dequant(const uint8_t* packed, int64_t n_weights, const void* absmax, int nested,
+                      const float* code2, const float* absmax2, float offset, int blocksize,
+                      int blocksize2, const float* nf4_table, void* out, int out_dtype,
+                      ql_stream_t stream);
+
+/*
+ * RMSNorm forward over rows of length n_cols (frozen weight).
+ * Replaces: solution/rmsnorm.py:24-39 (rmsnorm_fwd_kernel) + :64-78 (launch).
+ *   rstd[r] = 1 / sqrt(sum(x^2)/n_cols + eps)                  (fp32)
+ *   y = w * round_{x_dtype}(x * rstd)   (rounding only when x is 16-bit), stored as y_dtype.
+ * Strides are row strides; the last dimension must be unit-stride.
+ */
+int qlora_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row_stride, const void* w,
+                      int w_dtype, void* y, int y_dtype, int64_t y_row_stride, float* rstd,
+                      int64_t n_rows, int64_t n_cols, float eps, ql_stream_t stream);
+
+/*
+ * RMSNorm backward (no weight gradient: the weight is frozen).
+ * Replaces: solution/rmsnorm.py:42-55 (rmsnorm_bwd_kernel) + :81-90 (launch).
+ *   g = dy * w;  dx = rstd * (g - x * rstd^2 * mean(g * x)), stored as dx_dtype.
+ */
+int qlora_rmsnorm_bwd(const void* dy, int dy_dtype, int64_t dy_row_stride, const void* x,
+                      int x_dtype, int64_t x_row_stride, const void* w, int w_dtype,
+                      const float* rstd, void* dx, int dx_dtype, int64_t dx_row_stride,
+                      int64_t n_rows, int64_t n_cols, ql_stream_t stream);
+
+/*
+ * Rotary embedding of q and k in one launch, forward or backward (transpose).
+ * Replaces: solution/rope.py:24-62 (rope_qk_kernel) + :65-75 (_launch).
+ * q/k/q_out/k_out are (B, H, S, D) tensors given by strides {b, h, s} (last dim unit
+ * stride); cos/sin are (B or broadcast, S, D) with strides {cs_b, cs_s} (cs_b may be 0).
+ * With halves (x1,x2), (c1,c2), (s1,s2):
+ *   forward : o1 = x1*c1 - x2*s1 ;  o2 = x2*c2 + x1*s2
+ *   backward: d1 = g1*c1 + g2*s2 ;  d2 = g2*c2 - g1*s1
+ * in_dtype is the dtype of q and k; out_dtype of q_out and k_out; cs_dtype of cos/sin.
+ * D must be even.
+ */
+int qlora_rope_qk(const void* q, const void* k, void* q_out, void* k_out, const void* cos,
+                  const void* sin, int in_dtype, int cs_dtype, int out_dtype, int64_t B,
+                  int64_t S, int64_t HQ, int64_t HK, int64_t D, const int64_t* q_strides,
+                  const int64_t* k_strides, const int64_t* qo_strides, const int64_t* ko_strides,
+                  int64_t cs_stride_b, int64_t cs_stride_s, int backward, ql_stream_t stream);
+
+/*
+ * SwiGLU forward: out = silu(gate) * up, computed in fp32, all tensors contiguous, one dtype.
+ * Replaces: solution/swiglu.py:15-22 (example_swiglu_fwd_kernel) + :44-51.
+ */
+int qlora_swiglu_fwd(const void* gate, const void* up, void* out, int dtype, int64_t n,
+                     ql_stream_t stream);
+
+/*
+ * SwiGLU backward: dup = g*gate*sig ; dgate = g*up*sig*(1 + gate*(1 - sig)), sig = sigmoid(gate).
+ * Replaces: solution/swiglu.py:25-37 (example_swiglu_bwd_kernel) + :54-61.
+ */
+int qlora_swiglu_bwd(const void* grad, const void* gate, const void* up, void* dgate, void* dup,
+                     int dtype, int64_t n, ql_stream_t stream);
+
+/*
+ * LoRA input dropout + scale + cast, rows of n_cols.
+ * Replaces: solution/lora.py:29-46 (lora_dropout_scale_kernel) + :74-81 (_dropout_scale).
+ *   p > 0 : keep = U(seed, row*n_cols + col) > p ;  out = keep ? in*scale : 0
+ *   p <= 0: out = in * scale
+ * U is Philox4x32-10 (counter = {flat index as uint32, 0, 0, 0}, key = {seed lo, seed hi}),
+ * word 0 folded to non-negative int32 and multiplied by 4.6566127342e-10f: the uniform
+ * that Triton's tl.rand(seed, int32 offset) returns.
+ */
+int qlora_lora_dropout_scale(const void* in, int in_dtype, int64_t in_row_stride, void* out,
+                             int out_dtype, int64_t out_row_stride, int64_t n_rows,
+                             int64_t n_cols, uint64_t seed, float p, float scale,
+                             ql_stream_t stream);
+
+/*
+ * LoRA scaled add: out = base + lo * scaling in fp32, stored as out_dtype.
+ * Replaces: solution/lora.py:49-60 (lora_scaled_add_kernel) + :96-106 (ScaledAdd.forward).
+ */
+int qlora_lora_scaled_add(const void* base, int base_dtype, int64_t base_row_stride,
+                          const void* lo, int lo_dtype, int64_t lo_row_stride, void* out,
+                          int out_dtype, int64_t out_row_stride, int64_t n_rows, int64_t n_cols,
+                          float scaling, ql_stream_t stream);
+
+/*
+ * Per-row cross-entropy statistics over a chunk of logits, optionally overwriting the
+ * logits IN PLACE with the gradient.
+ * Replaces: solution/fused_ce.py:42-96 (ce_row_kernel) + :99-109 (ce_rows) and
+ *           solution/cross_entropy.py:48-90 (fused_ce_kernel).
+ *   lse = log(sum exp z); entropy = lse - sum(softmax*z); argmax = first index of the max.
+ *   A row is labelled when target >= 0 (ignore_mode 0, fused_ce.py:50) or
+ *   target != -100 (ignore_mode 1, cross_entropy.py:54).
+ *   loss = labelled ? lse - z[target] : 0
+ *   correct (int32, may be NULL) = labelled && argmax == target
+ *   pred (int64, may be NULL) = argmax
+ *   write_grad: z <- (softmax - onehot(target)) * (labelled ? grad_scale : 0)
+ * logits dtype: QL_F16, QL_BF16 or QL_F32; target is int64[n_rows].
+ */
+int qlora_ce_rows(void* logits, int logits_dtype, int64_t row_stride, int64_t n_rows,
+                  int64_t vocab, const int64_t* target, float* loss, float* entropy,
+                  int32_t* correct, int64_t* pred, int ignore_mode, int write_grad,
+                  float grad_scale, ql_stream_t stream);
+
+/*
+ * Dense GEMM on bf16/fp16 matrix cores (fp32 accumulation):
+ *   C[M,N] = alpha * sum_k A[m,k] * B[n,k]  + beta * C[M,N]  + bias[n]
+ * a_km = 0: A is [M,K] with row stride lda (k contiguous); a_km = 1: A is stored [K,M].
+ * b_kn = 0: B is [N,K] with row stride ldb (k contiguous); b_kn = 1: B is stored [K,N].
+ * in_dtype (A, B and bias): QL_BF16 or QL_F16. c_dtype: any. bias may be NULL; beta = 0
+ * never reads C. Any M, N, K and leading dimensions are accepted (ld >= row length, else
+ * QL_ESHAPE; element-aligned pointers, else QL_EALIGN); the fast path wants 16-B aligned
+ * k-contiguous rows (ld % 8 == 0) and 8-B aligned K-outer rows (ld % 4 == 0).
+ * Replaces the torch GEMM call sites of the path: F.linear / torch.matmul in
+ * solution/nf4.py:102,111; the LoRA A/B nn.Linear of solution/lora.py:172; the chunk GEMMs
+ * of solution/cross_entropy.py:117,123 and solution/fused_ce.py:135,143.
+ */
+int qlora_gemm(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+               const void* B, int64_t ldb, int in_dtype, void* C, int64_t ldc, int c_dtype,
+               const void* bias, float alpha, float beta, ql_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* QLORA_GFX950_H */

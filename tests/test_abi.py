@@ -1,0 +1,103 @@
+"""The C-ABI library: it loads, exports every symbol include/*.h declares, the ctypes binding
+covers exactly those, and argument checks return status codes without launching anything
+(so these run without a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from hackathon_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(scope="session")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        from hackathon_amd import build
+
+        build.build()
+    return _lib.load()
+
+
+def header_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(qlora_\w+)\s*\(", text))
+    return names
+
+
+def test_header_declares_the_kernel_set():
+    syms = header_symbols()
+    for name in ("qlora_nf4_dequant", "qlora_rmsnorm_fwd", "qlora_rmsnorm_bwd", "qlora_rope_qk",
+                 "qlora_swiglu_fwd", "qlora_swiglu_bwd", "qlora_lora_dropout_scale",
+                 "qlora_lora_scaled_add", "qlora_ce_rows", "qlora_gemm"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [s for s in sorted(header_symbols()) if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_binding_covers_exactly_the_header():
+    assert set(_lib.exported_symbols()) == header_symbols()
+
+
+def test_version_and_error_text(lib):
+    assert lib.qlora_abi_version() >= 1
+    assert lib.qlora_strerror(0) == b"ok"
+    assert b"dtype" in lib.qlora_strerror(-2)
+
+
+def test_rejected_arguments_return_codes(lib):
+    P = ctypes.c_void_p
+    fake = P(0x1000)  # never dereferenced: every call below is rejected before any launch
+    # odd weight count
+    assert lib.qlora_nf4_dequant(fake, 3, fake, 1, fake, fake, 0.0, 64, 256, fake, fake, 2,
+                                 None) == -1
+    # nested without a code map
+    assert lib.qlora_nf4_dequant(fake, 64, fake, 1, None, fake, 0.0, 64, 256, fake, fake, 2,
+                                 None) == -1
+    # odd blocksize
+    assert lib.qlora_nf4_dequant(fake, 64, fake, 0, None, None, 0.0, 63, 1, fake, fake, 2,
+                                 None) == -1
+    # unknown output dtype
+    assert lib.qlora_nf4_dequant(fake, 64, fake, 0, None, None, 0.0, 64, 1, fake, fake, 7,
+                                 None) == -2
+    # rmsnorm: bad dtype, zero columns
+    assert lib.qlora_rmsnorm_fwd(fake, 9, 8, fake, 2, fake, 2, 8, fake, 4, 8, 1e-6, None) == -2
+    assert lib.qlora_rmsnorm_fwd(fake, 2, 8, fake, 2, fake, 2, 8, fake, 4, 0, 1e-6, None) == -1
+    # rope: odd head dim, output dtype not the promotion of the inputs
+    s3 = _lib.i64_array((0, 0, 0))
+    assert lib.qlora_rope_qk(fake, fake, fake, fake, fake, fake, 2, 2, 2, 1, 1, 1, 1, 7, s3, s3,
+                             s3, s3, 0, 0, 0, None) == -1
+    assert lib.qlora_rope_qk(fake, fake, fake, fake, fake, fake, 2, 2, 0, 1, 1, 1, 1, 8, s3, s3,
+                             s3, s3, 0, 0, 0, None) == -2
+    # swiglu: negative size
+    assert lib.qlora_swiglu_fwd(fake, fake, fake, 2, -1, None) == -1
+    # scaled add: output dtype must be promote(base, lo)
+    assert lib.qlora_lora_scaled_add(fake, 0, 8, fake, 1, 8, fake, 1, 8, 2, 8, 2.0, None) == -2
+    # ce_rows: unknown ignore mode
+    assert lib.qlora_ce_rows(fake, 2, 8, 2, 8, fake, fake, fake, None, None, 2, 0, 1.0,
+                             None) == -1
+    # gemm: fp32 inputs are not a matrix-core type; an operand not element-aligned; a leading
+    # dimension shorter than the row
+    assert lib.qlora_gemm(0, 0, 4, 4, 8, fake, 8, fake, 8, 0, fake, 4, 0, None, 1.0, 0.0,
+                          None) == -2
+    assert lib.qlora_gemm(0, 0, 4, 4, 8, P(0x1001), 8, fake, 8, 2, fake, 4, 0, None, 1.0, 0.0,
+                          None) == -3
+    assert lib.qlora_gemm(0, 0, 4, 4, 12, fake, 8, fake, 16, 2, fake, 4, 0, None, 1.0, 0.0,
+                          None) == -4
+
+
+def test_empty_problems_are_no_ops(lib):
+    # zero-sized work returns OK without touching the (null) pointers or the device
+    assert lib.qlora_nf4_dequant(None, 0, None, 0, None, None, 0.0, 64, 1, None, None, 2,
+                                 None) == 0
+    assert lib.qlora_swiglu_fwd(None, None, None, 2, 0, None) == 0
+    assert lib.qlora_gemm(0, 0, 0, 4, 8, None, 8, None, 8, 2, None, 4, 2, None, 1.0, 0.0,
+                          None) == 0

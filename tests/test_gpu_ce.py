@@ -1,0 +1,165 @@
+"""Cross-entropy rows and the fused lm_head + CE façades on the GPU vs the CPU oracle.
+
+Bar: loss within 1e-4 relative error (fp32 accumulation); entropy likewise; argmax/pred and
+correct counts exact up to ties of equal 16-bit logits; hidden-state gradient within bf16/
+fp16 tolerance.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from hackathon_amd import cross_entropy, fused_ce
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("V,dtype", [(151936, torch.bfloat16), (1001, torch.float32),
+                                     (4096, torch.float16), (9001, torch.bfloat16)])
+@pytest.mark.parametrize("ignore_mode", [0, 1])
+def test_ce_rows_vs_oracle(V, dtype, ignore_mode):
+    print(f"ce_rows V={V} {dtype} mode={ignore_mode}", flush=True)
+    g = torch.Generator().manual_seed(V)
+    R = 24
+    z = (torch.randn(R, V, generator=g) * 3).to(dtype)
+    t = torch.randint(0, V, (R,), generator=g)
+    t[0] = -100
+    t[1] = -5 if ignore_mode == 0 else 7   # negative label: unlabelled under mode 0
+    loss_r, ent_r, am_r, cor_r, dz_r = ops.ce_rows(z, t, ignore_mode, grad_scale=3.0)
+    zg = z.cuda()
+    tg = t.cuda()
+    loss = torch.empty(R, device="cuda")
+    ent = torch.empty(R, device="cuda")
+    cor = torch.empty(R, dtype=torch.int32, device="cuda")
+    pred = torch.empty(R, dtype=torch.int64, device="cuda")
+    from hackathon_amd import _lib
+    _lib.call("qlora_ce_rows", zg.data_ptr(), _lib.tag(dtype), V, R, V, tg.data_ptr(),
+              loss.data_ptr(), ent.data_ptr(), cor.data_ptr(), pred.data_ptr(), ignore_mode, 1,
+              3.0, _lib.stream_of(zg))
+    torch.testing.assert_close(loss.cpu().double(), loss_r, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(ent.cpu().double(), ent_r, rtol=1e-4, atol=1e-4)
+    assert torch.equal(pred.cpu(), am_r)
+    assert torch.equal(cor.cpu(), cor_r)
+    tol = 1e-2 if dtype == torch.bfloat16 else (2e-3 if dtype == torch.float16 else 1e-5)
+    torch.testing.assert_close(zg.cpu().double(), dz_r.to(dtype).double(), rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("vocab", [1000, 4096, 9001])
+@pytest.mark.parametrize("with_num_items", [True, False])
+@pytest.mark.parametrize("matmul_dtype", [torch.float16, torch.bfloat16])
+def test_fused_causal_lm_loss_vs_oracle(vocab, with_num_items, matmul_dtype):
+    """solution/test_cross_entropy.py:35-66 at the reference's GPU shapes."""
+    print(f"fused_causal_lm_loss V={vocab} items={with_num_items} {matmul_dtype}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    B, T, H = 4, 512, 1536
+    hidden = torch.randn(B, T, H, generator=g)
+    weight = 0.05 * torch.randn(vocab, H, generator=g)
+    labels = torch.randint(0, vocab, (B, T), generator=g)
+    labels[:, : T // 3] = -100
+    labels[1, -2:] = -100
+    num_items = (labels[:, 1:] != -100).sum() if with_num_items else None
+    hg = hidden.cuda().requires_grad_()
+    with torch.autocast("cuda", dtype=matmul_dtype):
+        loss, step = cross_entropy.fused_causal_lm_loss(
+            hg, weight.cuda(), labels.cuda(),
+            num_items_in_batch=num_items.cuda() if num_items is not None else None)
+    hr = hidden.clone().requires_grad_()
+    loss_r, ent_r, tok_r, pred_r, correct_r, lab_r, _ = ops.fused_linear_ce(
+        hr, weight, labels, num_items, matmul_dtype)
+    torch.testing.assert_close(loss.cpu(), loss_r, rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(step.token_entropy.cpu(), ent_r, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(step.token_loss.cpu(), tok_r, rtol=1e-4, atol=1e-4)
+    assert int(step.labelled) == int(lab_r)
+    assert abs(int(step.correct) - int(correct_r)) <= 2  # ties of equal 16-bit logits
+    (loss * 1024.0).backward()
+    (loss_r * 1024.0).backward()
+    torch.testing.assert_close(hg.grad.cpu(), hr.grad, atol=5e-3, rtol=2e-2)
+
+
+def test_rewind_row_losses_from_token_loss():
+    """solution/test_cross_entropy.py:69-90: per-row means of token_loss equal the CE means."""
+    g = torch.Generator().manual_seed(1)
+    B, T, H, V = 3, 8, 16, 500
+    hidden = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+    weight = (0.1 * torch.randn(V, H, generator=g)).to(torch.bfloat16)
+    labels = torch.randint(0, V, (B, T), generator=g)
+    labels[:, :3] = -100
+    with torch.no_grad():
+        _, step = cross_entropy.fused_causal_lm_loss(hidden.cuda(), weight.cuda(), labels.cuda())
+    logits = (hidden.float() @ weight.float().t()).to(torch.bfloat16).float()
+    for i in range(B):
+        targets = labels[i, 1:]
+        ce = torch.nn.functional.cross_entropy(logits[i, :-1], targets, reduction="none",
+                                               ignore_index=-100)
+        mask = targets != -100
+        want = float((ce * mask).sum() / mask.sum())
+        got = float(step.token_loss[i].sum().cpu() / mask.sum())
+        assert abs(got - want) <= 1e-4 * max(1.0, abs(want))
+
+
+def test_fused_head_loss_vs_forcausallmloss():
+    """solution/test_kernels.py:104-136 at vocab 151936 (fp16 head, as the reference casts)."""
+    from transformers.loss.loss_utils import ForCausalLMLoss
+
+    print("fused_head_loss V=151936", flush=True)
+    g = torch.Generator().manual_seed(0)
+    b, t, h, v = 4, 300, 1536, 151936
+    hidden = torch.randn(b, t, h, generator=g)
+    weight = (torch.randn(v, h, generator=g) * 0.02).half().float()
+    labels = torch.randint(0, v, (b, t), generator=g)
+    labels[:, :40] = -100
+    mask = torch.ones(b, t, dtype=torch.long)
+    mask[1, 200:] = 0
+    labels[1, 200:] = -100
+    items = (labels[:, 1:] != -100).sum()
+    hg = hidden.cuda().requires_grad_()
+    loss, stats = fused_ce.fused_head_loss(hg, weight.cuda(), labels.cuda(), mask.cuda(),
+                                           items.cuda())
+    (loss * 1024).backward()
+    # reference on the GPU in fp16 for the logits, fp32 loss (as the reference test does)
+    h2 = hidden.cuda().requires_grad_()
+    logits = h2.half() @ weight.cuda().half().t()
+    ref = ForCausalLMLoss(logits, labels.cuda(), v, num_items_in_batch=items.cuda())
+    (ref * 1024).backward()
+    torch.testing.assert_close(loss, ref, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(hg.grad, h2.grad, rtol=2e-2, atol=2e-3)
+    with torch.no_grad():
+        lp = torch.log_softmax(logits.float(), -1)
+        ent = -(lp.exp() * lp).sum(-1)
+        ref_entropy = (ent * mask.cuda()).sum() / mask.sum()
+        pred = logits[:, :-1].argmax(-1)
+        lab = labels.cuda()[:, 1:]
+        ref_correct = ((pred == lab) & (lab != -100)).sum()
+    torch.testing.assert_close(stats.entropy_sum / mask.sum().cuda(), ref_entropy, rtol=1e-4,
+                               atol=1e-4)
+    assert abs(stats.correct.item() - ref_correct.item()) <= 2
+    assert stats.labelled.item() == (lab != -100).sum().item()
+
+
+def test_fused_ce_full_qwen25_shape_rows_vs_oracle():
+    """8192 tokens x 1536 hidden x 151936 vocab in bf16 with 10% ignored labels: the loss is
+    the mean of the per-token losses, and a random subset of rows matches the fp64 oracle."""
+    print("fused CE 8192x1536x151936", flush=True)
+    g = torch.Generator().manual_seed(0)
+    n, H, V = 8192, 1536, 151936
+    hidden = torch.randn(n, H, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16)
+    target = torch.randint(0, V, (n,), generator=g)
+    target[torch.rand(n, generator=g) < 0.1] = -100
+    hg = hidden.cuda().requires_grad_()
+    denom = (target != -100).sum()
+    loss, tok, ent, pred = cross_entropy.FusedLinearCrossEntropy.apply(
+        hg, weight.cuda(), target.cuda(), denom.cuda(), torch.bfloat16, 512)
+    loss.backward()
+    torch.testing.assert_close(loss.cpu(), tok.cpu().sum() / denom, rtol=1e-6, atol=0)
+    rows = torch.randperm(n, generator=g)[:48]
+    logits = (hidden[rows].float() @ weight.float().t()).to(torch.bfloat16)
+    l_r, e_r, am_r, _, dz_r = ops.ce_rows(logits, target[rows], 1, grad_scale=1.0)
+    torch.testing.assert_close(tok.cpu()[rows].double(), l_r, rtol=1e-4, atol=2e-4)
+    torch.testing.assert_close(ent.cpu()[rows].double(), e_r, rtol=1e-4, atol=2e-4)
+    agree = (pred.cpu()[rows] == am_r).float().mean().item()
+    assert agree >= 0.95  # argmax ties/near-ties of bf16 logits may resolve differently
+    grad_r = (dz_r / float(denom)).to(torch.float64) @ weight.double()
+    scale = grad_r.abs().max().item()
+    torch.testing.assert_close(hg.grad.cpu()[rows].double(), grad_r, rtol=2e-2, atol=2e-2 * scale)

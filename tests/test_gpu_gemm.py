@@ -1,0 +1,78 @@
+"""The MFMA GEMM vs an fp64 CPU product of the same 16-bit inputs.
+
+With fp32 accumulation over K terms of magnitude ~|a||b|, the error bound used is
+  |C - C_ref| <= 2^-22 * K * max|a| * max|b| * 4  + (one rounding of the output dtype).
+"""
+
+import pytest
+import torch
+
+from hackathon_amd import gemm
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(a, b, a_km, b_kn):
+    A = a.double().t() if a_km else a.double()
+    B = b.double() if b_kn else b.double().t()
+    return A @ B
+
+
+def _check(out, ref, K, a, b, out_dtype):
+    bound = 4 * 2.0**-22 * K * a.abs().max().item() * b.abs().max().item()
+    if out_dtype != torch.float32:
+        eps = 2.0**-8 if out_dtype == torch.bfloat16 else 2.0**-11
+        bound = bound + eps * ref.abs()
+    err = (out.double().cpu() - ref).abs()
+    assert torch.all(err <= bound + 1e-30), (err - bound).max().item()
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 384, 512), (130, 250, 72), (1, 3, 8), (4096, 16, 3584),
+                                   (16, 4096, 16), (777, 129, 1000)])
+@pytest.mark.parametrize("a_km,b_kn", [(False, False), (False, True), (True, True), (True, False)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_layouts(M, N, K, a_km, b_kn, dtype):
+    print(f"gemm M={M} N={N} K={K} a_km={a_km} b_kn={b_kn} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    a = torch.randn((K, M) if a_km else (M, K), generator=g).to(dtype)
+    b = torch.randn((K, N) if b_kn else (N, K), generator=g).to(dtype)
+    for out_dtype in (dtype, torch.float32):
+        out = gemm.gemm(a.cuda(), b.cuda(), a_km=a_km, b_kn=b_kn, out_dtype=out_dtype)
+        _check(out, _ref(a, b, a_km, b_kn), K, a, b, out_dtype)
+
+
+def test_gemm_bias_alpha_beta():
+    g = torch.Generator().manual_seed(9)
+    M, N, K = 200, 300, 256
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    c0 = torch.randn(M, N, generator=g)
+    out = c0.clone().cuda()
+    gemm.gemm(a.cuda(), b.cuda(), out=out, bias=bias.cuda(), alpha=0.5, beta=2.0)
+    ref = 0.5 * (a.double() @ b.double().t()) + 2.0 * c0.double() + bias.double()
+    _check(out, ref, K, a, b, torch.float32)
+
+
+def test_linear_and_matmul_helpers_match_torch_shapes():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 3, 64, generator=g).to(torch.bfloat16).cuda()
+    w = torch.randn(48, 64, generator=g).to(torch.bfloat16).cuda()
+    y = gemm.linear(x, w)
+    assert y.shape == (2, 3, 48) and y.dtype == torch.bfloat16
+    torch.testing.assert_close(y.float(), (x.float() @ w.float().t()), rtol=1e-2, atol=1e-2)
+    dy = torch.randn(2, 3, 48, generator=g).to(torch.bfloat16).cuda()
+    dx = gemm.matmul_nn(dy, w)
+    assert dx.shape == (2, 3, 64)
+    torch.testing.assert_close(dx.float(), dy.float() @ w.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_gemm_output_view_with_row_stride():
+    """An output chunk that is a row slice of a bigger buffer (as the CE chunk loop writes)."""
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(96, 64, generator=g).to(torch.bfloat16)
+    b = torch.randn(160, 64, generator=g).to(torch.bfloat16)
+    buf = torch.zeros(200, 160, device="cuda")
+    gemm.gemm(a.cuda(), b.cuda(), out=buf[50:146])
+    _check(buf[50:146], a.double() @ b.double().t(), 64, a, b, torch.float32)
+    assert torch.all(buf[:50] == 0) and torch.all(buf[146:] == 0)

@@ -1,0 +1,123 @@
+"""The composed layers on the GPU: NF4Linear (dequant + MFMA GEMM), the 4-bit LoRA layer and
+the patched Qwen2 MLP, forward and backward, vs CPU references built from the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from hackathon_amd import lora, nf4, quant
+from oracle import nf4 as onf4
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+TABLE = np.array(quant.NF4_CODE, dtype=np.float32)
+
+
+def _deq_ref(packed, st, dtype):
+    bits = onf4.dequant_state(packed, st, TABLE, out="bf16")
+    w = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).view(tuple(st.shape))
+    return w if dtype == torch.bfloat16 else w.float().to(dtype)
+
+
+def _close_gemm(got, want, K, xmax, wmax, dtype):
+    # fp32 accumulation + one output rounding
+    eps = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    bound = 4 * 2.0**-22 * K * xmax * wmax + eps * want.abs() + 1e-30
+    assert torch.all((got.double() - want).abs() <= bound)
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(64, 256, 512, False), (100, 96, 320, True),
+                                        (4096, 512, 3584, True)])
+def test_nf4_linear_fwd_bwd(M, N, K, bias):
+    print(f"NF4Linear M={M} N={N} K={K} bias={bias}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(N, K, generator=g) * 0.02
+    packed, st = quant.quantize_nf4(w, 64)
+    wq = _deq_ref(packed, st, torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, generator=g).to(torch.bfloat16) if bias else None
+    stg = st.to("cuda")
+    xg = x.cuda().requires_grad_()
+    y = nf4.NF4Linear.apply(xg, packed.cuda(), stg, b.cuda() if bias else None)
+    y_ref = x.double() @ wq.double().t() + (b.double() if bias else 0)
+    _close_gemm(y.cpu(), y_ref, K, x.abs().max().item(), wq.abs().max().item(), torch.bfloat16)
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    y.backward(dy.cuda())
+    dx_ref = dy.double() @ wq.double()
+    _close_gemm(xg.grad.cpu(), dx_ref, N, dy.abs().max().item(), wq.abs().max().item(),
+                torch.bfloat16)
+
+
+def test_linear4bit_module_and_original_path():
+    g = torch.Generator().manual_seed(2)
+    w = torch.randn(128, 256, generator=g) * 0.02
+    layer = quant.Linear4bit.from_weight(w, compute_dtype=torch.bfloat16).cuda()
+    layer.weight.quant_state.to("cuda")
+    x = torch.randn(4, 256, generator=g).cuda()
+    y = layer(x)            # fp32 input, bf16 compute, output cast back to fp32
+    assert y.dtype == torch.float32
+    wq = _deq_ref(layer.weight.data.cpu(), layer.weight.quant_state, torch.bfloat16)
+    y_ref = (x.cpu().to(torch.bfloat16).double() @ wq.double().t())
+    torch.testing.assert_close(y.cpu().double(), y_ref, rtol=1e-2, atol=1e-2)
+    # project() keeps the compute dtype
+    assert nf4.project(layer, x).dtype == torch.bfloat16
+
+
+def _lora_layer(in_f, out_f, seed, dropout=0.0):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(out_f, in_f, generator=g) * 0.02
+    base = quant.Linear4bit.from_weight(w, compute_dtype=torch.bfloat16)
+    layer = lora.LoraLinear4bit(base, r=16, lora_alpha=32, lora_dropout=dropout,
+                                compute_dtype=torch.bfloat16)
+    with torch.no_grad():
+        layer.lora_A["default"].weight.normal_(0, 0.25, generator=g)
+        layer.lora_B["default"].weight.normal_(0, 0.01, generator=g)
+    return layer
+
+
+@pytest.mark.parametrize("M,in_f,out_f", [(64, 256, 384), (4096, 3584, 512)])
+def test_lora_layer_fwd_bwd_vs_reference(M, in_f, out_f):
+    """base(x) + 2.0 * B(A(x)) with grads to x, A and B, against an fp64 CPU reference built
+    from the oracle's dequantised weight."""
+    print(f"LoRA layer M={M} in={in_f} out={out_f}", flush=True)
+    layer = _lora_layer(in_f, out_f, seed=M)
+    wq = _deq_ref(layer.base_layer.weight.data, layer.base_layer.weight.quant_state,
+                  torch.bfloat16).double()
+    A = layer.lora_A["default"].weight.detach().clone()
+    B = layer.lora_B["default"].weight.detach().clone()
+    layer = layer.cuda()
+    layer.base_layer.weight.quant_state.to("cuda")
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, in_f, generator=g).to(torch.bfloat16)
+    dy = torch.randn(M, out_f, generator=g).to(torch.bfloat16)
+    xg = x.cuda().requires_grad_()
+    y = layer(xg)
+    y.backward(dy.cuda())
+    # reference in fp64 on the bf16 values the layer computes with
+    xd = x.double().requires_grad_()
+    Ad = A.to(torch.bfloat16).double().requires_grad_()
+    Bd = B.to(torch.bfloat16).double().requires_grad_()
+    y_ref = xd @ wq.t() + 2.0 * ((xd @ Ad.t()) @ Bd.t())
+    y_ref.backward(dy.double())
+    scale = y_ref.abs().max().item()
+    torch.testing.assert_close(y.cpu().double(), y_ref.detach(), rtol=2e-2, atol=2e-2 * scale)
+    for got, want in ((xg.grad, xd.grad), (layer.lora_A["default"].weight.grad, Ad.grad),
+                      (layer.lora_B["default"].weight.grad, Bd.grad)):
+        s = want.abs().max().item()
+        torch.testing.assert_close(got.cpu().double(), want, rtol=2e-2, atol=2e-2 * s)
+
+
+def test_lora_layer_with_dropout_uses_the_reference_mask():
+    layer = _lora_layer(256, 128, seed=3, dropout=0.05).cuda()
+    layer.base_layer.weight.quant_state.to("cuda")
+    layer.train()
+    x = torch.randn(32, 256, device="cuda")
+    lora._Seeds.gen = torch.Generator().manual_seed(99)
+    seed = int(torch.randint(0, 2**31 - 1, (1,), generator=torch.Generator().manual_seed(99)))
+    y = layer(x)
+    xd = ops.dropout_scale(x.cpu(), 0.05, seed, 1 / 0.95, torch.bfloat16)
+    A = layer.lora_A["default"].weight.detach().cpu().to(torch.bfloat16).double()
+    B = layer.lora_B["default"].weight.detach().cpu().to(torch.bfloat16).double()
+    base = layer.base_layer(x).detach().cpu().double()
+    y_ref = base + 2.0 * ((xd.double() @ A.t()) @ B.t())
+    torch.testing.assert_close(y.detach().cpu().double(), y_ref, rtol=2e-2, atol=2e-2)

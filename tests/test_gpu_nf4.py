@@ -1,0 +1,75 @@
+"""NF4 dequant on the GPU vs the C oracle: bit-exact for bf16 and fp32 outputs."""
+
+import numpy as np
+import pytest
+import torch
+
+from hackathon_amd import nf4, quant
+from oracle import nf4 as onf4
+from tests._util import bits16
+
+pytestmark = pytest.mark.gpu
+TABLE = np.array(quant.NF4_CODE, dtype=np.float32)
+
+
+def _case(shape, nested, blocksize, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(shape, generator=g) * 0.02
+    packed, st = quant.quantize_nf4(w, blocksize, compress_statistics=nested)
+    want_bf16 = onf4.dequant_state(packed, st, TABLE, out="bf16")
+    want_f32 = onf4.dequant_state(packed, st, TABLE, out="f32")
+    return packed.cuda(), st.to("cuda"), want_bf16, want_f32
+
+
+@pytest.mark.parametrize("shape,nested,blocksize", [
+    ((4864, 896), True, 64),      # Qwen2.5-0.5B gate_proj, double quant
+    ((4864, 896), False, 64),
+    ((96, 320), True, 64),
+    ((256, 1536), True, 128),
+    ((33, 64), True, 32),
+    ((7, 6), True, 64),           # fewer bytes than one vector group: scalar tail only
+    ((3, 10), False, 64),
+    ((13, 18), True, 6),          # even, non power-of-two blocksize: scalar kernel
+])
+def test_dequant_bit_exact(shape, nested, blocksize):
+    print(f"nf4 dequant {shape} nested={nested} bs={blocksize}", flush=True)
+    packed, st, want_bf16, want_f32 = _case(shape, nested, blocksize)
+    out = nf4.dequantize_nf4(packed, st, torch.bfloat16)
+    assert out.shape == shape and out.dtype == torch.bfloat16
+    np.testing.assert_array_equal(bits16(out).cpu().numpy().reshape(-1).view(np.uint16), want_bf16)
+    out32 = nf4.dequantize_nf4(packed, st, torch.float32)
+    np.testing.assert_array_equal(out32.cpu().numpy().reshape(-1), want_f32)
+    out16 = nf4.dequantize_nf4(packed, st, torch.float16)
+    assert torch.equal(bits16(out16).cpu(),
+                       bits16(torch.from_numpy(want_f32).to(torch.float16)).view(shape))
+
+
+def test_dequant_unaligned_buffers_take_the_exact_path():
+    print("nf4 dequant unaligned", flush=True)
+    packed, st, want_bf16, _ = _case((64, 96), True, 64, seed=5)
+    big = torch.zeros(packed.numel() + 1, dtype=torch.uint8, device="cuda")
+    big[1:] = packed.reshape(-1)
+    out_big = torch.empty(64 * 96 + 1, dtype=torch.bfloat16, device="cuda")
+    out = out_big[1:].view(64, 96)                      # 2-byte aligned only
+    nf4.dequantize_nf4(big[1:], st, torch.bfloat16, out=out)
+    np.testing.assert_array_equal(bits16(out).cpu().numpy().reshape(-1).view(np.uint16), want_bf16)
+
+
+def test_dequant_full_qwen25_7b_gate_shape_bit_exact():
+    """18944 x 3584 (the gate/up projection of the 7B step), the full weight."""
+    print("nf4 dequant 18944x3584", flush=True)
+    packed, st, want_bf16, _ = _case((18944, 3584), True, 64, seed=7)
+    out = nf4.dequantize_nf4(packed, st, torch.bfloat16)
+    got = bits16(out).cpu().numpy().reshape(-1).view(np.uint16)
+    np.testing.assert_array_equal(got, want_bf16)
+
+
+def test_quantizer_on_gpu_matches_cpu():
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(128, 512, generator=g) * 0.02
+    p_cpu, s_cpu = quant.quantize_nf4(w, 64)
+    p_gpu, s_gpu = quant.quantize_nf4(w.cuda(), 64)
+    # codes come from elementwise fp32 ops: identical; the double-quant offset is a mean, whose
+    # summation order may differ between devices in the last bit
+    assert torch.equal(p_cpu, p_gpu.cpu())
+    torch.testing.assert_close(s_cpu.offset, s_gpu.offset.cpu(), rtol=1e-6, atol=0)
