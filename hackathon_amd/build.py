@@ -40,13 +40,20 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-file extra flags. nf4.hip must round the product nf4[code] * scale to fp32 before the
+# conversion to the output type (the reference's order); with contraction allowed the
+# compiler may fuse multiply and conversion into one v_fma_mix with a single rounding.
+FILE_FLAGS = {"nf4.hip": ["-ffp-contract=off"]}
+
+
 def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path) -> tuple[Path, str]:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(CSRC), "-c", str(src),
+           "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{proc.stderr}")

@@ -48,6 +48,14 @@ template <> struct Group8<QL_F32> {
   }
 };
 
+// The fp32 product must be rounded to fp32 before the conversion to the output type. The
+// AMDGPU backend otherwise fuses (fptrunc (fmul a b)) into one v_fma_mixlo_f16 with a single
+// rounding (also under -ffp-contract=off); an empty register barrier keeps the two steps.
+QL_DEV float fp32_rounded(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 // Block scale of block `blk`, exactly as the reference orders the fp32 operations.
 template <bool NESTED>
 QL_DEV float block_scale(int64_t blk, const uint8_t* __restrict__ absmax_q,
@@ -94,8 +102,8 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const uint32_t byte = (word[u] >> (8 * b)) & 0xffu;
-      w[2 * b] = table[byte >> 4] * s;      // high nibble: the first weight of the byte
-      w[2 * b + 1] = table[byte & 15u] * s;  // low nibble: the second
+      w[2 * b] = fp32_rounded(table[byte >> 4] * s);      // high nibble: the first weight
+      w[2 * b + 1] = fp32_rounded(table[byte & 15u] * s);  // low nibble: the second
     }
     Group8<OUT_DT>::store(out, g, w);
   }
@@ -121,8 +129,8 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_scalar(
     s = absmax_f[blk];
   }
   const uint32_t byte = packed[i];
-  Elem<OUT_DT>::store(out, 2 * i, nf4_table[byte >> 4] * s);
-  Elem<OUT_DT>::store(out, 2 * i + 1, nf4_table[byte & 15u] * s);
+  Elem<OUT_DT>::store(out, 2 * i, fp32_rounded(nf4_table[byte >> 4] * s));
+  Elem<OUT_DT>::store(out, 2 * i + 1, fp32_rounded(nf4_table[byte & 15u] * s));
 }
 
 int ilog2_exact(int64_t v) {  // log2 of a power of two, else -1
