@@ -1,0 +1,364 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 QLoRA kernel set on one MI355X; prints ONE JSON line.
+
+Headline (`value`): NF4 dequant HBM GB/s on the Qwen2.5-7B gate/up projection weight
+(18944 x 3584, NF4 blocksize 64, absmax double-quantised with blocksize 256, bf16 output),
+the dequant the 7B QLoRA step runs 392 times per step. A step = one dequant of one weight;
+`--sets` weight/output buffer sets (4 x 171 MB by default) are rotated so the working set
+exceeds the 256 MB Infinity Cache and every step streams from HBM. Inputs are resident in
+HBM before the timed region; the K steps are captured in one HIP graph and replayed, timed
+with HIP events on the stream the kernels run on.
+
+Also reported in the same line:
+  roofline       the dequant kernel against the 8 TB/s HBM peak (algorithmic bytes/launch)
+  cpu_baseline   the C oracle's dequant (oracle/nf4_oracle.c, 1 thread) on a bounded sample
+  nf4_4864x896   the same dequant on the Qwen2.5-0.5B gate_proj weight (32 rotated sets)
+  kernels        per-kernel device time and roofline of the other kernels at their shapes
+  qlora_step     Qwen2.5-7B-shaped QLoRA training step tokens/s, patched vs PyTorch eager
+
+`python bench.py --gpus N --steps K --warmup W`; N > 1 is not run (one GPU only).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+METRIC = "NF4 dequant HBM GB/s (% peak); QLoRA step tokens/s at Qwen2.5-7B shape"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def nf4_algorithmic_bytes(n, blocksize=64, blocksize2=256):
+    """Bytes one dequant call must move: packed nibbles n/2, absmax codes n/bs, second-level
+    scales 4*ceil(nblocks/bs2), bf16 output 2n, plus the 256-entry code2 and 16-entry NF4
+    tables (1088 B)."""
+    nb = math.ceil(n / blocksize)
+    return n // 2 + nb + 4 * math.ceil(nb / blocksize2) + 2 * n + 1088
+
+
+# ---------------------------------------------------------------------------------------------
+def _graph_time(fn_list, torch, replays=1):
+    """Capture the calls in one HIP graph, replay once to warm, then time `replays` replays with
+    events on the current stream. Returns seconds per call."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for f in fn_list[:2]:
+            f()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fn_list:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / (replays * len(fn_list))
+
+
+def bench_nf4(torch, shape, steps, warmup, sets, seed=0):
+    from hackathon_amd import nf4, quant
+
+    n = shape[0] * shape[1]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(shape, device="cuda", generator=g) * 0.02
+    packed, st = quant.quantize_nf4(w, 64, compress_statistics=True)
+    del w
+    bufs = []
+    for i in range(sets):
+        p = packed.clone()
+        s = quant.QuantState(st.absmax.clone(), st.shape, st.code, st.blocksize, offset=st.offset,
+                             state2=quant.QuantState(st.state2.absmax.clone(), code=st.state2.code,
+                                                     blocksize=st.state2.blocksize))
+        out = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+        bufs.append((p, s, out))
+    for i in range(max(warmup, sets)):  # every set once: its scalars are read before capture
+        p, s, o = bufs[i % sets]
+        nf4.dequantize_nf4(p, s, torch.bfloat16, out=o)
+    torch.cuda.synchronize()
+    calls = [(lambda b=bufs[i % sets]: nf4.dequantize_nf4(b[0], b[1], torch.bfloat16, out=b[2]))
+             for i in range(steps)]
+    sec = _graph_time(calls, torch)
+    nbytes = nf4_algorithmic_bytes(n)
+    return dict(sec_per_call=sec, bytes_per_call=nbytes, gbs=nbytes / sec / 1e9, n=n)
+
+
+def cpu_baseline_nf4(seconds, shape=(4864, 896)):
+    """The C oracle (1 thread) dequantising the Qwen2.5-0.5B gate_proj weight repeatedly for
+    about `seconds`; returns GB/s of algorithmic bytes."""
+    import numpy as np
+    import torch
+
+    from hackathon_amd import quant
+    from oracle import nf4 as onf4
+
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(shape, generator=g) * 0.02
+    packed, st = quant.quantize_nf4(w, 64, compress_statistics=True)
+    table = np.array(quant.NF4_CODE, dtype=np.float32)
+    n = shape[0] * shape[1]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        onf4.dequant_state(packed, st, table, out="bf16")
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    nbytes = nf4_algorithmic_bytes(n)
+    return dict(value=round(nbytes * reps / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                sample=f"C oracle nf4 dequant of a {shape[0]}x{shape[1]} weight (bf16 out), "
+                       f"{reps} repetitions in {el:.1f} s on one host thread")
+
+
+# ---------------------------------------------------------------------------------------------
+def bench_kernels(torch):
+    """Device time per call (graph replay) and roofline fraction of the other kernels."""
+    from hackathon_amd import cross_entropy, gemm, nf4, quant, rmsnorm, rope, swiglu
+    from hackathon_amd import _lib
+
+    res = {}
+    dev = "cuda"
+    # RMSNorm at Qwen2.5-1.5B: 4 x 2048 x 1536 bf16
+    M, N = 8192, 1536
+    x = torch.randn(M, N, device=dev).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(N, device=dev)).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    rstd = torch.empty(M, device=dev)
+    dy = torch.randn(M, N, device=dev).to(torch.bfloat16)
+    dx = torch.empty_like(x)
+    s = lambda: _lib.stream_of(x)  # noqa: E731
+
+    def fwd():
+        _lib.call("qlora_rmsnorm_fwd", x.data_ptr(), 2, N, w.data_ptr(), 2, y.data_ptr(), 2, N,
+                  rstd.data_ptr(), M, N, 1e-6, s())
+
+    def bwd():
+        _lib.call("qlora_rmsnorm_bwd", dy.data_ptr(), 2, N, x.data_ptr(), 2, N, w.data_ptr(), 2,
+                  rstd.data_ptr(), dx.data_ptr(), 2, N, M, N, s())
+    for name, fn, nbytes in (("rmsnorm_fwd_8192x1536", fwd, 2 * M * N * 2 + N * 2 + M * 4),
+                             ("rmsnorm_bwd_8192x1536", bwd, 3 * M * N * 2 + N * 2 + M * 4)):
+        t = _graph_time([fn] * 20, torch)
+        res[name] = dict(us=round(t * 1e6, 2), gbs=round(nbytes / t / 1e9, 1),
+                         frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3))
+    # RoPE at Qwen2.5-1.5B: q 4x12x2048x128, k 4x2x2048x128 (B,S,H,D buffers), bf16
+    B, S, HQ, HK, D = 4, 2048, 12, 2, 128
+    q = torch.randn(B, S, HQ, D, device=dev).to(torch.bfloat16).transpose(1, 2)
+    k = torch.randn(B, S, HK, D, device=dev).to(torch.bfloat16).transpose(1, 2)
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev).float() / D))
+    emb = torch.cat([torch.outer(torch.arange(S, device=dev).float(), inv)] * 2, -1)
+    cos, sin = emb.cos()[None].to(torch.bfloat16), emb.sin()[None].to(torch.bfloat16)
+    cos_e, sin_e = cos.expand(B, S, D), sin.expand(B, S, D)
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    rope_bytes = 2 * 2 * B * S * (HQ + HK) * D + 2 * 2 * S * D
+    t = _graph_time([lambda: rope._launch(q, k, cos_e, sin_e, qo, ko, False)] * 20, torch)
+    res["rope_fwd_4x2048x(12+2)x128"] = dict(us=round(t * 1e6, 2), gbs=round(rope_bytes / t / 1e9, 1),
+                                            frac_hbm=round(rope_bytes / t / 1e9 / HBM_PEAK_GBS, 3))
+    # SwiGLU at the 7B MLP: 4096 x 18944 bf16
+    n = 4096 * 18944
+    gt = torch.randn(n, device=dev).to(torch.bfloat16)
+    up = torch.randn(n, device=dev).to(torch.bfloat16)
+    o = torch.empty_like(gt)
+    gr = torch.randn(n, device=dev).to(torch.bfloat16)
+    dg, du = torch.empty_like(gt), torch.empty_like(gt)
+    for name, fn, nbytes in (
+            ("swiglu_fwd_4096x18944", lambda: _lib.call("qlora_swiglu_fwd", gt.data_ptr(), up.data_ptr(),
+                                                       o.data_ptr(), 2, n, s()), 3 * 2 * n),
+            ("swiglu_bwd_4096x18944", lambda: _lib.call("qlora_swiglu_bwd", gr.data_ptr(), gt.data_ptr(),
+                                                       up.data_ptr(), dg.data_ptr(), du.data_ptr(), 2,
+                                                       n, s()), 5 * 2 * n)):
+        t = _graph_time([fn] * 10, torch)
+        res[name] = dict(us=round(t * 1e6, 2), gbs=round(nbytes / t / 1e9, 1),
+                         frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3))
+    del gt, up, o, gr, dg, du
+    # GEMMs of the 7B MLP: x[4096,3584] @ W[18944,3584]^T and dY[4096,18944] @ W
+    for name, (Mm, Nn, Kk, b_kn) in (("gemm_nt_4096x18944x3584", (4096, 18944, 3584, False)),
+                                     ("gemm_nn_4096x3584x18944", (4096, 3584, 18944, True))):
+        a = torch.randn(Mm, Kk, device=dev).to(torch.bfloat16)
+        bm = torch.randn((Kk, Nn) if b_kn else (Nn, Kk), device=dev).to(torch.bfloat16)
+        c = torch.empty(Mm, Nn, device=dev, dtype=torch.bfloat16)
+        t = _graph_time([lambda: gemm.gemm(a, bm, b_kn=b_kn, out=c)] * 5, torch)
+        fl = 2.0 * Mm * Nn * Kk
+        res[name] = dict(us=round(t * 1e6, 1), tflops=round(fl / t / 1e12, 1),
+                         frac_mfma=round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 3))
+        ref = torch.empty_like(c)
+        tt = _graph_time([lambda: torch.matmul(a, bm if b_kn else bm.t(), out=ref)] * 5, torch)
+        res[name]["torch_hipblaslt_tflops"] = round(fl / tt / 1e12, 1)
+        del a, bm, c, ref
+    # fused lm_head + CE at Qwen2.5-1.5B: 8192 x 1536 x 151936 bf16, fwd + dz@W
+    n_rows, H, V = 8192, 1536, 151936
+    hid = torch.randn(n_rows, H, device=dev).to(torch.bfloat16).requires_grad_()
+    W = (torch.randn(V, H, device=dev) * 0.02).to(torch.bfloat16)
+    tgt = torch.randint(0, V, (n_rows,), device=dev)
+    tgt[torch.rand(n_rows, device=dev) < 0.1] = -100
+    denom = (tgt != -100).sum()
+
+    def ce_step():
+        loss, *_ = cross_entropy.FusedLinearCrossEntropy.apply(hid, W, tgt, denom, torch.bfloat16, 512)
+        return loss
+    ce_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        ce_step()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / 3
+    fl = 2 * 2.0 * n_rows * H * V
+    res["fused_ce_8192x1536x151936"] = dict(ms=round(t * 1e3, 2), tflops=round(fl / t / 1e12, 1),
+                                           frac_mfma=round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 3))
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=2048):
+    """Qwen2.5-7B-shaped QLoRA step (28 layers unless `layers`), tokens/s patched and eager."""
+    from hackathon_amd import qlora_step
+
+    over = {} if layers is None else {"num_hidden_layers": layers}
+    cfg = qlora_step.qwen2_config(**over)
+    t0 = time.perf_counter()
+    model = qlora_step.build_qlora_model(cfg, "cuda")
+    torch.cuda.synchronize()
+    log(f"[bench] model built in {time.perf_counter() - t0:.1f} s")
+    ids, labels = qlora_step.make_batch(batch, seq, cfg.vocab_size)
+    tokens = batch * seq
+
+    def run(step, k, w):
+        for _ in range(w):
+            step(ids, labels)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        loss = None
+        for _ in range(k):
+            loss = step(ids, labels)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / k, float(loss)
+
+    qlora_step.patched_mode()
+    step = qlora_step.QLoRAStep(model, fused_head=True)
+    t_p, loss_p = run(step, steps, warmup)
+    log(f"[bench] patched step {t_p * 1e3:.1f} ms loss {loss_p:.4f}")
+    peak_p = torch.cuda.max_memory_allocated() / 2**30
+    torch.cuda.reset_peak_memory_stats()
+    out = dict(tokens_per_step=tokens, ms_per_step=round(t_p * 1e3, 1),
+               tokens_per_s=round(tokens / t_p, 1), loss=round(loss_p, 5),
+               peak_mem_gib=round(peak_p, 1), layers=cfg.num_hidden_layers)
+    if eager_steps:
+        with qlora_step.eager_mode(model):
+            step_e = qlora_step.QLoRAStep(model, fused_head=False)
+            t_e, loss_e = run(step_e, eager_steps, 1)
+        log(f"[bench] eager step {t_e * 1e3:.1f} ms loss {loss_e:.4f}")
+        out.update(eager_ms_per_step=round(t_e * 1e3, 1), eager_tokens_per_s=round(tokens / t_e, 1),
+                   speedup_vs_eager=round(t_e / t_p, 3),
+                   eager_peak_mem_gib=round(torch.cuda.max_memory_allocated() / 2**30, 1))
+        qlora_step.patched_mode()
+    del model, step
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sets", type=int, default=4, help="rotated buffer sets for the dequant")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-step", action="store_true", help="skip the 7B QLoRA step")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
+    ap.add_argument("--step-steps", type=int, default=5)
+    ap.add_argument("--step-layers", type=int, default=None)
+    ap.add_argument("--nf4-only", action="store_true", help="only the dequant (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
+              f"multi-GPU path; see DESIGN.md for how it would shard", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from hackathon_amd import _lib
+
+    _lib.load()  # fail loudly if the kernel library is not built
+    shape = (18944, 3584)
+    torch.cuda.synchronize()
+    r = bench_nf4(torch, shape, args.steps, args.warmup, args.sets)
+    log(f"[bench] nf4 {shape}: {r['sec_per_call'] * 1e6:.2f} us/call, {r['gbs']:.0f} GB/s")
+    line = {
+        "metric": METRIC, "value": round(r["gbs"], 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["sec_per_call"] * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8->bf16 (fp32 math)",
+        "data": "synthetic: N(0,0.02) weights quantised to NF4 in-process",
+        "config": {"workload": "nf4_dequant 18944x3584 (Qwen2.5-7B gate_proj) blocksize 64, "
+                               "double-quant absmax blocksize 256, bf16 out",
+                   "weights": r["n"], "rotated_sets": args.sets, "timing": "HIP graph of "
+                   f"{args.steps} launches, HIP events on the launch stream"},
+        "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": _measured_traffic()},
+    }
+    if args.nf4_only:
+        print(json.dumps(line), flush=True)
+        return
+    r1 = bench_nf4(torch, (4864, 896), max(args.steps, 200), args.warmup, 32, seed=1)
+    line["nf4_4864x896"] = dict(us=round(r1["sec_per_call"] * 1e6, 3), gbs=round(r1["gbs"], 1),
+                                frac_hbm=round(r1["gbs"] / HBM_PEAK_GBS, 4),
+                                bytes=r1["bytes_per_call"], rotated_sets=32)
+    log(f"[bench] nf4 4864x896: {r1['sec_per_call'] * 1e6:.2f} us/call, {r1['gbs']:.0f} GB/s")
+    if not args.no_kernels:
+        line["kernels"] = bench_kernels(torch)
+        log(f"[bench] kernels: {json.dumps(line['kernels'])}")
+    if not args.no_step:
+        line["qlora_step"] = bench_step(torch, args.step_steps, 2, layers=args.step_layers)
+    line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
+    line["cpu_baseline"]["host_cpu"] = _cpu_model()
+    print(json.dumps(line), flush=True)
+
+
+def _measured_traffic():
+    """HBM bytes per dequant launch from the committed rocprofv3 PMC summary, if present."""
+    p = ROOT / "profiles" / "nf4_dequant_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip() + f" ({os.cpu_count()} logical cpus)"
+    except OSError:
+        pass
+    return None
+
+
+if __name__ == "__main__":
+    main()

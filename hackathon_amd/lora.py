@@ -163,6 +163,8 @@ def lora_forward(self, x, *args, **kwargs):
     p = float(drop.p) if isinstance(drop, torch.nn.Dropout) and drop.training else 0.0
     if TORCH_DROPOUT_RNG and p > 0:
         xd = DropoutCast.apply(drop(x), 0.0, 0, compute_dtype)
+    elif p == 0 and x.dtype == compute_dtype:
+        xd = x  # dropout off and no cast to do: the kernel would copy x unchanged
     else:
         xd = DropoutCast.apply(x, p, _Seeds.next() if p > 0 else 0, compute_dtype)
     with torch.autocast("cuda", enabled=False):

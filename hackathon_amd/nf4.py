@@ -42,6 +42,23 @@ def supported(quant_state):
             and (not quant_state.nested or quant_state.state2.blocksize % 2 == 0))
 
 
+def _offset_value(quant_state):
+    """The double-quant offset as a Python float. Reading it from a device tensor
+    synchronises the host (solution/nf4.py:81 does so on every call, 392 times per 7B step)
+    and is not allowed under graph capture, so the value is read once per offset tensor and
+    cached on the state; assigning a new offset tensor invalidates the cache."""
+    off = quant_state.offset
+    cached = getattr(quant_state, "_ql_offset", None)
+    if cached is not None and cached[0] is off:
+        return cached[1]
+    value = float(off)
+    try:
+        quant_state._ql_offset = (off, value)
+    except AttributeError:  # a state object that takes no new attributes
+        pass
+    return value
+
+
 def _scale_args(quant_state):
     """(absmax, nested, code2, absmax2, offset, blocksize2) for the C-ABI (solution/nf4.py:77-86)."""
     if quant_state.nested:
@@ -54,7 +71,7 @@ def _scale_args(quant_state):
         if code2.numel() != 256:
             raise ValueError("the double-quant code map must have 256 entries")
         return (absmax.contiguous(), 1, code2.contiguous(), absmax2.contiguous(),
-                float(quant_state.offset), int(s2.blocksize))
+                _offset_value(quant_state), int(s2.blocksize))
     absmax = quant_state.absmax
     absmax = (absmax if absmax.dtype == torch.float32 else absmax.float()).contiguous()
     return absmax, 0, None, None, 0.0, 1

@@ -1,0 +1,83 @@
+"""The QLoRA training step with every kernel patched vs the eager PyTorch path of the same
+(quantised) model.
+
+Reference: the eager path of the same model in fp32 (same NF4 codes and scales, fp32
+activations and GEMMs). The bf16 paths differ from it by rounding alone, and at random init
+(near-uniform predictions) adapter gradients are small differences of large terms, so both
+bf16 paths sit a few percent from it. The bar:
+  - loss within 1e-4 relative of the fp32 reference (and within 2e-3 of eager bf16);
+  - every adapter gradient at least as close to the fp32 reference as the eager bf16 path's
+    (relative Frobenius error <= 1.25 x eager's + 1e-3).
+"""
+
+import copy
+
+import pytest
+import torch
+
+from hackathon_amd import lora, qlora_step, quant
+
+pytestmark = pytest.mark.gpu
+
+
+def _grads(model):
+    return [p.grad.detach().float().clone() for p in qlora_step.lora_parameters(model)]
+
+
+def _fp32_copy(model):
+    m32 = copy.deepcopy(model).float()
+    for mod in m32.modules():
+        if isinstance(mod, (quant.Linear4bit, lora.LoraLinear4bit)):
+            mod.compute_dtype = torch.float32
+    return m32
+
+
+@pytest.mark.parametrize("shape", ["tiny", "qwen25_7b_2layers"])
+def test_patched_step_matches_fp32_reference(shape):
+    print(f"qlora step {shape}", flush=True)
+    if shape == "tiny":
+        cfg = qlora_step.qwen2_config(hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                      num_attention_heads=4, num_key_value_heads=2,
+                                      vocab_size=1000)
+        batch, seq = 2, 64
+    else:
+        cfg = qlora_step.qwen2_config(num_hidden_layers=2)
+        batch, seq = 2, 2048
+    model = qlora_step.build_qlora_model(cfg, "cuda", seed=0)
+    ids, labels = qlora_step.make_batch(batch, seq, cfg.vocab_size)
+    m32 = _fp32_copy(model)
+    with qlora_step.eager_mode(m32):
+        loss_32 = qlora_step.QLoRAStep(m32, fused_head=False).forward_backward(ids, labels)
+    g_32 = _grads(m32)
+    del m32
+    with qlora_step.eager_mode(model):
+        loss_e = qlora_step.QLoRAStep(model, fused_head=False).forward_backward(ids, labels)
+    g_e = _grads(model)
+    model.zero_grad(set_to_none=True)
+    qlora_step.patched_mode()
+    loss_p = qlora_step.QLoRAStep(model, fused_head=True).forward_backward(ids, labels)
+    g_p = _grads(model)
+    assert torch.isfinite(loss_p)
+    assert abs(loss_p.item() - loss_32.item()) <= 1e-4 * abs(loss_32.item()), (loss_p, loss_32)
+    assert abs(loss_p.item() - loss_e.item()) <= 2e-3 * abs(loss_e.item()), (loss_p, loss_e)
+    for a, b, c in zip(g_p, g_e, g_32):
+        err_p = ((a - c).norm() / c.norm()).item()
+        err_e = ((b - c).norm() / c.norm()).item()
+        assert err_p <= 1.25 * err_e + 1e-3, (err_p, err_e)
+
+
+def test_adamw_step_updates_only_adapters():
+    cfg = qlora_step.qwen2_config(hidden_size=256, intermediate_size=512, num_hidden_layers=1,
+                                  num_attention_heads=4, num_key_value_heads=2, vocab_size=1000)
+    model = qlora_step.build_qlora_model(cfg, "cuda", seed=1)
+    qlora_step.patched_mode()
+    ids, labels = qlora_step.make_batch(2, 32, cfg.vocab_size)
+    before = [p.detach().clone() for p in qlora_step.lora_parameters(model)]
+    head = model.lm_head.weight.detach().clone()
+    step = qlora_step.QLoRAStep(model, lr=1e-3)
+    l0 = step(ids, labels)
+    for _ in range(5):
+        l1 = step(ids, labels)
+    assert l1 < l0  # a few steps on one batch lower its loss
+    assert all(not torch.equal(a, p) for a, p in zip(before, qlora_step.lora_parameters(model)))
+    assert torch.equal(head, model.lm_head.weight)

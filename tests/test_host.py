@@ -1,0 +1,118 @@
+"""Host logic of the façades, on the CPU: patch installation and idempotence, the guards that
+hand unsupported inputs (CPU tensors, unsupported shapes) back to the original code, the
+quantizer's format, and the QLoRA step harness running end to end on the original path."""
+
+import pytest
+import torch
+
+import hackathon_amd
+from hackathon_amd import lora, nf4, qlora_step, quant, rope
+
+
+def test_apply_is_idempotent_and_patches_transformers():
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    hackathon_amd.apply()
+    first = (m.Qwen2RMSNorm.forward, m.apply_rotary_pos_emb, m.Qwen2MLP.forward,
+             m.Qwen2ForCausalLM.forward)
+    hackathon_amd.apply()
+    assert first == (m.Qwen2RMSNorm.forward, m.apply_rotary_pos_emb, m.Qwen2MLP.forward,
+                     m.Qwen2ForCausalLM.forward)
+    for fn in first:
+        assert getattr(fn, "_solution_patch", False)
+
+
+def test_patched_functions_fall_back_on_cpu_tensors():
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    hackathon_amd.apply()
+    norm = m.Qwen2RMSNorm(64, eps=1e-6)
+    norm.weight.requires_grad_(False)
+    x = torch.randn(2, 3, 64)
+    torch.testing.assert_close(norm(x), m.Qwen2RMSNorm.forward._original(norm, x))
+    q = torch.randn(1, 2, 5, 16)
+    k = torch.randn(1, 1, 5, 16)
+    cos, sin = torch.randn(1, 5, 16), torch.randn(1, 5, 16)
+    got = m.apply_rotary_pos_emb(q, k, cos, sin)
+    want = m.apply_rotary_pos_emb._original(q, k, cos, sin)
+    for a, b in zip(got, want):
+        torch.testing.assert_close(a, b)
+
+
+def test_rope_supported_guard():
+    q = torch.randn(2, 4, 5, 16)
+    k = torch.randn(2, 2, 5, 16)
+    c = torch.randn(1, 5, 16)
+    assert not rope._supported(q, k, c, c, 1)          # CPU tensors
+    assert not rope._supported(q, k, c, c, 2)          # other unsqueeze dims
+
+
+def test_nf4_supported_and_prepare_guards():
+    w = torch.randn(32, 64) * 0.02
+    layer = quant.Linear4bit.from_weight(w, compute_dtype=torch.bfloat16)
+    st = layer.weight.quant_state
+    assert nf4.supported(st)
+    assert not nf4.supported(None)
+    assert nf4._prepare(layer, torch.randn(2, 64)) is None   # CPU input: original path
+    y = layer(torch.randn(2, 64))                             # runs the eager original
+    assert y.shape == (2, 32) and y.dtype == torch.float32
+
+
+def test_quantizer_format():
+    w = torch.randn(10, 64) * 0.02
+    packed, st = quant.quantize_nf4(w, 64)
+    assert packed.shape == (320, 1) and packed.dtype == torch.uint8
+    assert st.nested and st.absmax.dtype == torch.uint8 and st.absmax.numel() == 10
+    assert st.state2.code.numel() == 256 and st.state2.blocksize == 256
+    # the largest-magnitude weight of every block maps to code 0 or 15 (+-absmax)
+    codes = torch.stack([packed.view(-1) >> 4, packed.view(-1) & 15], 1).view(10, 64)
+    idx = w.abs().argmax(1)
+    picked = codes[torch.arange(10), idx]
+    assert torch.all((picked == 0) | (picked == 15))
+    # plain (non-nested) state keeps fp32 absmax
+    _, st2 = quant.quantize_nf4(w, 64, compress_statistics=False)
+    assert not st2.nested and st2.absmax.dtype == torch.float32
+    torch.testing.assert_close(st2.absmax, w.abs().amax(1))
+
+
+def test_single_adapter_rules():
+    base = quant.Linear4bit.from_weight(torch.randn(16, 32) * 0.02, compute_dtype=torch.bfloat16)
+    layer = lora.LoraLinear4bit(base, r=4, lora_alpha=8)
+    assert lora._single_adapter(layer) == "default"
+    layer.disable_adapters = True
+    assert lora._single_adapter(layer) is None
+    layer.disable_adapters = False
+    layer.active_adapters = []
+    assert lora._single_adapter(layer) is None
+
+
+def test_seeds_are_reproducible():
+    lora._Seeds.gen = None
+    torch.manual_seed(5)
+    a = [lora._Seeds.next() for _ in range(3)]
+    lora._Seeds.gen = None
+    torch.manual_seed(5)
+    assert [lora._Seeds.next() for _ in range(3)] == a
+
+
+@pytest.mark.parametrize("eager", [True, False])
+def test_qlora_step_harness_runs_on_cpu(eager):
+    """On CPU tensors every patched forward keeps the original path, so the patched and eager
+    modes must give the same loss; AdamW updates only the adapters."""
+    cfg = qlora_step.qwen2_config(hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                                  num_attention_heads=4, num_key_value_heads=2, vocab_size=100)
+    model = qlora_step.build_qlora_model(cfg, "cpu", seed=0, compute_dtype=torch.float32)
+    n_lora = sum(p.numel() for p in qlora_step.lora_parameters(model))
+    assert n_lora == 2 * 16 * (2 * (64 + 64) + 2 * (64 + 32) + 3 * (64 + 128))
+    ids, labels = qlora_step.make_batch(2, 8, cfg.vocab_size, "cpu")
+    before = [p.detach().clone() for p in qlora_step.lora_parameters(model)]
+    frozen = model.model.embed_tokens.weight.detach().clone()
+    if eager:
+        with qlora_step.eager_mode(model):
+            loss = qlora_step.QLoRAStep(model, fused_head=False)(ids, labels)
+    else:
+        qlora_step.patched_mode()
+        loss = qlora_step.QLoRAStep(model, fused_head=True)(ids, labels)
+    assert torch.isfinite(loss)
+    assert any(not torch.equal(a, p) for a, p in zip(before, qlora_step.lora_parameters(model)))
+    assert torch.equal(frozen, model.model.embed_tokens.weight)
