@@ -45,6 +45,9 @@ _SIGNATURES = {
                               _c_i64, _c_i64, _c_i64, _c_f32, _c_ptr],
     "qlora_gemm": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int,
                    _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32, _c_f32, _c_ptr],
+    "qlora_gemm_ws": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+                      _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32, _c_f32, _c_ptr, _c_i64,
+                      _c_ptr],
     "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                       _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
 }
@@ -76,6 +79,8 @@ def load():
             fn.restype = ctypes.c_int
         lib.qlora_strerror.argtypes = [ctypes.c_int]
         lib.qlora_strerror.restype = ctypes.c_char_p
+        lib.qlora_gemm_workspace_size.argtypes = [_c_int, _c_int, _c_i64, _c_i64, _c_i64]
+        lib.qlora_gemm_workspace_size.restype = ctypes.c_int64
         lib.qlora_abi_version.argtypes = []
         lib.qlora_abi_version.restype = ctypes.c_int
         _lib = lib
@@ -84,7 +89,8 @@ def load():
 
 def exported_symbols():
     """Names the binding expects the library to export (used by the ABI tests)."""
-    return sorted(list(_SIGNATURES) + ["qlora_strerror", "qlora_abi_version"])
+    return sorted(list(_SIGNATURES) + ["qlora_strerror", "qlora_abi_version",
+                                       "qlora_gemm_workspace_size"])
 
 
 def check(status: int, what: str) -> None:

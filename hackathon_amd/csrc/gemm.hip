@@ -22,6 +22,7 @@
 //   one output row and 4 consecutive output columns: the epilogue stores 8 B (bf16) or 16 B
 //   (fp32) per lane per 16x16 tile.
 #include "ql_vec.h"
+#include "gemm_nt.h"
 
 namespace {
 
@@ -286,11 +287,13 @@ int dispatch_layout(int a_km, int b_kn, const void* A, int64_t lda, const void* 
 
 }  // namespace
 
-extern "C" int qlora_gemm(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* A,
-                          int64_t lda, const void* B, int64_t ldb, int in_dtype, void* C,
-                          int64_t ldc, int c_dtype, const void* bias, float alpha, float beta,
-                          ql_stream_t stream) {
-  if (M < 0 || N < 0 || K < 0) return QL_EINVAL;
+namespace {
+
+int gemm_checked(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                 const void* B, int64_t ldb, int in_dtype, void* C, int64_t ldc, int c_dtype,
+                 const void* bias, float alpha, float beta, void* ws, int64_t ws_bytes,
+                 hipStream_t s) {
+  if (M < 0 || N < 0 || K < 0 || ws_bytes < 0) return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   if (!ql_valid_dtype(c_dtype)) return QL_EDTYPE;
   if (M == 0 || N == 0) return QL_OK;
@@ -299,7 +302,13 @@ extern "C" int qlora_gemm(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, c
   if (!ql_aligned(A, 2) || !ql_aligned(B, 2) || !ql_aligned(C, ql_elem_size(c_dtype)))
     return QL_EALIGN;
   if (lda < (a_km ? M : K) || ldb < (b_kn ? N : K) || ldc < N) return QL_ESHAPE;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!a_km && !b_kn && ql_gemm_nt_fits(M, N, K, A, lda, B, ldb)) {
+    int splits = ql_gemm_nt_auto_splits(M, N, K);
+    const int64_t need = ql_gemm_nt_workspace_floats(M, N, splits) * (int64_t)sizeof(float);
+    if (need > ws_bytes || !ws || !ql_aligned(ws, 16)) splits = 1;
+    return ql_gemm_nt(in_dtype, c_dtype, M, N, K, A, lda, B, ldb, C, ldc, bias, alpha, beta,
+                      splits, static_cast<float*>(ws), s);
+  }
   if (in_dtype == QL_BF16) {
     QL_DISPATCH_DTYPE(c_dtype, OT,
                       return dispatch_layout<QL_BF16, OT>(a_km, b_kn, A, lda, B, ldb, C, ldc, bias,
@@ -310,4 +319,29 @@ extern "C" int qlora_gemm(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, c
                                                          M, N, K, alpha, beta, s));
   }
   return QL_EDTYPE;
+}
+
+}  // namespace
+
+extern "C" int qlora_gemm(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* A,
+                          int64_t lda, const void* B, int64_t ldb, int in_dtype, void* C,
+                          int64_t ldc, int c_dtype, const void* bias, float alpha, float beta,
+                          ql_stream_t stream) {
+  return gemm_checked(a_km, b_kn, M, N, K, A, lda, B, ldb, in_dtype, C, ldc, c_dtype, bias, alpha,
+                      beta, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t qlora_gemm_workspace_size(int a_km, int b_kn, int64_t M, int64_t N,
+                                             int64_t K) {
+  if (a_km || b_kn || M <= 0 || N <= 0 || K <= 0 || K % 64) return 0;
+  return ql_gemm_nt_workspace_floats(M, N, ql_gemm_nt_auto_splits(M, N, K)) *
+         (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_gemm_ws(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* A,
+                             int64_t lda, const void* B, int64_t ldb, int in_dtype, void* C,
+                             int64_t ldc, int c_dtype, const void* bias, float alpha, float beta,
+                             void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
+  return gemm_checked(a_km, b_kn, M, N, K, A, lda, B, ldb, in_dtype, C, ldc, c_dtype, bias, alpha,
+                      beta, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

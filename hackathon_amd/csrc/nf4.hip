@@ -13,31 +13,34 @@
 // 256 contiguous bytes and each store instruction writes 1 KiB contiguous; a workgroup
 // covers UNROLL such spans with all loads issued before the first store. The 16-entry
 // codebook and the 256-entry code2 table sit in LDS.
+// The 16-bit outputs are written with nontemporal stores: the dequantised weight is 80% of
+// the traffic and is not re-read by this kernel, and streaming it past the caches measured
+// 1.7x faster on MI355X than ordinary stores (24.8 vs 44.4 us for 18944 x 3584). Each such
+// store instruction covers whole 128-B lines (64 lanes x 16 B contiguous); nontemporal
+// stores that leave partial lines were measured far slower, so fp32 output (two 16-B
+// stores per lane, 32 B apart) keeps ordinary stores.
 #include "ql_common.h"
 
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int64_t kSmallGroups = int64_t(1) << 20;  // 8 Mi weights
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <int OUT_DT> struct Group8;  // 8 dequantised weights -> one vector store
 template <> struct Group8<QL_BF16> {
   static QL_DEV void store(uint16_t* out, int64_t g, const float* w) {
-    uint4 v;
-    v.x = pack_bf16x2(w[0], w[1]);
-    v.y = pack_bf16x2(w[2], w[3]);
-    v.z = pack_bf16x2(w[4], w[5]);
-    v.w = pack_bf16x2(w[6], w[7]);
-    reinterpret_cast<uint4*>(out)[g] = v;
+    const u32x4 v = {pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]), pack_bf16x2(w[4], w[5]),
+                     pack_bf16x2(w[6], w[7])};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out) + g);
   }
 };
 template <> struct Group8<QL_F16> {
   static QL_DEV void store(uint16_t* out, int64_t g, const float* w) {
-    uint4 v;
-    v.x = pack_f16x2(w[0], w[1]);
-    v.y = pack_f16x2(w[2], w[3]);
-    v.z = pack_f16x2(w[4], w[5]);
-    v.w = pack_f16x2(w[6], w[7]);
-    reinterpret_cast<uint4*>(out)[g] = v;
+    const u32x4 v = {pack_f16x2(w[0], w[1]), pack_f16x2(w[2], w[3]), pack_f16x2(w[4], w[5]),
+                     pack_f16x2(w[6], w[7])};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out) + g);
   }
 };
 template <> struct Group8<QL_F32> {
@@ -154,13 +157,20 @@ int launch_dequant(const uint8_t* packed, int64_t n_weights, const void* absmax,
   const bool fast = lbs >= 3 && lbs2 >= 0 && ql_aligned(packed, 4) && ql_aligned(out, 16);
   int64_t done = 0;
   if (fast) {
-    constexpr int kUnroll = 2;
     const int64_t n_groups = n_bytes / 4;
-    if (n_groups > 0) {
-      const int64_t grid = (n_groups + kThreads * kUnroll - 1) / (kThreads * kUnroll);
-      hipLaunchKernelGGL((nf4_dequant_vec<OUT_DT, NESTED, kUnroll>), dim3((unsigned)grid),
-                         dim3(kThreads), 0, stream, reinterpret_cast<const uint32_t*>(packed),
-                         n_groups, aq, af, code2, absmax2, offset, lbs, lbs2, table, out);
+    // Two words per lane once the grid has enough workgroups to fill the chip several times
+    // over; smaller weights take one word per lane for twice the workgroups.
+    const auto* p4 = reinterpret_cast<const uint32_t*>(packed);
+    if (n_groups >= kSmallGroups) {
+      const int64_t grid = (n_groups + kThreads * 2 - 1) / (kThreads * 2);
+      hipLaunchKernelGGL((nf4_dequant_vec<OUT_DT, NESTED, 2>), dim3((unsigned)grid),
+                         dim3(kThreads), 0, stream, p4, n_groups, aq, af, code2, absmax2, offset,
+                         lbs, lbs2, table, out);
+    } else if (n_groups > 0) {
+      const int64_t grid = (n_groups + kThreads - 1) / kThreads;
+      hipLaunchKernelGGL((nf4_dequant_vec<OUT_DT, NESTED, 1>), dim3((unsigned)grid),
+                         dim3(kThreads), 0, stream, p4, n_groups, aq, af, code2, absmax2, offset,
+                         lbs, lbs2, table, out);
     }
     done = n_groups * 4;
   }

@@ -32,7 +32,8 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a_km: bool = False, b_kn: bool = F
          out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
          bias: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
     """C = alpha * A @ B^T (+ beta C) (+ bias) with A [M,K] (or stored [K,M] when a_km) and
-    B [N,K] (or stored [K,N] when b_kn), both 2-D, unit stride along their last dim."""
+    B [N,K] (or stored [K,N] when b_kn), both 2-D, unit stride along their last dim.
+    Split-K workspace, when the library asks for one, comes from torch's caching allocator."""
     _lib.require_device(a, b)
     if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"GEMM operands must share dtype bf16/fp16, got {a.dtype}, {b.dtype}")
@@ -47,9 +48,13 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a_km: bool = False, b_kn: bool = F
         raise ValueError("out must be [M, N] with unit stride along N")
     if bias is not None:
         bias = bias.to(a.dtype).contiguous()
-    _lib.call("qlora_gemm", int(a_km), int(b_kn), M, N, K, a.data_ptr(), a.stride(0),
+    ws_bytes = int(_lib.load().qlora_gemm_workspace_size(int(a_km), int(b_kn), M, N, K))
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=out.device) \
+        if ws_bytes > 0 else None
+    _lib.call("qlora_gemm_ws", int(a_km), int(b_kn), M, N, K, a.data_ptr(), a.stride(0),
               b.data_ptr(), b.stride(0), _lib.tag(a.dtype), out.data_ptr(), out.stride(0),
-              _lib.tag(out.dtype), _lib.ptr(bias), float(alpha), float(beta), _lib.stream_of(out))
+              _lib.tag(out.dtype), _lib.ptr(bias), float(alpha), float(beta), _lib.ptr(ws),
+              ws_bytes, _lib.stream_of(out))
     return out
 
 

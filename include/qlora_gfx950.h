@@ -172,6 +172,27 @@ int qlora_gemm(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* 
                const void* B, int64_t ldb, int in_dtype, void* C, int64_t ldc, int c_dtype,
                const void* bias, float alpha, float beta, ql_stream_t stream);
 
+/*
+ * Bytes of workspace qlora_gemm_ws uses for split-K on this problem (0 = it runs unsplit).
+ * Split-K is chosen when the output has too few 256 x 256 tiles to fill the GPU and K is
+ * long: the dz @ W of a logits chunk (K = vocabulary) and skinny outputs. Only plain
+ * k-contiguous operands (a_km = b_kn = 0, K % 64 == 0) are split.
+ * Replaces: the cuBLAS split-K heuristics behind torch.mm in solution/cross_entropy.py:123
+ * and solution/fused_ce.py:143.
+ */
+int64_t qlora_gemm_workspace_size(int a_km, int b_kn, int64_t M, int64_t N, int64_t K);
+
+/*
+ * qlora_gemm with a caller-owned device workspace (16-B aligned) for split-K. With less
+ * workspace than qlora_gemm_workspace_size reports, it runs unsplit. Partials are summed in
+ * split order, so results do not depend on scheduling.
+ * Replaces: the same torch GEMM call sites as qlora_gemm.
+ */
+int qlora_gemm_ws(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const void* A,
+                  int64_t lda, const void* B, int64_t ldb, int in_dtype, void* C, int64_t ldc,
+                  int c_dtype, const void* bias, float alpha, float beta, void* workspace,
+                  int64_t workspace_bytes, ql_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -76,3 +76,57 @@ def test_gemm_output_view_with_row_stride():
     gemm.gemm(a.cuda(), b.cuda(), out=buf[50:146])
     _check(buf[50:146], a.double() @ b.double().t(), 64, a, b, torch.float32)
     assert torch.all(buf[:50] == 0) and torch.all(buf[146:] == 0)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 768, 1024), (300, 520, 192), (257, 255, 64),
+                                   (1000, 3000, 640)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_nt_large_tile_edges(M, N, K, dtype):
+    """k-contiguous operands with K % 64 == 0 take the 256 x 256 tile kernel; M and N edges
+    are loaded clamped and must never be stored."""
+    print(f"gemm_nt M={M} N={N} K={K} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M + 11 * N + K)
+    a = torch.randn(M, K, generator=g).to(dtype)
+    b = torch.randn(N, K, generator=g).to(dtype)
+    ref = a.double() @ b.double().t()
+    for out_dtype in (dtype, torch.float32):
+        buf = torch.full((M + 2, N + 8), 7.0, dtype=out_dtype, device="cuda")
+        out = buf[1:M + 1, 4:N + 4]
+        gemm.gemm(a.cuda(), b.cuda(), out=out)
+        _check(out, ref, K, a, b, out_dtype)
+        assert torch.all(buf[0] == 7) and torch.all(buf[M + 1] == 7)
+        assert torch.all(buf[:, :4] == 7) and torch.all(buf[:, N + 4:] == 7)
+
+
+def test_gemm_nt_bias_alpha_beta_large_tile():
+    g = torch.Generator().manual_seed(19)
+    M, N, K = 384, 320, 256
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    c0 = torch.randn(M, N, generator=g)
+    out = c0.clone().cuda()
+    gemm.gemm(a.cuda(), b.cuda(), out=out, bias=bias.cuda(), alpha=-1.5, beta=0.25)
+    ref = -1.5 * (a.double() @ b.double().t()) + 0.25 * c0.double() + bias.double()
+    _check(out, ref, K, a, b, torch.float32)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 8192), (512, 1536, 30464), (4096, 512, 3584),
+                                   (100, 70, 4096)])
+def test_gemm_split_k_matches_and_is_deterministic(M, N, K):
+    """Small outputs with long K are split over K into an fp32 workspace and summed in split
+    order: the result is within the fp32-accumulation bound and identical run to run."""
+    from hackathon_amd import _lib
+
+    print(f"gemm split-K M={M} N={N} K={K}", flush=True)
+    assert _lib.load().qlora_gemm_workspace_size(0, 0, M, N, K) > 0
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) * 0.1).to(torch.bfloat16)
+    b = (torch.randn(N, K, generator=g) * 0.1).to(torch.bfloat16)
+    ac, bc = a.cuda(), b.cuda()
+    out1 = gemm.gemm(ac, bc, out_dtype=torch.float32)
+    out2 = gemm.gemm(ac, bc, out_dtype=torch.float32)
+    _check(out1, a.double() @ b.double().t(), K, a, b, torch.float32)
+    assert torch.equal(out1, out2)
+    out16 = gemm.gemm(ac, bc, alpha=2.0)
+    _check(out16, 2.0 * (a.double() @ b.double().t()), K, a, b, torch.bfloat16)
