@@ -191,6 +191,7 @@ def bench_kernels(torch):
     del gt, up, o, gr, dg, du
     # GEMMs of the 7B MLP: x[4096,3584] @ W[18944,3584]^T and dY[4096,18944] @ W
     for name, (Mm, Nn, Kk, b_kn) in (("gemm_nt_4096x18944x3584", (4096, 18944, 3584, False)),
+                                     ("gemm_nt_4096x3584x18944", (4096, 3584, 18944, False)),
                                      ("gemm_nn_4096x3584x18944", (4096, 3584, 18944, True))):
         a = torch.randn(Mm, Kk, device=dev).to(torch.bfloat16)
         bm = torch.randn((Kk, Nn) if b_kn else (Nn, Kk), device=dev).to(torch.bfloat16)
@@ -230,7 +231,8 @@ def bench_kernels(torch):
 
 
 # ---------------------------------------------------------------------------------------------
-def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=2048):
+def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=2048,
+               parity=True):
     """Qwen2.5-7B-shaped QLoRA step (28 layers unless `layers`), tokens/s patched and eager."""
     from hackathon_amd import qlora_step
 
@@ -254,14 +256,27 @@ def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=20
         torch.cuda.synchronize()
         return (time.perf_counter() - t) / k, float(loss)
 
+    # loss parity at identical parameters, before any optimizer step
     qlora_step.patched_mode()
     step = qlora_step.QLoRAStep(model, fused_head=True)
+    loss_p0 = loss_e0 = float("nan")
+    if parity:
+        loss_p0 = float(step.forward_backward(ids, labels))
+        model.zero_grad(set_to_none=True)
+        with qlora_step.eager_mode(model):
+            loss_e0 = float(qlora_step.QLoRAStep(model, fused_head=False).forward_backward(ids,
+                                                                                         labels))
+        model.zero_grad(set_to_none=True)
+        qlora_step.patched_mode()
+        log(f"[bench] step-0 loss patched {loss_p0:.6f} eager {loss_e0:.6f}")
     t_p, loss_p = run(step, steps, warmup)
     log(f"[bench] patched step {t_p * 1e3:.1f} ms loss {loss_p:.4f}")
     peak_p = torch.cuda.max_memory_allocated() / 2**30
     torch.cuda.reset_peak_memory_stats()
     out = dict(tokens_per_step=tokens, ms_per_step=round(t_p * 1e3, 1),
                tokens_per_s=round(tokens / t_p, 1), loss=round(loss_p, 5),
+               step0_loss_patched=round(loss_p0, 6), step0_loss_eager=round(loss_e0, 6),
+               step0_loss_rel_diff=round(abs(loss_p0 - loss_e0) / abs(loss_e0), 7),
                peak_mem_gib=round(peak_p, 1), layers=cfg.num_hidden_layers)
     if eager_steps:
         with qlora_step.eager_mode(model):
@@ -288,6 +303,8 @@ def main():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     ap.add_argument("--step-steps", type=int, default=5)
     ap.add_argument("--step-layers", type=int, default=None)
+    ap.add_argument("--eager-steps", type=int, default=2,
+                    help="timed steps of the eager baseline (0: skip it and the parity check)")
     ap.add_argument("--nf4-only", action="store_true", help="only the dequant (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -333,7 +350,8 @@ def main():
         line["kernels"] = bench_kernels(torch)
         log(f"[bench] kernels: {json.dumps(line['kernels'])}")
     if not args.no_step:
-        line["qlora_step"] = bench_step(torch, args.step_steps, 2, layers=args.step_layers)
+        line["qlora_step"] = bench_step(torch, args.step_steps, 2, eager_steps=args.eager_steps,
+                                        layers=args.step_layers, parity=args.eager_steps > 0)
     line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     line["cpu_baseline"]["host_cpu"] = _cpu_model()
     print(json.dumps(line), flush=True)

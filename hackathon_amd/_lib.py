@@ -48,8 +48,26 @@ _SIGNATURES = {
     "qlora_gemm_ws": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
                       _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32, _c_f32, _c_ptr, _c_i64,
                       _c_ptr],
+    "qlora_nf4_dequant_t": [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_f32, _c_int,
+                            _c_int, _c_ptr, _c_ptr, _c_i64, _c_int, _c_ptr],
+    "qlora_transpose16": [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr],
+    "qlora_gemm_nt_cat": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr,
+                          _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32,
+                          _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64,
+                        _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_f32,
+                         _c_ptr, _c_i64, _c_ptr],
     "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                       _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
+}
+
+# name -> argtypes; these return a byte count (int64)
+_SIZE_QUERIES = {
+    "qlora_gemm_workspace_size": [_c_int, _c_int, _c_i64, _c_i64, _c_i64],
+    "qlora_gemm_nt_cat_workspace_size": [_c_i64, _c_i64, _c_i64],
+    "qlora_lora_down_workspace_size": [_c_i64, _c_i64],
+    "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64],
 }
 
 _lib = None
@@ -79,8 +97,10 @@ def load():
             fn.restype = ctypes.c_int
         lib.qlora_strerror.argtypes = [ctypes.c_int]
         lib.qlora_strerror.restype = ctypes.c_char_p
-        lib.qlora_gemm_workspace_size.argtypes = [_c_int, _c_int, _c_i64, _c_i64, _c_i64]
-        lib.qlora_gemm_workspace_size.restype = ctypes.c_int64
+        for name, argtypes in _SIZE_QUERIES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int64
         lib.qlora_abi_version.argtypes = []
         lib.qlora_abi_version.restype = ctypes.c_int
         _lib = lib
@@ -89,8 +109,8 @@ def load():
 
 def exported_symbols():
     """Names the binding expects the library to export (used by the ABI tests)."""
-    return sorted(list(_SIGNATURES) + ["qlora_strerror", "qlora_abi_version",
-                                       "qlora_gemm_workspace_size"])
+    return sorted(list(_SIGNATURES) + list(_SIZE_QUERIES) + ["qlora_strerror",
+                                                             "qlora_abi_version"])
 
 
 def check(status: int, what: str) -> None:
@@ -122,6 +142,15 @@ def require_device(*tensors: torch.Tensor) -> None:
 
 def i64_array(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+
+
+def workspace(name: str, *sizes, device) -> tuple:
+    """(fp32 tensor or None, bytes) holding the workspace the size query `name` asks for,
+    from torch's caching allocator (16-B aligned)."""
+    nbytes = int(getattr(load(), name)(*sizes))
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device), nbytes
 
 
 def call(name: str, *args) -> None:

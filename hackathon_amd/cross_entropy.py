@@ -7,7 +7,9 @@ The full logits never exist. Rows go through in chunks of CHUNK_ROWS tokens
   2. one workgroup per row, two sweeps over the vocab:  qlora_ce_rows (ignore_mode 1)
        sweep 1: online max / log-sum-exp, sum(p*z) for the entropy, first argmax, z[label]
        sweep 2: dz = (softmax - onehot) * GRAD_GAIN / denominator, IN PLACE over the chunk
-  3. grad_h_chunk = dz @ W                               qlora_gemm, fp32 output
+  3. grad_h_chunk = dz @ W                               qlora_gemm_ws, fp32 output, against
+                                                         the cached W^T (k = vocabulary
+                                                         contiguous), split over K
 The hidden gradient is taken in forward (the head is frozen); backward only rescales it.
 """
 
@@ -76,7 +78,7 @@ class FusedLinearCrossEntropy(torch.autograd.Function):
                          pred[start:stop], grad_scale, with_grad)
                 if with_grad:
                     if mm16:
-                        _gemm.gemm(logits, w, b_kn=True, out=grad_h[start:stop])
+                        _gemm.gemm(logits, _gemm.transposed_frozen(w), out=grad_h[start:stop])
                     else:
                         grad_h[start:stop] = logits @ w
             del w, buf

@@ -345,3 +345,35 @@ extern "C" int qlora_gemm_ws(int a_km, int b_kn, int64_t M, int64_t N, int64_t K
   return gemm_checked(a_km, b_kn, M, N, K, A, lda, B, ldb, in_dtype, C, ldc, c_dtype, bias, alpha,
                       beta, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
+
+extern "C" int64_t qlora_gemm_nt_cat_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K < 0 || K % 64) return 0;
+  return ql_gemm_nt_workspace_floats(M, N, ql_gemm_nt_auto_splits(M, N, K)) *
+         (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                                 const void* B, int64_t ldb, int64_t K2, const void* A2,
+                                 int64_t lda2, const void* B2, int64_t ldb2, int in_dtype, void* C,
+                                 int64_t ldc, int c_dtype, const void* bias, float alpha,
+                                 void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || K2 < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
+  if (!ql_valid_dtype(c_dtype)) return QL_EDTYPE;
+  if (M == 0 || N == 0) return QL_OK;
+  if (!C || (K > 0 && (!A || !B)) || (K2 > 0 && (!A2 || !B2))) return QL_EINVAL;
+  if (K % 64 || K2 % 64 || K + K2 == 0) return QL_ESHAPE;
+  if (lda < K || ldb < K || ldc < N || (K2 > 0 && (lda2 < K2 || ldb2 < K2))) return QL_ESHAPE;
+  if (!ql_aligned(C, ql_elem_size(c_dtype))) return QL_EALIGN;
+  if (K > 0 && !ql_gemm_nt_fits(M, N, K, A, lda, B, ldb)) return QL_EALIGN;
+  if (K2 > 0 && !ql_gemm_nt_fits(M, N, K2, A2, lda2, B2, ldb2)) return QL_EALIGN;
+  if (K == 0) {  // the second segment alone
+    A = A2; lda = lda2; B = B2; ldb = ldb2; K = K2; K2 = 0; A2 = B2 = nullptr;
+  }
+  int splits = ql_gemm_nt_auto_splits(M, N, K);
+  const int64_t need = ql_gemm_nt_workspace_floats(M, N, splits) * (int64_t)sizeof(float);
+  if (need > workspace_bytes || !workspace || !ql_aligned(workspace, 16)) splits = 1;
+  return ql_gemm_nt2(in_dtype, c_dtype, M, N, K, A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc,
+                     bias, alpha, 0.f, splits, static_cast<float*>(workspace),
+                     static_cast<hipStream_t>(stream));
+}

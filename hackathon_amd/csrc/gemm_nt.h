@@ -21,3 +21,10 @@ int64_t ql_gemm_nt_workspace_floats(int64_t M, int64_t N, int splits);
 int ql_gemm_nt(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias,
                float alpha, float beta, int splits, float* ws, hipStream_t s);
+
+// C = alpha * (A @ B^T + A2 @ B2^T) (+ beta C) (+ bias): a second k-contiguous segment with
+// K2 % 64 == 0 columns (A2 [M, K2], B2 [N, K2], same alignment rules; K2 = 0: none).
+int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
+                int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
+                const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
+                float alpha, float beta, int splits, float* ws, hipStream_t s);

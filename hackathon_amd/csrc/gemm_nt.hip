@@ -21,6 +21,10 @@
 //   - workgroup ids are remapped so that the tiles one XCD runs at a time are neighbours
 //     (XCDs take workgroups round-robin; each has its own L2), then rastered in groups of 4
 //     tile rows so that concurrently running tiles share A and B panels in L2;
+//   - a second K segment C += A2 B2^T (K2 % 64 == 0, same M and N) can follow the first:
+//     the rank-16 LoRA term of a LoRA linear rides along as one extra K step of the base
+//     GEMM (x W^T + u (sB)^T with u, sB zero-padded to 64 columns) instead of separate
+//     skinny GEMMs and an elementwise add;
 //   - split-K: blockIdx.y selects a K range; each split writes an fp32 partial tile to a
 //     caller-provided workspace and `splitk_reduce` sums the partials in split order
 //     (deterministic) and applies alpha / beta / bias / the output type.
@@ -118,7 +122,7 @@ QL_DEV void mma_step(f32x4_t (&acc)[8][8], char* __restrict__ cur, char* __restr
                      int64_t M, int64_t N, int64_t k_next, int wm, int wn, int fr, int fq) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (k_next >= 0) {
+  if (k_next >= 0) {  // A, B, lda, ldb: the segment the next K step belongs to
     load_tile(la, A, lda, m0, M, k_next, nxt);
     load_tile(la, B, ldb, n0, N, k_next, nxt + kTileBytes);
   }
@@ -163,7 +167,9 @@ QL_DEV void mma_step(f32x4_t (&acc)[8][8], char* __restrict__ cur, char* __restr
 template <int IT, int OT, bool PARTIAL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
-                    int64_t ldb, typename Elem<OT>::T* __restrict__ C, int64_t ldc,
+                    int64_t ldb, const uint16_t* __restrict__ A2, int64_t lda2,
+                    const uint16_t* __restrict__ B2, int64_t ldb2, int64_t K2,
+                    typename Elem<OT>::T* __restrict__ C, int64_t ldc,
                     float* __restrict__ ws, const uint16_t* __restrict__ bias, int64_t M,
                     int64_t N, int64_t K, int64_t k_per_split, float alpha, float beta,
                     bool vec_out) {
@@ -173,7 +179,9 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
   const int64_t m0 = tm * BM, n0 = tn * BN;
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = (kb + k_per_split < K) ? kb + k_per_split : K;
-  const int nk = (int)((ke - kb) / BK);
+  const int nk1 = (int)((ke - kb) / BK);
+  // the second segment (A2 B2^T, K2 columns) is appended to the last split
+  const int nk = nk1 + ((int)blockIdx.y == (int)gridDim.y - 1 ? (int)(K2 / BK) : 0);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -187,15 +195,18 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const TileLoader la = make_loader();
   if (nk > 0) {
-    load_tile(la, A, lda, m0, M, kb, smem);
-    load_tile(la, B, ldb, n0, N, kb, smem + kTileBytes);
+    const bool s1 = nk1 > 0;
+    load_tile(la, s1 ? A : A2, s1 ? lda : lda2, m0, M, s1 ? kb : 0, smem);
+    load_tile(la, s1 ? B : B2, s1 ? ldb : ldb2, n0, N, s1 ? kb : 0, smem + kTileBytes);
   }
-
   for (int kt = 0; kt < nk; ++kt) {
     char* cur = smem + (kt & 1) * kStageBytes;
     char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
-    mma_step<IT>(acc, cur, nxt, la, A, lda, B, ldb, m0, n0, M, N,
-                 kt + 1 < nk ? kb + (int64_t)(kt + 1) * BK : -1, wm, wn, fr, fq);
+    const int nx = kt + 1;
+    const bool s1 = nx < nk1;
+    const int64_t k_next = nx >= nk ? -1 : s1 ? kb + (int64_t)nx * BK : (int64_t)(nx - nk1) * BK;
+    mma_step<IT>(acc, cur, nxt, la, s1 ? A : A2, s1 ? lda : lda2, s1 ? B : B2, s1 ? ldb : ldb2,
+                 m0, n0, M, N, k_next, wm, wn, fr, fq);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -268,9 +279,10 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
 }
 
 template <int IT, int OT>
-int launch(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
-           const void* bias, int64_t M, int64_t N, int64_t K, float alpha, float beta,
-           int splits, float* ws, hipStream_t s) {
+int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
+           const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
+           int64_t M, int64_t N, int64_t K, float alpha, float beta, int splits, float* ws,
+           hipStream_t s) {
   using T = typename Elem<OT>::T;
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int64_t kps = ((K / BK + splits - 1) / splits) * BK;
@@ -278,13 +290,15 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int6
   if (nsplit <= 1) {
     const bool vec_out = ql_aligned(C, 4 * ql_elem_size(OT)) && ldc % 4 == 0;
     hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false>), dim3((unsigned)tiles, 1), dim3(kThreads), 0, s,
-                       (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (T*)C, ldc, nullptr,
+                       (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2,
+                       lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc, nullptr,
                        (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
     return ql_launch_status();
   }
   hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true>), dim3((unsigned)tiles, (unsigned)nsplit),
                      dim3(kThreads), 0, s,
-                     (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (float*)nullptr, (int64_t)0,
+                     (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
+                     (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0,
                      ws, (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false);
   int st = ql_launch_status();
   if (st != QL_OK) return st;
@@ -317,18 +331,28 @@ int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
   return s;
 }
 
+int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
+                int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
+                const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
+                float alpha, float beta, int splits, float* ws, hipStream_t s) {
+  if (splits > 1 && !ws) return QL_EINVAL;
+  if (K2 < 0 || K2 % BK) return QL_EINVAL;
+  if (K2 == 0) A2 = B2 = nullptr;
+  if (in_dtype == QL_BF16) {
+    QL_DISPATCH_DTYPE(c_dtype, OT,
+                      return launch<QL_BF16, OT>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc,
+                                                 bias, M, N, K, alpha, beta, splits, ws, s));
+  } else if (in_dtype == QL_F16) {
+    QL_DISPATCH_DTYPE(c_dtype, OT,
+                      return launch<QL_F16, OT>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc,
+                                                bias, M, N, K, alpha, beta, splits, ws, s));
+  }
+  return QL_EDTYPE;
+}
+
 int ql_gemm_nt(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias,
                float alpha, float beta, int splits, float* ws, hipStream_t s) {
-  if (splits > 1 && !ws) return QL_EINVAL;
-  if (in_dtype == QL_BF16) {
-    QL_DISPATCH_DTYPE(c_dtype, OT,
-                      return launch<QL_BF16, OT>(A, lda, B, ldb, C, ldc, bias, M, N, K, alpha,
-                                                 beta, splits, ws, s));
-  } else if (in_dtype == QL_F16) {
-    QL_DISPATCH_DTYPE(c_dtype, OT,
-                      return launch<QL_F16, OT>(A, lda, B, ldb, C, ldc, bias, M, N, K, alpha,
-                                                beta, splits, ws, s));
-  }
-  return QL_EDTYPE;
+  return ql_gemm_nt2(in_dtype, c_dtype, M, N, K, A, lda, B, ldb, nullptr, 0, nullptr, 0, 0, C,
+                     ldc, bias, alpha, beta, splits, ws, s);
 }

@@ -1,0 +1,371 @@
+// Rank-16 LoRA contractions on CDNA4 matrix cores, for gfx950.
+//
+// The adapter GEMMs of a LoRA layer (the nn.Linear pair of solution/lora.py:172 and what
+// autograd computes for it) are skinny: one side is the rank r = 16. As plain GEMMs they
+// leave most of the GPU idle (a 4096 x 16 output is 32 tiles of 128 x 128). Two kernels
+// cover them, both streaming the large operand from HBM exactly once:
+//
+//   lora_down   out[m, c] = alpha * sum_k X[m, k] * Y[c, k]        (c < 16)
+//               u = x A^T (forward) and du = s * g B (backward, Y = B^T): X [M, K]
+//               k-contiguous, Y [16, K] k-contiguous. Output bf16/fp16 [M, ldo] with
+//               columns 16 .. out_cols-1 zero-filled, so it can serve as the extra
+//               K = 64 segment of the base GEMM.
+//   lora_wgrad  out[n, c] = alpha * sum_m Q[m, n] * P[m, c]        (c < 16), fp32 [N, 16]
+//               dB = s * g^T u and dA^T = x^T du: the reduction runs over the token rows,
+//               which are the strided dimension of both operands.
+//
+// lora_down: one workgroup (4 waves) per 16 rows and K range. A v_mfma_f32_16x16x32 needs
+// 8 consecutive k per lane; the sum over k does not care which 8, so lane l reads 64
+// contiguous bytes of row l%16 (k = 32*(l/16) .. +31 of a 128-k chunk) with four 16-B loads
+// and feeds them to four MFMAs; Y is read with the same k map. Waves take alternate 128-k
+// chunks and are summed through LDS.
+//
+// lora_wgrad: one workgroup per 128 columns and M range. Lane l loads an 8 (rows) x 8
+// (columns) block of Q as eight 16-B row pieces (lanes 0-15 of a row read 256 contiguous
+// bytes), transposes it in registers with byte permutes into eight fragments that each hold
+// 8 consecutive rows of one column, and multiplies them by the fragment of P for the same 8
+// rows: MFMA t accumulates columns n0 + 8*(l%16) + t. Waves take alternate 32-row chunks and
+// are summed through LDS.
+//
+// Both kernels optionally split their reduction over blockIdx.y into an fp32 workspace,
+// summed in split order by the matching reduce kernel (deterministic).
+#include "ql_vec.h"
+#include "lora_mfma.h"
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+constexpr int kThreads = 256;
+constexpr int kRank = 16;
+
+template <int DT> QL_DEV f32x4_t mfma(const uint4& a, const uint4& b, f32x4_t c);
+template <> QL_DEV f32x4_t mfma<QL_BF16>(const uint4& a, const uint4& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+template <> QL_DEV f32x4_t mfma<QL_F16>(const uint4& a, const uint4& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Sum a per-lane f32x4 over the 4 waves of the workgroup; the result is valid in wave 0.
+QL_DEV f32x4_t wave_reduce4(f32x4_t v, f32x4_t* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  red[wave * 64 + lane] = v;
+  __syncthreads();
+  f32x4_t s = red[lane];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) s += red[w * 64 + lane];
+  __syncthreads();
+  return s;
+}
+
+// ---------------------------------------------------------------------------------------
+template <int IT, int OT, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void lora_down_kernel(
+    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
+    int64_t M, int64_t K, int64_t k_per_split, float* __restrict__ ws,
+    typename Elem<OT>::T* __restrict__ out, int64_t ldo, int out_cols, float alpha) {
+  __shared__ f32x4_t red[4 * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m0 = (int64_t)blockIdx.x * 16;
+  const int64_t row = m0 + (lane & 15);
+  const int64_t rowc = row < M ? row : M - 1;
+  const int64_t kb = (int64_t)blockIdx.y * k_per_split;
+  const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
+  const int koff = 32 * (lane >> 4);
+  const uint16_t* xr = X + rowc * ldx;
+  const uint16_t* yr = Y + (int64_t)(lane & 15) * ldy;
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  for (int64_t k = kb + 128 * wave; k < ke; k += 512) {  // uniform per wave
+    const int64_t kk = k + koff;
+    // K and every chunk start are multiples of 32, so a lane's 32 k are all in or all out.
+    // Lanes past the end contribute zeros: the MFMAs below must run with every lane's
+    // operands defined, so they are not placed under a lane-dependent branch.
+    const bool ok = kk < ke;
+    uint4 xv[4], yv[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      xv[t] = ok ? *reinterpret_cast<const uint4*>(xr + kk + 8 * t) : make_uint4(0, 0, 0, 0);
+      yv[t] = ok ? *reinterpret_cast<const uint4*>(yr + kk + 8 * t) : make_uint4(0, 0, 0, 0);
+    }
+    acc0 = mfma<IT>(yv[0], xv[0], acc0);
+    acc1 = mfma<IT>(yv[1], xv[1], acc1);
+    acc0 = mfma<IT>(yv[2], xv[2], acc0);
+    acc1 = mfma<IT>(yv[3], xv[3], acc1);
+  }
+  const f32x4_t s = wave_reduce4(acc0 + acc1, red);
+  if (wave != 0 || row >= M) return;
+  // lane holds out[row][c .. c+3], c = 4 * (lane / 16)
+  const int c = 4 * (lane >> 4);
+  if constexpr (PARTIAL) {
+    *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * kRank + c) =
+        make_float4(s[0], s[1], s[2], s[3]);
+  } else {
+    auto* o = out + row * ldo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[c + e] = Elem<OT>::from_f32(alpha * s[e]);
+    for (int z = kRank + c; z < out_cols; z += 16)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (z + e < out_cols) o[z + e] = Elem<OT>::from_f32(0.f);
+  }
+}
+
+template <int OT>
+__global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict__ ws, int splits,
+                                                        int64_t M, typename Elem<OT>::T* __restrict__ out,
+                                                        int64_t ldo, int out_cols, float alpha) {
+  const int64_t total = M * out_cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / out_cols;
+    const int c = (int)(i - m * out_cols);
+    float v = 0.f;
+    if (c < kRank) {
+      for (int z = 0; z < splits; ++z) v += ws[((int64_t)z * M + m) * kRank + c];
+      v *= alpha;
+    }
+    out[m * ldo + c] = Elem<OT>::from_f32(v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// 8 x 8 transpose of 16-bit values: in[i] holds row i (8 columns as 4 words, column pairs);
+// out[t] holds column t (8 rows as 4 words, row pairs).
+QL_DEV void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint4& r0 = in[2 * p];
+      const uint4& r1 = in[2 * p + 1];
+      const uint32_t a = (t >> 1) == 0 ? r0.x : (t >> 1) == 1 ? r0.y : (t >> 1) == 2 ? r0.z : r0.w;
+      const uint32_t b = (t >> 1) == 0 ? r1.x : (t >> 1) == 1 ? r1.y : (t >> 1) == 2 ? r1.z : r1.w;
+      // even column: low halves of a and b; odd column: high halves
+      w[p] = (t & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
+                     : __builtin_amdgcn_perm(b, a, 0x05040100u);
+    }
+    out[t] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <int IT, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
+    const uint16_t* __restrict__ P, int64_t ldp, const uint16_t* __restrict__ Q, int64_t ldq,
+    int64_t M, int64_t N, int64_t m_per_split, float* __restrict__ ws, float* __restrict__ out,
+    float alpha) {
+  __shared__ f32x4_t red[4 * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cg = lane & 15;                 // column group: columns n0 + 8 cg .. +7
+  const int mq = lane >> 4;                 // rows 8 mq .. 8 mq + 7 of a 32-row chunk
+  const int64_t n0 = (int64_t)blockIdx.x * 128;
+  const int64_t ncol = n0 + 8 * cg;
+  const bool col_ok = ncol < N;             // N % 8 == 0: a group is all in or all out
+  const int64_t mb = (int64_t)blockIdx.y * m_per_split;
+  const int64_t me = mb + m_per_split < M ? mb + m_per_split : M;
+  f32x4_t acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int64_t m = mb + 32 * wave; m < me; m += 128) {
+    const int64_t r0 = m + 8 * mq;
+    uint4 q[8];
+    uint16_t pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool ok = r0 + i < me;
+      const int64_t rc = ok ? r0 + i : mb;  // an in-range row; its values are dropped
+      q[i] = (ok && col_ok) ? *reinterpret_cast<const uint4*>(Q + rc * ldq + ncol)
+                            : make_uint4(0, 0, 0, 0);
+      pv[i] = ok ? P[rc * ldp + cg] : (uint16_t)0;
+    }
+    const uint4 pf = make_uint4((uint32_t)pv[0] | ((uint32_t)pv[1] << 16),
+                                (uint32_t)pv[2] | ((uint32_t)pv[3] << 16),
+                                (uint32_t)pv[4] | ((uint32_t)pv[5] << 16),
+                                (uint32_t)pv[6] | ((uint32_t)pv[7] << 16));
+    uint4 qt[8];
+    transpose8x8(q, qt);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = mfma<IT>(pf, qt[t], acc[t]);
+  }
+  // acc[t]: lane holds out[n = n0 + 8*(lane%16) + t][c = 4*(lane/16) .. +3]
+  const int c = 4 * (lane >> 4);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const f32x4_t s = wave_reduce4(acc[t], red);
+    if (wave == 0 && col_ok) {
+      const int64_t n = ncol + t;
+      if constexpr (PARTIAL) {
+        *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * N + n) * kRank + c) =
+            make_float4(s[0], s[1], s[2], s[3]);
+      } else {
+        *reinterpret_cast<float4*>(out + n * kRank + c) =
+            make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
+                                                         int64_t N, float* __restrict__ out,
+                                                         float alpha) {
+  const int64_t total = N * kRank;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (int z = 0; z < splits; ++z) v += ws[(int64_t)z * total + i];
+    out[i] = alpha * v;
+  }
+}
+
+unsigned grid1d(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 4096) g = 4096;
+  return (unsigned)(g > 0 ? g : 1);
+}
+
+}  // namespace
+
+// ---- host side -------------------------------------------------------------------------
+
+int ql_lora_down_splits(int64_t M, int64_t K) {
+  const int64_t groups = (M + 15) / 16;
+  int s = 1;
+  while (groups * s < 1024 && K / (512 * 2 * s) >= 1 && s < 64) s *= 2;
+  return s;
+}
+
+int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K) {
+  const int s = ql_lora_down_splits(M, K);
+  return s > 1 ? (int64_t)s * M * kRank : 0;
+}
+
+int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* Y,
+                 int64_t ldy, int64_t M, int64_t K, void* out, int64_t ldo, int out_cols,
+                 float alpha, float* ws, int64_t ws_floats, hipStream_t s) {
+  if (M <= 0 || K <= 0 || K % 32 || out_cols < kRank || ldo < out_cols) return QL_EINVAL;
+  if (ldx % 8 || ldy % 8 || !ql_aligned(X, 16) || !ql_aligned(Y, 16)) return QL_EALIGN;
+  if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
+  if (out_dtype != QL_BF16 && out_dtype != QL_F16 && out_dtype != QL_F32) return QL_EDTYPE;
+  int splits = ql_lora_down_splits(M, K);
+  if (ws_floats < (int64_t)splits * M * kRank || !ws) splits = 1;
+  // per-split K range: a multiple of 512 (4 waves x 128 k)
+  int64_t kps = ((K + splits - 1) / splits + 511) / 512 * 512;
+  splits = (int)((K + kps - 1) / kps);
+  const dim3 grid((unsigned)((M + 15) / 16), (unsigned)splits);
+#define QL_DOWN(IT, OT)                                                                      \
+  do {                                                                                       \
+    using T = typename Elem<OT>::T;                                                          \
+    if (splits == 1) {                                                                       \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false>), grid, dim3(kThreads), 0, s,      \
+                         (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,        \
+                         (float*)nullptr, (T*)out, ldo, out_cols, alpha);                    \
+    } else {                                                                                 \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true>), grid, dim3(kThreads), 0, s,       \
+                         (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps, ws,    \
+                         (T*)out, ldo, out_cols, alpha);                                     \
+      hipLaunchKernelGGL((lora_down_reduce<OT>), dim3(grid1d(M * out_cols)), dim3(256), 0,   \
+                         s, ws, splits, M, (T*)out, ldo, out_cols, alpha);                   \
+    }                                                                                        \
+  } while (0)
+  if (in_dtype == QL_BF16) {
+    if (out_dtype == QL_BF16) QL_DOWN(QL_BF16, QL_BF16);
+    else if (out_dtype == QL_F16) QL_DOWN(QL_BF16, QL_F16);
+    else QL_DOWN(QL_BF16, QL_F32);
+  } else {
+    if (out_dtype == QL_BF16) QL_DOWN(QL_F16, QL_BF16);
+    else if (out_dtype == QL_F16) QL_DOWN(QL_F16, QL_F16);
+    else QL_DOWN(QL_F16, QL_F32);
+  }
+#undef QL_DOWN
+  return ql_launch_status();
+}
+
+int ql_lora_wgrad_splits(int64_t M, int64_t N) {
+  const int64_t blocks = (N + 127) / 128;
+  int s = 1;
+  while (blocks * s < 512 && M / (128 * 2 * s) >= 1 && s < 64) s *= 2;
+  return s;
+}
+
+int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N) {
+  const int s = ql_lora_wgrad_splits(M, N);
+  return s > 1 ? (int64_t)s * N * kRank : 0;
+}
+
+int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64_t ldq,
+                  int64_t M, int64_t N, float* out, float alpha, float* ws, int64_t ws_floats,
+                  hipStream_t s) {
+  if (M <= 0 || N <= 0 || N % 8 || ldp < kRank) return QL_EINVAL;
+  if (ldq % 8 || !ql_aligned(Q, 16) || !ql_aligned(P, 2) || !ql_aligned(out, 16)) return QL_EALIGN;
+  if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
+  int splits = ql_lora_wgrad_splits(M, N);
+  if (ws_floats < (int64_t)splits * N * kRank || !ws) splits = 1;
+  int64_t mps = ((M + splits - 1) / splits + 127) / 128 * 128;
+  splits = (int)((M + mps - 1) / mps);
+  const dim3 grid((unsigned)((N + 127) / 128), (unsigned)splits);
+#define QL_WGRAD(IT)                                                                         \
+  do {                                                                                       \
+    if (splits == 1) {                                                                       \
+      hipLaunchKernelGGL((lora_wgrad_kernel<IT, false>), grid, dim3(kThreads), 0, s,         \
+                         (const uint16_t*)P, ldp, (const uint16_t*)Q, ldq, M, N, mps,        \
+                         (float*)nullptr, out, alpha);                                       \
+    } else {                                                                                 \
+      hipLaunchKernelGGL((lora_wgrad_kernel<IT, true>), grid, dim3(kThreads), 0, s,          \
+                         (const uint16_t*)P, ldp, (const uint16_t*)Q, ldq, M, N, mps, ws,    \
+                         out, alpha);                                                        \
+      hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0, s, ws,    \
+                         splits, N, out, alpha);                                             \
+    }                                                                                        \
+  } while (0)
+  if (in_dtype == QL_BF16) QL_WGRAD(QL_BF16);
+  else QL_WGRAD(QL_F16);
+#undef QL_WGRAD
+  return ql_launch_status();
+}
+
+// ---- C-ABI -------------------------------------------------------------------------------
+
+extern "C" int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0) return 0;
+  return ql_lora_down_workspace_floats(M, K) * (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_t ldy, int64_t M,
+                               int64_t K, int in_dtype, void* out, int64_t ldo, int out_cols,
+                               int out_dtype, float alpha, void* workspace,
+                               int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || K < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (M == 0) return QL_OK;
+  if (!X || !Y || !out) return QL_EINVAL;
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  return ql_lora_down(in_dtype, out_dtype, X, ldx, Y, ldy, M, K, out, ldo, out_cols, alpha,
+                      static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 0;
+  return ql_lora_wgrad_workspace_floats(M, N) * (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_lora_wgrad(const void* P, int64_t ldp, const void* Q, int64_t ldq, int64_t M,
+                                int64_t N, int in_dtype, float* out, float alpha, void* workspace,
+                                int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || N < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (N == 0) return QL_OK;
+  if (!P || !Q || !out) return QL_EINVAL;
+  if (M == 0) {  // an empty reduction: zeros (a fill kernel, not a memset node)
+    hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), (const float*)nullptr, 0, N,
+                       out, 0.f);
+    return ql_launch_status();
+  }
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  return ql_lora_wgrad(in_dtype, P, ldp, Q, ldq, M, N, out, alpha, static_cast<float*>(workspace),
+                       workspace_bytes / (int64_t)sizeof(float), static_cast<hipStream_t>(stream));
+}

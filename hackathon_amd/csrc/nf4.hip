@@ -136,6 +136,75 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_scalar(
   Elem<OUT_DT>::store(out, 2 * i + 1, fp32_rounded(nf4_table[byte & 15u] * s));
 }
 
+// Transposed dequantisation: outT[k][n] = W[n][k] for W [rows, cols] (row-major, packed two
+// per byte along k). The backward of the 4-bit linear needs dY @ W; with W^T stored [cols,
+// rows] that contraction is k-contiguous on both operands. One workgroup per tile of 64 rows
+// (n) x 128 columns (k): thread t dequantises 16 consecutive k of the rows 2p and 2p+1
+// (p = t % 32, k-chunk t / 32), packs each (n, n+1) pair into one 32-bit LDS word of the
+// [k][n] tile, and the tile leaves as 128 rows of 64 n = 128 contiguous bytes each, written
+// with nontemporal 16-B stores (8 lanes per row). Same per-weight arithmetic as above, so
+// outT is bit-identical to the transpose of the plain dequantisation.
+constexpr int kTRows = 64, kTCols = 128;
+constexpr int kTStride = 36;  // LDS words per k-row of the tile (32 used, 16-B aligned rows)
+
+template <int OUT_DT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
+    const uint8_t* __restrict__ packed, int64_t rows, int64_t cols,
+    const uint8_t* __restrict__ absmax_q, const float* __restrict__ absmax_f,
+    const float* __restrict__ code2, const float* __restrict__ absmax2, float offset, int log2_bs,
+    int log2_bs2, const float* __restrict__ nf4_table, uint16_t* __restrict__ outT,
+    int64_t ld_out) {
+#pragma clang fp contract(off)
+  __shared__ float table[16];
+  __shared__ float code2_lds[NESTED ? 256 : 1];
+  __shared__ __attribute__((aligned(16))) uint32_t tile[kTCols * kTStride];
+  if (threadIdx.x < 16) table[threadIdx.x] = nf4_table[threadIdx.x];
+  if constexpr (NESTED) code2_lds[threadIdx.x] = code2[threadIdx.x];  // kThreads == 256
+  __syncthreads();
+
+  const int64_t k0 = (int64_t)blockIdx.x * kTCols;
+  const int64_t n0 = (int64_t)blockIdx.y * kTRows;
+  const int p = threadIdx.x & 31, kc = threadIdx.x >> 5;
+  const int64_t k = k0 + 16 * kc;
+  float w[2][16];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t n = n0 + 2 * p + h;
+    if (n < rows) {
+      const int64_t j = n * cols + k;  // first weight index; j % 16 == 0
+      const uint2 b = *reinterpret_cast<const uint2*>(packed + j / 2);
+      const float s =
+          block_scale<NESTED>(j >> log2_bs, absmax_q, absmax_f, code2_lds, absmax2, offset, log2_bs2);
+      const uint32_t bw[2] = {b.x, b.y};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t byte = (bw[q >> 2] >> (8 * (q & 3))) & 0xffu;
+        w[h][2 * q] = fp32_rounded(table[byte >> 4] * s);
+        w[h][2 * q + 1] = fp32_rounded(table[byte & 15u] * s);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) w[h][q] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const uint32_t v = OUT_DT == QL_BF16 ? pack_bf16x2(w[0][q], w[1][q]) : pack_f16x2(w[0][q], w[1][q]);
+    tile[(16 * kc + q) * kTStride + p] = v;
+  }
+  __syncthreads();
+  const int c = threadIdx.x & 7;
+  const int64_t n = n0 + 8 * c;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kr = (threadIdx.x >> 3) + 32 * i;
+    if (n < rows) {  // rows % 8 == 0: a 16-B chunk is entirely in or out
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[kr * kTStride + 4 * c]);
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(outT + (k0 + kr) * ld_out + n));
+    }
+  }
+}
+
 int ilog2_exact(int64_t v) {  // log2 of a power of two, else -1
   if (v <= 0 || (v & (v - 1))) return -1;
   int l = 0;
@@ -207,4 +276,36 @@ extern "C" int qlora_nf4_dequant(const uint8_t* packed, int64_t n_weights, const
                                                        s));
   }
   return QL_EDTYPE;
+}
+
+extern "C" int qlora_nf4_dequant_t(const uint8_t* packed, int64_t rows, int64_t cols,
+                                   const void* absmax, int nested, const float* code2,
+                                   const float* absmax2, float offset, int blocksize,
+                                   int blocksize2, const float* nf4_table, void* out_t,
+                                   int64_t ld_out, int out_dtype, ql_stream_t stream) {
+  if (rows < 0 || cols < 0 || ld_out < rows) return QL_EINVAL;
+  if (rows == 0 || cols == 0) return QL_OK;
+  if (!packed || !absmax || !nf4_table || !out_t) return QL_EINVAL;
+  if (out_dtype != QL_BF16 && out_dtype != QL_F16) return QL_EDTYPE;
+  const int lbs = ilog2_exact(blocksize);
+  if (lbs < 4) return QL_EINVAL;  // a power of two >= 16
+  if (nested && (!code2 || !absmax2 || ilog2_exact(blocksize2) < 0)) return QL_EINVAL;
+  if (cols % kTCols || rows % 8 || ld_out % 8) return QL_ESHAPE;
+  if (!ql_aligned(packed, 8) || !ql_aligned(out_t, 16)) return QL_EALIGN;
+  const int lbs2 = nested ? ilog2_exact(blocksize2) : 0;
+  const dim3 grid((unsigned)(cols / kTCols), (unsigned)((rows + kTRows - 1) / kTRows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* aq = nested ? static_cast<const uint8_t*>(absmax) : nullptr;
+  const float* af = nested ? nullptr : static_cast<const float*>(absmax);
+  uint16_t* o = static_cast<uint16_t*>(out_t);
+#define QL_DQT(DT, NST)                                                                        \
+  hipLaunchKernelGGL((nf4_dequant_t_kernel<DT, NST>), grid, dim3(kThreads), 0, s, packed, rows, \
+                     cols, aq, af, code2, absmax2, offset, lbs, lbs2, nf4_table, o, ld_out)
+  if (out_dtype == QL_BF16) {
+    if (nested) QL_DQT(QL_BF16, true); else QL_DQT(QL_BF16, false);
+  } else {
+    if (nested) QL_DQT(QL_F16, true); else QL_DQT(QL_F16, false);
+  }
+#undef QL_DQT
+  return ql_launch_status();
 }

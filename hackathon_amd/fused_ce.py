@@ -52,9 +52,10 @@ def _head_gemm(h, w, out):
 
 
 def _grad_gemm(dz, w, out):
-    """out (fp32) = dz @ w."""
+    """out (fp32) = dz @ w, run as dz @ (w^T)^T against the cached transpose of the frozen
+    head weight, so both operands are k-contiguous (the vocabulary is the reduction)."""
     if dz.dtype in (torch.float16, torch.bfloat16):
-        _gemm.gemm(dz, w, b_kn=True, out=out)
+        _gemm.gemm(dz, _gemm.transposed_frozen(w), out=out)
     else:
         out.copy_(torch.mm(dz, w))
 

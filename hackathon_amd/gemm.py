@@ -8,6 +8,8 @@ bf16 or fp16 on a GPU; they are made unit-stride along their contiguous dimensio
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _lib
@@ -75,3 +77,76 @@ def matmul_nn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 def matmul_tn(a: torch.Tensor, b: torch.Tensor, out_dtype=None) -> torch.Tensor:
     """a^T @ b for a [K, M] and b [K, N], both stored row-major (reduction over rows)."""
     return gemm(_rows(a), _rows(b), a_km=True, b_kn=True, out_dtype=out_dtype)
+
+
+def transpose16(t: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """t.T as a contiguous [cols, rows] tensor (16-bit dtypes), by the library's tiled
+    transpose; `out` may be a wider buffer view whose rows are `rows` long."""
+    _lib.require_device(t)
+    if t.element_size() != 2 or t.dim() != 2:
+        raise TypeError("transpose16 takes a 2-D 16-bit tensor")
+    t2 = t if t.stride(-1) == 1 else t.contiguous()
+    rows, cols = t2.shape
+    if out is None:
+        out = torch.empty((cols, rows), dtype=t.dtype, device=t.device)
+    _lib.call("qlora_transpose16", t2.data_ptr(), rows, cols, t2.stride(0), out.data_ptr(),
+              out.stride(0), _lib.stream_of(t2))
+    return out
+
+
+_T_CACHE: dict = {}
+
+
+def transposed_frozen(w: torch.Tensor) -> torch.Tensor:
+    """w.T, contiguous, kept while `w` is alive and unmodified (same storage, same version).
+    For frozen weights read every step in the other orientation (the lm_head in dz @ W):
+    the transpose is paid once, not per call."""
+    key = id(w)
+    hit = _T_CACHE.get(key)
+    if hit is not None:
+        ref, ptr, version, wt = hit
+        if ref() is w and ptr == w.data_ptr() and version == w._version:
+            return wt
+    for k in [k for k, v in _T_CACHE.items() if v[0]() is None]:
+        del _T_CACHE[k]
+    wt = transpose16(w)
+    _T_CACHE[key] = (weakref.ref(w), w.data_ptr(), w._version, wt)
+    return wt
+
+
+def gemm_nt_cat(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None,
+                b2: torch.Tensor | None, out: torch.Tensor, bias: torch.Tensor | None = None,
+                alpha: float = 1.0) -> torch.Tensor:
+    """out = alpha * (a @ b^T + a2 @ b2^T) (+ bias) in one NT GEMM over the concatenated K
+    (qlora_gemm_nt_cat). All operands 2-D, unit stride along K, K and K2 multiples of 64."""
+    M, K = a.shape
+    N = b.shape[0]
+    K2 = 0 if a2 is None else a2.shape[1]
+    ws, ws_bytes = _lib.workspace("qlora_gemm_nt_cat_workspace_size", M, N, K, device=out.device)
+    _lib.call("qlora_gemm_nt_cat", M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+              K2, _lib.ptr(a2), a2.stride(0) if a2 is not None else 0, _lib.ptr(b2),
+              b2.stride(0) if b2 is not None else 0, _lib.tag(a.dtype), out.data_ptr(),
+              out.stride(0), _lib.tag(out.dtype), _lib.ptr(bias), float(alpha), _lib.ptr(ws),
+              ws_bytes, _lib.stream_of(out))
+    return out
+
+
+def lora_down(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+    """out[:, :16] = alpha * x @ y^T (y [16, K]) and out[:, 16:] = 0 (qlora_lora_down)."""
+    M, K = x.shape
+    ws, ws_bytes = _lib.workspace("qlora_lora_down_workspace_size", M, K, device=x.device)
+    _lib.call("qlora_lora_down", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), M, K,
+              _lib.tag(x.dtype), out.data_ptr(), out.stride(0), out.shape[1], _lib.tag(out.dtype),
+              float(alpha), _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+    return out
+
+
+def lora_wgrad(p: torch.Tensor, q: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+    """fp32 [N, 16] = alpha * q^T @ p[:, :16] for q [M, N], p [M, >=16] (qlora_lora_wgrad)."""
+    M, N = q.shape
+    out = torch.empty((N, 16), dtype=torch.float32, device=q.device)
+    ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_workspace_size", M, N, device=q.device)
+    _lib.call("qlora_lora_wgrad", p.data_ptr(), p.stride(0), q.data_ptr(), q.stride(0), M, N,
+              _lib.tag(q.dtype), out.data_ptr(), float(alpha), _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(q))
+    return out

@@ -9,6 +9,9 @@ Here (solution/lora.py:8-17):
                            1/(1-p) scale, cast to the compute dtype  -> qlora_lora_dropout_scale
     lo  = lora_B(lora_A(xd))                                        -> qlora_gemm (x2)
     out = ScaledAdd(result, lo, scaling) in fp32                    -> qlora_lora_scaled_add
+With dropout off and rank 16 on an NF4 base (the QLoRA step), the layer instead runs as
+`LoraNF4Linear`: the adapter term rides inside the base GEMM as one extra K step, and the
+adapter gradients come from dedicated rank-16 reduction kernels.
 peft is not installed in this environment, so `LoraLinear4bit` below carries the attribute
 surface the patched forward reads (base_layer, lora_A/lora_B/lora_dropout ModuleDicts,
 scaling, active_adapters, disable_adapters, merged) and always runs the patched forward.
@@ -129,6 +132,101 @@ class LoRALinearFn(torch.autograd.Function):
         return dx, da, db
 
 
+_PAD = 64  # rank-16 factors are zero-padded to one 64-wide K step of the NT GEMM
+
+
+class LoraNF4Linear(torch.autograd.Function):
+    """The whole 4-bit LoRA linear (p = 0, rank 16) as one MFMA GEMM per direction:
+
+        forward   u = x A^T                       qlora_lora_down  -> [M, 64], cols >= 16 zero
+                  y = [x | u] [W | s B]^T + bias   qlora_gemm_nt_cat (W dequantised first)
+        backward  du = s g B                      qlora_lora_down  (Y = B^T)
+                  dx = [g | du] [W^T | A^T]^T      qlora_gemm_nt_cat (W^T dequantised directly)
+                  dB = s g^T u,  dA = du^T x       qlora_lora_wgrad (reductions over tokens)
+
+    The same sums as base_layer(x) + ScaledAdd(B(A(x))) of solution/lora.py:157-173 with the
+    adapter term accumulated in fp32 inside the base GEMM instead of rounded to the compute
+    dtype and added in a separate pass; u, du and s*B are the compute-dtype values the
+    reference's autocast GEMMs see (s = alpha / r = 2 scales B exactly)."""
+
+    @staticmethod
+    def forward(ctx, x, a_weight, b_weight, packed, quant_state, bias, scaling):
+        from . import nf4
+
+        x2 = x.reshape(-1, x.shape[-1]).contiguous()
+        dt = x2.dtype
+        M, K = x2.shape
+        N = int(quant_state.shape[0])
+        w = nf4.dequantize_nf4(packed, quant_state, dt)
+        a16 = a_weight.to(dt).contiguous()
+        u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
+        _gemm.lora_down(x2, a16, u)
+        bs = torch.zeros((N, _PAD), dtype=dt, device=x2.device)
+        bs[:, :16] = (b_weight.detach() * scaling).to(dt)
+        y = torch.empty((M, N), dtype=dt, device=x2.device)
+        _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=None if bias is None else bias.to(dt))
+        del w
+        ctx.save_for_backward(x2, u, a16, b_weight)
+        ctx.packed, ctx.quant_state, ctx.scaling = packed, quant_state, float(scaling)
+        ctx.shape, ctx.wdtypes = x.shape, (a_weight.dtype, b_weight.dtype)
+        return y.view(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, g):
+        from . import nf4
+
+        x2, u, a16, b_weight = ctx.saved_tensors
+        dt = x2.dtype
+        M, K = x2.shape
+        g2 = _rows(g)
+        if g2.dtype != dt:
+            g2 = g2.to(dt)
+        g2 = g2.contiguous()
+        N = g2.shape[1]
+        s = ctx.scaling
+        bt = b_weight.detach().t().to(dt).contiguous()                  # [16, N]
+        du = torch.empty((M, _PAD), dtype=dt, device=g2.device)
+        _gemm.lora_down(g2, bt, du, alpha=s)
+        dx = da = db = None
+        if ctx.needs_input_grad[0]:
+            wt = nf4.dequantize_nf4_t(ctx.packed, ctx.quant_state, dt)  # [K, N]
+            at = torch.zeros((K, _PAD), dtype=dt, device=g2.device)
+            _gemm.transpose16(a16, out=at)                              # at[:, :16] = A^T
+            dx = torch.empty((M, K), dtype=dt, device=g2.device)
+            _gemm.gemm_nt_cat(g2, wt, du, at, dx)
+            del wt
+            dx = dx.view(ctx.shape)
+        if ctx.needs_input_grad[1]:
+            da = _gemm.lora_wgrad(du, x2).t().contiguous().to(ctx.wdtypes[0])  # [16, K]
+        if ctx.needs_input_grad[2]:
+            db = _gemm.lora_wgrad(u, g2, alpha=s).to(ctx.wdtypes[1])   # [N, 16]
+        return dx, da, db, None, None, None, None
+
+
+def _fused_base(layer, adapter, x, compute_dtype, p):
+    """(packed, quant_state, bias) when the layer can run as LoraNF4Linear, else None:
+    dropout off, rank 16, a frozen NF4 base whose shapes the k-contiguous kernels take."""
+    from . import nf4
+
+    if p != 0 or compute_dtype not in (torch.bfloat16, torch.float16):
+        return None
+    base = layer.base_layer
+    weight = getattr(base, "weight", None)
+    qs = getattr(weight, "quant_state", None)
+    if qs is None or not nf4.supported(qs) or weight.requires_grad or not weight.is_cuda:
+        return None
+    bias = getattr(base, "bias", None)
+    if bias is not None and bias.requires_grad:
+        return None
+    a_w, b_w = layer.lora_A[adapter].weight, layer.lora_B[adapter].weight
+    out_f, in_f = (int(d) for d in qs.shape)
+    if a_w.shape != (16, in_f) or b_w.shape != (out_f, 16):
+        return None
+    if in_f % 128 or out_f % 64 or not nf4.transposed_dequant_ok(qs):
+        return None
+    return weight, qs, bias
+
+
 def _single_adapter(layer):
     """The one active plain-Linear adapter, or None (solution/lora.py:127-142)."""
     if layer.disable_adapters or layer.merged:
@@ -158,9 +256,18 @@ def lora_forward(self, x, *args, **kwargs):
         adapter = _single_adapter(self)
     if adapter is None:
         return None
-    result = self.base_layer(x)
     drop = self.lora_dropout[adapter]
     p = float(drop.p) if isinstance(drop, torch.nn.Dropout) and drop.training else 0.0
+    fused = _fused_base(self, adapter, x, compute_dtype, p)
+    if fused is not None:
+        weight, qs, bias = fused
+        xc = x if x.dtype == compute_dtype else x.to(compute_dtype)
+        with torch.autocast("cuda", enabled=False):
+            y = LoraNF4Linear.apply(xc, self.lora_A[adapter].weight, self.lora_B[adapter].weight,
+                                    weight, qs, bias, self.scaling[adapter])
+        out_dtype = torch.promote_types(x.dtype, compute_dtype)
+        return y if y.dtype == out_dtype else y.to(out_dtype)
+    result = self.base_layer(x)
     if TORCH_DROPOUT_RNG and p > 0:
         xd = DropoutCast.apply(drop(x), 0.0, 0, compute_dtype)
     elif p == 0 and x.dtype == compute_dtype:

@@ -96,6 +96,33 @@ def dequantize_nf4(packed, quant_state, dtype=torch.float16, out=None):
     return out
 
 
+def dequantize_nf4_t(packed, quant_state, dtype=torch.bfloat16, out=None):
+    """The TRANSPOSED weight [in_features, out_features] in `dtype` (bit-identical to
+    dequantize_nf4(...).t()), for the k-contiguous backward GEMM dY @ W."""
+    rows, cols = tuple(quant_state.shape)
+    _lib.require_device(packed)
+    if out is None:
+        out = torch.empty((cols, rows), dtype=dtype, device=packed.device)
+    absmax, nested, code2, absmax2, offset, blocksize2 = _scale_args(quant_state)
+    _lib.call("qlora_nf4_dequant_t", packed.reshape(-1).data_ptr(), rows, cols, absmax.data_ptr(),
+              nested, _lib.ptr(code2), _lib.ptr(absmax2), offset, int(quant_state.blocksize),
+              blocksize2, _nf4_table(packed.device).data_ptr(), out.data_ptr(), out.stride(0),
+              _lib.tag(out.dtype), _lib.stream_of(out))
+    return out
+
+
+def transposed_dequant_ok(quant_state):
+    """Whether dequantize_nf4_t takes this weight: in_features % 128 == 0,
+    out_features % 8 == 0, blocksize a power of two >= 16."""
+    rows, cols = tuple(quant_state.shape)
+    bs = int(quant_state.blocksize)
+    ok = cols % 128 == 0 and rows % 8 == 0 and bs >= 16 and bs & (bs - 1) == 0
+    if ok and quant_state.nested:
+        bs2 = int(quant_state.state2.blocksize)
+        ok = bs2 > 0 and bs2 & (bs2 - 1) == 0
+    return ok
+
+
 class NF4Linear(torch.autograd.Function):
     """y = x @ W.T + b with W rebuilt by the dequant kernel in forward and again in backward
     (solution/nf4.py:95-112). Weight and bias are frozen."""
@@ -111,8 +138,16 @@ class NF4Linear(torch.autograd.Function):
     def backward(ctx, grad_out):
         grad_x = None
         if ctx.needs_input_grad[0]:
-            weight = dequantize_nf4(ctx.packed, ctx.quant_state, grad_out.dtype)
-            grad_x = _gemm.matmul_nn(grad_out, weight)
+            qs = ctx.quant_state
+            rows = tuple(qs.shape)[0]
+            if grad_out.dtype in (torch.bfloat16, torch.float16) and transposed_dequant_ok(qs) \
+                    and rows % 64 == 0:
+                # dY @ W as an NT GEMM against W^T, dequantised straight into that layout
+                weight_t = dequantize_nf4_t(ctx.packed, qs, grad_out.dtype)
+                grad_x = _gemm.linear(grad_out, weight_t)
+            else:
+                weight = dequantize_nf4(ctx.packed, qs, grad_out.dtype)
+                grad_x = _gemm.matmul_nn(grad_out, weight)
         return grad_x, None, None, None
 
 

@@ -193,6 +193,72 @@ int qlora_gemm_ws(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const voi
                   int c_dtype, const void* bias, float alpha, float beta, void* workspace,
                   int64_t workspace_bytes, ql_stream_t stream);
 
+/*
+ * NF4 dequantisation into the TRANSPOSED layout: out_t[k * ld_out + n] = W[n][k] for the
+ * weight W [rows, cols] that qlora_nf4_dequant would produce row-major; bit-identical
+ * values. The backward of the 4-bit linear (solution/nf4.py:110-111, grad_x = dY @ W) then
+ * runs as a k-contiguous GEMM against W^T.
+ * Replaces: solution/nf4.py:25-49 + :110 (the re-dequantisation in NF4Linear.backward).
+ * Requires cols % 128 == 0, rows % 8 == 0, ld_out % 8 == 0, blocksize a power of two >= 16
+ * (blocksize2 a power of two when nested), packed 8-B and out_t 16-B aligned (else
+ * QL_ESHAPE / QL_EINVAL / QL_EALIGN); out_dtype QL_BF16 or QL_F16.
+ */
+int qlora_nf4_dequant_t(const uint8_t* packed, int64_t rows, int64_t cols, const void* absmax,
+                        int nested, const float* code2, const float* absmax2, float offset,
+                        int blocksize, int blocksize2, const float* nf4_table, void* out_t,
+                        int64_t ld_out, int out_dtype, ql_stream_t stream);
+
+/*
+ * 16-bit transpose: out[c * ld_out + r] = in[r * ld_in + c] for r < rows, c < cols.
+ * Lays out k-contiguous operands: the frozen lm_head weight for dz @ W
+ * (solution/cross_entropy.py:123, solution/fused_ce.py:143) and the LoRA factors.
+ */
+int qlora_transpose16(const void* in, int64_t rows, int64_t cols, int64_t ld_in, void* out,
+                      int64_t ld_out, ql_stream_t stream);
+
+/*
+ * NT GEMM over two concatenated K segments (bf16/fp16 operands, fp32 accumulation):
+ *   C[M,N] = alpha * (A[M,K] B[N,K]^T + A2[M,K2] B2[N,K2]^T) (+ bias[n])
+ * K and K2 multiples of 64; all four operands k-contiguous, 16-B aligned, leading dimensions
+ * multiples of 8. With the rank-16 LoRA factors zero-padded to 64 columns this is the whole
+ * 4-bit LoRA linear in one GEMM: y = x W^T + u (s B)^T with u = x A^T (forward) and
+ * dx = g (W^T)^T + du A^T-padded (backward).
+ * Replaces: solution/nf4.py:102,111 (F.linear / matmul on the dequantised weight) together
+ * with solution/lora.py:49-60,172 (the adapter GEMMs and the fp32 scaled add).
+ * Workspace (16-B aligned) enables split-K; see qlora_gemm_nt_cat_workspace_size.
+ */
+int64_t qlora_gemm_nt_cat_workspace_size(int64_t M, int64_t N, int64_t K);
+int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* B,
+                      int64_t ldb, int64_t K2, const void* A2, int64_t lda2, const void* B2,
+                      int64_t ldb2, int in_dtype, void* C, int64_t ldc, int c_dtype,
+                      const void* bias, float alpha, void* workspace, int64_t workspace_bytes,
+                      ql_stream_t stream);
+
+/*
+ * LoRA down-projection (rank 16): out[m, c] = alpha * sum_k X[m,k] Y[c,k] for c < 16, and
+ * out[m, c] = 0 for 16 <= c < out_cols (the zero padding the GEMM segment above reads).
+ * u = x A^T in forward (Y = A [16, in]); du = s * g B in backward (Y = B^T [16, out]).
+ * K % 32 == 0; X, Y 16-B aligned with ldx, ldy multiples of 8; in_dtype QL_BF16/QL_F16;
+ * out_dtype QL_BF16/QL_F16/QL_F32. Streams X from HBM once.
+ * Replaces: solution/lora.py:172 (lora_A(x)) and its autograd backward through lora_B.
+ */
+int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K);
+int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_t ldy, int64_t M, int64_t K,
+                    int in_dtype, void* out, int64_t ldo, int out_cols, int out_dtype,
+                    float alpha, void* workspace, int64_t workspace_bytes, ql_stream_t stream);
+
+/*
+ * LoRA weight gradient (rank 16), a reduction over the token rows:
+ *   out[n, c] = alpha * sum_m Q[m, n] * P[m, c]      (fp32 [N, 16], c < 16)
+ * dB = s * g^T u (P = u, Q = g); dA^T = x^T du (P = du, Q = x).
+ * N % 8 == 0; Q 16-B aligned with ldq a multiple of 8; P [M, ldp >= 16]; out 16-B aligned.
+ * Replaces: the autograd weight gradients of solution/lora.py:172 (lora_A / lora_B).
+ */
+int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N);
+int qlora_lora_wgrad(const void* P, int64_t ldp, const void* Q, int64_t ldq, int64_t M, int64_t N,
+                     int in_dtype, float* out, float alpha, void* workspace,
+                     int64_t workspace_bytes, ql_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

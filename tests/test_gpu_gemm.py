@@ -130,3 +130,77 @@ def test_gemm_split_k_matches_and_is_deterministic(M, N, K):
     assert torch.equal(out1, out2)
     out16 = gemm.gemm(ac, bc, alpha=2.0)
     _check(out16, 2.0 * (a.double() @ b.double().t()), K, a, b, torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 3584), (130, 77), (1, 5), (512, 640)])
+def test_transpose16_exact(rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    t = torch.randn(rows, cols, generator=g).to(torch.bfloat16)
+    out = gemm.transpose16(t.cuda())
+    assert torch.equal(out.cpu(), t.t().contiguous())
+    # into the leading columns of a wider zero buffer (the padded LoRA factor layout)
+    buf = torch.zeros(cols, rows + 48, dtype=torch.bfloat16, device="cuda")
+    gemm.transpose16(t.cuda(), out=buf)
+    assert torch.equal(buf[:, :rows].cpu(), t.t()) and torch.all(buf[:, rows:] == 0)
+
+
+def test_transposed_frozen_cache_follows_the_weight():
+    w = torch.randn(96, 128, device="cuda").to(torch.bfloat16)
+    t1 = gemm.transposed_frozen(w)
+    assert gemm.transposed_frozen(w) is t1 and torch.equal(t1, w.t())
+    w.mul_(2)  # an in-place update bumps the version: the cache must not serve the old one
+    t2 = gemm.transposed_frozen(w)
+    assert t2 is not t1 and torch.equal(t2, w.t())
+
+
+@pytest.mark.parametrize("M,N,K,K2", [(4096, 512, 3584, 64), (300, 520, 256, 64),
+                                      (256, 384, 128, 128), (64, 3584, 0, 64)])
+def test_gemm_nt_cat(M, N, K, K2):
+    """a b^T + a2 b2^T over the concatenated K in one GEMM (split-K included for 4096x512)."""
+    print(f"gemm_nt_cat M={M} N={N} K={K} K2={K2}", flush=True)
+    g = torch.Generator().manual_seed(M + N + K + K2)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = torch.randn(N, K, generator=g).to(torch.bfloat16)
+    a2 = torch.randn(M, K2, generator=g).to(torch.bfloat16)
+    b2 = torch.randn(N, K2, generator=g).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    ref = a.double() @ b.double().t() + a2.double() @ b2.double().t() + bias.double()
+    for out_dtype in (torch.bfloat16, torch.float32):
+        out = torch.empty(M, N, dtype=out_dtype, device="cuda")
+        gemm.gemm_nt_cat(a.cuda(), b.cuda(), a2.cuda(), b2.cuda(), out, bias=bias.cuda())
+        amax = max(t.abs().max().item() if t.numel() else 0.0 for t in (a, a2))
+        bmax = max(t.abs().max().item() if t.numel() else 0.0 for t in (b, b2))
+        bound = 4 * 2.0**-22 * (K + K2) * amax * bmax
+        if out_dtype != torch.float32:
+            bound = bound + 2.0**-8 * ref.abs()
+        assert torch.all((out.double().cpu() - ref).abs() <= bound)
+
+
+@pytest.mark.parametrize("M,K,out_cols", [(4096, 3584, 64), (4096, 18944, 64), (77, 96, 16),
+                                          (1000, 512, 40)])
+def test_lora_down(M, K, out_cols):
+    """out[:, :16] = alpha x y^T, out[:, 16:] = 0, with and without the split-K workspace."""
+    print(f"lora_down M={M} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    y = (torch.randn(16, K, generator=g) * 0.25).to(torch.bfloat16)
+    ref = 2.0 * (x.double() @ y.double().t())
+    out = torch.full((M, out_cols), 3.0, dtype=torch.bfloat16, device="cuda")
+    gemm.lora_down(x.cuda(), y.cuda(), out, alpha=2.0)
+    bound = 2 * 4 * 2.0**-22 * K * x.abs().max().item() * y.abs().max().item() + 2.0**-8 * ref.abs()
+    assert torch.all((out[:, :16].double().cpu() - ref).abs() <= bound)
+    assert torch.all(out[:, 16:] == 0)
+
+
+@pytest.mark.parametrize("M,N", [(4096, 18944), (4096, 512), (100, 520), (33, 8)])
+def test_lora_wgrad(M, N):
+    """fp32 [N, 16] = alpha q^T p[:, :16] (a reduction over rows), p with a padded row stride."""
+    print(f"lora_wgrad M={M} N={N}", flush=True)
+    g = torch.Generator().manual_seed(M * 3 + N)
+    q = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    p = torch.randn(M, 64, generator=g).to(torch.bfloat16)
+    ref = 0.5 * (q.double().t() @ p[:, :16].double())
+    out = gemm.lora_wgrad(p.cuda(), q.cuda(), alpha=0.5)
+    assert out.shape == (N, 16) and out.dtype == torch.float32
+    bound = 0.5 * 4 * 2.0**-22 * M * q.abs().max().item() * p.abs().max().item()
+    assert torch.all((out.double().cpu() - ref).abs() <= bound)

@@ -121,3 +121,35 @@ def test_lora_layer_with_dropout_uses_the_reference_mask():
     base = layer.base_layer(x).detach().cpu().double()
     y_ref = base + 2.0 * ((xd.double() @ A.t()) @ B.t())
     torch.testing.assert_close(y.detach().cpu().double(), y_ref, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("in_f,out_f", [(256, 384), (320, 96)])
+def test_fused_and_unfused_lora_layer_agree(in_f, out_f):
+    """The fused single-GEMM layer (in % 128 == 0, out % 64 == 0) and the unfused path
+    (base GEMM + adapter GEMMs + ScaledAdd; forced here for the second shape and by turning
+    the fused path off for the first) give the same outputs and gradients within bf16."""
+    print(f"fused vs unfused LoRA in={in_f} out={out_f}", flush=True)
+    layer = _lora_layer(in_f, out_f, seed=11).cuda()
+    layer.base_layer.weight.quant_state.to("cuda")
+    x = torch.randn(128, in_f, device="cuda").to(torch.bfloat16)
+    dy = torch.randn(128, out_f, device="cuda").to(torch.bfloat16)
+    fusable = lora._fused_base(layer, "default", x, torch.bfloat16, 0.0) is not None
+    assert fusable == (in_f % 128 == 0 and out_f % 64 == 0)
+    results = []
+    for allow in (True, False):
+        saved = lora._fused_base
+        if not allow:
+            lora._fused_base = lambda *a, **k: None
+        try:
+            xg = x.clone().requires_grad_()
+            y = layer(xg)
+            y.backward(dy)
+        finally:
+            lora._fused_base = saved
+        results.append((y.detach().float(), xg.grad.float(),
+                        layer.lora_A["default"].weight.grad.clone(),
+                        layer.lora_B["default"].weight.grad.clone()))
+        layer.zero_grad(set_to_none=True)
+    for a, b in zip(*results):
+        s = b.abs().max().item()
+        torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2 * s)

@@ -73,3 +73,21 @@ def test_quantizer_on_gpu_matches_cpu():
     # summation order may differ between devices in the last bit
     assert torch.equal(p_cpu, p_gpu.cpu())
     torch.testing.assert_close(s_cpu.offset, s_gpu.offset.cpu(), rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("shape,nested,blocksize", [
+    ((384, 256), True, 64),
+    ((136, 512), True, 64),       # a partial 64-row tile
+    ((512, 3584), False, 64),
+    ((264, 1024), True, 128),
+    ((3584, 18944), True, 64),    # Qwen2.5-7B down_proj
+])
+def test_transposed_dequant_bit_exact(shape, nested, blocksize):
+    """dequantize_nf4_t writes W^T with the same bits as the oracle's W, transposed."""
+    print(f"nf4 dequant_t {shape} nested={nested} bs={blocksize}", flush=True)
+    packed, st, want_bf16, _ = _case(shape, nested, blocksize, seed=5)
+    assert nf4.transposed_dequant_ok(st)
+    out_t = nf4.dequantize_nf4_t(packed, st, torch.bfloat16)
+    assert out_t.shape == (shape[1], shape[0])
+    want_t = want_bf16.reshape(shape).T
+    np.testing.assert_array_equal(bits16(out_t).cpu().numpy().view(np.uint16), want_t)
