@@ -16,8 +16,12 @@
 //     each wave instruction fills 1 KiB of LDS = 8 rows of 64 k. Rows are 128 B with the
 //     16-B chunks XOR-swizzled by (row & 7), so both the DMA writes and the fragment reads
 //     (ds_read_b128, 8 rows x 16 B per phase) hit all 32 banks once;
-//   - two LDS stages (2 x 64 KiB): the loads of step k+1 are issued right after the barrier
-//     that opens step k and complete while step k is multiplied; one barrier per K step;
+//   - two LDS stages (2 x 64 KiB), software-pipelined across K steps: each step multiplies
+//     the first 32-k half of its stage while reading the second half's fragments, meets the
+//     other waves at the one barrier of the step, starts the DMA of step k+2 into the stage
+//     just consumed, and multiplies the second half while reading the first-half fragments
+//     of step k+1 (scheduling barriers keep that instruction order). Fragment reads are
+//     never exposed at a step boundary and the DMA has a full step to land;
 //   - workgroup ids are remapped so that the tiles one XCD runs at a time are neighbours
 //     (XCDs take workgroups round-robin; each has its own L2), then rastered in groups of 4
 //     tile rows so that concurrently running tiles share A and B panels in L2;
@@ -110,56 +114,68 @@ QL_DEV void tile_of(int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) 
   tn = in_group / gm;
 }
 
-// One K step: wait for this stage's DMA, barrier (every wave is also done reading the other
-// stage), start the DMA of the next K step into the other stage (k_next < 0: none), multiply
-// this stage. `cur` and `nxt` are restrict-qualified: the two stages never overlap, which
-// lets the compiler's wait-count pass see that the fragment reads below do not depend on
-// the DMA just issued into `nxt`.
+// Fragment reads of one 32-k half of a stage: a[i] rows wm*128 + 16 i + fr, b[j] likewise.
+QL_DEV void read_frags(const char* __restrict__ stage, int half, int wm, int wn, int fr, int fq,
+                       uint4 (&a)[8], uint4 (&b)[8]) {
+  const char* as = stage + (wm * 128 + fr) * kRowBytes;
+  const char* bs = stage + kTileBytes + (wn * 128 + fr) * kRowBytes;
+  const int c = ((half * 4 + fq) ^ (fr & 7)) * 16;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = *reinterpret_cast<const uint4*>(as + i * 16 * kRowBytes + c);
+    b[i] = *reinterpret_cast<const uint4*>(bs + i * 16 * kRowBytes + c);
+  }
+}
+
 template <int IT>
-QL_DEV void mma_step(f32x4_t (&acc)[8][8], char* __restrict__ cur, char* __restrict__ nxt,
-                     const TileLoader& la, const uint16_t* __restrict__ A, int64_t lda,
-                     const uint16_t* __restrict__ B, int64_t ldb, int64_t m0, int64_t n0,
-                     int64_t M, int64_t N, int64_t k_next, int wm, int wn, int fr, int fq) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (k_next >= 0) {  // A, B, lda, ldb: the segment the next K step belongs to
-    load_tile(la, A, lda, m0, M, k_next, nxt);
-    load_tile(la, B, ldb, n0, N, k_next, nxt + kTileBytes);
-  }
-  const char* as = cur + (wm * 128 + fr) * kRowBytes;
-  const char* bs = cur + kTileBytes + (wn * 128 + fr) * kRowBytes;
-  // Fragments of both 32-k halves of the step stay in registers (32 x 16 B per lane).
-  const int c0 = ((0 + fq) ^ (fr & 7)) * 16;
-  const int c1 = ((4 + fq) ^ (fr & 7)) * 16;
-  uint4 a0[8], b0[8], a1[8], b1[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a0[i] = *reinterpret_cast<const uint4*>(as + i * 16 * kRowBytes + c0);
-    b0[i] = *reinterpret_cast<const uint4*>(bs + i * 16 * kRowBytes + c0);
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a1[i] = *reinterpret_cast<const uint4*>(as + i * 16 * kRowBytes + c1);
-    b1[i] = *reinterpret_cast<const uint4*>(bs + i * 16 * kRowBytes + c1);
-  }
+QL_DEV void mma_half(f32x4_t (&acc)[8][8], const uint4 (&a)[8], const uint4 (&b)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = mfma<IT>(b0[j], a0[i], acc[i][j]);
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = mfma<IT>(b1[j], a1[i], acc[i][j]);
-  // Instruction order: the 16 reads of the first half, then its MFMAs with the 16 reads of
-  // the second half interleaved one by one, then the remaining MFMAs (masks: 0x100 DS read,
-  // 0x008 MFMA).
-  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+    for (int j = 0; j < 8; ++j) {
+      acc[i][j] = mfma<IT>(b[j], a[i], acc[i][j]);
+    }
+}
+
+// One K step kt, software-pipelined across steps. On entry f0 holds the first-half
+// fragments of stage `cur` (read during the previous step) and the DMA of step kt+1 into
+// `nxt` is in flight. The step reads the second half of `cur` while multiplying the first;
+// then every wave waits for its DMA of step kt+1 and meets at the barrier (after it, all of
+// `cur` has been read by every wave), issues the DMA of step kt+2 into `cur` (the last step
+// reloads itself: in bounds, never read), and reads the first half of `nxt` while
+// multiplying the second half of `cur`. `cur` and `nxt` are restrict-qualified so the
+// compiler's wait-count pass does not make these reads wait for the DMA into `cur`.
+template <int IT>
+QL_DEV void mma_step_pipe(f32x4_t (&acc)[8][8], uint4 (&f0a)[8], uint4 (&f0b)[8],
+                          char* __restrict__ cur, char* __restrict__ nxt, const TileLoader& la,
+                          const uint16_t* __restrict__ A2, int64_t lda2,
+                          const uint16_t* __restrict__ B2, int64_t ldb2, int64_t k2, int64_t m0,
+                          int64_t n0, int64_t M, int64_t N, int wm, int wn, int fr, int fq) {
+  uint4 f1a[8], f1b[8];
+  read_frags(cur, 1, wm, wn, fr, fq, f1a, f1b);
+  mma_half<IT>(acc, f0a, f0b);
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
   for (int t = 0; t < 16; ++t) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, 112, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 15, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  load_tile(la, A2, lda2, m0, M, k2, cur);
+  load_tile(la, B2, ldb2, n0, N, k2, cur + kTileBytes);
+  read_frags(nxt, 0, wm, wn, fr, fq, f0a, f0b);
+  mma_half<IT>(acc, f1a, f1b);
+  __builtin_amdgcn_sched_group_barrier(0x020, 16, 1);
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 32, 1);
 }
 
 // PARTIAL: write the raw fp32 sums of this split to ws[split][M][N]; otherwise the final
@@ -194,19 +210,28 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const TileLoader la = make_loader();
+  // k index of step t in its segment, and the segment's operands
+  auto seg_k = [&](int t) -> int64_t { return t < nk1 ? kb + (int64_t)t * BK : (int64_t)(t - nk1) * BK; };
   if (nk > 0) {
     const bool s1 = nk1 > 0;
-    load_tile(la, s1 ? A : A2, s1 ? lda : lda2, m0, M, s1 ? kb : 0, smem);
-    load_tile(la, s1 ? B : B2, s1 ? ldb : ldb2, n0, N, s1 ? kb : 0, smem + kTileBytes);
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-    char* cur = smem + (kt & 1) * kStageBytes;
-    char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
-    const int nx = kt + 1;
-    const bool s1 = nx < nk1;
-    const int64_t k_next = nx >= nk ? -1 : s1 ? kb + (int64_t)nx * BK : (int64_t)(nx - nk1) * BK;
-    mma_step<IT>(acc, cur, nxt, la, s1 ? A : A2, s1 ? lda : lda2, s1 ? B : B2, s1 ? ldb : ldb2,
-                 m0, n0, M, N, k_next, wm, wn, fr, fq);
+    load_tile(la, s1 ? A : A2, s1 ? lda : lda2, m0, M, seg_k(0), smem);
+    load_tile(la, s1 ? B : B2, s1 ? ldb : ldb2, n0, N, seg_k(0), smem + kTileBytes);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int t1 = nk > 1 ? 1 : 0;
+    const bool s1b = t1 < nk1;
+    load_tile(la, s1b ? A : A2, s1b ? lda : lda2, m0, M, seg_k(t1), smem + kStageBytes);
+    load_tile(la, s1b ? B : B2, s1b ? ldb : ldb2, n0, N, seg_k(t1), smem + kStageBytes + kTileBytes);
+    uint4 f0a[8], f0b[8];
+    read_frags(smem, 0, wm, wn, fr, fq, f0a, f0b);
+    for (int kt = 0; kt < nk; ++kt) {
+      char* cur = smem + (kt & 1) * kStageBytes;
+      char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
+      const int t2 = kt + 2 < nk ? kt + 2 : nk - 1;
+      const bool s2 = t2 < nk1;
+      mma_step_pipe<IT>(acc, f0a, f0b, cur, nxt, la, s2 ? A : A2, s2 ? lda : lda2, s2 ? B : B2,
+                        s2 ? ldb : ldb2, seg_k(t2), m0, n0, M, N, wm, wn, fr, fq);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
