@@ -306,6 +306,9 @@ def main():
     ap.add_argument("--eager-steps", type=int, default=2,
                     help="timed steps of the eager baseline (0: skip it and the parity check)")
     ap.add_argument("--nf4-only", action="store_true", help="only the dequant (for profiling)")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run a 256 MiB device copy (counter calibration) and eight eager dequant "
+                         "launches, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
@@ -321,6 +324,9 @@ def main():
 
     _lib.load()  # fail loudly if the kernel library is not built
     shape = (18944, 3584)
+    if args.pmc_probe:
+        pmc_probe(torch, shape)
+        return
     torch.cuda.synchronize()
     r = bench_nf4(torch, shape, args.steps, args.warmup, args.sets)
     log(f"[bench] nf4 {shape}: {r['sec_per_call'] * 1e6:.2f} us/call, {r['gbs']:.0f} GB/s")
@@ -355,6 +361,34 @@ def main():
     line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     line["cpu_baseline"]["host_cpu"] = _cpu_model()
     print(json.dumps(line), flush=True)
+
+
+def pmc_probe(torch, shape, sets=4, launches=8):
+    """Kernels for the HBM-traffic counter passes: one plain device-to-device copy of
+    256 MiB (hipMemcpyAsync, known bytes: it calibrates FETCH_SIZE / WRITE_SIZE), then
+    `launches` eager dequants of the 7B gate weight rotating over `sets` buffer sets."""
+    from hackathon_amd import nf4, quant
+
+    src = torch.ones(128 * 2**20, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    g = torch.Generator(device="cuda").manual_seed(0)
+    w = torch.randn(shape, device="cuda", generator=g) * 0.02
+    packed, st = quant.quantize_nf4(w, 64, compress_statistics=True)
+    del w
+    bufs = [(packed.clone(), torch.empty(shape, dtype=torch.bfloat16, device="cuda"))
+            for _ in range(sets)]
+    torch.cuda.synchronize()
+    for i in range(launches):
+        p, o = bufs[i % sets]
+        nf4.dequantize_nf4(p, st, torch.bfloat16, out=o)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_probe": True, "copy_bytes": 2 * 128 * 2**20,
+                      "dequant_alg_bytes": nf4_algorithmic_bytes(shape[0] * shape[1]),
+                      "dequant_launches": launches}), flush=True)
 
 
 def _measured_traffic():
