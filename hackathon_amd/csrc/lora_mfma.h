@@ -15,7 +15,8 @@ int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K);
 
 // out[n, c] = alpha * sum_m Q[m, n] P[m, c] for c < 16 (fp32 [N, 16], 16-B aligned).
 // N % 8 == 0; Q 16-B aligned with ldq a multiple of 8; P [M, ldp >= 16].
+// out_t = 1 stores out transposed, [16, N].
 int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64_t ldq,
-                  int64_t M, int64_t N, float* out, float alpha, float* ws, int64_t ws_floats,
-                  hipStream_t s);
+                  int64_t M, int64_t N, float* out, int out_t, float alpha, float* ws,
+                  int64_t ws_floats, hipStream_t s);
 int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N);

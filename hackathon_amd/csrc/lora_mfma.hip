@@ -15,10 +15,10 @@
 //               which are the strided dimension of both operands.
 //
 // lora_down: one workgroup (4 waves) per 16 rows and K range. A v_mfma_f32_16x16x32 needs
-// 8 consecutive k per lane; the sum over k does not care which 8, so lane l reads 64
-// contiguous bytes of row l%16 (k = 32*(l/16) .. +31 of a 128-k chunk) with four 16-B loads
-// and feeds them to four MFMAs; Y is read with the same k map. Waves take alternate 128-k
-// chunks and are summed through LDS.
+// 8 consecutive k per lane; the sum over k does not care which 8, so for MFMA t of a 128-k
+// chunk lane l supplies k = 32 t + 8 (l/16) .. +7 of row l%16: each 16-B load instruction
+// then reads 64 contiguous bytes from each of 16 rows. Y is read with the same k map. Waves
+// take alternate 128-k chunks and are summed through LDS.
 //
 // lora_wgrad: one workgroup per 128 columns and M range. Lane l loads an 8 (rows) x 8
 // (columns) block of Q as eight 16-B row pieces (lanes 0-15 of a row read 256 contiguous
@@ -76,21 +76,23 @@ __global__ __launch_bounds__(kThreads) void lora_down_kernel(
   const int64_t rowc = row < M ? row : M - 1;
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
-  const int koff = 32 * (lane >> 4);
+  const int koff = 8 * (lane >> 4);
   const uint16_t* xr = X + rowc * ldx;
   const uint16_t* yr = Y + (int64_t)(lane & 15) * ldy;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   for (int64_t k = kb + 128 * wave; k < ke; k += 512) {  // uniform per wave
-    const int64_t kk = k + koff;
-    // K and every chunk start are multiples of 32, so a lane's 32 k are all in or all out.
-    // Lanes past the end contribute zeros: the MFMAs below must run with every lane's
-    // operands defined, so they are not placed under a lane-dependent branch.
-    const bool ok = kk < ke;
+    // MFMA t takes k = k + 32 t + 8 (lane / 16) .. +7: each load instruction reads 64
+    // contiguous bytes of each of the 16 rows. K and every chunk start are multiples of 32,
+    // so a 32-k group is all in or all out; groups past the end contribute zeros (the MFMAs
+    // below must run with every lane's operands defined, so they are not placed under a
+    // lane-dependent branch).
     uint4 xv[4], yv[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      xv[t] = ok ? *reinterpret_cast<const uint4*>(xr + kk + 8 * t) : make_uint4(0, 0, 0, 0);
-      yv[t] = ok ? *reinterpret_cast<const uint4*>(yr + kk + 8 * t) : make_uint4(0, 0, 0, 0);
+      const bool ok = k + 32 * t < ke;
+      const int64_t kk = k + 32 * t + koff;
+      xv[t] = ok ? *reinterpret_cast<const uint4*>(xr + kk) : make_uint4(0, 0, 0, 0);
+      yv[t] = ok ? *reinterpret_cast<const uint4*>(yr + kk) : make_uint4(0, 0, 0, 0);
     }
     acc0 = mfma<IT>(yv[0], xv[0], acc0);
     acc1 = mfma<IT>(yv[1], xv[1], acc1);
@@ -158,7 +160,7 @@ template <int IT, bool PARTIAL>
 __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
     const uint16_t* __restrict__ P, int64_t ldp, const uint16_t* __restrict__ Q, int64_t ldq,
     int64_t M, int64_t N, int64_t m_per_split, float* __restrict__ ws, float* __restrict__ out,
-    float alpha) {
+    float alpha, bool out_t) {
   __shared__ f32x4_t red[4 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cg = lane & 15;                 // column group: columns n0 + 8 cg .. +7
@@ -202,6 +204,9 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
       if constexpr (PARTIAL) {
         *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * N + n) * kRank + c) =
             make_float4(s[0], s[1], s[2], s[3]);
+      } else if (out_t) {  // out [16, N]
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[(int64_t)(c + e) * N + n] = alpha * s[e];
       } else {
         *reinterpret_cast<float4*>(out + n * kRank + c) =
             make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]);
@@ -212,13 +217,59 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
 
 __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
                                                          int64_t N, float* __restrict__ out,
-                                                         float alpha) {
+                                                         float alpha, bool out_t) {
   const int64_t total = N * kRank;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
     float v = 0.f;
     for (int z = 0; z < splits; ++z) v += ws[(int64_t)z * total + i];
-    out[i] = alpha * v;
+    const int64_t n = i / kRank, c = i - n * kRank;
+    out[out_t ? c * N + n : i] = alpha * v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// The compute-dtype forms of one adapter's fp32 factors A [16, K] and B [N, 16], in one pass:
+//   a16 [16, K]  = A                    (the Y operand of u = x A^T)
+//   at  [K, 64]  = A^T | 0              (the second K segment of the backward dX GEMM)
+//   bs  [N, 64]  = s B | 0              (the second K segment of the forward GEMM)
+//   bt  [16, N]  = B^T                  (the Y operand of du = s g B)
+// Thread t of the flat range handles one row of at (t < K), then one row of bs and one
+// column of bt (K <= t < K + N), then 8 elements of a16.
+template <int OT>
+__global__ __launch_bounds__(256) void lora_pack_kernel(const float* __restrict__ A,
+                                                        const float* __restrict__ B, int64_t K,
+                                                        int64_t N, float scaling,
+                                                        typename Elem<OT>::T* __restrict__ a16,
+                                                        typename Elem<OT>::T* __restrict__ at,
+                                                        typename Elem<OT>::T* __restrict__ bs,
+                                                        typename Elem<OT>::T* __restrict__ bt,
+                                                        int pad) {
+  using T = typename Elem<OT>::T;
+  const int64_t n_a16 = kRank * K / 8;
+  const int64_t total = K + N + n_a16;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * 256) {
+    if (t < K) {
+      T* row = at + t * pad;
+#pragma unroll
+      for (int r = 0; r < kRank; ++r) row[r] = Elem<OT>::from_f32(A[(int64_t)r * K + t]);
+      for (int c = kRank; c < pad; ++c) row[c] = Elem<OT>::from_f32(0.f);
+    } else if (t < K + N) {
+      const int64_t n = t - K;
+      T* row = bs + n * pad;
+#pragma unroll
+      for (int r = 0; r < kRank; ++r) {
+        const float b = B[n * kRank + r];
+        row[r] = Elem<OT>::from_f32(scaling * b);
+        bt[(int64_t)r * N + n] = Elem<OT>::from_f32(b);
+      }
+      for (int c = kRank; c < pad; ++c) row[c] = Elem<OT>::from_f32(0.f);
+    } else {
+      const int64_t i = (t - K - N) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a16[i + e] = Elem<OT>::from_f32(A[i + e]);
+    }
   }
 }
 
@@ -298,10 +349,11 @@ int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N) {
 }
 
 int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64_t ldq,
-                  int64_t M, int64_t N, float* out, float alpha, float* ws, int64_t ws_floats,
-                  hipStream_t s) {
+                  int64_t M, int64_t N, float* out, int out_t, float alpha, float* ws,
+                  int64_t ws_floats, hipStream_t s) {
   if (M <= 0 || N <= 0 || N % 8 || ldp < kRank) return QL_EINVAL;
   if (ldq % 8 || !ql_aligned(Q, 16) || !ql_aligned(P, 2) || !ql_aligned(out, 16)) return QL_EALIGN;
+  if (out_t != 0 && out_t != 1) return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   int splits = ql_lora_wgrad_splits(M, N);
   if (ws_floats < (int64_t)splits * N * kRank || !ws) splits = 1;
@@ -313,13 +365,13 @@ int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64
     if (splits == 1) {                                                                       \
       hipLaunchKernelGGL((lora_wgrad_kernel<IT, false>), grid, dim3(kThreads), 0, s,         \
                          (const uint16_t*)P, ldp, (const uint16_t*)Q, ldq, M, N, mps,        \
-                         (float*)nullptr, out, alpha);                                       \
+                         (float*)nullptr, out, alpha, out_t);                                \
     } else {                                                                                 \
       hipLaunchKernelGGL((lora_wgrad_kernel<IT, true>), grid, dim3(kThreads), 0, s,          \
                          (const uint16_t*)P, ldp, (const uint16_t*)Q, ldq, M, N, mps, ws,    \
-                         out, alpha);                                                        \
+                         out, alpha, out_t);                                                 \
       hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0, s, ws,    \
-                         splits, N, out, alpha);                                             \
+                         splits, N, out, alpha, out_t);                                      \
     }                                                                                        \
   } while (0)
   if (in_dtype == QL_BF16) QL_WGRAD(QL_BF16);
@@ -354,18 +406,39 @@ extern "C" int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N) {
 }
 
 extern "C" int qlora_lora_wgrad(const void* P, int64_t ldp, const void* Q, int64_t ldq, int64_t M,
-                                int64_t N, int in_dtype, float* out, float alpha, void* workspace,
-                                int64_t workspace_bytes, ql_stream_t stream) {
+                                int64_t N, int in_dtype, float* out, int out_transposed,
+                                float alpha, void* workspace, int64_t workspace_bytes,
+                                ql_stream_t stream) {
   if (M < 0 || N < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (N == 0) return QL_OK;
   if (!P || !Q || !out) return QL_EINVAL;
   if (M == 0) {  // an empty reduction: zeros (a fill kernel, not a memset node)
     hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), (const float*)nullptr, 0, N,
-                       out, 0.f);
+                       out, 0.f, out_transposed != 0);
     return ql_launch_status();
   }
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
-  return ql_lora_wgrad(in_dtype, P, ldp, Q, ldq, M, N, out, alpha, static_cast<float*>(workspace),
-                       workspace_bytes / (int64_t)sizeof(float), static_cast<hipStream_t>(stream));
+  return ql_lora_wgrad(in_dtype, P, ldp, Q, ldq, M, N, out, out_transposed, alpha,
+                       static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
+                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float scaling,
+                               int out_dtype, void* a16, void* at_pad, void* bs_pad, void* bt,
+                               int pad, ql_stream_t stream) {
+  if (K < 0 || N < 0 || pad < kRank || K % 8) return QL_EINVAL;
+  if (K == 0 && N == 0) return QL_OK;
+  if (!A || !B || !a16 || !at_pad || !bs_pad || !bt) return QL_EINVAL;
+  if (out_dtype != QL_BF16 && out_dtype != QL_F16) return QL_EDTYPE;
+  const int64_t total = K + N + kRank * K / 8;
+  const dim3 grid(grid1d(total));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (out_dtype == QL_BF16)
+    hipLaunchKernelGGL((lora_pack_kernel<QL_BF16>), grid, dim3(256), 0, s, A, B, K, N, scaling,
+                       (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
+  else
+    hipLaunchKernelGGL((lora_pack_kernel<QL_F16>), grid, dim3(256), 0, s, A, B, K, N, scaling,
+                       (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
+  return ql_launch_status();
 }

@@ -141,12 +141,31 @@ def lora_down(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, alpha: float 
     return out
 
 
-def lora_wgrad(p: torch.Tensor, q: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
-    """fp32 [N, 16] = alpha * q^T @ p[:, :16] for q [M, N], p [M, >=16] (qlora_lora_wgrad)."""
+def lora_wgrad(p: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
+               transposed: bool = False) -> torch.Tensor:
+    """fp32 alpha * q^T @ p[:, :16] for q [M, N], p [M, >=16] (qlora_lora_wgrad): [N, 16], or
+    [16, N] when `transposed`."""
     M, N = q.shape
-    out = torch.empty((N, 16), dtype=torch.float32, device=q.device)
+    out = torch.empty((16, N) if transposed else (N, 16), dtype=torch.float32, device=q.device)
     ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_workspace_size", M, N, device=q.device)
     _lib.call("qlora_lora_wgrad", p.data_ptr(), p.stride(0), q.data_ptr(), q.stride(0), M, N,
-              _lib.tag(q.dtype), out.data_ptr(), float(alpha), _lib.ptr(ws), ws_bytes,
-              _lib.stream_of(q))
+              _lib.tag(q.dtype), out.data_ptr(), int(transposed), float(alpha), _lib.ptr(ws),
+              ws_bytes, _lib.stream_of(q))
     return out
+
+
+def lora_pack(a: torch.Tensor, b: torch.Tensor, scaling: float, dtype, pad: int = 64):
+    """(a16 [16,K], at_pad [K,pad], bs_pad [N,pad], bt [16,N]) in `dtype` from the fp32 adapter
+    factors a [16, K] and b [N, 16] in one launch (qlora_lora_pack)."""
+    _lib.require_device(a, b)
+    a = a.detach().float().contiguous()
+    b = b.detach().float().contiguous()
+    K, N = a.shape[1], b.shape[0]
+    dev = a.device
+    a16 = torch.empty((16, K), dtype=dtype, device=dev)
+    at = torch.empty((K, pad), dtype=dtype, device=dev)
+    bs = torch.empty((N, pad), dtype=dtype, device=dev)
+    bt = torch.empty((16, N), dtype=dtype, device=dev)
+    _lib.call("qlora_lora_pack", a.data_ptr(), b.data_ptr(), K, N, float(scaling), _lib.tag(dtype),
+              a16.data_ptr(), at.data_ptr(), bs.data_ptr(), bt.data_ptr(), pad, _lib.stream_of(a))
+    return a16, at, bs, bt

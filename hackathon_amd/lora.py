@@ -157,16 +157,15 @@ class LoraNF4Linear(torch.autograd.Function):
         dt = x2.dtype
         M, K = x2.shape
         N = int(quant_state.shape[0])
+        # A, A^T|0, s*B|0 and B^T in the compute dtype, one launch (kept for the backward)
+        a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
         w = nf4.dequantize_nf4(packed, quant_state, dt)
-        a16 = a_weight.to(dt).contiguous()
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
         _gemm.lora_down(x2, a16, u)
-        bs = torch.zeros((N, _PAD), dtype=dt, device=x2.device)
-        bs[:, :16] = (b_weight.detach() * scaling).to(dt)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
         _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=None if bias is None else bias.to(dt))
         del w
-        ctx.save_for_backward(x2, u, a16, b_weight)
+        ctx.save_for_backward(x2, u, at, bt)
         ctx.packed, ctx.quant_state, ctx.scaling = packed, quant_state, float(scaling)
         ctx.shape, ctx.wdtypes = x.shape, (a_weight.dtype, b_weight.dtype)
         return y.view(*x.shape[:-1], N)
@@ -175,31 +174,31 @@ class LoraNF4Linear(torch.autograd.Function):
     def backward(ctx, g):
         from . import nf4
 
-        x2, u, a16, b_weight = ctx.saved_tensors
+        x2, u, at, bt = ctx.saved_tensors
         dt = x2.dtype
         M, K = x2.shape
         g2 = _rows(g)
         if g2.dtype != dt:
             g2 = g2.to(dt)
         g2 = g2.contiguous()
-        N = g2.shape[1]
         s = ctx.scaling
-        bt = b_weight.detach().t().to(dt).contiguous()                  # [16, N]
         du = torch.empty((M, _PAD), dtype=dt, device=g2.device)
-        _gemm.lora_down(g2, bt, du, alpha=s)
+        _gemm.lora_down(g2, bt, du, alpha=s)                            # du = s g B
         dx = da = db = None
         if ctx.needs_input_grad[0]:
             wt = nf4.dequantize_nf4_t(ctx.packed, ctx.quant_state, dt)  # [K, N]
-            at = torch.zeros((K, _PAD), dtype=dt, device=g2.device)
-            _gemm.transpose16(a16, out=at)                              # at[:, :16] = A^T
             dx = torch.empty((M, K), dtype=dt, device=g2.device)
             _gemm.gemm_nt_cat(g2, wt, du, at, dx)
             del wt
             dx = dx.view(ctx.shape)
         if ctx.needs_input_grad[1]:
-            da = _gemm.lora_wgrad(du, x2).t().contiguous().to(ctx.wdtypes[0])  # [16, K]
+            da = _gemm.lora_wgrad(du, x2, transposed=True)              # [16, K] = du^T x
+            if da.dtype != ctx.wdtypes[0]:
+                da = da.to(ctx.wdtypes[0])
         if ctx.needs_input_grad[2]:
-            db = _gemm.lora_wgrad(u, g2, alpha=s).to(ctx.wdtypes[1])   # [N, 16]
+            db = _gemm.lora_wgrad(u, g2, alpha=s)                      # [N, 16] = s g^T u
+            if db.dtype != ctx.wdtypes[1]:
+                db = db.to(ctx.wdtypes[1])
         return dx, da, db, None, None, None, None
 
 
@@ -223,6 +222,8 @@ def _fused_base(layer, adapter, x, compute_dtype, p):
     if a_w.shape != (16, in_f) or b_w.shape != (out_f, 16):
         return None
     if in_f % 128 or out_f % 64 or not nf4.transposed_dequant_ok(qs):
+        return None
+    if not (a_w.is_cuda and b_w.is_cuda):
         return None
     return weight, qs, bias
 

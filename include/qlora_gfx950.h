@@ -249,15 +249,28 @@ int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_t ldy, int6
 
 /*
  * LoRA weight gradient (rank 16), a reduction over the token rows:
- *   out[n, c] = alpha * sum_m Q[m, n] * P[m, c]      (fp32 [N, 16], c < 16)
+ *   out[n, c] = alpha * sum_m Q[m, n] * P[m, c]      (fp32 [N, 16], c < 16; stored [16, N]
+ *                                                     when out_transposed = 1)
  * dB = s * g^T u (P = u, Q = g); dA^T = x^T du (P = du, Q = x).
  * N % 8 == 0; Q 16-B aligned with ldq a multiple of 8; P [M, ldp >= 16]; out 16-B aligned.
  * Replaces: the autograd weight gradients of solution/lora.py:172 (lora_A / lora_B).
  */
 int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N);
 int qlora_lora_wgrad(const void* P, int64_t ldp, const void* Q, int64_t ldq, int64_t M, int64_t N,
-                     int in_dtype, float* out, float alpha, void* workspace,
+                     int in_dtype, float* out, int out_transposed, float alpha, void* workspace,
                      int64_t workspace_bytes, ql_stream_t stream);
+
+/*
+ * The compute-dtype operands of one rank-16 adapter, from its fp32 factors A [16, K] and
+ * B [N, 16], in one launch (K % 8 == 0, pad >= 16):
+ *   a16 [16, K] = A;  at_pad [K, pad] = A^T | 0;  bs_pad [N, pad] = scaling * B | 0;
+ *   bt [16, N] = B^T;          out_dtype QL_BF16 or QL_F16, round to nearest even.
+ * Replaces: the casts of the adapter weights to the autocast dtype inside the nn.Linear
+ * calls of solution/lora.py:172 (and the layouts the fused GEMM segments need).
+ */
+int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float scaling,
+                    int out_dtype, void* a16, void* at_pad, void* bs_pad, void* bt, int pad,
+                    ql_stream_t stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

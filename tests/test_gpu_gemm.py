@@ -204,3 +204,24 @@ def test_lora_wgrad(M, N):
     assert out.shape == (N, 16) and out.dtype == torch.float32
     bound = 0.5 * 4 * 2.0**-22 * M * q.abs().max().item() * p.abs().max().item()
     assert torch.all((out.double().cpu() - ref).abs() <= bound)
+
+
+@pytest.mark.parametrize("K,N", [(3584, 512), (256, 18944), (8, 8)])
+def test_lora_pack_is_exact(K, N):
+    """The packed adapter operands equal torch's own casts of A, A^T, s*B and B^T (RNE)."""
+    g = torch.Generator().manual_seed(K + N)
+    a = torch.randn(16, K, generator=g) * 0.25
+    b = torch.randn(N, 16, generator=g) * 0.01
+    a16, at, bs, bt = gemm.lora_pack(a.cuda(), b.cuda(), 2.0, torch.bfloat16)
+    assert torch.equal(a16.cpu(), a.to(torch.bfloat16))
+    assert torch.equal(at[:, :16].cpu(), a.t().to(torch.bfloat16)) and torch.all(at[:, 16:] == 0)
+    assert torch.equal(bs[:, :16].cpu(), (2.0 * b).to(torch.bfloat16)) and torch.all(bs[:, 16:] == 0)
+    assert torch.equal(bt.cpu(), b.t().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("M,N", [(4096, 3584), (100, 520)])
+def test_lora_wgrad_transposed_output(M, N):
+    g = torch.Generator().manual_seed(N)
+    q = torch.randn(M, N, generator=g).to(torch.bfloat16).cuda()
+    p = torch.randn(M, 64, generator=g).to(torch.bfloat16).cuda()
+    assert torch.equal(gemm.lora_wgrad(p, q, transposed=True), gemm.lora_wgrad(p, q).t())
