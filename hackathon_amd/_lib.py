@@ -60,6 +60,8 @@ _SIGNATURES = {
                          _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_pack": [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_f32, _c_int, _c_ptr, _c_ptr, _c_ptr,
                         _c_ptr, _c_int, _c_ptr],
+    "qlora_nf4_quantize": [_c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
+                           _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr],
     "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                       _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
 }
@@ -70,6 +72,7 @@ _SIZE_QUERIES = {
     "qlora_gemm_nt_cat_workspace_size": [_c_i64, _c_i64, _c_i64],
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64],
+    "qlora_nf4_quantize_workspace_size": [_c_i64, _c_int, _c_int],
 }
 
 _lib = None

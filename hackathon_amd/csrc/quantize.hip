@@ -1,0 +1,143 @@
+// NF4 quantisation with a double-quantised absmax, for gfx950: the format producer that
+// feeds the dequant kernel (the weight format of solution/nf4.py:73-86, which the reference
+// takes from bitsandbytes' quantize_4bit; bitsandbytes is not part of this build).
+//
+//   stage 1  one thread per NF4 block of `blocksize` weights: absmax = max |w|, codes =
+//            nearest NF4 level of w * (1 / absmax) (fp32 multiply by the correctly rounded
+//            reciprocal; ties go to the lower level, i.e. the count of level midpoints
+//            strictly below the value), two codes per byte, high nibble first.
+//   stage 2  (double quantisation) offset = mean(absmax), accumulated in fp64: for the block
+//            absmax of a weight tensor the fp64 sum is exact, so the offset does not depend on
+//            the reduction order, and is rounded once to fp32.
+//   stage 3  one workgroup per 256 absmax values: absmax2 = max |absmax - offset|, codes =
+//            nearest entry of the 256-level dynamic map of (absmax - offset) / absmax2.
+// Every step uses the same fp32 operations, in the same order, as the torch quantizer in
+// hackathon_amd/quant.py, so the two produce identical bytes.
+#include "ql_vec.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// Number of the n sorted midpoints strictly below x (lower bound).
+QL_DEV int count_below(const float* mids, int n, float x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (mids[mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+template <int IT>
+__global__ __launch_bounds__(kThreads) void nf4_quantize_blocks(
+    const typename Elem<IT>::T* __restrict__ w, int64_t n, int64_t blocksize, int64_t n_blocks,
+    const float* __restrict__ nf4_code, uint8_t* __restrict__ packed, float* __restrict__ absmax) {
+#pragma clang fp contract(off)
+  __shared__ float mids[15];
+  if (threadIdx.x < 15) mids[threadIdx.x] = (nf4_code[threadIdx.x] + nf4_code[threadIdx.x + 1]) * 0.5f;
+  __syncthreads();
+  const int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (b >= n_blocks) return;
+  const int64_t j0 = b * blocksize;
+  const int64_t j1 = j0 + blocksize < n ? j0 + blocksize : n;
+  float am = 0.f;
+  for (int64_t j = j0; j < j1; ++j) am = fmaxf(am, fabsf(Elem<IT>::load(w, j)));
+  const float inv = am > 0.f ? 1.0f / am : 0.f;
+  for (int64_t j = j0; j < j1; j += 2) {  // j0 and n are even
+    const int hi = count_below(mids, 15, Elem<IT>::load(w, j) * inv);
+    const int lo = count_below(mids, 15, Elem<IT>::load(w, j + 1) * inv);
+    packed[j / 2] = (uint8_t)((hi << 4) | lo);
+  }
+  absmax[b] = am;
+}
+
+// fp64 partial sums of x[0..n): one per workgroup.
+__global__ __launch_bounds__(kThreads) void sum_f64_partials(const float* __restrict__ x,
+                                                             int64_t n, double* __restrict__ part) {
+  __shared__ double red[kThreads / 64];
+  double s = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    s += (double)x[i];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+// offset = (float)(sum(part) / n), one thread.
+__global__ void mean_from_partials(const double* __restrict__ part, int n_part, int64_t n,
+                                   float* __restrict__ offset) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  double s = 0.0;
+  for (int i = 0; i < n_part; ++i) s += part[i];
+  offset[0] = (float)(s / (double)n);
+}
+
+// One workgroup per block of 256 values of (absmax - offset): dynamic-map codes + absmax2.
+__global__ __launch_bounds__(kThreads) void quantize8_blocks(
+    const float* __restrict__ absmax, int64_t n, const float* __restrict__ offset,
+    const float* __restrict__ code2, uint8_t* __restrict__ codes, float* __restrict__ absmax2) {
+#pragma clang fp contract(off)
+  __shared__ float mids[255];
+  __shared__ float red[kThreads / 64];
+  if (threadIdx.x < 255) mids[threadIdx.x] = (code2[threadIdx.x] + code2[threadIdx.x + 1]) * 0.5f;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const float v = i < n ? absmax[i] - offset[0] : 0.f;
+  float m = fabsf(v);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  const float am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float inv = am > 0.f ? 1.0f / am : 0.f;
+  if (i < n) codes[i] = (uint8_t)count_below(mids, 255, v * inv);
+  if (threadIdx.x == 0) absmax2[blockIdx.x] = am;
+}
+
+constexpr int kPartials = 256;
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+}  // namespace
+
+extern "C" int64_t qlora_nf4_quantize_workspace_size(int64_t n, int blocksize, int nested) {
+  if (n <= 0 || blocksize <= 0 || !nested) return 0;
+  const int64_t nb = (n + blocksize - 1) / blocksize;
+  return align256(nb * (int64_t)sizeof(float)) + kPartials * (int64_t)sizeof(double);
+}
+
+extern "C" int qlora_nf4_quantize(const void* w, int w_dtype, int64_t n, int blocksize, int nested,
+                                  int blocksize2, const float* nf4_code, const float* code2,
+                                  uint8_t* packed, void* absmax, float* absmax2, float* offset,
+                                  void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
+  if (n < 0 || (n & 1) || blocksize < 2 || (blocksize & 1)) return QL_EINVAL;
+  if (nested && blocksize2 != 256) return QL_EINVAL;  // one workgroup per 256-value block
+  if (n == 0) return QL_OK;
+  if (!w || !nf4_code || !packed || !absmax) return QL_EINVAL;
+  if (nested && (!code2 || !absmax2 || !offset)) return QL_EINVAL;
+  if (!ql_valid_dtype(w_dtype)) return QL_EDTYPE;
+  const int64_t nb = (n + blocksize - 1) / blocksize;
+  if (nested && (workspace_bytes < qlora_nf4_quantize_workspace_size(n, blocksize, nested) ||
+                 !workspace || !ql_aligned(workspace, 16)))
+    return QL_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* am = nested ? static_cast<float*>(workspace) : static_cast<float*>(absmax);
+  const dim3 g1((unsigned)((nb + kThreads - 1) / kThreads));
+  QL_DISPATCH_DTYPE(w_dtype, DT,
+                    hipLaunchKernelGGL((nf4_quantize_blocks<DT>), g1, dim3(kThreads), 0, s,
+                                       static_cast<const typename Elem<DT>::T*>(w), n,
+                                       (int64_t)blocksize, nb, nf4_code, packed, am));
+  if (!nested) return ql_launch_status();
+  double* part = reinterpret_cast<double*>(static_cast<char*>(workspace) +
+                                           align256(nb * (int64_t)sizeof(float)));
+  hipLaunchKernelGGL(sum_f64_partials, dim3(kPartials), dim3(kThreads), 0, s, am, nb, part);
+  hipLaunchKernelGGL(mean_from_partials, dim3(1), dim3(64), 0, s, part, kPartials, nb, offset);
+  const dim3 g3((unsigned)((nb + 255) / 256));
+  hipLaunchKernelGGL(quantize8_blocks, g3, dim3(kThreads), 0, s, am, nb, offset, code2,
+                     static_cast<uint8_t*>(absmax), absmax2);
+  return ql_launch_status();
+}

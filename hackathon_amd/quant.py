@@ -22,7 +22,8 @@ Quantization" (Dettmers et al. 2022): value = ±10^(e-6) * f for exponent e in 0
 2^e linear fractions f at the midpoints of an even split of [0.1, 1], plus 0 and 1.
 
 Quantisation rounds to the nearest code (ties to the lower code), normalising by the
-reciprocal of the block absmax. Nothing of it is bit-compared with bitsandbytes (which is
+reciprocal of the block absmax; GPU tensors go through the library's kernel, CPU tensors
+through the same arithmetic in torch ops (identical bytes). Nothing of it is bit-compared with bitsandbytes (which is
 not installed); dequantisation of whatever this produces is what must be bit-exact.
 """
 
@@ -112,7 +113,14 @@ def quantize_blockwise_8bit(x: torch.Tensor, blocksize: int = 256):
 
 def quantize_nf4(w: torch.Tensor, blocksize: int = 64, compress_statistics: bool = True,
                  blocksize2: int = 256):
-    """NF4-quantise a weight tensor: returns (packed uint8 [n/2, 1], QuantState)."""
+    """NF4-quantise a weight tensor: returns (packed uint8 [n/2, 1], QuantState).
+
+    GPU tensors are quantised by the library's kernel (qlora_nf4_quantize); CPU tensors by the
+    same arithmetic in torch ops. Both give identical bytes: the double-quant offset, the mean
+    of the block absmax, is accumulated in fp64 (exact for these values, so independent of
+    the summation order) and rounded once to fp32."""
+    if w.is_cuda and (not compress_statistics or blocksize2 == 256):
+        return _quantize_nf4_gpu(w, blocksize, compress_statistics, blocksize2)
     flat = w.detach().reshape(-1).float()
     n = flat.numel()
     if n % 2:
@@ -127,9 +135,47 @@ def quantize_nf4(w: torch.Tensor, blocksize: int = 64, compress_statistics: bool
     idx = _nearest_code(blocks * inv[:, None], code).to(torch.uint8).reshape(-1)[:n]
     packed = ((idx[0::2] << 4) | idx[1::2]).reshape(-1, 1)
     if compress_statistics:
-        offset = absmax.mean()
+        offset = absmax.double().mean().float()
         qabs, state2 = quantize_blockwise_8bit(absmax - offset, blocksize2)
         state = QuantState(absmax=qabs, shape=w.shape, code=code, blocksize=blocksize,
+                           dtype=w.dtype, offset=offset, state2=state2)
+    else:
+        state = QuantState(absmax=absmax, shape=w.shape, code=code, blocksize=blocksize,
+                           dtype=w.dtype)
+    return packed, state
+
+
+def _quantize_nf4_gpu(w, blocksize, compress_statistics, blocksize2):
+    from . import _lib
+
+    x = w.detach()
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        x = x.float()
+    x = x.contiguous()
+    n = x.numel()
+    if n % 2:
+        raise ValueError("NF4 packing needs an even number of weights")
+    dev = x.device
+    nb = math.ceil(n / blocksize)
+    code = nf4_code(dev)
+    packed = torch.empty((n // 2, 1), dtype=torch.uint8, device=dev)
+    nested = bool(compress_statistics)
+    if nested:
+        code2 = dynamic_map(True).to(dev)
+        absmax = torch.empty(nb, dtype=torch.uint8, device=dev)
+        absmax2 = torch.empty(math.ceil(nb / blocksize2), dtype=torch.float32, device=dev)
+        offset = torch.empty((), dtype=torch.float32, device=dev)
+    else:
+        code2 = absmax2 = offset = None
+        absmax = torch.empty(nb, dtype=torch.float32, device=dev)
+    ws, ws_bytes = _lib.workspace("qlora_nf4_quantize_workspace_size", n, blocksize, int(nested),
+                                  device=dev)
+    _lib.call("qlora_nf4_quantize", x.data_ptr(), _lib.tag(x.dtype), n, blocksize, int(nested),
+              blocksize2, code.data_ptr(), _lib.ptr(code2), packed.data_ptr(), absmax.data_ptr(),
+              _lib.ptr(absmax2), _lib.ptr(offset), _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+    if nested:
+        state2 = QuantState(absmax=absmax2, code=code2, blocksize=blocksize2, dtype=torch.float32)
+        state = QuantState(absmax=absmax, shape=w.shape, code=code, blocksize=blocksize,
                            dtype=w.dtype, offset=offset, state2=state2)
     else:
         state = QuantState(absmax=absmax, shape=w.shape, code=code, blocksize=blocksize,

@@ -62,6 +62,25 @@ int qlora_nf4_dequant(const uint8_t* packed, int64_t n_weights, const void* absm
                       ql_stream_t stream);
 
 /*
+ * NF4 quantisation with optional double-quantised absmax: the format qlora_nf4_dequant reads.
+ *   per block of `blocksize` weights: absmax = max |w|; code = nearest NF4 level (nf4_code,
+ *   16 sorted fp32) of w * (1/absmax), ties to the lower level; packed two per byte, high
+ *   nibble first.  nested = 0: absmax (fp32 [nblocks]) is written as is.
+ *   nested = 1: offset = mean(absmax) accumulated in fp64, rounded to fp32 (*offset); absmax
+ *   (uint8 [nblocks]) = nearest code2 level (256 sorted fp32) of (absmax - offset) / absmax2,
+ *   with absmax2 (fp32 [ceil(nblocks/256)]) the max |absmax - offset| of each 256-block
+ *   (blocksize2 must be 256). Workspace: qlora_nf4_quantize_workspace_size bytes, 16-B aligned.
+ * n even, blocksize even; w_dtype QL_F32 / QL_F16 / QL_BF16.
+ * Replaces: bitsandbytes' quantize_4bit(..., compress_statistics=True) that produces the
+ * QuantState solution/nf4.py:73-86 reads (solution/test_kernels.py:41-52).
+ */
+int64_t qlora_nf4_quantize_workspace_size(int64_t n, int blocksize, int nested);
+int qlora_nf4_quantize(const void* w, int w_dtype, int64_t n, int blocksize, int nested,
+                       int blocksize2, const float* nf4_code, const float* code2, uint8_t* packed,
+                       void* absmax, float* absmax2, float* offset, void* workspace,
+                       int64_t workspace_bytes, ql_stream_t stream);
+
+/*
  * RMSNorm forward over rows of length n_cols (frozen weight).
  * Replaces: solution/rmsnorm.py:24-39 (rmsnorm_fwd_kernel) + :64-78 (launch).
  *   rstd[r] = 1 / sqrt(sum(x^2)/n_cols + eps)                  (fp32)

@@ -64,15 +64,27 @@ def test_dequant_full_qwen25_7b_gate_shape_bit_exact():
     np.testing.assert_array_equal(got, want_bf16)
 
 
-def test_quantizer_on_gpu_matches_cpu():
+@pytest.mark.parametrize("shape,dtype,nested,bs", [
+    ((128, 512), torch.float32, True, 64),
+    ((18944, 3584), torch.bfloat16, True, 64),   # Qwen2.5-7B gate_proj, as the step builds it
+    ((96, 320), torch.float16, False, 64),
+    ((33, 70), torch.float32, True, 6),           # partial last block, odd blocksize multiple
+    ((7, 6), torch.bfloat16, True, 64),           # fewer weights than one block
+])
+def test_quantizer_kernel_matches_cpu_bytes(shape, dtype, nested, bs):
+    """The GPU quantiser kernel and the CPU torch quantiser give identical packed codes, absmax
+    codes, second-level scales and offset (the offset is an fp64-accumulated mean)."""
+    print(f"nf4 quantize {shape} {dtype} nested={nested} bs={bs}", flush=True)
     g = torch.Generator().manual_seed(11)
-    w = torch.randn(128, 512, generator=g) * 0.02
-    p_cpu, s_cpu = quant.quantize_nf4(w, 64)
-    p_gpu, s_gpu = quant.quantize_nf4(w.cuda(), 64)
-    # codes come from elementwise fp32 ops: identical; the double-quant offset is a mean, whose
-    # summation order may differ between devices in the last bit
+    w = (torch.randn(shape, generator=g) * 0.02).to(dtype)
+    p_cpu, s_cpu = quant.quantize_nf4(w, bs, compress_statistics=nested)
+    p_gpu, s_gpu = quant.quantize_nf4(w.cuda(), bs, compress_statistics=nested)
     assert torch.equal(p_cpu, p_gpu.cpu())
-    torch.testing.assert_close(s_cpu.offset, s_gpu.offset.cpu(), rtol=1e-6, atol=0)
+    assert torch.equal(s_cpu.absmax, s_gpu.absmax.cpu())
+    if nested:
+        assert torch.equal(s_cpu.offset, s_gpu.offset.cpu())
+        assert torch.equal(s_cpu.state2.absmax, s_gpu.state2.absmax.cpu())
+        assert torch.equal(s_cpu.state2.code, s_gpu.state2.code.cpu())
 
 
 @pytest.mark.parametrize("shape,nested,blocksize", [
