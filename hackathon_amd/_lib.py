@@ -62,6 +62,8 @@ _SIGNATURES = {
                         _c_ptr, _c_int, _c_ptr],
     "qlora_nf4_quantize": [_c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
                            _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr],
+    "qlora_attn_fwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
+                       _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_f32, _c_ptr],
     "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                       _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
 }

@@ -291,6 +291,22 @@ int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float 
                     int out_dtype, void* a16, void* at_pad, void* bs_pad, void* bt, int pad,
                     ql_stream_t stream);
 
+/*
+ * Causal flash attention forward with grouped-query heads (HQ % HK == 0), head_dim 128:
+ *   o[b, hq, s, :] = sum_t softmax_t(scale * q[b,hq,s,:] . k[b,hk,t,:], t <= s) v[b,hk,t,:]
+ *   lse[b, hq, s] = log sum_{t <= s} exp(scale * q . k)    (fp32 [B, HQ, S]; may be NULL)
+ * with hk = hq / (HQ / HK). Tensors are (B, H, S, D) described by element strides {b, h, s}
+ * (last dim contiguous; every stride a multiple of 8, pointers 16-B aligned); dtype QL_BF16 or
+ * QL_F16; fp32 softmax and accumulation.
+ * Replaces: torch.nn.functional.scaled_dot_product_attention(..., is_causal=True) as
+ * Qwen2Attention calls it through transformers' SDPA integration
+ * (transformers/models/qwen2/modeling_qwen2.py:216-229); not patched by the reference.
+ */
+int qlora_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int dtype,
+                   int64_t B, int64_t HQ, int64_t HK, int64_t S, int64_t D,
+                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, float scale, ql_stream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif
