@@ -14,15 +14,17 @@ include/qlora_gfx950.h, bound through ctypes in `_lib`).
   cross_entropy.py  chunked lm_head + CE installed on Qwen2ForCausalLM.forward
   quant.py          NF4 storage format: codebook, QuantState, quantizer, Linear4bit
   gemm.py           the MFMA GEMM behind every contraction of the path
+  attention.py      causal flash attention behind transformers' "sdpa" entry (fwd + bwd)
 """
 
-PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora")
+PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora", "attention")
 
 _applied = set()
 
 
 def apply(include_example=True):
-    """Install every patch (idempotent), as solution/__init__.py:22-34 does."""
+    """Install every patch (idempotent), as solution/__init__.py:22-34 does; "attention" has no
+    counterpart in the reference, which leaves attention to torch's SDPA."""
     from importlib import import_module
 
     for name in PATCHES:

@@ -64,6 +64,9 @@ _SIGNATURES = {
                            _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr],
     "qlora_attn_fwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                        _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_f32, _c_ptr],
+    "qlora_attn_bwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                       _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p, _c_i64p, _c_i64p,
+                       _c_i64p, _c_i64p, _c_i64p, _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                       _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
 }
@@ -75,6 +78,7 @@ _SIZE_QUERIES = {
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64],
     "qlora_nf4_quantize_workspace_size": [_c_i64, _c_int, _c_int],
+    "qlora_attn_bwd_workspace_size": [_c_i64, _c_i64, _c_i64],
 }
 
 _lib = None

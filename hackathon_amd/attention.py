@@ -39,13 +39,61 @@ def attn_fwd(q, k, v, scale, with_lse=True):
     return o, lse
 
 
-def supported(module, query, key, value, attention_mask, dropout, kwargs):
+def attn_bwd(q, k, v, o, lse, do, scale):
+    """(dq, dk, dv) in the layouts of q, k and v as (B, H, S, D) views of (B, S, H, D) storage,
+    for the forward `attn_fwd(q, k, v, scale)` = (o, lse) and the output gradient `do`."""
+    _lib.require_device(q, k, v, o, do)
+    B, HQ, S, D = q.shape
+    HK = k.shape[1]
+    if do.stride() != o.stride():
+        do = do.contiguous()
+    dq = torch.empty((B, S, HQ, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+    dk = torch.empty((B, S, HK, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+    dv = torch.empty((B, S, HK, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+    ws, ws_bytes = _lib.workspace("qlora_attn_bwd_workspace_size", B, HQ, S, device=q.device)
+    _lib.call("qlora_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+              do.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+              _lib.tag(q.dtype), B, HQ, HK, S, D, _strides3(q), _strides3(k), _strides3(v),
+              _strides3(o.transpose(1, 2)), _strides3(dq), _strides3(dk), float(scale),
+              _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+    return dq, dk, dv
+
+
+class FlashAttention(torch.autograd.Function):
+    """Causal attention o [B, S, HQ, D] = softmax(scale q k^T) v for q [B, HQ, S, D] and k, v
+    [B, HK, S, D] (grouped-query heads), as the SDPA path computes it, on the flash kernels."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale):
+        o, lse = attn_fwd(q, k, v, scale, with_lse=True)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.scale = scale
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = attn_bwd(q, k, v, o, lse, do, ctx.scale)
+        return dq, dk, dv, None
+
+
+def flash_attention(q, k, v, scale=None):
+    """Causal attention on the flash kernels: o [B, S, HQ, D] (the layout transformers' SDPA
+    integration returns) for q [B, HQ, S, D] and k, v [B, HK, S, D]."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    return FlashAttention.apply(q, k, v, float(scale))
+
+
+def supported(module, query, key, value, attention_mask, dropout, is_causal, kwargs):
     """Whether a transformers attention call can take the flash kernels."""
     if not _common.on_gpu(query, key, value) or attention_mask is not None or dropout:
         return False
+    if is_causal is False or (is_causal is None and not getattr(module, "is_causal", True)):
+        return False
     if kwargs.get("output_attentions", False) or kwargs.get("position_bias") is not None:
         return False
-    if kwargs.get("sliding_window") is not None or not getattr(module, "is_causal", True):
+    if kwargs.get("sliding_window") is not None:
         return False
     if query.dtype not in (torch.bfloat16, torch.float16) or key.dtype != query.dtype \
             or value.dtype != query.dtype:
@@ -56,3 +104,24 @@ def supported(module, query, key, value, attention_mask, dropout, kwargs):
         return False
     return all(t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:3])
                and t.data_ptr() % 16 == 0 for t in (query, key, value))
+
+
+def patch():
+    """Route transformers' "sdpa" attention through `flash_attention` for the calls `supported`
+    accepts; every other call goes to the original function unchanged."""
+    from transformers.modeling_utils import AttentionInterface
+
+    original = AttentionInterface._global_mapping["sdpa"]
+    if getattr(original, "_solution_patch", False):
+        return
+
+    def sdpa_attention_forward(module, query, key, value, attention_mask, dropout=0.0,
+                               scaling=None, is_causal=None, **kwargs):
+        if not supported(module, query, key, value, attention_mask, dropout, is_causal, kwargs):
+            return original(module, query, key, value, attention_mask, dropout=dropout,
+                            scaling=scaling, is_causal=is_causal, **kwargs)
+        return flash_attention(query, key, value, scaling), None
+
+    sdpa_attention_forward._solution_patch = True
+    sdpa_attention_forward._original = original
+    AttentionInterface._global_mapping["sdpa"] = sdpa_attention_forward

@@ -51,3 +51,72 @@ def test_flash_attention_forward(B, HQ, HK, S, layout):
     assert o.shape == (B, S, HQ, 128)
     torch.testing.assert_close(o.transpose(1, 2).float(), o_ref, rtol=1e-2, atol=1e-2)
     torch.testing.assert_close(lse, lse_ref, rtol=0, atol=1e-4)
+
+
+def _ref_grads(q, k, v, do, scale):
+    qf, kf, vf = (t.detach().float().requires_grad_(True) for t in (q, k, v))
+    o, _ = _ref(qf, kf, vf, scale)
+    o.backward(do.float().transpose(1, 2))
+    return qf.grad, kf.grad, vf.grad
+
+
+def _rel_err(a, b):
+    return ((a.float() - b).norm() / b.norm()).item()
+
+
+@pytest.mark.parametrize("B,HQ,HK,S,layout", [(1, 4, 2, 256, "bshd"), (1, 2, 1, 200, "bhsd"),
+                                              (2, 28, 4, 2048, "bshd"), (1, 3, 3, 64, "bhsd"),
+                                              (1, 4, 1, 129, "bshd")])
+def test_flash_attention_backward(B, HQ, HK, S, layout):
+    """dq, dk, dv against fp32 autograd of the reference: relative Frobenius error below 1e-2
+    and every element within 2e-2 of the largest reference magnitude (bf16 inputs, P and dS
+    rounded to bf16 for the products, fp32 accumulation)."""
+    print(f"attn bwd B={B} HQ={HQ} HK={HK} S={S} {layout}", flush=True)
+    q, k, v = _inputs(B, HQ, HK, S, seed=3 * S + HQ, layout=layout)
+    g = torch.Generator(device="cuda").manual_seed(S)
+    do = torch.randn(B, S, HQ, 128, device="cuda", generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    qg, kg, vg = (t.detach().requires_grad_(True) for t in (q, k, v))
+    o = attention.flash_attention(qg, kg, vg, scale)
+    o.backward(do)
+    refs = _ref_grads(q, k, v, do, scale)
+    for name, got, want in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), refs):
+        assert got.shape == want.shape
+        err = _rel_err(got, want)
+        amax = (got.float() - want).abs().max().item()
+        print(f"  {name}: rel {err:.2e} max {amax:.2e} ref max {want.abs().max().item():.2e}")
+        assert err < 1e-2, name
+        assert amax <= 2e-2 * want.abs().max().item(), name
+
+
+def test_flash_attention_backward_is_deterministic():
+    q, k, v = _inputs(1, 8, 2, 384, seed=11)
+    do = torch.randn(1, 384, 8, 128, device="cuda").to(torch.bfloat16)
+    outs = []
+    for _ in range(2):
+        qg, kg, vg = (t.detach().requires_grad_(True) for t in (q, k, v))
+        attention.flash_attention(qg, kg, vg).backward(do)
+        outs.append((qg.grad, kg.grad, vg.grad))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_sdpa_patch_routes_supported_calls_to_flash():
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    attention.patch()
+    fn = ALL_ATTENTION_FUNCTIONS["sdpa"]
+
+    class Mod(torch.nn.Module):
+        is_causal = True
+        num_key_value_groups = 2
+
+    q, k, v = _inputs(1, 4, 2, 128, seed=5)
+    got, _ = fn(Mod(), q, k, v, None, scaling=0.088)
+    torch.testing.assert_close(got, attention.flash_attention(q, k, v, 0.088), rtol=0, atol=0)
+    # a mask sends the call to the original SDPA (fp32 here, so no bf16 batched products)
+    qf, kf, vf = q.float(), k.float(), v.float()
+    mask = torch.ones(1, 1, 128, 128, dtype=torch.bool, device="cuda").tril()
+    got, _ = fn(Mod(), qf, kf, vf, mask, scaling=0.088)
+    want, _ = fn._original(Mod(), qf, kf, vf, mask, scaling=0.088)
+    torch.testing.assert_close(got, want)

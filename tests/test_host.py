@@ -39,6 +39,28 @@ def test_patched_functions_fall_back_on_cpu_tensors():
         torch.testing.assert_close(a, b)
 
 
+def test_sdpa_patch_falls_back_on_cpu_and_unsupported_calls():
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    from hackathon_amd import attention
+
+    hackathon_amd.apply()
+    fn = ALL_ATTENTION_FUNCTIONS["sdpa"]
+    assert getattr(fn, "_solution_patch", False)
+
+    class Mod(torch.nn.Module):
+        is_causal = True
+        num_key_value_groups = 2
+
+    q = torch.randn(1, 4, 6, 128, dtype=torch.bfloat16)
+    k = torch.randn(1, 2, 6, 128, dtype=torch.bfloat16)
+    v = torch.randn(1, 2, 6, 128, dtype=torch.bfloat16)
+    got, _ = fn(Mod(), q, k, v, None, scaling=0.1)
+    want, _ = fn._original(Mod(), q, k, v, None, scaling=0.1)
+    torch.testing.assert_close(got, want)
+    assert not attention.supported(Mod(), q, k, v, None, 0.0, None, {})
+
+
 def test_rope_supported_guard():
     q = torch.randn(2, 4, 5, 16)
     k = torch.randn(2, 2, 5, 16)
