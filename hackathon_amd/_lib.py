@@ -78,7 +78,7 @@ _SIZE_QUERIES = {
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64],
     "qlora_nf4_quantize_workspace_size": [_c_i64, _c_int, _c_int],
-    "qlora_attn_bwd_workspace_size": [_c_i64, _c_i64, _c_i64],
+    "qlora_attn_bwd_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64],
 }
 
 _lib = None

@@ -50,7 +50,8 @@ def attn_bwd(q, k, v, o, lse, do, scale):
     dq = torch.empty((B, S, HQ, D), dtype=q.dtype, device=q.device).transpose(1, 2)
     dk = torch.empty((B, S, HK, D), dtype=q.dtype, device=q.device).transpose(1, 2)
     dv = torch.empty((B, S, HK, D), dtype=q.dtype, device=q.device).transpose(1, 2)
-    ws, ws_bytes = _lib.workspace("qlora_attn_bwd_workspace_size", B, HQ, S, device=q.device)
+    ws, ws_bytes = _lib.workspace("qlora_attn_bwd_workspace_size", B, HQ, HK, S,
+                                  device=q.device)
     _lib.call("qlora_attn_bwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
               do.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
               _lib.tag(q.dtype), B, HQ, HK, S, D, _strides3(q), _strides3(k), _strides3(v),

@@ -1,23 +1,27 @@
-// Causal flash attention (forward) for the QLoRA step's attention, on CDNA4 matrix cores.
+// Causal flash attention, forward and backward, for the QLoRA step on CDNA4 matrix cores.
 //
 // The reference step runs attention through torch's scaled_dot_product_attention
-// (transformers/models/qwen2/modeling_qwen2.py:220, the SDPA path of Qwen2Attention); this is
-// the native replacement: O = softmax(Q K^T * scale, causal) V with grouped-query heads, bf16
-// in and out, fp32 accumulation and softmax, and the row log-sum-exp kept for the backward.
+// (transformers/models/qwen2/modeling_qwen2.py:220, the SDPA path of Qwen2Attention); these
+// kernels are the native replacement: O = softmax(Q K^T * scale, causal) V with grouped-query
+// heads, 16-bit in and out, fp32 accumulation and softmax, and the row log-sum-exp kept for
+// the backward. The backward follows the FlashAttention-2 split: Delta = rowsum(dO * O), then
+// dK, dV per key block and dQ per query block, each recomputing P from Q, K and the lse.
 //
-// One workgroup (4 waves) per (batch, query head, 128-row query block); wave w owns query
-// rows 32w .. 32w+31 of the block. Per 64-key block:
-//   S^T = K Q^T      v_mfma_f32_16x16x32: K fragments from LDS ([key][d], 16-B chunks XOR-
-//                    swizzled by key & 7), Q fragments held in registers for the whole loop.
-//                    A lane ends up owning one query column (lane % 16) and 4 keys per 16-key
-//                    tile, so the online softmax is per lane plus two cross-lane steps.
-//   P = exp2(S log2e * scale - m)   online max / sum in fp32 (masked keys: -inf)
-//   O^T += V^T P^T   the P^T register tile is itself the B operand (a 32-key step is two
-//                    16-key tiles; the key order inside an MFMA step is a permutation, used
-//                    identically for V^T); V^T comes from LDS ([d][key], 8-B units XOR-
-//                    swizzled by d & 15), written there through an in-register 8 x 8 transpose.
-// The next key block is loaded into registers while the current one is multiplied.
-// Requires head_dim = 128; any sequence length (rows and keys past the end are masked).
+// Building blocks shared by every kernel:
+//  - v_mfma_f32_16x16x32 (bf16 or fp16). A pair of C tiles stacked along their rows is itself
+//    an MFMA operand whose contraction index is that row index (the order inside a 32-step is
+//    a permutation, applied identically to the other operand), so P, P^T, dS and dS^T feed
+//    the next product straight from registers.
+//  - 64-row x 128-d tiles (256-B rows) moved global -> LDS by direct-to-LDS loads (no VGPR
+//    staging), with the 16-B chunks of row r XOR-swizzled by f(r) = 2 (r & 3) | ((r >> 2) & 1).
+//    Row fragments (ds_read_b128: 8 lanes on 8 consecutive rows, one logical chunk) meet 8
+//    distinct f, and transposing reads (ds_read_b64_tr_b16: 16 lanes on 4 consecutive rows x
+//    32 B) meet 4 distinct f >> 1, i.e. 4 different 32-B bank groups: both are conflict-free,
+//    so one LDS copy of a matrix serves the matrix and its transpose.
+//  - two LDS stages per kernel: the next block's DMA runs under the current block's math,
+//    with one barrier per block.
+//  - 4 waves per workgroup and at most 256 registers per lane, so two workgroups share a CU.
+// Head dim 128; any sequence length (rows and keys past the end are masked and clamped).
 #include "ql_vec.h"
 
 namespace {
@@ -25,15 +29,22 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
-constexpr int HD = 128;        // head dim
-constexpr int BQ = 128;        // query rows per workgroup
-constexpr int BKV = 64;        // keys per block
+constexpr int HD = 128;                         // head dim
+constexpr int kRows = 64;                       // rows per LDS tile / key block
+constexpr int kRowBytes = HD * 2;               // 256
+constexpr int kTileBytes = kRows * kRowBytes;   // 16 KiB
+constexpr int BQ = 128;                         // forward, dQ: query rows per workgroup
 constexpr int kThreads = 256;
-constexpr int kKRow = HD * 2;  // bytes per K row in LDS (256)
-constexpr int kVRow = BKV * 2; // bytes per V^T row in LDS (128)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// Lazy rescaling threshold (log2 units): the running max m is only raised when a block's max
+// exceeds it by more than this, so P = exp2(x - m) <= 2^8 stays well inside fp32 and bf16.
+constexpr float kTau = 8.0f;
 
 template <int DT> QL_DEV f32x4_t mfma(const uint4& a, const uint4& b, f32x4_t c);
 template <> QL_DEV f32x4_t mfma<QL_BF16>(const uint4& a, const uint4& b, f32x4_t c) {
@@ -50,23 +61,98 @@ template <int DT> QL_DEV uint32_t pack2(float lo, float hi) {
   else return pack_f16x2(lo, hi);
 }
 
-// 8 x 8 transpose of 16-bit values: in[i] = row i as 4 words (column pairs) -> out[t] = column t.
-QL_DEV void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    uint32_t w[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint4& r0 = in[2 * p];
-      const uint4& r1 = in[2 * p + 1];
-      const int q = t >> 1;
-      const uint32_t a = q == 0 ? r0.x : q == 1 ? r0.y : q == 2 ? r0.z : r0.w;
-      const uint32_t b = q == 0 ? r1.x : q == 1 ? r1.y : q == 2 ? r1.z : r1.w;
-      w[p] = (t & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
-    }
-    out[t] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
+// Two stacked C tiles (rows 0-15 and 16-31 of a 32-step) as one 16-bit operand.
+template <int DT> QL_DEV uint4 pack_pair(const f32x4_t& a, const f32x4_t& c) {
+  return make_uint4(pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]),
+                    pack2<DT>(c[2], c[3]));
 }
+
+QL_DEV f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
+
+// ---- LDS tiles -------------------------------------------------------------------------------
+QL_DEV int swz_chunk(int chunk, int row) { return chunk ^ ((2 * (row & 3)) | ((row >> 2) & 1)); }
+QL_DEV int tile_off(int row, int chunk) { return row * kRowBytes + swz_chunk(chunk, row) * 16; }
+
+// Transposing LDS read (ds_read_b64_tr_b16). Within each group of 16 lanes, lane i receives
+// element i % 4 of the 8-B chunks addressed by lanes 4 j + i / 4, j = 0..3: with lane 4 j + c
+// addressing row r_j, columns n0 + 4 c .. +3 of a row-major tile, lane i gets column n0 + i
+// of rows r_0 .. r_3 (4 consecutive contraction values of an MFMA operand column).
+QL_DEV uint2 read_tr(const char* p) {
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Operand fragment (16 rows x 32 contraction) along the rows of a tile: lane holds row `row`,
+// head-dim values 32 ks + 8 (lane / 16) .. +7.
+QL_DEV uint4 frag_row(const char* __restrict__ t, int row, int ks, int fq) {
+  return *reinterpret_cast<const uint4*>(t + tile_off(row, 4 * ks + fq));
+}
+
+// Operand fragment whose contraction index runs over tile rows, read transposed: lane holds
+// head-dim column c0 + lane % 16 at tile rows r0 + 4 (lane / 16) + j (positions 0..3) and
+// r0 + 16 + 4 (lane / 16) + j (positions 4..7), the row order of two stacked C tiles, so it
+// pairs with `pack_pair` operands. r0 is a multiple of 8.
+QL_DEV uint4 frag_tr(const char* __restrict__ t, int r0, int c0, int fq, int fr) {
+  const int row = r0 + 4 * fq + (fr >> 2);
+  const int col = c0 + 4 * (fr & 3);
+  const int off = tile_off(row, col >> 3) + (col & 4) * 2;
+  const uint2 a = read_tr(t + off);
+  const uint2 b = read_tr(t + off + 16 * kRowBytes);  // row + 16: same swizzle
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+// Direct-to-LDS loader of one 64-row tile (rows row0 .. row0 + 63 of X, row stride ld
+// elements; rows past S re-read row S - 1) by the 4 waves of a workgroup: load i of wave w
+// fills tile rows 4p .. 4p + 3 with p = 4 i + w; lane l writes LDS bytes [16 l, 16 l + 16) of
+// that 1 KiB span, i.e. row 4p + l / 16, physical chunk l % 16, which holds the logical chunk
+// the swizzle maps there (an XOR is its own inverse). Row 4p + l / 16 has row & 7 =
+// 4 (w & 1) + l / 16 for every load, so the lane's byte offset from the span's first row is
+// fixed: each load is a wave-uniform base (SGPRs) plus that offset.
+struct TileDma {
+  uint32_t off;
+  int rsub, wave;
+  QL_DEV void init(int64_t ld, int wave_, int lane) {
+    wave = wave_;
+    rsub = lane >> 4;
+    off = (uint32_t)rsub * (uint32_t)(ld * 2) +
+          (uint32_t)(swz_chunk(lane & 15, 4 * (wave & 1) + rsub) * 16);
+  }
+  QL_DEV void issue(const uint16_t* __restrict__ X, int64_t ld, int64_t row0, int64_t S,
+                    char* __restrict__ tile) const {
+    const int lane = threadIdx.x & 63;
+    if (row0 + kRows <= S) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = 4 * i + wave;
+        const char* base = reinterpret_cast<const char*>(X + (row0 + 4 * p) * ld);
+        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(base + off), (lds_ptr_t)(tile + p * 1024),
+                                         16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = 4 * i + wave;
+        const int64_t gb = row0 + 4 * p;
+        const int64_t base_row = gb < S ? gb : S - 1;
+        const int64_t gr = gb + rsub < S ? gb + rsub : S - 1;
+        const uint32_t o = (uint32_t)(gr - base_row) * (uint32_t)(ld * 2) +
+                           (uint32_t)(swz_chunk(lane & 15, 4 * p + rsub) * 16);
+        const char* base = reinterpret_cast<const char*>(X + base_row * ld);
+        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(base + o), (lds_ptr_t)(tile + p * 1024),
+                                         16, 0, 0);
+      }
+    }
+  }
+};
+
+// This thread's DMA and LDS writes are done, and every wave of the workgroup got here.
+// (__syncthreads would also do, but inline asm keeps the compiler from adding its own waits.)
+QL_DEV void wait_all_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Index differences used by the branch-free masks, clamped into int range.
+QL_DEV int clamp_rel(int64_t x) { return (int)(x < -4096 ? -4096 : x > 4096 ? 4096 : x); }
 
 struct AttnShape {
   int64_t B, HQ, HK, S;
@@ -77,79 +163,127 @@ struct AttnShape {
   float scale;
 };
 
-// Staging registers of one 64-key block for this thread: threads 0..127 hold 8 16-B chunks of
-// K (key rows), threads 128..255 an 8 (key) x 8 (d) block of V.
-struct KVStage {
-  uint4 r[8];
+// =============================================================================================
+// Forward. One workgroup per (b, hq, 128-row query block), heaviest (last) blocks first; wave
+// w owns query rows 32 w .. +31. Per 64-key block:
+//   S^T = K Q^T     K fragments from LDS, Q fragments in registers for the whole loop; a lane
+//                   owns one query column (lane % 16) and 4 keys per 16-key tile
+//   online softmax  per lane: block max over the lane's 16 keys plus two cross-lane steps, lazy
+//                   rescaling of O (only when the max rises by more than kTau), the row sum
+//                   kept per lane and combined once at the end
+//   O^T += V^T P^T  V^T fragments by transposing reads, P^T straight from registers
+template <int DT>
+struct FwdState {
+  uint4 qf[2][4];     // B operands: column q = 16 qt + lane % 16, d = 32 ds + 8 (lane / 16) ..
+  f32x4_t o[2][8];    // [qt][dt]: rows d = 16 dt + 4 (lane / 16) + e, column q
+  float m[2], l[2];
 };
 
-QL_DEV void load_kv(KVStage& st, const uint16_t* __restrict__ kbase, int64_t ks_s,
-                    const uint16_t* __restrict__ vbase, int64_t vs_s, int64_t key0, int64_t S) {
-  const int t = threadIdx.x;
-  if (t < 128) {
-    // K: 64 rows x 16 chunks = 1024 chunks; chunk id c = t + 128 i: row c / 16, chunk c % 16
+// `kl`, `vl`: this block's K and V tiles; `kn`, `vn`: the other stage, which the next block's
+// DMA fills meanwhile (restrict keeps the compiler's wait-count pass from making these LDS
+// reads wait for that DMA).
+template <int DT>
+QL_DEV void fwd_block(FwdState<DT>& st, const char* __restrict__ kl, const char* __restrict__ vl,
+                      char* __restrict__ kn, char* __restrict__ vn, bool issue,
+                      const TileDma& kdma, const TileDma& vdma, const uint16_t* __restrict__ kbase,
+                      const uint16_t* __restrict__ vbase, int64_t ks_s, int64_t vs_s, int64_t key0,
+                      int64_t q0, int64_t S, float sl2, int lane) {
+  const int fr = lane & 15, fq = lane >> 4;
+  if (issue) {
+    kdma.issue(kbase, ks_s, key0 + kRows, S, kn);
+    vdma.issue(vbase, vs_s, key0 + kRows, S, vn);
+  }
+  if (key0 > q0 + 31) return;  // every key of the block is after this wave's rows
+  f32x4_t s[2][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = t + 128 * i;
-      const int64_t key = key0 + (c >> 4);
-      const int64_t kc = key < S ? key : S - 1;
-      st.r[i] = *reinterpret_cast<const uint4*>(kbase + kc * ks_s + (c & 15) * 8);
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) s[qt][kt] = zero4();
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const uint4 kf = frag_row(kl, 16 * kt + fr, ds, fq);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma<DT>(kf, st.qf[qt][ds], s[qt][kt]);
     }
-  } else {
-    // V: 8 key groups x 16 d groups; thread u = t - 128 takes key group u / 16, d group u % 16
-    const int u = t - 128;
-    const int64_t kg = key0 + 8 * (u >> 4);
-    const int dg = 8 * (u & 15);
+  // mask keys after the query row or past the end; block max per query column
+  const bool need_mask = key0 + kRows - 1 > q0 || key0 + kRows > S;
+  float bm[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t key = kg + i;
-      const int64_t kc = key < S ? key : S - 1;
-      st.r[i] = *reinterpret_cast<const uint4*>(vbase + kc * vs_s + dg);
+  for (int qt = 0; qt < 2; ++qt) {
+    if (need_mask) {
+      // key = key0 + 16 kt + 4 fq + e is kept iff 16 kt + e <= lim
+      const int64_t q = q0 + 16 * qt + fr;
+      const int64_t last = (q < S - 1 ? q : S - 1) - key0;
+      const int lim = (int)(last < kRows ? last : kRows) - 4 * fq;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[qt][kt][e] = 16 * kt + e > lim ? -INFINITY : s[qt][kt][e];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[qt][kt][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    bm[qt] = mx * sl2;
+  }
+  const bool raise = bm[0] > st.m[0] + kTau || bm[1] > st.m[1] + kTau;
+  if (__builtin_amdgcn_ballot_w64(raise)) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float mn = fmaxf(st.m[qt], bm[qt]);
+      const float alpha = __builtin_amdgcn_exp2f(st.m[qt] - mn);  // m = -inf: alpha = 0
+      st.l[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) st.o[qt][dt] *= alpha;
+      st.m[qt] = mn;
     }
   }
-}
-
-// Write a staged block into LDS: K rows swizzled by 16-B chunk, V transposed into [d][key]
-// rows swizzled by 8-B unit.
-QL_DEV void store_kv(const KVStage& st, char* __restrict__ kl, char* __restrict__ vl) {
-  const int t = threadIdx.x;
-  if (t < 128) {
+  uint4 pf[2][2];  // [ks][qt]
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = t + 128 * i;
-      const int row = c >> 4, ch = c & 15;
-      const int phys = ch ^ (row & 7);
-      *reinterpret_cast<uint4*>(kl + row * kKRow + phys * 16) = st.r[i];
-    }
-  } else {
-    const int u = t - 128;
-    const int k0 = 8 * (u >> 4);
-    const int d0 = 8 * (u & 15);
-    uint4 tr[8];
-    transpose8x8(st.r, tr);
+  for (int qt = 0; qt < 2; ++qt) {
+    const float nm = -st.m[qt];
+    float rs = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = d0 + j;
-      const int u0 = (k0 >> 2) ^ (d & 15), u1 = ((k0 >> 2) + 1) ^ (d & 15);
-      *reinterpret_cast<uint2*>(vl + d * kVRow + u0 * 8) = make_uint2(tr[j].x, tr[j].y);
-      *reinterpret_cast<uint2*>(vl + d * kVRow + u1 * 8) = make_uint2(tr[j].z, tr[j].w);
-    }
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][e], sl2, nm));
+        s[qt][kt][e] = p;
+        rs += p;
+      }
+    st.l[qt] += rs;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) pf[ks][qt] = pack_pair<DT>(s[qt][2 * ks], s[qt][2 * ks + 1]);
   }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint4 vf = frag_tr(vl, 32 * ks, 16 * dt, fq, fr);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) st.o[qt][dt] = mfma<DT>(vf, pf[ks][qt], st.o[qt][dt]);
+    }
 }
 
 template <int DT>
-__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    uint16_t* __restrict__ O, float* __restrict__ lse, AttnShape sh, int n_qblocks) {
-  __shared__ __attribute__((aligned(16))) char k_lds[2][BKV * kKRow];
-  __shared__ __attribute__((aligned(16))) char v_lds[2][HD * kVRow];
-  // heaviest (last) query blocks first
-  const int qb = n_qblocks - 1 - (int)(blockIdx.x % n_qblocks);
-  const int64_t bh = blockIdx.x / n_qblocks;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                     const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
+                     float* __restrict__ lse, AttnShape sh, int n_qblocks) {
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // [stage][K, V]
+  const int64_t BH = sh.B * sh.HQ;
+  const int qb = n_qblocks - 1 - (int)(blockIdx.x / BH);  // heaviest blocks first
+  const int64_t bh = blockIdx.x % BH;
   const int64_t b = bh / sh.HQ, hq = bh % sh.HQ;
   const int64_t hk = hq / (sh.HQ / sh.HK);
   const int64_t S = sh.S;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 15, fq = lane >> 4;
   const int64_t q0 = (int64_t)qb * BQ + 32 * wave;  // this wave's first query row
 
@@ -157,154 +291,62 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(
   const uint16_t* kbase = K + b * sh.ks_b + hk * sh.ks_h;
   const uint16_t* vbase = V + b * sh.vs_b + hk * sh.vs_h;
 
-  // Q fragments (B operand: column q = lane % 16, d = 32 ds + 8 (lane / 16) .. +7)
-  uint4 qf[2][4];
+  FwdState<DT> st;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int64_t q = q0 + 16 * qt + fr;
     const int64_t qc = q < S ? q : S - 1;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
-      qf[qt][ds] = *reinterpret_cast<const uint4*>(qbase + qc * sh.qs_s + 32 * ds + 8 * fq);
+      st.qf[qt][ds] = *reinterpret_cast<const uint4*>(qbase + qc * sh.qs_s + 32 * ds + 8 * fq);
+    st.m[qt] = -INFINITY;
+    st.l[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) st.o[qt][dt] = zero4();
   }
-
   const float sl2 = sh.scale * kLog2e;
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  f32x4_t o[2][8];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int64_t q_end = (int64_t)(qb + 1) * BQ;              // causal: keys < q_end
+  const int64_t q_end = (int64_t)(qb + 1) * BQ;  // causal: keys < q_end
   const int64_t kv_end = q_end < S ? q_end : S;
-  const int nkv = (int)((kv_end + BKV - 1) / BKV);
+  const int nkv = (int)((kv_end + kRows - 1) / kRows);
 
-  KVStage st;
-  load_kv(st, kbase, sh.ks_s, vbase, sh.vs_s, 0, S);
-  store_kv(st, k_lds[0], v_lds[0]);
-  __syncthreads();
+  TileDma kdma, vdma;
+  kdma.init(sh.ks_s, wave, lane);
+  vdma.init(sh.vs_s, wave, lane);
+  kdma.issue(kbase, sh.ks_s, 0, S, smem);
+  vdma.issue(vbase, sh.vs_s, 0, S, smem + kTileBytes);
   for (int j = 0; j < nkv; ++j) {
-    const int buf = j & 1;
-    const int64_t key0 = (int64_t)j * BKV;
-    if (j + 1 < nkv) load_kv(st, kbase, sh.ks_s, vbase, sh.vs_s, key0 + BKV, S);
-    const char* kl = k_lds[buf];
-    const char* vl = v_lds[buf];
-    // ---- S^T = K Q^T: s[qt][kt] holds keys 16 kt + 4 (lane/16) + e, query column lane % 16
-    f32x4_t s[2][4];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) s[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const int row = 16 * kt + fr;
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const int ch = (4 * ds + fq) ^ (row & 7);
-        const uint4 kf = *reinterpret_cast<const uint4*>(kl + row * kKRow + ch * 16);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma<DT>(kf, qf[qt][ds], s[qt][kt]);
-      }
-    }
-    // ---- online softmax per query column
-    const bool need_mask = key0 + BKV > q0 || key0 + BKV > S;  // this wave's rows start at q0
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const int64_t q = q0 + 16 * qt + fr;
-      float bm = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = s[qt][kt][e] * sl2;
-          if (need_mask) {
-            const int64_t key = key0 + 16 * kt + 4 * fq + e;
-            if (key > q || key >= S) v = -INFINITY;
-          }
-          s[qt][kt][e] = v;
-          bm = fmaxf(bm, v);
-        }
-      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-      const float mn = fmaxf(m[qt], bm);
-      const float alpha = exp2f(m[qt] - mn);  // m = -inf on the first block: alpha = 0
-      float rs = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = exp2f(s[qt][kt][e] - mn);
-          s[qt][kt][e] = p;
-          rs += p;
-        }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
-      l[qt] = l[qt] * alpha + rs;
-      m[qt] = mn;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= alpha;
-    }
-    // ---- O^T += V^T P^T over two 32-key steps; P^T tiles (2 ks, 2 ks + 1) form the B operand
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint4 pf[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const f32x4_t& a = s[qt][2 * ks];
-        const f32x4_t& c = s[qt][2 * ks + 1];
-        pf[qt] = make_uint4(pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]),
-                            pack2<DT>(c[2], c[3]));
-      }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = 16 * dt + fr;
-        const int u0 = (8 * ks + fq) ^ (d & 15);       // keys 32 ks + 4 (lane/16) .. +3
-        const int u1 = (8 * ks + 4 + fq) ^ (d & 15);   // keys 32 ks + 16 + 4 (lane/16) .. +3
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vl + d * kVRow + u0 * 8);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vl + d * kVRow + u1 * 8);
-        const uint4 vf = make_uint4(v0.x, v0.y, v1.x, v1.y);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) o[qt][dt] = mfma<DT>(vf, pf[qt], o[qt][dt]);
-      }
-    }
-    if (j + 1 < nkv) {
-      store_kv(st, k_lds[buf ^ 1], v_lds[buf ^ 1]);
-    }
-    __syncthreads();
+    // block j's tiles are in LDS, and every wave is past block j - 1, whose stage the DMA
+    // issued in this step overwrites
+    wait_all_barrier();
+    char* cur = smem + (j & 1) * 2 * kTileBytes;
+    char* nxt = smem + ((j + 1) & 1) * 2 * kTileBytes;
+    fwd_block<DT>(st, cur, cur + kTileBytes, nxt, nxt + kTileBytes, j + 1 < nkv, kdma, vdma,
+                  kbase, vbase, sh.ks_s, sh.vs_s, (int64_t)j * kRows, q0, S, sl2, lane);
   }
 
-  // ---- O = O^T / l, lse = (m + log2 l) ln 2 (natural log of sum exp(scale * s))
+  // O = O^T / l, lse = (m + log2 l) ln 2 (natural log of sum exp(scale * s))
   uint16_t* obase = O + b * sh.os_b + hq * sh.os_h;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
+    float l = st.l[qt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
     const int64_t q = q0 + 16 * qt + fr;
     if (q >= S) continue;
-    const float inv = 1.0f / l[qt];
+    const float inv = 1.0f / l;
     uint16_t* orow = obase + q * sh.os_s;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const f32x4_t v = o[qt][dt] * inv;
+      const f32x4_t v = st.o[qt][dt] * inv;
       *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * fq) =
           make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
     }
-    if (fq == 0 && lse) lse[bh * S + q] = (m[qt] + log2f(l[qt])) * kLn2;
+    if (fq == 0 && lse) lse[bh * S + q] = (st.m[qt] + log2f(l)) * kLn2;
   }
 }
 
-// =========================================================================================
-// Backward (FlashAttention-2 split): Delta = rowsum(dO * O); dK, dV per key block looping over
-// the query heads of its group and the query blocks at or below the diagonal; dQ per query
-// block looping over key blocks. P is recomputed from Q, K and the forward's log-sum-exp.
-// All products use v_mfma_f32_16x16x32 with the register tile of one product feeding the
-// next as an operand: a C tile pair stacked along its rows is an operand whose contraction
-// index is that row index (the positions inside a 32-step form a permutation, applied to
-// both operands). Transposed copies (Q^T, dO^T, K^T) are written to LDS through an
-// in-register 8 x 8 transpose; LDS rows are swizzled (16-B chunks by row & 7 for 256-B rows,
-// 8-B units by row & 15 for 128-B rows) so fragment reads are conflict-free.
-
-constexpr int BB = 64;  // rows per staged block in the backward kernels
-
+// =============================================================================================
+// Backward.
 struct BwdShape {
   int64_t B, HQ, HK, S;
   int64_t qs_b, qs_h, qs_s, ks_b, ks_h, ks_s, vs_b, vs_h, vs_s;
@@ -337,258 +379,287 @@ __global__ __launch_bounds__(256) void attn_bwd_delta(const uint16_t* __restrict
   if (part == 0 && r < total) delta[r] = acc;
 }
 
-// Stage an 8 (rows) x 8 (d) block of a [rows, 128] matrix: row-major into a 256-B-row LDS
-// tile and transposed into a 128-B-row ([d][row]) LDS tile.
-QL_DEV void put_rowmajor(char* __restrict__ lds, const uint4 (&r)[8], int row0, int d0) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = row0 + i;
-    const int phys = (d0 >> 3) ^ (row & 7);
-    *reinterpret_cast<uint4*>(lds + row * kKRow + phys * 16) = r[i];
-  }
-}
+// ---- dK, dV: one workgroup per (b, hq, 64-key block), heaviest (first) key blocks first; wave
+// w owns keys 16 w .. +15 of the block. Per 64-row query block at or below the diagonal:
+//   S = Q K^T, dP = dO V^T      Q, dO row fragments from LDS; K, V fragments in registers
+//   P = exp2(S scale log2e - lse log2e), dS = P (dP - Delta)
+//   dV^T += dO^T P, dK^T += Q^T dS    dO^T, Q^T by transposing reads; P, dS from registers
+// With several query heads per kv head, each head's dK, dV go to fp32 partials that
+// attn_bwd_reduce sums in head order; otherwise the kernel writes the 16-bit gradients itself.
+constexpr int kBwdStage = 2 * kTileBytes + 512;  // Q tile, dO tile, lse2 [64], delta [64]
 
-QL_DEV void put_transposed(char* __restrict__ lds, const uint4 (&r)[8], int row0, int d0) {
-  uint4 tr[8];
-  transpose8x8(r, tr);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int d = d0 + j;
-    const int u0 = (row0 >> 2) ^ (d & 15), u1 = ((row0 >> 2) + 1) ^ (d & 15);
-    *reinterpret_cast<uint2*>(lds + d * kVRow + u0 * 8) = make_uint2(tr[j].x, tr[j].y);
-    *reinterpret_cast<uint2*>(lds + d * kVRow + u1 * 8) = make_uint2(tr[j].z, tr[j].w);
-  }
-}
-
-// A fragment of a row-major [rows][128] LDS tile: row, d = 32 ds + 8 (lane/16) .. +7.
-QL_DEV uint4 frag_rm(const char* __restrict__ lds, int row, int ds, int fq) {
-  const int ch = (4 * ds + fq) ^ (row & 7);
-  return *reinterpret_cast<const uint4*>(lds + row * kKRow + ch * 16);
-}
-
-// A fragment of a transposed [128][64] LDS tile at row d over the permuted 32-step whose
-// positions 0-3 are columns 32 ks + 4 (lane/16) .. +3 and 4-7 are 32 ks + 16 + 4 (lane/16) ..
-QL_DEV uint4 frag_tr(const char* __restrict__ lds, int d, int ks, int fq) {
-  const int u0 = (8 * ks + fq) ^ (d & 15), u1 = (8 * ks + 4 + fq) ^ (d & 15);
-  const uint2 a = *reinterpret_cast<const uint2*>(lds + d * kVRow + u0 * 8);
-  const uint2 b = *reinterpret_cast<const uint2*>(lds + d * kVRow + u1 * 8);
-  return make_uint4(a.x, a.y, b.x, b.y);
-}
-
-// Pack two stacked C tiles (rows 0-15 and 16-31 of a 32-step) into one operand.
-template <int DT> QL_DEV uint4 pack_pair(const f32x4_t& a, const f32x4_t& c) {
-  return make_uint4(pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(c[0], c[1]),
-                    pack2<DT>(c[2], c[3]));
-}
-
-// ---- dK, dV: one workgroup per (b, hk, 64-key block). Wave w: query half qh = w & 1 (rows
-// 32 qh .. +31 of each 64-row query block), key half kh = w >> 1 (keys 32 kh .. +31). Each
-// wave accumulates dV^T and dK^T for its 32 keys over its query rows; the two query halves
-// are summed through LDS at the end.
 template <int DT>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
-    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, BwdShape sh, int n_kblocks) {
-  // per buffer: Q [64][128], Q^T [128][64], dO [64][128], dO^T [128][64], lse2 [64], delta [64]
-  constexpr int kTile = BB * kKRow;  // 16 KiB
-  constexpr int kBuf = 4 * kTile + 2 * BB * 4;
-  __shared__ __attribute__((aligned(16))) char smem[2 * kBuf];
-  const int kb = (int)(blockIdx.x % n_kblocks);
-  const int64_t bhk = blockIdx.x / n_kblocks;
-  const int64_t b = bhk / sh.HK, hk = bhk % sh.HK;
-  const int64_t S = sh.S;
-  const int group = (int)(sh.HQ / sh.HK);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct DkdvState {
+  uint4 kf[4], vf[4];      // B operands: column key lane % 16, d = 32 ds + 8 (lane / 16) .. +7
+  f32x4_t dv[8], dk[8];    // [dt]: rows d = 16 dt + 4 (lane / 16) + e, column key
+};
+
+template <int DT>
+QL_DEV void dkdv_block(DkdvState<DT>& st, const char* __restrict__ cur, char* __restrict__ nxt,
+                       bool issue, const TileDma& qdma, const TileDma& odma,
+                       const uint16_t* __restrict__ qbase, const uint16_t* __restrict__ obase,
+                       int64_t qs_s, int64_t os_s, int64_t qrow0, int64_t S, bool need_mask,
+                       int kq_rel, int qlim, float sl2, int lane) {
   const int fr = lane & 15, fq = lane >> 4;
-  const int qh = wave & 1, kh = wave >> 1;
-  const int64_t key0 = (int64_t)kb * BB + 32 * kh;  // this wave's first key
-  const float sl2 = sh.scale * kLog2e;
-
-  // K and V fragments of this wave's 32 keys (B operands: column key, k = d)
-  uint4 kf[2][4], vf[2][4];
-  const uint16_t* kbase = K + b * sh.ks_b + hk * sh.ks_h;
-  const uint16_t* vbase = V + b * sh.vs_b + hk * sh.vs_h;
+  if (issue) {
+    qdma.issue(qbase, qs_s, qrow0 + kRows, S, nxt);
+    odma.issue(obase, os_s, qrow0 + kRows, S, nxt + kTileBytes);
+  }
+  const char* q_l = cur;
+  const char* do_l = cur + kTileBytes;
+  const float* lse2 = reinterpret_cast<const float*>(cur + 2 * kTileBytes);
+  const float* dlt = lse2 + kRows;
+  f32x4_t sp[4], dp[4];  // [qt]: rows q = 16 qt + 4 (lane / 16) + e, column key
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    const int64_t key = key0 + 16 * kt + fr;
-    const int64_t kc = key < S ? key : S - 1;
+  for (int qt = 0; qt < 4; ++qt) sp[qt] = dp[qt] = zero4();
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      kf[kt][ds] = *reinterpret_cast<const uint4*>(kbase + kc * sh.ks_s + 32 * ds + 8 * fq);
-      vf[kt][ds] = *reinterpret_cast<const uint4*>(vbase + kc * sh.vs_s + 32 * ds + 8 * fq);
+  for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      const int row = 16 * qt + fr;
+      sp[qt] = mfma<DT>(frag_row(q_l, row, ds, fq), st.kf[ds], sp[qt]);
+      dp[qt] = mfma<DT>(frag_row(do_l, row, ds, fq), st.vf[ds], dp[qt]);
+    }
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const int r4 = 16 * qt + 4 * fq;
+    const float4 l4 = *reinterpret_cast<const float4*>(lse2 + r4);
+    const float4 d4 = *reinterpret_cast<const float4*>(dlt + r4);
+    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+    const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][e], sl2, -lv[e]));
+      // key - q = kq_rel - 16 qt - e; rows at or past the end: 16 qt + e >= qlim
+      if (need_mask) p = (kq_rel - 16 * qt - e > 0 || 16 * qt + e >= qlim) ? 0.f : p;
+      sp[qt][e] = p;
+      dp[qt][e] = p * (dp[qt][e] - dv[e]);
     }
   }
-  f32x4_t dvt[2][8], dkt[2][8];  // [kt][dt]: rows d = 16 dt + 4 (lane/16) + e, column key
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int ks = 0; ks < 2; ++ks) {
+    const uint4 pb = pack_pair<DT>(sp[2 * ks], sp[2 * ks + 1]);
+    const uint4 sb = pack_pair<DT>(dp[2 * ks], dp[2 * ks + 1]);
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) dvt[kt][dt] = dkt[kt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const int n_qb = (int)((S + BB - 1) / BB);
-  const int n_iter = group * (n_qb - kb);  // (head, query block) pairs at or below the diagonal
-  // staging: threads 0..127 take an 8 x 8 block of Q, 128..255 of dO; row group (t%128)/16,
-  // d group t%16; threads 0..63 also stage lse, 64..127 delta
-  const int t = threadIdx.x;
-  const int u = t & 127;
-  const int srow0 = 8 * (u >> 4), sd0 = 8 * (u & 15);
-  uint4 st[8];
-  float st_x = 0.f;
-  auto load_stage = [&](int it) {
-    const int64_t hq = hk * group + it / (n_qb - kb);
-    const int qb = kb + it % (n_qb - kb);
-    const uint16_t* base = t < 128 ? Q + b * sh.qs_b + hq * sh.qs_h : dO + b * sh.os_b + hq * sh.os_h;
-    const int64_t rs = t < 128 ? sh.qs_s : sh.os_s;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t q = (int64_t)qb * BB + srow0 + i;
-      const int64_t qc = q < S ? q : S - 1;
-      st[i] = *reinterpret_cast<const uint4*>(base + qc * rs + sd0);
-    }
-    if (t < 128) {
-      const int64_t q = (int64_t)qb * BB + (t & 63);
-      const int64_t qc = q < S ? q : S - 1;
-      const int64_t row = (b * sh.HQ + hq) * S + qc;
-      st_x = t < 64 ? lse[row] * kLog2e : delta[row];
-    }
-  };
-  auto store_stage = [&](char* buf) {
-    char* rm = buf + (t < 128 ? 0 : 2 * kTile);
-    char* tr = buf + (t < 128 ? kTile : 3 * kTile);
-    put_rowmajor(rm, st, srow0, sd0);
-    put_transposed(tr, st, srow0, sd0);
-    if (t < 128) reinterpret_cast<float*>(buf + 4 * kTile)[t] = st_x;  // lse2 [64], delta [64]
-  };
-
-  if (n_iter > 0) {
-    load_stage(0);
-    store_stage(smem);
-  }
-  __syncthreads();
-  for (int it = 0; it < n_iter; ++it) {
-    char* buf = smem + (it & 1) * kBuf;
-    if (it + 1 < n_iter) load_stage(it + 1);
-    const int qb = kb + it % (n_qb - kb);
-    const int64_t qrow0 = (int64_t)qb * BB + 32 * qh;  // this wave's first query row
-    const char* q_rm = buf;
-    const char* q_tr = buf + kTile;
-    const char* do_rm = buf + 2 * kTile;
-    const char* do_tr = buf + 3 * kTile;
-    const float* lse2 = reinterpret_cast<const float*>(buf + 4 * kTile);
-    const float* dlt = lse2 + BB;
-    // S and dP tiles [qt][kt]: rows q = 32 qh + 16 qt + 4 (lane/16) + e, column key 16 kt + lane%16
-    f32x4_t sp[2][2], dp[2][2];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) sp[qt][kt] = dp[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const int row = 32 * qh + 16 * qt + fr;
-        const uint4 qa = frag_rm(q_rm, row, ds, fq);
-        const uint4 da = frag_rm(do_rm, row, ds, fq);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          sp[qt][kt] = mfma<DT>(qa, kf[kt][ds], sp[qt][kt]);
-          dp[qt][kt] = mfma<DT>(da, vf[kt][ds], dp[qt][kt]);
-        }
-      }
-    }
-    // P = exp2(S log2e scale - lse2), dS = P (dP - delta); causal / length mask -> 0
-    const bool diag = qb == kb;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 32 * qh + 16 * qt + 4 * fq + e;
-        const int64_t q = (int64_t)qb * BB + r;
-        const float l2 = lse2[r], dl = dlt[r];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int64_t key = key0 + 16 * kt + fr;
-          float p = exp2f(sp[qt][kt][e] * sl2 - l2);
-          if ((diag && key > q) || q >= S) p = 0.f;
-          sp[qt][kt][e] = p;
-          dp[qt][kt][e] = p * (dp[qt][kt][e] - dl);
-        }
-      }
-    // dV^T += dO^T P ; dK^T += Q^T dS   (contraction over this wave's 32 query rows)
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const uint4 pb = pack_pair<DT>(sp[0][kt], sp[1][kt]);
-      const uint4 sb = pack_pair<DT>(dp[0][kt], dp[1][kt]);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = 16 * dt + fr;
-        dvt[kt][dt] = mfma<DT>(frag_tr(do_tr, d, qh, fq), pb, dvt[kt][dt]);
-        dkt[kt][dt] = mfma<DT>(frag_tr(q_tr, d, qh, fq), sb, dkt[kt][dt]);
-      }
-    }
-    if (it + 1 < n_iter) store_stage(smem + ((it + 1) & 1) * kBuf);
-    __syncthreads();
-  }
-
-  // sum the two query halves (wave pairs with the same kh) through LDS, then store
-  float* red = reinterpret_cast<float*>(smem);  // [kh][kt][dt][lane] f32x4 of dV then dK
-  auto slot = [&](int which, int kt, int dt) -> f32x4_t* {
-    return reinterpret_cast<f32x4_t*>(red) + ((((kh * 2 + which) * 2 + kt) * 8 + dt) * 64 + lane);
-  };
-  if (qh == 1) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        *slot(0, kt, dt) = dvt[kt][dt];
-        *slot(1, kt, dt) = dkt[kt][dt];
-      }
-  }
-  __syncthreads();
-  if (qh == 0) {
-    uint16_t* dkb = dK + b * sh.dk_b + hk * sh.dk_h;
-    uint16_t* dvb = dV + b * sh.dk_b + hk * sh.dk_h;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int64_t key = key0 + 16 * kt + fr;
-      if (key >= S) continue;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const f32x4_t v = dvt[kt][dt] + *slot(0, kt, dt);
-        const f32x4_t k4 = (dkt[kt][dt] + *slot(1, kt, dt)) * sh.scale;
-        const int d = 16 * dt + 4 * fq;
-        *reinterpret_cast<uint2*>(dvb + key * sh.dk_s + d) =
-            make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
-        *reinterpret_cast<uint2*>(dkb + key * sh.dk_s + d) =
-            make_uint2(pack2<DT>(k4[0], k4[1]), pack2<DT>(k4[2], k4[3]));
-      }
+    for (int dt = 0; dt < 8; ++dt) {
+      st.dv[dt] = mfma<DT>(frag_tr(do_l, 32 * ks, 16 * dt, fq, fr), pb, st.dv[dt]);
+      st.dk[dt] = mfma<DT>(frag_tr(q_l, 32 * ks, 16 * dt, fq, fr), sb, st.dk[dt]);
     }
   }
 }
 
-// ---- dQ: one workgroup per (b, hq, 128-row query block); wave w owns rows 32 w .. +31.
 template <int DT>
-__global__ __launch_bounds__(256) void attn_bwd_dq(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
-    uint16_t* __restrict__ dQ, BwdShape sh, int n_qblocks) {
-  // per buffer: K [64][128], K^T [128][64], V [64][128]
-  constexpr int kTile = BB * kKRow;
-  constexpr int kBuf = 3 * kTile;
-  __shared__ __attribute__((aligned(16))) char smem[2 * kBuf];
-  const int qb = n_qblocks - 1 - (int)(blockIdx.x % n_qblocks);  // heaviest first
-  const int64_t bh = blockIdx.x / n_qblocks;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                   const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
+                   const float* __restrict__ lse, const float* __restrict__ delta,
+                   uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+                   float* __restrict__ pk, float* __restrict__ pv, BwdShape sh, int n_kblocks) {
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kBwdStage];
+  const int64_t BH = sh.B * sh.HQ;
+  const int kb = (int)(blockIdx.x / BH);  // heaviest (first) key blocks first
+  const int64_t bh = blockIdx.x % BH;
   const int64_t b = bh / sh.HQ, hq = bh % sh.HQ;
   const int64_t hk = hq / (sh.HQ / sh.HK);
   const int64_t S = sh.S;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int fr = lane & 15, fq = lane >> 4;
+  const int64_t key0w = (int64_t)kb * kRows + 16 * wave;  // this wave's first key
+  const float sl2 = sh.scale * kLog2e;
+
+  DkdvState<DT> st;
+  const uint16_t* kbase = K + b * sh.ks_b + hk * sh.ks_h;
+  const uint16_t* vbase = V + b * sh.vs_b + hk * sh.vs_h;
+  {
+    const int64_t key = key0w + fr;
+    const int64_t kc = key < S ? key : S - 1;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      st.kf[ds] = *reinterpret_cast<const uint4*>(kbase + kc * sh.ks_s + 32 * ds + 8 * fq);
+      st.vf[ds] = *reinterpret_cast<const uint4*>(vbase + kc * sh.vs_s + 32 * ds + 8 * fq);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) st.dv[dt] = st.dk[dt] = zero4();
+  }
+
+  const uint16_t* qbase = Q + b * sh.qs_b + hq * sh.qs_h;
+  const uint16_t* obase = dO + b * sh.os_b + hq * sh.os_h;
+  const float* lse_row = lse + bh * S;
+  const float* dl_row = delta + bh * S;
+  const int n_qb = n_kblocks;  // 64-row query blocks
+  TileDma qdma, odma;
+  qdma.init(sh.qs_s, wave, lane);
+  odma.init(sh.os_s, wave, lane);
+  // lse * log2e and Delta of a query block: thread t < 128 stages row t & 63 of one of them
+  const int t = threadIdx.x;
+  auto row_stat = [&](int qb) -> float {
+    const int64_t q = (int64_t)qb * kRows + (t & 63);
+    const int64_t qc = q < S ? q : S - 1;
+    return t < 64 ? lse_row[qc] * kLog2e : dl_row[qc];
+  };
+  qdma.issue(qbase, sh.qs_s, (int64_t)kb * kRows, S, smem);
+  odma.issue(obase, sh.os_s, (int64_t)kb * kRows, S, smem + kTileBytes);
+  if (t < 128) reinterpret_cast<float*>(smem + 2 * kTileBytes)[t] = row_stat(kb);
+  for (int qb = kb; qb < n_qb; ++qb) {
+    wait_all_barrier();
+    const int it = qb - kb;
+    char* cur = smem + (it & 1) * kBwdStage;
+    char* nxt = smem + ((it + 1) & 1) * kBwdStage;
+    const bool more = qb + 1 < n_qb;
+    float stat = 0.f;
+    if (more && t < 128) stat = row_stat(qb + 1);
+    const int64_t qrow0 = (int64_t)qb * kRows;
+    const bool need_mask = qb == kb || qrow0 + kRows > S;
+    const int kq_rel = clamp_rel(key0w + fr - (qrow0 + 4 * fq));
+    const int qlim = clamp_rel(S - (qrow0 + 4 * fq));
+    dkdv_block<DT>(st, cur, nxt, more, qdma, odma, qbase, obase, sh.qs_s, sh.os_s, qrow0, S,
+                   need_mask, kq_rel, qlim, sl2, lane);
+    if (more && t < 128) reinterpret_cast<float*>(nxt + 2 * kTileBytes)[t] = stat;
+  }
+
+  const int64_t key = key0w + fr;
+  if (key >= S) return;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const f32x4_t v = st.dv[dt];
+    const f32x4_t k4 = st.dk[dt] * sh.scale;
+    const int d = 16 * dt + 4 * fq;
+    if (pk) {
+      const int64_t row = (bh * S + key) * HD + d;
+      *reinterpret_cast<f32x4_t*>(pv + row) = v;
+      *reinterpret_cast<f32x4_t*>(pk + row) = k4;
+    } else {
+      uint16_t* dvp = dV + b * sh.dk_b + hk * sh.dk_h + key * sh.dk_s + d;
+      uint16_t* dkp = dK + b * sh.dk_b + hk * sh.dk_h + key * sh.dk_s + d;
+      *reinterpret_cast<uint2*>(dvp) = make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
+      *reinterpret_cast<uint2*>(dkp) = make_uint2(pack2<DT>(k4[0], k4[1]), pack2<DT>(k4[2], k4[3]));
+    }
+  }
+}
+
+// dK[b, s, hk] = sum_g pk[b, hk G + g, s], dV likewise, in head order (one thread per 8 d).
+template <int DT>
+__global__ __launch_bounds__(256) void attn_bwd_reduce(const float* __restrict__ pk,
+                                                        const float* __restrict__ pv,
+                                                        uint16_t* __restrict__ dK,
+                                                        uint16_t* __restrict__ dV, BwdShape sh) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = sh.B * sh.HK * sh.S * (HD / 8);
+  if (idx >= total) return;
+  const int part = (int)(idx & 15);
+  const int64_t r = idx >> 4;  // (b, hk, s)
+  const int64_t s = r % sh.S, bhk = r / sh.S;
+  const int64_t b = bhk / sh.HK, hk = bhk % sh.HK;
+  const int64_t G = sh.HQ / sh.HK;
+  float ak[8] = {}, av[8] = {};
+  for (int64_t g = 0; g < G; ++g) {
+    const int64_t off = ((b * sh.HQ + hk * G + g) * sh.S + s) * HD + 8 * part;
+    const float4 k0 = *reinterpret_cast<const float4*>(pk + off);
+    const float4 k1 = *reinterpret_cast<const float4*>(pk + off + 4);
+    const float4 v0 = *reinterpret_cast<const float4*>(pv + off);
+    const float4 v1 = *reinterpret_cast<const float4*>(pv + off + 4);
+    ak[0] += k0.x; ak[1] += k0.y; ak[2] += k0.z; ak[3] += k0.w;
+    ak[4] += k1.x; ak[5] += k1.y; ak[6] += k1.z; ak[7] += k1.w;
+    av[0] += v0.x; av[1] += v0.y; av[2] += v0.z; av[3] += v0.w;
+    av[4] += v1.x; av[5] += v1.y; av[6] += v1.z; av[7] += v1.w;
+  }
+  const int64_t o = b * sh.dk_b + hk * sh.dk_h + s * sh.dk_s + 8 * part;
+  Vec8<DT>::store(dK + o, ak);
+  Vec8<DT>::store(dV + o, av);
+}
+
+// ---- dQ: one workgroup per (b, hq, 128-row query block), heaviest first; wave w owns rows
+// 32 w .. +31. Per 64-key block, in two 32-key halves:
+//   S^T = K Q^T, dP^T = V dO^T    K, V row fragments from LDS; Q, dO fragments in registers
+//   dS^T = P^T (dP^T - Delta)
+//   dQ^T += K^T dS^T               K^T by transposing reads; dS^T from registers
+template <int DT>
+struct DqState {
+  uint4 qf[2][4], df[2][4];  // B operands: column q = 16 qt + lane % 16, d = 32 ds + 8 (lane/16)
+  f32x4_t dq[2][8];          // [qt][dt]: rows d = 16 dt + 4 (lane / 16) + e, column q
+  float l2[2], dl[2];        // lse * log2e and Delta of the lane's query columns
+};
+
+template <int DT>
+QL_DEV void dq_block(DqState<DT>& st, const char* __restrict__ kl, const char* __restrict__ vl,
+                     char* __restrict__ kn, char* __restrict__ vn, bool issue, const TileDma& kdma,
+                     const TileDma& vdma, const uint16_t* __restrict__ kbase,
+                     const uint16_t* __restrict__ vbase, int64_t ks_s, int64_t vs_s, int64_t key0,
+                     int64_t q0, int64_t S, float sl2, int lane) {
+  const int fr = lane & 15, fq = lane >> 4;
+  if (issue) {
+    kdma.issue(kbase, ks_s, key0 + kRows, S, kn);
+    vdma.issue(vbase, vs_s, key0 + kRows, S, vn);
+  }
+  if (key0 > q0 + 31) return;
+  const bool need_mask = key0 + kRows - 1 > q0 || key0 + kRows > S;
+  // key - q = kq_rel + 32 h + 16 kk + e - 16 qt; keys at or past the end: 32 h + 16 kk + e >= klim
+  const int kq_rel = clamp_rel(key0 + 4 * fq - (q0 + fr));
+  const int klim = clamp_rel(S - key0 - 4 * fq);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    f32x4_t sp[2][2], dp[2][2];  // [qt][kk]: rows key 32 h + 16 kk + 4 (lane/16) + e, column q
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) sp[qt][kk] = dp[qt][kk] = zero4();
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int row = 32 * h + 16 * kk + fr;
+        const uint4 ka = frag_row(kl, row, ds, fq);
+        const uint4 va = frag_row(vl, row, ds, fq);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          sp[qt][kk] = mfma<DT>(ka, st.qf[qt][ds], sp[qt][kk]);
+          dp[qt][kk] = mfma<DT>(va, st.df[qt][ds], dp[qt][kk]);
+        }
+      }
+    uint4 sb[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][kk][e], sl2, -st.l2[qt]));
+          const int rel = 32 * h + 16 * kk + e;
+          if (need_mask) p = (kq_rel + rel - 16 * qt > 0 || rel >= klim) ? 0.f : p;
+          dp[qt][kk][e] = p * (dp[qt][kk][e] - st.dl[qt]);
+        }
+      sb[qt] = pack_pair<DT>(dp[qt][0], dp[qt][1]);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint4 ka = frag_tr(kl, 32 * h, 16 * dt, fq, fr);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) st.dq[qt][dt] = mfma<DT>(ka, sb[qt], st.dq[qt][dt]);
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_bwd_dq(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                 const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
+                 const float* __restrict__ lse, const float* __restrict__ delta,
+                 uint16_t* __restrict__ dQ, BwdShape sh, int n_qblocks) {
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // [stage][K, V]
+  const int64_t BH = sh.B * sh.HQ;
+  const int qb = n_qblocks - 1 - (int)(blockIdx.x / BH);  // heaviest blocks first
+  const int64_t bh = blockIdx.x % BH;
+  const int64_t b = bh / sh.HQ, hq = bh % sh.HQ;
+  const int64_t hk = hq / (sh.HQ / sh.HK);
+  const int64_t S = sh.S;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int fr = lane & 15, fq = lane >> 4;
   const int64_t q0 = (int64_t)qb * BQ + 32 * wave;
   const float sl2 = sh.scale * kLog2e;
 
-  // Q and dO fragments (B operands: column q = lane%16, k = d); lse2 and delta per column
-  uint4 qf[2][4], df[2][4];
-  float l2[2], dl[2];
+  DqState<DT> st;
   const uint16_t* qbase = Q + b * sh.qs_b + hq * sh.qs_h;
   const uint16_t* dobase = dO + b * sh.os_b + hq * sh.os_h;
 #pragma unroll
@@ -597,105 +668,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(
     const int64_t qc = q < S ? q : S - 1;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
-      qf[qt][ds] = *reinterpret_cast<const uint4*>(qbase + qc * sh.qs_s + 32 * ds + 8 * fq);
-      df[qt][ds] = *reinterpret_cast<const uint4*>(dobase + qc * sh.os_s + 32 * ds + 8 * fq);
+      st.qf[qt][ds] = *reinterpret_cast<const uint4*>(qbase + qc * sh.qs_s + 32 * ds + 8 * fq);
+      st.df[qt][ds] = *reinterpret_cast<const uint4*>(dobase + qc * sh.os_s + 32 * ds + 8 * fq);
     }
-    l2[qt] = lse[bh * S + qc] * kLog2e;
-    dl[qt] = delta[bh * S + qc];
+    st.l2[qt] = lse[bh * S + qc] * kLog2e;
+    st.dl[qt] = delta[bh * S + qc];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) st.dq[qt][dt] = zero4();
   }
-  f32x4_t dqt[2][8];  // [qt][dt]: rows d = 16 dt + 4 (lane/16) + e, column q
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) dqt[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
   const int64_t q_end = (int64_t)(qb + 1) * BQ;
   const int64_t kv_end = q_end < S ? q_end : S;
-  const int nkv = (int)((kv_end + BB - 1) / BB);
-  // staging: threads 0..127 an 8 x 8 block of K (row-major + transposed), 128..255 of V
-  const int t = threadIdx.x;
-  const int u = t & 127;
-  const int srow0 = 8 * (u >> 4), sd0 = 8 * (u & 15);
-  const uint16_t* sbase = t < 128 ? K + b * sh.ks_b + hk * sh.ks_h : V + b * sh.vs_b + hk * sh.vs_h;
-  const int64_t srs = t < 128 ? sh.ks_s : sh.vs_s;
-  uint4 st[8];
-  auto load_stage = [&](int j) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t key = (int64_t)j * BB + srow0 + i;
-      const int64_t kc = key < S ? key : S - 1;
-      st[i] = *reinterpret_cast<const uint4*>(sbase + kc * srs + sd0);
-    }
-  };
-  auto store_stage = [&](char* buf) {
-    if (t < 128) {
-      put_rowmajor(buf, st, srow0, sd0);
-      put_transposed(buf + kTile, st, srow0, sd0);
-    } else {
-      put_rowmajor(buf + 2 * kTile, st, srow0, sd0);
-    }
-  };
-  load_stage(0);
-  store_stage(smem);
-  __syncthreads();
+  const int nkv = (int)((kv_end + kRows - 1) / kRows);
+  const uint16_t* kbase = K + b * sh.ks_b + hk * sh.ks_h;
+  const uint16_t* vbase = V + b * sh.vs_b + hk * sh.vs_h;
+  TileDma kdma, vdma;
+  kdma.init(sh.ks_s, wave, lane);
+  vdma.init(sh.vs_s, wave, lane);
+  kdma.issue(kbase, sh.ks_s, 0, S, smem);
+  vdma.issue(vbase, sh.vs_s, 0, S, smem + kTileBytes);
   for (int j = 0; j < nkv; ++j) {
-    char* buf = smem + (j & 1) * kBuf;
-    if (j + 1 < nkv) load_stage(j + 1);
-    const char* k_rm = buf;
-    const char* k_tr = buf + kTile;
-    const char* v_rm = buf + 2 * kTile;
-    const int64_t key0 = (int64_t)j * BB;
-    // S^T and dP^T tiles [qt][kt]: rows key 16 kt + 4 (lane/16) + e, column q
-    f32x4_t sp[2][4], dp[2][4];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) sp[qt][kt] = dp[qt][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const int row = 16 * kt + fr;
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const uint4 ka = frag_rm(k_rm, row, ds, fq);
-        const uint4 va = frag_rm(v_rm, row, ds, fq);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          sp[qt][kt] = mfma<DT>(ka, qf[qt][ds], sp[qt][kt]);
-          dp[qt][kt] = mfma<DT>(va, df[qt][ds], dp[qt][kt]);
-        }
-      }
-    }
-    const bool need_mask = key0 + BB > q0 || key0 + BB > S;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const int64_t q = q0 + 16 * qt + fr;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float p = exp2f(sp[qt][kt][e] * sl2 - l2[qt]);
-          if (need_mask) {
-            const int64_t key = key0 + 16 * kt + 4 * fq + e;
-            if (key > q || key >= S) p = 0.f;
-          }
-          dp[qt][kt][e] = p * (dp[qt][kt][e] - dl[qt]);
-        }
-    }
-    // dQ^T += K^T dS^T (contraction over the 64 keys in two permuted 32-steps)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint4 sb[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) sb[qt] = pack_pair<DT>(dp[qt][2 * ks], dp[qt][2 * ks + 1]);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint4 ka = frag_tr(k_tr, 16 * dt + fr, ks, fq);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) dqt[qt][dt] = mfma<DT>(ka, sb[qt], dqt[qt][dt]);
-      }
-    }
-    if (j + 1 < nkv) store_stage(smem + ((j + 1) & 1) * kBuf);
-    __syncthreads();
+    wait_all_barrier();
+    char* cur = smem + (j & 1) * 2 * kTileBytes;
+    char* nxt = smem + ((j + 1) & 1) * 2 * kTileBytes;
+    dq_block<DT>(st, cur, cur + kTileBytes, nxt, nxt + kTileBytes, j + 1 < nkv, kdma, vdma,
+                 kbase, vbase, sh.ks_s, sh.vs_s, (int64_t)j * kRows, q0, S, sl2, lane);
   }
   uint16_t* dqb = dQ + b * sh.dq_b + hq * sh.dq_h;
 #pragma unroll
@@ -704,12 +700,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(
     if (q >= S) continue;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const f32x4_t v = dqt[qt][dt] * sh.scale;
+      const f32x4_t v = st.dq[qt][dt] * sh.scale;
       *reinterpret_cast<uint2*>(dqb + q * sh.dq_s + 16 * dt + 4 * fq) =
           make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
     }
   }
 }
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -751,9 +749,11 @@ extern "C" int qlora_attn_fwd(const void* q, const void* k, const void* v, void*
   return ql_launch_status();
 }
 
-extern "C" int64_t qlora_attn_bwd_workspace_size(int64_t B, int64_t HQ, int64_t S) {
-  if (B <= 0 || HQ <= 0 || S <= 0) return 0;
-  return B * HQ * S * (int64_t)sizeof(float);
+extern "C" int64_t qlora_attn_bwd_workspace_size(int64_t B, int64_t HQ, int64_t HK, int64_t S) {
+  if (B <= 0 || HQ <= 0 || HK <= 0 || S <= 0 || HQ % HK) return 0;
+  int64_t bytes = align256(B * HQ * S * (int64_t)sizeof(float));   // Delta
+  if (HQ != HK) bytes += 2 * align256(B * HQ * S * HD * (int64_t)sizeof(float));  // partials
+  return bytes;
 }
 
 extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const void* o,
@@ -770,7 +770,7 @@ extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv || !q_strides || !k_strides ||
       !v_strides || !o_strides || !dq_strides || !dkv_strides)
     return QL_EINVAL;
-  if (workspace_bytes < qlora_attn_bwd_workspace_size(B, HQ, S) || !workspace ||
+  if (workspace_bytes < qlora_attn_bwd_workspace_size(B, HQ, HK, S) || !workspace ||
       !ql_aligned(workspace, 16))
     return QL_EINVAL;
   BwdShape sh;
@@ -790,21 +790,34 @@ extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const
   for (const void* p : ptrs)
     if (!ql_aligned(p, 16)) return QL_EALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* delta = static_cast<float*>(workspace);
+  char* ws = static_cast<char*>(workspace);
+  float* delta = reinterpret_cast<float*>(ws);
+  float* pk = nullptr;
+  float* pv = nullptr;
+  if (HQ != HK) {
+    const int64_t part_bytes = align256(B * HQ * S * HD * (int64_t)sizeof(float));
+    pk = reinterpret_cast<float*>(ws + align256(B * HQ * S * (int64_t)sizeof(float)));
+    pv = reinterpret_cast<float*>(reinterpret_cast<char*>(pk) + part_bytes);
+  }
   const int64_t rows = B * HQ * S;
-  const int n_kblocks = (int)((S + BB - 1) / BB);
+  const int n_kblocks = (int)((S + kRows - 1) / kRows);
   const int n_qblocks = (int)((S + BQ - 1) / BQ);
-  if (B * HK * n_kblocks > INT32_MAX || B * HQ * n_qblocks > INT32_MAX) return QL_EINVAL;
+  if (B * HQ * n_kblocks > INT32_MAX || (rows * 16 + 255) / 256 > INT32_MAX ||
+      (B * HK * S * 16 + 255) / 256 > INT32_MAX)
+    return QL_EINVAL;
 #define QL_ATTN_BWD(DTC)                                                                          \
   do {                                                                                            \
     hipLaunchKernelGGL((attn_bwd_delta<DTC>), dim3((unsigned)((rows * 16 + 255) / 256)), dim3(256), \
                        0, s, (const uint16_t*)o, (const uint16_t*)d_o, delta, sh);                \
-    hipLaunchKernelGGL((attn_bwd_dkdv<DTC>), dim3((unsigned)(B * HK * n_kblocks)), dim3(256), 0, s, \
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,                \
-                       (const uint16_t*)d_o, lse, delta, (uint16_t*)dk, (uint16_t*)dv, sh,        \
-                       n_kblocks);                                                                \
-    hipLaunchKernelGGL((attn_bwd_dq<DTC>), dim3((unsigned)(B * HQ * n_qblocks)), dim3(256), 0, s,  \
-                       (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,                \
+    hipLaunchKernelGGL((attn_bwd_dkdv<DTC>), dim3((unsigned)(B * HQ * n_kblocks)), dim3(kThreads), \
+                       0, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,          \
+                       (const uint16_t*)d_o, lse, delta, (uint16_t*)dk, (uint16_t*)dv, pk, pv,    \
+                       sh, n_kblocks);                                                            \
+    if (pk)                                                                                       \
+      hipLaunchKernelGGL((attn_bwd_reduce<DTC>), dim3((unsigned)((B * HK * S * 16 + 255) / 256)), \
+                         dim3(256), 0, s, pk, pv, (uint16_t*)dk, (uint16_t*)dv, sh);              \
+    hipLaunchKernelGGL((attn_bwd_dq<DTC>), dim3((unsigned)(B * HQ * n_qblocks)), dim3(kThreads),  \
+                       0, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,          \
                        (const uint16_t*)d_o, lse, delta, (uint16_t*)dq, sh, n_qblocks);           \
   } while (0)
   if (dtype == QL_BF16) QL_ATTN_BWD(QL_BF16);

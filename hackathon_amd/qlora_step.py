@@ -99,6 +99,11 @@ def _unpatch_transformers():
         orig = getattr(fn, "_original", None)
         if orig is not None:
             setattr(owner, name, orig)
+    from transformers.modeling_utils import AttentionInterface
+
+    orig = getattr(AttentionInterface._global_mapping["sdpa"], "_original", None)
+    if orig is not None:
+        AttentionInterface._global_mapping["sdpa"] = orig
     import hackathon_amd
 
     hackathon_amd._applied.clear()

@@ -314,11 +314,12 @@ int qlora_attn_fwd(const void* q, const void* k, const void* v, void* o, float* 
  *   dv = P^T d_o (summed likewise), with P = exp(scale q k^T - lse) causal and
  *   dS = P * (d_o v^T - rowsum(d_o * o)).
  * d_o uses o's strides; dk and dv share dkv_strides. dq, dk and dv are written, not added to.
- * The workspace (qlora_attn_bwd_workspace_size bytes, 16-B aligned) holds rowsum(d_o * o).
- * Deterministic: every output element is reduced by one workgroup in a fixed order.
+ * The workspace (qlora_attn_bwd_workspace_size bytes, 16-B aligned) holds rowsum(d_o * o) and,
+ * when HQ > HK, the per-query-head fp32 dk and dv that are summed over each kv head's group.
+ * Deterministic: every output element is reduced in a fixed order.
  * Replaces: the autograd backward of the SDPA call that qlora_attn_fwd replaces.
  */
-int64_t qlora_attn_bwd_workspace_size(int64_t B, int64_t HQ, int64_t S);
+int64_t qlora_attn_bwd_workspace_size(int64_t B, int64_t HQ, int64_t HK, int64_t S);
 int qlora_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* d_o,
                    const float* lse, void* dq, void* dk, void* dv, int dtype, int64_t B,
                    int64_t HQ, int64_t HK, int64_t S, int64_t D, const int64_t* q_strides,
