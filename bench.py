@@ -292,6 +292,51 @@ def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=20
 
 
 # ---------------------------------------------------------------------------------------------
+def _trace_category(name):
+    """Step-breakdown category of a kernel name from a rocprofv3 kernel trace."""
+    table = (("attn_fwd_kernel", "attention fwd (flash)"), ("attn_bwd_dkdv", "attention dK/dV"),
+             ("attn_bwd_dq", "attention dQ"), ("attn_bwd_delta", "attention Delta"),
+             ("attn_bwd_reduce", "attention dK/dV head sum"),
+             ("gemm_nt_kernel", "NT GEMM (incl. the LoRA K segment)"),
+             ("splitk_reduce", "GEMM split-K reduce"), ("gemm_mfma_kernel", "GEMM (general)"),
+             ("lora_down", "lora_down (+reduce)"), ("lora_wgrad", "lora_wgrad (+reduce)"),
+             ("lora_pack", "lora_pack"), ("nf4_dequant_t", "NF4 dequant (transposed)"),
+             ("nf4_dequant", "NF4 dequant"), ("swiglu", "SwiGLU"), ("rmsnorm", "RMSNorm"),
+             ("rope", "RoPE"), ("ce_rows", "CE rows"), ("transpose16", "transpose"),
+             ("Cijk", "hipBLASLt"), ("multi_tensor_apply", "torch AdamW (foreach)"),
+             ("CUDAFunctor_add", "torch add"))
+    for key, cat in table:
+        if key in name:
+            return cat
+    return "torch other"
+
+
+def trace_summary(path):
+    """Per-step kernel time of the patched QLoRA step from a rocprofv3 --kernel-trace CSV.
+    Steps are delimited by the embedding gather (one vectorized_gather_kernel per step); the
+    table is for the last complete step."""
+    import collections
+    import csv
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(rows) if "vectorized_gather_kernel" in r["Kernel_Name"]]
+    if len(marks) < 2:
+        raise SystemExit("trace holds fewer than two steps")
+    a, b = marks[-2], marks[-1]
+    agg, cnt = collections.Counter(), collections.Counter()
+    for r in rows[a:b]:
+        c = _trace_category(r["Kernel_Name"])
+        agg[c] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
+        cnt[c] += 1
+    span = (int(rows[b]["Start_Timestamp"]) - int(rows[a]["Start_Timestamp"])) / 1e6
+    total = sum(agg.values())
+    print(f"steps in trace: {len(marks)}; last complete step: wall {span:.1f} ms, "
+          f"kernel time {total:.1f} ms")
+    print("| category | launches | ms per step | % of kernel time |\n|---|---|---|---|")
+    for k, v in agg.most_common():
+        print(f"| {k} | {cnt[k]} | {v:.2f} | {100 * v / total:.1f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -309,7 +354,12 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run a 256 MiB device copy (counter calibration) and eight eager dequant "
                          "launches, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="print the per-step kernel table of a rocprofv3 kernel trace and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
               f"multi-GPU path; see DESIGN.md for how it would shard", file=sys.stderr)
