@@ -304,6 +304,7 @@ def _trace_category(name):
              ("nf4_dequant", "NF4 dequant"), ("swiglu", "SwiGLU"), ("rmsnorm", "RMSNorm"),
              ("rope", "RoPE"), ("ce_rows", "CE rows"), ("transpose16", "transpose"),
              ("Cijk", "hipBLASLt"), ("multi_tensor_apply", "torch AdamW (foreach)"),
+             ("adamw_multi_fp32", "AdamW (fused)"),
              ("CUDAFunctor_add", "torch add"))
     for key, cat in table:
         if key in name:

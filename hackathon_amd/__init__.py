@@ -15,16 +15,19 @@ include/qlora_gfx950.h, bound through ctypes in `_lib`).
   quant.py          NF4 storage format: codebook, QuantState, quantizer, Linear4bit
   gemm.py           the MFMA GEMM behind every contraction of the path
   attention.py      causal flash attention behind transformers' "sdpa" entry (fwd + bwd)
+  residual.py       Qwen2DecoderLayer with the residual adds fused into its two RMSNorms
+  optim.py          FusedAdamW: AdamW over the adapters in one launch
 """
 
-PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora", "attention")
+PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora", "attention", "residual")
 
 _applied = set()
 
 
 def apply(include_example=True):
-    """Install every patch (idempotent), as solution/__init__.py:22-34 does; "attention" has no
-    counterpart in the reference, which leaves attention to torch's SDPA."""
+    """Install every patch (idempotent), as solution/__init__.py:22-34 does; "attention" and
+    "residual" have no counterpart in the reference, which leaves attention to torch's SDPA and
+    the decoder layer's residual adds to transformers."""
     from importlib import import_module
 
     for name in PATCHES:

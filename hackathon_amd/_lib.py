@@ -62,6 +62,13 @@ _SIGNATURES = {
                         _c_ptr, _c_int, _c_ptr],
     "qlora_nf4_quantize": [_c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
                            _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr],
+    "qlora_add_rmsnorm_fwd": [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr,
+                              _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_i64, _c_i64, _c_f32,
+                              _c_ptr],
+    "qlora_rmsnorm_bwd_residual": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,
+                                   _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr],
+    "qlora_adamw_fp32": [_c_ptr, _c_int, _c_i64, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32, _c_f32,
+                         _c_f32, _c_ptr],
     "qlora_attn_fwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64,
                        _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_f32, _c_ptr],
     "qlora_attn_bwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
@@ -79,6 +86,7 @@ _SIZE_QUERIES = {
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64],
     "qlora_nf4_quantize_workspace_size": [_c_i64, _c_int, _c_int],
     "qlora_attn_bwd_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64],
+    "qlora_adamw_chunk_elems": [],
 }
 
 _lib = None

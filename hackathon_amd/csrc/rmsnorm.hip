@@ -18,11 +18,14 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRowsPerBlock = kThreads / 64;
 
-template <int XT, int WT, int YT, int VPL>
+// ADD: the row is h = round_{x dtype}(x + d) (the residual add of a decoder layer), written
+// to `h` and normalised; otherwise the row is x and `d`, `h` are unused.
+template <int XT, int WT, int YT, int VPL, bool ADD>
 __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_wave(
-    const typename Elem<XT>::T* __restrict__ x, int64_t xs, const typename Elem<WT>::T* __restrict__ w,
-    typename Elem<YT>::T* __restrict__ y, int64_t ys, float* __restrict__ rstd, int64_t n_rows,
-    int n_cols, float eps) {
+    const typename Elem<XT>::T* __restrict__ x, int64_t xs, const typename Elem<XT>::T* __restrict__ d,
+    int64_t ds, typename Elem<XT>::T* __restrict__ h, int64_t hs,
+    const typename Elem<WT>::T* __restrict__ w, typename Elem<YT>::T* __restrict__ y, int64_t ys,
+    float* __restrict__ rstd, int64_t n_rows, int n_cols, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= n_rows) return;
@@ -35,6 +38,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_wave(
     const int c = i * 64 + lane;
     if (c < nvec) {
       Vec8<XT>::load(xr + 8 * c, v[i]);
+      if constexpr (ADD) {
+        float dv[8];
+        Vec8<XT>::load(d + row * ds + 8 * c, dv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[i][j] = round_through<XT>(v[i][j] + dv[j]);
+        Vec8<XT>::store(h + row * hs + 8 * c, v[i]);
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += v[i][j] * v[i][j];
     }
@@ -56,10 +66,13 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_wave(
   }
 }
 
-template <int GT, int XT, int WT, int DXT, int VPL>
+// RES: dx also receives the gradient `dres` of the row's other use (the residual stream),
+// added in fp32 before the one rounding to dx's dtype.
+template <int GT, int XT, int WT, int DXT, int VPL, bool RES>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_wave(
     const typename Elem<GT>::T* __restrict__ dy, int64_t dys, const typename Elem<XT>::T* __restrict__ x,
     int64_t xs, const typename Elem<WT>::T* __restrict__ w, const float* __restrict__ rstd,
+    const typename Elem<DXT>::T* __restrict__ dres, int64_t drs,
     typename Elem<DXT>::T* __restrict__ dx, int64_t dxs, int64_t n_rows, int n_cols) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
@@ -92,6 +105,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_wave(
       float o[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = r * (g[i][j] - xv[i][j] * k);
+      if constexpr (RES) {
+        float rv[8];
+        Vec8<DXT>::load(dres + row * drs + 8 * c, rv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] += rv[j];
+      }
       Vec8<DXT>::store(dx + row * dxs + 8 * c, o);
     }
   }
@@ -151,18 +170,20 @@ bool row_vec_ok(const void* p, int64_t stride, int dt) {
   return ql_aligned(p, 16) && ((stride * ql_elem_size(dt)) % 16) == 0;
 }
 
-template <int XT, int WT>
+template <int XT, int WT, bool ADD = false>
 int fwd_fast(const void* x, int64_t xs, const void* w, void* y, int64_t ys, float* rstd,
-             int64_t n_rows, int n_cols, float eps, hipStream_t s) {
+             int64_t n_rows, int n_cols, float eps, hipStream_t s, const void* d = nullptr,
+             int64_t ds = 0, void* h = nullptr, int64_t hs = 0) {
   constexpr int YT = (XT == WT) ? XT : QL_F32;
   using X = typename Elem<XT>::T;
   using W = typename Elem<WT>::T;
   using Y = typename Elem<YT>::T;
   const dim3 grid((unsigned)((n_rows + kRowsPerBlock - 1) / kRowsPerBlock));
   const int nvec = n_cols / 8;
-#define QL_RMS_FWD(VPL)                                                                   \
-  hipLaunchKernelGGL((rmsnorm_fwd_wave<XT, WT, YT, VPL>), grid, dim3(kThreads), 0, s,     \
-                     (const X*)x, xs, (const W*)w, (Y*)y, ys, rstd, n_rows, n_cols, eps)
+#define QL_RMS_FWD(VPL)                                                                       \
+  hipLaunchKernelGGL((rmsnorm_fwd_wave<XT, WT, YT, VPL, ADD>), grid, dim3(kThreads), 0, s,    \
+                     (const X*)x, xs, (const X*)d, ds, (X*)h, hs, (const W*)w, (Y*)y, ys, rstd, \
+                     n_rows, n_cols, eps)
   if (nvec <= 4 * 64) QL_RMS_FWD(4);
   else if (nvec <= 8 * 64) QL_RMS_FWD(8);
   else QL_RMS_FWD(16);
@@ -170,19 +191,20 @@ int fwd_fast(const void* x, int64_t xs, const void* w, void* y, int64_t ys, floa
   return ql_launch_status();
 }
 
-template <int XT, int WT>
+template <int XT, int WT, bool RES = false>
 int bwd_fast(const void* dy, int64_t dys, const void* x, int64_t xs, const void* w,
-             const float* rstd, void* dx, int64_t dxs, int64_t n_rows, int n_cols, hipStream_t s) {
+             const float* rstd, void* dx, int64_t dxs, int64_t n_rows, int n_cols, hipStream_t s,
+             const void* dres = nullptr, int64_t drs = 0) {
   constexpr int GT = (XT == WT) ? XT : QL_F32;  // dy has the forward output's dtype
   using G = typename Elem<GT>::T;
   using X = typename Elem<XT>::T;
   using W = typename Elem<WT>::T;
   const dim3 grid((unsigned)((n_rows + kRowsPerBlock - 1) / kRowsPerBlock));
   const int nvec = n_cols / 8;
-#define QL_RMS_BWD(VPL)                                                                      \
-  hipLaunchKernelGGL((rmsnorm_bwd_wave<GT, XT, WT, XT, VPL>), grid, dim3(kThreads), 0, s,    \
-                     (const G*)dy, dys, (const X*)x, xs, (const W*)w, rstd, (X*)dx, dxs, n_rows, \
-                     n_cols)
+#define QL_RMS_BWD(VPL)                                                                         \
+  hipLaunchKernelGGL((rmsnorm_bwd_wave<GT, XT, WT, XT, VPL, RES>), grid, dim3(kThreads), 0, s,  \
+                     (const G*)dy, dys, (const X*)x, xs, (const W*)w, rstd, (const X*)dres, drs, \
+                     (X*)dx, dxs, n_rows, n_cols)
   if (nvec <= 4 * 64) QL_RMS_BWD(4);
   else if (nvec <= 8 * 64) QL_RMS_BWD(8);
   else QL_RMS_BWD(16);
@@ -242,4 +264,53 @@ extern "C" int qlora_rmsnorm_bwd(const void* dy, int dy_dtype, int64_t dy_row_st
                      dy_dtype, dy_row_stride, x, x_dtype, x_row_stride, w, w_dtype, rstd, dx,
                      dx_dtype, dx_row_stride, nc);
   return ql_launch_status();
+}
+
+extern "C" int qlora_add_rmsnorm_fwd(const void* x, const void* d, int x_dtype, int64_t x_row_stride,
+                                     int64_t d_row_stride, const void* w, int w_dtype, void* h,
+                                     int64_t h_row_stride, void* y, int y_dtype,
+                                     int64_t y_row_stride, float* rstd, int64_t n_rows,
+                                     int64_t n_cols, float eps, ql_stream_t stream) {
+  if (n_rows < 0 || n_cols <= 0 || n_cols > INT32_MAX) return QL_EINVAL;
+  if (!ql_valid_dtype(x_dtype) || !ql_valid_dtype(w_dtype) || y_dtype != ql_promote(x_dtype, w_dtype))
+    return QL_EDTYPE;
+  if (n_rows == 0) return QL_OK;
+  if (!x || !d || !h || !w || !y || !rstd) return QL_EINVAL;
+  const int nc = (int)n_cols;
+  if (nc % 8 || nc > 16 * 64 * 8) return QL_ESHAPE;
+  if (!row_vec_ok(x, x_row_stride, x_dtype) || !row_vec_ok(d, d_row_stride, x_dtype) ||
+      !row_vec_ok(h, h_row_stride, x_dtype) || !row_vec_ok(y, y_row_stride, y_dtype) ||
+      !ql_aligned(w, 16))
+    return QL_EALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  QL_DISPATCH_DTYPE2(x_dtype, w_dtype, XT, WT,
+                     return (fwd_fast<XT, WT, true>(x, x_row_stride, w, y, y_row_stride, rstd,
+                                                    n_rows, nc, eps, s, d, d_row_stride, h,
+                                                    h_row_stride)));
+  return QL_EDTYPE;
+}
+
+extern "C" int qlora_rmsnorm_bwd_residual(const void* dy, int dy_dtype, int64_t dy_row_stride,
+                                          const void* x, int x_dtype, int64_t x_row_stride,
+                                          const void* w, int w_dtype, const float* rstd,
+                                          const void* dres, int64_t dres_row_stride, void* dx,
+                                          int64_t dx_row_stride, int64_t n_rows, int64_t n_cols,
+                                          ql_stream_t stream) {
+  if (n_rows < 0 || n_cols <= 0 || n_cols > INT32_MAX) return QL_EINVAL;
+  if (!ql_valid_dtype(x_dtype) || !ql_valid_dtype(w_dtype) || dy_dtype != ql_promote(x_dtype, w_dtype))
+    return QL_EDTYPE;
+  if (n_rows == 0) return QL_OK;
+  if (!dy || !x || !w || !rstd || !dres || !dx) return QL_EINVAL;
+  const int nc = (int)n_cols;
+  if (nc % 8 || nc > 16 * 64 * 8) return QL_ESHAPE;
+  if (!row_vec_ok(dy, dy_row_stride, dy_dtype) || !row_vec_ok(x, x_row_stride, x_dtype) ||
+      !row_vec_ok(dres, dres_row_stride, x_dtype) || !row_vec_ok(dx, dx_row_stride, x_dtype) ||
+      !ql_aligned(w, 16))
+    return QL_EALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  QL_DISPATCH_DTYPE2(x_dtype, w_dtype, XT, WT,
+                     return (bwd_fast<XT, WT, true>(dy, dy_row_stride, x, x_row_stride, w, rstd, dx,
+                                                    dx_row_stride, n_rows, nc, s, dres,
+                                                    dres_row_stride)));
+  return QL_EDTYPE;
 }

@@ -8,10 +8,11 @@ this module builds the same model shape from a local `Qwen2Config` with random w
 (no checkpoint, no network), swaps every q/k/v/o/gate/up/down projection for
 `LoraLinear4bit(Linear4bit)` and runs the step either
   - patched: `hackathon_amd.apply()` installed and the fused head loss armed, so every
-    RMSNorm, RoPE, SwiGLU, NF4 linear, LoRA cast/GEMM/add and the lm_head + CE run on the
-    gfx950 kernels; or
+    RMSNorm (with the decoder layer's residual adds), RoPE, attention, SwiGLU, NF4 linear,
+    LoRA cast/GEMM/add, the lm_head + CE and the AdamW update run on the gfx950 kernels; or
   - eager: the plain PyTorch-ROCm path (torch-op dequant, hipBLASLt GEMMs through F.linear,
-    transformers' own RMSNorm/RoPE/MLP and full-logits ForCausalLMLoss), the baseline.
+    transformers' own RMSNorm/RoPE/MLP, torch SDPA, full-logits ForCausalLMLoss and torch's
+    foreach AdamW), the baseline.
 """
 
 from __future__ import annotations
@@ -94,7 +95,8 @@ def _unpatch_transformers():
     from transformers.models.qwen2 import modeling_qwen2 as m
 
     for owner, name in ((m.Qwen2RMSNorm, "forward"), (m.Qwen2MLP, "forward"),
-                        (m.Qwen2ForCausalLM, "forward"), (m, "apply_rotary_pos_emb")):
+                        (m.Qwen2ForCausalLM, "forward"), (m, "apply_rotary_pos_emb"),
+                        (m.Qwen2DecoderLayer, "forward")):
         fn = getattr(owner, name)
         orig = getattr(fn, "_original", None)
         if orig is not None:
@@ -137,13 +139,23 @@ def patched_mode():
 
 class QLoRAStep:
     """forward + backward + AdamW on the adapters. `fused_head` arms the chunked lm_head + CE
-    for the forward (what the reference's trainer hook does, solution/cross_entropy.py:294)."""
+    for the forward (what the reference's trainer hook does, solution/cross_entropy.py:294);
+    `fused_adamw` updates the adapters with `optim.FusedAdamW` (one HIP launch) instead of
+    torch's foreach AdamW."""
 
-    def __init__(self, model, lr=1e-4, fused_head=True):
+    def __init__(self, model, lr=1e-4, fused_head=True, fused_adamw=None):
         self.model = model
         self.fused_head = fused_head
-        self.opt = torch.optim.AdamW(lora_parameters(model), lr=lr, betas=(0.9, 0.999),
-                                     weight_decay=0.0, foreach=True)
+        if fused_adamw is None:
+            fused_adamw = fused_head
+        params = lora_parameters(model)
+        if fused_adamw:
+            from .optim import FusedAdamW
+
+            self.opt = FusedAdamW(params, lr=lr, betas=(0.9, 0.999), weight_decay=0.0)
+        else:
+            self.opt = torch.optim.AdamW(params, lr=lr, betas=(0.9, 0.999), weight_decay=0.0,
+                                         foreach=True)
 
     def forward_backward(self, input_ids, labels):
         if self.fused_head:

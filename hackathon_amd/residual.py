@@ -1,0 +1,141 @@
+"""RMSNorm fused with the residual stream of Qwen2DecoderLayer (gfx950 kernels).
+
+transformers' Qwen2DecoderLayer.forward (modeling_qwen2.py:269-297) runs
+    residual = x;  a = input_layernorm(x);  ... attention ...
+    h = residual + attn;  b = post_attention_layernorm(h);  ... mlp ...;  out = h + mlp
+and autograd adds the gradients of each stream where it forks. `patch()` replaces the layer's
+forward with the same computation on two fused operations:
+
+  ResidualRMSNorm(x, None)    -> (x, rmsnorm(x))
+  ResidualRMSNorm(x, delta)   -> (h = x + delta, rmsnorm(h))        one kernel, h rounded to
+                                                                     x's dtype as torch's add
+whose backward is one kernel: dh = rmsnorm_bwd(dy) + d(residual output), the gradient of the
+stream's two uses summed in fp32 and rounded once (autograd rounds each term, then adds).
+The final `h + mlp` stays a plain add. The reference leaves the layer to transformers; this
+is the "RMSNorm + residual-add" fusion around modeling_qwen2.py:280-297.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _common, _lib
+
+
+class ResidualRMSNorm(torch.autograd.Function):
+    """(x, delta) -> (h, y): h = x + delta (or x when delta is None), y = weight * rmsnorm(h)
+    with Qwen2RMSNorm's rounding (solution/rmsnorm.py:13-14 math). The weight is frozen."""
+
+    @staticmethod
+    def forward(ctx, x, delta, weight, eps):
+        _lib.require_device(x, weight)
+        shape = x.shape
+        N = shape[-1]
+        x2 = x.reshape(-1, N)
+        M = x2.shape[0]
+        out_dtype = torch.promote_types(weight.dtype, x.dtype)
+        y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+        rstd = torch.empty(M, dtype=torch.float32, device=x.device)
+        stream = _lib.stream_of(x2)
+        if delta is None:
+            h2 = x2
+            _lib.call("qlora_rmsnorm_fwd", x2.data_ptr(), _lib.tag(x2.dtype), x2.stride(0),
+                      weight.data_ptr(), _lib.tag(weight.dtype), y.data_ptr(),
+                      _lib.tag(out_dtype), y.stride(0), rstd.data_ptr(), M, N, float(eps), stream)
+            h = x.view_as(x)
+        else:
+            d2 = delta.reshape(-1, N)
+            h2 = torch.empty_like(x2)
+            _lib.call("qlora_add_rmsnorm_fwd", x2.data_ptr(), d2.data_ptr(), _lib.tag(x2.dtype),
+                      x2.stride(0), d2.stride(0), weight.data_ptr(), _lib.tag(weight.dtype),
+                      h2.data_ptr(), h2.stride(0), y.data_ptr(), _lib.tag(out_dtype), y.stride(0),
+                      rstd.data_ptr(), M, N, float(eps), stream)
+            h = h2.view(shape)
+        ctx.save_for_backward(h2, weight, rstd)
+        ctx.shape = shape
+        ctx.has_delta = delta is not None
+        return h, y.view(shape)
+
+    @staticmethod
+    def backward(ctx, dh, dy):
+        h2, w, rstd = ctx.saved_tensors
+        M, N = h2.shape
+        if dy is None:
+            return dh, (dh if ctx.has_delta else None), None, None
+        dy2 = dy.reshape(M, N)
+        if dy2.stride(-1) != 1 or dy2.stride(0) % 8:
+            dy2 = dy2.contiguous()
+        dres = torch.zeros_like(h2) if dh is None else dh.reshape(M, N)
+        if dres.stride(-1) != 1 or dres.stride(0) % 8:
+            dres = dres.contiguous()
+        dx = torch.empty_like(h2)
+        _lib.call("qlora_rmsnorm_bwd_residual", dy2.data_ptr(), _lib.tag(dy2.dtype), dy2.stride(0),
+                  h2.data_ptr(), _lib.tag(h2.dtype), h2.stride(0), w.data_ptr(), _lib.tag(w.dtype),
+                  rstd.data_ptr(), dres.data_ptr(), dres.stride(0), dx.data_ptr(), dx.stride(0),
+                  M, N, _lib.stream_of(dx))
+        dx = dx.view(ctx.shape)
+        return dx, (dx if ctx.has_delta else None), None, None
+
+
+def residual_rmsnorm(x, delta, weight, eps):
+    """(h, y) = (x + delta, weight * rmsnorm(x + delta)); delta None: (x, weight * rmsnorm(x))."""
+    return ResidualRMSNorm.apply(x, delta, weight, eps)
+
+
+def _rows_ok(t):
+    n = t.shape[-1]
+    return (t.dim() >= 2 and t.is_contiguous() and n % 8 == 0 and n <= 8192
+            and t.data_ptr() % 16 == 0)
+
+
+def _norm_ok(norm, x):
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    w = getattr(norm, "weight", None)
+    return (type(norm) is m.Qwen2RMSNorm and isinstance(w, torch.Tensor) and w.dim() == 1
+            and w.shape[0] == x.shape[-1] and not w.requires_grad and _common.on_gpu(w)
+            and w.data_ptr() % 16 == 0 and w.is_contiguous())
+
+
+def supported(layer, hidden_states):
+    """Whether a Qwen2DecoderLayer call can take the fused norms."""
+    return (_common.on_gpu(hidden_states)
+            and hidden_states.dtype in (torch.float32, torch.float16, torch.bfloat16)
+            and _rows_ok(hidden_states)
+            and _norm_ok(layer.input_layernorm, hidden_states)
+            and _norm_ok(layer.post_attention_layernorm, hidden_states)
+            and layer.input_layernorm.weight.dtype == hidden_states.dtype
+            and layer.post_attention_layernorm.weight.dtype == hidden_states.dtype)
+
+
+def patch():
+    """Install the fused-norm Qwen2DecoderLayer.forward (unsupported calls run the original)."""
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    original = m.Qwen2DecoderLayer.forward
+    if getattr(original, "_solution_patch", False):
+        return
+
+    def forward(self, hidden_states, attention_mask=None, position_ids=None,
+                past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
+        if not supported(self, hidden_states):
+            return original(self, hidden_states, attention_mask=attention_mask,
+                            position_ids=position_ids, past_key_values=past_key_values,
+                            use_cache=use_cache, position_embeddings=position_embeddings,
+                            **kwargs)
+        ln1, ln2 = self.input_layernorm, self.post_attention_layernorm
+        residual, x = residual_rmsnorm(hidden_states, None, ln1.weight, ln1.variance_epsilon)
+        attn, _ = self.self_attn(hidden_states=x, attention_mask=attention_mask,
+                                 position_ids=position_ids, past_key_values=past_key_values,
+                                 use_cache=use_cache, position_embeddings=position_embeddings,
+                                 **kwargs)
+        if attn.dtype != residual.dtype or not _rows_ok(attn):
+            h = residual + attn
+            x = ln2(h)
+        else:
+            h, x = residual_rmsnorm(residual, attn, ln2.weight, ln2.variance_epsilon)
+        return h + self.mlp(x)
+
+    forward._solution_patch = True
+    forward._original = original
+    m.Qwen2DecoderLayer.forward = forward

@@ -102,6 +102,34 @@ int qlora_rmsnorm_bwd(const void* dy, int dy_dtype, int64_t dy_row_stride, const
                       int64_t n_rows, int64_t n_cols, ql_stream_t stream);
 
 /*
+ * RMSNorm of a residual sum: h = x + d rounded to x's dtype (written to h), then the
+ * qlora_rmsnorm_fwd of h (y, rstd). x, d and h share x_dtype; y_dtype = promote(x, w).
+ * Rows must hold a multiple of 8 elements (at most 8192), start 16-B aligned, w 16-B aligned
+ * (QL_ESHAPE / QL_EALIGN otherwise).
+ * Replaces: `residual + hidden_states` followed by the post-attention Qwen2RMSNorm in
+ * Qwen2DecoderLayer.forward (transformers/models/qwen2/modeling_qwen2.py:280-291), the
+ * decoder layer around the reference's RMSNorm patch (solution/rmsnorm.py:99-115).
+ */
+int qlora_add_rmsnorm_fwd(const void* x, const void* d, int x_dtype, int64_t x_row_stride,
+                          int64_t d_row_stride, const void* w, int w_dtype, void* h,
+                          int64_t h_row_stride, void* y, int y_dtype, int64_t y_row_stride,
+                          float* rstd, int64_t n_rows, int64_t n_cols, float eps,
+                          ql_stream_t stream);
+
+/*
+ * qlora_rmsnorm_bwd plus the gradient of the normalised row's other use (the residual
+ * stream): dx = rmsnorm_bwd(dy) + dres, summed in fp32 and rounded once to x's dtype (dres
+ * and dx have x's dtype). Same row requirements as qlora_add_rmsnorm_fwd.
+ * Replaces: the RMSNorm backward of solution/rmsnorm.py:42-55 and the gradient add autograd
+ * performs where Qwen2DecoderLayer's residual stream forks.
+ */
+int qlora_rmsnorm_bwd_residual(const void* dy, int dy_dtype, int64_t dy_row_stride,
+                               const void* x, int x_dtype, int64_t x_row_stride, const void* w,
+                               int w_dtype, const float* rstd, const void* dres,
+                               int64_t dres_row_stride, void* dx, int64_t dx_row_stride,
+                               int64_t n_rows, int64_t n_cols, ql_stream_t stream);
+
+/*
  * Rotary embedding of q and k in one launch, forward or backward (transpose).
  * Replaces: solution/rope.py:24-62 (rope_qk_kernel) + :65-75 (_launch).
  * q/k/q_out/k_out are (B, H, S, D) tensors given by strides {b, h, s} (last dim unit
@@ -326,6 +354,32 @@ int qlora_attn_bwd(const void* q, const void* k, const void* v, const void* o, c
                    const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
                    const int64_t* dq_strides, const int64_t* dkv_strides, float scale,
                    void* workspace, int64_t workspace_bytes, ql_stream_t stream);
+
+/*
+ * AdamW (torch.optim.AdamW semantics: decoupled weight decay, bias-corrected moments, no
+ * amsgrad) over many fp32 tensors in one launch. `table` is a DEVICE array of n_tensors
+ * descriptors; tensor t covers chunks [first_chunk, first_chunk + ceil(numel / C)) of the
+ * launch, C = qlora_adamw_chunk_elems(), the tensors in order and without gaps, n_chunks the
+ * total. The scalars are the values torch computes in double for this step, rounded to fp32:
+ *   decay = 1 - lr * weight_decay, one_minus_beta1 = 1 - beta1, one_minus_beta2 = 1 - beta2,
+ *   step_size = lr / (1 - beta1^step), bias_correction2_sqrt = sqrt(1 - beta2^step).
+ * Per element: p *= decay; m = lerp(m, g, 1 - beta1); v = v beta2 + (1 - beta2) g g;
+ *   p += -step_size * m / (sqrt(v) / bias_correction2_sqrt + eps).
+ * Replaces: the optimizer of the reference's training step (the trainer's torch AdamW over the
+ * LoRA parameters); the reference has no kernel for it.
+ */
+typedef struct ql_adamw_tensor {
+  float* param;
+  const float* grad;
+  float* exp_avg;
+  float* exp_avg_sq;
+  int64_t numel;
+  int64_t first_chunk;
+} ql_adamw_tensor;
+int64_t qlora_adamw_chunk_elems(void);
+int qlora_adamw_fp32(const ql_adamw_tensor* table, int n_tensors, int64_t n_chunks, float decay,
+                     float beta2, float one_minus_beta1, float one_minus_beta2, float step_size,
+                     float bias_correction2_sqrt, float eps, ql_stream_t stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

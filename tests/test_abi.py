@@ -92,6 +92,21 @@ def test_rejected_arguments_return_codes(lib):
                           None) == -3
     assert lib.qlora_gemm(0, 0, 4, 4, 12, fake, 8, fake, 16, 2, fake, 4, 0, None, 1.0, 0.0,
                           None) == -4
+    # adamw: a table is required when there is work; the bias correction must be positive
+    assert lib.qlora_adamw_fp32(None, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 1.0, 1e-8, None) == -1
+    assert lib.qlora_adamw_fp32(fake, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 0.0, 1e-8, None) == -1
+    assert lib.qlora_adamw_chunk_elems() == 2048
+    # add + rmsnorm: the row length must be a multiple of 8; rows must be 16-B aligned
+    assert lib.qlora_add_rmsnorm_fwd(fake, fake, 2, 12, 12, fake, 2, fake, 12, fake, 2, 12, fake,
+                                     4, 12, 1e-6, None) == -4
+    assert lib.qlora_add_rmsnorm_fwd(P(0x1008), fake, 2, 16, 16, fake, 2, fake, 16, fake, 2, 16,
+                                     fake, 4, 16, 1e-6, None) == -3
+    assert lib.qlora_rmsnorm_bwd_residual(fake, 2, 16, fake, 2, 16, fake, 2, fake, None, 16, fake,
+                                          16, 4, 16, None) == -1
+    # attention: head_dim must be 128
+    strides = (ctypes.c_int64 * 3)(0, 0, 0)
+    assert lib.qlora_attn_fwd(fake, fake, fake, fake, None, 2, 1, 1, 1, 64, 64, strides, strides,
+                              strides, strides, 0.1, None) == -4
 
 
 def test_empty_problems_are_no_ops(lib):

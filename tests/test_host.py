@@ -61,6 +61,45 @@ def test_sdpa_patch_falls_back_on_cpu_and_unsupported_calls():
     assert not attention.supported(Mod(), q, k, v, None, 0.0, None, {})
 
 
+def test_decoder_layer_patch_falls_back_on_cpu():
+    from transformers.models.qwen2 import modeling_qwen2 as m
+
+    from hackathon_amd import qlora_step as qs
+
+    hackathon_amd.apply()
+    assert getattr(m.Qwen2DecoderLayer.forward, "_solution_patch", False)
+    cfg = qs.qwen2_config(hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                          num_attention_heads=2, num_key_value_heads=1, vocab_size=32)
+    torch.manual_seed(0)
+    layer = m.Qwen2DecoderLayer(cfg, 0)
+    rot = m.Qwen2RotaryEmbedding(cfg)
+    x = torch.randn(1, 5, 64)
+    pos = torch.arange(5)[None]
+    pe = rot(x, pos)
+    got = layer(x, position_embeddings=pe, position_ids=pos)
+    want = m.Qwen2DecoderLayer.forward._original(layer, x, position_embeddings=pe,
+                                                 position_ids=pos)
+    torch.testing.assert_close(got, want)
+
+
+def test_fused_adamw_uses_torch_on_cpu():
+    from hackathon_amd.optim import FusedAdamW
+
+    torch.manual_seed(0)
+    a = [torch.nn.Parameter(torch.randn(5, 3)), torch.nn.Parameter(torch.randn(7))]
+    b = [torch.nn.Parameter(t.detach().clone()) for t in a]
+    oa = torch.optim.AdamW(a, lr=1e-2, weight_decay=0.1, foreach=False)
+    ob = FusedAdamW(b, lr=1e-2, weight_decay=0.1)
+    for _ in range(3):
+        for x, y in zip(a, b):
+            g = torch.randn_like(x)
+            x.grad, y.grad = g.clone(), g.clone()
+        oa.step()
+        ob.step()
+    for x, y in zip(a, b):
+        torch.testing.assert_close(y, x, rtol=0, atol=0)
+
+
 def test_rope_supported_guard():
     q = torch.randn(2, 4, 5, 16)
     k = torch.randn(2, 2, 5, 16)
