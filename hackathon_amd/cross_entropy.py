@@ -184,7 +184,127 @@ def _patch_causal_lm():
     m.Qwen2ForCausalLM.forward = forward
 
 
-def patch():
-    """Install the model hook (solution/cross_entropy.py:319-321 also patches trl's
-    SFTTrainer.compute_loss to arm it; trl is not part of this package's scope)."""
+def _causal_lm_of(trainer, model):
+    """The Qwen2ForCausalLM under accelerate / peft wrappers (solution/cross_entropy.py:225-229)."""
+    unwrap = getattr(getattr(trainer, "accelerator", None), "unwrap_model", None)
+    inner = unwrap(model) if callable(unwrap) else model
+    get_base = getattr(inner, "get_base_model", None)
+    return get_base() if callable(get_base) else inner
+
+
+def _can_fuse(trainer, model, inputs):
+    """Whether this compute_loss call may take the fused head: a training step of plain NLL on
+    a Qwen2 causal LM whose frozen head lives on the GPU, with the trainer state TRL's metrics
+    need and no other loss machinery (solution/cross_entropy.py:232-262)."""
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2ForCausalLM
+
+    args = getattr(trainer, "args", None)
+    if not (isinstance(model, torch.nn.Module) and isinstance(inputs, dict) and args is not None):
+        return False
+    if not getattr(trainer.model, "training", False):
+        return False
+    if "labels" not in inputs or "shift_labels" in inputs or "attention_mask" not in inputs:
+        return False
+    if not _common.on_gpu(inputs["labels"], inputs["attention_mask"]):
+        return False
+    if getattr(args, "use_liger_kernel", False) or getattr(args, "loss_type", "nll") != "nll":
+        return False
+    if getattr(trainer, "num_virtual_tokens", 0) or getattr(trainer, "aux_loss_enabled", False):
+        return False
+    if getattr(trainer, "compute_loss_func", None) is not None or \
+            getattr(trainer, "label_smoother", None) is not None:
+        return False
+    if getattr(trainer, "_soup_chunked_head_loss", None) is not None:
+        return False
+    if not all(hasattr(trainer, name) for name in ("_metrics", "_total_train_tokens")):
+        return False
+    lm = _causal_lm_of(trainer, model)
+    return isinstance(lm, Qwen2ForCausalLM) and _head_ok(lm)
+
+
+def entropy_from_logits(logits, chunk_size=128):
+    """Per-position entropy of softmax(logits), by the formula of trl's
+    `trl.trainer.utils.entropy_from_logits` (trl 0.29.1, not installed here): -sum(p log p)
+    with log p = log_softmax, in chunks of rows."""
+    flat = logits.reshape(-1, logits.shape[-1])
+    parts = []
+    for chunk in flat.split(chunk_size, dim=0):
+        logp = torch.nn.functional.log_softmax(chunk, dim=-1)
+        parts.append(-(torch.exp(logp) * logp).sum(-1))
+    return torch.cat(parts, dim=0).reshape(logits.shape[:-1])
+
+
+def _log_metrics(trainer, mode, inputs, step):
+    """entropy, num_tokens and mean_token_accuracy as trl 0.29.1 SFTTrainer.compute_loss logs
+    them (attention_mask present, no virtual tokens), from the fused step's per-row statistics
+    instead of the logits (solution/cross_entropy.py:265-287)."""
+    gather = trainer.accelerator.gather_for_metrics
+    attention_mask = inputs["attention_mask"]
+    with torch.no_grad():
+        entropy = torch.sum(step.token_entropy * attention_mask) / attention_mask.sum()
+        entropy = gather(entropy).mean().item()
+    trainer._metrics[mode]["entropy"].append(entropy)
+    if mode == "train":
+        trainer._total_train_tokens += gather(attention_mask.sum()).sum().item()
+    trainer._metrics[mode]["num_tokens"] = [trainer._total_train_tokens]
+    with torch.no_grad():
+        correct = gather(step.correct)
+        total = gather(step.labelled)
+        total_sum = total.sum()
+        accuracy = (correct.sum() / total_sum).item() if total_sum > 0 else 0.0
+    trainer._metrics[mode]["mean_token_accuracy"].append(accuracy)
+
+
+def _patch_trainer(trainer_cls=None):
+    """Arm the fused head inside `trainer_cls.compute_loss` (default: trl's SFTTrainer; returns
+    False when trl is not importable) and log TRL's metrics from the fused statistics
+    (solution/cross_entropy.py:290-316). The loss itself comes from the parent class's
+    compute_loss (transformers' Trainer), which calls the model with the labels."""
+    if trainer_cls is None:
+        try:
+            from trl import SFTTrainer as trainer_cls
+        except ImportError:
+            return False
+    original = trainer_cls.compute_loss
+    if getattr(original, "_solution_patch", False):
+        return True
+
+    def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
+        if not _can_fuse(self, model, inputs):
+            return original(self, model, inputs, return_outputs=return_outputs,
+                            num_items_in_batch=num_items_in_batch)
+        mode = "train" if self.model.training else "eval"
+        inputs.pop("_prediction_loss_only", None)
+        labels = inputs["labels"]
+        inputs["use_cache"] = False
+        STATE.armed, STATE.step = True, None
+        try:
+            loss, outputs = super(trainer_cls, self).compute_loss(
+                model, inputs, return_outputs=True, num_items_in_batch=num_items_in_batch)
+        finally:
+            STATE.armed = False
+        step, STATE.step = STATE.step, None
+        if step is None:
+            # the model took its original path after all (it has logits): same metrics from them
+            with torch.no_grad():
+                logits = outputs.logits
+                step = ChunkedStep(entropy_from_logits(logits), None, logits.argmax(dim=-1),
+                                   shift_labels_of(labels))
+            setattr(self, STEP_ATTR, None)
+        else:
+            setattr(self, STEP_ATTR, step)
+        _log_metrics(self, mode, inputs, step)
+        return (loss, outputs) if return_outputs else loss
+
+    compute_loss._solution_patch = True
+    compute_loss._original = original
+    trainer_cls.compute_loss = compute_loss
+    return True
+
+
+def patch(trainer_cls=None):
+    """Install the model hook and the trainer hook that arms it (solution/cross_entropy.py:
+    319-321). The trainer hook goes on `trainer_cls`, by default trl's SFTTrainer when trl is
+    importable (it is not in this image, so only the model hook is installed then)."""
     _patch_causal_lm()
+    _patch_trainer(trainer_cls)

@@ -166,3 +166,164 @@ def fused_head_loss(hidden, weight, labels, attention_mask, num_items_in_batch):
                       correct=row_correct[:n_labelled].sum(),
                       labelled=torch.tensor(n_labelled, device=device))
     return loss, stats
+
+
+# ---- model and trainer hooks (solution/fused_ce.py:222-355) ---------------------------------
+class _State:
+    active = False   # set by the trainer hook for exactly one model forward
+    stats = None
+
+
+STATE = _State()
+_ORIGINAL = {}
+
+
+def _causal_lm(model):
+    get_base_model = getattr(model, "get_base_model", None)
+    return get_base_model() if callable(get_base_model) else model
+
+
+def _head_fits(causal_lm):
+    """A Qwen2 causal LM whose lm_head is a frozen, bias-free fp32/fp16 Linear on the GPU with
+    no logit soft-capping (solution/fused_ce.py:236-246)."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    if not isinstance(causal_lm, modeling_qwen2.Qwen2ForCausalLM):
+        return False
+    head = getattr(causal_lm, "lm_head", None)
+    weight = getattr(head, "weight", None)
+    return (type(head) is torch.nn.Linear and head.bias is None and weight is not None
+            and not weight.requires_grad and weight.is_cuda
+            and weight.dtype in (torch.float32, torch.float16)
+            and getattr(causal_lm.config, "final_logit_softcapping", None) is None)
+
+
+def patch_qwen2_causal_lm():
+    """Qwen2ForCausalLM.forward runs `fused_head_loss` when the trainer hook is active and the
+    call is a plain training forward with labels; otherwise the original
+    (solution/fused_ce.py:249-280)."""
+    from transformers.modeling_outputs import CausalLMOutputWithPast
+    from transformers.models.qwen2 import modeling_qwen2
+
+    cls = modeling_qwen2.Qwen2ForCausalLM
+    if "causal_forward" in _ORIGINAL:
+        return
+    original = cls.forward
+    _ORIGINAL["causal_forward"] = original
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None,
+                past_key_values=None, inputs_embeds=None, labels=None, use_cache=None,
+                logits_to_keep=0, **kwargs):
+        if (not STATE.active or labels is None or not self.training
+                or not (isinstance(logits_to_keep, int) and logits_to_keep == 0)
+                or kwargs.get("shift_labels") is not None or kwargs.get("return_dict") is False
+                or not _head_fits(self)):
+            return original(self, input_ids=input_ids, attention_mask=attention_mask,
+                            position_ids=position_ids, past_key_values=past_key_values,
+                            inputs_embeds=inputs_embeds, labels=labels, use_cache=use_cache,
+                            logits_to_keep=logits_to_keep, **kwargs)
+        kwargs.pop("return_dict", None)
+        outputs = self.model(input_ids=input_ids, attention_mask=attention_mask,
+                             position_ids=position_ids, past_key_values=past_key_values,
+                             inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
+        loss, STATE.stats = fused_head_loss(outputs.last_hidden_state, self.lm_head.weight,
+                                            labels, attention_mask,
+                                            kwargs.get("num_items_in_batch"))
+        return CausalLMOutputWithPast(loss=loss, logits=None,
+                                      past_key_values=outputs.past_key_values,
+                                      hidden_states=outputs.hidden_states,
+                                      attentions=outputs.attentions)
+
+    forward._original = original
+    cls.forward = forward
+
+
+def _can_fuse(trainer, model, inputs):
+    """solution/fused_ce.py:283-301: a training step of plain NLL with labels and an attention
+    mask, the trainer state TRL's metrics need, and a head `_head_fits` accepts."""
+    args = getattr(trainer, "args", None)
+    if args is None or not isinstance(model, torch.nn.Module) or not model.training:
+        return False
+    if getattr(args, "use_liger_kernel", False) or getattr(args, "loss_type", "nll") != "nll":
+        return False
+    if getattr(trainer, "compute_loss_func", None) is not None:
+        return False
+    if getattr(trainer, "label_smoother", None) is not None:
+        return False
+    if getattr(trainer, "num_virtual_tokens", 0) or getattr(trainer, "aux_loss_enabled", False):
+        return False
+    if not hasattr(trainer, "_metrics") or not hasattr(trainer, "_total_train_tokens"):
+        return False
+    if not isinstance(inputs, dict) or "labels" not in inputs or "attention_mask" not in inputs:
+        return False
+    if "shift_labels" in inputs:
+        return False
+    return _head_fits(_causal_lm(model))
+
+
+def patch_sft_trainer(trainer_cls=None):
+    """Activate the fused head inside `trainer_cls.compute_loss` (default: trl's SFTTrainer;
+    returns False when trl is not importable), log TRL's metrics from the fused statistics and
+    leave the per-token loss for a recorder under STEP_ATTR (solution/fused_ce.py:304-355)."""
+    from transformers import Trainer
+
+    if trainer_cls is None:
+        try:
+            from trl import SFTTrainer as trainer_cls
+        except ImportError:
+            return False
+    if "compute_loss" in _ORIGINAL:
+        return True
+    original = trainer_cls.compute_loss
+    _ORIGINAL["compute_loss"] = (trainer_cls, original)
+
+    def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
+        if not _can_fuse(self, model, inputs):
+            if getattr(self, STEP_ATTR, None) is not None:
+                setattr(self, STEP_ATTR, None)
+            return original(self, model, inputs, return_outputs=return_outputs,
+                            num_items_in_batch=num_items_in_batch)
+        mode = "train"
+        inputs.pop("_prediction_loss_only", None)
+        inputs["use_cache"] = False
+        STATE.active, STATE.stats = True, None
+        try:
+            loss, outputs = Trainer.compute_loss(self, model, inputs, return_outputs=True,
+                                                 num_items_in_batch=num_items_in_batch)
+        finally:
+            STATE.active = False
+        stats, STATE.stats = STATE.stats, None
+        if stats is None:
+            raise RuntimeError("hackathon_amd: the fused head loss did not run in this step")
+
+        gather = self.accelerator.gather_for_metrics
+        attention_mask = inputs["attention_mask"]
+        with torch.no_grad():
+            entropy = stats.entropy_sum / attention_mask.sum()
+            entropy = gather(entropy).mean().item()
+        self._metrics[mode]["entropy"].append(entropy)
+        self._total_train_tokens += gather(attention_mask.sum()).sum().item()
+        self._metrics[mode]["num_tokens"] = [self._total_train_tokens]
+        with torch.no_grad():
+            correct_tokens = gather(stats.correct)
+            total_tokens = gather(stats.labelled)
+            total_sum = total_tokens.sum()
+            accuracy = (correct_tokens.sum() / total_sum).item() if total_sum > 0 else 0.0
+        self._metrics[mode]["mean_token_accuracy"].append(accuracy)
+        setattr(self, STEP_ATTR, _Step(stats.token_loss))
+        return (loss, outputs) if return_outputs else loss
+
+    trainer_cls.compute_loss = compute_loss
+    return True
+
+
+def unpatch():
+    """Restore what patch_qwen2_causal_lm / patch_sft_trainer replaced."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    cls_forward = _ORIGINAL.pop("causal_forward", None)
+    if cls_forward is not None:
+        modeling_qwen2.Qwen2ForCausalLM.forward = cls_forward
+    hooked = _ORIGINAL.pop("compute_loss", None)
+    if hooked is not None:
+        hooked[0].compute_loss = hooked[1]
