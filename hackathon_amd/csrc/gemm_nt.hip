@@ -45,7 +45,9 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
-constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int BM = 256, BK = 64;
+// Tile width: NJ 16-column fragments per wave, 2 waves across N (NJ = 8: 256; NJ = 7: 224).
+template <int NJ> constexpr int bn_of() { return 32 * NJ; }
 constexpr int kThreads = 256;
 constexpr int kRowBytes = BK * 2;                  // 128 B: one tile row of 64 k
 constexpr int kTileBytes = 256 * kRowBytes;        // 32 KiB: one operand, one stage
@@ -83,10 +85,11 @@ QL_DEV TileLoader make_loader() {
   return t;
 }
 
+template <int R8 = 8>  // tile rows / 32: 8 (256 rows) or 7 (224 rows)
 QL_DEV void load_tile(const TileLoader& t, const uint16_t* __restrict__ X, int64_t ld,
                       int64_t row0, int64_t rows, int64_t k0, char* __restrict__ lds_tile) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < R8; ++j) {
     const int r0 = (4 * j + t.wave) * 8;
     const int64_t grow0 = row0 + r0;
     const int64_t base_row = grow0 < rows ? grow0 : rows - 1;
@@ -114,25 +117,27 @@ QL_DEV void tile_of(int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) 
   tn = in_group / gm;
 }
 
-// Fragment reads of one 32-k half of a stage: a[i] rows wm*128 + 16 i + fr, b[j] likewise.
+// Fragment reads of one 32-k half of a stage: a[i] rows wm*128 + 16 i + fr, b[j] rows
+// wn*16*NJ + 16 j + fr.
+template <int NJ>
 QL_DEV void read_frags(const char* __restrict__ stage, int half, int wm, int wn, int fr, int fq,
-                       uint4 (&a)[8], uint4 (&b)[8]) {
+                       uint4 (&a)[8], uint4 (&b)[NJ]) {
   const char* as = stage + (wm * 128 + fr) * kRowBytes;
-  const char* bs = stage + kTileBytes + (wn * 128 + fr) * kRowBytes;
+  const char* bs = stage + kTileBytes + (wn * 16 * NJ + fr) * kRowBytes;
   const int c = ((half * 4 + fq) ^ (fr & 7)) * 16;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     a[i] = *reinterpret_cast<const uint4*>(as + i * 16 * kRowBytes + c);
-    b[i] = *reinterpret_cast<const uint4*>(bs + i * 16 * kRowBytes + c);
+    if (i < NJ) b[i] = *reinterpret_cast<const uint4*>(bs + i * 16 * kRowBytes + c);
   }
 }
 
-template <int IT>
-QL_DEV void mma_half(f32x4_t (&acc)[8][8], const uint4 (&a)[8], const uint4 (&b)[8]) {
+template <int IT, int NJ>
+QL_DEV void mma_half(f32x4_t (&acc)[8][NJ], const uint4 (&a)[8], const uint4 (&b)[NJ]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       acc[i][j] = mfma<IT>(b[j], a[i], acc[i][j]);
     }
 }
@@ -145,42 +150,44 @@ QL_DEV void mma_half(f32x4_t (&acc)[8][8], const uint4 (&a)[8], const uint4 (&b)
 // reloads itself: in bounds, never read), and reads the first half of `nxt` while
 // multiplying the second half of `cur`. `cur` and `nxt` are restrict-qualified so the
 // compiler's wait-count pass does not make these reads wait for the DMA into `cur`.
-template <int IT>
-QL_DEV void mma_step_pipe(f32x4_t (&acc)[8][8], uint4 (&f0a)[8], uint4 (&f0b)[8],
+// Per half step: R = 8 + NJ fragment reads, 8 NJ MFMAs, and (second half) R DMA loads.
+template <int IT, int NJ>
+QL_DEV void mma_step_pipe(f32x4_t (&acc)[8][NJ], uint4 (&f0a)[8], uint4 (&f0b)[NJ],
                           char* __restrict__ cur, char* __restrict__ nxt, const TileLoader& la,
                           const uint16_t* __restrict__ A2, int64_t lda2,
                           const uint16_t* __restrict__ B2, int64_t ldb2, int64_t k2, int64_t m0,
                           int64_t n0, int64_t M, int64_t N, int wm, int wn, int fr, int fq) {
-  uint4 f1a[8], f1b[8];
-  read_frags(cur, 1, wm, wn, fr, fq, f1a, f1b);
-  mma_half<IT>(acc, f0a, f0b);
+  constexpr int R = 8 + NJ, MF = 8 * NJ;
+  uint4 f1a[8], f1b[NJ];
+  read_frags<NJ>(cur, 1, wm, wn, fr, fq, f1a, f1b);
+  mma_half<IT, NJ>(acc, f0a, f0b);
   __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
+  for (int t = 0; t < R; ++t) {
     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, 15, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, MF - 1 - 3 * R, 0);
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
   load_tile(la, A2, lda2, m0, M, k2, cur);
-  load_tile(la, B2, ldb2, n0, N, k2, cur + kTileBytes);
-  read_frags(nxt, 0, wm, wn, fr, fq, f0a, f0b);
-  mma_half<IT>(acc, f1a, f1b);
-  __builtin_amdgcn_sched_group_barrier(0x020, 16, 1);
+  load_tile<NJ>(la, B2, ldb2, n0, N, k2, cur + kTileBytes);
+  read_frags<NJ>(nxt, 0, wm, wn, fr, fq, f0a, f0b);
+  mma_half<IT, NJ>(acc, f1a, f1b);
+  __builtin_amdgcn_sched_group_barrier(0x020, R, 1);
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
+  for (int t = 0; t < R; ++t) {
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, 32, 1);
+  __builtin_amdgcn_sched_group_barrier(0x008, MF - 2 * R, 1);
 }
 
 // PARTIAL: write the raw fp32 sums of this split to ws[split][M][N]; otherwise the final
 // alpha / beta / bias epilogue into C (type OT).
-template <int IT, int OT, bool PARTIAL>
+template <int IT, int OT, bool PARTIAL, int NJ>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
                     int64_t ldb, const uint16_t* __restrict__ A2, int64_t lda2,
@@ -190,6 +197,7 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
                     int64_t N, int64_t K, int64_t k_per_split, float alpha, float beta,
                     bool vec_out) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
+  constexpr int BN = bn_of<NJ>();
   int64_t tm, tn;
   tile_of((M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const int64_t m0 = tm * BM, n0 = tn * BN;
@@ -204,32 +212,33 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
   const int fr = lane & 15;  // fragment row within a 16-row sub-tile
   const int fq = lane >> 4;  // fragment k quarter (8 k each) within a 32-k step
 
-  f32x4_t acc[8][8];
+  f32x4_t acc[8][NJ];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const TileLoader la = make_loader();
   // k index of step t in its segment, and the segment's operands
   auto seg_k = [&](int t) -> int64_t { return t < nk1 ? kb + (int64_t)t * BK : (int64_t)(t - nk1) * BK; };
   if (nk > 0) {
     const bool s1 = nk1 > 0;
     load_tile(la, s1 ? A : A2, s1 ? lda : lda2, m0, M, seg_k(0), smem);
-    load_tile(la, s1 ? B : B2, s1 ? ldb : ldb2, n0, N, seg_k(0), smem + kTileBytes);
+    load_tile<NJ>(la, s1 ? B : B2, s1 ? ldb : ldb2, n0, N, seg_k(0), smem + kTileBytes);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const int t1 = nk > 1 ? 1 : 0;
     const bool s1b = t1 < nk1;
     load_tile(la, s1b ? A : A2, s1b ? lda : lda2, m0, M, seg_k(t1), smem + kStageBytes);
-    load_tile(la, s1b ? B : B2, s1b ? ldb : ldb2, n0, N, seg_k(t1), smem + kStageBytes + kTileBytes);
-    uint4 f0a[8], f0b[8];
-    read_frags(smem, 0, wm, wn, fr, fq, f0a, f0b);
+    load_tile<NJ>(la, s1b ? B : B2, s1b ? ldb : ldb2, n0, N, seg_k(t1),
+                  smem + kStageBytes + kTileBytes);
+    uint4 f0a[8], f0b[NJ];
+    read_frags<NJ>(smem, 0, wm, wn, fr, fq, f0a, f0b);
     for (int kt = 0; kt < nk; ++kt) {
       char* cur = smem + (kt & 1) * kStageBytes;
       char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
       const int t2 = kt + 2 < nk ? kt + 2 : nk - 1;
       const bool s2 = t2 < nk1;
-      mma_step_pipe<IT>(acc, f0a, f0b, cur, nxt, la, s2 ? A : A2, s2 ? lda : lda2, s2 ? B : B2,
+      mma_step_pipe<IT, NJ>(acc, f0a, f0b, cur, nxt, la, s2 ? A : A2, s2 ? lda : lda2, s2 ? B : B2,
                         s2 ? ldb : ldb2, seg_k(t2), m0, n0, M, N, wm, wn, fr, fq);
     }
   }
@@ -242,8 +251,8 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
     const int64_t row = m0 + wm * 128 + i * 16 + fr;
     if (row >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t col = n0 + wn * 128 + j * 16 + 4 * fq;
+    for (int j = 0; j < NJ; ++j) {
+      const int64_t col = n0 + wn * 16 * NJ + j * 16 + 4 * fq;
       if (col >= N) continue;
       if constexpr (PARTIAL) {
         float* p = ws + ((int64_t)blockIdx.y * M + row) * N + col;
@@ -303,24 +312,25 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
   }
 }
 
-template <int IT, int OT>
+template <int IT, int OT, int NJ>
 int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
            const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
            int64_t M, int64_t N, int64_t K, float alpha, float beta, int splits, float* ws,
            hipStream_t s) {
   using T = typename Elem<OT>::T;
+  constexpr int BN = bn_of<NJ>();
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int64_t kps = ((K / BK + splits - 1) / splits) * BK;
   const int nsplit = (int)((K + kps - 1) / kps);
   if (nsplit <= 1) {
     const bool vec_out = ql_aligned(C, 4 * ql_elem_size(OT)) && ldc % 4 == 0;
-    hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false>), dim3((unsigned)tiles, 1), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NJ>), dim3((unsigned)tiles, 1), dim3(kThreads), 0, s,
                        (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2,
                        lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc, nullptr,
                        (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
     return ql_launch_status();
   }
-  hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true>), dim3((unsigned)tiles, (unsigned)nsplit),
+  hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NJ>), dim3((unsigned)tiles, (unsigned)nsplit),
                      dim3(kThreads), 0, s,
                      (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
                      (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0,
@@ -335,12 +345,23 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
   return ql_launch_status();
 }
 
+// Tile width for an M x N output: 224 (NJ = 7) when N is a multiple of 224 and the narrower
+// tiles take fewer (waves x tile width) on 256 CUs, else 256. The 4096 x 3584 outputs of the
+// 7B step are 224 tiles of 256 x 256 (one partial wave) but exactly 256 tiles of 256 x 224.
+int choose_nj(int64_t M, int64_t N) {
+  if (N % 224) return 8;
+  const int64_t tm = (M + BM - 1) / BM;
+  const int64_t w8 = (tm * ((N + 255) / 256) + 255) / 256;
+  const int64_t w7 = (tm * (N / 224) + 255) / 256;
+  return w7 * 7 < w8 * 8 ? 7 : 8;
+}
+
 }  // namespace
 
 bool ql_gemm_nt_fits(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* B,
                      int64_t ldb) {
   return M > 0 && N > 0 && K > 0 && K % BK == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
-         ql_aligned(A, 16) && ql_aligned(B, 16) && (M + BM - 1) / BM * ((N + BN - 1) / BN) < (1 << 30);
+         ql_aligned(A, 16) && ql_aligned(B, 16) && (M + BM - 1) / BM * ((N + 223) / 224) < (1 << 30);
 }
 
 int64_t ql_gemm_nt_workspace_floats(int64_t M, int64_t N, int splits) {
@@ -350,7 +371,8 @@ int64_t ql_gemm_nt_workspace_floats(int64_t M, int64_t N, int splits) {
 int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
   // Enough workgroups for 256 CUs: split K while there are fewer tiles than CUs and each
   // split keeps at least 8 K steps.
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int64_t bn = 32 * choose_nj(M, N);
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + bn - 1) / bn);
   int s = 1;
   while (tiles * s < 192 && (K / BK) / (2 * s) >= 8 && s < 64) s *= 2;
   return s;
@@ -363,15 +385,25 @@ int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, cons
   if (splits > 1 && !ws) return QL_EINVAL;
   if (K2 < 0 || K2 % BK) return QL_EINVAL;
   if (K2 == 0) A2 = B2 = nullptr;
+  const bool narrow = choose_nj(M, N) == 7;
+#define QL_GEMM_NT_LAUNCH(ITC, NJC)                                                            \
+  QL_DISPATCH_DTYPE(c_dtype, OT,                                                               \
+                    return (launch<ITC, OT, NJC>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc, \
+                                                 bias, M, N, K, alpha, beta, splits, ws, s)))
   if (in_dtype == QL_BF16) {
-    QL_DISPATCH_DTYPE(c_dtype, OT,
-                      return launch<QL_BF16, OT>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc,
-                                                 bias, M, N, K, alpha, beta, splits, ws, s));
+    if (narrow) {
+      QL_GEMM_NT_LAUNCH(QL_BF16, 7);
+    } else {
+      QL_GEMM_NT_LAUNCH(QL_BF16, 8);
+    }
   } else if (in_dtype == QL_F16) {
-    QL_DISPATCH_DTYPE(c_dtype, OT,
-                      return launch<QL_F16, OT>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc,
-                                                bias, M, N, K, alpha, beta, splits, ws, s));
+    if (narrow) {
+      QL_GEMM_NT_LAUNCH(QL_F16, 7);
+    } else {
+      QL_GEMM_NT_LAUNCH(QL_F16, 8);
+    }
   }
+#undef QL_GEMM_NT_LAUNCH
   return QL_EDTYPE;
 }
 

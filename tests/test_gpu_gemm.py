@@ -79,11 +79,13 @@ def test_gemm_output_view_with_row_stride():
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 768, 1024), (300, 520, 192), (257, 255, 64),
-                                   (1000, 3000, 640)])
+                                   (1000, 3000, 640), (300, 448, 128), (1000, 3584, 640),
+                                   (4096, 3584, 256)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_large_tile_edges(M, N, K, dtype):
-    """k-contiguous operands with K % 64 == 0 take the 256 x 256 tile kernel; M and N edges
-    are loaded clamped and must never be stored."""
+    """k-contiguous operands with K % 64 == 0 take the large-tile kernel (256 x 256, or
+    256 x 224 when N is a multiple of 224 and that fills the CUs better: the N = 448 and 3584
+    cases); M and N edges are loaded clamped and must never be stored."""
     print(f"gemm_nt M={M} N={N} K={K} {dtype}", flush=True)
     g = torch.Generator().manual_seed(M + 11 * N + K)
     a = torch.randn(M, K, generator=g).to(dtype)
@@ -98,9 +100,10 @@ def test_gemm_nt_large_tile_edges(M, N, K, dtype):
         assert torch.all(buf[:, :4] == 7) and torch.all(buf[:, N + 4:] == 7)
 
 
-def test_gemm_nt_bias_alpha_beta_large_tile():
-    g = torch.Generator().manual_seed(19)
-    M, N, K = 384, 320, 256
+@pytest.mark.parametrize("N", [320, 448])
+def test_gemm_nt_bias_alpha_beta_large_tile(N):
+    g = torch.Generator().manual_seed(19 + N)
+    M, K = 384, 256
     a = torch.randn(M, K, generator=g).to(torch.bfloat16)
     b = torch.randn(N, K, generator=g).to(torch.bfloat16)
     bias = torch.randn(N, generator=g).to(torch.bfloat16)
@@ -112,7 +115,7 @@ def test_gemm_nt_bias_alpha_beta_large_tile():
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 8192), (512, 1536, 30464), (4096, 512, 3584),
-                                   (100, 70, 4096)])
+                                   (100, 70, 4096), (256, 3584, 8192)])
 def test_gemm_split_k_matches_and_is_deterministic(M, N, K):
     """Small outputs with long K are split over K into an fp32 workspace and summed in split
     order: the result is within the fp32-accumulation bound and identical run to run."""
