@@ -55,7 +55,7 @@ _SIGNATURES = {
                           _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32,
                           _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64,
-                        _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr],
+                        _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_int,
                          _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_pack": [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_f32, _c_int, _c_ptr, _c_ptr, _c_ptr,

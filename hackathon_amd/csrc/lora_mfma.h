@@ -1,22 +1,25 @@
 // Internal interface of the rank-16 LoRA MFMA kernels (lora_mfma.hip). Not part of the
-// public C-ABI; the C-ABI entry points in lora.hip call these.
+// public C-ABI; the C-ABI entry points at the end of lora_mfma.hip call these.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// out[m, c] = alpha * sum_k X[m, k] Y[c, k] for c < 16, zeros for 16 <= c < out_cols.
-// K % 32 == 0; X, Y 16-B aligned with ldx, ldy multiples of 8. ws (fp32, may be null) lets
-// the K reduction split over more workgroups.
+// out[m, c] = alpha * sum_k X[m, k] Y[c, k] for c < 16, zeros for 16 <= c < out_cols, and
+// (out_t not null) the same 16 columns transposed into out_t [16, ldt >= M] in the input
+// dtype. K % 32 == 0; X, Y 16-B aligned with ldx, ldy multiples of 8. ws (fp32, may be null)
+// lets the K reduction split over more workgroups.
 int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* Y,
                  int64_t ldy, int64_t M, int64_t K, void* out, int64_t ldo, int out_cols,
-                 float alpha, float* ws, int64_t ws_floats, hipStream_t s);
+                 float alpha, void* out_t, int64_t ldt, float* ws, int64_t ws_floats,
+                 hipStream_t s);
 int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K);
 
-// out[n, c] = alpha * sum_m Q[m, n] P[m, c] for c < 16 (fp32 [N, 16], 16-B aligned).
-// N % 8 == 0; Q 16-B aligned with ldq a multiple of 8; P [M, ldp >= 16].
-// out_t = 1 stores out transposed, [16, N].
-int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64_t ldq,
+// out[n, c] = alpha * sum_m Q[m, n] PT[c, m] for c < 16 (fp32 [N, 16], 16-B aligned).
+// N % 8 == 0; Q 16-B aligned with ldq a multiple of 8; PT [16, ldpt >= M] (P transposed,
+// token-contiguous), 16-B aligned with ldpt a multiple of 8. out_t = 1 stores out
+// transposed, [16, N].
+int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
                   int64_t M, int64_t N, float* out, int out_t, float alpha, float* ws,
                   int64_t ws_floats, hipStream_t s);
 int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N);

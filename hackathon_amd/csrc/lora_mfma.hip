@@ -64,12 +64,27 @@ QL_DEV f32x4_t wave_reduce4(f32x4_t v, f32x4_t* red) {
 }
 
 // ---------------------------------------------------------------------------------------
+constexpr int kDownUnroll = 4;  // 128-k chunks per wave in flight (16 x 16-B loads per lane)
+constexpr int kDownWaves = 8;   // two waves per SIMD: twice the loads in flight per CU
+
+// Sum a per-lane f32x4 over the kDownWaves waves of the workgroup; valid in wave 0.
+QL_DEV f32x4_t wave_reduce_n(f32x4_t v, f32x4_t* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  red[wave * 64 + lane] = v;
+  __syncthreads();
+  f32x4_t s = red[lane];
+#pragma unroll
+  for (int w = 1; w < kDownWaves; ++w) s += red[w * 64 + lane];
+  return s;
+}
+
 template <int IT, int OT, bool PARTIAL>
-__global__ __launch_bounds__(kThreads) void lora_down_kernel(
+__global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
     int64_t M, int64_t K, int64_t k_per_split, float* __restrict__ ws,
-    typename Elem<OT>::T* __restrict__ out, int64_t ldo, int out_cols, float alpha) {
-  __shared__ f32x4_t red[4 * 64];
+    typename Elem<OT>::T* __restrict__ out, int64_t ldo, int out_cols, float alpha,
+    uint16_t* __restrict__ out_t, int64_t ldt) {
+  __shared__ f32x4_t red[kDownWaves * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t m0 = (int64_t)blockIdx.x * 16;
   const int64_t row = m0 + (lane & 15);
@@ -80,26 +95,50 @@ __global__ __launch_bounds__(kThreads) void lora_down_kernel(
   const uint16_t* xr = X + rowc * ldx;
   const uint16_t* yr = Y + (int64_t)(lane & 15) * ldy;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  for (int64_t k = kb + 128 * wave; k < ke; k += 512) {  // uniform per wave
-    // MFMA t takes k = k + 32 t + 8 (lane / 16) .. +7: each load instruction reads 64
-    // contiguous bytes of each of the 16 rows. K and every chunk start are multiples of 32,
-    // so a 32-k group is all in or all out; groups past the end contribute zeros (the MFMAs
-    // below must run with every lane's operands defined, so they are not placed under a
-    // lane-dependent branch).
-    uint4 xv[4], yv[4];
+  // Wave w takes the 128-k chunks w, w + 8, w + 16, ... (slots j = 0 .. J-1) of its K range,
+  // kDownUnroll at a time, starting at slot (blockIdx.x mod J): workgroups running at the
+  // same time then read different parts of Y, which every workgroup reads whole, instead of
+  // all asking the same L2 lines at once. MFMA t of a chunk takes k = chunk + 32 t +
+  // 8 (lane / 16) .. +7: each load instruction reads 64 contiguous bytes of each of the 16
+  // rows. K and every chunk start are multiples of 32, so a 32-k group is all in or all out;
+  // groups past the end load an in-range address and contribute zeros (the MFMAs below must
+  // run with every lane's operands defined, so nothing here is under a lane-dependent branch).
+  constexpr int64_t kStride = 128 * kDownWaves;
+  const int64_t J = (ke - kb + kStride - 1) / kStride;
+  const int64_t rot = J > 0 ? (int64_t)blockIdx.x % J : 0;
+  for (int64_t j0 = 0; j0 < J; j0 += kDownUnroll) {  // uniform per workgroup
+    uint4 xv[kDownUnroll][4], yv[kDownUnroll][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const bool ok = k + 32 * t < ke;
-      const int64_t kk = k + 32 * t + koff;
-      xv[t] = ok ? *reinterpret_cast<const uint4*>(xr + kk) : make_uint4(0, 0, 0, 0);
-      yv[t] = ok ? *reinterpret_cast<const uint4*>(yr + kk) : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < kDownUnroll; ++u) {
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      if (j0 + u >= J) {  // workgroup-uniform: no slot left, no loads
+#pragma unroll
+        for (int t = 0; t < 4; ++t) xv[u][t] = yv[u][t] = z;
+        continue;
+      }
+      int64_t js = j0 + u + rot;
+      js = js >= J ? js - J : js;
+      const int64_t c0 = kb + 128 * wave + kStride * js;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int64_t k = c0 + 32 * t;
+        const bool ok = k < ke;
+        const int64_t kk = (ok ? k : kb) + koff;
+        const uint4 xr4 = *reinterpret_cast<const uint4*>(xr + kk);
+        const uint4 yr4 = *reinterpret_cast<const uint4*>(yr + kk);
+        xv[u][t] = ok ? xr4 : z;
+        yv[u][t] = ok ? yr4 : z;
+      }
     }
-    acc0 = mfma<IT>(yv[0], xv[0], acc0);
-    acc1 = mfma<IT>(yv[1], xv[1], acc1);
-    acc0 = mfma<IT>(yv[2], xv[2], acc0);
-    acc1 = mfma<IT>(yv[3], xv[3], acc1);
+#pragma unroll
+    for (int u = 0; u < kDownUnroll; ++u) {
+      acc0 = mfma<IT>(yv[u][0], xv[u][0], acc0);
+      acc1 = mfma<IT>(yv[u][1], xv[u][1], acc1);
+      acc0 = mfma<IT>(yv[u][2], xv[u][2], acc0);
+      acc1 = mfma<IT>(yv[u][3], xv[u][3], acc1);
+    }
   }
-  const f32x4_t s = wave_reduce4(acc0 + acc1, red);
+  const f32x4_t s = wave_reduce_n(acc0 + acc1, red);
   if (wave != 0 || row >= M) return;
   // lane holds out[row][c .. c+3], c = 4 * (lane / 16)
   const int c = 4 * (lane >> 4);
@@ -114,13 +153,19 @@ __global__ __launch_bounds__(kThreads) void lora_down_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (z + e < out_cols) o[z + e] = Elem<OT>::from_f32(0.f);
+    if (out_t) {  // [16, M]: the 16 lanes of a row group write 32 contiguous bytes per c
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        out_t[(int64_t)(c + e) * ldt + row] = Elem<IT>::from_f32(alpha * s[e]);
+    }
   }
 }
 
-template <int OT>
+template <int IT, int OT>
 __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict__ ws, int splits,
                                                         int64_t M, typename Elem<OT>::T* __restrict__ out,
-                                                        int64_t ldo, int out_cols, float alpha) {
+                                                        int64_t ldo, int out_cols, float alpha,
+                                                        uint16_t* __restrict__ out_t, int64_t ldt) {
   const int64_t total = M * out_cols;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
@@ -130,6 +175,7 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
     if (c < kRank) {
       for (int z = 0; z < splits; ++z) v += ws[((int64_t)z * M + m) * kRank + c];
       v *= alpha;
+      if (out_t) out_t[(int64_t)c * ldt + m] = Elem<IT>::from_f32(v);
     }
     out[m * ldo + c] = Elem<OT>::from_f32(v);
   }
@@ -156,9 +202,28 @@ QL_DEV void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
   }
 }
 
+constexpr int kWgradUnroll = 4;  // 32-row chunks per wave in flight
+
+// Store 4 consecutive values (n, c .. c+3) of out [N, 16] (or of its transpose [16, N]).
+QL_DEV void store_wgrad4(float* __restrict__ out, bool out_t, int64_t N, int64_t n, int64_t c,
+                         float4 v) {
+  if (out_t) {
+    out[(c + 0) * N + n] = v.x;
+    out[(c + 1) * N + n] = v.y;
+    out[(c + 2) * N + n] = v.z;
+    out[(c + 3) * N + n] = v.w;
+  } else {
+    *reinterpret_cast<float4*>(out + n * kRank + c) = v;
+  }
+}
+
+// PARTIAL: each split writes its fp32 [N, 16] partial to ws[split]; lora_wgrad_reduce sums
+// them in split order. (Summing inside this launch by the last workgroup of each column block
+// needs device-scope release/acquire fences per workgroup, whose L2 write-back and invalidate
+// cost more than the separate reduce launch.)
 template <int IT, bool PARTIAL>
 __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
-    const uint16_t* __restrict__ P, int64_t ldp, const uint16_t* __restrict__ Q, int64_t ldq,
+    const uint16_t* __restrict__ PT, int64_t ldpt, const uint16_t* __restrict__ Q, int64_t ldq,
     int64_t M, int64_t N, int64_t m_per_split, float* __restrict__ ws, float* __restrict__ out,
     float alpha, bool out_t) {
   __shared__ f32x4_t red[4 * 64];
@@ -170,29 +235,43 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
   const bool col_ok = ncol < N;             // N % 8 == 0: a group is all in or all out
   const int64_t mb = (int64_t)blockIdx.y * m_per_split;
   const int64_t me = mb + m_per_split < M ? mb + m_per_split : M;
+  const uint16_t* ptr_c = PT + (int64_t)cg * ldpt;  // row cg of P^T: P[:, cg], m-contiguous
   f32x4_t acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int64_t m = mb + 32 * wave; m < me; m += 128) {
-    const int64_t r0 = m + 8 * mq;
-    uint4 q[8];
-    uint16_t pv[8];
+  for (int64_t m = mb + 32 * wave; m < me; m += 128 * kWgradUnroll) {  // uniform per wave
+    uint4 q[kWgradUnroll][8], pf[kWgradUnroll];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool ok = r0 + i < me;
-      const int64_t rc = ok ? r0 + i : mb;  // an in-range row; its values are dropped
-      q[i] = (ok && col_ok) ? *reinterpret_cast<const uint4*>(Q + rc * ldq + ncol)
-                            : make_uint4(0, 0, 0, 0);
-      pv[i] = ok ? P[rc * ldp + cg] : (uint16_t)0;
+    for (int u = 0; u < kWgradUnroll; ++u) {
+      const int64_t r0 = m + 128 * u + 8 * mq;
+      if (r0 + 8 <= me) {
+        pf[u] = *reinterpret_cast<const uint4*>(ptr_c + r0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          q[u][i] = col_ok ? *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncol)
+                           : make_uint4(0, 0, 0, 0);
+      } else {  // rows past the range contribute zeros
+        uint16_t pv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bool ok = r0 + i < me;
+          pv[i] = ok ? ptr_c[r0 + i] : (uint16_t)0;
+          q[u][i] = (ok && col_ok) ? *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncol)
+                                   : make_uint4(0, 0, 0, 0);
+        }
+        pf[u] = make_uint4((uint32_t)pv[0] | ((uint32_t)pv[1] << 16),
+                           (uint32_t)pv[2] | ((uint32_t)pv[3] << 16),
+                           (uint32_t)pv[4] | ((uint32_t)pv[5] << 16),
+                           (uint32_t)pv[6] | ((uint32_t)pv[7] << 16));
+      }
     }
-    const uint4 pf = make_uint4((uint32_t)pv[0] | ((uint32_t)pv[1] << 16),
-                                (uint32_t)pv[2] | ((uint32_t)pv[3] << 16),
-                                (uint32_t)pv[4] | ((uint32_t)pv[5] << 16),
-                                (uint32_t)pv[6] | ((uint32_t)pv[7] << 16));
-    uint4 qt[8];
-    transpose8x8(q, qt);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = mfma<IT>(pf, qt[t], acc[t]);
+    for (int u = 0; u < kWgradUnroll; ++u) {
+      uint4 qt[8];
+      transpose8x8(q[u], qt);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] = mfma<IT>(pf[u], qt[t], acc[t]);
+    }
   }
   // acc[t]: lane holds out[n = n0 + 8*(lane%16) + t][c = 4*(lane/16) .. +3]
   const int c = 4 * (lane >> 4);
@@ -204,27 +283,30 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
       if constexpr (PARTIAL) {
         *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * N + n) * kRank + c) =
             make_float4(s[0], s[1], s[2], s[3]);
-      } else if (out_t) {  // out [16, N]
-#pragma unroll
-        for (int e = 0; e < 4; ++e) out[(int64_t)(c + e) * N + n] = alpha * s[e];
       } else {
-        *reinterpret_cast<float4*>(out + n * kRank + c) =
-            make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]);
+        store_wgrad4(out, out_t, N, n, c,
+                     make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]));
       }
     }
   }
 }
 
+// out = alpha * sum over splits of ws[split] ([N, 16] fp32 each), in split order; one thread
+// per 4 consecutive values. splits = 0 writes zeros.
 __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
                                                          int64_t N, float* __restrict__ out,
                                                          float alpha, bool out_t) {
-  const int64_t total = N * kRank;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+  const int64_t total4 = N * kRank / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total4;
        i += (int64_t)gridDim.x * 256) {
-    float v = 0.f;
-    for (int z = 0; z < splits; ++z) v += ws[(int64_t)z * total + i];
-    const int64_t n = i / kRank, c = i - n * kRank;
-    out[out_t ? c * N + n : i] = alpha * v;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < splits; ++z) {
+      const float4 w = reinterpret_cast<const float4*>(ws + (int64_t)z * N * kRank)[i];
+      v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+    }
+    const int64_t n = (4 * i) / kRank, c = 4 * i - n * kRank;
+    store_wgrad4(out, out_t, N, n, c, make_float4(alpha * v.x, alpha * v.y, alpha * v.z,
+                                                  alpha * v.w));
   }
 }
 
@@ -283,10 +365,12 @@ unsigned grid1d(int64_t n) {
 
 // ---- host side -------------------------------------------------------------------------
 
+// Split K only while there are fewer than 256 row groups (one workgroup per CU is enough to
+// stream X at full bandwidth with kDownUnroll chunks in flight per wave).
 int ql_lora_down_splits(int64_t M, int64_t K) {
   const int64_t groups = (M + 15) / 16;
   int s = 1;
-  while (groups * s < 1024 && K / (512 * 2 * s) >= 1 && s < 64) s *= 2;
+  while (groups * s < 256 && K / (128 * kDownWaves * 2 * s) >= 1 && s < 64) s *= 2;
   return s;
 }
 
@@ -297,30 +381,35 @@ int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K) {
 
 int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* Y,
                  int64_t ldy, int64_t M, int64_t K, void* out, int64_t ldo, int out_cols,
-                 float alpha, float* ws, int64_t ws_floats, hipStream_t s) {
+                 float alpha, void* out_t, int64_t ldt, float* ws, int64_t ws_floats,
+                 hipStream_t s) {
   if (M <= 0 || K <= 0 || K % 32 || out_cols < kRank || ldo < out_cols) return QL_EINVAL;
+  if (out_t && ldt < M) return QL_EINVAL;
   if (ldx % 8 || ldy % 8 || !ql_aligned(X, 16) || !ql_aligned(Y, 16)) return QL_EALIGN;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   if (out_dtype != QL_BF16 && out_dtype != QL_F16 && out_dtype != QL_F32) return QL_EDTYPE;
   int splits = ql_lora_down_splits(M, K);
   if (ws_floats < (int64_t)splits * M * kRank || !ws) splits = 1;
-  // per-split K range: a multiple of 512 (4 waves x 128 k)
-  int64_t kps = ((K + splits - 1) / splits + 511) / 512 * 512;
+  // per-split K range: a multiple of 128 k per wave
+  constexpr int64_t kq = 128 * kDownWaves;
+  int64_t kps = ((K + splits - 1) / splits + kq - 1) / kq * kq;
   splits = (int)((K + kps - 1) / kps);
   const dim3 grid((unsigned)((M + 15) / 16), (unsigned)splits);
 #define QL_DOWN(IT, OT)                                                                      \
   do {                                                                                       \
     using T = typename Elem<OT>::T;                                                          \
     if (splits == 1) {                                                                       \
-      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false>), grid, dim3(kThreads), 0, s,      \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false>), grid, dim3(64 * kDownWaves), 0, s, \
                          (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,        \
-                         (float*)nullptr, (T*)out, ldo, out_cols, alpha);                    \
+                         (float*)nullptr, (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t,   \
+                         ldt);                                                               \
     } else {                                                                                 \
-      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true>), grid, dim3(kThreads), 0, s,       \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true>), grid, dim3(64 * kDownWaves), 0, s,  \
                          (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps, ws,    \
-                         (T*)out, ldo, out_cols, alpha);                                     \
-      hipLaunchKernelGGL((lora_down_reduce<OT>), dim3(grid1d(M * out_cols)), dim3(256), 0,   \
-                         s, ws, splits, M, (T*)out, ldo, out_cols, alpha);                   \
+                         (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);              \
+      hipLaunchKernelGGL((lora_down_reduce<IT, OT>), dim3(grid1d(M * out_cols)), dim3(256),  \
+                         0, s, ws, splits, M, (T*)out, ldo, out_cols, alpha,                 \
+                         (uint16_t*)out_t, ldt);                                             \
     }                                                                                        \
   } while (0)
   if (in_dtype == QL_BF16) {
@@ -336,10 +425,12 @@ int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const 
   return ql_launch_status();
 }
 
+// Split the token range until there are at least 256 workgroups, keeping at least one
+// 32-row chunk per wave in each split.
 int ql_lora_wgrad_splits(int64_t M, int64_t N) {
   const int64_t blocks = (N + 127) / 128;
   int s = 1;
-  while (blocks * s < 512 && M / (128 * 2 * s) >= 1 && s < 64) s *= 2;
+  while (blocks * s < 256 && M / (128 * 2 * s) >= 1 && s < 64) s *= 2;
   return s;
 }
 
@@ -348,11 +439,12 @@ int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N) {
   return s > 1 ? (int64_t)s * N * kRank : 0;
 }
 
-int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64_t ldq,
+int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
                   int64_t M, int64_t N, float* out, int out_t, float alpha, float* ws,
                   int64_t ws_floats, hipStream_t s) {
-  if (M <= 0 || N <= 0 || N % 8 || ldp < kRank) return QL_EINVAL;
-  if (ldq % 8 || !ql_aligned(Q, 16) || !ql_aligned(P, 2) || !ql_aligned(out, 16)) return QL_EALIGN;
+  if (M <= 0 || N <= 0 || N % 8 || ldpt < M) return QL_EINVAL;
+  if (ldq % 8 || ldpt % 8 || !ql_aligned(Q, 16) || !ql_aligned(PT, 16) || !ql_aligned(out, 16))
+    return QL_EALIGN;
   if (out_t != 0 && out_t != 1) return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   int splits = ql_lora_wgrad_splits(M, N);
@@ -364,11 +456,11 @@ int ql_lora_wgrad(int in_dtype, const void* P, int64_t ldp, const void* Q, int64
   do {                                                                                       \
     if (splits == 1) {                                                                       \
       hipLaunchKernelGGL((lora_wgrad_kernel<IT, false>), grid, dim3(kThreads), 0, s,         \
-                         (const uint16_t*)P, ldp, (const uint16_t*)Q, ldq, M, N, mps,        \
+                         (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps,      \
                          (float*)nullptr, out, alpha, out_t);                                \
     } else {                                                                                 \
       hipLaunchKernelGGL((lora_wgrad_kernel<IT, true>), grid, dim3(kThreads), 0, s,          \
-                         (const uint16_t*)P, ldp, (const uint16_t*)Q, ldq, M, N, mps, ws,    \
+                         (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,  \
                          out, alpha, out_t);                                                 \
       hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0, s, ws,    \
                          splits, N, out, alpha, out_t);                                      \
@@ -389,14 +481,16 @@ extern "C" int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K) {
 
 extern "C" int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_t ldy, int64_t M,
                                int64_t K, int in_dtype, void* out, int64_t ldo, int out_cols,
-                               int out_dtype, float alpha, void* workspace,
-                               int64_t workspace_bytes, ql_stream_t stream) {
+                               int out_dtype, float alpha, void* out_t, int64_t ldt,
+                               void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
   if (M < 0 || K < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (M == 0) return QL_OK;
   if (!X || !Y || !out) return QL_EINVAL;
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  if (out_t && !ql_aligned(out_t, 2)) return QL_EALIGN;
   return ql_lora_down(in_dtype, out_dtype, X, ldx, Y, ldy, M, K, out, ldo, out_cols, alpha,
-                      static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
+                      out_t, ldt, static_cast<float*>(workspace),
+                      workspace_bytes / (int64_t)sizeof(float),
                       static_cast<hipStream_t>(stream));
 }
 
@@ -405,13 +499,13 @@ extern "C" int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N) {
   return ql_lora_wgrad_workspace_floats(M, N) * (int64_t)sizeof(float);
 }
 
-extern "C" int qlora_lora_wgrad(const void* P, int64_t ldp, const void* Q, int64_t ldq, int64_t M,
+extern "C" int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M,
                                 int64_t N, int in_dtype, float* out, int out_transposed,
                                 float alpha, void* workspace, int64_t workspace_bytes,
                                 ql_stream_t stream) {
   if (M < 0 || N < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (N == 0) return QL_OK;
-  if (!P || !Q || !out) return QL_EINVAL;
+  if (!PT || !Q || !out) return QL_EINVAL;
   if (M == 0) {  // an empty reduction: zeros (a fill kernel, not a memset node)
     hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), (const float*)nullptr, 0, N,
@@ -419,7 +513,7 @@ extern "C" int qlora_lora_wgrad(const void* P, int64_t ldp, const void* Q, int64
     return ql_launch_status();
   }
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
-  return ql_lora_wgrad(in_dtype, P, ldp, Q, ldq, M, N, out, out_transposed, alpha,
+  return ql_lora_wgrad(in_dtype, PT, ldpt, Q, ldq, M, N, out, out_transposed, alpha,
                        static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
                        static_cast<hipStream_t>(stream));
 }

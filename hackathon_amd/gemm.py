@@ -131,24 +131,33 @@ def gemm_nt_cat(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None,
     return out
 
 
-def lora_down(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
-    """out[:, :16] = alpha * x @ y^T (y [16, K]) and out[:, 16:] = 0 (qlora_lora_down)."""
+def lora_down(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, alpha: float = 1.0,
+              out_t: torch.Tensor | None = None) -> torch.Tensor:
+    """out[:, :16] = alpha * x @ y^T (y [16, K]) and out[:, 16:] = 0 (qlora_lora_down); with
+    `out_t` ([16, >= M], x's dtype) also the 16 columns transposed, the operand lora_wgrad
+    takes."""
     M, K = x.shape
     ws, ws_bytes = _lib.workspace("qlora_lora_down_workspace_size", M, K, device=x.device)
     _lib.call("qlora_lora_down", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), M, K,
               _lib.tag(x.dtype), out.data_ptr(), out.stride(0), out.shape[1], _lib.tag(out.dtype),
-              float(alpha), _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+              float(alpha), _lib.ptr(out_t), out_t.stride(0) if out_t is not None else 0,
+              _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
     return out
 
 
-def lora_wgrad(p: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
+def lora_t_buffer(m: int, dtype, device) -> torch.Tensor:
+    """A [16, m] buffer for lora_down's transposed output (row stride a multiple of 8)."""
+    return torch.empty((16, (m + 7) // 8 * 8), dtype=dtype, device=device)[:, :m]
+
+
+def lora_wgrad(pt: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
                transposed: bool = False) -> torch.Tensor:
-    """fp32 alpha * q^T @ p[:, :16] for q [M, N], p [M, >=16] (qlora_lora_wgrad): [N, 16], or
-    [16, N] when `transposed`."""
+    """fp32 alpha * q^T @ pt^T for q [M, N] and pt [16, M] (token-contiguous, as lora_down's
+    `out_t`) (qlora_lora_wgrad): [N, 16], or [16, N] when `transposed`."""
     M, N = q.shape
     out = torch.empty((16, N) if transposed else (N, 16), dtype=torch.float32, device=q.device)
     ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_workspace_size", M, N, device=q.device)
-    _lib.call("qlora_lora_wgrad", p.data_ptr(), p.stride(0), q.data_ptr(), q.stride(0), M, N,
+    _lib.call("qlora_lora_wgrad", pt.data_ptr(), pt.stride(0), q.data_ptr(), q.stride(0), M, N,
               _lib.tag(q.dtype), out.data_ptr(), int(transposed), float(alpha), _lib.ptr(ws),
               ws_bytes, _lib.stream_of(q))
     return out

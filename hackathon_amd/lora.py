@@ -161,11 +161,12 @@ class LoraNF4Linear(torch.autograd.Function):
         a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
         w = nf4.dequantize_nf4(packed, quant_state, dt)
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
-        _gemm.lora_down(x2, a16, u)
+        ut = _gemm.lora_t_buffer(M, dt, x2.device)                     # u^T, for dB
+        _gemm.lora_down(x2, a16, u, out_t=ut)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
         _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=None if bias is None else bias.to(dt))
-        del w
-        ctx.save_for_backward(x2, u, at, bt)
+        del w, u
+        ctx.save_for_backward(x2, ut, at, bt)
         ctx.packed, ctx.quant_state, ctx.scaling = packed, quant_state, float(scaling)
         ctx.shape, ctx.wdtypes = x.shape, (a_weight.dtype, b_weight.dtype)
         return y.view(*x.shape[:-1], N)
@@ -174,7 +175,7 @@ class LoraNF4Linear(torch.autograd.Function):
     def backward(ctx, g):
         from . import nf4
 
-        x2, u, at, bt = ctx.saved_tensors
+        x2, ut, at, bt = ctx.saved_tensors
         dt = x2.dtype
         M, K = x2.shape
         g2 = _rows(g)
@@ -183,7 +184,8 @@ class LoraNF4Linear(torch.autograd.Function):
         g2 = g2.contiguous()
         s = ctx.scaling
         du = torch.empty((M, _PAD), dtype=dt, device=g2.device)
-        _gemm.lora_down(g2, bt, du, alpha=s)                            # du = s g B
+        dut = _gemm.lora_t_buffer(M, dt, g2.device)
+        _gemm.lora_down(g2, bt, du, alpha=s, out_t=dut)                 # du = s g B
         dx = da = db = None
         if ctx.needs_input_grad[0]:
             wt = nf4.dequantize_nf4_t(ctx.packed, ctx.quant_state, dt)  # [K, N]
@@ -192,11 +194,11 @@ class LoraNF4Linear(torch.autograd.Function):
             del wt
             dx = dx.view(ctx.shape)
         if ctx.needs_input_grad[1]:
-            da = _gemm.lora_wgrad(du, x2, transposed=True)              # [16, K] = du^T x
+            da = _gemm.lora_wgrad(dut, x2, transposed=True)             # [16, K] = du^T x
             if da.dtype != ctx.wdtypes[0]:
                 da = da.to(ctx.wdtypes[0])
         if ctx.needs_input_grad[2]:
-            db = _gemm.lora_wgrad(u, g2, alpha=s)                      # [N, 16] = s g^T u
+            db = _gemm.lora_wgrad(ut, g2, alpha=s)                     # [N, 16] = s g^T u
             if db.dtype != ctx.wdtypes[1]:
                 db = db.to(ctx.wdtypes[1])
         return dx, da, db, None, None, None, None

@@ -180,33 +180,47 @@ def test_gemm_nt_cat(M, N, K, K2):
 
 
 @pytest.mark.parametrize("M,K,out_cols", [(4096, 3584, 64), (4096, 18944, 64), (77, 96, 16),
-                                          (1000, 512, 40)])
+                                          (1000, 512, 40), (512, 8192, 64)])
 def test_lora_down(M, K, out_cols):
-    """out[:, :16] = alpha x y^T, out[:, 16:] = 0, with and without the split-K workspace."""
+    """out[:, :16] = alpha x y^T, out[:, 16:] = 0 and the transposed copy equal to out[:, :16]
+    bit for bit, with and without the split-K workspace (512 x 8192 splits)."""
     print(f"lora_down M={M} K={K}", flush=True)
     g = torch.Generator().manual_seed(M + K)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
     y = (torch.randn(16, K, generator=g) * 0.25).to(torch.bfloat16)
     ref = 2.0 * (x.double() @ y.double().t())
     out = torch.full((M, out_cols), 3.0, dtype=torch.bfloat16, device="cuda")
-    gemm.lora_down(x.cuda(), y.cuda(), out, alpha=2.0)
+    out_t = gemm.lora_t_buffer(M, torch.bfloat16, "cuda")
+    gemm.lora_down(x.cuda(), y.cuda(), out, alpha=2.0, out_t=out_t)
     bound = 2 * 4 * 2.0**-22 * K * x.abs().max().item() * y.abs().max().item() + 2.0**-8 * ref.abs()
     assert torch.all((out[:, :16].double().cpu() - ref).abs() <= bound)
     assert torch.all(out[:, 16:] == 0)
+    assert torch.equal(out_t, out[:, :16].t())
 
 
-@pytest.mark.parametrize("M,N", [(4096, 18944), (4096, 512), (100, 520), (33, 8)])
+def _pt(M, g):
+    """A [16, M] token-contiguous operand with a padded row stride, as lora_down writes it."""
+    buf = torch.randn(16, (M + 7) // 8 * 8 + 8, generator=g).to(torch.bfloat16)
+    return buf[:, :M]
+
+
+@pytest.mark.parametrize("M,N", [(4096, 18944), (4096, 3584), (4096, 512), (1000, 3584),
+                                 (100, 520), (33, 8)])
 def test_lora_wgrad(M, N):
-    """fp32 [N, 16] = alpha q^T p[:, :16] (a reduction over rows), p with a padded row stride."""
+    """fp32 [N, 16] = alpha q^T pt^T (a reduction over the M token rows, split over workgroups
+    and summed in split order); ragged M exercises the partial 8-row groups."""
     print(f"lora_wgrad M={M} N={N}", flush=True)
     g = torch.Generator().manual_seed(M * 3 + N)
     q = torch.randn(M, N, generator=g).to(torch.bfloat16)
-    p = torch.randn(M, 64, generator=g).to(torch.bfloat16)
-    ref = 0.5 * (q.double().t() @ p[:, :16].double())
-    out = gemm.lora_wgrad(p.cuda(), q.cuda(), alpha=0.5)
+    pt = _pt(M, g)
+    ref = 0.5 * (q.double().t() @ pt.double().t())
+    pt_dev = gemm.lora_t_buffer(M, torch.bfloat16, "cuda")  # row stride a multiple of 8
+    pt_dev.copy_(pt)
+    out = gemm.lora_wgrad(pt_dev, q.cuda(), alpha=0.5)
     assert out.shape == (N, 16) and out.dtype == torch.float32
-    bound = 0.5 * 4 * 2.0**-22 * M * q.abs().max().item() * p.abs().max().item()
+    bound = 0.5 * 4 * 2.0**-22 * M * q.abs().max().item() * pt.abs().max().item()
     assert torch.all((out.double().cpu() - ref).abs() <= bound)
+    assert torch.equal(out, gemm.lora_wgrad(pt_dev, q.cuda(), alpha=0.5))  # deterministic
 
 
 @pytest.mark.parametrize("K,N", [(3584, 512), (256, 18944), (8, 8)])
@@ -226,5 +240,6 @@ def test_lora_pack_is_exact(K, N):
 def test_lora_wgrad_transposed_output(M, N):
     g = torch.Generator().manual_seed(N)
     q = torch.randn(M, N, generator=g).to(torch.bfloat16).cuda()
-    p = torch.randn(M, 64, generator=g).to(torch.bfloat16).cuda()
-    assert torch.equal(gemm.lora_wgrad(p, q, transposed=True), gemm.lora_wgrad(p, q).t())
+    pt = gemm.lora_t_buffer(M, torch.bfloat16, "cuda")
+    pt.copy_(torch.randn(16, M, generator=g).to(torch.bfloat16))
+    assert torch.equal(gemm.lora_wgrad(pt, q, transposed=True), gemm.lora_wgrad(pt, q).t())
