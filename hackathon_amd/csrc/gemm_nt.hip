@@ -345,13 +345,17 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
   return ql_launch_status();
 }
 
-// Tile width for an M x N output: 224 (NJ = 7) when N is a multiple of 224 and the narrower
-// tiles take fewer (waves x tile width) on 256 CUs, else 256. The 4096 x 3584 outputs of the
-// 7B step are 224 tiles of 256 x 256 (one partial wave) but exactly 256 tiles of 256 x 224.
+// Tile width for an M x N output: 224 (NJ = 7) when N is a multiple of 224, the output is
+// large enough to run without split-K (>= 128 tiles of 256 x 256) and the narrower tiles take
+// fewer (waves x tile width) on 256 CUs, else 256. The 4096 x 3584 outputs of the 7B step are
+// 224 tiles of 256 x 256 (one partial wave) but exactly 256 tiles of 256 x 224. Small outputs
+// are split over K instead, where narrower tiles only add operand traffic.
 int choose_nj(int64_t M, int64_t N) {
   if (N % 224) return 8;
   const int64_t tm = (M + BM - 1) / BM;
-  const int64_t w8 = (tm * ((N + 255) / 256) + 255) / 256;
+  const int64_t t8 = tm * ((N + 255) / 256);
+  if (t8 < 128) return 8;
+  const int64_t w8 = (t8 + 255) / 256;
   const int64_t w7 = (tm * (N / 224) + 255) / 256;
   return w7 * 7 < w8 * 8 ? 7 : 8;
 }
