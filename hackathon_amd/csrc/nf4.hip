@@ -156,13 +156,16 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_scalar(
 // Transposed dequantisation: outT[k][n] = W[n][k] for W [rows, cols] (row-major, packed two
 // per byte along k). The backward of the 4-bit linear needs dY @ W; with W^T stored [cols,
 // rows] that contraction is k-contiguous on both operands. One workgroup per tile of 64 rows
-// (n) x 128 columns (k): thread t dequantises 16 consecutive k of the rows 2p and 2p+1
-// (p = t % 32, k-chunk t / 32), packs each (n, n+1) pair into one 32-bit LDS word of the
-// [k][n] tile, and the tile leaves as 128 rows of 64 n = 128 contiguous bytes each, written
-// with nontemporal 16-B stores (8 lanes per row). Same per-weight arithmetic as above, so
-// outT is bit-identical to the transpose of the plain dequantisation.
+// (n) x 128 columns (k). The packed tile (64 rows x 64 B) comes in with one coalesced 16-B
+// load per thread (4 lanes per row) into LDS rows of 17 words (an odd stride: the row reads
+// below meet distinct banks). Thread t then dequantises 16 consecutive k of the rows 2p and
+// 2p+1 (p = t % 32, k-chunk t / 32), packs each (n, n+1) pair into one 32-bit LDS word of
+// the [k][n] tile, and the tile leaves as 128 rows of 64 n = 128 contiguous bytes each,
+// written with nontemporal 16-B stores (8 lanes per row). Same per-weight arithmetic as
+// above, so outT is bit-identical to the transpose of the plain dequantisation.
 constexpr int kTRows = 64, kTCols = 128;
 constexpr int kTStride = 36;  // LDS words per k-row of the tile (32 used, 16-B aligned rows)
+constexpr int kTInStride = 17;  // LDS words per packed input row (16 used)
 
 template <int OUT_DT, bool NESTED>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
@@ -175,12 +178,23 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
   __shared__ float table[16];
   __shared__ float code2_lds[NESTED ? 256 : 1];
   __shared__ __attribute__((aligned(16))) uint32_t tile[kTCols * kTStride];
+  __shared__ uint32_t tile_in[kTRows * kTInStride];
+  // n-tiles vary fastest: workgroups running together write adjacent 128-B pieces of the same
+  // output rows (whole DRAM pages) instead of one piece each of many rows
+  const int64_t n0 = (int64_t)blockIdx.x * kTRows;
+  const int64_t k0 = (int64_t)blockIdx.y * kTCols;
+  {  // packed input: thread t loads 16 B of row t / 4 (chunk t % 4)
+    const int r = threadIdx.x >> 2, c = threadIdx.x & 3;
+    if (n0 + r < rows) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(packed + ((n0 + r) * cols + k0) / 2 + 16 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tile_in[r * kTInStride + 4 * c + e] = v[e];
+    }
+  }
   if (threadIdx.x < 16) table[threadIdx.x] = nf4_table[threadIdx.x];
   if constexpr (NESTED) code2_lds[threadIdx.x] = code2[threadIdx.x];  // kThreads == 256
   __syncthreads();
 
-  const int64_t k0 = (int64_t)blockIdx.x * kTCols;
-  const int64_t n0 = (int64_t)blockIdx.y * kTRows;
   const int p = threadIdx.x & 31, kc = threadIdx.x >> 5;
   const int64_t k = k0 + 16 * kc;
   float w[2][16];
@@ -189,7 +203,8 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
     const int64_t n = n0 + 2 * p + h;
     if (n < rows) {
       const int64_t j = n * cols + k;  // first weight index; j % 16 == 0
-      const uint2 b = *reinterpret_cast<const uint2*>(packed + j / 2);
+      const uint32_t* src = tile_in + (2 * p + h) * kTInStride + 2 * kc;
+      const uint2 b = make_uint2(src[0], src[1]);
       const float s =
           block_scale<NESTED>(j >> log2_bs, absmax_q, absmax_f, code2_lds, absmax2, offset, log2_bs2);
       const uint32_t bw[2] = {b.x, b.y};
@@ -303,9 +318,10 @@ extern "C" int qlora_nf4_dequant_t(const uint8_t* packed, int64_t rows, int64_t 
   if (lbs < 4) return QL_EINVAL;  // a power of two >= 16
   if (nested && (!code2 || !absmax2 || ilog2_exact(blocksize2) < 0)) return QL_EINVAL;
   if (cols % kTCols || rows % 8 || ld_out % 8) return QL_ESHAPE;
-  if (!ql_aligned(packed, 8) || !ql_aligned(out_t, 16)) return QL_EALIGN;
+  if (!ql_aligned(packed, 16) || !ql_aligned(out_t, 16)) return QL_EALIGN;
   const int lbs2 = nested ? ilog2_exact(blocksize2) : 0;
-  const dim3 grid((unsigned)(cols / kTCols), (unsigned)((rows + kTRows - 1) / kTRows));
+  if ((rows + kTRows - 1) / kTRows > INT32_MAX || cols / kTCols > 65535) return QL_ESHAPE;
+  const dim3 grid((unsigned)((rows + kTRows - 1) / kTRows), (unsigned)(cols / kTCols));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* aq = nested ? static_cast<const uint8_t*>(absmax) : nullptr;
   const float* af = nested ? nullptr : static_cast<const float*>(absmax);

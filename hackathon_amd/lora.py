@@ -223,7 +223,7 @@ def _fused_base(layer, adapter, x, compute_dtype, p):
     out_f, in_f = (int(d) for d in qs.shape)
     if a_w.shape != (16, in_f) or b_w.shape != (out_f, 16):
         return None
-    if in_f % 128 or out_f % 64 or not nf4.transposed_dequant_ok(qs):
+    if in_f % 128 or out_f % 64 or not nf4.transposed_dequant_ok(qs, weight):
         return None
     if not (a_w.is_cuda and b_w.is_cuda):
         return None

@@ -111,9 +111,12 @@ def dequantize_nf4_t(packed, quant_state, dtype=torch.bfloat16, out=None):
     return out
 
 
-def transposed_dequant_ok(quant_state):
+def transposed_dequant_ok(quant_state, packed=None):
     """Whether dequantize_nf4_t takes this weight: in_features % 128 == 0,
-    out_features % 8 == 0, blocksize a power of two >= 16."""
+    out_features % 8 == 0, blocksize a power of two >= 16 (and, when given, the packed codes
+    16-B aligned)."""
+    if packed is not None and packed.data_ptr() % 16:
+        return False
     rows, cols = tuple(quant_state.shape)
     bs = int(quant_state.blocksize)
     ok = cols % 128 == 0 and rows % 8 == 0 and bs >= 16 and bs & (bs - 1) == 0
@@ -140,8 +143,8 @@ class NF4Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             qs = ctx.quant_state
             rows = tuple(qs.shape)[0]
-            if grad_out.dtype in (torch.bfloat16, torch.float16) and transposed_dequant_ok(qs) \
-                    and rows % 64 == 0:
+            if grad_out.dtype in (torch.bfloat16, torch.float16) \
+                    and transposed_dequant_ok(qs, ctx.packed) and rows % 64 == 0:
                 # dY @ W as an NT GEMM against W^T, dequantised straight into that layout
                 weight_t = dequantize_nf4_t(ctx.packed, qs, grad_out.dtype)
                 grad_x = _gemm.linear(grad_out, weight_t)

@@ -247,7 +247,7 @@ int qlora_gemm_ws(int a_km, int b_kn, int64_t M, int64_t N, int64_t K, const voi
  * runs as a k-contiguous GEMM against W^T.
  * Replaces: solution/nf4.py:25-49 + :110 (the re-dequantisation in NF4Linear.backward).
  * Requires cols % 128 == 0, rows % 8 == 0, ld_out % 8 == 0, blocksize a power of two >= 16
- * (blocksize2 a power of two when nested), packed 8-B and out_t 16-B aligned (else
+ * (blocksize2 a power of two when nested), packed and out_t 16-B aligned (else
  * QL_ESHAPE / QL_EINVAL / QL_EALIGN); out_dtype QL_BF16 or QL_F16.
  */
 int qlora_nf4_dequant_t(const uint8_t* packed, int64_t rows, int64_t cols, const void* absmax,
