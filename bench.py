@@ -398,6 +398,10 @@ def main():
     if args.nf4_only:
         print(json.dumps(line), flush=True)
         return
+    hp = hbm_practical(torch)
+    hp["dequant_frac_of_write"] = round(r["gbs"] / hp["write_fill_gbs"], 4)
+    line["hbm_practical"] = hp
+    log(f"[bench] HBM practical: {json.dumps(hp)}")
     r1 = bench_nf4(torch, (4864, 896), max(args.steps, 200), args.warmup, 32, seed=1)
     line["nf4_4864x896"] = dict(us=round(r1["sec_per_call"] * 1e6, 3), gbs=round(r1["gbs"], 1),
                                 frac_hbm=round(r1["gbs"] / HBM_PEAK_GBS, 4),
@@ -412,6 +416,33 @@ def main():
     line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     line["cpu_baseline"]["host_cpu"] = _cpu_model()
     print(json.dumps(line), flush=True)
+
+
+def hbm_practical(torch, mib=1024, reps=20):
+    """The box's practical HBM rates for the same kind of traffic, measured beside the
+    dequant: a 1 GiB fill (pure write, the dequant's 79% share) and a 1 GiB device copy
+    (read + write), HIP events on the current stream."""
+    n = mib * 2**20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    write = n / timed(lambda: b.fill_(7)) / 1e9
+    copy = 2 * n / timed(lambda: b.copy_(a)) / 1e9
+    del a, b
+    return {"write_fill_gbs": round(write, 1), "copy_rw_gbs": round(copy, 1),
+            "buffer_mib": mib}
 
 
 def pmc_probe(torch, shape, sets=4, launches=8):
