@@ -9,26 +9,32 @@
 // dz @ W with the head weight transposed (solution/cross_entropy.py:123).
 //
 // Tiling for gfx950 (256 CUs in 8 XCDs, wave64, 160 KiB LDS per CU, 512 VGPRs per lane):
-//   - workgroup tile 256 x 256 x 64, 256 threads = 4 waves in a 2 x 2 grid; each wave owns a
-//     128 x 128 block of C as 8 x 8 v_mfma_f32_16x16x32 accumulators (256 fp32 per lane, held
-//     in AGPRs), so every 16-B fragment read from LDS feeds 8 MFMAs;
+//   - workgroup tile 256 x BN x 64 with BN = 256 or 224, 256 threads = 4 waves, one workgroup
+//     per CU. The products are v_mfma_f32_32x32x16: a single wave per SIMD issues them at the
+//     full matrix-core rate (one per 32 cycles), where it can only issue the 16x16x32 form
+//     about once per 25 cycles instead of 16. Each wave owns BI x BJ blocks of 32 x 32 (16 fp32
+//     per lane each, in AGPRs): 256 wide as 2 x 2 waves of 4 x 4 blocks, 224 wide as 4 x 1
+//     waves of 2 x 7 blocks;
 //   - operands go global -> LDS with global_load_lds_dwordx4 (no VGPR staging, no ds_write):
 //     each wave instruction fills 1 KiB of LDS = 8 rows of 64 k. Rows are 128 B with the
 //     16-B chunks XOR-swizzled by (row & 7), so both the DMA writes and the fragment reads
-//     (ds_read_b128, 8 rows x 16 B per phase) hit all 32 banks once;
-//   - two LDS stages (2 x 64 KiB), software-pipelined across K steps: each step multiplies
-//     the first 32-k half of its stage while reading the second half's fragments, meets the
-//     other waves at the one barrier of the step, starts the DMA of step k+2 into the stage
-//     just consumed, and multiplies the second half while reading the first-half fragments
-//     of step k+1 (scheduling barriers keep that instruction order). Fragment reads are
-//     never exposed at a step boundary and the DMA has a full step to land;
+//     (ds_read_b128 of 32 rows x 16 B, 8 rows per phase) hit all 32 banks once;
+//   - two LDS stages, software-pipelined across K steps: each step multiplies the first 32-k
+//     half of its stage while reading the second half's fragments, meets the other waves at
+//     the one barrier of the step, starts the DMA of step k+2 into the stage just consumed
+//     (each load placed behind one MFMA, first thing after the barrier, so it has the most
+//     time to land) and multiplies the second half while reading the first-half fragments of
+//     step k+1. Scheduling barriers keep that instruction order;
 //   - workgroup ids are remapped so that the tiles one XCD runs at a time are neighbours
 //     (XCDs take workgroups round-robin; each has its own L2), then rastered in groups of 4
 //     tile rows so that concurrently running tiles share A and B panels in L2;
-//   - a second K segment C += A2 B2^T (K2 % 64 == 0, same M and N) can follow the first:
-//     the rank-16 LoRA term of a LoRA linear rides along as one extra K step of the base
-//     GEMM (x W^T + u (sB)^T with u, sB zero-padded to 64 columns) instead of separate
-//     skinny GEMMs and an elementwise add;
+//   - a second K segment C += A2 B2^T (K2 % 64 == 0, at most 128 columns, same M and N) can
+//     join the first: the rank-16 LoRA term of a LoRA linear rides along as one extra K step
+//     of the base GEMM (x W^T + u (sB)^T with u, sB zero-padded to 64 columns) instead of
+//     separate skinny GEMMs and an elementwise add. Its steps come first, loaded by the
+//     prologue, so every load inside the K loop is a step of the first segment; for operands
+//     with a multiple of 8 rows those loads use addresses built once per tile (Panel), and a
+//     step only adds its k offset;
 //   - split-K: blockIdx.y selects a K range; each split writes an fp32 partial tile to a
 //     caller-provided workspace and `splitk_reduce` sums the partials in split order
 //     (deterministic) and applies alpha / beta / bias / the output type.
@@ -43,29 +49,38 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
 constexpr int BM = 256, BK = 64;
-// Tile width: NJ 16-column fragments per wave, 2 waves across N (NJ = 8: 256; NJ = 7: 224).
-template <int NJ> constexpr int bn_of() { return 32 * NJ; }
 constexpr int kThreads = 256;
-constexpr int kRowBytes = BK * 2;                  // 128 B: one tile row of 64 k
-constexpr int kTileBytes = 256 * kRowBytes;        // 32 KiB: one operand, one stage
-constexpr int kStageBytes = 2 * kTileBytes;        // A + B
+constexpr int kRowBytes = BK * 2;              // 128 B: one tile row of 64 k
+constexpr int kATileBytes = BM * kRowBytes;    // 32 KiB: the A operand, one stage
 constexpr int kGroupM = 4;
+constexpr int kPrologueSteps = 2;              // the second K segment fits in the prologue
 
-template <int DT> QL_DEV f32x4_t mfma(const uint4& a, const uint4& b, f32x4_t c);
-template <> QL_DEV f32x4_t mfma<QL_BF16>(const uint4& a, const uint4& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+// Tile width NB x 32 and the wave layout of a 256 x BN tile: WM x WN waves, each owning
+// BI x BJ blocks of 32 x 32.
+template <int NB> struct Layout;
+template <> struct Layout<8> { static constexpr int WM = 2, WN = 2, BI = 4, BJ = 4; };
+template <> struct Layout<7> { static constexpr int WM = 4, WN = 1, BI = 2, BJ = 7; };
+template <int NB> constexpr int bn_of() { return 32 * NB; }
+// one stage: A (256 rows) then B (BN rows): 64 KiB at BN = 256
+template <int NB> constexpr int stage_bytes() { return kATileBytes + bn_of<NB>() * kRowBytes; }
+
+// D[32 x 32] += a[32 x 16] b[16 x 32]: lane l supplies row l%32, k 8(l/32) .. +7 of each
+// operand and holds D[8i + 4(l/32) + j][l%32] in element 4i + j.
+template <int DT> QL_DEV f32x16_t mfma(const uint4& a, const uint4& b, f32x16_t c);
+template <> QL_DEV f32x16_t mfma<QL_BF16>(const uint4& a, const uint4& b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
-template <> QL_DEV f32x4_t mfma<QL_F16>(const uint4& a, const uint4& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+template <> QL_DEV f32x16_t mfma<QL_F16>(const uint4& a, const uint4& b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-// Issue this wave's share of one operand tile (256 rows x 64 k starting at (row0, k0)) as
-// 8 direct-to-LDS loads. Instruction j of wave w fills tile rows r0 = (4j + w) * 8 .. +7;
+// Issue this wave's share of one operand tile (32 R8 rows x 64 k starting at (row0, k0)) as
+// R8 direct-to-LDS loads. Instruction j of wave w fills tile rows r0 = (4j + w) * 8 .. +7;
 // lane l writes LDS bytes [16 l, 16 l + 16) of that 1 KiB span, i.e. row r0 + l/8,
 // physical chunk l%8, which holds logical chunk (l%8) ^ (l/8) of the row.
 // Addresses are a wave-uniform 64-bit base (SGPRs) plus a 32-bit lane offset; rows past the
@@ -85,7 +100,7 @@ QL_DEV TileLoader make_loader() {
   return t;
 }
 
-template <int R8 = 8>  // tile rows / 32: 8 (256 rows) or 7 (224 rows)
+template <int R8 = 8>  // tile rows / 32: 7 or 8 (224 or 256 rows)
 QL_DEV void load_tile(const TileLoader& t, const uint16_t* __restrict__ X, int64_t ld,
                       int64_t row0, int64_t rows, int64_t k0, char* __restrict__ lds_tile) {
 #pragma unroll
@@ -99,6 +114,39 @@ QL_DEV void load_tile(const TileLoader& t, const uint16_t* __restrict__ X, int64
     __builtin_amdgcn_global_load_lds((gbl_ptr_t)(base + off), (lds_ptr_t)(lds_tile + r0 * kRowBytes),
                                      16, 0, 0);
   }
+}
+
+// The same loads for an operand whose row count is a multiple of 8, with the addresses
+// computed once per tile: every 8-row group a load covers is then either wholly inside the
+// operand or wholly past its end (a group past the end re-reads the last 8 rows, tile rows
+// that are never stored), so each load keeps a wave-uniform row base and all of them share
+// one lane offset; a K step only adds its k offset.
+template <int R8>
+struct Panel {
+  const char* base[R8];  // wave-uniform: first row of load j at the panel's first k
+  uint32_t off;          // lane offset: (lane / 8) rows + physical 16-B chunk
+};
+
+template <int R8>
+QL_DEV void panel_init(Panel<R8>& p, const TileLoader& t, const uint16_t* __restrict__ X,
+                       int64_t ld, int64_t row0, int64_t rows, int64_t k0) {
+#pragma unroll
+  for (int j = 0; j < R8; ++j) {
+    const int64_t g = row0 + (4 * j + t.wave) * 8;
+    p.base[j] = reinterpret_cast<const char*>(X + (g < rows ? g : rows - 8) * ld + k0);
+  }
+  p.off = (uint32_t)(t.rsub * ld * 2) + t.chunk16;
+}
+
+template <int R8>
+QL_DEV void panel_issue(const Panel<R8>& p, const TileLoader& t, uint32_t kbytes,
+                        char* __restrict__ lds_tile) {
+  const uint32_t off = p.off + kbytes;
+#pragma unroll
+  for (int j = 0; j < R8; ++j)
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)(p.base[j] + off),
+                                     (lds_ptr_t)(lds_tile + (4 * j + t.wave) * 8 * kRowBytes), 16,
+                                     0, 0);
 }
 
 // Tile coordinates of this workgroup: XCD-contiguous renumbering, then grouped raster.
@@ -117,77 +165,105 @@ QL_DEV void tile_of(int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) 
   tn = in_group / gm;
 }
 
-// Fragment reads of one 32-k half of a stage: a[i] rows wm*128 + 16 i + fr, b[j] rows
-// wn*16*NJ + 16 j + fr.
-template <int NJ>
-QL_DEV void read_frags(const char* __restrict__ stage, int half, int wm, int wn, int fr, int fq,
-                       uint4 (&a)[8], uint4 (&b)[NJ]) {
-  const char* as = stage + (wm * 128 + fr) * kRowBytes;
-  const char* bs = stage + kTileBytes + (wn * 16 * NJ + fr) * kRowBytes;
-  const int c = ((half * 4 + fq) ^ (fr & 7)) * 16;
+template <int NB>
+struct Frags {
+  uint4 a[2][Layout<NB>::BI];  // [16-k block][row block]
+  uint4 b[2][Layout<NB>::BJ];  // [16-k block][column block]
+};
+
+// Fragment reads of one 32-k half of a stage: lane l reads row l%32 of each block, logical
+// chunk 4 half + 2 kk + l/32 for the half's 16-k blocks kk = 0, 1.
+template <int NB>
+QL_DEV void read_frags(const char* __restrict__ stage, int half, int wm, int wn, int lane,
+                       Frags<NB>& f) {
+  using L = Layout<NB>;
+  const int r = lane & 31;
+  const char* as = stage + (wm * L::BI * 32 + r) * kRowBytes;
+  const char* bs = stage + kATileBytes + (wn * L::BJ * 32 + r) * kRowBytes;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a[i] = *reinterpret_cast<const uint4*>(as + i * 16 * kRowBytes + c);
-    if (i < NJ) b[i] = *reinterpret_cast<const uint4*>(bs + i * 16 * kRowBytes + c);
+  for (int kk = 0; kk < 2; ++kk) {
+    const int c = ((half * 4 + kk * 2 + (lane >> 5)) ^ (r & 7)) * 16;
+#pragma unroll
+    for (int i = 0; i < L::BI; ++i) f.a[kk][i] = *reinterpret_cast<const uint4*>(as + i * 32 * kRowBytes + c);
+#pragma unroll
+    for (int j = 0; j < L::BJ; ++j) f.b[kk][j] = *reinterpret_cast<const uint4*>(bs + j * 32 * kRowBytes + c);
   }
 }
 
-template <int IT, int NJ>
-QL_DEV void mma_half(f32x4_t (&acc)[8][NJ], const uint4 (&a)[8], const uint4 (&b)[NJ]) {
+// B fragments go in as the first operand, so each lane's accumulator holds 4 consecutive
+// output columns of one output row (element 4g + e: row l%32, column 8g + 4(l/32) + e).
+template <int IT, int NB>
+QL_DEV void mma_half(f32x16_t (&acc)[Layout<NB>::BI][Layout<NB>::BJ], const Frags<NB>& f) {
+  using L = Layout<NB>;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      acc[i][j] = mfma<IT>(b[j], a[i], acc[i][j]);
-    }
+    for (int i = 0; i < L::BI; ++i)
+#pragma unroll
+      for (int j = 0; j < L::BJ; ++j) acc[i][j] = mfma<IT>(f.b[kk][j], f.a[kk][i], acc[i][j]);
 }
 
-// One K step kt, software-pipelined across steps. On entry f0 holds the first-half
-// fragments of stage `cur` (read during the previous step) and the DMA of step kt+1 into
-// `nxt` is in flight. The step reads the second half of `cur` while multiplying the first;
-// then every wave waits for its DMA of step kt+1 and meets at the barrier (after it, all of
-// `cur` has been read by every wave), issues the DMA of step kt+2 into `cur` (the last step
-// reloads itself: in bounds, never read), and reads the first half of `nxt` while
-// multiplying the second half of `cur`. `cur` and `nxt` are restrict-qualified so the
-// compiler's wait-count pass does not make these reads wait for the DMA into `cur`.
-// Per half step: R = 8 + NJ fragment reads, 8 NJ MFMAs, and (second half) R DMA loads.
-template <int IT, int NJ>
-QL_DEV void mma_step_pipe(f32x4_t (&acc)[8][NJ], uint4 (&f0a)[8], uint4 (&f0b)[NJ],
-                          char* __restrict__ cur, char* __restrict__ nxt, const TileLoader& la,
-                          const uint16_t* __restrict__ A2, int64_t lda2,
-                          const uint16_t* __restrict__ B2, int64_t ldb2, int64_t k2, int64_t m0,
-                          int64_t n0, int64_t M, int64_t N, int wm, int wn, int fr, int fq) {
-  constexpr int R = 8 + NJ, MF = 8 * NJ;
-  uint4 f1a[8], f1b[NJ];
-  read_frags<NJ>(cur, 1, wm, wn, fr, fq, f1a, f1b);
-  mma_half<IT, NJ>(acc, f0a, f0b);
+// One K step, software-pipelined across steps. On entry f0 holds the first-half fragments of
+// stage `cur` (read during the previous step) and the DMA of the next step into `nxt` is in
+// flight. The step reads the second half of `cur` while multiplying the first; then every
+// wave waits for its DMA of the next step and meets at the barrier (after it, all of `cur`
+// has been read by every wave), starts the DMA of the step after next into `cur` through
+// `issue` (each load placed behind one MFMA, first thing after the barrier, so it has the
+// most time to land), and reads the first half of `nxt` while multiplying the second half of
+// `cur`. `cur` and `nxt` are restrict-qualified so the compiler's wait-count pass does not
+// make these reads wait for the DMA into `cur`. Per half step: RH fragment reads and MF
+// MFMAs; the second half also issues the G DMA loads.
+template <int IT, int NB, typename Issue>
+QL_DEV void mma_step_pipe(f32x16_t (&acc)[Layout<NB>::BI][Layout<NB>::BJ], Frags<NB>& f0,
+                          char* __restrict__ cur, char* __restrict__ nxt, const Issue& issue,
+                          int wm, int wn, int lane) {
+  using L = Layout<NB>;
+  constexpr int RH = 2 * (L::BI + L::BJ), MF = 2 * L::BI * L::BJ, G = 8 + NB;
+  constexpr int REST = MF - G;                    // second-half MFMAs left for the reads
+  constexpr int DBL = RH > REST ? RH - REST : 0;  // of which carry two reads
+  static_assert(MF - 1 - RH >= 0 && REST >= DBL, "schedule does not fit the tile");
+  Frags<NB> f1;
+  read_frags<NB>(cur, 1, wm, wn, lane, f1);
+  mma_half<IT, NB>(acc, f0);
   __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
-  for (int t = 0; t < R; ++t) {
+  for (int t = 0; t < RH; ++t) {
     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, MF - 1 - 3 * R, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, MF - 1 - RH, 0);
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
-  load_tile(la, A2, lda2, m0, M, k2, cur);
-  load_tile<NJ>(la, B2, ldb2, n0, N, k2, cur + kTileBytes);
-  read_frags<NJ>(nxt, 0, wm, wn, fr, fq, f0a, f0b);
-  mma_half<IT, NJ>(acc, f1a, f1b);
-  __builtin_amdgcn_sched_group_barrier(0x020, R, 1);
+  issue(cur);
+  read_frags<NB>(nxt, 0, wm, wn, lane, f0);
+  mma_half<IT, NB>(acc, f1);
 #pragma unroll
-  for (int t = 0; t < R; ++t) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+  for (int t = 0; t < G; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, MF - 2 * R, 1);
+#pragma unroll
+  for (int t = 0; t < DBL; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+  }
+#pragma unroll
+  for (int t = 0; t < RH - 2 * DBL; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+  }
+  if constexpr (REST - DBL - (RH - 2 * DBL) > 0)
+    __builtin_amdgcn_sched_group_barrier(0x008, REST - DBL - (RH - 2 * DBL), 1);
 }
 
 // PARTIAL: write the raw fp32 sums of this split to ws[split][M][N]; otherwise the final
-// alpha / beta / bias epilogue into C (type OT).
-template <int IT, int OT, bool PARTIAL, int NJ>
+// alpha / beta / bias epilogue into C (type OT). AL8: M and N are multiples of 8 and the
+// loop's loads come from panels; otherwise every load clamps its rows per lane.
+// K order: the second segment (A2 B2^T, K2 <= 128 columns, last split only) is loaded by the
+// prologue, so every load inside the loop is a step of the first segment.
+template <int IT, int OT, bool PARTIAL, int NB, bool AL8>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
                     int64_t ldb, const uint16_t* __restrict__ A2, int64_t lda2,
@@ -196,96 +272,118 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
                     float* __restrict__ ws, const uint16_t* __restrict__ bias, int64_t M,
                     int64_t N, int64_t K, int64_t k_per_split, float alpha, float beta,
                     bool vec_out) {
+  using L = Layout<NB>;
+  constexpr int kStageBytes = stage_bytes<NB>();
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
-  constexpr int BN = bn_of<NJ>();
+  constexpr int BN = bn_of<NB>();
   int64_t tm, tn;
   tile_of((M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
   const int64_t m0 = tm * BM, n0 = tn * BN;
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int nk1 = (int)((ke - kb) / BK);
-  // the second segment (A2 B2^T, K2 columns) is appended to the last split
-  const int nk = nk1 + ((int)blockIdx.y == (int)gridDim.y - 1 ? (int)(K2 / BK) : 0);
+  // steps 0 .. nk2-1: the second segment; nk2 .. nk-1: the first (the host guarantees nk1 >= 1)
+  const int nk2 = (int)blockIdx.y == (int)gridDim.y - 1 ? (int)(K2 / BK) : 0;
+  const int nk = nk1 + nk2;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int fr = lane & 15;  // fragment row within a 16-row sub-tile
-  const int fq = lane >> 4;  // fragment k quarter (8 k each) within a 32-k step
+  const int wm = wave / L::WN, wn = wave % L::WN;
 
-  f32x4_t acc[8][NJ];
+  f32x16_t acc[L::BI][L::BJ];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < L::BI; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < L::BJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const TileLoader la = make_loader();
-  // k index of step t in its segment, and the segment's operands
-  auto seg_k = [&](int t) -> int64_t { return t < nk1 ? kb + (int64_t)t * BK : (int64_t)(t - nk1) * BK; };
   if (nk > 0) {
-    const bool s1 = nk1 > 0;
-    load_tile(la, s1 ? A : A2, s1 ? lda : lda2, m0, M, seg_k(0), smem);
-    load_tile<NJ>(la, s1 ? B : B2, s1 ? ldb : ldb2, n0, N, seg_k(0), smem + kTileBytes);
+    // prologue: steps 0 and 1, of either segment
+    auto prologue_load = [&](int t, char* stage) {
+      const bool s2 = t < nk2;
+      const int64_t k0 = s2 ? (int64_t)t * BK : kb + (int64_t)(t - nk2) * BK;
+      load_tile(la, s2 ? A2 : A, s2 ? lda2 : lda, m0, M, k0, stage);
+      load_tile<NB>(la, s2 ? B2 : B, s2 ? ldb2 : ldb, n0, N, k0, stage + kATileBytes);
+    };
+    prologue_load(0, smem);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    const int t1 = nk > 1 ? 1 : 0;
-    const bool s1b = t1 < nk1;
-    load_tile(la, s1b ? A : A2, s1b ? lda : lda2, m0, M, seg_k(t1), smem + kStageBytes);
-    load_tile<NJ>(la, s1b ? B : B2, s1b ? ldb : ldb2, n0, N, seg_k(t1),
-                  smem + kStageBytes + kTileBytes);
-    uint4 f0a[8], f0b[NJ];
-    read_frags<NJ>(smem, 0, wm, wn, fr, fq, f0a, f0b);
+    prologue_load(nk > 1 ? 1 : 0, smem + kStageBytes);
+    Frags<NB> f0;
+    read_frags<NB>(smem, 0, wm, wn, lane, f0);
+    // loop loads: step t2 = kt + 2 (the last step reloads itself: in bounds, never read),
+    // always of the first segment: k offset (t2 - nk2) * 64 from kb
+    Panel<8> pa;
+    Panel<NB> pb;
+    if constexpr (AL8) {
+      panel_init(pa, la, A, lda, m0, M, kb);
+      panel_init(pb, la, B, ldb, n0, N, kb);
+    }
     for (int kt = 0; kt < nk; ++kt) {
       char* cur = smem + (kt & 1) * kStageBytes;
       char* nxt = smem + ((kt + 1) & 1) * kStageBytes;
       const int t2 = kt + 2 < nk ? kt + 2 : nk - 1;
-      const bool s2 = t2 < nk1;
-      mma_step_pipe<IT, NJ>(acc, f0a, f0b, cur, nxt, la, s2 ? A : A2, s2 ? lda : lda2, s2 ? B : B2,
-                        s2 ? ldb : ldb2, seg_k(t2), m0, n0, M, N, wm, wn, fr, fq);
+      const int q = t2 - nk2;  // >= 0: nk2 <= 2 and nk1 >= 1
+      auto issue = [&](char* stage) {
+        if constexpr (AL8) {
+          const uint32_t kbytes = (uint32_t)q * (uint32_t)(BK * 2);
+          panel_issue(pa, la, kbytes, stage);
+          panel_issue(pb, la, kbytes, stage + kATileBytes);
+        } else {
+          const int64_t k0 = kb + (int64_t)q * BK;
+          load_tile(la, A, lda, m0, M, k0, stage);
+          load_tile<NB>(la, B, ldb, n0, N, k0, stage + kATileBytes);
+        }
+      };
+      mma_step_pipe<IT, NB>(acc, f0, cur, nxt, issue, wm, wn, lane);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Epilogue: lane owns row fr of each 16-row sub-tile i and columns 4*fq .. 4*fq+3 of each
-  // 16-column sub-tile j.
+  // Epilogue: block (i, j) element 4g + e of lane l is row l%32, column 8g + 4(l/32) + e.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t row = m0 + wm * 128 + i * 16 + fr;
+  for (int i = 0; i < L::BI; ++i) {
+    const int64_t row = m0 + (wm * L::BI + i) * 32 + (lane & 31);
     if (row >= M) continue;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int64_t col = n0 + wn * 16 * NJ + j * 16 + 4 * fq;
-      if (col >= N) continue;
-      if constexpr (PARTIAL) {
-        float* p = ws + ((int64_t)blockIdx.y * M + row) * N + col;
-        if (col + 3 < N && (N & 3) == 0) {
-          *reinterpret_cast<float4*>(p) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2],
-                                                      acc[i][j][3]);
-        } else {
-          for (int e = 0; e < 4; ++e)
-            if (col + e < N) p[e] = acc[i][j][e];
-        }
-      } else {
-        float v[4];
+    for (int j = 0; j < L::BJ; ++j) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = alpha * acc[i][j][e];
-        auto* cp = C + row * ldc + col;
-        if (beta != 0.f)
-          for (int e = 0; e < 4; ++e)
-            if (col + e < N) v[e] += beta * Elem<OT>::to_f32(cp[e]);
-        if (bias)
-          for (int e = 0; e < 4; ++e)
-            if (col + e < N) v[e] += Elem<IT>::to_f32(bias[col + e]);
-        const bool vec = vec_out && col + 3 < N;
-        if (vec) {
-          if constexpr (OT == QL_F32) {
-            *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
-          } else if constexpr (OT == QL_BF16) {
-            *reinterpret_cast<uint2*>(cp) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      for (int g = 0; g < 4; ++g) {
+        const int64_t col = n0 + (wn * L::BJ + j) * 32 + 8 * g + 4 * (lane >> 5);
+        if (col >= N) continue;
+        const float a0 = acc[i][j][4 * g], a1 = acc[i][j][4 * g + 1];
+        const float a2 = acc[i][j][4 * g + 2], a3 = acc[i][j][4 * g + 3];
+        if constexpr (PARTIAL) {
+          float* p = ws + ((int64_t)blockIdx.y * M + row) * N + col;
+          if (col + 3 < N && (N & 3) == 0) {
+            *reinterpret_cast<float4*>(p) = make_float4(a0, a1, a2, a3);
           } else {
-            *reinterpret_cast<uint2*>(cp) = make_uint2(pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3]));
+            const float v[4] = {a0, a1, a2, a3};
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) p[e] = v[e];
           }
         } else {
-          for (int e = 0; e < 4; ++e)
-            if (col + e < N) cp[e] = Elem<OT>::from_f32(v[e]);
+          float v[4] = {alpha * a0, alpha * a1, alpha * a2, alpha * a3};
+          auto* cp = C + row * ldc + col;
+          if (beta != 0.f)
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) v[e] += beta * Elem<OT>::to_f32(cp[e]);
+          if (bias)
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) v[e] += Elem<IT>::to_f32(bias[col + e]);
+          const bool vec = vec_out && col + 3 < N;
+          if (vec) {
+            if constexpr (OT == QL_F32) {
+              *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
+            } else if constexpr (OT == QL_BF16) {
+              *reinterpret_cast<uint2*>(cp) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            } else {
+              *reinterpret_cast<uint2*>(cp) = make_uint2(pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3]));
+            }
+          } else {
+            for (int e = 0; e < 4; ++e)
+              if (col + e < N) cp[e] = Elem<OT>::from_f32(v[e]);
+          }
         }
       }
     }
@@ -312,29 +410,45 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
   }
 }
 
-template <int IT, int OT, int NJ>
+template <int IT, int OT, int NB>
 int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
            const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
            int64_t M, int64_t N, int64_t K, float alpha, float beta, int splits, float* ws,
            hipStream_t s) {
   using T = typename Elem<OT>::T;
-  constexpr int BN = bn_of<NJ>();
+  constexpr int BN = bn_of<NB>();
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int64_t kps = ((K / BK + splits - 1) / splits) * BK;
   const int nsplit = (int)((K + kps - 1) / kps);
+  // panel loads: 8-row-aligned operands whose lane offsets (7 rows + K) fit in 32 bits
+  constexpr int64_t kOffMax = int64_t(1) << 26;
+  const bool al8 = M % 8 == 0 && N % 8 == 0 && lda < kOffMax && ldb < kOffMax && K < kOffMax;
   if (nsplit <= 1) {
     const bool vec_out = ql_aligned(C, 4 * ql_elem_size(OT)) && ldc % 4 == 0;
-    hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NJ>), dim3((unsigned)tiles, 1), dim3(kThreads), 0, s,
-                       (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2,
-                       lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc, nullptr,
-                       (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
+    if (al8)
+      hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, true>), dim3((unsigned)tiles, 1),
+                         dim3(kThreads), 0, s, (const uint16_t*)A, lda, (const uint16_t*)B, ldb,
+                         (const uint16_t*)A2, lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc,
+                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
+    else
+      hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, false>), dim3((unsigned)tiles, 1),
+                         dim3(kThreads), 0, s, (const uint16_t*)A, lda, (const uint16_t*)B, ldb,
+                         (const uint16_t*)A2, lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc,
+                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
     return ql_launch_status();
   }
-  hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NJ>), dim3((unsigned)tiles, (unsigned)nsplit),
-                     dim3(kThreads), 0, s,
-                     (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
-                     (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0,
-                     ws, (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false);
+  if (al8)
+    hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, true>),
+                       dim3((unsigned)tiles, (unsigned)nsplit), dim3(kThreads), 0, s,
+                       (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
+                       (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0, ws,
+                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, false>),
+                       dim3((unsigned)tiles, (unsigned)nsplit), dim3(kThreads), 0, s,
+                       (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
+                       (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0, ws,
+                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false);
   int st = ql_launch_status();
   if (st != QL_OK) return st;
   const int64_t total = M * N;
@@ -345,12 +459,12 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
   return ql_launch_status();
 }
 
-// Tile width for an M x N output: 224 (NJ = 7) when N is a multiple of 224, the output is
-// large enough to run without split-K (>= 128 tiles of 256 x 256) and the narrower tiles take
-// fewer (waves x tile width) on 256 CUs, else 256. The 4096 x 3584 outputs of the 7B step are
-// 224 tiles of 256 x 256 (one partial wave) but exactly 256 tiles of 256 x 224. Small outputs
-// are split over K instead, where narrower tiles only add operand traffic.
-int choose_nj(int64_t M, int64_t N) {
+// Tile width for an M x N output: 224 when N is a multiple of 224, the output is large enough
+// to run without split-K (>= 128 tiles of 256 x 256) and the narrower tiles take fewer
+// (waves x tile width) on 256 CUs, else 256. The 4096 x 3584 outputs of the 7B step are 224
+// tiles of 256 x 256 (one partial wave) but exactly 256 tiles of 256 x 224. Small outputs are
+// split over K instead, where narrower tiles only add operand traffic.
+int choose_nb(int64_t M, int64_t N) {
   if (N % 224) return 8;
   const int64_t tm = (M + BM - 1) / BM;
   const int64_t t8 = tm * ((N + 255) / 256);
@@ -375,7 +489,7 @@ int64_t ql_gemm_nt_workspace_floats(int64_t M, int64_t N, int splits) {
 int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
   // Enough workgroups for 256 CUs: split K while there are fewer tiles than CUs and each
   // split keeps at least 8 K steps.
-  const int64_t bn = 32 * choose_nj(M, N);
+  const int64_t bn = 32 * choose_nb(M, N);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + bn - 1) / bn);
   int s = 1;
   while (tiles * s < 192 && (K / BK) / (2 * s) >= 8 && s < 64) s *= 2;
@@ -387,12 +501,22 @@ int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, cons
                 const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
                 float alpha, float beta, int splits, float* ws, hipStream_t s) {
   if (splits > 1 && !ws) return QL_EINVAL;
-  if (K2 < 0 || K2 % BK) return QL_EINVAL;
+  if (K2 < 0 || K2 % BK || K <= 0 || K % BK) return QL_EINVAL;
+  // the kernel loads the second segment in its prologue: at most kPrologueSteps steps; the
+  // sum is symmetric in the two segments, so a short first segment may take that place
+  if (K2 > kPrologueSteps * BK) {
+    if (K > kPrologueSteps * BK) return QL_ESHAPE;
+    const void* t = A; A = A2; A2 = t;
+    t = B; B = B2; B2 = t;
+    int64_t u = lda; lda = lda2; lda2 = u;
+    u = ldb; ldb = ldb2; ldb2 = u;
+    u = K; K = K2; K2 = u;
+  }
   if (K2 == 0) A2 = B2 = nullptr;
-  const bool narrow = choose_nj(M, N) == 7;
-#define QL_GEMM_NT_LAUNCH(ITC, NJC)                                                            \
+  const bool narrow = choose_nb(M, N) == 7;
+#define QL_GEMM_NT_LAUNCH(ITC, NBC)                                                            \
   QL_DISPATCH_DTYPE(c_dtype, OT,                                                               \
-                    return (launch<ITC, OT, NJC>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc, \
+                    return (launch<ITC, OT, NBC>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc, \
                                                  bias, M, N, K, alpha, beta, splits, ws, s)))
   if (in_dtype == QL_BF16) {
     if (narrow) {

@@ -266,8 +266,9 @@ int qlora_transpose16(const void* in, int64_t rows, int64_t cols, int64_t ld_in,
 /*
  * NT GEMM over two concatenated K segments (bf16/fp16 operands, fp32 accumulation):
  *   C[M,N] = alpha * (A[M,K] B[N,K]^T + A2[M,K2] B2[N,K2]^T) (+ bias[n])
- * K and K2 multiples of 64; all four operands k-contiguous, 16-B aligned, leading dimensions
- * multiples of 8. With the rank-16 LoRA factors zero-padded to 64 columns this is the whole
+ * K and K2 multiples of 64, one of them at most 128 (QL_ESHAPE otherwise); all four operands
+ * k-contiguous, 16-B aligned, leading dimensions multiples of 8. The short segment is summed
+ * first. With the rank-16 LoRA factors zero-padded to 64 columns this is the whole
  * 4-bit LoRA linear in one GEMM: y = x W^T + u (s B)^T with u = x A^T (forward) and
  * dx = g (W^T)^T + du A^T-padded (backward).
  * Replaces: solution/nf4.py:102,111 (F.linear / matmul on the dequantised weight) together

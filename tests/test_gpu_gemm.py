@@ -80,13 +80,14 @@ def test_gemm_output_view_with_row_stride():
 
 @pytest.mark.parametrize("M,N,K", [(512, 768, 1024), (300, 520, 192), (257, 255, 64),
                                    (1000, 3000, 640), (300, 448, 128), (1000, 3584, 640),
-                                   (4096, 3584, 256), (4000, 3584, 128)])
+                                   (4096, 3584, 256), (4000, 3584, 128), (4096, 4608, 192),
+                                   (4000, 4608, 128)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_large_tile_edges(M, N, K, dtype):
     """k-contiguous operands with K % 64 == 0 take the large-tile kernel (256 x 256, or
-    256 x 224 when N is a multiple of 224 and that fills the CUs better: the 4096 and 4000 x
-    3584 cases, the latter with a ragged last row of tiles); M and N edges are loaded clamped
-    and must never be stored."""
+    256 x 224 / 256 x 288 when N is a multiple of that width and it fills the CUs better: the
+    4096 and 4000 x 3584 cases take 224, the x 4608 cases 288, the 4000-row ones with a ragged
+    last row of tiles); M and N edges are loaded clamped and must never be stored."""
     print(f"gemm_nt M={M} N={N} K={K} {dtype}", flush=True)
     g = torch.Generator().manual_seed(M + 11 * N + K)
     a = torch.randn(M, K, generator=g).to(dtype)
@@ -158,7 +159,8 @@ def test_transposed_frozen_cache_follows_the_weight():
 
 
 @pytest.mark.parametrize("M,N,K,K2", [(4096, 512, 3584, 64), (300, 520, 256, 64),
-                                      (256, 384, 128, 128), (64, 3584, 0, 64)])
+                                      (256, 384, 128, 128), (64, 3584, 0, 64),
+                                      (4096, 4608, 256, 64)])
 def test_gemm_nt_cat(M, N, K, K2):
     """a b^T + a2 b2^T over the concatenated K in one GEMM (split-K included for 4096x512)."""
     print(f"gemm_nt_cat M={M} N={N} K={K} K2={K2}", flush=True)
