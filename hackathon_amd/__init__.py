@@ -17,6 +17,7 @@ include/qlora_gfx950.h, bound through ctypes in `_lib`).
   attention.py      causal flash attention behind transformers' "sdpa" entry (fwd + bwd)
   residual.py       Qwen2DecoderLayer with the residual adds fused into its two RMSNorms
   optim.py          FusedAdamW: AdamW over the adapters in one launch
+  fused_proj.py     q/k/v (+ RoPE) and gate/up (+ SwiGLU) of a decoder layer as one LoRA GEMM each
 """
 
 PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora", "attention", "residual")
@@ -25,9 +26,11 @@ _applied = set()
 
 
 def apply(include_example=True):
-    """Install every patch (idempotent), as solution/__init__.py:22-34 does; "attention" and
-    "residual" have no counterpart in the reference, which leaves attention to torch's SDPA and
-    the decoder layer's residual adds to transformers."""
+    """Install every patch (idempotent), as solution/__init__.py:22-34 does; "attention",
+    "residual" and "fused_proj" have no counterpart in the reference, which leaves attention to
+    torch's SDPA, the decoder layer's residual adds to transformers and runs every projection
+    as its own layer. "fused_proj" goes last: its forwards fall back to the ones installed
+    before them."""
     from importlib import import_module
 
     for name in PATCHES:
@@ -39,3 +42,8 @@ def apply(include_example=True):
 
         patch_qwen2_mlp()
         _applied.add("swiglu")
+    if "fused_proj" not in _applied:
+        from .fused_proj import patch as patch_fused_proj
+
+        patch_fused_proj()
+        _applied.add("fused_proj")

@@ -39,6 +39,10 @@ _SIGNATURES = {
                       _c_i64, _c_i64, _c_int, _c_ptr],
     "qlora_swiglu_fwd": [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_ptr],
     "qlora_swiglu_bwd": [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_ptr],
+    "qlora_swiglu_fwd_rows": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64,
+                              _c_int, _c_ptr],
+    "qlora_swiglu_bwd_rows": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+                              _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr],
     "qlora_lora_dropout_scale": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64,
                                  _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_scaled_add": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,
@@ -60,6 +64,8 @@ _SIGNATURES = {
                          _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_pack": [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_f32, _c_int, _c_ptr, _c_ptr, _c_ptr,
                         _c_ptr, _c_int, _c_ptr],
+    "qlora_lora_pack_group": [_c_ptr, _c_int, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                              _c_int, _c_ptr],
     "qlora_nf4_quantize": [_c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
                            _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr],
     "qlora_add_rmsnorm_fwd": [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr,
@@ -161,6 +167,20 @@ def require_device(*tensors: torch.Tensor) -> None:
 
 def i64_array(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+
+
+class LoraFactor(ctypes.Structure):
+    """ql_lora_factor: one adapter's fp32 factors A [16, K], B [n, 16] and its scaling."""
+    _fields_ = [("A", ctypes.c_void_p), ("B", ctypes.c_void_p), ("n", ctypes.c_int64),
+                ("scaling", ctypes.c_float)]
+
+
+def lora_factors(items) -> ctypes.Array:
+    """A host array of ql_lora_factor from (A tensor, B tensor, scaling) triples."""
+    arr = (LoraFactor * len(items))()
+    for i, (a, b, s) in enumerate(items):
+        arr[i] = LoraFactor(a.data_ptr(), b.data_ptr(), b.shape[0], float(s))
+    return arr
 
 
 def workspace(name: str, *sizes, device) -> tuple:

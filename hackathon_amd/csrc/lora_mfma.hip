@@ -355,6 +355,78 @@ __global__ __launch_bounds__(256) void lora_pack_kernel(const float* __restrict_
   }
 }
 
+// The compute-dtype operands of up to four rank-16 adapters that share an input (the q/k/v or
+// gate/up projections of one layer) for one fused GEMM per direction: adapter g owns columns
+// 16g .. 16g+15 of the padded operands and rows off[g] .. off[g+1]-1 of the concatenated
+// outputs. Work items: t < K: row t of at (all pad columns); K <= t < K + N: row n of bs and
+// column n of bt; then 8 elements of a16 per item.
+constexpr int kMaxGroup = 4;
+struct PackGroupArgs {
+  const float* A[kMaxGroup];  // [16, K]
+  const float* B[kMaxGroup];  // [n_g, 16]
+  float scale[kMaxGroup];
+  int64_t off[kMaxGroup + 1];  // prefix sums of n_g
+  int G;
+};
+
+template <int OT>
+__global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, int64_t K,
+                                                              typename Elem<OT>::T* __restrict__ a16,
+                                                              typename Elem<OT>::T* __restrict__ at,
+                                                              typename Elem<OT>::T* __restrict__ bs,
+                                                              typename Elem<OT>::T* __restrict__ bt,
+                                                              int pad) {
+  using T = typename Elem<OT>::T;
+  const int64_t N = p.off[p.G];
+  const int64_t n_a16 = (int64_t)kRank * p.G * K / 8;
+  const int64_t total = K + N + n_a16;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * 256) {
+    if (t < K) {
+      // row t of at: 8 columns (one 16-B store) at a time
+      T* row = at + t * pad;
+      for (int c0 = 0; c0 < pad; c0 += 8) {
+        const int g = c0 / kRank;
+        float v[8];
+        if (g < p.G) {
+          const float* a = p.A[g] + (int64_t)(c0 & (kRank - 1)) * K + t;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = a[(int64_t)e * K];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = 0.f;
+        }
+        Vec8<OT>::store(row + c0, v);
+      }
+    } else if (t < K + N) {
+      const int64_t n = t - K;
+      int g = 0;
+      while (g + 1 < p.G && n >= p.off[g + 1]) ++g;
+      const int64_t ln = n - p.off[g];
+      T* row = bs + n * pad;
+      float b[kRank];
+#pragma unroll
+      for (int r = 0; r < kRank; ++r) {
+        b[r] = p.B[g][ln * kRank + r];
+        bt[(int64_t)r * N + n] = Elem<OT>::from_f32(b[r]);
+      }
+      for (int c0 = 0; c0 < pad; c0 += 8) {
+        float v[8];
+        const bool mine = c0 / kRank == g;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = mine ? p.scale[g] * b[(c0 & (kRank - 1)) + e] : 0.f;
+        Vec8<OT>::store(row + c0, v);
+      }
+    } else {
+      const int64_t i = (t - K - N) * 8;  // into a16 [16 G, K]
+      const int64_t gr = i / K, col = i - gr * K;
+      const int g = (int)(gr / kRank), r = (int)(gr - (int64_t)g * kRank);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a16[i + e] = Elem<OT>::from_f32(p.A[g][(int64_t)r * K + col + e]);
+    }
+  }
+}
+
 unsigned grid1d(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 4096) g = 4096;
@@ -534,5 +606,35 @@ extern "C" int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_
   else
     hipLaunchKernelGGL((lora_pack_kernel<QL_F16>), grid, dim3(256), 0, s, A, B, K, N, scaling,
                        (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
+  return ql_launch_status();
+}
+
+extern "C" int qlora_lora_pack_group(const ql_lora_factor* factors, int count, int64_t K,
+                                     int out_dtype, void* a16, void* at_pad, void* bs_pad,
+                                     void* bt, int pad, ql_stream_t stream) {
+  if (count < 1 || count > kMaxGroup || K < 0 || K % 8 || pad < kRank * count || pad % 8)
+    return QL_EINVAL;
+  if (!factors || !a16 || !at_pad || !bs_pad || !bt) return QL_EINVAL;
+  if (!ql_aligned(at_pad, 16) || !ql_aligned(bs_pad, 16)) return QL_EALIGN;
+  if (out_dtype != QL_BF16 && out_dtype != QL_F16) return QL_EDTYPE;
+  PackGroupArgs p{};
+  p.G = count;
+  p.off[0] = 0;
+  for (int g = 0; g < count; ++g) {
+    if (!factors[g].A || !factors[g].B || factors[g].n < 0) return QL_EINVAL;
+    p.A[g] = factors[g].A;
+    p.B[g] = factors[g].B;
+    p.scale[g] = factors[g].scaling;
+    p.off[g + 1] = p.off[g] + factors[g].n;
+  }
+  const int64_t total = K + p.off[count] + (int64_t)kRank * count * K / 8;
+  if (total == 0) return QL_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (out_dtype == QL_BF16)
+    hipLaunchKernelGGL((lora_pack_group_kernel<QL_BF16>), dim3(grid1d(total)), dim3(256), 0, s, p,
+                       K, (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
+  else
+    hipLaunchKernelGGL((lora_pack_group_kernel<QL_F16>), dim3(grid1d(total)), dim3(256), 0, s, p,
+                       K, (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
   return ql_launch_status();
 }

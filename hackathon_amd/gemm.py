@@ -178,3 +178,26 @@ def lora_pack(a: torch.Tensor, b: torch.Tensor, scaling: float, dtype, pad: int 
     _lib.call("qlora_lora_pack", a.data_ptr(), b.data_ptr(), K, N, float(scaling), _lib.tag(dtype),
               a16.data_ptr(), at.data_ptr(), bs.data_ptr(), bt.data_ptr(), pad, _lib.stream_of(a))
     return a16, at, bs, bt
+
+
+def lora_pack_group(factors, dtype, pad: int = 64):
+    """(a16 [16G, K], at_pad [K, pad], bs_pad [N, pad], bt [16, N]) in `dtype` for G <= 4
+    adapters (a_g [16, K], b_g [n_g, 16], scaling_g) that read the same input, adapter g in
+    columns 16g .. 16g+15 and output rows off_g .. off_g + n_g - 1, N = sum n_g
+    (qlora_lora_pack_group, one launch)."""
+    items = []
+    for a, b, s in factors:
+        _lib.require_device(a, b)
+        items.append((a.detach().float().contiguous(), b.detach().float().contiguous(), s))
+    K = items[0][0].shape[1]
+    N = sum(b.shape[0] for _, b, _ in items)
+    G = len(items)
+    dev = items[0][0].device
+    a16 = torch.empty((16 * G, K), dtype=dtype, device=dev)
+    at = torch.empty((K, pad), dtype=dtype, device=dev)
+    bs = torch.empty((N, pad), dtype=dtype, device=dev)
+    bt = torch.empty((16, N), dtype=dtype, device=dev)
+    _lib.call("qlora_lora_pack_group", _lib.lora_factors(items), G, K, _lib.tag(dtype),
+              a16.data_ptr(), at.data_ptr(), bs.data_ptr(), bt.data_ptr(), pad,
+              _lib.stream_of(a16))
+    return a16, at, bs, bt

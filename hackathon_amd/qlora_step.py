@@ -96,11 +96,11 @@ def _unpatch_transformers():
 
     for owner, name in ((m.Qwen2RMSNorm, "forward"), (m.Qwen2MLP, "forward"),
                         (m.Qwen2ForCausalLM, "forward"), (m, "apply_rotary_pos_emb"),
-                        (m.Qwen2DecoderLayer, "forward")):
+                        (m.Qwen2DecoderLayer, "forward"), (m.Qwen2Attention, "forward")):
         fn = getattr(owner, name)
-        orig = getattr(fn, "_original", None)
-        if orig is not None:
-            setattr(owner, name, orig)
+        while getattr(fn, "_original", None) is not None:  # patches may stack
+            fn = fn._original
+        setattr(owner, name, fn)
     from transformers.modeling_utils import AttentionInterface
 
     orig = getattr(AttentionInterface._global_mapping["sdpa"], "_original", None)

@@ -43,6 +43,25 @@ def swiglu(gate, up):
     return SwiGLU.apply(gate, up)
 
 
+def swiglu_rows(gate, up, out):
+    """out = silu(gate) * up for [rows, cols] operands with their own row strides
+    (qlora_swiglu_fwd_rows): gate and up may be column ranges of one buffer."""
+    rows, cols = gate.shape
+    _lib.call("qlora_swiglu_fwd_rows", gate.data_ptr(), gate.stride(0), up.data_ptr(),
+              up.stride(0), out.data_ptr(), out.stride(0), rows, cols, _lib.tag(gate.dtype),
+              _lib.stream_of(gate))
+    return out
+
+
+def swiglu_bwd_rows(grad, gate, up, dgate, dup):
+    """The SwiGLU gradients into dgate / dup for row-strided operands (qlora_swiglu_bwd_rows)."""
+    rows, cols = gate.shape
+    _lib.call("qlora_swiglu_bwd_rows", grad.data_ptr(), grad.stride(0), gate.data_ptr(),
+              gate.stride(0), up.data_ptr(), up.stride(0), dgate.data_ptr(), dgate.stride(0),
+              dup.data_ptr(), dup.stride(0), rows, cols, _lib.tag(gate.dtype),
+              _lib.stream_of(gate))
+
+
 def patch_qwen2_mlp():
     """Send Qwen2MLP.forward through the fused kernel for GPU inputs (solution/swiglu.py:68-81)."""
     from transformers.models.qwen2 import modeling_qwen2

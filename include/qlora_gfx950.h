@@ -161,6 +161,21 @@ int qlora_swiglu_bwd(const void* grad, const void* gate, const void* up, void* d
                      int dtype, int64_t n, ql_stream_t stream);
 
 /*
+ * The same two operations on [rows, cols] operands with their own row strides (element
+ * leading dimensions), e.g. gate and up as the two column halves of one fused gate|up
+ * projection output and dgate / dup written into the halves of one gradient buffer.
+ * cols % 8 == 0; every pointer 16-B aligned and every leading dimension 16-B granular
+ * (QL_EALIGN otherwise); the math is exactly that of the contiguous forms.
+ * Replaces: solution/swiglu.py:44-61 when gate and up are views of one buffer.
+ */
+int qlora_swiglu_fwd_rows(const void* gate, int64_t ldg, const void* up, int64_t ldu, void* out,
+                          int64_t ldo, int64_t rows, int64_t cols, int dtype, ql_stream_t stream);
+int qlora_swiglu_bwd_rows(const void* grad, int64_t ldgr, const void* gate, int64_t ldg,
+                          const void* up, int64_t ldu, void* dgate, int64_t lddg, void* dup,
+                          int64_t lddu, int64_t rows, int64_t cols, int dtype,
+                          ql_stream_t stream);
+
+/*
  * LoRA input dropout + scale + cast, rows of n_cols.
  * Replaces: solution/lora.py:29-46 (lora_dropout_scale_kernel) + :74-81 (_dropout_scale).
  *   p > 0 : keep = U(seed, row*n_cols + col) > p ;  out = keep ? in*scale : 0
@@ -323,6 +338,29 @@ int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, i
 int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float scaling,
                     int out_dtype, void* a16, void* at_pad, void* bs_pad, void* bt, int pad,
                     ql_stream_t stream);
+
+/*
+ * The operands of up to four rank-16 adapters that read the same input (the q/k/v or gate/up
+ * projections of a layer), packed for one GEMM per direction over the concatenated outputs.
+ * factors[g] (host array, count <= 4, count * 16 <= pad): A [16, K] and B [n_g, 16] fp32,
+ * scaling s_g; N = sum n_g, off_g = n_0 + .. + n_{g-1}:
+ *   a16 [16 count, K]: rows 16g .. 16g+15 = A_g;
+ *   at_pad [K, pad]:   columns 16g .. 16g+15 = A_g^T, the rest 0;
+ *   bs_pad [N, pad]:   row off_g + n: columns 16g .. 16g+15 = s_g B_g[n], the rest 0;
+ *   bt [16, N]:        columns off_g .. = B_g^T.
+ * out_dtype QL_BF16 or QL_F16, round to nearest even; K % 8 == 0.
+ * Replaces: the per-projection casts of solution/lora.py:172 for projections fused into one
+ * GEMM (no reference counterpart for the fused layout itself).
+ */
+typedef struct ql_lora_factor {
+  const float* A;
+  const float* B;
+  int64_t n;
+  float scaling;
+} ql_lora_factor;
+int qlora_lora_pack_group(const ql_lora_factor* factors, int count, int64_t K, int out_dtype,
+                          void* a16, void* at_pad, void* bs_pad, void* bt, int pad,
+                          ql_stream_t stream);
 
 /*
  * Causal flash attention forward with grouped-query heads (HQ % HK == 0), head_dim 128:

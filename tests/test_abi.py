@@ -92,6 +92,9 @@ def test_rejected_arguments_return_codes(lib):
                           None) == -3
     assert lib.qlora_gemm(0, 0, 4, 4, 12, fake, 8, fake, 16, 2, fake, 4, 0, None, 1.0, 0.0,
                           None) == -4
+    # cat gemm: the two K segments may not both exceed 128 (the short one is loaded up front)
+    assert lib.qlora_gemm_nt_cat(256, 256, 256, fake, 256, fake, 256, 192, fake, 192, fake, 192,
+                                 2, fake, 256, 2, None, 1.0, None, 0, None) == -4
     # adamw: a table is required when there is work; the bias correction must be positive
     assert lib.qlora_adamw_fp32(None, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 1.0, 1e-8, None) == -1
     assert lib.qlora_adamw_fp32(fake, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 0.0, 1e-8, None) == -1

@@ -1,0 +1,170 @@
+"""The fused q/k/v (+ RoPE) and gate/up (+ SwiGLU) projections against the same layers run one
+by one (each its own LoraNF4Linear, then HipRoPE / SwiGLU, gradients summed by autograd).
+
+Both compute every sum in fp32 from the same bf16 operands; they differ in the order of the fp32
+accumulation (split-K of the narrow k/v outputs, one dX GEMM instead of three added in bf16),
+so outputs agree to bf16 rounding and gradients to a small relative error (tolerances below).
+"""
+
+import pytest
+import torch
+
+import hackathon_amd
+from hackathon_amd import fused_proj, qlora_step, rope, swiglu
+
+pytestmark = pytest.mark.gpu
+
+
+def _model(seed=0):
+    cfg = qlora_step.qwen2_config(hidden_size=512, intermediate_size=1024, num_hidden_layers=1,
+                                  num_attention_heads=4, num_key_value_heads=2, vocab_size=1000)
+    return cfg, qlora_step.build_qlora_model(cfg, "cuda", seed=seed)
+
+
+def _rel(a, b):
+    return ((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-30)).item()
+
+
+def _params(layers):
+    out = []
+    for layer in layers:
+        out += [layer.lora_A["default"].weight, layer.lora_B["default"].weight]
+    return out
+
+
+def _zero(params, x):
+    for p in params:
+        p.grad = None
+    x.grad = None
+
+
+@pytest.mark.parametrize("seq", [64, 200])
+def test_qkv_rope_matches_separate_layers(seq):
+    print(f"fused qkv seq={seq}", flush=True)
+    cfg, model = _model()
+    attn = model.model.layers[0].self_attn
+    layers = (attn.q_proj, attn.k_proj, attn.v_proj)
+    params = _params(layers)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    pos = torch.arange(seq, device="cuda")[None]
+    cos, sin = model.model.rotary_emb(x, pos)
+    hq, hk, d = 4, 2, 128
+    wq = torch.randn(2, hq, seq, d, device="cuda", generator=g).to(torch.bfloat16)
+    wk = torch.randn(2, hk, seq, d, device="cuda", generator=g).to(torch.bfloat16)
+    wv = torch.randn(2, hk, seq, d, device="cuda", generator=g).to(torch.bfloat16)
+
+    def loss_of(q, k, v):
+        return (q.float() * wq).sum() + (k.float() * wk).sum() + (v.float() * wv).sum()
+
+    # one by one
+    q = attn.q_proj(x).view(2, seq, hq, d).transpose(1, 2)
+    k = attn.k_proj(x).view(2, seq, hk, d).transpose(1, 2)
+    v = attn.v_proj(x).view(2, seq, hk, d).transpose(1, 2)
+    q, k = rope.HipRoPE.apply(q, k, cos, sin)
+    loss_of(q, k, v).backward()
+    ref = [t.detach().clone() for t in (q, k, v)]
+    ref_g = [x.grad.clone()] + [p.grad.clone() for p in params]
+    _zero(params, x)
+
+    specs, ab = fused_proj._group(layers, x)
+    q2, k2, v2 = fused_proj.QKVRoPE.apply(x, cos, sin, hq, hk, tuple(specs), *ab)
+    loss_of(q2, k2, v2).backward()
+    for a, b in zip((q2, k2, v2), ref):
+        assert a.shape == b.shape
+        assert _rel(a, b) < 4e-3
+    got_g = [x.grad] + [p.grad for p in params]
+    for name, a, b in zip(["x", "Aq", "Bq", "Ak", "Bk", "Av", "Bv"], got_g, ref_g):
+        assert a is not None and a.dtype == b.dtype, name
+        assert _rel(a, b) < 1e-2, (name, _rel(a, b))
+
+
+def test_gate_up_swiglu_matches_separate_layers():
+    print("fused gate/up", flush=True)
+    cfg, model = _model()
+    mlp = model.model.layers[0].mlp
+    layers = (mlp.gate_proj, mlp.up_proj)
+    params = _params(layers)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn(2, 96, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(2, 96, 1024, device="cuda", generator=g).to(torch.bfloat16)
+
+    h = swiglu.swiglu(mlp.gate_proj(x), mlp.up_proj(x))
+    (h.float() * w).sum().backward()
+    ref = h.detach().clone()
+    ref_g = [x.grad.clone()] + [p.grad.clone() for p in params]
+    _zero(params, x)
+
+    specs, ab = fused_proj._group(layers, x)
+    h2 = fused_proj.GateUpSwiGLU.apply(x, tuple(specs), *ab)
+    (h2.float() * w).sum().backward()
+    assert h2.shape == ref.shape and _rel(h2, ref) < 4e-3
+    got_g = [x.grad] + [p.grad for p in params]
+    for name, a, b in zip(["x", "Ag", "Bg", "Au", "Bu"], got_g, ref_g):
+        assert _rel(a, b) < 1e-2, (name, _rel(a, b))
+
+
+def test_swiglu_rows_match_the_contiguous_kernels():
+    print("swiglu rows", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    y = torch.randn(37, 2 * 264, device="cuda", generator=g).to(torch.bfloat16)
+    gate, up = y[:, :264], y[:, 264:]
+    h = torch.empty(37, 264, dtype=torch.bfloat16, device="cuda")
+    swiglu.swiglu_rows(gate, up, h)
+    assert torch.equal(h, swiglu.swiglu(gate.contiguous(), up.contiguous()))
+    dh = torch.randn(37, 264, device="cuda", generator=g).to(torch.bfloat16)
+    gbuf = torch.empty(37, 2 * 264, dtype=torch.bfloat16, device="cuda")
+    swiglu.swiglu_bwd_rows(dh, gate, up, gbuf[:, :264], gbuf[:, 264:])
+    dg, du = swiglu.SwiGLU.backward(
+        type("C", (), {"saved_tensors": (gate.contiguous(), up.contiguous())})(), dh)
+    assert torch.equal(gbuf[:, :264], dg) and torch.equal(gbuf[:, 264:], du)
+
+
+def test_decoder_layer_takes_the_fused_path(monkeypatch):
+    print("fused routing", flush=True)
+    cfg, model = _model()
+    hackathon_amd.apply()
+    calls = {"qkv": 0, "mlp": 0}
+    qkv_apply, mlp_apply = fused_proj.QKVRoPE.apply, fused_proj.GateUpSwiGLU.apply
+
+    def count_qkv(*a):
+        calls["qkv"] += 1
+        return qkv_apply(*a)
+
+    def count_mlp(*a):
+        calls["mlp"] += 1
+        return mlp_apply(*a)
+
+    monkeypatch.setattr(fused_proj.QKVRoPE, "apply", count_qkv)
+    monkeypatch.setattr(fused_proj.GateUpSwiGLU, "apply", count_mlp)
+    ids = torch.randint(0, 1000, (2, 64), device="cuda")
+    out = model(input_ids=ids, labels=ids, use_cache=False)
+    out.loss.backward()
+    assert calls == {"qkv": 1, "mlp": 1}
+    assert all(p.grad is not None and torch.isfinite(p.grad).all()
+               for p in qlora_step.lora_parameters(model))
+
+
+def test_lora_pack_group_matches_the_single_packs():
+    print("lora pack group", flush=True)
+    from hackathon_amd import gemm
+
+    g = torch.Generator(device="cuda").manual_seed(4)
+    K, ns, scales = 256, (512, 128, 64), (2.0, 0.5, 1.5)
+    facs = [(torch.randn(16, K, device="cuda", generator=g),
+             torch.randn(n, 16, device="cuda", generator=g), s) for n, s in zip(ns, scales)]
+    a16, at, bs, bt = gemm.lora_pack_group(facs, torch.bfloat16)
+    off = 0
+    for i, ((a, b, s), n) in enumerate(zip(facs, ns)):
+        a1, at1, bs1, bt1 = gemm.lora_pack(a, b, s, torch.bfloat16, 64)
+        cols = slice(16 * i, 16 * i + 16)
+        assert torch.equal(a16[cols], a1)
+        assert torch.equal(at[:, cols], at1[:, :16])
+        rows = slice(off, off + n)
+        assert torch.equal(bs[rows, cols], bs1[:, :16])
+        others = torch.ones(64, dtype=torch.bool, device="cuda")
+        others[cols] = False
+        assert torch.all(bs[rows][:, others] == 0)
+        assert torch.equal(bt[:, rows], bt1)
+        off += n
+    assert torch.all(at[:, 48:] == 0)

@@ -160,9 +160,11 @@ def test_transposed_frozen_cache_follows_the_weight():
 
 @pytest.mark.parametrize("M,N,K,K2", [(4096, 512, 3584, 64), (300, 520, 256, 64),
                                       (256, 384, 128, 128), (64, 3584, 0, 64),
-                                      (4096, 4608, 256, 64)])
+                                      (4096, 4608, 256, 64), (300, 256, 64, 320),
+                                      (256, 3584, 128, 1024)])
 def test_gemm_nt_cat(M, N, K, K2):
-    """a b^T + a2 b2^T over the concatenated K in one GEMM (split-K included for 4096x512)."""
+    """a b^T + a2 b2^T over the concatenated K in one GEMM (split-K included for 4096x512; a
+    second segment longer than 128 with a first of at most 128 swaps their roles)."""
     print(f"gemm_nt_cat M={M} N={N} K={K} K2={K2}", flush=True)
     g = torch.Generator().manual_seed(M + N + K + K2)
     a = torch.randn(M, K, generator=g).to(torch.bfloat16)
