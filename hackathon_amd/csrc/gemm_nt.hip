@@ -399,8 +399,17 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
   const int64_t total = M * N;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
+    // 8 partials loaded at a time (independent loads in flight), added in split order
     float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += ws[z * total + i];
+    int z = 0;
+    for (; z + 8 <= splits; z += 8) {
+      float w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = ws[(int64_t)(z + j) * total + i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += w[j];
+    }
+    for (; z < splits; ++z) s += ws[(int64_t)z * total + i];
     const int64_t row = i / N, col = i - row * N;
     float v = alpha * s;
     auto* cp = C + row * ldc + col;

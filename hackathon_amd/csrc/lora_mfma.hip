@@ -173,7 +173,18 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
     const int c = (int)(i - m * out_cols);
     float v = 0.f;
     if (c < kRank) {
-      for (int z = 0; z < splits; ++z) v += ws[((int64_t)z * M + m) * kRank + c];
+      // 8 partials loaded at a time, added in split order
+      const float* wp = ws + m * kRank + c;
+      const int64_t stride = M * kRank;
+      int z = 0;
+      for (; z + 8 <= splits; z += 8) {
+        float w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = wp[(int64_t)(z + j) * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v += w[j];
+      }
+      for (; z < splits; ++z) v += wp[(int64_t)z * stride];
       v *= alpha;
       if (out_t) out_t[(int64_t)c * ldt + m] = Elem<IT>::from_f32(v);
     }
@@ -299,9 +310,21 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict
   const int64_t total4 = N * kRank / 4;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total4;
        i += (int64_t)gridDim.x * 256) {
+    // 8 partials loaded at a time (independent loads in flight), added in split order
+    const float4* w4 = reinterpret_cast<const float4*>(ws) + i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int z = 0; z < splits; ++z) {
-      const float4 w = reinterpret_cast<const float4*>(ws + (int64_t)z * N * kRank)[i];
+    int z = 0;
+    for (; z + 8 <= splits; z += 8) {
+      float4 w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = w4[(int64_t)(z + j) * total4];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v.x += w[j].x; v.y += w[j].y; v.z += w[j].z; v.w += w[j].w;
+      }
+    }
+    for (; z < splits; ++z) {
+      const float4 w = w4[(int64_t)z * total4];
       v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
     }
     const int64_t n = (4 * i) / kRank, c = 4 * i - n * kRank;

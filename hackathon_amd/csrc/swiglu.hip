@@ -79,25 +79,23 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(
 }
 
 // Row-strided forms for gate / up (and their gradients) that are column ranges of wider
-// buffers, e.g. the two halves of one fused gate|up projection output. One workgroup per row,
-// 8 elements (16 B) per thread per step; cols, leading dimensions and pointers are 16-B
-// granular (checked by the host).
+// buffers, e.g. the two halves of one fused gate|up projection output. A grid-stride loop
+// over the rows x cols/8 vectors of 8 elements (16 B per tensor); cols, leading dimensions and
+// pointers are 16-B granular (checked by the host).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void swiglu_fwd_rows(
     const typename Elem<DT>::T* __restrict__ gate, int64_t ldg,
     const typename Elem<DT>::T* __restrict__ up, int64_t ldu, typename Elem<DT>::T* __restrict__ out,
-    int64_t ldo, int64_t cols) {
-  const int64_t r = blockIdx.x;
-  const auto* gr = gate + r * ldg;
-  const auto* ur = up + r * ldu;
-  auto* orow = out + r * ldo;
-  for (int64_t c = 8 * (int64_t)threadIdx.x; c < cols; c += 8 * kThreads) {
+    int64_t ldo, int64_t cv, int64_t n_vec) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_vec;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = i / cv, c = 8 * (i - r * cv);
     float g[8], u[8], o[8];
-    Vec8<DT>::load(gr + c, g);
-    Vec8<DT>::load(ur + c, u);
+    Vec8<DT>::load(gate + r * ldg + c, g);
+    Vec8<DT>::load(up + r * ldu + c, u);
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = g[j] * sigmoidf(g[j]) * u[j];
-    Vec8<DT>::store(orow + c, o);
+    Vec8<DT>::store(out + r * ldo + c, o);
   }
 }
 
@@ -107,9 +105,10 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_rows(
     const typename Elem<DT>::T* __restrict__ gate, int64_t ldg,
     const typename Elem<DT>::T* __restrict__ up, int64_t ldu,
     typename Elem<DT>::T* __restrict__ dgate, int64_t lddg, typename Elem<DT>::T* __restrict__ dup,
-    int64_t lddu, int64_t cols) {
-  const int64_t r = blockIdx.x;
-  for (int64_t c = 8 * (int64_t)threadIdx.x; c < cols; c += 8 * kThreads) {
+    int64_t lddu, int64_t cv, int64_t n_vec) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_vec;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = i / cv, c = 8 * (i - r * cv);
     float gr[8], g[8], u[8], dg[8], du[8];
     Vec8<DT>::load(grad + r * ldgr + c, gr);
     Vec8<DT>::load(gate + r * ldg + c, g);
@@ -205,14 +204,14 @@ extern "C" int qlora_swiglu_fwd_rows(const void* gate, int64_t ldg, const void* 
   if (!ql_valid_dtype(dtype)) return QL_EDTYPE;
   if (rows == 0 || cols == 0) return QL_OK;
   if (!gate || !up || !out || ldg < cols || ldu < cols || ldo < cols) return QL_EINVAL;
-  if (rows > INT32_MAX) return QL_ESHAPE;
   if (cols % 8 || !rows_ok(gate, ldg, dtype) || !rows_ok(up, ldu, dtype) || !rows_ok(out, ldo, dtype))
     return QL_EALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   QL_DISPATCH_DTYPE(dtype, DT, {
     using T = typename Elem<DT>::T;
-    hipLaunchKernelGGL((swiglu_fwd_rows<DT>), dim3((unsigned)rows), dim3(kThreads), 0, s,
-                       (const T*)gate, ldg, (const T*)up, ldu, (T*)out, ldo, cols);
+    hipLaunchKernelGGL((swiglu_fwd_rows<DT>), dim3(stream_grid(rows * (cols / 8))),
+                       dim3(kThreads), 0, s, (const T*)gate, ldg, (const T*)up, ldu, (T*)out, ldo,
+                       cols / 8, rows * (cols / 8));
     return ql_launch_status();
   });
   return QL_EDTYPE;
@@ -227,16 +226,16 @@ extern "C" int qlora_swiglu_bwd_rows(const void* grad, int64_t ldgr, const void*
   if (rows == 0 || cols == 0) return QL_OK;
   if (!grad || !gate || !up || !dgate || !dup) return QL_EINVAL;
   if (ldgr < cols || ldg < cols || ldu < cols || lddg < cols || lddu < cols) return QL_EINVAL;
-  if (rows > INT32_MAX) return QL_ESHAPE;
   if (cols % 8 || !rows_ok(grad, ldgr, dtype) || !rows_ok(gate, ldg, dtype) ||
       !rows_ok(up, ldu, dtype) || !rows_ok(dgate, lddg, dtype) || !rows_ok(dup, lddu, dtype))
     return QL_EALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   QL_DISPATCH_DTYPE(dtype, DT, {
     using T = typename Elem<DT>::T;
-    hipLaunchKernelGGL((swiglu_bwd_rows<DT>), dim3((unsigned)rows), dim3(kThreads), 0, s,
-                       (const T*)grad, ldgr, (const T*)gate, ldg, (const T*)up, ldu, (T*)dgate,
-                       lddg, (T*)dup, lddu, cols);
+    hipLaunchKernelGGL((swiglu_bwd_rows<DT>), dim3(stream_grid(rows * (cols / 8))),
+                       dim3(kThreads), 0, s, (const T*)grad, ldgr, (const T*)gate, ldg,
+                       (const T*)up, ldu, (T*)dgate, lddg, (T*)dup, lddu, cols / 8,
+                       rows * (cols / 8));
     return ql_launch_status();
   });
   return QL_EDTYPE;
