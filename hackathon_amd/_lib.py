@@ -58,10 +58,10 @@ _SIGNATURES = {
     "qlora_gemm_nt_cat": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr,
                           _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32,
                           _c_ptr, _c_i64, _c_ptr],
-    "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_i64,
-                        _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
-    "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_ptr, _c_int,
-                         _c_f32, _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
+                        _c_i64, _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
+                         _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_pack": [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_f32, _c_int, _c_ptr, _c_ptr, _c_ptr,
                         _c_ptr, _c_int, _c_ptr],
     "qlora_lora_pack_group": [_c_ptr, _c_int, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
@@ -88,8 +88,8 @@ _SIGNATURES = {
 _SIZE_QUERIES = {
     "qlora_gemm_workspace_size": [_c_int, _c_int, _c_i64, _c_i64, _c_i64],
     "qlora_gemm_nt_cat_workspace_size": [_c_i64, _c_i64, _c_i64],
-    "qlora_lora_down_workspace_size": [_c_i64, _c_i64],
-    "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64],
+    "qlora_lora_down_workspace_size": [_c_i64, _c_i64, _c_int],
+    "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_nf4_quantize_workspace_size": [_c_i64, _c_int, _c_int],
     "qlora_attn_bwd_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64],
     "qlora_adamw_chunk_elems": [],
@@ -101,6 +101,9 @@ _lock = threading.Lock()
 
 class KernelLibraryMissing(RuntimeError):
     pass
+
+
+ABI_VERSION = 2  # qlora_abi_version() of the library these signatures describe
 
 
 def load():
@@ -128,6 +131,11 @@ def load():
             fn.restype = ctypes.c_int64
         lib.qlora_abi_version.argtypes = []
         lib.qlora_abi_version.restype = ctypes.c_int
+        version = lib.qlora_abi_version()
+        if version != ABI_VERSION:
+            raise KernelLibraryMissing(
+                f"{LIB_PATH.name} has C-ABI version {version}, these bindings expect "
+                f"{ABI_VERSION}: rebuild it with `python -m hackathon_amd.build`")
         _lib = lib
     return _lib
 

@@ -3,29 +3,39 @@
 // The adapter GEMMs of a LoRA layer (the nn.Linear pair of solution/lora.py:172 and what
 // autograd computes for it) are skinny: one side is the rank r = 16. As plain GEMMs they
 // leave most of the GPU idle (a 4096 x 16 output is 32 tiles of 128 x 128). Two kernels
-// cover them, both streaming the large operand from HBM exactly once:
+// cover them, both streaming the large operand from HBM exactly once, for G = 1 .. 4 adapters
+// ("slots") at a time when the adapters share that operand (the q/k/v or gate/up projections
+// all read the same normalised hidden state):
 //
-//   lora_down   out[m, c] = alpha * sum_k X[m, k] * Y[c, k]        (c < 16)
+//   lora_down   out[m, c] = alpha * sum_k X[m, k] * Y[c, k]        (c < 16 G)
 //               u = x A^T (forward) and du = s * g B (backward, Y = B^T): X [M, K]
-//               k-contiguous, Y [16, K] k-contiguous. Output bf16/fp16 [M, ldo] with
-//               columns 16 .. out_cols-1 zero-filled, so it can serve as the extra
-//               K = 64 segment of the base GEMM.
-//   lora_wgrad  out[n, c] = alpha * sum_m Q[m, n] * P[m, c]        (c < 16), fp32 [N, 16]
+//               k-contiguous, Y [16 G, K] k-contiguous (slot g in rows 16 g .. 16 g + 15).
+//               Output bf16/fp16/fp32 [M, ldo] with columns 16 G .. out_cols-1 zero-filled,
+//               so it can serve as the extra K = 64 segment of the base GEMM.
+//   lora_wgrad  out[n, c] = alpha * sum_m Q[m, n] * P[m, c]        (c < 16 G), fp32 [N, 16 G]
 //               dB = s * g^T u and dA^T = x^T du: the reduction runs over the token rows,
 //               which are the strided dimension of both operands.
 //
-// lora_down: one workgroup (4 waves) per 16 rows and K range. A v_mfma_f32_16x16x32 needs
+// lora_down: one workgroup (8 waves) per 16 rows and K range. A v_mfma_f32_16x16x32 needs
 // 8 consecutive k per lane; the sum over k does not care which 8, so for MFMA t of a 128-k
 // chunk lane l supplies k = 32 t + 8 (l/16) .. +7 of row l%16: each 16-B load instruction
-// then reads 64 contiguous bytes from each of 16 rows. Y is read with the same k map. Waves
-// take alternate 128-k chunks and are summed through LDS.
+// then reads 64 contiguous bytes from each of 16 rows. Y is read with the same k map, one
+// fragment per slot for each fragment of X. Waves take alternate 128-k chunks and are summed
+// through LDS.
 //
-// lora_wgrad: one workgroup per 128 columns and M range. Lane l loads an 8 (rows) x 8
-// (columns) block of Q as eight 16-B row pieces (lanes 0-15 of a row read 256 contiguous
+// lora_wgrad: one workgroup (4 waves) per 128 columns and M range. Lane l loads an 8 (rows) x
+// 8 (columns) block of Q as eight 16-B row pieces (lanes 0-15 of a row read 256 contiguous
 // bytes), transposes it in registers with byte permutes into eight fragments that each hold
-// 8 consecutive rows of one column, and multiplies them by the fragment of P for the same 8
-// rows: MFMA t accumulates columns n0 + 8*(l%16) + t. Waves take alternate 32-row chunks and
-// are summed through LDS.
+// 8 consecutive rows of one column, and multiplies them by each slot's fragment of P for the
+// same 8 rows: MFMA t accumulates columns n0 + 8*(l%16) + t. Waves take alternate 32-row
+// chunks and are summed through LDS.
+//
+// Both main loops are one straight-line block per step: every load of the step is issued
+// before the first wait (a load under a branch, or a select between a load and zero inside
+// the loop, splits the block and the compiler then waits for each load before the next, which
+// leaves a few KiB in flight per wave and the kernel latency-bound). The load addresses are a
+// wave-uniform base (scalar registers) plus a loop-invariant 32-bit lane offset. Partial
+// chunks are handled after the main loop.
 //
 // Both kernels optionally split their reduction over blockIdx.y into an fp32 workspace,
 // summed in split order by the matching reduce kernel (deterministic).
@@ -51,119 +61,154 @@ template <> QL_DEV f32x4_t mfma<QL_F16>(const uint4& a, const uint4& b, f32x4_t 
                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-// Sum a per-lane f32x4 over the 4 waves of the workgroup; the result is valid in wave 0.
-QL_DEV f32x4_t wave_reduce4(f32x4_t v, f32x4_t* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  red[wave * 64 + lane] = v;
-  __syncthreads();
-  f32x4_t s = red[lane];
-#pragma unroll
-  for (int w = 1; w < 4; ++w) s += red[w * 64 + lane];
-  __syncthreads();
-  return s;
-}
-
 // ---------------------------------------------------------------------------------------
-constexpr int kDownUnroll = 4;  // 128-k chunks per wave in flight (16 x 16-B loads per lane)
-constexpr int kDownWaves = 8;   // two waves per SIMD: twice the loads in flight per CU
+constexpr int kMaxSlots = 4;    // rank-16 adapters per launch (a q/k/v or gate/up group)
+constexpr int kDownWaves = 8;   // two waves per SIMD
 
-// Sum a per-lane f32x4 over the kDownWaves waves of the workgroup; valid in wave 0.
-QL_DEV f32x4_t wave_reduce_n(f32x4_t v, f32x4_t* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  red[wave * 64 + lane] = v;
-  __syncthreads();
-  f32x4_t s = red[lane];
-#pragma unroll
-  for (int w = 1; w < kDownWaves; ++w) s += red[w * 64 + lane];
-  return s;
+// 128-k chunks a lora_down wave keeps in flight for G slots.
+template <int G> struct Unroll { static constexpr int value = G == 1 ? 4 : 2; };
+
+// 16-B load from a wave-uniform base plus a per-lane 32-bit byte offset: the global load
+// takes the base in scalar registers, so a stream costs one VGPR of address, not two.
+QL_DEV uint4 ld16(const char* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(base + off);
 }
 
-template <int IT, int OT, bool PARTIAL>
+template <int IT, int OT, bool PARTIAL, int G>
 __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
     int64_t M, int64_t K, int64_t k_per_split, float* __restrict__ ws,
     typename Elem<OT>::T* __restrict__ out, int64_t ldo, int out_cols, float alpha,
     uint16_t* __restrict__ out_t, int64_t ldt) {
-  __shared__ f32x4_t red[kDownWaves * 64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int U = Unroll<G>::value;
+  constexpr int NC = kRank * G;
+  constexpr int64_t kStride = 128 * kDownWaves;
+  __shared__ f32x4_t red[G * kDownWaves * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t m0 = (int64_t)blockIdx.x * 16;
   const int64_t row = m0 + (lane & 15);
-  const int64_t rowc = row < M ? row : M - 1;
+  const int64_t rsub = (row < M ? row : M - 1) - m0;  // rows past M read row M - 1
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
   const int koff = 8 * (lane >> 4);
-  const uint16_t* xr = X + rowc * ldx;
-  const uint16_t* yr = Y + (int64_t)(lane & 15) * ldy;
-  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  // Wave w takes the 128-k chunks w, w + 8, w + 16, ... (slots j = 0 .. J-1) of its K range,
-  // kDownUnroll at a time, starting at slot (blockIdx.x mod J): workgroups running at the
-  // same time then read different parts of Y, which every workgroup reads whole, instead of
-  // all asking the same L2 lines at once. MFMA t of a chunk takes k = chunk + 32 t +
-  // 8 (lane / 16) .. +7: each load instruction reads 64 contiguous bytes of each of the 16
-  // rows. K and every chunk start are multiples of 32, so a 32-k group is all in or all out;
-  // groups past the end load an in-range address and contribute zeros (the MFMAs below must
-  // run with every lane's operands defined, so nothing here is under a lane-dependent branch).
-  constexpr int64_t kStride = 128 * kDownWaves;
-  const int64_t J = (ke - kb + kStride - 1) / kStride;
-  const int64_t rot = J > 0 ? (int64_t)blockIdx.x % J : 0;
-  for (int64_t j0 = 0; j0 < J; j0 += kDownUnroll) {  // uniform per workgroup
-    uint4 xv[kDownUnroll][4], yv[kDownUnroll][4];
+  const char* xb = reinterpret_cast<const char*>(X + m0 * ldx);
+  const char* yb = reinterpret_cast<const char*>(Y);
+  const uint32_t xo = (uint32_t)((rsub * ldx + koff) * 2);
+  uint32_t yo[G];
 #pragma unroll
-    for (int u = 0; u < kDownUnroll; ++u) {
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      if (j0 + u >= J) {  // workgroup-uniform: no slot left, no loads
+  for (int g = 0; g < G; ++g) yo[g] = (uint32_t)(((16 * g + (lane & 15)) * ldy + koff) * 2);
+  f32x4_t acc[G][2];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) xv[u][t] = yv[u][t] = z;
-        continue;
-      }
+  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Slots: wave w takes the 128-k chunks kb + 128 w + kStride j, j = 0 .. J-1. Every slot but
+  // the last is whole for every wave; those are visited first, U per step, starting at slot
+  // blockIdx.x mod (J - 1) so that workgroups running together read different parts of Y
+  // (which every workgroup reads whole). K and the split bounds are multiples of 32, so each
+  // 32-k group of the last slot is all in or all out.
+  const int64_t J = (ke - kb + kStride - 1) / kStride;  // >= 1 for every launched split
+  const int64_t nfull = J - 1;
+  const int64_t rot = nfull > 0 ? (int64_t)blockIdx.x % nfull : 0;
+  const int64_t wk = kb + 128 * wave;
+  int64_t j0 = 0;
+  for (; j0 + U <= nfull; j0 += U) {  // whole slots: loads only, all issued before any wait
+    uint4 xv[U][4], yv[U][G][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
       int64_t js = j0 + u + rot;
-      js = js >= J ? js - J : js;
-      const int64_t c0 = kb + 128 * wave + kStride * js;
+      js = js >= nfull ? js - nfull : js;
+      const int64_t c0 = wk + kStride * js;
+      const char* xc = xb + 2 * c0;
+      const char* yc = yb + 2 * c0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        xv[u][t] = ld16(xc + 64 * t, xo);
+#pragma unroll
+        for (int g = 0; g < G; ++g) yv[u][g][t] = ld16(yc + 64 * t, yo[g]);
+      }
+    }
+    // Keep the scheduler from interleaving the MFMAs (and register reuse) with the loads:
+    // the step's loads all go out before the first wait.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g][t & 1] = mfma<IT>(yv[u][g][t], xv[u][t], acc[g][t & 1]);
+  }
+  {
+    // The rest (at most U slots): the remaining whole slots and the last one. A 32-k group
+    // past ke, or a slot past J - 1, loads the in-range group at kb and contributes zeros; the
+    // conditions are wave-uniform and the loads unconditional.
+    uint4 xv[U][4], yv[U][G][4];
+    bool ok[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + u;
+      int64_t js = j + rot;
+      js = js >= nfull ? js - nfull : js;
+      const int64_t c0 = wk + kStride * (j < nfull ? js : nfull);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int64_t k = c0 + 32 * t;
-        const bool ok = k < ke;
-        const int64_t kk = (ok ? k : kb) + koff;
-        const uint4 xr4 = *reinterpret_cast<const uint4*>(xr + kk);
-        const uint4 yr4 = *reinterpret_cast<const uint4*>(yr + kk);
-        xv[u][t] = ok ? xr4 : z;
-        yv[u][t] = ok ? yr4 : z;
+        ok[u][t] = j < J && k < ke;
+        const int64_t kk = ok[u][t] ? k : kb;
+        xv[u][t] = ld16(xb + 2 * kk, xo);
+#pragma unroll
+        for (int g = 0; g < G; ++g) yv[u][g][t] = ld16(yb + 2 * kk, yo[g]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4 z = make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int u = 0; u < kDownUnroll; ++u) {
-      acc0 = mfma<IT>(yv[u][0], xv[u][0], acc0);
-      acc1 = mfma<IT>(yv[u][1], xv[u][1], acc1);
-      acc0 = mfma<IT>(yv[u][2], xv[u][2], acc0);
-      acc1 = mfma<IT>(yv[u][3], xv[u][3], acc1);
-    }
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          acc[g][t & 1] = mfma<IT>(ok[u][t] ? yv[u][g][t] : z, ok[u][t] ? xv[u][t] : z,
+                                   acc[g][t & 1]);
   }
-  const f32x4_t s = wave_reduce_n(acc0 + acc1, red);
-  if (wave != 0 || row >= M) return;
-  // lane holds out[row][c .. c+3], c = 4 * (lane / 16)
-  const int c = 4 * (lane >> 4);
-  if constexpr (PARTIAL) {
-    *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * kRank + c) =
-        make_float4(s[0], s[1], s[2], s[3]);
-  } else {
-    auto* o = out + row * ldo;
+  // Sum over the waves (in wave order); wave g < G finishes slot g, wave kDownWaves - 1
+  // writes the zero columns NC .. out_cols - 1.
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[c + e] = Elem<OT>::from_f32(alpha * s[e]);
-    for (int z = kRank + c; z < out_cols; z += 16)
+  for (int g = 0; g < G; ++g) red[(g * kDownWaves + wave) * 64 + lane] = acc[g][0] + acc[g][1];
+  __syncthreads();
+  if (row >= M) return;
+  const int c = 4 * (lane >> 4);  // lane holds out[row][16 g + c .. +3]
+  if (wave < G) {
+    const int g = wave;
+    f32x4_t s = red[g * kDownWaves * 64 + lane];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (z + e < out_cols) o[z + e] = Elem<OT>::from_f32(0.f);
-    if (out_t) {  // [16, M]: the 16 lanes of a row group write 32 contiguous bytes per c
+    for (int w = 1; w < kDownWaves; ++w) s += red[(g * kDownWaves + w) * 64 + lane];
+    const int col = kRank * g + c;
+    if constexpr (PARTIAL) {
+      *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * NC + col) =
+          make_float4(s[0], s[1], s[2], s[3]);
+    } else {
+      auto* o = out + row * ldo;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        out_t[(int64_t)(c + e) * ldt + row] = Elem<IT>::from_f32(alpha * s[e]);
+      for (int e = 0; e < 4; ++e) o[col + e] = Elem<OT>::from_f32(alpha * s[e]);
+      if (out_t) {  // [NC, M]: the 16 lanes of a row group write 32 contiguous bytes per column
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          out_t[(int64_t)(col + e) * ldt + row] = Elem<IT>::from_f32(alpha * s[e]);
+      }
     }
+  } else if (!PARTIAL && wave == kDownWaves - 1) {
+    auto* o = out + row * ldo;
+    for (int zc = NC + c; zc < out_cols; zc += 16)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (zc + e < out_cols) o[zc + e] = Elem<OT>::from_f32(0.f);
   }
 }
 
 template <int IT, int OT>
 __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict__ ws, int splits,
-                                                        int64_t M, typename Elem<OT>::T* __restrict__ out,
+                                                        int64_t M, int nc,
+                                                        typename Elem<OT>::T* __restrict__ out,
                                                         int64_t ldo, int out_cols, float alpha,
                                                         uint16_t* __restrict__ out_t, int64_t ldt) {
   const int64_t total = M * out_cols;
@@ -172,10 +217,10 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
     const int64_t m = i / out_cols;
     const int c = (int)(i - m * out_cols);
     float v = 0.f;
-    if (c < kRank) {
+    if (c < nc) {
       // 8 partials loaded at a time, added in split order
-      const float* wp = ws + m * kRank + c;
-      const int64_t stride = M * kRank;
+      const float* wp = ws + m * nc + c;
+      const int64_t stride = M * nc;
       int z = 0;
       for (; z + 8 <= splits; z += 8) {
         float w[8];
@@ -213,101 +258,167 @@ QL_DEV void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
   }
 }
 
-constexpr int kWgradUnroll = 4;  // 32-row chunks per wave in flight
-
-// Store 4 consecutive values (n, c .. c+3) of out [N, 16] (or of its transpose [16, N]).
-QL_DEV void store_wgrad4(float* __restrict__ out, bool out_t, int64_t N, int64_t n, int64_t c,
-                         float4 v) {
+// Store 4 consecutive values (n, c .. c+3) of out [N, nc] (or of its transpose [nc, N]).
+QL_DEV void store_wgrad4(float* __restrict__ out, bool out_t, int64_t N, int nc, int64_t n,
+                         int64_t c, float4 v) {
   if (out_t) {
     out[(c + 0) * N + n] = v.x;
     out[(c + 1) * N + n] = v.y;
     out[(c + 2) * N + n] = v.z;
     out[(c + 3) * N + n] = v.w;
   } else {
-    *reinterpret_cast<float4*>(out + n * kRank + c) = v;
+    *reinterpret_cast<float4*>(out + n * nc + c) = v;
   }
 }
 
-// PARTIAL: each split writes its fp32 [N, 16] partial to ws[split]; lora_wgrad_reduce sums
+// PARTIAL: each split writes its fp32 [N, NC] partial to ws[split]; lora_wgrad_reduce sums
 // them in split order. (Summing inside this launch by the last workgroup of each column block
 // needs device-scope release/acquire fences per workgroup, whose L2 write-back and invalidate
 // cost more than the separate reduce launch.)
-template <int IT, bool PARTIAL>
+// U: 32-row chunks per wave per step of the main loop (the host picks one that divides the
+// chunks of a split, so only a ragged last split reaches the single-chunk loops after it).
+template <int IT, bool PARTIAL, int G, int U>
 __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
     const uint16_t* __restrict__ PT, int64_t ldpt, const uint16_t* __restrict__ Q, int64_t ldq,
     int64_t M, int64_t N, int64_t m_per_split, float* __restrict__ ws, float* __restrict__ out,
     float alpha, bool out_t) {
-  __shared__ f32x4_t red[4 * 64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int NC = kRank * G;
+  __shared__ f32x4_t red[4 * 8 * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int cg = lane & 15;                 // column group: columns n0 + 8 cg .. +7
   const int mq = lane >> 4;                 // rows 8 mq .. 8 mq + 7 of a 32-row chunk
   const int64_t n0 = (int64_t)blockIdx.x * 128;
   const int64_t ncol = n0 + 8 * cg;
   const bool col_ok = ncol < N;             // N % 8 == 0: a group is all in or all out
+  // Lanes past N read columns 0 .. 7 instead: output column j of an MFMA depends only on the
+  // lanes that supply column j, and those sums are never stored.
+  const int64_t ncolc = col_ok ? ncol : 0;
   const int64_t mb = (int64_t)blockIdx.y * m_per_split;
   const int64_t me = mb + m_per_split < M ? mb + m_per_split : M;
-  const uint16_t* ptr_c = PT + (int64_t)cg * ldpt;  // row cg of P^T: P[:, cg], m-contiguous
-  f32x4_t acc[8];
+  const uint32_t qo = (uint32_t)(((int64_t)8 * mq * ldq + ncolc) * 2);
+  const uint32_t ldq2 = (uint32_t)(ldq * 2);
+  uint32_t po[G];  // row 16 g + cg of P^T (P[:, 16 g + cg], m-contiguous), rows 8 mq .. +7
 #pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int64_t m = mb + 32 * wave; m < me; m += 128 * kWgradUnroll) {  // uniform per wave
-    uint4 q[kWgradUnroll][8], pf[kWgradUnroll];
+  for (int g = 0; g < G; ++g) po[g] = (uint32_t)(((int64_t)(16 * g + cg) * ldpt + 8 * mq) * 2);
+  f32x4_t acc[G][8];
 #pragma unroll
-    for (int u = 0; u < kWgradUnroll; ++u) {
-      const int64_t r0 = m + 128 * u + 8 * mq;
-      if (r0 + 8 <= me) {
-        pf[u] = *reinterpret_cast<const uint4*>(ptr_c + r0);
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          q[u][i] = col_ok ? *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncol)
-                           : make_uint4(0, 0, 0, 0);
-      } else {  // rows past the range contribute zeros
+    for (int t = 0; t < 8; ++t) acc[g][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Wave w takes the 32-row chunks mb + 32 w + 128 i; lane l loads rows 8 (l / 16) .. +7 of a
+  // chunk at columns 8 (l % 16) .. +7 as eight 16-B row pieces (lanes 0-15 of a row read 256
+  // contiguous bytes) and the matching 8 rows of P, transposes the block in registers into
+  // eight fragments that each hold 8 consecutive rows of one column, and multiplies them by
+  // P's fragment: MFMA t accumulates column n0 + 8 (l % 16) + t.
+  int64_t m = mb + 32 * wave;
+  for (; m + 128 * (U - 1) + 32 <= me; m += 128 * U) {  // U whole chunks: loads only
+    uint4 q[U][8], pf[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const char* qb = reinterpret_cast<const char*>(Q + (m + 128 * u) * ldq);
+      const char* pb = reinterpret_cast<const char*>(PT + m + 128 * u);
+#pragma unroll
+      for (int g = 0; g < G; ++g) pf[u][g] = ld16(pb, po[g]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[u][i] = ld16(qb, qo + i * ldq2);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the step's loads all go out before the first wait
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint4 qt[8];
+      transpose8x8(q[u], qt);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[u][g], qt[t], acc[g][t]);
+    }
+  }
+  for (; m + 32 <= me; m += 128) {  // whole chunks left (fewer than U), one at a time
+    uint4 q[8], pf[G];
+    const char* qb = reinterpret_cast<const char*>(Q + m * ldq);
+    const char* pb = reinterpret_cast<const char*>(PT + m);
+#pragma unroll
+    for (int g = 0; g < G; ++g) pf[g] = ld16(pb, po[g]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = ld16(qb, qo + i * ldq2);
+    uint4 qt[8];
+    transpose8x8(q, qt);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[g], qt[t], acc[g][t]);
+  }
+  if (m < me) {  // a partial chunk: rows past me contribute zeros
+    const int64_t r0 = m + 8 * mq;
+    uint4 q[8], pf[G];
+    if (r0 + 8 <= me) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        pf[g] = *reinterpret_cast<const uint4*>(PT + (int64_t)(16 * g + cg) * ldpt + r0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        q[i] = *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncolc);
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint16_t* pr = PT + (int64_t)(16 * g + cg) * ldpt;
         uint16_t pv[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const bool ok = r0 + i < me;
-          pv[i] = ok ? ptr_c[r0 + i] : (uint16_t)0;
-          q[u][i] = (ok && col_ok) ? *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncol)
-                                   : make_uint4(0, 0, 0, 0);
-        }
-        pf[u] = make_uint4((uint32_t)pv[0] | ((uint32_t)pv[1] << 16),
+        for (int i = 0; i < 8; ++i) pv[i] = r0 + i < me ? pr[r0 + i] : (uint16_t)0;
+        pf[g] = make_uint4((uint32_t)pv[0] | ((uint32_t)pv[1] << 16),
                            (uint32_t)pv[2] | ((uint32_t)pv[3] << 16),
                            (uint32_t)pv[4] | ((uint32_t)pv[5] << 16),
                            (uint32_t)pv[6] | ((uint32_t)pv[7] << 16));
       }
-    }
 #pragma unroll
-    for (int u = 0; u < kWgradUnroll; ++u) {
-      uint4 qt[8];
-      transpose8x8(q[u], qt);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[t] = mfma<IT>(pf[u], qt[t], acc[t]);
+      for (int i = 0; i < 8; ++i)
+        q[i] = r0 + i < me ? *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncolc)
+                           : make_uint4(0, 0, 0, 0);
     }
+    uint4 qt[8];
+    transpose8x8(q, qt);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[g], qt[t], acc[g][t]);
   }
-  // acc[t]: lane holds out[n = n0 + 8*(lane%16) + t][c = 4*(lane/16) .. +3]
-  const int c = 4 * (lane >> 4);
+  // acc[g][t]: lane holds out[n = ncol + t][16 g + 4 (lane / 16) .. +3]. Per slot: every wave
+  // writes its 8 accumulators, then wave w sums t = 2w, 2w + 1 over the waves in wave order.
+  const int c = 4 * mq;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const f32x4_t s = wave_reduce4(acc[t], red);
-    if (wave == 0 && col_ok) {
-      const int64_t n = ncol + t;
-      if constexpr (PARTIAL) {
-        *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * N + n) * kRank + c) =
-            make_float4(s[0], s[1], s[2], s[3]);
-      } else {
-        store_wgrad4(out, out_t, N, n, c,
-                     make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]));
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) red[(wave * 8 + t) * 64 + lane] = acc[g][t];
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = 2 * wave + h;
+      f32x4_t s = red[t * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) s += red[(w * 8 + t) * 64 + lane];
+      if (col_ok) {
+        const int64_t n = ncol + t;
+        if constexpr (PARTIAL) {
+          *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * N + n) * NC + kRank * g + c) =
+              make_float4(s[0], s[1], s[2], s[3]);
+        } else {
+          store_wgrad4(out, out_t, N, NC, n, kRank * g + c,
+                       make_float4(alpha * s[0], alpha * s[1], alpha * s[2], alpha * s[3]));
+        }
       }
     }
+    __syncthreads();
   }
 }
 
-// out = alpha * sum over splits of ws[split] ([N, 16] fp32 each), in split order; one thread
+// out = alpha * sum over splits of ws[split] ([N, nc] fp32 each), in split order; one thread
 // per 4 consecutive values. splits = 0 writes zeros.
 __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
-                                                         int64_t N, float* __restrict__ out,
-                                                         float alpha, bool out_t) {
-  const int64_t total4 = N * kRank / 4;
+                                                         int64_t N, int nc,
+                                                         float* __restrict__ out, float alpha,
+                                                         bool out_t) {
+  const int64_t total4 = N * nc / 4;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total4;
        i += (int64_t)gridDim.x * 256) {
     // 8 partials loaded at a time (independent loads in flight), added in split order
@@ -327,13 +438,12 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict
       const float4 w = w4[(int64_t)z * total4];
       v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
     }
-    const int64_t n = (4 * i) / kRank, c = 4 * i - n * kRank;
-    store_wgrad4(out, out_t, N, n, c, make_float4(alpha * v.x, alpha * v.y, alpha * v.z,
-                                                  alpha * v.w));
+    const int64_t n = (4 * i) / nc, c = 4 * i - n * nc;
+    store_wgrad4(out, out_t, N, nc, n, c, make_float4(alpha * v.x, alpha * v.y, alpha * v.z,
+                                                      alpha * v.w));
   }
 }
 
-// ---------------------------------------------------------------------------------------
 // The compute-dtype forms of one adapter's fp32 factors A [16, K] and B [N, 16], in one pass:
 //   a16 [16, K]  = A                    (the Y operand of u = x A^T)
 //   at  [K, 64]  = A^T | 0              (the second K segment of the backward dX GEMM)
@@ -461,7 +571,7 @@ unsigned grid1d(int64_t n) {
 // ---- host side -------------------------------------------------------------------------
 
 // Split K only while there are fewer than 256 row groups (one workgroup per CU is enough to
-// stream X at full bandwidth with kDownUnroll chunks in flight per wave).
+// stream X at full bandwidth with a few 128-k chunks in flight per wave).
 int ql_lora_down_splits(int64_t M, int64_t K) {
   const int64_t groups = (M + 15) / 16;
   int s = 1;
@@ -469,43 +579,57 @@ int ql_lora_down_splits(int64_t M, int64_t K) {
   return s;
 }
 
-int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K) {
+int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K, int slots) {
   const int s = ql_lora_down_splits(M, K);
-  return s > 1 ? (int64_t)s * M * kRank : 0;
+  return s > 1 ? (int64_t)s * M * kRank * slots : 0;
 }
 
 int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* Y,
-                 int64_t ldy, int64_t M, int64_t K, void* out, int64_t ldo, int out_cols,
-                 float alpha, void* out_t, int64_t ldt, float* ws, int64_t ws_floats,
-                 hipStream_t s) {
-  if (M <= 0 || K <= 0 || K % 32 || out_cols < kRank || ldo < out_cols) return QL_EINVAL;
+                 int64_t ldy, int64_t M, int64_t K, int slots, void* out, int64_t ldo,
+                 int out_cols, float alpha, void* out_t, int64_t ldt, float* ws,
+                 int64_t ws_floats, hipStream_t s) {
+  if (slots < 1 || slots > kMaxSlots) return QL_EINVAL;
+  const int nc = kRank * slots;
+  if (M <= 0 || K <= 0 || K % 32 || out_cols < nc || ldo < out_cols) return QL_EINVAL;
   if (out_t && ldt < M) return QL_EINVAL;
   if (ldx % 8 || ldy % 8 || !ql_aligned(X, 16) || !ql_aligned(Y, 16)) return QL_EALIGN;
+  // per-lane byte offsets within 16 rows of X and within Y are 32-bit
+  if (ldx < K || ldy < K || 32 * ldx >= (int64_t(1) << 31) || 2 * nc * ldy >= (int64_t(1) << 31))
+    return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   if (out_dtype != QL_BF16 && out_dtype != QL_F16 && out_dtype != QL_F32) return QL_EDTYPE;
   int splits = ql_lora_down_splits(M, K);
-  if (ws_floats < (int64_t)splits * M * kRank || !ws) splits = 1;
+  if (ws_floats < (int64_t)splits * M * nc || !ws) splits = 1;
   // per-split K range: a multiple of 128 k per wave
   constexpr int64_t kq = 128 * kDownWaves;
   int64_t kps = ((K + splits - 1) / splits + kq - 1) / kq * kq;
   splits = (int)((K + kps - 1) / kps);
   const dim3 grid((unsigned)((M + 15) / 16), (unsigned)splits);
-#define QL_DOWN(IT, OT)                                                                      \
-  do {                                                                                       \
-    using T = typename Elem<OT>::T;                                                          \
-    if (splits == 1) {                                                                       \
-      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false>), grid, dim3(64 * kDownWaves), 0, s, \
-                         (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,        \
-                         (float*)nullptr, (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t,   \
-                         ldt);                                                               \
-    } else {                                                                                 \
-      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true>), grid, dim3(64 * kDownWaves), 0, s,  \
-                         (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps, ws,    \
-                         (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);              \
-      hipLaunchKernelGGL((lora_down_reduce<IT, OT>), dim3(grid1d(M * out_cols)), dim3(256),  \
-                         0, s, ws, splits, M, (T*)out, ldo, out_cols, alpha,                 \
-                         (uint16_t*)out_t, ldt);                                             \
-    }                                                                                        \
+#define QL_DOWN_G(IT, OT, G)                                                                  \
+  do {                                                                                        \
+    using T = typename Elem<OT>::T;                                                           \
+    if (splits == 1) {                                                                        \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false, G>), grid, dim3(64 * kDownWaves), 0, \
+                         s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,      \
+                         (float*)nullptr, (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t,    \
+                         ldt);                                                                \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true, G>), grid, dim3(64 * kDownWaves), 0,  \
+                         s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps, ws,  \
+                         (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);               \
+      hipLaunchKernelGGL((lora_down_reduce<IT, OT>), dim3(grid1d(M * out_cols)), dim3(256),   \
+                         0, s, ws, splits, M, nc, (T*)out, ldo, out_cols, alpha,              \
+                         (uint16_t*)out_t, ldt);                                              \
+    }                                                                                         \
+  } while (0)
+#define QL_DOWN(IT, OT)                        \
+  do {                                         \
+    switch (slots) {                           \
+      case 1: QL_DOWN_G(IT, OT, 1); break;     \
+      case 2: QL_DOWN_G(IT, OT, 2); break;     \
+      case 3: QL_DOWN_G(IT, OT, 3); break;     \
+      default: QL_DOWN_G(IT, OT, 4); break;    \
+    }                                          \
   } while (0)
   if (in_dtype == QL_BF16) {
     if (out_dtype == QL_BF16) QL_DOWN(QL_BF16, QL_BF16);
@@ -517,98 +641,126 @@ int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const 
     else QL_DOWN(QL_F16, QL_F32);
   }
 #undef QL_DOWN
+#undef QL_DOWN_G
   return ql_launch_status();
 }
 
-// Split the token range until there are at least 256 workgroups, keeping at least one
+// Split the token range until there are at least 256 workgroups, keeping at least one whole
 // 32-row chunk per wave in each split.
-int ql_lora_wgrad_splits(int64_t M, int64_t N) {
+int ql_lora_wgrad_splits(int64_t M, int64_t N, int slots) {
+  (void)slots;
   const int64_t blocks = (N + 127) / 128;
   int s = 1;
-  while (blocks * s < 256 && M / (128 * 2 * s) >= 1 && s < 64) s *= 2;
+  while (blocks * s < 256 && M >= 128 * 2 * s && s < 64) s *= 2;
   return s;
 }
 
-int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N) {
-  const int s = ql_lora_wgrad_splits(M, N);
-  return s > 1 ? (int64_t)s * N * kRank : 0;
+int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N, int slots) {
+  const int s = ql_lora_wgrad_splits(M, N, slots);
+  return s > 1 ? (int64_t)s * N * kRank * slots : 0;
 }
 
 int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
-                  int64_t M, int64_t N, float* out, int out_t, float alpha, float* ws,
+                  int64_t M, int64_t N, int slots, float* out, int out_t, float alpha, float* ws,
                   int64_t ws_floats, hipStream_t s) {
-  if (M <= 0 || N <= 0 || N % 8 || ldpt < M) return QL_EINVAL;
+  if (slots < 1 || slots > kMaxSlots) return QL_EINVAL;
+  const int nc = kRank * slots;
+  if (M <= 0 || N <= 0 || N % 8 || ldpt < M || ldq < N) return QL_EINVAL;
+  // per-lane byte offsets within 32 rows of Q and within P^T are 32-bit
+  if (64 * ldq >= (int64_t(1) << 31) || 2 * nc * ldpt >= (int64_t(1) << 31)) return QL_EINVAL;
   if (ldq % 8 || ldpt % 8 || !ql_aligned(Q, 16) || !ql_aligned(PT, 16) || !ql_aligned(out, 16))
     return QL_EALIGN;
   if (out_t != 0 && out_t != 1) return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
-  int splits = ql_lora_wgrad_splits(M, N);
-  if (ws_floats < (int64_t)splits * N * kRank || !ws) splits = 1;
+  int splits = ql_lora_wgrad_splits(M, N, slots);
+  if (ws_floats < (int64_t)splits * N * nc || !ws) splits = 1;
   int64_t mps = ((M + splits - 1) / splits + 127) / 128 * 128;
   splits = (int)((M + mps - 1) / mps);
   const dim3 grid((unsigned)((N + 127) / 128), (unsigned)splits);
-#define QL_WGRAD(IT)                                                                         \
-  do {                                                                                       \
-    if (splits == 1) {                                                                       \
-      hipLaunchKernelGGL((lora_wgrad_kernel<IT, false>), grid, dim3(kThreads), 0, s,         \
-                         (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps,      \
-                         (float*)nullptr, out, alpha, out_t);                                \
-    } else {                                                                                 \
-      hipLaunchKernelGGL((lora_wgrad_kernel<IT, true>), grid, dim3(kThreads), 0, s,          \
-                         (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,  \
-                         out, alpha, out_t);                                                 \
-      hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0, s, ws,    \
-                         splits, N, out, alpha, out_t);                                      \
-    }                                                                                        \
+  // chunks per wave per step: the largest of 4 (one slot) or 2 (several; their accumulators
+  // take the registers) that divides a split's mps / 128 chunks per wave
+  const int64_t per_wave = mps / 128;
+  const int unroll = (slots == 1 && per_wave % 4 == 0) ? 4 : (per_wave % 2 == 0 ? 2 : 1);
+#define QL_WGRAD_GU(IT, G, U)                                                                 \
+  do {                                                                                        \
+    if (splits == 1) {                                                                        \
+      hipLaunchKernelGGL((lora_wgrad_kernel<IT, false, G, U>), grid, dim3(kThreads), 0, s,    \
+                         (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps,       \
+                         (float*)nullptr, out, alpha, out_t);                                 \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U>), grid, dim3(kThreads), 0, s,     \
+                         (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,   \
+                         out, alpha, out_t);                                                  \
+      hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * nc / 4)), dim3(256), 0, s, ws,    \
+                         splits, N, nc, out, alpha, out_t);                                   \
+    }                                                                                         \
+  } while (0)
+#define QL_WGRAD_G(IT, G)                                          \
+  do {                                                             \
+    if (unroll == 4) QL_WGRAD_GU(IT, G, (G == 1 ? 4 : 2));         \
+    else if (unroll == 2) QL_WGRAD_GU(IT, G, 2);                   \
+    else QL_WGRAD_GU(IT, G, 1);                                    \
+  } while (0)
+#define QL_WGRAD(IT)                         \
+  do {                                       \
+    switch (slots) {                         \
+      case 1: QL_WGRAD_G(IT, 1); break;      \
+      case 2: QL_WGRAD_G(IT, 2); break;      \
+      case 3: QL_WGRAD_G(IT, 3); break;      \
+      default: QL_WGRAD_G(IT, 4); break;     \
+    }                                        \
   } while (0)
   if (in_dtype == QL_BF16) QL_WGRAD(QL_BF16);
   else QL_WGRAD(QL_F16);
 #undef QL_WGRAD
+#undef QL_WGRAD_G
+#undef QL_WGRAD_GU
   return ql_launch_status();
 }
 
 // ---- C-ABI -------------------------------------------------------------------------------
 
-extern "C" int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K) {
-  if (M <= 0 || K <= 0) return 0;
-  return ql_lora_down_workspace_floats(M, K) * (int64_t)sizeof(float);
+extern "C" int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K, int slots) {
+  if (M <= 0 || K <= 0 || slots < 1 || slots > kMaxSlots) return 0;
+  return ql_lora_down_workspace_floats(M, K, slots) * (int64_t)sizeof(float);
 }
 
 extern "C" int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_t ldy, int64_t M,
-                               int64_t K, int in_dtype, void* out, int64_t ldo, int out_cols,
-                               int out_dtype, float alpha, void* out_t, int64_t ldt,
+                               int64_t K, int slots, int in_dtype, void* out, int64_t ldo,
+                               int out_cols, int out_dtype, float alpha, void* out_t, int64_t ldt,
                                void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
   if (M < 0 || K < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (M == 0) return QL_OK;
   if (!X || !Y || !out) return QL_EINVAL;
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
   if (out_t && !ql_aligned(out_t, 2)) return QL_EALIGN;
-  return ql_lora_down(in_dtype, out_dtype, X, ldx, Y, ldy, M, K, out, ldo, out_cols, alpha,
-                      out_t, ldt, static_cast<float*>(workspace),
+  return ql_lora_down(in_dtype, out_dtype, X, ldx, Y, ldy, M, K, slots, out, ldo, out_cols,
+                      alpha, out_t, ldt, static_cast<float*>(workspace),
                       workspace_bytes / (int64_t)sizeof(float),
                       static_cast<hipStream_t>(stream));
 }
 
-extern "C" int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N) {
-  if (M <= 0 || N <= 0) return 0;
-  return ql_lora_wgrad_workspace_floats(M, N) * (int64_t)sizeof(float);
+extern "C" int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N, int slots) {
+  if (M <= 0 || N <= 0 || slots < 1 || slots > kMaxSlots) return 0;
+  return ql_lora_wgrad_workspace_floats(M, N, slots) * (int64_t)sizeof(float);
 }
 
 extern "C" int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M,
-                                int64_t N, int in_dtype, float* out, int out_transposed,
-                                float alpha, void* workspace, int64_t workspace_bytes,
-                                ql_stream_t stream) {
-  if (M < 0 || N < 0 || workspace_bytes < 0) return QL_EINVAL;
+                                int64_t N, int slots, int in_dtype, float* out,
+                                int out_transposed, float alpha, void* workspace,
+                                int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || N < 0 || workspace_bytes < 0 || slots < 1 || slots > kMaxSlots) return QL_EINVAL;
   if (N == 0) return QL_OK;
   if (!PT || !Q || !out) return QL_EINVAL;
   if (M == 0) {  // an empty reduction: zeros (a fill kernel, not a memset node)
-    hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank)), dim3(256), 0,
+    if (!ql_aligned(out, 16)) return QL_EALIGN;
+    hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank * slots / 4)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), (const float*)nullptr, 0, N,
-                       out, 0.f, out_transposed != 0);
+                       kRank * slots, out, 0.f, out_transposed != 0);
     return ql_launch_status();
   }
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
-  return ql_lora_wgrad(in_dtype, PT, ldpt, Q, ldq, M, N, out, out_transposed, alpha,
+  return ql_lora_wgrad(in_dtype, PT, ldpt, Q, ldq, M, N, slots, out, out_transposed, alpha,
                        static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
                        static_cast<hipStream_t>(stream));
 }

@@ -4,14 +4,15 @@ In the reference each projection is its own peft 4-bit LoRA layer (solution/lora
 solution/nf4.py:95-149): q, k and v read the same normalised hidden state, and so do gate and
 up. Here each group runs as one fused computation with the same sums:
 
-  forward   u_g = x A_g^T for every projection g            qlora_lora_down into column slot g
+  forward   u_g = x A_g^T for every projection g            qlora_lora_down, all slots at once
             [y_1 | y_2 | ..] = [x | u] [W_cat | sB_cat]^T + b  qlora_gemm_nt_cat into column ranges
                                                             of one output (W_g dequantised into
                                                             row ranges of one buffer; slot g of
                                                             sB_cat holds s_g B_g in g's rows)
   backward  du_g = s_g dY_g B_g                              qlora_lora_down into slot g
             dx = [dY_1 | dY_2 | .. | du] [W_cat^T | A_cat^T]^T  one GEMM over the concatenated K
-            dA_g = du_g^T x,  dB_g = s_g dY_g^T u_g          qlora_lora_wgrad per projection
+            dA_g = du_g^T x                                 qlora_lora_wgrad, all slots at once
+            dB_g = s_g dY_g^T u_g                           qlora_lora_wgrad per projection
 
 so the gradient that autograd would otherwise assemble from one dX GEMM per projection plus the
 element-wise adds becomes one fp32 accumulation. The attention group also applies RoPE (the q
@@ -133,8 +134,7 @@ def group_forward(x2, specs, ab):
         nf4.dequantize_nf4(s.packed, s.qs, dt, out=w[offs[g]:offs[g + 1]])
     u = torch.empty((M, _PAD), dtype=dt, device=dev)
     ut = _t_buffer(16 * G, M, dt, dev)
-    for g in range(G):  # ascending: slot g's zero fill of the later columns is overwritten
-        _gemm.lora_down(x2, a16[16 * g:16 * g + 16], u[:, 16 * g:], out_t=ut[16 * g:16 * g + 16])
+    _gemm.lora_down(x2, a16, u, out_t=ut)  # every slot in one pass over x
     y = torch.empty((M, offs[-1]), dtype=dt, device=dev)
     bias = _bias_cat(specs, dt, dev)
     for p0, p1 in _column_blocks(specs):
@@ -166,10 +166,13 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab):
         _gemm.gemm_nt_cat(g, wt, du, at, dx)
         del wt
     grads = []
+    da_all = None
+    if any(need_ab[0::2]):  # dA_g^T for every slot in one pass over x: [16 G, K]
+        da_all = _gemm.lora_wgrad(dut, x2, transposed=True)
     for i, s in enumerate(specs):
         da = db = None
         if need_ab[2 * i]:
-            da = _gemm.lora_wgrad(dut[16 * i:16 * i + 16], x2, transposed=True)
+            da = da_all[16 * i:16 * i + 16]
         if need_ab[2 * i + 1]:
             db = _gemm.lora_wgrad(ut[16 * i:16 * i + 16], g[:, offs[i]:offs[i + 1]],
                                   alpha=s.scaling)

@@ -131,35 +131,47 @@ def gemm_nt_cat(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None,
     return out
 
 
+def _slots(rows: int, what: str) -> int:
+    if rows % 16 or not 16 <= rows <= 64:
+        raise ValueError(f"{what} must have 16, 32, 48 or 64 rows (1-4 rank-16 adapters), got {rows}")
+    return rows // 16
+
+
 def lora_down(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, alpha: float = 1.0,
               out_t: torch.Tensor | None = None) -> torch.Tensor:
-    """out[:, :16] = alpha * x @ y^T (y [16, K]) and out[:, 16:] = 0 (qlora_lora_down); with
-    `out_t` ([16, >= M], x's dtype) also the 16 columns transposed, the operand lora_wgrad
-    takes."""
+    """out[:, :16G] = alpha * x @ y^T (y [16G, K]: G <= 4 rank-16 adapters that read x) and
+    out[:, 16G:] = 0 (qlora_lora_down, x read once); with `out_t` ([16G, >= M], x's dtype)
+    also the 16G columns transposed, the operand lora_wgrad takes."""
     M, K = x.shape
-    ws, ws_bytes = _lib.workspace("qlora_lora_down_workspace_size", M, K, device=x.device)
+    slots = _slots(y.shape[0], "y")
+    ws, ws_bytes = _lib.workspace("qlora_lora_down_workspace_size", M, K, slots, device=x.device)
     _lib.call("qlora_lora_down", x.data_ptr(), x.stride(0), y.data_ptr(), y.stride(0), M, K,
-              _lib.tag(x.dtype), out.data_ptr(), out.stride(0), out.shape[1], _lib.tag(out.dtype),
-              float(alpha), _lib.ptr(out_t), out_t.stride(0) if out_t is not None else 0,
-              _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+              slots, _lib.tag(x.dtype), out.data_ptr(), out.stride(0), out.shape[1],
+              _lib.tag(out.dtype), float(alpha), _lib.ptr(out_t),
+              out_t.stride(0) if out_t is not None else 0, _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(x))
     return out
 
 
-def lora_t_buffer(m: int, dtype, device) -> torch.Tensor:
-    """A [16, m] buffer for lora_down's transposed output (row stride a multiple of 8)."""
-    return torch.empty((16, (m + 7) // 8 * 8), dtype=dtype, device=device)[:, :m]
+def lora_t_buffer(m: int, dtype, device, rows: int = 16) -> torch.Tensor:
+    """A [rows, m] buffer for lora_down's transposed output (row stride a multiple of 8)."""
+    return torch.empty((rows, (m + 7) // 8 * 8), dtype=dtype, device=device)[:, :m]
 
 
 def lora_wgrad(pt: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
                transposed: bool = False) -> torch.Tensor:
-    """fp32 alpha * q^T @ pt^T for q [M, N] and pt [16, M] (token-contiguous, as lora_down's
-    `out_t`) (qlora_lora_wgrad): [N, 16], or [16, N] when `transposed`."""
+    """fp32 alpha * q^T @ pt^T for q [M, N] and pt [16G, M] (token-contiguous, as lora_down's
+    `out_t`; G <= 4 adapters whose gradients reduce over the same q, q read once)
+    (qlora_lora_wgrad): [N, 16G], or [16G, N] when `transposed`."""
     M, N = q.shape
-    out = torch.empty((16, N) if transposed else (N, 16), dtype=torch.float32, device=q.device)
-    ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_workspace_size", M, N, device=q.device)
+    slots = _slots(pt.shape[0], "pt")
+    nc = 16 * slots
+    out = torch.empty((nc, N) if transposed else (N, nc), dtype=torch.float32, device=q.device)
+    ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_workspace_size", M, N, slots,
+                                  device=q.device)
     _lib.call("qlora_lora_wgrad", pt.data_ptr(), pt.stride(0), q.data_ptr(), q.stride(0), M, N,
-              _lib.tag(q.dtype), out.data_ptr(), int(transposed), float(alpha), _lib.ptr(ws),
-              ws_bytes, _lib.stream_of(q))
+              slots, _lib.tag(q.dtype), out.data_ptr(), int(transposed), float(alpha),
+              _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
     return out
 
 

@@ -37,7 +37,8 @@ enum {
 
 typedef void* ql_stream_t; /* hipStream_t */
 
-/* Library identification and error text. */
+/* Library identification and error text. qlora_abi_version() is 2 for the signatures in this
+ * file (version 1 had no `slots` argument in the qlora_lora_down / qlora_lora_wgrad family). */
 int qlora_abi_version(void);
 const char* qlora_strerror(int status);
 
@@ -298,34 +299,39 @@ int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
                       ql_stream_t stream);
 
 /*
- * LoRA down-projection (rank 16): out[m, c] = alpha * sum_k X[m,k] Y[c,k] for c < 16, and
- * out[m, c] = 0 for 16 <= c < out_cols (the zero padding the GEMM segment above reads).
- * u = x A^T in forward (Y = A [16, in]); du = s * g B in backward (Y = B^T [16, out]).
- * When out_t is not NULL the 16 columns are also written transposed, out_t[c * ldt + m]
- * (ldt >= M, in_dtype): the token-contiguous operand qlora_lora_wgrad takes.
- * K % 32 == 0; X, Y 16-B aligned with ldx, ldy multiples of 8; in_dtype QL_BF16/QL_F16;
- * out_dtype QL_BF16/QL_F16/QL_F32. Streams X from HBM once.
+ * LoRA down-projection (rank 16) for `slots` = G adapters (1 <= G <= 4) that share X:
+ *   out[m, c] = alpha * sum_k X[m,k] Y[c,k]  for c < 16 G   (Y [16 G, K]: adapter g in rows
+ *                                                            16 g .. 16 g + 15)
+ *   out[m, c] = 0  for 16 G <= c < out_cols   (the zero padding the GEMM segment above reads).
+ * u = x A^T in forward (Y = A [16, in], or the A of q/k/v stacked); du = s * g B in backward
+ * (Y = B^T [16, out]). When out_t is not NULL the 16 G columns are also written transposed,
+ * out_t[c * ldt + m] (ldt >= M, in_dtype): the token-contiguous operand qlora_lora_wgrad
+ * takes. K % 32 == 0; X, Y 16-B aligned with ldx, ldy multiples of 8, ldx, ldy >= K,
+ * 32 * ldx < 2^31 and 32 * G * ldy < 2^31; in_dtype QL_BF16/QL_F16; out_dtype
+ * QL_BF16/QL_F16/QL_F32. Streams X from HBM once for all G adapters.
  * Replaces: solution/lora.py:172 (lora_A(x)) and its autograd backward through lora_B.
  */
-int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K);
+int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K, int slots);
 int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_t ldy, int64_t M, int64_t K,
-                    int in_dtype, void* out, int64_t ldo, int out_cols, int out_dtype,
+                    int slots, int in_dtype, void* out, int64_t ldo, int out_cols, int out_dtype,
                     float alpha, void* out_t, int64_t ldt, void* workspace,
                     int64_t workspace_bytes, ql_stream_t stream);
 
 /*
- * LoRA weight gradient (rank 16), a reduction over the token rows:
- *   out[n, c] = alpha * sum_m Q[m, n] * PT[c, m]     (fp32 [N, 16], c < 16; stored [16, N]
- *                                                     when out_transposed = 1)
- * dB = s * g^T u (PT = u^T, Q = g); dA^T = x^T du (PT = du^T, Q = x); PT is the transposed
- * output of qlora_lora_down. N % 8 == 0; Q 16-B aligned with ldq a multiple of 8; PT
- * [16, ldpt >= M] 16-B aligned with ldpt a multiple of 8; out 16-B aligned.
+ * LoRA weight gradient (rank 16) for `slots` = G adapters that share Q, a reduction over the
+ * token rows:
+ *   out[n, c] = alpha * sum_m Q[m, n] * PT[c, m]     (fp32 [N, 16 G], c < 16 G; stored
+ *                                                     [16 G, N] when out_transposed = 1)
+ * dB = s * g^T u (PT = u^T, Q = g); dA^T = x^T du (PT = du^T stacked over the adapters that
+ * read x, Q = x); PT is the transposed output of qlora_lora_down. N % 8 == 0; Q 16-B aligned
+ * with ldq a multiple of 8, N <= ldq, 64 * ldq < 2^31; PT [16 G, ldpt >= M] 16-B aligned with
+ * ldpt a multiple of 8, 32 * G * ldpt < 2^31; out 16-B aligned.
  * Replaces: the autograd weight gradients of solution/lora.py:172 (lora_A / lora_B).
  */
-int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N);
+int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N, int slots);
 int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M, int64_t N,
-                     int in_dtype, float* out, int out_transposed, float alpha, void* workspace,
-                     int64_t workspace_bytes, ql_stream_t stream);
+                     int slots, int in_dtype, float* out, int out_transposed, float alpha,
+                     void* workspace, int64_t workspace_bytes, ql_stream_t stream);
 
 /*
  * The compute-dtype operands of one rank-16 adapter, from its fp32 factors A [16, K] and

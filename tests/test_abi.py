@@ -48,7 +48,7 @@ def test_binding_covers_exactly_the_header():
 
 
 def test_version_and_error_text(lib):
-    assert lib.qlora_abi_version() >= 1
+    assert lib.qlora_abi_version() == _lib.ABI_VERSION
     assert lib.qlora_strerror(0) == b"ok"
     assert b"dtype" in lib.qlora_strerror(-2)
 
@@ -95,6 +95,18 @@ def test_rejected_arguments_return_codes(lib):
     # cat gemm: the two K segments may not both exceed 128 (the short one is loaded up front)
     assert lib.qlora_gemm_nt_cat(256, 256, 256, fake, 256, fake, 256, 192, fake, 192, fake, 192,
                                  2, fake, 256, 2, None, 1.0, None, 0, None) == -4
+    # rank-16 LoRA kernels: 1 to 4 adapters per call; the workspace query is 0 outside that
+    assert lib.qlora_lora_down(fake, 64, fake, 64, 16, 64, 0, 2, fake, 64, 64, 2, 1.0, None, 0,
+                               None, 0, None) == -1
+    assert lib.qlora_lora_down(fake, 64, fake, 64, 16, 64, 5, 2, fake, 64, 64, 2, 1.0, None, 0,
+                               None, 0, None) == -1
+    # ... the output must hold the 16 G adapter columns
+    assert lib.qlora_lora_down(fake, 64, fake, 64, 16, 64, 3, 2, fake, 64, 32, 2, 1.0, None, 0,
+                               None, 0, None) == -1
+    assert lib.qlora_lora_wgrad(fake, 64, fake, 64, 64, 64, 5, 2, fake, 0, 1.0, None, 0,
+                                None) == -1
+    assert lib.qlora_lora_down_workspace_size(4096, 3584, 0) == 0
+    assert lib.qlora_lora_wgrad_workspace_size(4096, 3584, 5) == 0
     # adamw: a table is required when there is work; the bias correction must be positive
     assert lib.qlora_adamw_fp32(None, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 1.0, 1e-8, None) == -1
     assert lib.qlora_adamw_fp32(fake, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 0.0, 1e-8, None) == -1

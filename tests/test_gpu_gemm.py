@@ -228,6 +228,52 @@ def test_lora_wgrad(M, N):
     assert torch.equal(out, gemm.lora_wgrad(pt_dev, q.cuda(), alpha=0.5))  # deterministic
 
 
+@pytest.mark.parametrize("M,K,G,out_cols", [(4096, 3584, 3, 64), (1000, 512, 2, 32),
+                                            (77, 96, 4, 64), (512, 8192, 3, 48),
+                                            (4096, 18944, 2, 64)])
+def test_lora_down_slots(M, K, G, out_cols):
+    """G adapters in one pass over x: out[:, :16G] = alpha x y^T for y [16G, K], zeros after,
+    the transposed copy exact, and each slot bit-identical to a single-adapter call (the same
+    chunks reach the same accumulator in the same order)."""
+    print(f"lora_down slots={G} M={M} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M + K + G)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    y = (torch.randn(16 * G, K, generator=g) * 0.25).to(torch.bfloat16)
+    ref = 2.0 * (x.double() @ y.double().t())
+    xd, yd = x.cuda(), y.cuda()
+    out = torch.full((M, out_cols), 3.0, dtype=torch.bfloat16, device="cuda")
+    out_t = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=16 * G)
+    gemm.lora_down(xd, yd, out, alpha=2.0, out_t=out_t)
+    bound = 2 * 4 * 2.0**-22 * K * x.abs().max().item() * y.abs().max().item() + 2.0**-8 * ref.abs()
+    assert torch.all((out[:, :16 * G].double().cpu() - ref).abs() <= bound)
+    assert torch.all(out[:, 16 * G:] == 0)
+    assert torch.equal(out_t, out[:, :16 * G].t())
+    for s in range(G):
+        one = torch.empty((M, 16), dtype=torch.bfloat16, device="cuda")
+        gemm.lora_down(xd, yd[16 * s:16 * s + 16].contiguous(), one, alpha=2.0)
+        assert torch.equal(one, out[:, 16 * s:16 * s + 16]), s
+
+
+@pytest.mark.parametrize("M,N,G", [(4096, 3584, 3), (4096, 3584, 2), (100, 520, 2),
+                                   (1000, 3584, 4), (33, 8, 3), (4096, 18944, 2)])
+def test_lora_wgrad_slots(M, N, G):
+    """G adapters' gradients in one pass over q: fp32 [N, 16G] = alpha q^T pt^T for pt
+    [16G, M], and its transposed form exact."""
+    print(f"lora_wgrad slots={G} M={M} N={N}", flush=True)
+    g = torch.Generator().manual_seed(M * 5 + N + G)
+    q = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    pt = torch.randn(16 * G, M, generator=g).to(torch.bfloat16)
+    ref = 0.5 * (q.double().t() @ pt.double().t())
+    pt_dev = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=16 * G)
+    pt_dev.copy_(pt)
+    qd = q.cuda()
+    out = gemm.lora_wgrad(pt_dev, qd, alpha=0.5)
+    assert out.shape == (N, 16 * G) and out.dtype == torch.float32
+    bound = 0.5 * 4 * 2.0**-22 * M * q.abs().max().item() * pt.abs().max().item()
+    assert torch.all((out.double().cpu() - ref).abs() <= bound)
+    assert torch.equal(gemm.lora_wgrad(pt_dev, qd, alpha=0.5, transposed=True), out.t())
+
+
 @pytest.mark.parametrize("K,N", [(3584, 512), (256, 18944), (8, 8)])
 def test_lora_pack_is_exact(K, N):
     """The packed adapter operands equal torch's own casts of A, A^T, s*B and B^T (RNE)."""
