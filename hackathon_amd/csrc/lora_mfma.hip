@@ -65,8 +65,14 @@ template <> QL_DEV f32x4_t mfma<QL_F16>(const uint4& a, const uint4& b, f32x4_t 
 constexpr int kMaxSlots = 4;    // rank-16 adapters per launch (a q/k/v or gate/up group)
 constexpr int kDownWaves = 8;   // two waves per SIMD
 
-// 128-k chunks a lora_down wave keeps in flight for G slots.
-template <int G> struct Unroll { static constexpr int value = G == 1 ? 4 : 2; };
+// R: 16-row groups per lora_down workgroup. Each fragment of Y is loaded once for R fragments
+// of X: a fragment of Y served from L2 costs the load path as much as one of X from HBM, and
+// at R = 1 (one fragment of each) a read-pattern probe streamed X at 3.1 TB/s against 5.5
+// without the Y loads (4.2 at R = 2, 4.9 at R = 4).
+// U: 128-k chunks a wave keeps in flight per step.
+template <int G, int R> struct DownUnroll {
+  static constexpr int value = R == 1 ? (G == 1 ? 4 : 2) : 2;
+};
 
 // 16-B load from a wave-uniform base plus a per-lane 32-bit byte offset: the global load
 // takes the base in scalar registers, so a stream costs one VGPR of address, not two.
@@ -74,33 +80,38 @@ QL_DEV uint4 ld16(const char* base, uint32_t off) {
   return *reinterpret_cast<const uint4*>(base + off);
 }
 
-template <int IT, int OT, bool PARTIAL, int G>
+template <int IT, int OT, bool PARTIAL, int G, int R>
 __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
     int64_t M, int64_t K, int64_t k_per_split, float* __restrict__ ws,
     typename Elem<OT>::T* __restrict__ out, int64_t ldo, int out_cols, float alpha,
     uint16_t* __restrict__ out_t, int64_t ldt) {
-  constexpr int U = Unroll<G>::value;
+  constexpr int U = DownUnroll<G, R>::value;
   constexpr int NC = kRank * G;
   constexpr int64_t kStride = 128 * kDownWaves;
-  __shared__ f32x4_t red[G * kDownWaves * 64];
+  __shared__ f32x4_t red[R * G * kDownWaves * 64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t m0 = (int64_t)blockIdx.x * 16;
-  const int64_t row = m0 + (lane & 15);
-  const int64_t rsub = (row < M ? row : M - 1) - m0;  // rows past M read row M - 1
+  const int64_t m0 = (int64_t)blockIdx.x * 16 * R;
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
   const int koff = 8 * (lane >> 4);
   const char* xb = reinterpret_cast<const char*>(X + m0 * ldx);
   const char* yb = reinterpret_cast<const char*>(Y);
-  const uint32_t xo = (uint32_t)((rsub * ldx + koff) * 2);
+  uint32_t xo[R];  // row m0 + 16 r + lane % 16; rows past M read row M - 1
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = m0 + 16 * r + (lane & 15);
+    xo[r] = (uint32_t)((((row < M ? row : M - 1) - m0) * ldx + koff) * 2);
+  }
   uint32_t yo[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) yo[g] = (uint32_t)(((16 * g + (lane & 15)) * ldy + koff) * 2);
-  f32x4_t acc[G][2];
+  f32x4_t acc[R][G][2];
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[r][g][0] = acc[r][g][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // Slots: wave w takes the 128-k chunks kb + 128 w + kStride j, j = 0 .. J-1. Every slot but
   // the last is whole for every wave; those are visited first, U per step, starting at slot
   // blockIdx.x mod (J - 1) so that workgroups running together read different parts of Y
@@ -112,7 +123,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
   const int64_t wk = kb + 128 * wave;
   int64_t j0 = 0;
   for (; j0 + U <= nfull; j0 += U) {  // whole slots: loads only, all issued before any wait
-    uint4 xv[U][4], yv[U][G][4];
+    uint4 xv[U][R][4], yv[U][G][4];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       int64_t js = j0 + u + rot;
@@ -122,7 +133,8 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
       const char* yc = yb + 2 * c0;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        xv[u][t] = ld16(xc + 64 * t, xo);
+#pragma unroll
+        for (int r = 0; r < R; ++r) xv[u][r][t] = ld16(xc + 64 * t, xo[r]);
 #pragma unroll
         for (int g = 0; g < G; ++g) yv[u][g][t] = ld16(yc + 64 * t, yo[g]);
       }
@@ -135,13 +147,16 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc[g][t & 1] = mfma<IT>(yv[u][g][t], xv[u][t], acc[g][t & 1]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+            acc[r][g][t & 1] = mfma<IT>(yv[u][g][t], xv[u][r][t], acc[r][g][t & 1]);
   }
   {
     // The rest (at most U slots): the remaining whole slots and the last one. A 32-k group
     // past ke, or a slot past J - 1, loads the in-range group at kb and contributes zeros; the
     // conditions are wave-uniform and the loads unconditional.
-    uint4 xv[U][4], yv[U][G][4];
+    uint4 xv[U][R][4], yv[U][G][4];
     bool ok[U][4];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -154,7 +169,8 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
         const int64_t k = c0 + 32 * t;
         ok[u][t] = j < J && k < ke;
         const int64_t kk = ok[u][t] ? k : kb;
-        xv[u][t] = ld16(xb + 2 * kk, xo);
+#pragma unroll
+        for (int r = 0; r < R; ++r) xv[u][r][t] = ld16(xb + 2 * kk, xo[r]);
 #pragma unroll
         for (int g = 0; g < G; ++g) yv[u][g][t] = ld16(yb + 2 * kk, yo[g]);
       }
@@ -166,22 +182,28 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int g = 0; g < G; ++g)
-          acc[g][t & 1] = mfma<IT>(ok[u][t] ? yv[u][g][t] : z, ok[u][t] ? xv[u][t] : z,
-                                   acc[g][t & 1]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+            acc[r][g][t & 1] = mfma<IT>(ok[u][t] ? yv[u][g][t] : z, ok[u][t] ? xv[u][r][t] : z,
+                                        acc[r][g][t & 1]);
   }
-  // Sum over the waves (in wave order); wave g < G finishes slot g, wave kDownWaves - 1
-  // writes the zero columns NC .. out_cols - 1.
+  // Sum over the waves (in wave order): wave w finishes the (row group, slot) pairs w, w + 8,
+  // ...; wave kDownWaves - 1 - r writes the zero columns NC .. out_cols - 1 of row group r.
 #pragma unroll
-  for (int g = 0; g < G; ++g) red[(g * kDownWaves + wave) * 64 + lane] = acc[g][0] + acc[g][1];
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      red[((r * G + g) * kDownWaves + wave) * 64 + lane] = acc[r][g][0] + acc[r][g][1];
   __syncthreads();
-  if (row >= M) return;
   const int c = 4 * (lane >> 4);  // lane holds out[row][16 g + c .. +3]
-  if (wave < G) {
-    const int g = wave;
-    f32x4_t s = red[g * kDownWaves * 64 + lane];
+  for (int p = wave; p < R * G; p += kDownWaves) {
+    const int r = p / G, g = p - (p / G) * G;
+    const int64_t row = m0 + 16 * r + (lane & 15);
+    if (row >= M) continue;
+    f32x4_t s = red[p * kDownWaves * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < kDownWaves; ++w) s += red[(g * kDownWaves + w) * 64 + lane];
+    for (int w = 1; w < kDownWaves; ++w) s += red[(p * kDownWaves + w) * 64 + lane];
     const int col = kRank * g + c;
     if constexpr (PARTIAL) {
       *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * NC + col) =
@@ -196,12 +218,18 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
           out_t[(int64_t)(col + e) * ldt + row] = Elem<IT>::from_f32(alpha * s[e]);
       }
     }
-  } else if (!PARTIAL && wave == kDownWaves - 1) {
-    auto* o = out + row * ldo;
-    for (int zc = NC + c; zc < out_cols; zc += 16)
+  }
+  if constexpr (!PARTIAL) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (zc + e < out_cols) o[zc + e] = Elem<OT>::from_f32(0.f);
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = m0 + 16 * r + (lane & 15);
+      if (wave != kDownWaves - 1 - r || row >= M) continue;
+      auto* o = out + row * ldo;
+      for (int zc = NC + c; zc < out_cols; zc += 16)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (zc + e < out_cols) o[zc + e] = Elem<OT>::from_f32(0.f);
+    }
   }
 }
 
@@ -570,17 +598,25 @@ unsigned grid1d(int64_t n) {
 
 // ---- host side -------------------------------------------------------------------------
 
-// Split K only while there are fewer than 256 row groups (one workgroup per CU is enough to
-// stream X at full bandwidth with a few 128-k chunks in flight per wave).
-int ql_lora_down_splits(int64_t M, int64_t K) {
-  const int64_t groups = (M + 15) / 16;
+// 16-row groups per workgroup: 4 for a long single-adapter reduction (each fragment of Y then
+// serves four of X; the K split below restores the workgroup count), else 1.
+static int lora_down_rows(int64_t M, int64_t K, int slots) {
+  return (slots == 1 && K >= 8192 && M >= 1024) ? 4 : 1;
+}
+
+// Split K only while there are fewer than 256 row blocks (one workgroup per CU is enough to
+// stream X at full bandwidth with a few 128-k chunks in flight per wave), keeping at least
+// two chunks per wave in each split.
+int ql_lora_down_splits(int64_t M, int64_t K, int slots) {
+  const int64_t rows = 16 * lora_down_rows(M, K, slots);
+  const int64_t blocks = (M + rows - 1) / rows;
   int s = 1;
-  while (groups * s < 256 && K / (128 * kDownWaves * 2 * s) >= 1 && s < 64) s *= 2;
+  while (blocks * s < 256 && K / (128 * kDownWaves * 2 * s) >= 1 && s < 64) s *= 2;
   return s;
 }
 
 int64_t ql_lora_down_workspace_floats(int64_t M, int64_t K, int slots) {
-  const int s = ql_lora_down_splits(M, K);
+  const int s = ql_lora_down_splits(M, K, slots);
   return s > 1 ? (int64_t)s * M * kRank * slots : 0;
 }
 
@@ -598,38 +634,42 @@ int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const 
     return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   if (out_dtype != QL_BF16 && out_dtype != QL_F16 && out_dtype != QL_F32) return QL_EDTYPE;
-  int splits = ql_lora_down_splits(M, K);
+  const int rows = lora_down_rows(M, K, slots);
+  int splits = ql_lora_down_splits(M, K, slots);
   if (ws_floats < (int64_t)splits * M * nc || !ws) splits = 1;
   // per-split K range: a multiple of 128 k per wave
   constexpr int64_t kq = 128 * kDownWaves;
   int64_t kps = ((K + splits - 1) / splits + kq - 1) / kq * kq;
   splits = (int)((K + kps - 1) / kps);
-  const dim3 grid((unsigned)((M + 15) / 16), (unsigned)splits);
-#define QL_DOWN_G(IT, OT, G)                                                                  \
+  const dim3 grid((unsigned)((M + 16 * rows - 1) / (16 * rows)), (unsigned)splits);
+#define QL_DOWN_GR(IT, OT, G, R)                                                              \
   do {                                                                                        \
     using T = typename Elem<OT>::T;                                                           \
     if (splits == 1) {                                                                        \
-      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false, G>), grid, dim3(64 * kDownWaves), 0, \
-                         s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,      \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, false, G, R>), grid, dim3(64 * kDownWaves), \
+                         0, s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,   \
                          (float*)nullptr, (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t,    \
                          ldt);                                                                \
     } else {                                                                                  \
-      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true, G>), grid, dim3(64 * kDownWaves), 0,  \
-                         s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps, ws,  \
-                         (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);               \
+      hipLaunchKernelGGL((lora_down_kernel<IT, OT, true, G, R>), grid, dim3(64 * kDownWaves),  \
+                         0, s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,   \
+                         ws, (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);           \
       hipLaunchKernelGGL((lora_down_reduce<IT, OT>), dim3(grid1d(M * out_cols)), dim3(256),   \
                          0, s, ws, splits, M, nc, (T*)out, ldo, out_cols, alpha,              \
                          (uint16_t*)out_t, ldt);                                              \
     }                                                                                         \
   } while (0)
-#define QL_DOWN(IT, OT)                        \
-  do {                                         \
-    switch (slots) {                           \
-      case 1: QL_DOWN_G(IT, OT, 1); break;     \
-      case 2: QL_DOWN_G(IT, OT, 2); break;     \
-      case 3: QL_DOWN_G(IT, OT, 3); break;     \
-      default: QL_DOWN_G(IT, OT, 4); break;    \
-    }                                          \
+#define QL_DOWN(IT, OT)                                   \
+  do {                                                    \
+    switch (slots) {                                      \
+      case 1:                                             \
+        if (rows == 4) QL_DOWN_GR(IT, OT, 1, 4);          \
+        else QL_DOWN_GR(IT, OT, 1, 1);                    \
+        break;                                            \
+      case 2: QL_DOWN_GR(IT, OT, 2, 1); break;            \
+      case 3: QL_DOWN_GR(IT, OT, 3, 1); break;            \
+      default: QL_DOWN_GR(IT, OT, 4, 1); break;           \
+    }                                                     \
   } while (0)
   if (in_dtype == QL_BF16) {
     if (out_dtype == QL_BF16) QL_DOWN(QL_BF16, QL_BF16);
@@ -641,7 +681,7 @@ int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const 
     else QL_DOWN(QL_F16, QL_F32);
   }
 #undef QL_DOWN
-#undef QL_DOWN_G
+#undef QL_DOWN_GR
   return ql_launch_status();
 }
 

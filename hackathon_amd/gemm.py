@@ -30,12 +30,17 @@ def padded_rows(n_rows: int, n_cols: int, dtype, device) -> torch.Tensor:
     return torch.empty((n_rows, stride), dtype=dtype, device=device)[:, :n_cols]
 
 
+_NN_VIA_T_MIN_M = 512  # below this many rows the transpose would cost more than it saves
+
+
 def gemm(a: torch.Tensor, b: torch.Tensor, *, a_km: bool = False, b_kn: bool = False,
          out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
          bias: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 0.0) -> torch.Tensor:
     """C = alpha * A @ B^T (+ beta C) (+ bias) with A [M,K] (or stored [K,M] when a_km) and
     B [N,K] (or stored [K,N] when b_kn), both 2-D, unit stride along their last dim.
-    Split-K workspace, when the library asks for one, comes from torch's caching allocator."""
+    Split-K workspace, when the library asks for one, comes from torch's caching allocator.
+    A large NN product (b_kn, M >= 512, K % 64 == 0) transposes B into a temporary and takes
+    the NT kernel."""
     _lib.require_device(a, b)
     if a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"GEMM operands must share dtype bf16/fp16, got {a.dtype}, {b.dtype}")
@@ -50,6 +55,10 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a_km: bool = False, b_kn: bool = F
         raise ValueError("out must be [M, N] with unit stride along N")
     if bias is not None:
         bias = bias.to(a.dtype).contiguous()
+    if b_kn and not a_km and M >= _NN_VIA_T_MIN_M and N >= 64 and K % 64 == 0:
+        # B stored [K, N]: one tiled transpose (2·K·N·2 bytes of traffic) puts it k-contiguous,
+        # and the large-tile NT kernel then runs at about twice the general kernel's rate
+        b, b_kn = transpose16(b), False
     ws_bytes = int(_lib.load().qlora_gemm_workspace_size(int(a_km), int(b_kn), M, N, K))
     ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=out.device) \
         if ws_bytes > 0 else None
