@@ -39,6 +39,7 @@
 //
 // Both kernels optionally split their reduction over blockIdx.y into an fp32 workspace,
 // summed in split order by the matching reduce kernel (deterministic).
+#include "ql_swiglu.h"
 #include "ql_vec.h"
 #include "lora_mfma.h"
 
@@ -233,11 +234,14 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
   }
 }
 
+// alpha scales columns 0 .. 15 and alpha_hi the rest (the two adapters of the fused SwiGLU
+// backward have their own scalings; lora_down passes the same value twice).
 template <int IT, int OT>
 __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict__ ws, int splits,
                                                         int64_t M, int nc,
                                                         typename Elem<OT>::T* __restrict__ out,
                                                         int64_t ldo, int out_cols, float alpha,
+                                                        float alpha_hi,
                                                         uint16_t* __restrict__ out_t, int64_t ldt) {
   const int64_t total = M * out_cols;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
@@ -258,10 +262,165 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
         for (int j = 0; j < 8; ++j) v += w[j];
       }
       for (; z < splits; ++z) v += wp[(int64_t)z * stride];
-      v *= alpha;
+      v *= c < kRank ? alpha : alpha_hi;
       if (out_t) out_t[(int64_t)c * ldt + m] = Elem<IT>::from_f32(v);
     }
     out[m * ldo + c] = Elem<OT>::from_f32(v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// SwiGLU backward fused with the down-projections of its two gradients (the gate and up
+// adapters' du of a LoRA MLP):
+//   dgate, dup     = the SwiGLU gradients of (grad, gate, up)     stored, as swiglu_bwd_rows
+//   out[m, c]      = alpha_g * sum_k dgate[m, k] * YG[c, k]        c < 16
+//   out[m, 16 + c] = alpha_u * sum_k dup[m, k] * YU[c, k]
+// Lane l computes the gradients of row l % 16 of a row group at k = chunk + 32 t + 8 (l / 16)
+// .. +7, which is the lane layout of lora_down's MFMA operands: they are stored once and
+// multiplied straight from registers, so the down-projections do not read them back. Each
+// workgroup takes kSwigluRows row groups (each fragment of YG / YU then serves all of them)
+// and one 128-k chunk per wave per step: 3 kSwigluRows + 2 fragments of 16 B per lane per
+// 32-k group, all issued before the first wait.
+constexpr int kSwigluRows = 2;
+
+template <int IT, bool PARTIAL>
+__global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
+    const uint16_t* __restrict__ GR, int64_t ldgr, const uint16_t* __restrict__ GA,
+    int64_t ldga, const uint16_t* __restrict__ UP, int64_t ldup, uint16_t* __restrict__ DG,
+    int64_t lddg, uint16_t* __restrict__ DU, int64_t lddu, const uint16_t* __restrict__ YG,
+    const uint16_t* __restrict__ YU, int64_t ldy, int64_t M, int64_t K, int64_t k_per_split,
+    float* __restrict__ ws, uint16_t* __restrict__ out, int64_t ldo, int out_cols,
+    float alpha_g, float alpha_u, uint16_t* __restrict__ out_t, int64_t ldt) {
+  constexpr int R = kSwigluRows;
+  constexpr int NC = 2 * kRank;
+  constexpr int64_t kStride = 128 * kDownWaves;
+  __shared__ f32x4_t red[R * 2 * kDownWaves * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t m0 = (int64_t)blockIdx.x * 16 * R;
+  const int64_t kb = (int64_t)blockIdx.y * k_per_split;
+  const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
+  const int koff = 8 * (lane >> 4);
+  // wave-uniform bases at row m0; lane offsets of row m0 + 16 r + lane % 16 (a row past M
+  // works on row M - 1)
+  const char* grb = reinterpret_cast<const char*>(GR + m0 * ldgr);
+  const char* gab = reinterpret_cast<const char*>(GA + m0 * ldga);
+  const char* upb = reinterpret_cast<const char*>(UP + m0 * ldup);
+  char* dgb = reinterpret_cast<char*>(DG + m0 * lddg);
+  char* dub = reinterpret_cast<char*>(DU + m0 * lddu);
+  const char* ygb = reinterpret_cast<const char*>(YG);
+  const char* yub = reinterpret_cast<const char*>(YU);
+  uint32_t ogr[R], oga[R], oup[R], odg[R], odu[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = m0 + 16 * r + (lane & 15);
+    const int64_t rs = (row < M ? row : M - 1) - m0;
+    ogr[r] = (uint32_t)((rs * ldgr + koff) * 2);
+    oga[r] = (uint32_t)((rs * ldga + koff) * 2);
+    oup[r] = (uint32_t)((rs * ldup + koff) * 2);
+    odg[r] = (uint32_t)((rs * lddg + koff) * 2);
+    odu[r] = (uint32_t)((rs * lddu + koff) * 2);
+  }
+  const uint32_t oy = (uint32_t)(((lane & 15) * ldy + koff) * 2);
+  f32x4_t acc[R][2][2];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) acc[r][q][0] = acc[r][q][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Slots as in lora_down: wave w takes the 128-k chunks kb + 128 w + kStride j; the whole
+  // ones first, in an order rotated by blockIdx.x, then the last one, whose 32-k groups past
+  // ke work on the in-range group at kb and contribute zeros to the products.
+  const int64_t J = (ke - kb + kStride - 1) / kStride;  // >= 1 for every launched split
+  const int64_t nfull = J - 1;
+  const int64_t rot = nfull > 0 ? (int64_t)blockIdx.x % nfull : 0;
+  const int64_t wk = kb + 128 * wave;
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  for (int64_t j = 0; j < J; ++j) {
+    int64_t js = j + rot;
+    js = js >= nfull ? js - nfull : js;
+    const int64_t c0 = wk + kStride * (j < nfull ? js : nfull);
+    uint4 vgr[R][4], vga[R][4], vup[R][4], yg[4], yu[4];
+    bool ok[4];
+    int64_t kk[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int64_t k = c0 + 32 * t;
+      ok[t] = k < ke;
+      kk[t] = ok[t] ? k : kb;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        vgr[r][t] = ld16(grb + 2 * kk[t], ogr[r]);
+        vga[r][t] = ld16(gab + 2 * kk[t], oga[r]);
+        vup[r][t] = ld16(upb + 2 * kk[t], oup[r]);
+      }
+      yg[t] = ld16(ygb + 2 * kk[t], oy);
+      yu[t] = ld16(yub + 2 * kk[t], oy);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the step's loads all go out before the first wait
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float gr8[8], ga8[8], up8[8], dg8[8], du8[8];
+        Vec8<IT>::unpack(vgr[r][t], gr8);
+        Vec8<IT>::unpack(vga[r][t], ga8);
+        Vec8<IT>::unpack(vup[r][t], up8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ql_swiglu_bwd1(gr8[e], ga8[e], up8[e], dg8[e], du8[e]);
+        const uint4 pdg = Vec8<IT>::pack(dg8);
+        const uint4 pdu = Vec8<IT>::pack(du8);
+        // Unconditional stores: a lane whose row is past M, or a group past ke, recomputed
+        // the gradients of row M - 1 or of the group at kb from the same inputs and writes the
+        // same bits their owner writes (a branch here split the step, and the compiler then
+        // spilled and waited on the stores).
+        *reinterpret_cast<uint4*>(dgb + 2 * kk[t] + odg[r]) = pdg;
+        *reinterpret_cast<uint4*>(dub + 2 * kk[t] + odu[r]) = pdu;
+        acc[r][0][t & 1] = mfma<IT>(ok[t] ? yg[t] : z, ok[t] ? pdg : z, acc[r][0][t & 1]);
+        acc[r][1][t & 1] = mfma<IT>(ok[t] ? yu[t] : z, ok[t] ? pdu : z, acc[r][1][t & 1]);
+      }
+    }
+  }
+  // Sum over the waves (in wave order): wave p < 2R finishes row group p / 2, adapter p % 2;
+  // wave kDownWaves - 1 - r writes the zero columns NC .. out_cols - 1 of row group r.
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      red[((r * 2 + q) * kDownWaves + wave) * 64 + lane] = acc[r][q][0] + acc[r][q][1];
+  __syncthreads();
+  const int c = 4 * (lane >> 4);
+  if (wave < 2 * R) {
+    const int r = wave >> 1, q = wave & 1;
+    const int64_t row = m0 + 16 * r + (lane & 15);
+    if (row < M) {
+      f32x4_t sum = red[wave * kDownWaves * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < kDownWaves; ++w) sum += red[(wave * kDownWaves + w) * 64 + lane];
+      const int col = kRank * q + c;
+      if constexpr (PARTIAL) {
+        *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * NC + col) =
+            make_float4(sum[0], sum[1], sum[2], sum[3]);
+      } else {
+        const float a = q ? alpha_u : alpha_g;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint16_t v = Elem<IT>::from_f32(a * sum[e]);
+          out[row * ldo + col + e] = v;
+          if (out_t) out_t[(int64_t)(col + e) * ldt + row] = v;
+        }
+      }
+    }
+  }
+  if constexpr (!PARTIAL) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = m0 + 16 * r + (lane & 15);
+      if (wave != kDownWaves - 1 - r || row >= M) continue;
+      for (int zc = NC + c; zc < out_cols; zc += 16)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (zc + e < out_cols) out[row * ldo + zc + e] = Elem<IT>::from_f32(0.f);
+    }
   }
 }
 
@@ -655,7 +814,7 @@ int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const 
                          0, s, (const uint16_t*)X, ldx, (const uint16_t*)Y, ldy, M, K, kps,   \
                          ws, (T*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);           \
       hipLaunchKernelGGL((lora_down_reduce<IT, OT>), dim3(grid1d(M * out_cols)), dim3(256),   \
-                         0, s, ws, splits, M, nc, (T*)out, ldo, out_cols, alpha,              \
+                         0, s, ws, splits, M, nc, (T*)out, ldo, out_cols, alpha, alpha,       \
                          (uint16_t*)out_t, ldt);                                              \
     }                                                                                         \
   } while (0)
@@ -758,7 +917,95 @@ int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int
   return ql_launch_status();
 }
 
+// SwiGLU backward + the two down-projections: kSwigluRows row groups per workgroup, K split
+// as for lora_down.
+int ql_swiglu_bwd_down_splits(int64_t M, int64_t K) {
+  const int64_t blocks = (M + 16 * kSwigluRows - 1) / (16 * kSwigluRows);
+  int s = 1;
+  while (blocks * s < 256 && K / (128 * kDownWaves * 2 * s) >= 1 && s < 64) s *= 2;
+  return s;
+}
+
+static bool rows16_ok(const void* p, int64_t ld) { return ql_aligned(p, 16) && ld % 8 == 0; }
+
+int ql_swiglu_bwd_down(int dtype, const void* GR, int64_t ldgr, const void* GA, int64_t ldga,
+                       const void* UP, int64_t ldup, void* DG, int64_t lddg, void* DU,
+                       int64_t lddu, int64_t M, int64_t K, const void* YG, const void* YU,
+                       int64_t ldy, float alpha_g, float alpha_u, void* out, int64_t ldo,
+                       int out_cols, void* out_t, int64_t ldt, float* ws, int64_t ws_floats,
+                       hipStream_t s) {
+  constexpr int NC = 2 * kRank;
+  if (M <= 0 || K <= 0 || K % 32 || out_cols < NC || ldo < out_cols) return QL_EINVAL;
+  if (out_t && ldt < M) return QL_EINVAL;
+  if (ldgr < K || ldga < K || ldup < K || lddg < K || lddu < K || ldy < K) return QL_EINVAL;
+  // per-lane byte offsets within a workgroup's rows are 32-bit
+  const int64_t lim = int64_t(1) << 31;
+  if (32 * kSwigluRows * (ldgr > ldga ? (ldgr > ldup ? ldgr : ldup) : (ldga > ldup ? ldga : ldup)) >= lim ||
+      32 * kSwigluRows * (lddg > lddu ? lddg : lddu) >= lim || 32 * ldy >= lim)
+    return QL_EINVAL;
+  if (!rows16_ok(GR, ldgr) || !rows16_ok(GA, ldga) || !rows16_ok(UP, ldup) ||
+      !rows16_ok(DG, lddg) || !rows16_ok(DU, lddu) || !rows16_ok(YG, ldy) || !rows16_ok(YU, ldy))
+    return QL_EALIGN;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  int splits = ql_swiglu_bwd_down_splits(M, K);
+  if (ws_floats < (int64_t)splits * M * NC || !ws) splits = 1;
+  constexpr int64_t kq = 128 * kDownWaves;
+  int64_t kps = ((K + splits - 1) / splits + kq - 1) / kq * kq;
+  splits = (int)((K + kps - 1) / kps);
+  const dim3 grid((unsigned)((M + 16 * kSwigluRows - 1) / (16 * kSwigluRows)), (unsigned)splits);
+#define QL_SWD(IT)                                                                            \
+  do {                                                                                        \
+    if (splits == 1) {                                                                        \
+      hipLaunchKernelGGL((swiglu_bwd_down_kernel<IT, false>), grid, dim3(64 * kDownWaves), 0,  \
+                         s, (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,             \
+                         (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU, lddu, \
+                         (const uint16_t*)YG, (const uint16_t*)YU, ldy, M, K, kps,            \
+                         (float*)nullptr, (uint16_t*)out, ldo, out_cols, alpha_g, alpha_u,    \
+                         (uint16_t*)out_t, ldt);                                              \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((swiglu_bwd_down_kernel<IT, true>), grid, dim3(64 * kDownWaves), 0,   \
+                         s, (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,             \
+                         (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU, lddu, \
+                         (const uint16_t*)YG, (const uint16_t*)YU, ldy, M, K, kps, ws,        \
+                         (uint16_t*)out, ldo, out_cols, alpha_g, alpha_u, (uint16_t*)out_t,   \
+                         ldt);                                                                \
+      hipLaunchKernelGGL((lora_down_reduce<IT, IT>), dim3(grid1d(M * out_cols)), dim3(256),   \
+                         0, s, ws, splits, M, NC, (uint16_t*)out, ldo, out_cols, alpha_g,     \
+                         alpha_u, (uint16_t*)out_t, ldt);                                     \
+    }                                                                                         \
+  } while (0)
+  if (dtype == QL_BF16) QL_SWD(QL_BF16);
+  else QL_SWD(QL_F16);
+#undef QL_SWD
+  return ql_launch_status();
+}
+
 // ---- C-ABI -------------------------------------------------------------------------------
+
+extern "C" int64_t qlora_swiglu_bwd_lora_down_workspace_size(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int s = ql_swiglu_bwd_down_splits(rows, cols);
+  return s > 1 ? (int64_t)s * rows * 2 * kRank * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int qlora_swiglu_bwd_lora_down(
+    const void* grad, int64_t ldgr, const void* gate, int64_t ldg, const void* up, int64_t ldu,
+    void* dgate, int64_t lddg, void* dup, int64_t lddu, int64_t rows, int64_t cols,
+    const void* bt_gate, const void* bt_up, int64_t ldbt, float alpha_gate, float alpha_up,
+    int dtype, void* du, int64_t ldo, int out_cols, void* du_t, int64_t ldt, void* workspace,
+    int64_t workspace_bytes, ql_stream_t stream) {
+  if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (rows == 0) return QL_OK;
+  if (!grad || !gate || !up || !dgate || !dup || !bt_gate || !bt_up || !du) return QL_EINVAL;
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  if (!ql_aligned(du, 2) || (du_t && !ql_aligned(du_t, 2))) return QL_EALIGN;
+  return ql_swiglu_bwd_down(dtype, grad, ldgr, gate, ldg, up, ldu, dgate, lddg, dup, lddu, rows,
+                            cols, bt_gate, bt_up, ldbt, alpha_gate, alpha_up, du, ldo, out_cols,
+                            du_t, ldt, static_cast<float*>(workspace),
+                            workspace_bytes / (int64_t)sizeof(float),
+                            static_cast<hipStream_t>(stream));
+}
+
 
 extern "C" int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K, int slots) {
   if (M <= 0 || K <= 0 || slots < 1 || slots > kMaxSlots) return 0;

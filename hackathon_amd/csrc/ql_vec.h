@@ -6,9 +6,10 @@
 
 template <int DT> struct Vec8;
 
+// unpack / pack convert between 8 floats and the 16-byte register image of 8 16-bit values
+// (element 2i in the low half of word i).
 template <> struct Vec8<QL_BF16> {
-  static QL_DEV void load(const uint16_t* p, float* v) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
+  static QL_DEV void unpack(const uint4& r, float* v) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -16,19 +17,24 @@ template <> struct Vec8<QL_BF16> {
       v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
-  static QL_DEV void store(uint16_t* p, const float* v) {
+  static QL_DEV uint4 pack(const float* v) {
     uint4 r;
     r.x = pack_bf16x2(v[0], v[1]);
     r.y = pack_bf16x2(v[2], v[3]);
     r.z = pack_bf16x2(v[4], v[5]);
     r.w = pack_bf16x2(v[6], v[7]);
-    *reinterpret_cast<uint4*>(p) = r;
+    return r;
+  }
+  static QL_DEV void load(const uint16_t* p, float* v) {
+    unpack(*reinterpret_cast<const uint4*>(p), v);
+  }
+  static QL_DEV void store(uint16_t* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) = pack(v);
   }
 };
 
 template <> struct Vec8<QL_F16> {
-  static QL_DEV void load(const uint16_t* p, float* v) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
+  static QL_DEV void unpack(const uint4& r, float* v) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -36,13 +42,19 @@ template <> struct Vec8<QL_F16> {
       v[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16));
     }
   }
-  static QL_DEV void store(uint16_t* p, const float* v) {
+  static QL_DEV uint4 pack(const float* v) {
     uint4 r;
     r.x = pack_f16x2(v[0], v[1]);
     r.y = pack_f16x2(v[2], v[3]);
     r.z = pack_f16x2(v[4], v[5]);
     r.w = pack_f16x2(v[6], v[7]);
-    *reinterpret_cast<uint4*>(p) = r;
+    return r;
+  }
+  static QL_DEV void load(const uint16_t* p, float* v) {
+    unpack(*reinterpret_cast<const uint4*>(p), v);
+  }
+  static QL_DEV void store(uint16_t* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) = pack(v);
   }
 };
 

@@ -8,13 +8,12 @@
 // HBM-bound: fwd 2 reads + 1 write, bwd 3 reads + 2 writes per element. Each thread handles
 // 8 consecutive elements per step (16 B per tensor for 16-bit dtypes) in a grid-stride loop
 // sized to a few waves per SIMD, so each wave-level access is 1 KiB contiguous.
+#include "ql_swiglu.h"
 #include "ql_vec.h"
 
 namespace {
 
 constexpr int kThreads = 256;
-
-QL_DEV float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const typename Elem<DT>::T* __restrict__ gate,
@@ -27,7 +26,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const typename Elem<D
     Vec8<DT>::load(gate + 8 * i, g);
     Vec8<DT>::load(up + 8 * i, u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = g[j] * sigmoidf(g[j]) * u[j];
+    for (int j = 0; j < 8; ++j) o[j] = ql_swiglu_fwd1(g[j], u[j]);
     Vec8<DT>::store(out + 8 * i, o);
   }
 }
@@ -44,11 +43,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(
     Vec8<DT>::load(gate + 8 * i, g);
     Vec8<DT>::load(up + 8 * i, u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float sg = sigmoidf(g[j]);
-      du[j] = gr[j] * g[j] * sg;
-      dg[j] = gr[j] * u[j] * sg * (1.0f + g[j] * (1.0f - sg));
-    }
+    for (int j = 0; j < 8; ++j) ql_swiglu_bwd1(gr[j], g[j], u[j], dg[j], du[j]);
     Vec8<DT>::store(dgate + 8 * i, dg);
     Vec8<DT>::store(dup + 8 * i, du);
   }
@@ -61,8 +56,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(const typename Ele
                                                               int64_t begin, int64_t n) {
   const int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= n) return;
-  const float g = Elem<DT>::load(gate, i);
-  Elem<DT>::store(out, i, g * sigmoidf(g) * Elem<DT>::load(up, i));
+  Elem<DT>::store(out, i, ql_swiglu_fwd1(Elem<DT>::load(gate, i), Elem<DT>::load(up, i)));
 }
 
 template <int DT>
@@ -72,10 +66,10 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(
     typename Elem<DT>::T* __restrict__ dup, int64_t begin, int64_t n) {
   const int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= n) return;
-  const float gr = Elem<DT>::load(grad, i), g = Elem<DT>::load(gate, i), u = Elem<DT>::load(up, i);
-  const float sg = sigmoidf(g);
-  Elem<DT>::store(dup, i, gr * g * sg);
-  Elem<DT>::store(dgate, i, gr * u * sg * (1.0f + g * (1.0f - sg)));
+  float dg, du;
+  ql_swiglu_bwd1(Elem<DT>::load(grad, i), Elem<DT>::load(gate, i), Elem<DT>::load(up, i), dg, du);
+  Elem<DT>::store(dup, i, du);
+  Elem<DT>::store(dgate, i, dg);
 }
 
 // Row-strided forms for gate / up (and their gradients) that are column ranges of wider
@@ -94,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_rows(
     Vec8<DT>::load(gate + r * ldg + c, g);
     Vec8<DT>::load(up + r * ldu + c, u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = g[j] * sigmoidf(g[j]) * u[j];
+    for (int j = 0; j < 8; ++j) o[j] = ql_swiglu_fwd1(g[j], u[j]);
     Vec8<DT>::store(out + r * ldo + c, o);
   }
 }
@@ -114,11 +108,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_rows(
     Vec8<DT>::load(gate + r * ldg + c, g);
     Vec8<DT>::load(up + r * ldu + c, u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float sg = sigmoidf(g[j]);
-      du[j] = gr[j] * g[j] * sg;
-      dg[j] = gr[j] * u[j] * sg * (1.0f + g[j] * (1.0f - sg));
-    }
+    for (int j = 0; j < 8; ++j) ql_swiglu_bwd1(gr[j], g[j], u[j], dg[j], du[j]);
     Vec8<DT>::store(dgate + r * lddg + c, dg);
     Vec8<DT>::store(dup + r * lddu + c, du);
   }

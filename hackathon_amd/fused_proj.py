@@ -9,7 +9,9 @@ up. Here each group runs as one fused computation with the same sums:
                                                             of one output (W_g dequantised into
                                                             row ranges of one buffer; slot g of
                                                             sB_cat holds s_g B_g in g's rows)
-  backward  du_g = s_g dY_g B_g                              qlora_lora_down into slot g
+  backward  du_g = s_g dY_g B_g                              qlora_lora_down into slot g (for
+                                                            gate/up fused into the SwiGLU
+                                                            backward that makes dY_g)
             dx = [dY_1 | dY_2 | .. | du] [W_cat^T | A_cat^T]^T  one GEMM over the concatenated K
             dA_g = du_g^T x                                 qlora_lora_wgrad, all slots at once
             dB_g = s_g dY_g^T u_g                           qlora_lora_wgrad per projection
@@ -144,19 +146,23 @@ def group_forward(x2, specs, ab):
     return y, (at, bt, ut)
 
 
-def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab):
+def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None):
     """(dx or None, [dA_0, dB_0, dA_1, ...] with None where not needed) for the output
-    gradient g [M, sum n_g] (row stride a multiple of 8, unit column stride)."""
+    gradient g [M, sum n_g] (row stride a multiple of 8, unit column stride). `du_dut`, when
+    given, holds the adapters' down-projections of g already (du [M, 64], du^T [16 G, M])."""
     dt = x2.dtype
     dev = x2.device
     M, K = x2.shape
     G = len(specs)
     offs = _offsets(specs)
-    du = torch.empty((M, _PAD), dtype=dt, device=dev)
-    dut = _t_buffer(16 * G, M, dt, dev)
-    for i, s in enumerate(specs):
-        _gemm.lora_down(g[:, offs[i]:offs[i + 1]], bt[:, offs[i]:offs[i + 1]], du[:, 16 * i:],
-                        alpha=s.scaling, out_t=dut[16 * i:16 * i + 16])
+    if du_dut is None:
+        du = torch.empty((M, _PAD), dtype=dt, device=dev)
+        dut = _t_buffer(16 * G, M, dt, dev)
+        for i, s in enumerate(specs):
+            _gemm.lora_down(g[:, offs[i]:offs[i + 1]], bt[:, offs[i]:offs[i + 1]],
+                            du[:, 16 * i:], alpha=s.scaling, out_t=dut[16 * i:16 * i + 16])
+    else:
+        du, dut = du_dut
     dx = None
     if need_dx:
         wt = torch.empty((K, offs[-1]), dtype=dt, device=dev)
@@ -266,9 +272,20 @@ class GateUpSwiGLU(torch.autograd.Function):
         if dh2.stride(-1) != 1 or dh2.stride(0) % 8 or dh2.data_ptr() % 16:
             dh2 = dh2.contiguous()
         g = torch.empty((M, 2 * n), dtype=x2.dtype, device=x2.device)
-        swiglu.swiglu_bwd_rows(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:])
+        du_dut = None
+        if n % 32 == 0:
+            # the SwiGLU gradients and, in the same pass, du_gate = s dgate B_gate and
+            # du_up = s dup B_up (the gradients are not read back for the down-projections)
+            du = torch.empty((M, _PAD), dtype=x2.dtype, device=x2.device)
+            dut = _t_buffer(32, M, x2.dtype, x2.device)
+            gate_s, up_s = ctx.specs
+            swiglu.swiglu_bwd_lora_down(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:, :n],
+                                        bt[:, n:], gate_s.scaling, up_s.scaling, du, dut)
+            du_dut = (du, dut)
+        else:
+            swiglu.swiglu_bwd_rows(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:])
         dx, grads = group_backward(g, x2, at, bt, ut, ctx.specs, ctx.needs_input_grad[0],
-                                   ctx.needs_input_grad[2:])
+                                   ctx.needs_input_grad[2:], du_dut=du_dut)
         grads = [None if gr is None else gr.to(t) for gr, t in zip(grads, ctx.ab_dtypes)]
         return (None if dx is None else dx.view(ctx.shape)), None, *grads
 

@@ -62,6 +62,26 @@ def swiglu_bwd_rows(grad, gate, up, dgate, dup):
               _lib.stream_of(gate))
 
 
+def swiglu_bwd_lora_down(grad, gate, up, dgate, dup, bt_gate, bt_up, alpha_gate, alpha_up,
+                         du, du_t=None):
+    """The SwiGLU gradients into dgate / dup (as swiglu_bwd_rows) and, in the same pass, the
+    gate and up adapters' down-projections of them: du[:, :16] = alpha_gate dgate bt_gate^T,
+    du[:, 16:32] = alpha_up dup bt_up^T, du[:, 32:] = 0, du_t = du[:, :32]^T when given
+    (qlora_swiglu_bwd_lora_down)."""
+    rows, cols = gate.shape
+    if bt_up.stride(0) != bt_gate.stride(0):
+        raise ValueError("bt_gate and bt_up must share a row stride (slices of one B^T buffer)")
+    ws, ws_bytes = _lib.workspace("qlora_swiglu_bwd_lora_down_workspace_size", rows, cols,
+                                  device=gate.device)
+    _lib.call("qlora_swiglu_bwd_lora_down", grad.data_ptr(), grad.stride(0), gate.data_ptr(),
+              gate.stride(0), up.data_ptr(), up.stride(0), dgate.data_ptr(), dgate.stride(0),
+              dup.data_ptr(), dup.stride(0), rows, cols, bt_gate.data_ptr(), bt_up.data_ptr(),
+              bt_gate.stride(0), float(alpha_gate), float(alpha_up), _lib.tag(gate.dtype),
+              du.data_ptr(), du.stride(0), du.shape[1], _lib.ptr(du_t),
+              du_t.stride(0) if du_t is not None else 0, _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(gate))
+
+
 def patch_qwen2_mlp():
     """Send Qwen2MLP.forward through the fused kernel for GPU inputs (solution/swiglu.py:68-81)."""
     from transformers.models.qwen2 import modeling_qwen2

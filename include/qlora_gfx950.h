@@ -334,6 +334,29 @@ int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, i
                      void* workspace, int64_t workspace_bytes, ql_stream_t stream);
 
 /*
+ * SwiGLU backward fused with the gate and up adapters' down-projections of its gradients
+ * (a LoRA MLP whose gate/up outputs are the two halves gate, up [rows, cols]):
+ *   dgate, dup = exactly as qlora_swiglu_bwd_rows (stored, row-strided)
+ *   du[m, c]      = alpha_gate * sum_k dgate[m, k] * bt_gate[c, k]    c < 16
+ *   du[m, 16 + c] = alpha_up   * sum_k dup[m, k]   * bt_up[c, k]
+ *   du[m, c] = 0 for 32 <= c < out_cols; du_t (optional, [32, ldt >= rows]) = du[:, :32]^T.
+ * bt_gate / bt_up are the adapters' B^T [16, cols] (ld ldbt). The gradients are multiplied
+ * from registers, so the two down-projections do not read them back from HBM.
+ * cols % 32 == 0; every matrix 16-B aligned with a leading dimension that is a multiple of 8,
+ * at least cols, and below 2^24; dtype QL_BF16 or QL_F16 (du and du_t in it too).
+ * Replaces: solution/swiglu.py:25-37 (the SwiGLU backward) and the lora_B autograd backward
+ * of solution/lora.py:172 for the gate and up projections.
+ */
+int64_t qlora_swiglu_bwd_lora_down_workspace_size(int64_t rows, int64_t cols);
+int qlora_swiglu_bwd_lora_down(const void* grad, int64_t ldgr, const void* gate, int64_t ldg,
+                               const void* up, int64_t ldu, void* dgate, int64_t lddg, void* dup,
+                               int64_t lddu, int64_t rows, int64_t cols, const void* bt_gate,
+                               const void* bt_up, int64_t ldbt, float alpha_gate, float alpha_up,
+                               int dtype, void* du, int64_t ldo, int out_cols, void* du_t,
+                               int64_t ldt, void* workspace, int64_t workspace_bytes,
+                               ql_stream_t stream);
+
+/*
  * The compute-dtype operands of one rank-16 adapter, from its fp32 factors A [16, K] and
  * B [N, 16], in one launch (K % 8 == 0, pad >= 16):
  *   a16 [16, K] = A;  at_pad [K, pad] = A^T | 0;  bs_pad [N, pad] = scaling * B | 0;

@@ -168,3 +168,35 @@ def test_lora_pack_group_matches_the_single_packs():
         assert torch.equal(bt[:, rows], bt1)
         off += n
     assert torch.all(at[:, 48:] == 0)
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 18944), (37, 1024), (300, 96)])
+def test_swiglu_bwd_lora_down(rows, cols):
+    """The fused SwiGLU backward writes the same gradient bits as qlora_swiglu_bwd_rows and the
+    two scaled down-projections of them (fp32 accumulation bound vs fp64), zeros after column
+    32, and the transposed copy exactly; ragged row counts exercise rows past M."""
+    print(f"swiglu_bwd_lora_down {rows}x{cols}", flush=True)
+    from hackathon_amd import gemm
+
+    g = torch.Generator(device="cuda").manual_seed(rows + cols)
+    y = torch.randn(rows, 2 * cols, device="cuda", generator=g).to(torch.bfloat16)
+    gate, up = y[:, :cols], y[:, cols:]
+    dh = torch.randn(rows, cols, device="cuda", generator=g).to(torch.bfloat16)
+    bt = (torch.randn(16, 2 * cols, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+    buf = torch.empty(rows, 2 * cols, dtype=torch.bfloat16, device="cuda")
+    du = torch.full((rows, 64), 5.0, dtype=torch.bfloat16, device="cuda")
+    dut = gemm.lora_t_buffer(rows, torch.bfloat16, "cuda", rows=32)
+    swiglu.swiglu_bwd_lora_down(dh, gate, up, buf[:, :cols], buf[:, cols:], bt[:, :cols],
+                                bt[:, cols:], 2.0, 0.5, du, dut)
+    ref = torch.empty_like(buf)
+    swiglu.swiglu_bwd_rows(dh, gate, up, ref[:, :cols], ref[:, cols:])
+    assert torch.equal(buf, ref)
+    for q, (c0, a) in enumerate(((0, 2.0), (cols, 0.5))):
+        x = ref[:, c0:c0 + cols].double()
+        w = bt[:, c0:c0 + cols].double()
+        exact = a * (x @ w.t())
+        bound = a * 4 * 2.0**-22 * cols * x.abs().max() * w.abs().max() + 2.0**-8 * exact.abs()
+        got = du[:, 16 * q:16 * q + 16].double()
+        assert torch.all((got - exact).abs() <= bound), q
+    assert torch.all(du[:, 32:] == 0)
+    assert torch.equal(dut, du[:, :32].t())
