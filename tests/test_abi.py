@@ -107,6 +107,17 @@ def test_rejected_arguments_return_codes(lib):
                                 None) == -1
     assert lib.qlora_lora_down_workspace_size(4096, 3584, 0) == 0
     assert lib.qlora_lora_wgrad_workspace_size(4096, 3584, 5) == 0
+    # fused SwiGLU backward + down-projections: columns a multiple of 32, room for both
+    # adapters' 32 output columns, 16-bit dtypes only
+    assert lib.qlora_swiglu_bwd_lora_down(fake, 48, fake, 96, fake, 96, fake, 96, fake, 96, 16, 48,
+                                          fake, fake, 96, 1.0, 1.0, 2, fake, 64, 64, None, 0,
+                                          None, 0, None) == -1
+    assert lib.qlora_swiglu_bwd_lora_down(fake, 64, fake, 128, fake, 128, fake, 128, fake, 128, 16,
+                                          64, fake, fake, 128, 1.0, 1.0, 2, fake, 64, 16, None, 0,
+                                          None, 0, None) == -1
+    assert lib.qlora_swiglu_bwd_lora_down(fake, 64, fake, 128, fake, 128, fake, 128, fake, 128, 16,
+                                          64, fake, fake, 128, 1.0, 1.0, 0, fake, 64, 64, None, 0,
+                                          None, 0, None) == -2
     # adamw: a table is required when there is work; the bias correction must be positive
     assert lib.qlora_adamw_fp32(None, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 1.0, 1e-8, None) == -1
     assert lib.qlora_adamw_fp32(fake, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 0.0, 1e-8, None) == -1
