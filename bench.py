@@ -13,7 +13,9 @@ Also reported in the same line:
   roofline       the dequant kernel against the 8 TB/s HBM peak (algorithmic bytes/launch)
   cpu_baseline   the C oracle's dequant (oracle/nf4_oracle.c, 1 thread) on a bounded sample
   nf4_4864x896   the same dequant on the Qwen2.5-0.5B gate_proj weight (32 rotated sets)
-  kernels        per-kernel device time and roofline of the other kernels at their shapes
+  kernels        per-kernel device time and roofline of the other kernels at their shapes,
+                 and the Qwen2.5-7B LoRA MLP forward + backward at 4096 tokens (patched vs
+                 eager, TFLOP/s against 3.364 TFLOP of work)
   qlora_step     Qwen2.5-7B-shaped QLoRA training step tokens/s, patched vs PyTorch eager
 
 `python bench.py --gpus N --steps K --warmup W`; N > 1 is not run (one GPU only).
@@ -227,7 +229,57 @@ def bench_kernels(torch):
     fl = 2 * 2.0 * n_rows * H * V
     res["fused_ce_8192x1536x151936"] = dict(ms=round(t * 1e3, 2), tflops=round(fl / t / 1e12, 1),
                                            frac_mfma=round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 3))
+    del hid, W, tgt
+    res["qwen25_7b_mlp_lora_4096tok"] = bench_mlp(torch)
     return res
+
+
+def bench_mlp(torch, tokens=4096, reps=3):
+    """The Qwen2.5-7B MLP with NF4 bases and LoRA r=16 on gate/up/down, forward + backward at
+    `tokens` tokens (gradients to the adapters and the input), patched and eager. Work: the
+    three base projections forward and their dX backward, 2 x (3 x 2 T H I) FLOP, plus the
+    rank-16 products, 6 T r (H + I) FLOP per projection (u, its share of y; du, its share of
+    dX, dA, dB): 3.364 TFLOP at T = 4096."""
+    from hackathon_amd import qlora_step
+
+    cfg = qlora_step.qwen2_config(num_hidden_layers=1, vocab_size=1024)
+    model = qlora_step.build_qlora_model(cfg, "cuda")
+    mlp = model.model.layers[0].mlp
+    H, I, r = cfg.hidden_size, cfg.intermediate_size, 16
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(1, tokens, H, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    dy = torch.randn(1, tokens, H, device="cuda", generator=g).to(torch.bfloat16)
+    params = qlora_step.lora_parameters(model)
+    base = 2 * (3 * 2.0 * tokens * H * I)
+    lora = 3 * 6.0 * tokens * r * (H + I)
+    fl = base + lora
+
+    def one():
+        x.grad = None
+        for p in params:
+            p.grad = None
+        mlp(x).backward(dy)
+
+    def timed():
+        one()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            one()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+
+    qlora_step.patched_mode()
+    t = timed()
+    with qlora_step.eager_mode(model):
+        t_e = timed()
+    qlora_step.patched_mode()
+    del model, mlp, x, dy, params
+    return dict(ms=round(t * 1e3, 3), tflops=round(fl / t / 1e12, 1),
+                frac_mfma=round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 3), work_tflop=round(fl / 1e12, 3),
+                eager_ms=round(t_e * 1e3, 3), speedup_vs_eager=round(t_e / t, 2))
 
 
 # ---------------------------------------------------------------------------------------------
