@@ -184,21 +184,27 @@ def test_gemm_nt_cat(M, N, K, K2):
         assert torch.all((out.double().cpu() - ref).abs() <= bound)
 
 
-@pytest.mark.parametrize("M,K,out_cols", [(4096, 3584, 64), (4096, 18944, 64), (77, 96, 16),
-                                          (1000, 512, 40), (512, 8192, 64), (1100, 8192, 40)])
-def test_lora_down(M, K, out_cols):
+@pytest.mark.parametrize("M,K,out_cols,dtype", [(4096, 3584, 64, torch.bfloat16),
+                                                (4096, 18944, 64, torch.bfloat16),
+                                                (77, 96, 16, torch.bfloat16),
+                                                (1000, 512, 40, torch.bfloat16),
+                                                (512, 8192, 64, torch.bfloat16),
+                                                (1100, 8192, 40, torch.bfloat16),
+                                                (2048, 8192, 64, torch.float16)])
+def test_lora_down(M, K, out_cols, dtype):
     """out[:, :16] = alpha x y^T, out[:, 16:] = 0 and the transposed copy equal to out[:, :16]
     bit for bit, with and without the split-K workspace (512 x 8192 splits; 4096 x 18944 and
     1100 x 8192 take 64-row blocks split over K, the latter with row groups past M)."""
-    print(f"lora_down M={M} K={K}", flush=True)
+    print(f"lora_down M={M} K={K} {dtype}", flush=True)
     g = torch.Generator().manual_seed(M + K)
-    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
-    y = (torch.randn(16, K, generator=g) * 0.25).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    y = (torch.randn(16, K, generator=g) * 0.25).to(dtype)
     ref = 2.0 * (x.double() @ y.double().t())
-    out = torch.full((M, out_cols), 3.0, dtype=torch.bfloat16, device="cuda")
-    out_t = gemm.lora_t_buffer(M, torch.bfloat16, "cuda")
+    out = torch.full((M, out_cols), 3.0, dtype=dtype, device="cuda")
+    out_t = gemm.lora_t_buffer(M, dtype, "cuda")
     gemm.lora_down(x.cuda(), y.cuda(), out, alpha=2.0, out_t=out_t)
-    bound = 2 * 4 * 2.0**-22 * K * x.abs().max().item() * y.abs().max().item() + 2.0**-8 * ref.abs()
+    rnd = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11  # one rounding to the output
+    bound = 2 * 4 * 2.0**-22 * K * x.abs().max().item() * y.abs().max().item() + rnd * ref.abs()
     assert torch.all((out[:, :16].double().cpu() - ref).abs() <= bound)
     assert torch.all(out[:, 16:] == 0)
     assert torch.equal(out_t, out[:, :16].t())
