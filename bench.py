@@ -12,6 +12,8 @@ with HIP events on the stream the kernels run on.
 Also reported in the same line:
   roofline       the dequant kernel against the 8 TB/s HBM peak (algorithmic bytes/launch)
   cpu_baseline   the C oracle's dequant (oracle/nf4_oracle.c, 1 thread) on a bounded sample
+  cpu_baselines  the other configs' CPU side on the host (oracle torch restatements and the
+                 eager model path), bounded samples with stated extrapolation
   nf4_4864x896   the same dequant on the Qwen2.5-0.5B gate_proj weight (32 rotated sets)
   kernels        per-kernel device time and roofline of the other kernels at their shapes,
                  and the Qwen2.5-7B LoRA MLP forward + backward at 4096 tokens (patched vs
@@ -129,6 +131,104 @@ def cpu_baseline_nf4(seconds, shape=(4864, 896)):
     return dict(value=round(nbytes * reps / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
                 sample=f"C oracle nf4 dequant of a {shape[0]}x{shape[1]} weight (bf16 out), "
                        f"{reps} repetitions in {el:.1f} s on one host thread")
+
+
+def cpu_baselines(torch):
+    """The reference path's CPU side at the other configs, timed on the host beside the GPU
+    run (reported baselines, not targets): the oracle's torch restatements of RMSNorm, RoPE
+    and the unfused lm_head + cross-entropy (oracle/ops.py), and the plain PyTorch path of a
+    Qwen2.5-7B-shaped layer (the eager model path, torch-op NF4 dequant, LoRA, attention) for
+    the MLP and the step. Each runs a bounded sample, and the extrapolation is stated."""
+    import torch.nn.functional as F
+
+    from hackathon_amd import qlora_step
+    from oracle import ops
+
+    def tm(fn, min_s=0.5):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= min_s:
+                return el / n
+
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+    res = {"cores": torch.get_num_threads(), "kind": "port", "host_cpu": _cpu_model()}
+    # cfg2: RMSNorm 4 x 2048 x 1536 and RoPE q 4x12x2048x128 / k 4x2x2048x128, full shape
+    x = torch.randn(8192, 1536, generator=g).to(bf)
+    w = (1 + 0.1 * torch.randn(1536, generator=g)).to(bf)
+    dy = torch.randn(8192, 1536, generator=g).to(bf)
+    _, rstd = ops.rmsnorm_fwd(x, w, 1e-6)
+    for name, fn, nbytes in (("rmsnorm_fwd_8192x1536", lambda: ops.rmsnorm_fwd(x, w, 1e-6),
+                              50_367_488),
+                             ("rmsnorm_bwd_8192x1536", lambda: ops.rmsnorm_bwd(dy, x, w, rstd),
+                              75_533_312)):
+        t = tm(fn)
+        res[name] = dict(ms=round(t * 1e3, 2), gbs=round(nbytes / t / 1e9, 2), sample="full shape")
+    q = torch.randn(4, 2048, 12, 128, generator=g).to(bf).transpose(1, 2)
+    k = torch.randn(4, 2048, 2, 128, generator=g).to(bf).transpose(1, 2)
+    cos, sin = ops.qwen_cos_sin(1, 2048, 128, dtype=bf)
+    t = tm(lambda: ops.rope(q, k, cos, sin))
+    res["rope_fwd_4x2048x(12+2)x128"] = dict(ms=round(t * 1e3, 2),
+                                             gbs=round(59_768_832 / t / 1e9, 2),
+                                             sample="full shape")
+    del x, w, dy, q, k
+    # cfg3: full-logits lm_head + cross-entropy forward and dz @ W on 256 of the 8192 rows
+    rows, H, V = 256, 1536, 151936
+    W32 = (torch.randn(V, H, generator=g) * 0.02).to(bf).float()
+    h = torch.randn(rows, H, generator=g).to(bf).float().requires_grad_()
+    tgt = torch.randint(0, V, (rows,), generator=g)
+    tgt[torch.rand(rows, generator=g) < 0.1] = -100
+
+    def ce():
+        h.grad = None
+        F.cross_entropy(h @ W32.t(), tgt, ignore_index=-100).backward()
+    t = tm(ce, 1.0) * (8192 / rows)
+    fl = 2 * 2.0 * 8192 * H * V
+    res["fused_ce_8192x1536x151936"] = dict(
+        ms=round(t * 1e3, 1), tflops=round(fl / t / 1e12, 3),
+        sample=f"{rows} of 8192 rows (fp32 full logits), scaled linearly by rows")
+    ce_rate = fl / t
+    del W32, h
+    # cfg4 and cfg5: the eager PyTorch path of one Qwen2.5-7B-shaped layer on the host
+    cfg = qlora_step.qwen2_config(num_hidden_layers=1, vocab_size=1024)
+    model = qlora_step.build_qlora_model(cfg, "cpu")
+    mlp = model.model.layers[0].mlp
+    gm = torch.Generator().manual_seed(1)
+
+    def mlp_step(T):
+        xm = torch.randn(1, T, cfg.hidden_size, generator=gm).to(bf).requires_grad_()
+        mlp(xm).float().sum().backward()
+
+    def model_step(T):
+        ids = torch.randint(0, cfg.vocab_size, (1, T), generator=gm)
+        model(input_ids=ids, labels=ids, use_cache=False).loss.backward()
+
+    with qlora_step.eager_mode(model):
+        pts = [(T, tm(lambda T=T: mlp_step(T), 1.0)) for T in (256, 1024)]
+        slope = (pts[1][1] - pts[0][1]) / (pts[1][0] - pts[0][0])
+        t_mlp = pts[0][1] + slope * (4096 - pts[0][0])
+        res["qwen25_7b_mlp_lora_4096tok"] = dict(
+            ms=round(t_mlp * 1e3, 1), tflops=round(3.3638e12 / t_mlp / 1e12, 3),
+            sample="MLP fwd+bwd at 256 and 1024 tokens (NF4 dequant, LoRA, SwiGLU), "
+                   "fitted a + b*tokens and evaluated at 4096")
+        pts = [(T, tm(lambda T=T: model_step(T), 1.0)) for T in (512, 1024)]
+        slope = (pts[1][1] - pts[0][1]) / (pts[1][0] - pts[0][0])
+        t_layer = pts[0][1] + slope * (4096 - pts[0][0])
+    qlora_step.patched_mode()
+    head = 2 * 2.0 * 4096 * cfg.hidden_size * 152064 / ce_rate
+    t_step = 28 * t_layer + head
+    res["qlora_step_qwen25_7b"] = dict(
+        ms=round(t_step * 1e3, 0), tokens_per_s=round(4096 / t_step, 1),
+        sample="extrapolated: one decoder layer fwd+bwd (with its embedding, norm and a 1024-word "
+               "head) at 512 and 1024 tokens, fitted linearly to 4096 tokens x 28 layers, plus the "
+               "152064-word head at the cfg3 CPU rate; attention's quadratic term is only "
+               "partly in the fit, so this is a lower bound on the CPU time")
+    del model, mlp
+    return res
 
 
 # ---------------------------------------------------------------------------------------------
@@ -399,6 +499,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-step", action="store_true", help="skip the 7B QLoRA step")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
+    ap.add_argument("--no-cpu-configs", action="store_true",
+                    help="skip the host CPU baselines of the other configs")
     ap.add_argument("--step-steps", type=int, default=5)
     ap.add_argument("--step-layers", type=int, default=None)
     ap.add_argument("--eager-steps", type=int, default=2,
@@ -467,6 +569,11 @@ def main():
                                         layers=args.step_layers, parity=args.eager_steps > 0)
     line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     line["cpu_baseline"]["host_cpu"] = _cpu_model()
+    if not args.no_cpu_configs:
+        t0 = time.perf_counter()
+        line["cpu_baselines"] = cpu_baselines(torch)
+        log(f"[bench] cpu baselines in {time.perf_counter() - t0:.0f} s: "
+            f"{json.dumps(line['cpu_baselines'])}")
     print(json.dumps(line), flush=True)
 
 
