@@ -516,8 +516,8 @@ def main():
         trace_summary(args.trace_summary)
         return
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
-              f"multi-GPU path; see DESIGN.md for how it would shard", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the kernels work on one "
+              f"GPU's share and there is no multi-GPU path", file=sys.stderr)
         sys.exit(2)
 
     import torch

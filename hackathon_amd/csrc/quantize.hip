@@ -1,6 +1,6 @@
 // NF4 quantisation with a double-quantised absmax, for gfx950: the format producer that
 // feeds the dequant kernel (the weight format of solution/nf4.py:73-86, which the reference
-// takes from bitsandbytes' quantize_4bit; bitsandbytes is not part of this build).
+// takes from bitsandbytes' quantize_4bit; this kernel produces the same layout without it).
 //
 //   stage 1  one thread per NF4 block of `blocksize` weights: absmax = max |w|, codes =
 //            nearest NF4 level of w * (1 / absmax) (fp32 multiply by the correctly rounded

@@ -7,8 +7,8 @@ reference file:line it follows:
   ops.py                  RMSNorm, RoPE, SwiGLU, LoRA cast/add, CE rows, fused head loss
                           (torch fp32 on the CPU)
 
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package,
-and only as the checker (or the timed CPU baseline); the product package `hackathon_amd`
-never imports it. Each function is pinned by a test against golden vectors, library
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline legs may import this
+package, and only as the reference results are compared against (or the timed CPU
+baseline); the product package `hackathon_amd` never imports it. Each function is pinned by a test against golden vectors, library
 routines or invariants (tests/test_oracle_*.py); see the pin list in each module.
 """
