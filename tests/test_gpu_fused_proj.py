@@ -79,15 +79,17 @@ def test_qkv_rope_matches_separate_layers(seq):
         assert _rel(a, b) < 1e-2, (name, _rel(a, b))
 
 
-def test_gate_up_swiglu_matches_separate_layers():
-    print("fused gate/up", flush=True)
+@pytest.mark.parametrize("seq", [96, 37])
+def test_gate_up_swiglu_matches_separate_layers(seq):
+    """seq 37: 74 token rows, so the fused SwiGLU backward's last 32-row block is ragged."""
+    print(f"fused gate/up seq={seq}", flush=True)
     cfg, model = _model()
     mlp = model.model.layers[0].mlp
     layers = (mlp.gate_proj, mlp.up_proj)
     params = _params(layers)
     g = torch.Generator(device="cuda").manual_seed(2)
-    x = torch.randn(2, 96, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
-    w = torch.randn(2, 96, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    x = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(2, seq, 1024, device="cuda", generator=g).to(torch.bfloat16)
 
     h = swiglu.swiglu(mlp.gate_proj(x), mlp.up_proj(x))
     (h.float() * w).sum().backward()
