@@ -599,35 +599,51 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
   }
 }
 
-// out = alpha * sum over splits of ws[split] ([N, nc] fp32 each), in split order; one thread
-// per 4 consecutive values. splits = 0 writes zeros.
+// out = alpha * sum over splits of ws[split] ([N, nc] fp32 each); splits = 0 writes zeros.
+// 64 float4 outputs per workgroup: wave w sums splits [w S / 4, (w + 1) S / 4) in split order
+// (all of its loads for an output in flight together, 4 at a time), and wave 0 adds the other
+// waves' sums in wave order, so the result does not depend on the launch shape.
 __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
                                                          int64_t N, int nc,
                                                          float* __restrict__ out, float alpha,
                                                          bool out_t) {
+  __shared__ float4 part[3][64];
   const int64_t total4 = N * nc / 4;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total4;
-       i += (int64_t)gridDim.x * 256) {
-    // 8 partials loaded at a time (independent loads in flight), added in split order
-    const float4* w4 = reinterpret_cast<const float4*>(ws) + i;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int z0 = splits * w / 4, z1 = splits * (w + 1) / 4;
+  for (int64_t base = (int64_t)blockIdx.x * 64; base < total4; base += (int64_t)gridDim.x * 64) {
+    const int64_t i = base + lane;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    int z = 0;
-    for (; z + 8 <= splits; z += 8) {
-      float4 w[8];
+    if (i < total4) {
+      const float4* w4 = reinterpret_cast<const float4*>(ws) + i;
+      int z = z0;
+      for (; z + 4 <= z1; z += 4) {
+        float4 t[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) w[j] = w4[(int64_t)(z + j) * total4];
+        for (int j = 0; j < 4; ++j) t[j] = w4[(int64_t)(z + j) * total4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v.x += w[j].x; v.y += w[j].y; v.z += w[j].z; v.w += w[j].w;
+        for (int j = 0; j < 4; ++j) {
+          v.x += t[j].x; v.y += t[j].y; v.z += t[j].z; v.w += t[j].w;
+        }
+      }
+      for (; z < z1; ++z) {
+        const float4 t = w4[(int64_t)z * total4];
+        v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
       }
     }
-    for (; z < splits; ++z) {
-      const float4 w = w4[(int64_t)z * total4];
-      v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+    if (w > 0) part[w - 1][lane] = v;
+    __syncthreads();
+    if (w == 0 && i < total4) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const float4 t = part[q][lane];
+        v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
+      }
+      const int64_t n = (4 * i) / nc, c = 4 * i - n * nc;
+      store_wgrad4(out, out_t, N, nc, n, c, make_float4(alpha * v.x, alpha * v.y, alpha * v.z,
+                                                        alpha * v.w));
     }
-    const int64_t n = (4 * i) / nc, c = 4 * i - n * nc;
-    store_wgrad4(out, out_t, N, nc, n, c, make_float4(alpha * v.x, alpha * v.y, alpha * v.z,
-                                                      alpha * v.w));
+    __syncthreads();
   }
 }
 
@@ -749,6 +765,12 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
 
 unsigned grid1d(int64_t n) {
   int64_t g = (n + 255) / 256;
+  if (g > 4096) g = 4096;
+  return (unsigned)(g > 0 ? g : 1);
+}
+// lora_wgrad_reduce: 64 outputs per workgroup
+unsigned grid64(int64_t n) {
+  int64_t g = (n + 63) / 64;
   if (g > 4096) g = 4096;
   return (unsigned)(g > 0 ? g : 1);
 }
@@ -894,7 +916,7 @@ int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int
       hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U>), grid, dim3(kThreads), 0, s,     \
                          (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,   \
                          out, alpha, out_t);                                                  \
-      hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * nc / 4)), dim3(256), 0, s, ws,    \
+      hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(N * nc / 4)), dim3(256), 0, s, ws,    \
                          splits, N, nc, out, alpha, out_t);                                   \
     }                                                                                         \
   } while (0)
@@ -1045,7 +1067,7 @@ extern "C" int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int
   if (!PT || !Q || !out) return QL_EINVAL;
   if (M == 0) {  // an empty reduction: zeros (a fill kernel, not a memset node)
     if (!ql_aligned(out, 16)) return QL_EALIGN;
-    hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid1d(N * kRank * slots / 4)), dim3(256), 0,
+    hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(N * kRank * slots / 4)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), (const float*)nullptr, 0, N,
                        kRank * slots, out, 0.f, out_transposed != 0);
     return ql_launch_status();
