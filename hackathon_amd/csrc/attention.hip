@@ -116,6 +116,25 @@ QL_DEV uint4 frag_tr(const char* __restrict__ t, int r0, int c0, int fq, int fr)
 // the swizzle maps there (an XOR is its own inverse). Row 4p + l / 16 has row & 15 =
 // 4 w + l / 16 for every load, so the lane's byte offset from the span's first row is fixed:
 // each load is a wave-uniform base (SGPRs) plus that offset.
+// One direct-to-LDS load (16 B per lane from sbase + voff, lane l writing LDS bytes
+// [lds + 16 l, lds + 16 l + 16)), written as inline assembly: the compiler's wait-count pass
+// treats a pending direct-to-LDS load as an out-of-order LDS-counter event and then drains
+// every LDS read (lgkmcnt(0)) before each product that uses one; with the load hidden from
+// it, fragment reads are waited for in order, so reads issued ahead stay in flight. Nothing
+// waits for these loads but wait_all_barrier, which every kernel runs before it reads a tile
+// it loaded. (s_nop 4: the wait states a write of M0, or a VALU write of an address SGPR,
+// needs before a vector memory load reads it; inline assembly gets no hazard padding.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is clobbered on purpose
+QL_DEV void dma_b128(const char* sbase, uint32_t voff, char* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t)lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 struct TileDma {
   uint32_t off;
   int rsub, wave;
@@ -133,8 +152,7 @@ struct TileDma {
       for (int i = 0; i < 4; ++i) {
         const int p = 4 * i + wave;
         const char* base = reinterpret_cast<const char*>(X + (row0 + 4 * p) * ld);
-        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(base + off), (lds_ptr_t)(tile + p * 1024),
-                                         16, 0, 0);
+        dma_b128(base, off, tile + p * 1024);
       }
     } else {
 #pragma unroll
@@ -146,8 +164,7 @@ struct TileDma {
         const uint32_t o = (uint32_t)(gr - base_row) * (uint32_t)(ld * 2) +
                            (uint32_t)(swz_chunk(lane & 15, 4 * p + rsub) * 16);
         const char* base = reinterpret_cast<const char*>(X + base_row * ld);
-        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(base + o), (lds_ptr_t)(tile + p * 1024),
-                                         16, 0, 0);
+        dma_b128(base, o, tile + p * 1024);
       }
     }
   }
@@ -207,6 +224,7 @@ QL_DEV void fwd_block(FwdState<DT>& st, const char* __restrict__ kl, const char*
   for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) s[qt][kt] = zero4();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
@@ -215,6 +233,15 @@ QL_DEV void fwd_block(FwdState<DT>& st, const char* __restrict__ kl, const char*
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) s[qt][kt] = mfma<DT>(kf, st.qf[qt][ds], s[qt][kt]);
     }
+  // 16 steps of 1 row read and 2 products; reads two steps ahead of their products
+  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+  for (int i = 0; i < 14; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  __builtin_amdgcn_sched_barrier(0);
   // mask keys after the query row or past the end; block max per query column
   const bool need_mask = key0 + kRows - 1 > q0 || key0 + kRows > S;
   float bm[2];
@@ -444,16 +471,31 @@ QL_DEV void dkdv_block(DkdvState<DT>& st, const char* __restrict__ cur, char* __
       dp[qt][e] = p * (dp[qt][e] - dv[e]);
     }
   }
+  uint4 pb[2], sb[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const uint4 pb = pack_pair<DT>(sp[2 * ks], sp[2 * ks + 1]);
-    const uint4 sb = pack_pair<DT>(dp[2 * ks], dp[2 * ks + 1]);
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      st.dv[dt] = mfma<DT>(frag_tr(do_l, 32 * ks, 16 * dt, fq, fr), pb, st.dv[dt]);
-      st.dk[dt] = mfma<DT>(frag_tr(q_l, 32 * ks, 16 * dt, fq, fr), sb, st.dk[dt]);
-    }
+    pb[ks] = pack_pair<DT>(sp[2 * ks], sp[2 * ks + 1]);
+    sb[ks] = pack_pair<DT>(dp[2 * ks], dp[2 * ks + 1]);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // 16 steps (ks, dt) of 4 transposing reads and 2 products. The reads run two steps ahead
+  // of their products, so a product waits on reads issued two steps earlier rather than on
+  // the latest one (left to itself the scheduler, short of registers, put each read right
+  // before its product and waited for it).
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int ks = i >> 3, dt = i & 7;
+    st.dv[dt] = mfma<DT>(frag_tr(do_l, 32 * ks, 16 * dt, fq, fr), pb[ks], st.dv[dt]);
+    st.dk[dt] = mfma<DT>(frag_tr(q_l, 32 * ks, 16 * dt, fq, fr), sb[ks], st.dk[dt]);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+  for (int i = 0; i < 14; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int DT>
@@ -612,6 +654,7 @@ QL_DEV void dq_block(DqState<DT>& st, const char* __restrict__ kl, const char* _
     for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) sp[qt][kk] = dp[qt][kk] = zero4();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
@@ -625,6 +668,15 @@ QL_DEV void dq_block(DqState<DT>& st, const char* __restrict__ kl, const char* _
           dp[qt][kk] = mfma<DT>(va, st.df[qt][ds], dp[qt][kk]);
         }
       }
+    // 8 steps of 2 row reads and 4 products; reads two steps ahead of their products
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
     uint4 sb[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -639,12 +691,22 @@ QL_DEV void dq_block(DqState<DT>& st, const char* __restrict__ kl, const char* _
         }
       sb[qt] = pack_pair<DT>(dp[qt][0], dp[qt][1]);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const uint4 ka = frag_tr(kl, 32 * h, 16 * dt, fq, fr);
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) st.dq[qt][dt] = mfma<DT>(ka, sb[qt], st.dq[qt][dt]);
     }
+    // 8 steps of 2 transposing reads and 2 products; reads two steps ahead
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
