@@ -24,8 +24,8 @@
 //      8 aligned rows: bits 1..3 of f run through all 8 values;
 //      ds_read_b64_tr_b16 (32 lanes a cycle on 8 consecutive rows x 32 B): f >> 1 distinct
 //      over 8 aligned rows, the same condition.
-//    Swizzles meeting only one condition left the dK/dV kernel, which LDS bandwidth bounds, at
-//    1.2 to 2.45 stall cycles per LDS instruction.
+//    Swizzles meeting only one condition left the dK/dV kernel at 1.2 to 2.45 bank-conflict
+//    stall cycles per LDS instruction.
 //  - two LDS stages per kernel: the next block's DMA runs under the current block's math,
 //    with one barrier per block.
 //  - 4 waves per workgroup and at most 256 registers per lane, so two workgroups share a CU.
