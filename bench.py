@@ -12,7 +12,7 @@ with HIP events on the stream the kernels run on.
 Also reported in the same line:
   roofline       the dequant kernel against the 8 TB/s HBM peak (algorithmic bytes/launch)
   cpu_baseline   the C oracle's dequant (oracle/nf4_oracle.c, 1 thread) on a bounded sample
-  cpu_baselines  the other configs' CPU side on the host (oracle torch restatements and the
+  cpu_baselines  the other workloads' CPU side on the host (oracle torch restatements and the
                  eager model path), bounded samples with stated extrapolation
   nf4_4864x896   the same dequant on the Qwen2.5-0.5B gate_proj weight (32 rotated sets)
   kernels        per-kernel device time and roofline of the other kernels at their shapes,
@@ -157,7 +157,7 @@ def cpu_baselines(torch):
     g = torch.Generator().manual_seed(0)
     bf = torch.bfloat16
     res = {"cores": torch.get_num_threads(), "kind": "port", "host_cpu": _cpu_model()}
-    # cfg2: RMSNorm 4 x 2048 x 1536 and RoPE q 4x12x2048x128 / k 4x2x2048x128, full shape
+    # RMSNorm 4 x 2048 x 1536 and RoPE q 4x12x2048x128 / k 4x2x2048x128, full shape
     x = torch.randn(8192, 1536, generator=g).to(bf)
     w = (1 + 0.1 * torch.randn(1536, generator=g)).to(bf)
     dy = torch.randn(8192, 1536, generator=g).to(bf)
@@ -176,7 +176,7 @@ def cpu_baselines(torch):
                                              gbs=round(59_768_832 / t / 1e9, 2),
                                              sample="full shape")
     del x, w, dy, q, k
-    # cfg3: full-logits lm_head + cross-entropy forward and dz @ W on 256 of the 8192 rows
+    # full-logits lm_head + cross-entropy forward and dz @ W on 256 of the 8192 rows
     rows, H, V = 256, 1536, 151936
     W32 = (torch.randn(V, H, generator=g) * 0.02).to(bf).float()
     h = torch.randn(rows, H, generator=g).to(bf).float().requires_grad_()
@@ -193,7 +193,8 @@ def cpu_baselines(torch):
         sample=f"{rows} of 8192 rows (fp32 full logits), scaled linearly by rows")
     ce_rate = fl / t
     del W32, h
-    # cfg4 and cfg5: the eager PyTorch path of one Qwen2.5-7B-shaped layer on the host
+    # the 7B MLP and the QLoRA step: the eager PyTorch path of one Qwen2.5-7B-shaped layer on
+    # the host
     cfg = qlora_step.qwen2_config(num_hidden_layers=1, vocab_size=1024)
     model = qlora_step.build_qlora_model(cfg, "cpu")
     mlp = model.model.layers[0].mlp
@@ -225,7 +226,7 @@ def cpu_baselines(torch):
         ms=round(t_step * 1e3, 0), tokens_per_s=round(4096 / t_step, 1),
         sample="extrapolated: one decoder layer fwd+bwd (with its embedding, norm and a 1024-word "
                "head) at 512 and 1024 tokens, fitted linearly to 4096 tokens x 28 layers, plus the "
-               "152064-word head at the cfg3 CPU rate; attention's quadratic term is only "
+               "152064-word head at the lm_head + CE CPU rate above; attention's quadratic term is only "
                "partly in the fit, so this is a lower bound on the CPU time")
     del model, mlp
     return res
