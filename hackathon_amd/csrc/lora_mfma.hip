@@ -275,13 +275,23 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
 //   dgate, dup     = the SwiGLU gradients of (grad, gate, up)     stored, as swiglu_bwd_rows
 //   out[m, c]      = alpha_g * sum_k dgate[m, k] * YG[c, k]        c < 16
 //   out[m, 16 + c] = alpha_u * sum_k dup[m, k] * YU[c, k]
-// Lane l computes the gradients of row l % 16 of a row group at k = chunk + 32 t + 8 (l / 16)
-// .. +7, which is the lane layout of lora_down's MFMA operands: they are stored once and
-// multiplied straight from registers, so the down-projections do not read them back. Each
+// Lane l computes the gradients of row l / 4 of a row group at k = chunk + 32 t + 8 (l % 4)
+// .. +7 (four lanes cover a row's 64 contiguous bytes, so loads and stores coalesce); lane
+// permutes hand them to the MFMAs in the operand layout (row l % 16, k = .. + 8 (l / 16)), so
+// they are stored once and multiplied straight from registers and the down-projections do
+// not read them back. Each
 // workgroup takes kSwigluRows row groups (each fragment of YG / YU then serves all of them)
 // and one 128-k chunk per wave per step: 3 kSwigluRows + 2 fragments of 16 B per lane per
 // 32-k group, all issued before the first wait.
 constexpr int kSwigluRows = 2;
+
+// Lane m receives the 16 B lane src_byte / 4 holds (ds_bpermute, one per dword).
+QL_DEV uint4 to_mfma_layout(const uint4& v, int src_byte) {
+  return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.x),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.y),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.z),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.w));
+}
 
 template <int IT, bool PARTIAL>
 __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
@@ -300,8 +310,14 @@ __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
   const int64_t m0 = (int64_t)blockIdx.x * 16 * R;
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
-  const int koff = 8 * (lane >> 4);
-  // wave-uniform bases at row m0; lane offsets of row m0 + 16 r + lane % 16 (a row past M
+  // Loads, the gradients and their stores use a coalesced layout: lane l takes row l / 4 of
+  // a row group and the 8 elements 8 (l % 4) .. +7 of each 32-k group, so four lanes read one
+  // row's 64 contiguous bytes (in the MFMA layout every lane would touch a row of its own).
+  // The two MFMA operands are then moved to the MFMA layout (row l % 16, elements 8 (l / 16)
+  // .. +7) by lane permutes.
+  const int koff = 8 * (lane & 3);
+  const int mfma_src = 4 * (4 * (lane & 15) + (lane >> 4));  // ds_bpermute byte address
+  // wave-uniform bases at row m0; lane offsets of row m0 + 16 r + lane / 4 (a row past M
   // works on row M - 1)
   const char* grb = reinterpret_cast<const char*>(GR + m0 * ldgr);
   const char* gab = reinterpret_cast<const char*>(GA + m0 * ldga);
@@ -313,7 +329,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
   uint32_t ogr[R], oga[R], oup[R], odg[R], odu[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t row = m0 + 16 * r + (lane & 15);
+    const int64_t row = m0 + 16 * r + (lane >> 2);
     const int64_t rs = (row < M ? row : M - 1) - m0;
     ogr[r] = (uint32_t)((rs * ldgr + koff) * 2);
     oga[r] = (uint32_t)((rs * ldga + koff) * 2);
@@ -321,7 +337,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
     odg[r] = (uint32_t)((rs * lddg + koff) * 2);
     odu[r] = (uint32_t)((rs * lddu + koff) * 2);
   }
-  const uint32_t oy = (uint32_t)(((lane & 15) * ldy + koff) * 2);
+  const uint32_t oy = (uint32_t)(((lane >> 2) * ldy + koff) * 2);  // coalesced, as the rows
   f32x4_t acc[R][2][2];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -359,6 +375,11 @@ __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
     __builtin_amdgcn_sched_barrier(0);  // the step's loads all go out before the first wait
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      yg[t] = to_mfma_layout(yg[t], mfma_src);
+      yu[t] = to_mfma_layout(yu[t], mfma_src);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float gr8[8], ga8[8], up8[8], dg8[8], du8[8];
@@ -375,8 +396,10 @@ __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
         // spilled and waited on the stores).
         *reinterpret_cast<uint4*>(dgb + 2 * kk[t] + odg[r]) = pdg;
         *reinterpret_cast<uint4*>(dub + 2 * kk[t] + odu[r]) = pdu;
-        acc[r][0][t & 1] = mfma<IT>(ok[t] ? yg[t] : z, ok[t] ? pdg : z, acc[r][0][t & 1]);
-        acc[r][1][t & 1] = mfma<IT>(ok[t] ? yu[t] : z, ok[t] ? pdu : z, acc[r][1][t & 1]);
+        const uint4 mdg = to_mfma_layout(pdg, mfma_src);
+        const uint4 mdu = to_mfma_layout(pdu, mfma_src);
+        acc[r][0][t & 1] = mfma<IT>(ok[t] ? yg[t] : z, ok[t] ? mdg : z, acc[r][0][t & 1]);
+        acc[r][1][t & 1] = mfma<IT>(ok[t] ? yu[t] : z, ok[t] ? mdu : z, acc[r][1][t & 1]);
       }
     }
   }
