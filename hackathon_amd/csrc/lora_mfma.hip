@@ -81,6 +81,14 @@ QL_DEV uint4 ld16(const char* base, uint32_t off) {
   return *reinterpret_cast<const uint4*>(base + off);
 }
 
+// Lane m receives the 16 B lane src_byte / 4 holds (ds_bpermute, one per dword).
+QL_DEV uint4 to_mfma_layout(const uint4& v, int src_byte) {
+  return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.x),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.y),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.z),
+                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.w));
+}
+
 template <int IT, int OT, bool PARTIAL, int G, int R>
 __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ Y, int64_t ldy,
@@ -96,18 +104,22 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
   const int64_t m0 = (int64_t)blockIdx.x * 16 * R;
   const int64_t kb = (int64_t)blockIdx.y * k_per_split;
   const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
-  const int koff = 8 * (lane >> 4);
+  // Loads use a coalesced layout (lane l: row l / 4 of a 16-row group, elements 8 (l % 4)
+  // .. +7 of each 32-k group, four lanes per 64 contiguous bytes); lane permutes then move
+  // each fragment to the MFMA operand layout (row l % 16, elements 8 (l / 16) .. +7).
+  const int koff = 8 * (lane & 3);
+  const int mfma_src = 4 * (4 * (lane & 15) + (lane >> 4));  // ds_bpermute byte address
   const char* xb = reinterpret_cast<const char*>(X + m0 * ldx);
   const char* yb = reinterpret_cast<const char*>(Y);
-  uint32_t xo[R];  // row m0 + 16 r + lane % 16; rows past M read row M - 1
+  uint32_t xo[R];  // row m0 + 16 r + lane / 4; rows past M read row M - 1
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t row = m0 + 16 * r + (lane & 15);
+    const int64_t row = m0 + 16 * r + (lane >> 2);
     xo[r] = (uint32_t)((((row < M ? row : M - 1) - m0) * ldx + koff) * 2);
   }
   uint32_t yo[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) yo[g] = (uint32_t)(((16 * g + (lane & 15)) * ldy + koff) * 2);
+  for (int g = 0; g < G; ++g) yo[g] = (uint32_t)(((16 * g + (lane >> 2)) * ldy + koff) * 2);
   f32x4_t acc[R][G][2];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -146,6 +158,15 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) xv[u][r][t] = to_mfma_layout(xv[u][r][t], mfma_src);
+#pragma unroll
+        for (int g = 0; g < G; ++g) yv[u][g][t] = to_mfma_layout(yv[u][g][t], mfma_src);
+      }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -178,6 +199,15 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
     }
     __builtin_amdgcn_sched_barrier(0);
     const uint4 z = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) xv[u][r][t] = to_mfma_layout(xv[u][r][t], mfma_src);
+#pragma unroll
+        for (int g = 0; g < G; ++g) yv[u][g][t] = to_mfma_layout(yv[u][g][t], mfma_src);
+      }
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -285,13 +315,6 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
 // 32-k group, all issued before the first wait.
 constexpr int kSwigluRows = 2;
 
-// Lane m receives the 16 B lane src_byte / 4 holds (ds_bpermute, one per dword).
-QL_DEV uint4 to_mfma_layout(const uint4& v, int src_byte) {
-  return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.x),
-                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.y),
-                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.z),
-                    (uint32_t)__builtin_amdgcn_ds_bpermute(src_byte, (int)v.w));
-}
 
 template <int IT, bool PARTIAL>
 __global__ __launch_bounds__(64 * kDownWaves) void swiglu_bwd_down_kernel(
