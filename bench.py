@@ -106,9 +106,46 @@ def bench_nf4(torch, shape, steps, warmup, sets, seed=0):
     return dict(sec_per_call=sec, bytes_per_call=nbytes, gbs=nbytes / sec / 1e9, n=n)
 
 
-def cpu_baseline_nf4(seconds, shape=(4864, 896)):
-    """The C oracle (1 thread) dequantising the Qwen2.5-0.5B gate_proj weight repeatedly for
-    about `seconds`; returns GB/s of algorithmic bytes."""
+def cpu_baseline_nf4(seconds, shape=(4864, 896), threads=None):
+    """The reference path's dequant on the host: the oracle's vectorised torch restatement
+    (oracle/nf4.py dequant_torch, bit-exact to the C oracle) on `threads` intra-op threads
+    (default: every host CPU), dequantising the Qwen2.5-0.5B gate_proj weight repeatedly for
+    about `seconds`. Returns GB/s of algorithmic bytes."""
+    import numpy as np
+    import torch
+
+    from hackathon_amd import quant
+    from oracle import nf4 as onf4
+
+    threads = threads or os.cpu_count()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g = torch.Generator().manual_seed(0)
+        w = torch.randn(shape, generator=g) * 0.02
+        packed, st = quant.quantize_nf4(w, 64, compress_statistics=True)
+        table = np.array(quant.NF4_CODE, dtype=np.float32)
+        n = shape[0] * shape[1]
+        onf4.dequant_torch(packed, st, table)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            onf4.dequant_torch(packed, st, table)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    nbytes = nf4_algorithmic_bytes(n)
+    return dict(value=round(nbytes * reps / el / 1e9, 3), unit="GB/s", cores=threads,
+                kind="port",
+                sample=f"torch CPU restatement of the reference dequant (oracle dequant_torch, "
+                       f"bit-exact to the C oracle) of a {shape[0]}x{shape[1]} weight to bf16, "
+                       f"{reps} repetitions in {el:.1f} s on {threads} threads")
+
+
+def cpu_baseline_nf4_c(seconds, shape=(4864, 896)):
+    """The C oracle (one host thread) on the same weight, for comparison."""
     import numpy as np
     import torch
 
@@ -233,66 +270,117 @@ def cpu_baselines(torch):
 
 
 # ---------------------------------------------------------------------------------------------
-def bench_kernels(torch):
-    """Device time per call (graph replay) and roofline fraction of the other kernels."""
-    from hackathon_amd import cross_entropy, gemm, nf4, quant, rmsnorm, rope, swiglu
+MALL_BYTES = 256 * 2**20   # MI355X Infinity Cache: rotated working sets must exceed it
+
+
+def _rotated_sets(bytes_per_set, minimum=5):
+    """Buffer sets to rotate so that the sets together exceed the MALL (at least `minimum`)."""
+    return max(minimum, math.ceil(1.25 * MALL_BYTES / bytes_per_set))
+
+
+def _rate(name, t, nbytes, res):
+    res[name] = dict(us=round(t * 1e6, 2), gbs=round(nbytes / t / 1e9, 1),
+                     frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3), bytes=nbytes)
+
+
+def bench_rmsnorm(torch, res, replays=4):
+    """RMSNorm forward and backward at 4 x 2048 x 1536 bf16 (eps 1e-6), rotating buffer sets
+    larger than the MALL so every launch streams from HBM."""
     from hackathon_amd import _lib
 
-    res = {}
-    dev = "cuda"
-    # RMSNorm at Qwen2.5-1.5B: 4 x 2048 x 1536 bf16
     M, N = 8192, 1536
-    x = torch.randn(M, N, device=dev).to(torch.bfloat16)
-    w = (1 + 0.1 * torch.randn(N, device=dev)).to(torch.bfloat16)
-    y = torch.empty_like(x)
-    rstd = torch.empty(M, device=dev)
-    dy = torch.randn(M, N, device=dev).to(torch.bfloat16)
-    dx = torch.empty_like(x)
-    s = lambda: _lib.stream_of(x)  # noqa: E731
+    g = torch.Generator(device="cuda").manual_seed(0)
+    w = (1 + 0.1 * torch.randn(N, device="cuda", generator=g)).to(torch.bfloat16)
+    fwd_bytes = 2 * M * N * 2 + N * 2 + M * 4
+    bwd_bytes = 3 * M * N * 2 + N * 2 + M * 4
+    sets = _rotated_sets(bwd_bytes)
+    bufs = []
+    for _ in range(sets):
+        x = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
+        dy = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
+        bufs.append((x, dy, torch.empty_like(x), torch.empty(M, device="cuda"),
+                     torch.empty_like(x)))
+    s = _lib.stream_of(w)
 
-    def fwd():
+    def fwd(b):
+        x, _, y, rstd, _ = b
         _lib.call("qlora_rmsnorm_fwd", x.data_ptr(), 2, N, w.data_ptr(), 2, y.data_ptr(), 2, N,
-                  rstd.data_ptr(), M, N, 1e-6, s())
+                  rstd.data_ptr(), M, N, 1e-6, s)
 
-    def bwd():
+    def bwd(b):
+        x, dy, _, rstd, dx = b
         _lib.call("qlora_rmsnorm_bwd", dy.data_ptr(), 2, N, x.data_ptr(), 2, N, w.data_ptr(), 2,
-                  rstd.data_ptr(), dx.data_ptr(), 2, N, M, N, s())
-    for name, fn, nbytes in (("rmsnorm_fwd_8192x1536", fwd, 2 * M * N * 2 + N * 2 + M * 4),
-                             ("rmsnorm_bwd_8192x1536", bwd, 3 * M * N * 2 + N * 2 + M * 4)):
-        t = _graph_time([fn] * 20, torch)
-        res[name] = dict(us=round(t * 1e6, 2), gbs=round(nbytes / t / 1e9, 1),
-                         frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3))
-    # RoPE at Qwen2.5-1.5B: q 4x12x2048x128, k 4x2x2048x128 (B,S,H,D buffers), bf16
+                  rstd.data_ptr(), dx.data_ptr(), 2, N, M, N, s)
+    for b in bufs:
+        fwd(b)
+    calls = 4 * sets
+    t = _graph_time([lambda b=bufs[i % sets]: fwd(b) for i in range(calls)], torch, replays)
+    _rate("rmsnorm_fwd_8192x1536", t, fwd_bytes, res)
+    t = _graph_time([lambda b=bufs[i % sets]: bwd(b) for i in range(calls)], torch, replays)
+    _rate("rmsnorm_bwd_8192x1536", t, bwd_bytes, res)
+    res["rmsnorm_fwd_8192x1536"]["rotated_sets"] = res["rmsnorm_bwd_8192x1536"]["rotated_sets"] = sets
+
+
+def bench_rope(torch, res, replays=4):
+    """RoPE forward and backward of q (4,12,2048,128) and k (4,2,2048,128), (B,H,S,D) views of
+    (B,S,H,D) buffers, cos/sin (1,2048,128) broadcast over the batch, theta 1e6, bf16; rotated
+    buffer sets larger than the MALL."""
+    from hackathon_amd import rope
+
+    dev = "cuda"
     B, S, HQ, HK, D = 4, 2048, 12, 2, 128
-    q = torch.randn(B, S, HQ, D, device=dev).to(torch.bfloat16).transpose(1, 2)
-    k = torch.randn(B, S, HK, D, device=dev).to(torch.bfloat16).transpose(1, 2)
     inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev).float() / D))
     emb = torch.cat([torch.outer(torch.arange(S, device=dev).float(), inv)] * 2, -1)
     cos, sin = emb.cos()[None].to(torch.bfloat16), emb.sin()[None].to(torch.bfloat16)
     cos_e, sin_e = cos.expand(B, S, D), sin.expand(B, S, D)
-    qo, ko = torch.empty_like(q), torch.empty_like(k)
-    rope_bytes = 2 * 2 * B * S * (HQ + HK) * D + 2 * 2 * S * D
-    t = _graph_time([lambda: rope._launch(q, k, cos_e, sin_e, qo, ko, False)] * 20, torch)
-    res["rope_fwd_4x2048x(12+2)x128"] = dict(us=round(t * 1e6, 2), gbs=round(rope_bytes / t / 1e9, 1),
-                                            frac_hbm=round(rope_bytes / t / 1e9 / HBM_PEAK_GBS, 3))
-    # SwiGLU at the 7B MLP: 4096 x 18944 bf16
+    nbytes = 2 * 2 * B * S * (HQ + HK) * D + 2 * 2 * S * D
+    sets = _rotated_sets(nbytes)
+    g = torch.Generator(device=dev).manual_seed(0)
+    bufs = []
+    for _ in range(sets):
+        q = torch.randn(B, S, HQ, D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+        k = torch.randn(B, S, HK, D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+        bufs.append((q, k, torch.empty_like(q), torch.empty_like(k)))
+    calls = 4 * sets
+    for name, backward in (("rope_fwd_4x2048x(12+2)x128", False),
+                           ("rope_bwd_4x2048x(12+2)x128", True)):
+        fns = [lambda b=bufs[i % sets], bw=backward: rope._launch(b[0], b[1], cos_e, sin_e, b[2],
+                                                                  b[3], bw)
+               for i in range(calls)]
+        t = _graph_time(fns, torch, replays)
+        _rate(name, t, nbytes, res)
+        res[name]["rotated_sets"] = sets
+
+
+def bench_swiglu(torch, res):
+    """SwiGLU forward and backward at the 7B MLP, 4096 x 18944 bf16 (465.6 / 775.9 MB per
+    call, more than the MALL)."""
+    from hackathon_amd import _lib
+
     n = 4096 * 18944
-    gt = torch.randn(n, device=dev).to(torch.bfloat16)
-    up = torch.randn(n, device=dev).to(torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    gt = torch.randn(n, device="cuda", generator=g).to(torch.bfloat16)
+    up = torch.randn(n, device="cuda", generator=g).to(torch.bfloat16)
     o = torch.empty_like(gt)
-    gr = torch.randn(n, device=dev).to(torch.bfloat16)
+    gr = torch.randn(n, device="cuda", generator=g).to(torch.bfloat16)
     dg, du = torch.empty_like(gt), torch.empty_like(gt)
+    s = _lib.stream_of(gt)
     for name, fn, nbytes in (
-            ("swiglu_fwd_4096x18944", lambda: _lib.call("qlora_swiglu_fwd", gt.data_ptr(), up.data_ptr(),
-                                                       o.data_ptr(), 2, n, s()), 3 * 2 * n),
-            ("swiglu_bwd_4096x18944", lambda: _lib.call("qlora_swiglu_bwd", gr.data_ptr(), gt.data_ptr(),
-                                                       up.data_ptr(), dg.data_ptr(), du.data_ptr(), 2,
-                                                       n, s()), 5 * 2 * n)):
-        t = _graph_time([fn] * 10, torch)
-        res[name] = dict(us=round(t * 1e6, 2), gbs=round(nbytes / t / 1e9, 1),
-                         frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3))
-    del gt, up, o, gr, dg, du
-    # GEMMs of the 7B MLP: x[4096,3584] @ W[18944,3584]^T and dY[4096,18944] @ W
+            ("swiglu_fwd_4096x18944", lambda: _lib.call("qlora_swiglu_fwd", gt.data_ptr(),
+                                                       up.data_ptr(), o.data_ptr(), 2, n, s),
+             3 * 2 * n),
+            ("swiglu_bwd_4096x18944", lambda: _lib.call("qlora_swiglu_bwd", gr.data_ptr(),
+                                                       gt.data_ptr(), up.data_ptr(), dg.data_ptr(),
+                                                       du.data_ptr(), 2, n, s), 5 * 2 * n)):
+        _rate(name, _graph_time([fn] * 10, torch), nbytes, res)
+
+
+def bench_gemms(torch, res):
+    """The MLP's GEMM shapes: x[4096,3584] @ W[18944,3584]^T and dY[4096,18944] @ W, beside
+    hipBLASLt through torch.matmul on the same operands."""
+    from hackathon_amd import gemm
+
+    dev = "cuda"
     for name, (Mm, Nn, Kk, b_kn) in (("gemm_nt_4096x18944x3584", (4096, 18944, 3584, False)),
                                      ("gemm_nt_4096x3584x18944", (4096, 3584, 18944, False)),
                                      ("gemm_nn_4096x3584x18944", (4096, 3584, 18944, True))):
@@ -307,32 +395,73 @@ def bench_kernels(torch):
         tt = _graph_time([lambda: torch.matmul(a, bm if b_kn else bm.t(), out=ref)] * 5, torch)
         res[name]["torch_hipblaslt_tflops"] = round(fl / tt / 1e12, 1)
         del a, bm, c, ref
-    # fused lm_head + CE at Qwen2.5-1.5B: 8192 x 1536 x 151936 bf16, fwd + dz@W
+
+
+def bench_ce(torch, res, reps=3):
+    """Fused lm_head + cross-entropy at 8192 x 1536 x 151936 bf16 (hidden ~N(0,1), W
+    ~N(0,0.02), 10% of the labels ignored): forward with the hidden gradient, 2 x 3.824 TFLOP."""
+    from hackathon_amd import cross_entropy
+
+    dev = "cuda"
     n_rows, H, V = 8192, 1536, 151936
-    hid = torch.randn(n_rows, H, device=dev).to(torch.bfloat16).requires_grad_()
-    W = (torch.randn(V, H, device=dev) * 0.02).to(torch.bfloat16)
-    tgt = torch.randint(0, V, (n_rows,), device=dev)
-    tgt[torch.rand(n_rows, device=dev) < 0.1] = -100
+    g = torch.Generator(device=dev).manual_seed(0)
+    hid = torch.randn(n_rows, H, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    W = (torch.randn(V, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    tgt = torch.randint(0, V, (n_rows,), device=dev, generator=g)
+    tgt[torch.rand(n_rows, device=dev, generator=g) < 0.1] = -100
     denom = (tgt != -100).sum()
 
     def ce_step():
-        loss, *_ = cross_entropy.FusedLinearCrossEntropy.apply(hid, W, tgt, denom, torch.bfloat16, 512)
+        loss, *_ = cross_entropy.FusedLinearCrossEntropy.apply(hid, W, tgt, denom,
+                                                               torch.bfloat16, 512)
         return loss
     ce_step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(3):
+    for _ in range(reps):
         ce_step()
     e1.record()
     torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) * 1e-3 / 3
+    t = e0.elapsed_time(e1) * 1e-3 / reps
     fl = 2 * 2.0 * n_rows * H * V
     res["fused_ce_8192x1536x151936"] = dict(ms=round(t * 1e3, 2), tflops=round(fl / t / 1e12, 1),
                                            frac_mfma=round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 3))
-    del hid, W, tgt
+
+
+def bench_kernels(torch):
+    """Device time per call and roofline fraction of the other kernels at their configs."""
+    res = {}
+    bench_rmsnorm(torch, res)
+    bench_rope(torch, res)
+    bench_swiglu(torch, res)
+    bench_gemms(torch, res)
+    bench_ce(torch, res)
     res["qwen25_7b_mlp_lora_4096tok"] = bench_mlp(torch)
     return res
+
+
+WORKLOADS = {
+    "rmsnorm": lambda torch, res: bench_rmsnorm(torch, res),
+    "rope": lambda torch, res: bench_rope(torch, res),
+    "swiglu": lambda torch, res: bench_swiglu(torch, res),
+    "gemm": lambda torch, res: bench_gemms(torch, res),
+    "ce": lambda torch, res: bench_ce(torch, res),
+    "mlp": lambda torch, res: res.update(qwen25_7b_mlp_lora_4096tok=bench_mlp(torch)),
+    "nf4_small": lambda torch, res: res.update(nf4_4864x896=bench_nf4(
+        torch, (4864, 896), 200, 5, 32, seed=1)),
+}
+
+
+def calibration_copy(torch, mib=256):
+    """One plain device-to-device copy of `mib` MiB (known bytes each way): the reference
+    dispatch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes in the same run."""
+    src = torch.ones(mib * 2**19, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def bench_mlp(torch, tokens=4096, reps=3):
@@ -491,6 +620,79 @@ def trace_summary(path):
         print(f"| {k} | {cnt[k]} | {v:.2f} | {100 * v / total:.1f} |")
 
 
+def _short_kernel(name, width=64):
+    """Kernel name without its argument list, clipped for a table."""
+    name = name.replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):
+        depth += (ch == "<") - (ch == ">")
+        if ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    return name if len(name) <= width else name[: width - 3] + "..."
+
+
+def profile_summary(trace_csv, fetch_csv=None, write_csv=None, copy_mib=256):
+    """Markdown table of a rocprofv3 run: per (kernel, grid size) the dispatch count and the
+    average / min / max duration from the kernel trace; with the two PMC passes of the same
+    command, FETCH_SIZE and WRITE_SIZE per dispatch scaled to bytes by the run's calibration
+    copy (the largest __amd_rocclr_copyBuffer dispatch, `copy_mib` MiB each way)."""
+    import collections
+    import csv
+
+    def key(name, grid):
+        return (_short_kernel(name), int(grid))
+
+    durs = collections.defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        durs[key(r["Kernel_Name"], r["Grid_Size_X"])].append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+
+    def counters(path, counter):
+        per, calib = collections.defaultdict(list), None
+        if path is None:
+            return per, None
+        vals = collections.defaultdict(float)
+        names = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            d = r["Dispatch_Id"]
+            vals[d] += float(r["Counter_Value"])
+            names[d] = (r["Kernel_Name"], r["Grid_Size"])
+        copies = [v for d, v in vals.items() if "copyBuffer" in names[d][0]]
+        if copies:
+            calib = copy_mib * 1024 / max(copies)
+        for d, v in vals.items():
+            per[key(*names[d])].append(v * 1024 * (calib or 1.0))
+        return per, calib
+
+    fetch, fcal = counters(fetch_csv, "FETCH_SIZE")
+    write, wcal = counters(write_csv, "WRITE_SIZE")
+    total = sum(sum(v) for v in durs.values())
+    head = "| kernel | grid | calls | avg us | min us | max us | % time |"
+    sep = "|---|---|---|---|---|---|---|"
+    if fetch_csv:
+        head += " fetch MB/call | write MB/call |"
+        sep += "---|---|"
+    print(head)
+    print(sep)
+    for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+        row = (f"| `{k[0]}` | {k[1]} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | "
+               f"{max(v):.2f} | {100 * sum(v) / total:.1f} |")
+        if fetch_csv:
+            f, w = fetch.get(k), write.get(k)
+            row += (f" {sum(f) / len(f) / 1e6:.2f} |" if f else " - |")
+            row += (f" {sum(w) / len(w) / 1e6:.2f} |" if w else " - |")
+        print(row)
+    if fetch_csv:
+        print(f"\ncalibration ({copy_mib} MiB device copy in the same run): FETCH_SIZE x"
+              f"{fcal if fcal is None else round(fcal, 4)}, WRITE_SIZE x"
+              f"{wcal if wcal is None else round(wcal, 4)}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -512,9 +714,19 @@ def main():
                          "launches, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="print the per-step kernel table of a rocprofv3 kernel trace and exit")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS),
+                    help="run one workload of the kernel table alone, after a 256 MiB calibration "
+                         "copy, and print its JSON (for rocprofv3 kernel-trace and PMC passes)")
+    ap.add_argument("--profile-summary", nargs="+", metavar="CSV",
+                    help="per-kernel table from a rocprofv3 kernel_trace.csv, optionally followed "
+                         "by FETCH_SIZE and WRITE_SIZE counter_collection.csv files of the same "
+                         "command (calibrated by its copy kernel); prints markdown and exits")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
+        return
+    if args.profile_summary:
+        profile_summary(*args.profile_summary)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the kernels work on one "
@@ -532,6 +744,13 @@ def main():
     shape = (18944, 3584)
     if args.pmc_probe:
         pmc_probe(torch, shape)
+        return
+    if args.workload:
+        calibration_copy(torch)
+        res = {}
+        WORKLOADS[args.workload](torch, res)
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": args.workload, **res}), flush=True)
         return
     torch.cuda.synchronize()
     r = bench_nf4(torch, shape, args.steps, args.warmup, args.sets)
@@ -570,6 +789,7 @@ def main():
                                         layers=args.step_layers, parity=args.eager_steps > 0)
     line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     line["cpu_baseline"]["host_cpu"] = _cpu_model()
+    line["cpu_baseline_c_1thread"] = cpu_baseline_nf4_c(min(args.cpu_seconds, 5.0))
     if not args.no_cpu_configs:
         t0 = time.perf_counter()
         line["cpu_baselines"] = cpu_baselines(torch)

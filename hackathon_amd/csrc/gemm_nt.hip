@@ -501,14 +501,37 @@ int64_t ql_gemm_nt_workspace_floats(int64_t M, int64_t N, int splits) {
   return splits > 1 ? (int64_t)splits * M * N : 0;
 }
 
+// Split count of an M x N x K product: the s in 1..64 (at least 8 K steps per split) with the
+// least modelled time, in units of one workgroup's K step:
+//   ceil(tiles * s / 256) rounds of the 256 CUs, each (K steps per split + kTileFixedSteps)
+//   long (the prologue's first load and the epilogue's stores of a tile), plus, for s > 1,
+//   the split-K reduce reading s fp32 partials of the output and writing it once, at
+//   kStepBytes of HBM traffic per step-time.
+// An output of 192 tiles of 256 x 256 (8192 x 1536, the hidden gradient of the fused
+// lm_head + CE) takes s = 4: three full rounds instead of one round on 75% of the CUs.
+constexpr int64_t kCUs = 256;
+constexpr int64_t kTileFixedSteps = 8;
+constexpr double kStepBytes = 9.6e6;  // ~1.6 us of a K step at ~6 TB/s
+
 int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
-  // Enough workgroups for 256 CUs: split K while there are fewer tiles than CUs and each
-  // split keeps at least 8 K steps.
   const int64_t bn = 32 * choose_nb(M, N);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + bn - 1) / bn);
-  int s = 1;
-  while (tiles * s < 192 && (K / BK) / (2 * s) >= 8 && s < 64) s *= 2;
-  return s;
+  const int64_t steps = K / BK;
+  auto cost = [&](int64_t s) {
+    const int64_t rounds = (tiles * s + kCUs - 1) / kCUs;
+    const double reduce = s > 1 ? double(s + 1) * double(M) * double(N) * 4.0 / kStepBytes : 0.0;
+    return double(rounds * ((steps + s - 1) / s + kTileFixedSteps)) + reduce;
+  };
+  int best = 1;
+  double best_cost = cost(1);
+  for (int s = 2; s <= 64 && steps / s >= 8; ++s) {
+    const double c = cost(s);
+    if (c < 0.97 * best_cost) {  // a split must save at least 3% to be worth its workspace
+      best = s;
+      best_cost = c;
+    }
+  }
+  return best;
 }
 
 int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,

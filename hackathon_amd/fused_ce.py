@@ -1,112 +1,82 @@
-"""The output head and the loss without the full logits tensor (drop-in for solution/fused_ce.py).
+"""The output head and the loss without the full logits tensor, with row selection: drop-in
+for solution/fused_ce.py (the variant that keeps only the rows a training step needs).
 
-Per training forward (solution/fused_ce.py:8-19):
-1. only the positions that matter are kept, labelled rows first, then real unlabelled rows
-   (for the entropy metric); padding is dropped;
-2. the head runs on CHUNK rows at a time into one reused [CHUNK, vocab] buffer
-   (qlora_gemm, fp16 operands as the reference's autocast run);
-3. one workgroup per row reads the row of logits and computes logsumexp, the cross-entropy at
-   the label, the entropy and the argmax; a second sweep overwrites the logits in place with
-   softmax - onehot (qlora_ce_rows);
-4. the hidden-state gradient dz @ W is taken right there, chunk by chunk (qlora_gemm into an
-   fp32 buffer), so nothing of vocabulary size outlives its chunk; backward only scales it.
+`fused_head_loss` computes transformers' ForCausalLMLoss(lm_head(hidden), labels) and the
+per-row statistics TRL's metrics need, through `vocab_pass` (head GEMM, row kernel, hidden
+gradient per group of rows, the head in fp16 as the reference's autocast run has it):
+
+  - the rows of the pass are the positions with a label, then the real positions without one
+    (entropy only), each in position order; padding positions are left out. The order comes
+    from one stable sort of a per-position rank (0 labelled, 1 real unlabelled, 2 padding);
+  - the hidden gradient is taken in the forward for the labelled rows only, divided by the
+    loss's denominator; backward only scales it (the head is frozen);
+  - per-position loss and entropy are scattered back to [batch, seq] for the trainer hook
+    (TRL's metrics) and for a rewind recorder (`token_loss`).
+
+The model and trainer hooks (solution/fused_ce.py:222-355) are built from `head_hooks`.
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import _lib
-from . import gemm as _gemm
+from . import _lib, head_hooks, vocab_pass
 
-CHUNK = 512  # rows of logits alive at a time (solution/fused_ce.py:33)
+CHUNK = 512  # rows of logits per chunk, the unit of the logits budget (solution/fused_ce.py:33)
 IGNORE = -100
-STEP_ATTR = "_soup_chunked_step"
+STEP_ATTR = head_hooks.STEP_ATTR
+VARIANT = "fused_ce"
+
+_LABELLED, _UNLABELLED, _PADDING = 0, 1, 2
 
 
 def ce_rows(logits, target, write_grad):
     """Per-row loss, entropy and correct flag of [n, vocab] logits; with write_grad the logits
-    are overwritten by softmax - onehot (solution/fused_ce.py:99-109)."""
+    are overwritten by softmax - onehot (solution/fused_ce.py:99-109). Rows with a negative
+    target are unlabelled."""
     _lib.require_device(logits, target)
-    n, vocab = logits.shape
     if logits.stride(-1) != 1:
         raise ValueError("logits rows must be unit-stride")
-    target = target.to(torch.int64).contiguous()
-    loss = torch.empty(n, dtype=torch.float32, device=logits.device)
-    entropy = torch.empty(n, dtype=torch.float32, device=logits.device)
-    correct = torch.empty(n, dtype=torch.int32, device=logits.device)
-    if n:
-        _lib.call("qlora_ce_rows", logits.data_ptr(), _lib.tag(logits.dtype), logits.stride(0),
-                  n, vocab, target.data_ptr(), loss.data_ptr(), entropy.data_ptr(),
-                  correct.data_ptr(), None, 0, int(bool(write_grad)), 1.0,
-                  _lib.stream_of(logits))
-    return loss, entropy, correct
-
-
-def _head_gemm(h, w, out):
-    """logits chunk = h @ w.T into `out` (MFMA kernel for 16-bit operands)."""
-    if h.dtype in (torch.float16, torch.bfloat16):
-        _gemm.gemm(h, w, out=out)
-    else:
-        torch.mm(h, w.t(), out=out)
-
-
-def _grad_gemm(dz, w, out):
-    """out (fp32) = dz @ w, run as dz @ (w^T)^T against the cached transpose of the frozen
-    head weight, so both operands are k-contiguous (the vocabulary is the reduction)."""
-    if dz.dtype in (torch.float16, torch.bfloat16):
-        _gemm.gemm(dz, _gemm.transposed_frozen(w), out=out)
-    else:
-        out.copy_(torch.mm(dz, w))
+    out = vocab_pass.RowResults(logits.shape[0], logits.device, correct=True)
+    vocab_pass.row_statistics(logits, target.to(torch.int64).contiguous(), out, 0,
+                              vocab_pass.IGNORE_NEGATIVE, write_grad, 1.0)
+    return out.loss, out.entropy, out.correct
 
 
 class FusedLinearCE(torch.autograd.Function):
-    """Rows of hidden states [n, hidden] -> sum of their cross-entropies / denominator
-    (solution/fused_ce.py:112-158). Rows [0, n_labelled) have a label; the head is frozen and
-    the hidden gradient is computed in forward and only scaled in backward."""
+    """Rows of hidden states [n, hidden] -> sum of their cross-entropies / denominator, and the
+    per-row loss, entropy and correct flag (solution/fused_ce.py:112-158). Rows [0, n_labelled)
+    carry a label; the others only feed the metrics. weight16 is the frozen fp16 head."""
 
     @staticmethod
     def forward(ctx, hidden, weight16, target, n_labelled, denominator):
+        _lib.require_device(hidden, weight16)
         n, width = hidden.shape
-        vocab = weight16.shape[0]
-        with_grad = ctx.needs_input_grad[0]
-        hidden16 = hidden.to(weight16.dtype).contiguous()
-        weight16 = weight16.contiguous()
-        grad = torch.zeros((n, width), dtype=torch.float32, device=hidden.device) \
-            if with_grad else None
-        buffer = _gemm.padded_rows(min(CHUNK, max(n, 1)), vocab, weight16.dtype, hidden.device)
-        losses, entropies, corrects = [], [], []
+        rows = vocab_pass.RowResults(n, hidden.device, correct=True)
+        grad = None
+        if ctx.needs_input_grad[0]:
+            grad = torch.zeros((n, width), dtype=torch.float32, device=hidden.device)
         with torch.autocast(hidden.device.type, enabled=False):
-            for start in range(0, n, CHUNK):
-                stop = min(n, start + CHUNK)
-                logits = buffer[: stop - start]
-                _head_gemm(hidden16[start:stop], weight16, logits)
-                labelled = max(0, min(stop, n_labelled) - start)
-                write_grad = with_grad and labelled > 0
-                loss, entropy, correct = ce_rows(logits, target[start:stop], write_grad)
-                losses.append(loss)
-                entropies.append(entropy)
-                corrects.append(correct)
-                if write_grad:
-                    _grad_gemm(logits[:labelled], weight16, grad[start:start + labelled])
-        del buffer
-        row_loss = torch.cat(losses) if losses else hidden.new_zeros(0, dtype=torch.float32)
-        row_entropy = torch.cat(entropies) if entropies else row_loss
-        row_correct = torch.cat(corrects) if corrects else row_loss.int()
-        total = row_loss.sum() / denominator
-        if with_grad:
-            grad /= denominator
-            ctx.save_for_backward(grad)
-        ctx.mark_non_differentiable(row_loss, row_entropy, row_correct)
-        return total, row_loss, row_entropy, row_correct
+            vocab_pass.run(hidden.to(weight16.dtype).contiguous(), weight16.contiguous(),
+                           target.to(torch.int64).contiguous(), rows,
+                           ignore_mode=vocab_pass.IGNORE_NEGATIVE, chunk_rows=CHUNK, grad=grad,
+                           grad_rows=int(n_labelled))
+        if grad is not None:
+            ctx.save_for_backward(grad.div_(denominator))
+        ctx.mark_non_differentiable(rows.loss, rows.entropy, rows.correct)
+        return rows.loss.sum() / denominator, rows.loss, rows.entropy, rows.correct
 
     @staticmethod
-    def backward(ctx, grad_total, _l, _e, _c):
+    def backward(ctx, grad_total, _loss, _entropy, _correct):
         (grad,) = ctx.saved_tensors
         return grad * grad_total, None, None, None, None
 
 
 class Stats:
+    """What `fused_head_loss` reports beside the loss: token_loss [batch, seq] (0 off the
+    labelled positions), entropy_sum over the real positions, and the correct and labelled
+    token counts (0-dim tensors)."""
+
     __slots__ = ("token_loss", "entropy_sum", "correct", "labelled")
 
     def __init__(self, token_loss, entropy_sum, correct, labelled):
@@ -115,7 +85,7 @@ class Stats:
 
 
 class _Step:
-    """What a trainer's per-row loss recorder reads for a step without logits."""
+    """What a rewind recorder reads for a step without logits: the per-token loss."""
 
     __slots__ = ("token_loss",)
 
@@ -123,207 +93,150 @@ class _Step:
         self.token_loss = token_loss
 
 
+def _row_order(targets, attention_mask):
+    """(rows, n_labelled): the positions the pass runs, labelled ones first, then real
+    unlabelled ones, each group in position order (one stable sort of the rank)."""
+    rank = torch.full_like(targets, _UNLABELLED)
+    if attention_mask is not None:
+        rank.masked_fill_(attention_mask.reshape(-1) == 0, _PADDING)
+    rank.masked_fill_(targets != IGNORE, _LABELLED)
+    order = torch.sort(rank, stable=True).indices
+    n_labelled, n_unlabelled, _ = torch.bincount(rank, minlength=3).tolist()
+    return order[: n_labelled + n_unlabelled], n_labelled
+
+
+def _denominator(num_items_in_batch, n_labelled, device):
+    """ForCausalLMLoss's divisor: num_items_in_batch when given (a tensor moves to the
+    device), else the number of labelled positions (a mean)."""
+    if num_items_in_batch is None:
+        return torch.tensor(float(n_labelled), device=device)
+    if torch.is_tensor(num_items_in_batch):
+        return num_items_in_batch.to(device)
+    return num_items_in_batch
+
+
 def fused_head_loss(hidden, weight, labels, attention_mask, num_items_in_batch):
-    """ForCausalLMLoss(lm_head(hidden), labels) and TRL's metrics without the logits
-    (solution/fused_ce.py:178-219)."""
+    """ForCausalLMLoss(hidden @ weight.T, labels) and a Stats for TRL's metrics, without the
+    logits (solution/fused_ce.py:178-219). hidden [batch, seq, width]; labels [batch, seq]
+    are shifted here (position t is scored against labels[t + 1])."""
     batch, seq, width = hidden.shape
     device = hidden.device
-    labels = labels.to(device)
-    target = torch.nn.functional.pad(labels, (0, 1), value=IGNORE)[:, 1:].reshape(-1)
-    has_label = target != IGNORE
-    if attention_mask is None:
-        real = torch.ones_like(has_label)
-    else:
-        real = attention_mask.to(device).reshape(-1) != 0
-    other = real & ~has_label
-    label_rows = has_label.nonzero().squeeze(1)
-    other_rows = other.nonzero().squeeze(1)
-    rows = torch.cat([label_rows, other_rows])
-    n_labelled = label_rows.numel()
-
-    if num_items_in_batch is None:
-        denominator = torch.tensor(float(n_labelled), device=device)
-    elif torch.is_tensor(num_items_in_batch):
-        denominator = num_items_in_batch.to(device)
-    else:
-        denominator = num_items_in_batch
-
-    weight16 = weight if weight.dtype == torch.float16 else weight.detach().to(torch.float16)
-    picked = hidden.reshape(-1, width).index_select(0, rows)
+    targets = torch.cat([labels.to(device)[:, 1:],
+                         torch.full((batch, 1), IGNORE, dtype=labels.dtype, device=device)],
+                        dim=1).reshape(-1)
+    if attention_mask is not None:
+        attention_mask = attention_mask.to(device)
+    rows, n_labelled = _row_order(targets, attention_mask)
+    denominator = _denominator(num_items_in_batch, n_labelled, device)
+    head = weight if weight.dtype == torch.float16 else weight.detach().to(torch.float16)
     loss, row_loss, row_entropy, row_correct = FusedLinearCE.apply(
-        picked, weight16, target.index_select(0, rows), n_labelled, denominator)
-
+        hidden.reshape(-1, width)[rows], head, targets[rows], n_labelled, denominator)
     with torch.no_grad():
-        token_loss = torch.zeros(batch * seq, dtype=torch.float32, device=device)
-        token_loss.index_copy_(0, rows, row_loss)
-        token_entropy = torch.zeros(batch * seq, dtype=torch.float32, device=device)
-        token_entropy.index_copy_(0, rows, row_entropy)
-        if attention_mask is None:
-            entropy_sum = token_entropy.sum()
-        else:
-            entropy_sum = (token_entropy * attention_mask.to(device).reshape(-1)).sum()
-        stats = Stats(token_loss=token_loss.view(batch, seq), entropy_sum=entropy_sum,
+        per_position = torch.zeros((2, batch * seq), dtype=torch.float32, device=device)
+        per_position[:, rows] = torch.stack((row_loss, row_entropy))
+        token_loss, token_entropy = per_position
+        if attention_mask is not None:
+            token_entropy = token_entropy * attention_mask.reshape(-1)
+        stats = Stats(token_loss=token_loss.view(batch, seq), entropy_sum=token_entropy.sum(),
                       correct=row_correct[:n_labelled].sum(),
                       labelled=torch.tensor(n_labelled, device=device))
     return loss, stats
 
 
-# ---- model and trainer hooks (solution/fused_ce.py:222-355) ---------------------------------
-class _State:
-    active = False   # set by the trainer hook for exactly one model forward
+# ---- hooks (solution/fused_ce.py:222-355) ----------------------------------------------------
+class _Armed:
+    """Set by the trainer hook around exactly one model forward; the forward leaves its Stats."""
+
+    active = False
     stats = None
 
 
-STATE = _State()
-_ORIGINAL = {}
-
-
-def _causal_lm(model):
-    get_base_model = getattr(model, "get_base_model", None)
-    return get_base_model() if callable(get_base_model) else model
+STATE = _Armed()
+_HEAD_DTYPES = (torch.float32, torch.float16)
 
 
 def _head_fits(causal_lm):
-    """A Qwen2 causal LM whose lm_head is a frozen, bias-free fp32/fp16 Linear on the GPU with
-    no logit soft-capping (solution/fused_ce.py:236-246)."""
-    from transformers.models.qwen2 import modeling_qwen2
-
-    if not isinstance(causal_lm, modeling_qwen2.Qwen2ForCausalLM):
-        return False
-    head = getattr(causal_lm, "lm_head", None)
-    weight = getattr(head, "weight", None)
-    return (type(head) is torch.nn.Linear and head.bias is None and weight is not None
-            and not weight.requires_grad and weight.is_cuda
-            and weight.dtype in (torch.float32, torch.float16)
-            and getattr(causal_lm.config, "final_logit_softcapping", None) is None)
+    """A Qwen2 causal LM whose lm_head is a frozen, bias-free fp32 or fp16 Linear on the GPU
+    with no logit soft-capping (solution/fused_ce.py:236-246)."""
+    return (head_hooks.is_qwen2_causal_lm(causal_lm)
+            and head_hooks.head_refusal(causal_lm, _HEAD_DTYPES) is None)
 
 
-def patch_qwen2_causal_lm():
-    """Qwen2ForCausalLM.forward runs `fused_head_loss` when the trainer hook is active and the
-    call is a plain training forward with labels; otherwise the original
-    (solution/fused_ce.py:249-280)."""
-    from transformers.modeling_outputs import CausalLMOutputWithPast
-    from transformers.models.qwen2 import modeling_qwen2
-
-    cls = modeling_qwen2.Qwen2ForCausalLM
-    if "causal_forward" in _ORIGINAL:
-        return
-    original = cls.forward
-    _ORIGINAL["causal_forward"] = original
-
-    def forward(self, input_ids=None, attention_mask=None, position_ids=None,
-                past_key_values=None, inputs_embeds=None, labels=None, use_cache=None,
-                logits_to_keep=0, **kwargs):
-        if (not STATE.active or labels is None or not self.training
-                or not (isinstance(logits_to_keep, int) and logits_to_keep == 0)
-                or kwargs.get("shift_labels") is not None or kwargs.get("return_dict") is False
-                or not _head_fits(self)):
-            return original(self, input_ids=input_ids, attention_mask=attention_mask,
-                            position_ids=position_ids, past_key_values=past_key_values,
-                            inputs_embeds=inputs_embeds, labels=labels, use_cache=use_cache,
-                            logits_to_keep=logits_to_keep, **kwargs)
-        kwargs.pop("return_dict", None)
-        outputs = self.model(input_ids=input_ids, attention_mask=attention_mask,
-                             position_ids=position_ids, past_key_values=past_key_values,
-                             inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
-        loss, STATE.stats = fused_head_loss(outputs.last_hidden_state, self.lm_head.weight,
-                                            labels, attention_mask,
-                                            kwargs.get("num_items_in_batch"))
-        return CausalLMOutputWithPast(loss=loss, logits=None,
-                                      past_key_values=outputs.past_key_values,
-                                      hidden_states=outputs.hidden_states,
-                                      attentions=outputs.attentions)
-
-    forward._original = original
-    cls.forward = forward
+_REFUSALS = head_hooks.TRAINER_REFUSALS + (
+    ("model is not training", lambda t, m, i: not m.training),
+    ("head does not fit", lambda t, m, i: not _head_fits(head_hooks.base_model(m))),
+)
 
 
 def _can_fuse(trainer, model, inputs):
-    """solution/fused_ce.py:283-301: a training step of plain NLL with labels and an attention
-    mask, the trainer state TRL's metrics need, and a head `_head_fits` accepts."""
-    args = getattr(trainer, "args", None)
-    if args is None or not isinstance(model, torch.nn.Module) or not model.training:
-        return False
-    if getattr(args, "use_liger_kernel", False) or getattr(args, "loss_type", "nll") != "nll":
-        return False
-    if getattr(trainer, "compute_loss_func", None) is not None:
-        return False
-    if getattr(trainer, "label_smoother", None) is not None:
-        return False
-    if getattr(trainer, "num_virtual_tokens", 0) or getattr(trainer, "aux_loss_enabled", False):
-        return False
-    if not hasattr(trainer, "_metrics") or not hasattr(trainer, "_total_train_tokens"):
-        return False
-    if not isinstance(inputs, dict) or "labels" not in inputs or "attention_mask" not in inputs:
-        return False
-    if "shift_labels" in inputs:
-        return False
-    return _head_fits(_causal_lm(model))
+    """Whether a compute_loss call takes the fused head: none of the trainer refusals applies
+    and the (peft-unwrapped) model is a Qwen2 causal LM whose head fits
+    (solution/fused_ce.py:285-303)."""
+    return head_hooks.refusal(_REFUSALS, trainer, model, inputs) is None
+
+
+def _wants(model, labels, logits_to_keep, kwargs):
+    return (STATE.active and labels is not None and model.training
+            and head_hooks.plain_training_call(logits_to_keep, kwargs)
+            and kwargs.get("shift_labels") is None and _head_fits(model))
+
+
+def _head_loss(model, hidden, labels, attention_mask, kwargs):
+    loss, STATE.stats = fused_head_loss(hidden, model.lm_head.weight, labels, attention_mask,
+                                        kwargs.get("num_items_in_batch"))
+    return loss
+
+
+def patch_qwen2_causal_lm():
+    """Qwen2ForCausalLM.forward answers with `fused_head_loss` (no logits) when the trainer hook
+    is active and the call is a plain training forward with labels; any other call runs the
+    forward it wrapped (solution/fused_ce.py:249-282)."""
+    head_hooks.install_model_hook(VARIANT, _wants, _head_loss)
+
+
+def _armed_loss(trainer, model, inputs, num_items_in_batch):
+    from transformers import Trainer
+
+    STATE.active, STATE.stats = True, None
+    try:
+        loss, outputs = Trainer.compute_loss(trainer, model, inputs, return_outputs=True,
+                                             num_items_in_batch=num_items_in_batch)
+    finally:
+        STATE.active = False
+    stats, STATE.stats = STATE.stats, None
+    if stats is None:
+        raise RuntimeError("hackathon_amd: the fused head loss did not run in this step")
+    mask = inputs["attention_mask"]
+    head_hooks.log_trl_metrics(trainer, "train", mask, stats.entropy_sum / mask.sum(),
+                               stats.correct, stats.labelled, count_tokens=True)
+    setattr(trainer, STEP_ATTR, _Step(stats.token_loss))
+    return loss, outputs
+
+
+def _forget_step(trainer):
+    if getattr(trainer, STEP_ATTR, None) is not None:
+        setattr(trainer, STEP_ATTR, None)
+
+
+_HOOKED = []  # trainer classes whose compute_loss this variant wraps
 
 
 def patch_sft_trainer(trainer_cls=None):
     """Activate the fused head inside `trainer_cls.compute_loss` (default: trl's SFTTrainer;
     returns False when trl is not importable), log TRL's metrics from the fused statistics and
-    leave the per-token loss for a recorder under STEP_ATTR (solution/fused_ce.py:304-355)."""
-    from transformers import Trainer
-
+    leave the per-token loss under STEP_ATTR (solution/fused_ce.py:306-355)."""
+    trainer_cls = trainer_cls or head_hooks.default_trainer_class()
     if trainer_cls is None:
-        try:
-            from trl import SFTTrainer as trainer_cls
-        except ImportError:
-            return False
-    if "compute_loss" in _ORIGINAL:
-        return True
-    original = trainer_cls.compute_loss
-    _ORIGINAL["compute_loss"] = (trainer_cls, original)
-
-    def compute_loss(self, model, inputs, return_outputs=False, num_items_in_batch=None):
-        if not _can_fuse(self, model, inputs):
-            if getattr(self, STEP_ATTR, None) is not None:
-                setattr(self, STEP_ATTR, None)
-            return original(self, model, inputs, return_outputs=return_outputs,
-                            num_items_in_batch=num_items_in_batch)
-        mode = "train"
-        inputs.pop("_prediction_loss_only", None)
-        inputs["use_cache"] = False
-        STATE.active, STATE.stats = True, None
-        try:
-            loss, outputs = Trainer.compute_loss(self, model, inputs, return_outputs=True,
-                                                 num_items_in_batch=num_items_in_batch)
-        finally:
-            STATE.active = False
-        stats, STATE.stats = STATE.stats, None
-        if stats is None:
-            raise RuntimeError("hackathon_amd: the fused head loss did not run in this step")
-
-        gather = self.accelerator.gather_for_metrics
-        attention_mask = inputs["attention_mask"]
-        with torch.no_grad():
-            entropy = stats.entropy_sum / attention_mask.sum()
-            entropy = gather(entropy).mean().item()
-        self._metrics[mode]["entropy"].append(entropy)
-        self._total_train_tokens += gather(attention_mask.sum()).sum().item()
-        self._metrics[mode]["num_tokens"] = [self._total_train_tokens]
-        with torch.no_grad():
-            correct_tokens = gather(stats.correct)
-            total_tokens = gather(stats.labelled)
-            total_sum = total_tokens.sum()
-            accuracy = (correct_tokens.sum() / total_sum).item() if total_sum > 0 else 0.0
-        self._metrics[mode]["mean_token_accuracy"].append(accuracy)
-        setattr(self, STEP_ATTR, _Step(stats.token_loss))
-        return (loss, outputs) if return_outputs else loss
-
-    trainer_cls.compute_loss = compute_loss
+        return False
+    head_hooks.install_trainer_hook(VARIANT, trainer_cls, _can_fuse, _armed_loss,
+                                    on_fallback=_forget_step)
+    if trainer_cls not in _HOOKED:
+        _HOOKED.append(trainer_cls)
     return True
 
 
 def unpatch():
-    """Restore what patch_qwen2_causal_lm / patch_sft_trainer replaced."""
-    from transformers.models.qwen2 import modeling_qwen2
-
-    cls_forward = _ORIGINAL.pop("causal_forward", None)
-    if cls_forward is not None:
-        modeling_qwen2.Qwen2ForCausalLM.forward = cls_forward
-    hooked = _ORIGINAL.pop("compute_loss", None)
-    if hooked is not None:
-        hooked[0].compute_loss = hooked[1]
+    """Remove this variant's model and trainer hooks."""
+    head_hooks.remove_model_hook(VARIANT)
+    while _HOOKED:
+        head_hooks.remove_trainer_hook(VARIANT, _HOOKED.pop())

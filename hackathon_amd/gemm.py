@@ -103,24 +103,40 @@ def transpose16(t: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     return out
 
 
-_T_CACHE: dict = {}
+_FROZEN: dict = {}
+
+
+def _frozen(w: torch.Tensor, kind, make):
+    """make(w), kept while `w` is alive and unmodified (same storage, same version) under the
+    key (w, kind): operands derived once from frozen weights that every step reads."""
+    key = (id(w), kind)
+    hit = _FROZEN.get(key)
+    if hit is not None:
+        ref, ptr, version, derived = hit
+        if ref() is w and ptr == w.data_ptr() and version == w._version:
+            return derived
+    for k in [k for k, v in _FROZEN.items() if v[0]() is None]:
+        del _FROZEN[k]
+    derived = make(w)
+    _FROZEN[key] = (weakref.ref(w), w.data_ptr(), w._version, derived)
+    return derived
 
 
 def transposed_frozen(w: torch.Tensor) -> torch.Tensor:
-    """w.T, contiguous, kept while `w` is alive and unmodified (same storage, same version).
-    For frozen weights read every step in the other orientation (the lm_head in dz @ W):
-    the transpose is paid once, not per call."""
-    key = id(w)
-    hit = _T_CACHE.get(key)
-    if hit is not None:
-        ref, ptr, version, wt = hit
-        if ref() is w and ptr == w.data_ptr() and version == w._version:
-            return wt
-    for k in [k for k, v in _T_CACHE.items() if v[0]() is None]:
-        del _T_CACHE[k]
-    wt = transpose16(w)
-    _T_CACHE[key] = (weakref.ref(w), w.data_ptr(), w._version, wt)
-    return wt
+    """w.T, contiguous, kept while `w` is alive and unmodified. For frozen weights read every
+    step in the other orientation (the lm_head in dz @ W): the transpose is paid once, not per
+    call."""
+    return _frozen(w, "T", transpose16)
+
+
+def frozen_as(w: torch.Tensor, dtype) -> torch.Tensor:
+    """w in `dtype`, contiguous: `w` itself when it already is, else a copy kept while `w` is
+    alive, unmodified and frozen (a weight that requires grad is cast on every call)."""
+    if w.dtype == dtype and w.is_contiguous():
+        return w
+    if w.requires_grad:
+        return w.detach().to(dtype).contiguous()
+    return _frozen(w, dtype, lambda t: t.to(dtype).contiguous())
 
 
 def gemm_nt_cat(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None,

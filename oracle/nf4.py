@@ -111,3 +111,34 @@ def dequant_numpy(packed, n_weights, table, *, absmax, nested, code2, absmax2, o
     else:
         s = absmax[b].astype(np.float32)
     return (table[nib].astype(np.float32) * s).astype(np.float32)
+
+
+def dequant_torch(packed, state, table, out_dtype=None):
+    """Torch restatement on the CPU, vectorised over every weight (runs on all of torch's
+    intra-op threads): the reference's dequant (solution/nf4.py:26-49) with the same fp32
+    operation order as the C oracle: s = code2[q] * absmax2[b // bs2], s = s + offset,
+    w = nf4[c] * s, each rounded to fp32, then one RNE conversion to `out_dtype` (bf16 by
+    default). Used as the CPU baseline of the dequant; pinned bit-exact to the C oracle."""
+    import torch
+
+    st = unpack_state(state)
+    p = torch.as_tensor(packed).reshape(-1).to(torch.uint8)
+    n = int(np.prod(tuple(state.shape)))
+    nib = torch.stack(((p >> 4) & 15, p & 15), dim=1).reshape(-1)[:n].long()
+    bs = st["blocksize"]
+    nb = -(-n // bs)
+    if st["nested"]:
+        q = torch.from_numpy(st["absmax"]).long()
+        code2 = torch.from_numpy(st["code2"])
+        a2 = torch.from_numpy(st["absmax2"])
+        s = code2[q] * a2[torch.arange(nb) // st["blocksize2"]]
+        s = s + torch.tensor(st["offset"], dtype=torch.float32)
+    else:
+        s = torch.from_numpy(st["absmax"]).float()
+    tab = torch.as_tensor(np.asarray(table, np.float32))
+    w = tab[nib]
+    full = (n // bs) * bs
+    head = (w[:full].view(-1, bs) * s[: n // bs, None]).reshape(-1)
+    if full < n:
+        head = torch.cat([head, w[full:] * s[-1]])
+    return head.to(out_dtype or torch.bfloat16)

@@ -92,8 +92,16 @@ def dropout_scale(x: torch.Tensor, p: float, seed: int, scale: float, out_dtype)
 
 
 def scaled_add(base, lo, scaling):
+    """out = base + lo * s computed in fp32 with one rounding (the fused multiply-add of
+    solution/lora.py:57-59, where s reaches the kernel as an fp32 argument), then cast to
+    promote(base, lo) (solution/lora.py:99-100). Evaluated in fp64: the product of an fp32 (or
+    16-bit) lo and an fp32 s is exact there, and rounding the fp64 sum to fp32 equals the single
+    rounding of the exact sum unless that sum needs more than 53 bits and its fp64 rounding
+    lands on an fp32 halfway point (never the case in the tests, which use operands within 29
+    binades of each other)."""
+    s = float(np.float32(scaling))
     out_dtype = torch.promote_types(base.dtype, lo.dtype)
-    return (base.double() + lo.double() * scaling).to(out_dtype)
+    return (base.double() + lo.double() * s).float().to(out_dtype)
 
 
 # ---- CE rows (solution/fused_ce.py:42-96, solution/cross_entropy.py:48-90) -------------------

@@ -143,28 +143,53 @@ def test_fused_head_loss_vs_forcausallmloss():
 
 
 def test_fused_ce_full_qwen25_shape_rows_vs_oracle():
-    """8192 tokens x 1536 hidden x 151936 vocab in bf16 with 10% ignored labels: the loss is
-    the mean of the per-token losses, and a random subset of rows matches the fp64 oracle."""
+    """8192 tokens x 1536 hidden x 151936 vocab in bf16 with 10% ignored labels, every row
+    against the fp64 oracle: logits from an fp32-accumulated product rounded to bf16, then the
+    oracle's row math in fp64 (both on the device, 512 rows at a time). Per-row loss and
+    entropy within 1e-4 (plus one bf16 ulp of a logit: the GEMMs sum in different orders, so a
+    logit on a rounding boundary may round the other way); the total loss within 1e-4 of the
+    oracle's; argmax exact except where the oracle's two largest logits are within one bf16
+    ulp; the hidden gradient within bf16 tolerance."""
     print("fused CE 8192x1536x151936", flush=True)
     g = torch.Generator().manual_seed(0)
     n, H, V = 8192, 1536, 151936
-    hidden = torch.randn(n, H, generator=g).to(torch.bfloat16)
-    weight = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16)
+    hidden = torch.randn(n, H, generator=g).to(torch.bfloat16).cuda()
+    weight = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16).cuda()
     target = torch.randint(0, V, (n,), generator=g)
     target[torch.rand(n, generator=g) < 0.1] = -100
-    hg = hidden.cuda().requires_grad_()
+    target = target.cuda()
+    hg = hidden.clone().requires_grad_()
     denom = (target != -100).sum()
     loss, tok, ent, pred = cross_entropy.FusedLinearCrossEntropy.apply(
-        hg, weight.cuda(), target.cuda(), denom.cuda(), torch.bfloat16, 512)
+        hg, weight, target, denom, torch.bfloat16, 512)
     loss.backward()
-    torch.testing.assert_close(loss.cpu(), tok.cpu().sum() / denom, rtol=1e-6, atol=0)
-    rows = torch.randperm(n, generator=g)[:48]
-    logits = (hidden[rows].float() @ weight.float().t()).to(torch.bfloat16)
-    l_r, e_r, am_r, _, dz_r = ops.ce_rows(logits, target[rows], 1, grad_scale=1.0)
-    torch.testing.assert_close(tok.cpu()[rows].double(), l_r, rtol=1e-4, atol=2e-4)
-    torch.testing.assert_close(ent.cpu()[rows].double(), e_r, rtol=1e-4, atol=2e-4)
-    agree = (pred.cpu()[rows] == am_r).float().mean().item()
-    assert agree >= 0.95  # argmax ties/near-ties of bf16 logits may resolve differently
-    grad_r = (dz_r / float(denom)).to(torch.float64) @ weight.double()
-    scale = grad_r.abs().max().item()
-    torch.testing.assert_close(hg.grad.cpu()[rows].double(), grad_r, rtol=2e-2, atol=2e-2 * scale)
+    w32, w64 = weight.float(), weight.double()
+    total_r = 0.0
+    ulp_ties = boundary_rows = 0
+    for a in range(0, n, 512):
+        b = a + 512
+        logits = (hidden[a:b].float() @ w32.t()).to(torch.bfloat16)
+        l_r, e_r, am_r, _, dz_r = ops.ce_rows(logits, target[a:b], 1, grad_scale=1.0)
+        total_r += float(l_r.sum())
+        z = logits.double()
+        zmax = z.max(dim=-1).values  # one bf16 ulp at the row's largest logit bounds the others'
+        ulp = torch.ldexp(torch.ones_like(zmax), torch.frexp(zmax).exponent - 8)
+        for got_, want_ in ((tok[a:b].double(), l_r), (ent[a:b].double(), e_r)):
+            err = (got_ - want_).abs()
+            strict = err <= 1e-4 * want_.abs() + 1e-4
+            assert torch.all(err <= 1e-4 * want_.abs() + 1e-4 + ulp), "beyond one logit ulp"
+            boundary_rows += int((~strict).sum())
+        differ = pred[a:b] != am_r
+        if differ.any():
+            zi = z[differ]
+            got = zi.gather(1, pred[a:b][differ][:, None]).squeeze(1)
+            best = zi.gather(1, am_r[differ][:, None]).squeeze(1)
+            assert torch.all(best - got <= ulp[differ]), "argmax differs beyond a rounding tie"
+            ulp_ties += int(differ.sum())
+        grad_r = (dz_r / float(denom)) @ w64
+        scale = grad_r.abs().max().item()
+        torch.testing.assert_close(hg.grad[a:b].double(), grad_r, rtol=2e-2, atol=2e-2 * scale)
+    print(f"argmax differences at one-ulp ties: {ulp_ties} of {n}; loss/entropy values past "
+          f"1e-4 (within one logit ulp): {boundary_rows}", flush=True)
+    assert abs(float(loss) - total_r / float(denom)) <= 1e-4 * abs(total_r / float(denom))
+    assert ulp_ties <= n // 100 and boundary_rows <= n // 100

@@ -66,6 +66,46 @@ def test_patched_step_matches_fp32_reference(shape):
         assert err_p <= 1.25 * err_e + 1e-3, (err_p, err_e)
 
 
+def _rel(a, b):
+    return abs(a - b) / abs(b)
+
+
+def test_full_depth_step_matches_fp32_reference():
+    """The Qwen2.5-7B-shaped step at its full depth (28 layers, 2 x 2048 tokens, vocab 152064):
+    the same bar as above against an fp32 copy of the same quantised model. Prints the
+    fp32-relative loss error of both bf16 paths and the worst adapter-gradient errors."""
+    print("qlora step qwen25_7b 28 layers, 2x2048 tokens", flush=True)
+    cfg = qlora_step.qwen2_config()
+    model = qlora_step.build_qlora_model(cfg, "cuda", seed=0)
+    ids, labels = qlora_step.make_batch(2, 2048, cfg.vocab_size)
+    m32 = _fp32_copy(model)
+    with qlora_step.eager_mode(m32):
+        loss_32 = qlora_step.QLoRAStep(m32, fused_head=False).forward_backward(ids, labels).item()
+    g_32 = _grads(m32)
+    del m32
+    torch.cuda.empty_cache()
+    with qlora_step.eager_mode(model):
+        loss_e = qlora_step.QLoRAStep(model, fused_head=False).forward_backward(ids, labels).item()
+    g_e = _grads(model)
+    model.zero_grad(set_to_none=True)
+    qlora_step.patched_mode()
+    loss_p = qlora_step.QLoRAStep(model, fused_head=True).forward_backward(ids, labels).item()
+    g_p = _grads(model)
+    errs = []
+    for a, b, c in zip(g_p, g_e, g_32):
+        errs.append((((a - c).norm() / c.norm()).item(), ((b - c).norm() / c.norm()).item()))
+    worst = max(errs, key=lambda e: e[0] - 1.25 * e[1])
+    print(f"loss fp32 {loss_32:.7f} patched {loss_p:.7f} (rel {_rel(loss_p, loss_32):.2e}) "
+          f"eager bf16 {loss_e:.7f} (rel {_rel(loss_e, loss_32):.2e}); adapter grads: "
+          f"{len(errs)} tensors, median err patched "
+          f"{sorted(e[0] for e in errs)[len(errs) // 2]:.3e} eager "
+          f"{sorted(e[1] for e in errs)[len(errs) // 2]:.3e}, worst patched {worst[0]:.3e} "
+          f"(eager {worst[1]:.3e})", flush=True)
+    assert _rel(loss_p, loss_32) <= 1e-4, (loss_p, loss_32)
+    for err_p, err_e in errs:
+        assert err_p <= 1.25 * err_e + 1e-3, (err_p, err_e)
+
+
 def test_adamw_step_updates_only_adapters():
     cfg = qlora_step.qwen2_config(hidden_size=256, intermediate_size=512, num_hidden_layers=1,
                                   num_attention_heads=4, num_key_value_heads=2, vocab_size=1000)

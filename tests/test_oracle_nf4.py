@@ -151,3 +151,15 @@ def test_dequant_error_is_bounded_by_half_the_code_gap():
     half_gap = np.max(np.diff(TABLE)) / 2
     absmax = w.reshape(-1, 64).abs().amax(1).repeat_interleave(64).reshape(64, 256).numpy()
     assert np.all(np.abs(deq - w.numpy()) <= absmax * half_gap * (1 + 1e-5))
+
+
+@pytest.mark.parametrize("shape,nested", [((4864, 896), True), ((7, 50), True), ((96, 320), False)])
+def test_torch_restatement_matches_the_c_oracle(shape, nested):
+    """The vectorised torch dequant (the CPU baseline) equals the C oracle bit for bit, on the
+    Qwen2.5-0.5B gate_proj weight and on a ragged shape whose last block is partial."""
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(shape, generator=g) * 0.02
+    packed, st = quant.quantize_nf4(w, 64, compress_statistics=nested)
+    want = onf4.dequant_state(packed, st, TABLE, out="bf16")
+    got = onf4.dequant_torch(packed, st, TABLE)
+    np.testing.assert_array_equal(got.view(torch.int16).numpy().view(np.uint16), want)

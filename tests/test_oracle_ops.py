@@ -162,3 +162,82 @@ def test_fused_linear_ce_oracle_is_forcausallmloss():
     assert int(lab) == int(items)
     # the per-token losses sum to the total
     torch.testing.assert_close(tok.sum() / items, want)
+
+
+# ---- scaled add: pinned against exact rational arithmetic ------------------------------------
+def _round_f32(x):
+    """The fp32 value nearest the rational x, ties to even (IEEE 754 round-to-nearest), from
+    the definition: 24 significand bits for normal numbers, a quantum of 2^-149 below."""
+    from fractions import Fraction
+
+    if x == 0:
+        return 0.0
+    sign, x = (-1.0 if x < 0 else 1.0), abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    q = max(e - 23, -149)
+    scaled = x / Fraction(2) ** q
+    n = scaled.numerator // scaled.denominator
+    rem = scaled - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * n * 2.0 ** q
+
+
+def _exact_scaled_add(base, lo, scaling, out_dtype):
+    """base + lo * fp32(scaling) evaluated exactly, rounded once to fp32, then cast."""
+    from fractions import Fraction
+
+    s = Fraction(float(np.float32(scaling)))
+    vals = [_round_f32(Fraction(float(b)) + Fraction(float(v)) * s)
+            for b, v in zip(base.reshape(-1).tolist(), lo.reshape(-1).tolist())]
+    return torch.tensor(vals, dtype=torch.float32).view(base.shape).to(out_dtype)
+
+
+@pytest.mark.parametrize("base_dtype,lo_dtype", [(torch.float32, torch.float16),
+                                                 (torch.float32, torch.bfloat16),
+                                                 (torch.bfloat16, torch.bfloat16),
+                                                 (torch.float16, torch.float32),
+                                                 (torch.float32, torch.float32)])
+@pytest.mark.parametrize("scaling", [2.0, 0.5, 3.0, 0.3])
+def test_scaled_add_is_one_fp32_rounding_then_the_promoted_cast(base_dtype, lo_dtype, scaling):
+    g = torch.Generator().manual_seed(7)
+    base = torch.randn(3, 67, generator=g).to(base_dtype)
+    lo = (torch.randn(3, 67, generator=g) * 4).to(lo_dtype)
+    out_dtype = torch.promote_types(base_dtype, lo_dtype)
+    got = ops.scaled_add(base, lo, scaling)
+    assert got.dtype == out_dtype
+    assert torch.equal(got, _exact_scaled_add(base, lo, scaling, out_dtype))
+
+
+def test_scaled_add_crafted_cases():
+    f32 = torch.float32
+    # one rounding, not two: (1 + 2^-12)^2 - (1 + 2^-11) = 2^-24 exactly; rounding the product
+    # to fp32 first (a tie, to even) would give 0
+    a = torch.tensor([1 + 2.0 ** -12], dtype=f32)
+    got = ops.scaled_add(torch.tensor([-(1 + 2.0 ** -11)], dtype=f32), a, 1 + 2.0 ** -12)
+    assert got.item() == 2.0 ** -24
+    # fp32 arithmetic for 16-bit lo: 65504 * 2 overflows fp16 but not fp32
+    got = ops.scaled_add(torch.tensor([0.5], dtype=f32), torch.tensor([65504.0]).half(), 2.0)
+    assert got.dtype == f32 and got.item() == 131008.5
+    # the scaling multiplies lo only: s = 0 returns base, and base is never scaled
+    base = torch.tensor([1.5, -2.25, 3.0], dtype=f32)
+    lo = torch.tensor([7.0, 9.0, -1.0]).half()
+    assert torch.equal(ops.scaled_add(base, lo, 0.0), base)
+    assert ops.scaled_add(base, lo, 2.0).tolist() == [15.5, 15.75, 1.0]
+    # s reaches the kernel as fp32: 0.3 is 0.30000001192..., visible in an fp32 result
+    got = ops.scaled_add(torch.tensor([0.0], dtype=f32), torch.tensor([2.0 ** 20], dtype=f32), 0.3)
+    assert got.item() == float(np.float32(0.3)) * 2.0 ** 20
+    # a 16-bit output is rounded from the fp32 result, not from the exact sum: 1 + 2^-8 + 2^-30
+    # rounds to fp32 1 + 2^-8, a bf16 halfway point that ties to even (1.0), while rounding the
+    # exact sum straight to bf16 would give 1 + 2^-7
+    bf = torch.bfloat16
+    got = ops.scaled_add(torch.tensor([1.0], dtype=bf), torch.tensor([2.0 ** -8], dtype=bf),
+                         1 + 2.0 ** -22)
+    assert got.dtype == bf and got.item() == 1.0
+    # the exact reference agrees on every case above
+    for b, v, s, dt in (([-(1 + 2.0 ** -11)], [1 + 2.0 ** -12], 1 + 2.0 ** -12, f32),
+                        ([0.5], [3.0], 2.0, f32), ([1.0], [2.0 ** -8], 1 + 2.0 ** -22, bf)):
+        bt, vt = torch.tensor(b, dtype=dt), torch.tensor(v, dtype=dt)
+        assert torch.equal(ops.scaled_add(bt, vt, s), _exact_scaled_add(bt, vt, s, dt))
