@@ -279,6 +279,9 @@ def _rotated_sets(bytes_per_set, minimum=5):
 
 
 def _rate(name, t, nbytes, res):
+    if nbytes / t / 1e9 > 1.25 * HBM_PEAK_GBS:  # every set exceeds the MALL: HBM bounds the rate
+        raise RuntimeError(f"{name}: {nbytes / t / 1e9:.0f} GB/s is above the HBM peak; the timed "
+                           f"region did not run the kernels")
     res[name] = dict(us=round(t * 1e6, 2), gbs=round(nbytes / t / 1e9, 1),
                      frac_hbm=round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3), bytes=nbytes)
 
@@ -300,17 +303,15 @@ def bench_rmsnorm(torch, res, replays=4):
         dy = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
         bufs.append((x, dy, torch.empty_like(x), torch.empty(M, device="cuda"),
                      torch.empty_like(x)))
-    s = _lib.stream_of(w)
-
-    def fwd(b):
+    def fwd(b):  # the stream is looked up at launch: inside graph capture it is the capture's
         x, _, y, rstd, _ = b
         _lib.call("qlora_rmsnorm_fwd", x.data_ptr(), 2, N, w.data_ptr(), 2, y.data_ptr(), 2, N,
-                  rstd.data_ptr(), M, N, 1e-6, s)
+                  rstd.data_ptr(), M, N, 1e-6, _lib.stream_of(x))
 
     def bwd(b):
         x, dy, _, rstd, dx = b
         _lib.call("qlora_rmsnorm_bwd", dy.data_ptr(), 2, N, x.data_ptr(), 2, N, w.data_ptr(), 2,
-                  rstd.data_ptr(), dx.data_ptr(), 2, N, M, N, s)
+                  rstd.data_ptr(), dx.data_ptr(), 2, N, M, N, _lib.stream_of(x))
     for b in bufs:
         fwd(b)
     calls = 4 * sets
@@ -364,14 +365,16 @@ def bench_swiglu(torch, res):
     o = torch.empty_like(gt)
     gr = torch.randn(n, device="cuda", generator=g).to(torch.bfloat16)
     dg, du = torch.empty_like(gt), torch.empty_like(gt)
-    s = _lib.stream_of(gt)
+
+    def s():  # looked up at launch: inside graph capture it is the capture's stream
+        return _lib.stream_of(gt)
     for name, fn, nbytes in (
             ("swiglu_fwd_4096x18944", lambda: _lib.call("qlora_swiglu_fwd", gt.data_ptr(),
-                                                       up.data_ptr(), o.data_ptr(), 2, n, s),
+                                                       up.data_ptr(), o.data_ptr(), 2, n, s()),
              3 * 2 * n),
             ("swiglu_bwd_4096x18944", lambda: _lib.call("qlora_swiglu_bwd", gr.data_ptr(),
                                                        gt.data_ptr(), up.data_ptr(), dg.data_ptr(),
-                                                       du.data_ptr(), 2, n, s), 5 * 2 * n)):
+                                                       du.data_ptr(), 2, n, s()), 5 * 2 * n)):
         _rate(name, _graph_time([fn] * 10, torch), nbytes, res)
 
 
@@ -647,7 +650,8 @@ def profile_summary(trace_csv, fetch_csv=None, write_csv=None, copy_mib=256):
 
     durs = collections.defaultdict(list)
     for r in csv.DictReader(open(trace_csv)):
-        durs[key(r["Kernel_Name"], r["Grid_Size_X"])].append(
+        grid = int(r["Grid_Size_X"]) * int(r.get("Grid_Size_Y") or 1) * int(r.get("Grid_Size_Z") or 1)
+        durs[key(r["Kernel_Name"], grid)].append(
             (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
 
     def counters(path, counter):
