@@ -66,6 +66,8 @@ _SIGNATURES = {
                         _c_i64, _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
                          _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_wgrad_noalloc": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                 _c_ptr, _c_int, _c_f32, _c_ptr],
     "qlora_lora_pack": [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_f32, _c_int, _c_ptr, _c_ptr, _c_ptr,
                         _c_ptr, _c_int, _c_ptr],
     "qlora_lora_pack_group": [_c_ptr, _c_int, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,

@@ -39,6 +39,8 @@
 //
 // Both kernels optionally split their reduction over blockIdx.y into an fp32 workspace,
 // summed in split order by the matching reduce kernel (deterministic).
+#include <mutex>
+
 #include "ql_swiglu.h"
 #include "ql_vec.h"
 #include "lora_mfma.h"
@@ -1122,6 +1124,67 @@ extern "C" int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int
   return ql_lora_wgrad(in_dtype, PT, ldpt, Q, ldq, M, N, slots, out, out_transposed, alpha,
                        static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
                        static_cast<hipStream_t>(stream));
+}
+
+// ---- qlora_lora_wgrad without a caller workspace -------------------------------------------
+// The split partials live in a file-scope device array instead: each GPU the library runs on
+// holds its own kWgradScratchBytes copy until the process ends. On the host the array's name
+// is a stand-in, not a device address, so host code never passes it to a kernel: it uses the
+// address hipGetSymbolAddress returns, looked up once per device with that device current and
+// kept per device. Every call on a GPU reuses that GPU's array; each split writes its whole
+// partial before the reduce reads it, so nothing needs clearing, and calls that overlap on one
+// GPU (two streams, two threads) race on it.
+constexpr int64_t kWgradScratchBytes = int64_t(16) << 20;
+static __device__ __align__(256) float lora_wgrad_scratch[kWgradScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices];  // device address of lora_wgrad_scratch per device, or null
+
+// The device the launch goes to: the stream's, or the current one for the null stream.
+int wgrad_scratch_of(hipStream_t stream, float** out) {
+  int dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return QL_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return (int)e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    void* p = nullptr;
+    const hipError_t got = hipGetSymbolAddress(&p, HIP_SYMBOL(lora_wgrad_scratch));
+    if (cur != dev && (e = hipSetDevice(cur)) != hipSuccess) return (int)e;
+    if (got != hipSuccess) return (int)got;
+    if (!p || !ql_aligned(p, 256)) return QL_EALIGN;
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return QL_OK;
+}
+
+}  // namespace
+
+extern "C" int qlora_lora_wgrad_noalloc(const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
+                                        int64_t M, int64_t N, int slots, int in_dtype, float* out,
+                                        int out_transposed, float alpha, ql_stream_t stream) {
+  if (M < 0 || N < 0 || slots < 1 || slots > kMaxSlots) return QL_EINVAL;
+  if (N == 0) return QL_OK;
+  if (!PT || !Q || !out) return QL_EINVAL;
+  const int64_t need = M > 0 ? ql_lora_wgrad_workspace_floats(M, N, slots) * (int64_t)sizeof(float)
+                             : 0;
+  if (need > kWgradScratchBytes) return QL_ESHAPE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (need == 0)  // unsplit (or empty) reductions use no scratch: the workspace entry point as is
+    return qlora_lora_wgrad(PT, ldpt, Q, ldq, M, N, slots, in_dtype, out, out_transposed, alpha,
+                            nullptr, 0, stream);
+  float* ws = nullptr;
+  const int st = wgrad_scratch_of(s, &ws);
+  if (st != QL_OK) return st;
+  return qlora_lora_wgrad(PT, ldpt, Q, ldq, M, N, slots, in_dtype, out, out_transposed, alpha, ws,
+                          need, stream);
 }
 
 extern "C" int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float scaling,

@@ -334,6 +334,21 @@ int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, i
                      void* workspace, int64_t workspace_bytes, ql_stream_t stream);
 
 /*
+ * qlora_lora_wgrad without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving or training loops, C hosts without an
+ * allocator). No counterpart in the reference. Same arguments, results and rules as
+ * qlora_lora_wgrad, bit for bit: the split partials go to a 16 MiB array inside the library,
+ * one per GPU, held until the process ends. A call whose split partials need more than
+ * 16 MiB (qlora_lora_wgrad_workspace_size > 16 MiB: e.g. 4 slots, N > 16384, M >= 4096) returns
+ * QL_ESHAPE and launches nothing. All calls on one GPU share its array: calls that overlap on
+ * that GPU (different streams or threads) race and must be ordered by the caller. The call
+ * allocates nothing (no hipMalloc, no library allocation).
+ */
+int qlora_lora_wgrad_noalloc(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M,
+                             int64_t N, int slots, int in_dtype, float* out, int out_transposed,
+                             float alpha, ql_stream_t stream);
+
+/*
  * SwiGLU backward fused with the gate and up adapters' down-projections of its gradients
  * (a LoRA MLP whose gate/up outputs are the two halves gate, up [rows, cols]):
  *   dgate, dup = exactly as qlora_swiglu_bwd_rows (stored, row-strided)

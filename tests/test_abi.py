@@ -142,3 +142,20 @@ def test_empty_problems_are_no_ops(lib):
     assert lib.qlora_swiglu_fwd(None, None, None, 2, 0, None) == 0
     assert lib.qlora_gemm(0, 0, 0, 4, 8, None, 8, None, 8, 2, None, 4, 2, None, 1.0, 0.0,
                           None) == 0
+
+
+def test_noalloc_wgrad_rejects_scratch_beyond_its_array(lib):
+    """qlora_lora_wgrad_noalloc returns QL_ESHAPE, launching nothing, when the split partials
+    would need more than its 16 MiB array (4 slots, N = 16392, M = 4096: 4 splits x 16392 x 64
+    fp32 = 16.8 MB); bad arguments are rejected as by qlora_lora_wgrad."""
+    P = ctypes.c_void_p
+    fake = P(0x1000)  # never dereferenced: every call below is rejected before any launch
+    assert lib.qlora_lora_wgrad_workspace_size(4096, 16392, 4) > 16 << 20
+    assert lib.qlora_lora_wgrad_noalloc(fake, 4096, fake, 16392, 4096, 16392, 4, 2, fake, 0,
+                                        1.0, None) == -4
+    assert lib.qlora_lora_wgrad_noalloc(fake, 4096, fake, 16392, 4096, 16392, 5, 2, fake, 0,
+                                        1.0, None) == -1  # slots > 4
+    assert lib.qlora_lora_wgrad_noalloc(None, 4096, fake, 512, 4096, 512, 1, 2, fake, 0,
+                                        1.0, None) == -1  # null operand
+    assert lib.qlora_lora_wgrad_noalloc(fake, 4096, fake, 512, -1, 512, 1, 2, fake, 0,
+                                        1.0, None) == -1  # negative size
