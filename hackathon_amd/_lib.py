@@ -180,6 +180,21 @@ def require_device(*tensors: torch.Tensor) -> None:
             raise ValueError("HIP kernels need tensors on a GPU device")
 
 
+def require_rows(dtype: torch.dtype, **tensors: torch.Tensor | None) -> None:
+    """Each named tensor (None skips it) is a 2-D matrix on a GPU, of `dtype`, with unit stride
+    along its rows: what the C-ABI's single dtype tag and row-stride arguments describe. Raises
+    TypeError (dtype) or ValueError (device, layout) naming the tensor."""
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a GPU device")
+        if t.dtype != dtype:
+            raise TypeError(f"{name} is {t.dtype}; this call takes {dtype} operands")
+        if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+            raise ValueError(f"{name} must be a 2-D matrix with unit stride along its rows")
+
+
 def i64_array(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
 

@@ -858,12 +858,13 @@ int ql_lora_down(int in_dtype, int out_dtype, const void* X, int64_t ldx, const 
   if (M <= 0 || K <= 0 || K % 32 || out_cols < nc || ldo < out_cols) return QL_EINVAL;
   if (out_t && ldt < M) return QL_EINVAL;
   if (ldx % 8 || ldy % 8 || !ql_aligned(X, 16) || !ql_aligned(Y, 16)) return QL_EALIGN;
-  // per-lane byte offsets within 16 rows of X and within Y are 32-bit
-  if (ldx < K || ldy < K || 32 * ldx >= (int64_t(1) << 31) || 2 * nc * ldy >= (int64_t(1) << 31))
+  // per-lane byte offsets within a workgroup's 16 * rows rows of X and within Y are 32-bit
+  const int rows = lora_down_rows(M, K, slots);
+  if (ldx < K || ldy < K || 32 * rows * ldx >= (int64_t(1) << 31) ||
+      2 * nc * ldy >= (int64_t(1) << 31))
     return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   if (out_dtype != QL_BF16 && out_dtype != QL_F16 && out_dtype != QL_F32) return QL_EDTYPE;
-  const int rows = lora_down_rows(M, K, slots);
   int splits = ql_lora_down_splits(M, K, slots);
   if (ws_floats < (int64_t)splits * M * nc || !ws) splits = 1;
   // per-split K range: a multiple of 128 k per wave
@@ -1071,6 +1072,14 @@ extern "C" int qlora_swiglu_bwd_lora_down(
   if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (rows == 0) return QL_OK;
   if (!grad || !gate || !up || !dgate || !dup || !bt_gate || !bt_up || !du) return QL_EINVAL;
+  // lanes past the last row or group recompute the last one and re-read its inputs after
+  // other lanes stored: outputs that overlap the inputs would be read back modified
+  const void* ins[3] = {grad, gate, up};
+  const int64_t in_ld[3] = {ldgr, ldg, ldu};
+  for (int i = 0; i < 3; ++i)
+    if (ql_spans_overlap(dgate, lddg, ins[i], in_ld[i], rows, cols, 2) ||
+        ql_spans_overlap(dup, lddu, ins[i], in_ld[i], rows, cols, 2))
+      return QL_EINVAL;
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
   if (!ql_aligned(du, 2) || (du_t && !ql_aligned(du_t, 2))) return QL_EALIGN;
   return ql_swiglu_bwd_down(dtype, grad, ldgr, gate, ldg, up, ldu, dgate, lddg, dup, lddu, rows,

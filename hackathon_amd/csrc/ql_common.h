@@ -94,6 +94,18 @@ static inline int ql_hip_status(hipError_t e) { return e == hipSuccess ? QL_OK :
 
 static inline bool ql_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Whether the byte ranges spanned by two row-strided matrices of `rows` x `cols` elements of
+// `elem` bytes (leading dimensions lda, ldb) intersect. Conservative for interleaved strided
+// matrices: it compares the spans, not the elements.
+static inline bool ql_spans_overlap(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                    int64_t rows, int64_t cols, int64_t elem) {
+  if (rows <= 0 || cols <= 0) return false;
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  const uintptr_t a1 = a0 + (uintptr_t)(((rows - 1) * lda + cols) * elem);
+  const uintptr_t b1 = b0 + (uintptr_t)(((rows - 1) * ldb + cols) * elem);
+  return a0 < b1 && b0 < a1;
+}
+
 static inline int ql_launch_status() { return ql_hip_status(hipGetLastError()); }
 
 #define QL_DISPATCH_DTYPE(dt, DTC, ...)                  \

@@ -167,6 +167,8 @@ def lora_down(x: torch.Tensor, y: torch.Tensor, out: torch.Tensor, alpha: float 
     """out[:, :16G] = alpha * x @ y^T (y [16G, K]: G <= 4 rank-16 adapters that read x) and
     out[:, 16G:] = 0 (qlora_lora_down, x read once); with `out_t` ([16G, >= M], x's dtype)
     also the 16G columns transposed, the operand lora_wgrad takes."""
+    _lib.require_rows(x.dtype, x=x, y=y, out_t=out_t)
+    _lib.require_rows(out.dtype, out=out)
     M, K = x.shape
     slots = _slots(y.shape[0], "y")
     ws, ws_bytes = _lib.workspace("qlora_lora_down_workspace_size", M, K, slots, device=x.device)
@@ -188,6 +190,7 @@ def lora_wgrad(pt: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
     """fp32 alpha * q^T @ pt^T for q [M, N] and pt [16G, M] (token-contiguous, as lora_down's
     `out_t`; G <= 4 adapters whose gradients reduce over the same q, q read once)
     (qlora_lora_wgrad): [N, 16G], or [16G, N] when `transposed`."""
+    _lib.require_rows(q.dtype, q=q, pt=pt)
     M, N = q.shape
     slots = _slots(pt.shape[0], "pt")
     nc = 16 * slots

@@ -68,6 +68,8 @@ def swiglu_bwd_lora_down(grad, gate, up, dgate, dup, bt_gate, bt_up, alpha_gate,
     gate and up adapters' down-projections of them: du[:, :16] = alpha_gate dgate bt_gate^T,
     du[:, 16:32] = alpha_up dup bt_up^T, du[:, 32:] = 0, du_t = du[:, :32]^T when given
     (qlora_swiglu_bwd_lora_down)."""
+    _lib.require_rows(gate.dtype, grad=grad, gate=gate, up=up, dgate=dgate, dup=dup,
+                      bt_gate=bt_gate, bt_up=bt_up, du=du, du_t=du_t)
     rows, cols = gate.shape
     if bt_up.stride(0) != bt_gate.stride(0):
         raise ValueError("bt_gate and bt_up must share a row stride (slices of one B^T buffer)")

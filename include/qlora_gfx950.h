@@ -307,7 +307,8 @@ int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
  * (Y = B^T [16, out]). When out_t is not NULL the 16 G columns are also written transposed,
  * out_t[c * ldt + m] (ldt >= M, in_dtype): the token-contiguous operand qlora_lora_wgrad
  * takes. K % 32 == 0; X, Y 16-B aligned with ldx, ldy multiples of 8, ldx, ldy >= K,
- * 32 * ldx < 2^31 and 32 * G * ldy < 2^31; in_dtype QL_BF16/QL_F16; out_dtype
+ * 32 * ldx < 2^31 (128 * ldx < 2^31 when G = 1, K >= 8192 and M >= 1024: those calls stream
+ * X in 64-row blocks) and 32 * G * ldy < 2^31, else QL_EINVAL; in_dtype QL_BF16/QL_F16; out_dtype
  * QL_BF16/QL_F16/QL_F32. Streams X from HBM once for all G adapters.
  * Replaces: solution/lora.py:172 (lora_A(x)) and its autograd backward through lora_B.
  */
@@ -358,7 +359,9 @@ int qlora_lora_wgrad_noalloc(const void* PT, int64_t ldpt, const void* Q, int64_
  * bt_gate / bt_up are the adapters' B^T [16, cols] (ld ldbt). The gradients are multiplied
  * from registers, so the two down-projections do not read them back from HBM.
  * cols % 32 == 0; every matrix 16-B aligned with a leading dimension that is a multiple of 8,
- * at least cols, and below 2^24; dtype QL_BF16 or QL_F16 (du and du_t in it too).
+ * at least cols, and below 2^24; dtype QL_BF16 or QL_F16 (du and du_t in it too). Not in
+ * place: the byte ranges dgate and dup span must not meet those of grad, gate or up
+ * (QL_EINVAL otherwise).
  * Replaces: solution/swiglu.py:25-37 (the SwiGLU backward) and the lora_B autograd backward
  * of solution/lora.py:172 for the gate and up projections.
  */

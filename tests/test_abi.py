@@ -13,6 +13,19 @@ from hackathon_amd import _lib
 ROOT = Path(__file__).resolve().parents[1]
 
 
+def _no_device():
+    """The fake-pointer calls below are only safe where no GPU is visible: a call that passed
+    its checks by mistake would launch on a bad address. (Counting devices does not initialise
+    the GPU.)"""
+    import torch
+
+    return torch.cuda.device_count() == 0
+
+
+needs_no_device = pytest.mark.skipif(not _no_device(),
+                                     reason="fake-pointer argument checks run only without a GPU")
+
+
 @pytest.fixture(scope="session")
 def lib():
     if not _lib.LIB_PATH.exists():
@@ -53,6 +66,7 @@ def test_version_and_error_text(lib):
     assert b"dtype" in lib.qlora_strerror(-2)
 
 
+@needs_no_device
 def test_rejected_arguments_return_codes(lib):
     P = ctypes.c_void_p
     fake = P(0x1000)  # never dereferenced: every call below is rejected before any launch
@@ -105,6 +119,13 @@ def test_rejected_arguments_return_codes(lib):
                                None, 0, None) == -1
     assert lib.qlora_lora_wgrad(fake, 64, fake, 64, 64, 64, 5, 2, fake, 0, 1.0, None, 0,
                                 None) == -1
+    # lane byte offsets are 32-bit: a 64-row block (one adapter, K >= 8192, M >= 1024) spans
+    # 128 * ldx bytes, so ldx = 2^24 is refused there; 16-row blocks refuse ldx >= 2^26
+    big = 1 << 24
+    assert lib.qlora_lora_down(fake, big, fake, 8192, 1024, 8192, 1, 2, fake, 64, 64, 2, 1.0,
+                               None, 0, None, 0, None) == -1
+    assert lib.qlora_lora_down(fake, 1 << 26, fake, 64, 16, 64, 1, 2, fake, 64, 64, 2,
+                               1.0, None, 0, None, 0, None) == -1
     assert lib.qlora_lora_down_workspace_size(4096, 3584, 0) == 0
     assert lib.qlora_lora_wgrad_workspace_size(4096, 3584, 5) == 0
     # fused SwiGLU backward + down-projections: columns a multiple of 32, room for both
@@ -115,9 +136,15 @@ def test_rejected_arguments_return_codes(lib):
     assert lib.qlora_swiglu_bwd_lora_down(fake, 64, fake, 128, fake, 128, fake, 128, fake, 128, 16,
                                           64, fake, fake, 128, 1.0, 1.0, 2, fake, 64, 16, None, 0,
                                           None, 0, None) == -1
-    assert lib.qlora_swiglu_bwd_lora_down(fake, 64, fake, 128, fake, 128, fake, 128, fake, 128, 16,
+    gr, ga, up, dg, du = (P(0x10000 * (i + 1)) for i in range(5))  # disjoint fake matrices
+    assert lib.qlora_swiglu_bwd_lora_down(gr, 64, ga, 128, up, 128, dg, 128, du, 128, 16,
                                           64, fake, fake, 128, 1.0, 1.0, 0, fake, 64, 64, None, 0,
                                           None, 0, None) == -2
+    # ... and never in place: an output whose bytes meet an input's is refused before launching
+    for dgate, dup in ((ga, du), (dg, up), (dg, gr), (P(0x20000 + 64), du)):
+        assert lib.qlora_swiglu_bwd_lora_down(gr, 64, ga, 128, up, 128, dgate, 128, dup, 128,
+                                              16, 64, fake, fake, 128, 1.0, 1.0, 2, fake, 64, 64,
+                                              None, 0, None, 0, None) == -1
     # adamw: a table is required when there is work; the bias correction must be positive
     assert lib.qlora_adamw_fp32(None, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 1.0, 1e-8, None) == -1
     assert lib.qlora_adamw_fp32(fake, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 0.0, 1e-8, None) == -1
@@ -144,6 +171,7 @@ def test_empty_problems_are_no_ops(lib):
                           None) == 0
 
 
+@needs_no_device
 def test_noalloc_wgrad_rejects_scratch_beyond_its_array(lib):
     """qlora_lora_wgrad_noalloc returns QL_ESHAPE, launching nothing, when the split partials
     would need more than its 16 MiB array (4 slots, N = 16392, M = 4096: 4 splits x 16392 x 64

@@ -177,3 +177,31 @@ def test_qlora_step_harness_runs_on_cpu(eager):
     assert torch.isfinite(loss)
     assert any(not torch.equal(a, p) for a, p in zip(before, qlora_step.lora_parameters(model)))
     assert torch.equal(frozen, model.model.embed_tokens.weight)
+
+
+def test_rank16_wrappers_check_dtype_layout_and_device():
+    """The rank-16 wrappers pass one dtype tag and row strides to the C-ABI, so a mixed dtype,
+    a transposed view or a CPU tensor is refused before any call."""
+    from hackathon_amd import _lib, gemm
+
+    x = torch.zeros(64, 32, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        gemm.lora_down(x, torch.zeros(16, 32, dtype=torch.bfloat16),
+                       torch.zeros(64, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU"):
+        _lib.require_rows(torch.bfloat16, x=x)
+    # the dtype and layout rules, on stand-ins that report being on a GPU
+    for bad, err in ((torch.empty(64, 32, dtype=torch.float16), TypeError),
+                     (torch.empty(32, 64, dtype=torch.bfloat16).t(), ValueError)):
+        class Fake:  # a stand-in with the attributes require_rows reads, "on a GPU"
+            is_cuda = True
+            dtype = bad.dtype
+            shape = bad.shape
+
+            def dim(self):
+                return bad.dim()
+
+            def stride(self, i):
+                return bad.stride(i)
+        with pytest.raises(err):
+            _lib.require_rows(torch.bfloat16, y=Fake())
