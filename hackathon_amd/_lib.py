@@ -64,6 +64,9 @@ _SIGNATURES = {
                           _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
                         _c_i64, _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
+    "qlora_gemm_nf4": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_ptr,
+                       _c_ptr, _c_f32, _c_int, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr,
+                       _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
                          _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_wgrad_noalloc": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
@@ -94,6 +97,7 @@ _SIGNATURES = {
 _SIZE_QUERIES = {
     "qlora_gemm_workspace_size": [_c_int, _c_int, _c_i64, _c_i64, _c_i64],
     "qlora_gemm_nt_cat_workspace_size": [_c_i64, _c_i64, _c_i64],
+    "qlora_gemm_nf4_workspace_size": [_c_i64, _c_i64, _c_i64],
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_swiglu_bwd_lora_down_workspace_size": [_c_i64, _c_i64],

@@ -264,12 +264,260 @@ QL_DEV void mma_step_pipe(f32x16_t (&acc)[Layout<NB>::BI][Layout<NB>::BJ], Frags
     __builtin_amdgcn_sched_group_barrier(0x008, REST - DBL - (RH - 2 * DBL), 1);
 }
 
+// ---- B as packed NF4 (dequantised on the way into LDS) ----------------------------------------
+// The B operand can be an NF4 weight W [N, K] (packed two per byte, high nibble first; one
+// absmax per block of bs = 2^log2_bs >= 64 consecutive weights of a row, bs dividing K) instead
+// of a 16-bit matrix. Thread t of the workgroup owns B tile row t: per K step it loads the
+// row's 32 packed bytes and its block scale one step ahead into registers, and after the step's
+// barrier dequantises the 64 weights into that row of the LDS stage, in the swizzled layout the
+// fragment reads expect, with the dequant kernel's operation order (scale = code2[q] * absmax2,
+// then + offset, two fp32 roundings; product nf4[c] * scale rounded to fp32, then to bf16/fp16
+// by RNE): the products see exactly the 16-bit W that qlora_nf4_dequant writes.
+// The 16 products of a block are built once, then each weight is a table lookup: the table's
+// low and high bytes sit in two 16-byte planes, and v_perm_b32 selects 4 entries at a time.
+enum { kBDense = 0, kBNf4Nested = 1, kBNf4Plain = 2 };
+
+struct Nf4Operand {
+  const uint8_t* packed;  // weight (n, k) in byte (n K + k) / 2
+  const void* absmax;     // uint8 codes (nested) or fp32 absmax, one per block
+  const float* absmax2;   // nested: second-level scale per 2^log2_bs2 blocks
+  const float* code2;     // nested: 256-entry code table
+  const float* nf4;       // the 16 NF4 levels
+  float offset;
+  int log2_bs, log2_bs2;
+};
+
+// In-flight state of one thread's B row for the next K step.
+struct Nf4Row {
+  const uint8_t* row;  // packed bytes of (clamped) row n, k = 0
+  int64_t w0;          // weight index of (n, 0)
+  uint4 pk[2];         // 64 weights, k0 .. k0 + 63
+  uint32_t code;       // absmax code (nested) or the fp32 absmax bits
+  float a2;            // second-level scale (nested)
+};
+
+template <int BQ>
+QL_DEV void nf4_issue(Nf4Row& r, const Nf4Operand& op, int64_t k0) {
+  const uint4* p = reinterpret_cast<const uint4*>(r.row + (k0 >> 1));
+  r.pk[0] = p[0];
+  r.pk[1] = p[1];
+  const int64_t blk = (r.w0 + k0) >> op.log2_bs;
+  if constexpr (BQ == kBNf4Nested) {
+    r.code = static_cast<const uint8_t*>(op.absmax)[blk];
+    r.a2 = op.absmax2[blk >> op.log2_bs2];
+  } else {
+    r.code = __float_as_uint(static_cast<const float*>(op.absmax)[blk]);
+    r.a2 = 0.f;
+  }
+}
+
+// The product must reach fp32 before the 16-bit conversion (the backend would otherwise fuse
+// multiply and conversion into one v_fma_mix with a single rounding).
+QL_DEV float nf4_round32(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
+template <int IT>
+QL_DEV uint32_t nf4_pack2(float lo, float hi) {
+  if constexpr (IT == QL_BF16) return pack_bf16x2(lo, hi);
+  else return pack_f16x2(lo, hi);
+}
+
+// Byte j of the result: table entry idx.byte[j] (each 0..15) of the planes (lo and hi bytes of
+// the 16 entries, four per dword), low or high byte.
+QL_DEV uint32_t nf4_plane_lookup(const uint32_t (&pl)[4], uint32_t sel7, uint32_t pick) {
+  const uint32_t a = __builtin_amdgcn_perm(pl[1], pl[0], sel7);  // entries 0..7
+  const uint32_t b = __builtin_amdgcn_perm(pl[3], pl[2], sel7);  // entries 8..15
+  return __builtin_amdgcn_perm(b, a, pick);
+}
+
+// A block's 16 products as byte planes, and the packed words of its last 4 chunks: what the
+// second half of a row's dequantisation needs, carried from one K step to the next.
+struct Nf4Pending {
+  uint32_t lo[4], hi[4];
+  uint32_t d[4];
+};
+
+// Block scale and table planes of row state r (the dequant kernel's fp32 order).
+template <int BQ, int IT>
+QL_DEV void nf4_planes(const Nf4Row& r, const Nf4Operand& op, const float (&nf4)[16],
+                       const float* code2_lds, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+#pragma clang fp contract(off)
+  float s;
+  if constexpr (BQ == kBNf4Nested) {
+    s = code2_lds[r.code] * r.a2;
+    s = s + op.offset;
+  } else {
+    s = __uint_as_float(r.code);
+  }
+  uint32_t pair[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    pair[i] = nf4_pack2<IT>(nf4_round32(nf4[2 * i] * s), nf4_round32(nf4[2 * i + 1] * s));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    lo[j] = __builtin_amdgcn_perm(pair[2 * j + 1], pair[2 * j], 0x06040200u);
+    hi[j] = __builtin_amdgcn_perm(pair[2 * j + 1], pair[2 * j], 0x07050301u);
+  }
+}
+
+// Half h of an NF4 chunk: weights 4h .. 4h + 3 of the 8 in packed word d (byte i holds weight
+// 2i in its high nibble, 2i + 1 in its low one), as two dwords of 16-bit pairs.
+QL_DEV void nf4_half(const uint32_t (&lo)[4], const uint32_t (&hi)[4], uint32_t d, int h,
+                     uint32_t& w0, uint32_t& w1) {
+  const uint32_t even = (d >> 4) & 0x0f0f0f0fu, odd = d & 0x0f0f0f0fu;
+  const uint32_t idx = __builtin_amdgcn_perm(even, odd, h ? 0x03070206u : 0x01050004u);
+  const uint32_t sel7 = idx & 0x07070707u;
+  const uint32_t pick = ((idx >> 1) & 0x04040404u) | 0x03020100u;
+  const uint32_t l = nf4_plane_lookup(lo, sel7, pick);
+  const uint32_t u = nf4_plane_lookup(hi, sel7, pick);
+  w0 = __builtin_amdgcn_perm(u, l, 0x05010400u);
+  w1 = __builtin_amdgcn_perm(u, l, 0x07030602u);
+}
+
+// Chunks c0 .. c0 + 3 of a row (packed words d[0..3], 8 weights each) into its LDS row
+// (128 B, 16-B chunks swizzled by swz).
+QL_DEV void nf4_chunks(const uint32_t (&lo)[4], const uint32_t (&hi)[4], const uint32_t* d,
+                       int c0, char* __restrict__ lds_row, uint32_t swz) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint32_t w[4];
+    nf4_half(lo, hi, d[c], 0, w[0], w[1]);
+    nf4_half(lo, hi, d[c], 1, w[2], w[3]);
+    *reinterpret_cast<uint4*>(lds_row + 16 * ((c0 + c) ^ swz)) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Dequantise a whole row (the prologue's steps): planes, then all 8 chunks; when `pend` is
+// given, only chunks 0..3 are stored and the rest is left in it for the first K step.
+template <int BQ, int IT>
+QL_DEV void nf4_store_row(const Nf4Row& r, const Nf4Operand& op, const float (&nf4)[16],
+                          const float* code2_lds, char* __restrict__ lds_row, uint32_t swz,
+                          Nf4Pending* pend) {
+  uint32_t lo[4], hi[4];
+  nf4_planes<BQ, IT>(r, op, nf4, code2_lds, lo, hi);
+  const uint32_t d0[4] = {r.pk[0].x, r.pk[0].y, r.pk[0].z, r.pk[0].w};
+  const uint32_t d1[4] = {r.pk[1].x, r.pk[1].y, r.pk[1].z, r.pk[1].w};
+  nf4_chunks(lo, hi, d0, 0, lds_row, swz);
+  if (pend) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pend->lo[j] = lo[j];
+      pend->hi[j] = hi[j];
+      pend->d[j] = d1[j];
+    }
+  } else {
+    nf4_chunks(lo, hi, d1, 4, lds_row, swz);
+  }
+}
+
+// MFMAs 4s .. 4s + 3 of a half step (16-k block s / 4, row block s % 4, all 4 column blocks).
+template <int IT>
+QL_DEV void mma_slice(f32x16_t (&acc)[4][4], const Frags<8>& f, int s) {
+  const int kk = s >> 2, i = s & 3;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[i][j] = mfma<IT>(f.b[kk][j], f.a[kk][i], acc[i][j]);
+}
+
+// Part p (0..3) of read_frags: the A (p even) or B (p odd) fragments of 16-k block p / 2.
+QL_DEV void read_frags_part(const char* __restrict__ stage, int half, int wm, int wn, int lane,
+                            Frags<8>& f, int p) {
+  const int r = lane & 31;
+  const int kk = p >> 1;
+  const int c = ((half * 4 + kk * 2 + (lane >> 5)) ^ (((r >> 1) & 3) | ((r >> 3) & 1) << 2)) * 16;
+  if (p & 1) {
+    const char* bs = stage + kATileBytes + (wn * 4 * 32 + r) * kRowBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.b[kk][j] = *reinterpret_cast<const uint4*>(bs + j * 32 * kRowBytes + c);
+  } else {
+    const char* as = stage + (wm * 4 * 32 + r) * kRowBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.a[kk][i] = *reinterpret_cast<const uint4*>(as + i * 32 * kRowBytes + c);
+  }
+}
+
+// One K step of the NF4-B kernel: mma_step_pipe's products, fragment reads and barrier, with
+// B dequantised by the threads, cut into 8 slices of 4 MFMAs per half (scheduling fences
+// between slices keep the dequantisation's VALU work spread between the products):
+//   first half:  chunks 4..7 of step kt + 1's row (planes and words carried in `pend`), half a
+//                chunk per slice, into `nxt` (no wave reads it before this step's barrier);
+//   second half: A's DMA of step kt + 2 into `cur` (issue_a), the packed bytes and scale of
+//                step kt + 3 into `brow` (issue_b), then step kt + 2's row (landed at this
+//                step's barrier): planes, chunks 0..3 into `cur`, chunks 4..7 into `pend`;
+//                the first-half fragments of `nxt` are read a quarter per slice.
+template <int BQ, int IT, typename IssueA, typename IssueB>
+QL_DEV void mma_step_pipe_nf4(f32x16_t (&acc)[4][4], Frags<8>& f0, char* __restrict__ cur,
+                              char* __restrict__ nxt, const IssueA& issue_a, const IssueB& issue_b,
+                              Nf4Row& brow, Nf4Pending& pend, const Nf4Operand& op,
+                              const float (&nf4)[16], const float* code2_lds, int row_off,
+                              uint32_t swz, int wm, int wn, int lane) {
+  Frags<8> f1;
+  read_frags<8>(cur, 1, wm, wn, lane, f1);
+  uint32_t w[4];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int c = s >> 1, h = s & 1;
+    nf4_half(pend.lo, pend.hi, pend.d[c], h, w[2 * h], w[2 * h + 1]);
+    if (h)
+      *reinterpret_cast<uint4*>(nxt + row_off + 16 * ((4 + c) ^ swz)) =
+          make_uint4(w[0], w[1], w[2], w[3]);
+    mma_slice<IT>(acc, f0, s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  // slice 0: A's DMA, the next row's loads
+  issue_a(cur);
+  const Nf4Row now = brow;
+  issue_b(brow);
+  mma_slice<IT>(acc, f1, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  // slices 1, 2: this row's scale and table planes
+  uint32_t lo[4], hi[4];
+  nf4_planes<BQ, IT>(now, op, nf4, code2_lds, lo, hi);
+  read_frags_part(nxt, 0, wm, wn, lane, f0, 0);
+  mma_slice<IT>(acc, f1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  read_frags_part(nxt, 0, wm, wn, lane, f0, 1);
+  mma_slice<IT>(acc, f1, 2);
+  __builtin_amdgcn_sched_barrier(0);
+  // slices 3..7: the 8 half-chunks of chunks 0..3, [first[s], first[s + 1]) in slice s
+  const uint32_t d0[4] = {now.pk[0].x, now.pk[0].y, now.pk[0].z, now.pk[0].w};
+  constexpr int first[9] = {0, 0, 0, 0, 1, 3, 5, 7, 8};
+#pragma unroll
+  for (int s = 3; s < 8; ++s) {
+#pragma unroll
+    for (int e = first[s]; e < first[s + 1]; ++e) {
+      const int c = e >> 1, h = e & 1;
+      nf4_half(lo, hi, d0[c], h, w[2 * h], w[2 * h + 1]);
+      if (h)
+        *reinterpret_cast<uint4*>(cur + row_off + 16 * (c ^ swz)) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    if (s == 3) read_frags_part(nxt, 0, wm, wn, lane, f0, 2);
+    if (s == 4) read_frags_part(nxt, 0, wm, wn, lane, f0, 3);
+    mma_slice<IT>(acc, f1, s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pend.lo[j] = lo[j];
+    pend.hi[j] = hi[j];
+  }
+  pend.d[0] = now.pk[1].x;
+  pend.d[1] = now.pk[1].y;
+  pend.d[2] = now.pk[1].z;
+  pend.d[3] = now.pk[1].w;
+}
+
 // PARTIAL: write the raw fp32 sums of this split to ws[split][M][N]; otherwise the final
 // alpha / beta / bias epilogue into C (type OT). AL8: M and N are multiples of 8 and the
 // loop's loads come from panels; otherwise every load clamps its rows per lane.
 // K order: the second segment (A2 B2^T, K2 <= 128 columns, last split only) is loaded by the
 // prologue, so every load inside the loop is a step of the first segment.
-template <int IT, int OT, bool PARTIAL, int NB, bool AL8>
+template <int IT, int OT, bool PARTIAL, int NB, bool AL8, int BQ = kBDense>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ B,
                     int64_t ldb, const uint16_t* __restrict__ A2, int64_t lda2,
@@ -277,10 +525,13 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
                     typename Elem<OT>::T* __restrict__ C, int64_t ldc,
                     float* __restrict__ ws, const uint16_t* __restrict__ bias, int64_t M,
                     int64_t N, int64_t K, int64_t k_per_split, float alpha, float beta,
-                    bool vec_out) {
+                    bool vec_out, Nf4Operand nf4op) {
   using L = Layout<NB>;
+  constexpr bool kNf4 = BQ != kBDense;
+  static_assert(!kNf4 || NB == 8, "the NF4 B operand takes 256-row tiles: one row per thread");
   constexpr int kStageBytes = stage_bytes<NB>();
   __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
+  __shared__ float code2_lds[BQ == kBNf4Nested ? 256 : 1];
   constexpr int BN = bn_of<NB>();
   int64_t tm, tn;
   tile_of((M + BM - 1) / BM, (N + BN - 1) / BN, tm, tn);
@@ -295,6 +546,23 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / L::WN, wn = wave % L::WN;
 
+  // NF4 B: this thread's tile row, its LDS offset and swizzle, the 16 levels, code2 in LDS
+  Nf4Row brow{};
+  Nf4Pending pend{};
+  float nf4v[16];
+  uint32_t bswz = 0;
+  if constexpr (kNf4) {
+    const int r = threadIdx.x;
+    const int64_t n = n0 + r < N ? n0 + r : N - 1;
+    brow.row = nf4op.packed + n * (ldb >> 1);
+    brow.w0 = n * ldb;
+    bswz = (uint32_t)(((r >> 1) & 3) | ((r >> 3) & 1) << 2);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) nf4v[i] = nf4op.nf4[i];
+    if constexpr (BQ == kBNf4Nested) code2_lds[threadIdx.x] = nf4op.code2[threadIdx.x];
+  }
+  char* const brow_lds = smem + kATileBytes + threadIdx.x * kRowBytes;  // NF4: this thread's row
+
   f32x16_t acc[L::BI][L::BJ];
 #pragma unroll
   for (int i = 0; i < L::BI; ++i)
@@ -304,17 +572,31 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
   const TileLoader la = make_loader();
   if (nk > 0) {
-    // prologue: steps 0 and 1, of either segment
+    // prologue: steps 0 and 1, of either segment; an NF4 first-segment step's B is loaded,
+    // dequantised and stored right here
     auto prologue_load = [&](int t, char* stage) {
       const bool s2 = t < nk2;
       const int64_t k0 = s2 ? (int64_t)t * BK : kb + (int64_t)(t - nk2) * BK;
       load_tile(la, s2 ? A2 : A, s2 ? lda2 : lda, m0, M, k0, stage);
-      load_tile<NB>(la, s2 ? B2 : B, s2 ? ldb2 : ldb, n0, N, k0, stage + kATileBytes);
+      if (!kNf4 || s2) {
+        load_tile<NB>(la, s2 ? B2 : B, s2 ? ldb2 : ldb, n0, N, k0, stage + kATileBytes);
+      } else if constexpr (kNf4) {
+        // step 1's chunks 4..7 are left to the first loop step (K2 <= 64: step 1 is NF4)
+        Nf4Row now = brow;
+        nf4_issue<BQ>(now, nf4op, k0);
+        nf4_store_row<BQ, IT>(now, nf4op, nf4v, code2_lds, stage + (brow_lds - smem), bswz,
+                              stage == smem ? nullptr : &pend);
+      }
     };
+    if constexpr (BQ == kBNf4Nested) __syncthreads();  // code2_lds filled
     prologue_load(0, smem);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     prologue_load(nk > 1 ? 1 : 0, smem + kStageBytes);
+    if constexpr (kNf4) {  // B of loop step 0's reload target (step 2), one step ahead
+      const int t2 = 2 < nk ? 2 : nk - 1;
+      nf4_issue<BQ>(brow, nf4op, kb + (int64_t)(t2 - nk2) * BK);
+    }
     Frags<NB> f0;
     read_frags<NB>(smem, 0, wm, wn, lane, f0);
     // loop loads: step t2 = kt + 2 (the last step reloads itself: in bounds, never read),
@@ -323,7 +605,7 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
     Panel<NB> pb;
     if constexpr (AL8) {
       panel_init(pa, la, A, lda, m0, M, kb);
-      panel_init(pb, la, B, ldb, n0, N, kb);
+      if constexpr (!kNf4) panel_init(pb, la, B, ldb, n0, N, kb);
     }
     for (int kt = 0; kt < nk; ++kt) {
       char* cur = smem + (kt & 1) * kStageBytes;
@@ -334,14 +616,24 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
         if constexpr (AL8) {
           const uint32_t kbytes = (uint32_t)q * (uint32_t)(BK * 2);
           panel_issue(pa, la, kbytes, stage);
-          panel_issue(pb, la, kbytes, stage + kATileBytes);
+          if constexpr (!kNf4) panel_issue(pb, la, kbytes, stage + kATileBytes);
         } else {
           const int64_t k0 = kb + (int64_t)q * BK;
           load_tile(la, A, lda, m0, M, k0, stage);
-          load_tile<NB>(la, B, ldb, n0, N, k0, stage + kATileBytes);
+          if constexpr (!kNf4) load_tile<NB>(la, B, ldb, n0, N, k0, stage + kATileBytes);
         }
       };
-      mma_step_pipe<IT, NB>(acc, f0, cur, nxt, issue, wm, wn, lane);
+      if constexpr (kNf4) {
+        // B of step t2 + 1 (clamped: in bounds, never read past the last step), one step ahead
+        auto issue_b = [&](Nf4Row& r) {
+          const int t3 = t2 + 1 < nk ? t2 + 1 : nk - 1;
+          nf4_issue<BQ>(r, nf4op, kb + (int64_t)(t3 - nk2) * BK);
+        };
+        mma_step_pipe_nf4<BQ, IT>(acc, f0, cur, nxt, issue, issue_b, brow, pend, nf4op, nf4v,
+                                  code2_lds, (int)(brow_lds - smem), bswz, wm, wn, lane);
+      } else {
+        mma_step_pipe<IT, NB>(acc, f0, cur, nxt, issue, wm, wn, lane);
+      }
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -425,11 +717,11 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
   }
 }
 
-template <int IT, int OT, int NB>
+template <int IT, int OT, int NB, int BQ = kBDense>
 int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
            const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
            int64_t M, int64_t N, int64_t K, float alpha, float beta, int splits, float* ws,
-           hipStream_t s) {
+           hipStream_t s, const Nf4Operand& nf4op = Nf4Operand{}) {
   using T = typename Elem<OT>::T;
   constexpr int BN = bn_of<NB>();
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
@@ -441,29 +733,29 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
   if (nsplit <= 1) {
     const bool vec_out = ql_aligned(C, 4 * ql_elem_size(OT)) && ldc % 4 == 0;
     if (al8)
-      hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, true>), dim3((unsigned)tiles, 1),
+      hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, true, BQ>), dim3((unsigned)tiles, 1),
                          dim3(kThreads), 0, s, (const uint16_t*)A, lda, (const uint16_t*)B, ldb,
                          (const uint16_t*)A2, lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc,
-                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
+                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out, nf4op);
     else
-      hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, false>), dim3((unsigned)tiles, 1),
+      hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, false, BQ>), dim3((unsigned)tiles, 1),
                          dim3(kThreads), 0, s, (const uint16_t*)A, lda, (const uint16_t*)B, ldb,
                          (const uint16_t*)A2, lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc,
-                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out);
+                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out, nf4op);
     return ql_launch_status();
   }
   if (al8)
-    hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, true>),
+    hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, true, BQ>),
                        dim3((unsigned)tiles, (unsigned)nsplit), dim3(kThreads), 0, s,
                        (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
                        (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0, ws,
-                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false);
+                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false, nf4op);
   else
-    hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, false>),
+    hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, false, BQ>),
                        dim3((unsigned)tiles, (unsigned)nsplit), dim3(kThreads), 0, s,
                        (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
                        (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0, ws,
-                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false);
+                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false, nf4op);
   int st = ql_launch_status();
   if (st != QL_OK) return st;
   const int64_t total = M * N;
@@ -501,7 +793,9 @@ int64_t ql_gemm_nt_workspace_floats(int64_t M, int64_t N, int splits) {
   return splits > 1 ? (int64_t)splits * M * N : 0;
 }
 
-// Split count of an M x N x K product: the s in 1..64 (at least 8 K steps per split) with the
+namespace {
+
+// Split count of an M x N x K product (tile width bn): the s in 1..64 (at least 8 K steps per split) with the
 // least modelled time, in units of one workgroup's K step:
 //   ceil(tiles * s / 256) rounds of the 256 CUs, each (K steps per split + kTileFixedSteps)
 //   long (the prologue's first load and the epilogue's stores of a tile), plus, for s > 1,
@@ -513,8 +807,7 @@ constexpr int64_t kCUs = 256;
 constexpr int64_t kTileFixedSteps = 8;
 constexpr double kStepBytes = 9.6e6;  // ~1.6 us of a K step at ~6 TB/s
 
-int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
-  const int64_t bn = 32 * choose_nb(M, N);
+int auto_splits_bn(int64_t M, int64_t N, int64_t K, int64_t bn) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + bn - 1) / bn);
   const int64_t steps = K / BK;
   auto cost = [&](int64_t s) {
@@ -532,6 +825,16 @@ int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
     }
   }
   return best;
+}
+
+}  // namespace
+
+int ql_gemm_nt_auto_splits(int64_t M, int64_t N, int64_t K) {
+  return auto_splits_bn(M, N, K, 32 * choose_nb(M, N));
+}
+
+int ql_gemm_nf4_auto_splits(int64_t M, int64_t N, int64_t K) {
+  return auto_splits_bn(M, N, K, 256);
 }
 
 int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
@@ -578,4 +881,67 @@ int ql_gemm_nt(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const
                float alpha, float beta, int splits, float* ws, hipStream_t s) {
   return ql_gemm_nt2(in_dtype, c_dtype, M, N, K, A, lda, B, ldb, nullptr, 0, nullptr, 0, 0, C,
                      ldc, bias, alpha, beta, splits, ws, s);
+}
+
+// ---- the 4-bit base GEMM: B is an NF4 weight, dequantised on its way into LDS ----------------
+
+namespace {
+
+int log2_exact(int64_t v) {  // log2 of a power of two, else -1
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int l = 0;
+  while ((int64_t(1) << l) < v) ++l;
+  return l;
+}
+
+}  // namespace
+
+extern "C" int64_t qlora_gemm_nf4_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 0;
+  return ql_gemm_nt_workspace_floats(M, N, ql_gemm_nf4_auto_splits(M, N, K)) *
+         (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_gemm_nf4(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                              const uint8_t* packed, const void* absmax, int nested,
+                              const float* code2, const float* absmax2, float offset,
+                              int blocksize, int blocksize2, const float* nf4_table, int64_t K2,
+                              const void* A2, int64_t lda2, const void* B2, int64_t ldb2,
+                              int in_dtype, void* C, int64_t ldc, const void* bias, float alpha,
+                              void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || N < 0 || K < 0 || K2 < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
+  if (M == 0 || N == 0) return QL_OK;
+  if (!A || !packed || !absmax || !nf4_table || !C) return QL_EINVAL;
+  if (nested && (!code2 || !absmax2)) return QL_EINVAL;
+  if (K2 > 0 && (!A2 || !B2)) return QL_EINVAL;
+  // the LoRA segment takes one prologue step, so prologue step 1 is always an NF4 step
+  if (K <= 0 || K % BK || K2 % BK || K2 > BK) return QL_ESHAPE;
+  const int log2_bs = log2_exact(blocksize);
+  const int log2_bs2 = nested ? log2_exact(blocksize2) : 0;
+  if (log2_bs < 6 || K % blocksize || log2_bs2 < 0) return QL_EINVAL;
+  if (lda < K || ldc < N || (K2 > 0 && (lda2 < K2 || ldb2 < K2))) return QL_ESHAPE;
+  if (lda % 8 || !ql_aligned(A, 16) || !ql_aligned(packed, 16) || !ql_aligned(C, 2) ||
+      (bias && !ql_aligned(bias, 2)))
+    return QL_EALIGN;
+  if (K2 > 0 && !ql_gemm_nt_fits(M, N, K2, A2, lda2, B2, ldb2)) return QL_EALIGN;
+  if ((M + BM - 1) / BM * ((N + 255) / 256) >= (int64_t(1) << 30)) return QL_ESHAPE;
+  int splits = ql_gemm_nf4_auto_splits(M, N, K);
+  const int64_t need = ql_gemm_nt_workspace_floats(M, N, splits) * (int64_t)sizeof(float);
+  if (need > workspace_bytes || !workspace || !ql_aligned(workspace, 16)) splits = 1;
+  const Nf4Operand op{packed, absmax, absmax2, code2, nf4_table, offset, log2_bs, log2_bs2};
+  float* ws = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (K2 == 0) A2 = B2 = nullptr;
+  // B's leading dimension is K: the weight's row length, in weights
+#define QL_NF4_LAUNCH(ITC, BQC)                                                                \
+  return launch<ITC, ITC, 8, BQC>(A, lda, nullptr, K, A2, lda2, B2, ldb2, K2, C, ldc, bias, M, \
+                                  N, K, alpha, 0.f, splits, ws, s, op)
+  if (in_dtype == QL_BF16) {
+    if (nested) QL_NF4_LAUNCH(QL_BF16, kBNf4Nested);
+    QL_NF4_LAUNCH(QL_BF16, kBNf4Plain);
+  }
+  if (nested) QL_NF4_LAUNCH(QL_F16, kBNf4Nested);
+  QL_NF4_LAUNCH(QL_F16, kBNf4Plain);
+#undef QL_NF4_LAUNCH
 }

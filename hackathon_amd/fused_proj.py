@@ -131,14 +131,22 @@ def group_forward(x2, specs, ab):
     offs = _offsets(specs)
     a16, at, bs, bt = _gemm.lora_pack_group(
         [(ab[2 * g], ab[2 * g + 1], specs[g].scaling) for g in range(G)], dt, _PAD)
-    w = torch.empty((offs[-1], K), dtype=dt, device=dev)
-    for g, s in enumerate(specs):
-        nf4.dequantize_nf4(s.packed, s.qs, dt, out=w[offs[g]:offs[g + 1]])
     u = torch.empty((M, _PAD), dtype=dt, device=dev)
     ut = _t_buffer(16 * G, M, dt, dev)
     _gemm.lora_down(x2, a16, u, out_t=ut)  # every slot in one pass over x
     y = torch.empty((M, offs[-1]), dtype=dt, device=dev)
     bias = _bias_cat(specs, dt, dev)
+    if all(nf4.use_fused_gemm(x2, s.qs, s.packed) for s in specs):
+        # few rows: each projection's W dequantised inside its GEMM (bs rows of projection g
+        # are zero outside slot g, so u's other slots add nothing)
+        for g, s in enumerate(specs):
+            c0, c1 = offs[g], offs[g + 1]
+            nf4.gemm_nf4(x2, s.packed, s.qs, out=y[:, c0:c1], a2=u, b2=bs[c0:c1],
+                         bias=None if bias is None else bias[c0:c1])
+        return y, (at, bt, ut)
+    w = torch.empty((offs[-1], K), dtype=dt, device=dev)
+    for g, s in enumerate(specs):
+        nf4.dequantize_nf4(s.packed, s.qs, dt, out=w[offs[g]:offs[g + 1]])
     for p0, p1 in _column_blocks(specs):
         c0, c1 = offs[p0], offs[p1]
         _gemm.gemm_nt_cat(x2, w[c0:c1], u, bs[c0:c1], y[:, c0:c1],

@@ -159,13 +159,18 @@ class LoraNF4Linear(torch.autograd.Function):
         N = int(quant_state.shape[0])
         # A, A^T|0, s*B|0 and B^T in the compute dtype, one launch (kept for the backward)
         a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
-        w = nf4.dequantize_nf4(packed, quant_state, dt)
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
         ut = _gemm.lora_t_buffer(M, dt, x2.device)                     # u^T, for dB
         _gemm.lora_down(x2, a16, u, out_t=ut)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
-        _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=None if bias is None else bias.to(dt))
-        del w, u
+        b16 = None if bias is None else bias.to(dt)
+        if nf4.use_fused_gemm(x2, quant_state, packed):   # few rows: W dequantised in the GEMM
+            nf4.gemm_nf4(x2, packed, quant_state, out=y, a2=u, b2=bs, bias=b16)
+        else:
+            w = nf4.dequantize_nf4(packed, quant_state, dt)
+            _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=b16)
+            del w
+        del u
         ctx.save_for_backward(x2, ut, at, bt)
         ctx.packed, ctx.quant_state, ctx.scaling = packed, quant_state, float(scaling)
         ctx.shape, ctx.wdtypes = x.shape, (a_weight.dtype, b_weight.dtype)

@@ -299,6 +299,31 @@ int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
                       ql_stream_t stream);
 
 /*
+ * The 4-bit base GEMM with its NF4 weight dequantised inside the GEMM, on the way into LDS:
+ *   C[M,N] = alpha * (A[M,K] W[N,K]^T + A2[M,K2] B2[N,K2]^T) (+ bias[n]),  C in in_dtype,
+ * where W is the weight qlora_nf4_dequant produces from (packed, absmax, nested, code2,
+ * absmax2, offset, blocksize, blocksize2, nf4_table) for n_weights = N * K, rounded to
+ * in_dtype: the products see exactly those 16-bit values, so C equals qlora_gemm_nt_cat on
+ * the dequantised W bit for bit. W's packed bytes are read once per 256-row tile of A instead
+ * of writing and re-reading a dense 16-bit copy.
+ * K % 64 == 0; blocksize a power of two >= 64 dividing K (blocksize2 a power of two when
+ * nested); K2 % 64 == 0 and K2 <= 128 (the rank-16 LoRA segment, zero-padded to 64 columns,
+ * as in qlora_gemm_nt_cat); A, packed 16-B aligned, lda >= K a multiple of 8; A2/B2 as in
+ * qlora_gemm_nt_cat; in_dtype QL_BF16 or QL_F16. Workspace (16-B aligned,
+ * qlora_gemm_nf4_workspace_size bytes) enables split-K for outputs with few 256 x 256 tiles.
+ * Replaces: solution/nf4.py:101-102 (dequantize_nf4 + F.linear in NF4Linear.forward) together
+ * with solution/lora.py:49-60,172 (the adapter GEMMs and the scaled add).
+ */
+int64_t qlora_gemm_nf4_workspace_size(int64_t M, int64_t N, int64_t K);
+int qlora_gemm_nf4(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                   const uint8_t* packed, const void* absmax, int nested, const float* code2,
+                   const float* absmax2, float offset, int blocksize, int blocksize2,
+                   const float* nf4_table, int64_t K2, const void* A2, int64_t lda2,
+                   const void* B2, int64_t ldb2, int in_dtype, void* C, int64_t ldc,
+                   const void* bias, float alpha, void* workspace, int64_t workspace_bytes,
+                   ql_stream_t stream);
+
+/*
  * LoRA down-projection (rank 16) for `slots` = G adapters (1 <= G <= 4) that share X:
  *   out[m, c] = alpha * sum_k X[m,k] Y[c,k]  for c < 16 G   (Y [16 G, K]: adapter g in rows
  *                                                            16 g .. 16 g + 15)
