@@ -512,6 +512,68 @@ QL_DEV void mma_step_pipe_nf4(f32x16_t (&acc)[4][4], Frags<8>& f0, char* __restr
   pend.d[3] = now.pk[1].w;
 }
 
+// Epilogue of a 16-bit output tile through LDS. Lane l holds 4 consecutive columns of one row
+// per (block, group); stored to global memory straight from there, every store instruction
+// writes 16 B into each of 32 rows, and measured on MI355X the 128 KiB of a 256 x 256 tile
+// then take 11-16 us per tile (a GEMM with K = 3584 spent 15% of its time there). Here the
+// waves first write the rounded values into LDS (free once the K loop is done: 256 rows of
+// 512 B, or 448 B for 224-wide tiles, the 16-B chunks of row r XOR-swizzled by r % 32, or
+// r % 4, against bank conflicts), then the threads store whole rows, 16 B per lane (a wave
+// covers two rows of a 256-wide tile: 1 KiB of full 128-B lines per instruction). The arithmetic is the
+// direct path's: alpha * acc, plus the bias, rounded once.
+template <int IT, int OT, int NB>
+QL_DEV void tile_store_via_lds(const f32x16_t (&acc)[Layout<NB>::BI][Layout<NB>::BJ],
+                               char* __restrict__ smem, typename Elem<OT>::T* __restrict__ C,
+                               int64_t ldc, const uint16_t* __restrict__ bias, int64_t m0,
+                               int64_t n0, int64_t M, int64_t N, float alpha, int wm, int wn,
+                               int lane) {
+#pragma clang fp contract(off)  // alpha * acc, then + bias: two roundings, as the direct path
+  using L = Layout<NB>;
+  using T = typename Elem<OT>::T;
+  constexpr int kChunks = 4 * NB;      // 16-B chunks of 8 values per tile row: 32 or 28
+  constexpr int kRow = 16 * kChunks;   // LDS bytes per row: BM rows fit the two K-loop stages
+  constexpr int kSwz = NB == 8 ? 31 : 3;  // chunk q of row r sits at q ^ (r & kSwz) < kChunks
+  static_assert(BM * kRow <= 2 * stage_bytes<NB>(), "the output tile must fit the stages");
+  __syncthreads();                     // every wave is done with the K loop's LDS tiles
+#pragma unroll
+  for (int i = 0; i < L::BI; ++i) {
+    const int r = (wm * L::BI + i) * 32 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < L::BJ; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c = (wn * L::BJ + j) * 32 + 8 * g + 4 * (lane >> 5);  // tile column
+        float v[4] = {alpha * acc[i][j][4 * g], alpha * acc[i][j][4 * g + 1],
+                      alpha * acc[i][j][4 * g + 2], alpha * acc[i][j][4 * g + 3]};
+        if (bias) {
+          const int64_t col = n0 + c;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < N) v[e] += Elem<IT>::to_f32(bias[col + e]);
+        }
+        const uint32_t lo = OT == QL_BF16 ? pack_bf16x2(v[0], v[1]) : pack_f16x2(v[0], v[1]);
+        const uint32_t hi = OT == QL_BF16 ? pack_bf16x2(v[2], v[3]) : pack_f16x2(v[2], v[3]);
+        const int q = (c >> 3) ^ (r & kSwz);
+        *reinterpret_cast<uint2*>(smem + r * kRow + q * 16 + (c & 4) * 2) = make_uint2(lo, hi);
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < BM * kChunks; idx += kThreads) {
+    const int r = idx / kChunks, q = idx % kChunks;
+    const int64_t row = m0 + r, col = n0 + 8 * q;
+    if (row >= M || col >= N) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(smem + r * kRow + ((q ^ (r & kSwz)) * 16));
+    T* cp = C + row * ldc + col;
+    if (col + 8 <= N) {
+      *reinterpret_cast<uint4*>(cp) = v;
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      for (int e = 0; e < 8 && col + e < N; ++e) cp[e] = (T)(w[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
 // PARTIAL: write the raw fp32 sums of this split to ws[split][M][N]; otherwise the final
 // alpha / beta / bias epilogue into C (type OT). AL8: M and N are multiples of 8 and the
 // loop's loads come from panels; otherwise every load clamps its rows per lane.
@@ -638,7 +700,19 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  // 16-bit output without beta, 16-B aligned rows: the tile goes out through LDS, whole rows at
+  // a time (see tile_store_via_lds); the values are those of the direct path below.
+  if constexpr (!PARTIAL && OT != QL_F32) {
+    if (beta == 0.f && ((uintptr_t)C & 15) == 0 && (ldc & 7) == 0) {
+      tile_store_via_lds<IT, OT, NB>(acc, smem, C, ldc, bias, m0, n0, M, N, alpha, wm, wn, lane);
+      return;
+    }
+  }
+
   // Epilogue: block (i, j) element 4g + e of lane l is row l%32, column 8g + 4(l/32) + e.
+  // alpha * acc, + beta * C, + bias: each rounded to fp32 (no contraction), in both paths.
+  {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int i = 0; i < L::BI; ++i) {
     const int64_t row = m0 + (wm * L::BI + i) * 32 + (lane & 31);
@@ -685,6 +759,7 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
         }
       }
     }
+  }
   }
 }
 
