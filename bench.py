@@ -10,11 +10,15 @@ HBM before the timed region; the K steps are captured in one HIP graph and repla
 with HIP events on the stream the kernels run on.
 
 Also reported in the same line:
-  roofline       the dequant kernel against the 8 TB/s HBM peak (algorithmic bytes/launch)
-  cpu_baseline   the C oracle's dequant (oracle/nf4_oracle.c, 1 thread) on a bounded sample
+  roofline       the dequant kernel against the 8 TB/s HBM peak (algorithmic bytes/launch);
+                 `traffic` is the stored rocprofv3 FETCH+WRITE figure (not measured here)
+  cpu_baseline   the reference path's dequant on the host CPU: the oracle's torch restatement
+                 on every host thread, Qwen2.5-0.5B gate_proj weight, bounded sample; the C
+                 oracle on one thread is reported beside it (cpu_baseline_c_1thread)
   cpu_baselines  the other workloads' CPU side on the host (oracle torch restatements and the
                  eager model path), bounded samples with stated extrapolation
-  nf4_4864x896   the same dequant on the Qwen2.5-0.5B gate_proj weight (32 rotated sets)
+  nf4_4864x896   the same dequant on the Qwen2.5-0.5B gate_proj weight (32 rotated sets), with
+                 the graph launch floor (an empty kernel's per-launch time) beside it
   kernels        per-kernel device time and roofline of the other kernels at their shapes,
                  and the Qwen2.5-7B LoRA MLP forward + backward at 4096 tokens (patched vs
                  eager, TFLOP/s against 3.364 TFLOP of work)
@@ -104,6 +108,29 @@ def bench_nf4(torch, shape, steps, warmup, sets, seed=0):
     sec = _graph_time(calls, torch)
     nbytes = nf4_algorithmic_bytes(n)
     return dict(sec_per_call=sec, bytes_per_call=nbytes, gbs=nbytes / sec / 1e9, n=n)
+
+
+def launch_floor(torch, steps=200, sets=32):
+    """Seconds per launch of the smallest kernel (a one-element fill) captured `steps` times in
+    one HIP graph and timed like the dequant: the per-launch cost any kernel pays in this
+    timing, before it moves a byte. On MI355X it is about 1.6 us, with one workgroup or
+    a thousand."""
+    bufs = [torch.empty(1, device="cuda") for _ in range(sets)]
+    return _graph_time([(lambda b=bufs[i % sets]: b.zero_()) for i in range(steps)], torch,
+                       replays=3)
+
+
+def bench_nf4_small(torch, steps=200, warmup=5):
+    """The dequant on the Qwen2.5-0.5B gate_proj weight (4864 x 896, 10.97 MB per call, 32
+    rotated sets) beside the launch floor: `above_floor_gbs` is the rate of the time the
+    dequant adds to an empty launch."""
+    r = bench_nf4(torch, (4864, 896), steps, warmup, 32, seed=1)
+    floor = launch_floor(torch, steps)
+    extra = r["sec_per_call"] - floor
+    return dict(us=round(r["sec_per_call"] * 1e6, 3), gbs=round(r["gbs"], 1),
+                frac_hbm=round(r["gbs"] / HBM_PEAK_GBS, 4), bytes=r["bytes_per_call"],
+                rotated_sets=32, launch_floor_us=round(floor * 1e6, 3),
+                above_floor_gbs=round(r["bytes_per_call"] / extra / 1e9, 1) if extra > 0 else None)
 
 
 def cpu_baseline_nf4(seconds, shape=(4864, 896), threads=None):
@@ -375,7 +402,21 @@ def bench_swiglu(torch, res):
             ("swiglu_bwd_4096x18944", lambda: _lib.call("qlora_swiglu_bwd", gr.data_ptr(),
                                                        gt.data_ptr(), up.data_ptr(), dg.data_ptr(),
                                                        du.data_ptr(), 2, n, s()), 5 * 2 * n)):
-        _rate(name, _graph_time([fn] * 10, torch), nbytes, res)
+        _rate(name, _graph_time([fn] * 10, torch, replays=3), nbytes, res)
+    # the backward fused with the gate and up adapters' down-projections (the LoRA MLP's
+    # backward): the same 775.9 MB plus B^T of both adapters (1.2 MB) and du, du^T (0.8 MB)
+    from hackathon_amd import gemm, swiglu
+
+    M, N = 4096, 18944
+    bt = (torch.randn(32, N, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    dlo = torch.empty(M, 64, device="cuda", dtype=torch.bfloat16)
+    dlo_t = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=32)
+    views = [t.view(M, N) for t in (gr, gt, up, dg, du)]
+
+    def fused():
+        swiglu.swiglu_bwd_lora_down(*views, bt[:16], bt[16:], 1.0, 1.0, dlo, dlo_t)
+    _rate("swiglu_bwd_lora_down_4096x18944", _graph_time([fused] * 10, torch, replays=3),
+          5 * 2 * n + 2 * 32 * N + 2 * (M * 64 + 32 * M), res)
 
 
 def bench_gemms(torch, res):
@@ -451,8 +492,7 @@ WORKLOADS = {
     "gemm": lambda torch, res: bench_gemms(torch, res),
     "ce": lambda torch, res: bench_ce(torch, res),
     "mlp": lambda torch, res: res.update(qwen25_7b_mlp_lora_4096tok=bench_mlp(torch)),
-    "nf4_small": lambda torch, res: res.update(nf4_4864x896=bench_nf4(
-        torch, (4864, 896), 200, 5, 32, seed=1)),
+    "nf4_small": lambda torch, res: res.update(nf4_4864x896=bench_nf4_small(torch)),
 }
 
 
@@ -771,7 +811,10 @@ def main():
                    f"{args.steps} launches, HIP events on the launch stream"},
         "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": _measured_traffic()},
+                     "traffic": _measured_traffic(),
+                     "traffic_source": "stored: profiles/nf4_dequant_traffic.json, rocprofv3 "
+                                       "--pmc FETCH_SIZE and WRITE_SIZE passes over bench.py "
+                                       "--pmc-probe, scaled by a 256 MiB copy in the same run"},
     }
     if args.nf4_only:
         print(json.dumps(line), flush=True)
@@ -780,11 +823,9 @@ def main():
     hp["dequant_frac_of_write"] = round(r["gbs"] / hp["write_fill_gbs"], 4)
     line["hbm_practical"] = hp
     log(f"[bench] HBM practical: {json.dumps(hp)}")
-    r1 = bench_nf4(torch, (4864, 896), max(args.steps, 200), args.warmup, 32, seed=1)
-    line["nf4_4864x896"] = dict(us=round(r1["sec_per_call"] * 1e6, 3), gbs=round(r1["gbs"], 1),
-                                frac_hbm=round(r1["gbs"] / HBM_PEAK_GBS, 4),
-                                bytes=r1["bytes_per_call"], rotated_sets=32)
-    log(f"[bench] nf4 4864x896: {r1['sec_per_call'] * 1e6:.2f} us/call, {r1['gbs']:.0f} GB/s")
+    r1 = line["nf4_4864x896"] = bench_nf4_small(torch, max(args.steps, 200), args.warmup)
+    log(f"[bench] nf4 4864x896: {r1['us']:.2f} us/call, {r1['gbs']:.0f} GB/s; launch floor "
+        f"{r1['launch_floor_us']:.2f} us, {r1['above_floor_gbs']} GB/s above it")
     if not args.no_kernels:
         line["kernels"] = bench_kernels(torch)
         log(f"[bench] kernels: {json.dumps(line['kernels'])}")

@@ -28,13 +28,22 @@ QL_DEV uint16_t f32_to_bf16_bits(float f) {
 QL_DEV float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 QL_DEV uint16_t f32_to_f16_bits(float f) {
+  // The value is an fp32 result when it is converted: without the empty register barrier the
+  // AMDGPU backend may fuse the multiply that produced it with this conversion into one
+  // v_fma_mixlo_f16 (a single rounding), and does so at some call sites and not at others,
+  // so two kernels that evaluate the same expression would disagree in the last fp16 bit.
+  asm("" : "+v"(f));
   _Float16 h = (_Float16)f;
   return __builtin_bit_cast(uint16_t, h);
 }
 
 // Two fp32 -> one packed 32-bit word of bf16 (lo in bits 0..15), RNE.
+// One v_cvt_pk_bf16_f32 converts both values (the same RNE rounding as f32_to_bf16_bits; the
+// scalar form costs a conversion per value plus the shift and or that join them).
 QL_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 QL_DEV uint32_t pack_f16x2(float lo, float hi) {

@@ -25,8 +25,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const typename Elem<D
     float g[8], u[8], o[8];
     Vec8<DT>::load(gate + 8 * i, g);
     Vec8<DT>::load(up + 8 * i, u);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = ql_swiglu_fwd1(g[j], u[j]);
+    ql_swiglu_fwd8(g, u, o);
     Vec8<DT>::store(out + 8 * i, o);
   }
 }
@@ -42,8 +41,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(
     Vec8<DT>::load(grad + 8 * i, gr);
     Vec8<DT>::load(gate + 8 * i, g);
     Vec8<DT>::load(up + 8 * i, u);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ql_swiglu_bwd1(gr[j], g[j], u[j], dg[j], du[j]);
+    ql_swiglu_bwd8(gr, g, u, dg, du);
     Vec8<DT>::store(dgate + 8 * i, dg);
     Vec8<DT>::store(dup + 8 * i, du);
   }
@@ -87,8 +85,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_fwd_rows(
     float g[8], u[8], o[8];
     Vec8<DT>::load(gate + r * ldg + c, g);
     Vec8<DT>::load(up + r * ldu + c, u);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = ql_swiglu_fwd1(g[j], u[j]);
+    ql_swiglu_fwd8(g, u, o);
     Vec8<DT>::store(out + r * ldo + c, o);
   }
 }
@@ -107,8 +104,7 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_rows(
     Vec8<DT>::load(grad + r * ldgr + c, gr);
     Vec8<DT>::load(gate + r * ldg + c, g);
     Vec8<DT>::load(up + r * ldu + c, u);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ql_swiglu_bwd1(gr[j], g[j], u[j], dg[j], du[j]);
+    ql_swiglu_bwd8(gr, g, u, dg, du);
     Vec8<DT>::store(dgate + r * lddg + c, dg);
     Vec8<DT>::store(dup + r * lddu + c, du);
   }

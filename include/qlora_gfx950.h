@@ -382,7 +382,8 @@ int qlora_lora_wgrad_noalloc(const void* PT, int64_t ldpt, const void* Q, int64_
  *   du[m, 16 + c] = alpha_up   * sum_k dup[m, k]   * bt_up[c, k]
  *   du[m, c] = 0 for 32 <= c < out_cols; du_t (optional, [32, ldt >= rows]) = du[:, :32]^T.
  * bt_gate / bt_up are the adapters' B^T [16, cols] (ld ldbt). The gradients are multiplied
- * from registers, so the two down-projections do not read them back from HBM.
+ * from an on-chip copy of each tile, so the two down-projections do not read them back from
+ * HBM.
  * cols % 32 == 0; every matrix 16-B aligned with a leading dimension that is a multiple of 8,
  * at least cols, and below 2^24; dtype QL_BF16 or QL_F16 (du and du_t in it too). Not in
  * place: the byte ranges dgate and dup span must not meet those of grad, gate or up
