@@ -12,6 +12,13 @@
 // One 512-thread workgroup per row; each thread walks 8-element (16 B) chunks with a stride
 // of the workgroup, keeping a running (m, s, t, best, best_idx) per thread, rescaling once
 // per chunk. Threads combine through wave butterflies and one LDS exchange.
+//
+// Second reads stay on chip: each thread keeps its first chunks of the row (the row's first
+// 64 KiB) in LDS for sweep 2, and the 64 KiB per workgroup hold the GPU at two rows per CU,
+// so the 512 rows in flight (156 MB at the Qwen2 vocabulary, 151936 x 2 B a row) stay inside
+// the 256 MB MALL and the rest of sweep 2 reads from there. Sweep 1 issues 4 chunk loads and
+// sweep 2 8 before their arithmetic. 8192 x 151936 bf16 on MI355X: 1.15 ms, against 1.45 ms
+// with four rows per CU and one chunk per step (the 1024 rows in flight spilled the MALL).
 #include "ql_vec.h"
 
 namespace {
@@ -49,25 +56,50 @@ QL_DEV RowStat shfl_stat(const RowStat& v, int off) {
   return r;
 }
 
+constexpr int kCacheBytes = 64 * 1024;  // LDS row cache per workgroup (dynamic)
+constexpr int kUnroll1 = 4, kUnroll2 = 8;  // chunk loads in flight per thread, sweeps 1 and 2
+
+// VW = 8: 8-element chunks (V % 8 == 0, 16-B aligned rows), 16-bit ones cached in LDS;
+// VW = 1: one element per step, no cache.
 template <int DT, int VW>
 __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     typename Elem<DT>::T* __restrict__ logits, int64_t row_stride, int64_t V,
     const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ entropy,
     int32_t* __restrict__ correct, int64_t* __restrict__ pred, int ignore_mode, int write_grad,
     float grad_scale) {
+  extern __shared__ uint4 cache[];  // kCacheBytes when VW == 8
   __shared__ RowStat part[kWaves];
   __shared__ float lse_sh;
+  constexpr bool kCached = VW == 8 && DT != QL_F32;  // a 16-B chunk per 8 elements
+  constexpr int64_t kCacheChunks = kCached ? kCacheBytes / 16 : 0;
+  constexpr int U1 = VW == 8 ? kUnroll1 : 1, U2 = VW == 8 ? kUnroll2 : 1;
   const int64_t row = blockIdx.x;
   auto* z = logits + row * row_stride;
   const int64_t tgt = target[row];
   const bool labelled = ignore_mode == 0 ? (tgt >= 0) : (tgt != -100);
+  const int64_t nchunk = V / VW;
+  auto load = [&](int64_t c, float* v) {  // sweep 2
+    if constexpr (kCached) {
+      const uint4 raw = c < kCacheChunks ? cache[c] : *reinterpret_cast<const uint4*>(z + 8 * c);
+      Vec8<DT>::unpack(raw, v);
+    } else if constexpr (VW == 8) {
+      Vec8<DT>::load(z + 8 * c, v);
+    } else {
+      v[0] = Elem<DT>::to_f32(z[c]);
+    }
+  };
+  auto load_keep = [&](int64_t c, float* v) {  // sweep 1: also fills the cache
+    if constexpr (kCached) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(z + 8 * c);
+      if (c < kCacheChunks) cache[c] = raw;
+      Vec8<DT>::unpack(raw, v);
+    } else {
+      load(c, v);
+    }
+  };
 
   RowStat st{-INFINITY, 0.f, 0.f, -INFINITY, 0};
-  const int64_t nchunk = V / VW;
-  for (int64_t c = threadIdx.x; c < nchunk; c += kThreads) {
-    float v[VW];
-    if constexpr (VW == 8) Vec8<DT>::load(z + 8 * c, v);
-    else v[0] = Elem<DT>::to_f32(z[c]);
+  auto absorb = [&](const float* v, int64_t c) {
     float cm = v[0];
     int cj = 0;
 #pragma unroll
@@ -86,6 +118,21 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     st.s = st.s * alpha + es;
     st.t = st.t * alpha + et;
     st.m = m;
+  };
+  // Sweep 1, in increasing chunk order per thread (the first maximum wins): U1 loads, then
+  // their arithmetic; chunks below kCacheChunks are also kept in LDS for sweep 2.
+  int64_t c0 = threadIdx.x;
+  for (; c0 + (U1 - 1) * kThreads < nchunk; c0 += U1 * kThreads) {
+    float v[U1][VW];
+#pragma unroll
+    for (int u = 0; u < U1; ++u) load_keep(c0 + u * kThreads, v[u]);
+#pragma unroll
+    for (int u = 0; u < U1; ++u) absorb(v[u], c0 + u * kThreads);
+  }
+  for (int64_t c = c0; c < nchunk; c += kThreads) {
+    float v[VW];
+    load_keep(c, v);
+    absorb(v, c);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) merge(st, shfl_stat(st, off));
@@ -109,10 +156,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   __syncthreads();
   const float lse = lse_sh;
   const float gs = labelled ? grad_scale : 0.f;
-  for (int64_t c = threadIdx.x; c < nchunk; c += kThreads) {
-    float v[VW];
-    if constexpr (VW == 8) Vec8<DT>::load(z + 8 * c, v);
-    else v[0] = Elem<DT>::to_f32(z[c]);
+  auto emit = [&](float* v, int64_t c) {
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
       const float onehot = (c * VW + j == tgt) ? 1.f : 0.f;
@@ -120,6 +164,21 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     }
     if constexpr (VW == 8) Vec8<DT>::store(z + 8 * c, v);
     else z[c] = Elem<DT>::from_f32(v[0]);
+  };
+  // Sweep 2: every thread rewrites the chunks it read (its cached ones from LDS), U2 loads
+  // ahead of their arithmetic.
+  c0 = threadIdx.x;
+  for (; c0 + (U2 - 1) * kThreads < nchunk; c0 += U2 * kThreads) {
+    float v[U2][VW];
+#pragma unroll
+    for (int u = 0; u < U2; ++u) load(c0 + u * kThreads, v[u]);
+#pragma unroll
+    for (int u = 0; u < U2; ++u) emit(v[u], c0 + u * kThreads);
+  }
+  for (int64_t c = c0; c < nchunk; c += kThreads) {
+    float v[VW];
+    load(c, v);
+    emit(v, c);
   }
 }
 
@@ -130,7 +189,8 @@ int launch_ce(void* logits, int64_t rs, int64_t n_rows, int64_t V, const int64_t
   using T = typename Elem<DT>::T;
   const bool vec = (V % 8) == 0 && ql_aligned(logits, 16) && ((rs * ql_elem_size(DT)) % 16) == 0;
   if (vec)
-    hipLaunchKernelGGL((ce_rows_kernel<DT, 8>), dim3((unsigned)n_rows), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL((ce_rows_kernel<DT, 8>), dim3((unsigned)n_rows), dim3(kThreads),
+                       DT == QL_F32 ? 0 : kCacheBytes, s,
                        (T*)logits, rs, V, target, loss, entropy, correct, pred, ignore_mode,
                        write_grad, grad_scale);
   else
