@@ -77,6 +77,47 @@ template <int DT> QL_DEV uint4 pack_pair(const f32x4_t& a, const f32x4_t& c) {
 
 QL_DEV f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
 
+// ---- The direct-to-LDS ordering rule, and its check ------------------------------------------
+// Every kernel here keeps one rule for the tiles its direct-to-LDS loads (dma_b128) fill: a
+// tile is read only after the next wait_all_barrier (the loads are hidden from the compiler,
+// so nothing else waits for them), and no load writes a tile that any wave may still read
+// before that barrier. Built with -DQL_DMA_CHECK (the GPU tests build such a library beside
+// the release one), each workgroup records in LDS which 1-KiB spans were loaded and which were
+// read since the last wait_all_barrier; at every wait_all_barrier a span in both sets counts
+// as a violation in a device counter (qlora_debug_dma_violations). Release builds compile the
+// hooks to nothing.
+#ifdef QL_DMA_CHECK
+constexpr int kSpanWords = 160 / 32;  // 160 KiB of LDS in 1-KiB spans
+__shared__ uint32_t dma_loaded[kSpanWords], dma_read[kSpanWords];
+__device__ unsigned long long g_dma_violations;
+QL_DEV void dma_mark(uint32_t* set, const void* p) {
+  const uint32_t span = (uint32_t)(uintptr_t)(lds_ptr_t)p >> 10;
+  atomicOr(&set[span >> 5], 1u << (span & 31));
+}
+QL_DEV void dma_ledger_clear() {
+  if (threadIdx.x < kSpanWords) dma_loaded[threadIdx.x] = dma_read[threadIdx.x] = 0;
+}
+// every wave has passed the barrier: count the phase's overlaps, clear, meet again so that
+// no wave marks the next phase before the clear
+QL_DEV void dma_ledger_settle() {
+  if (threadIdx.x < kSpanWords) {
+    const uint32_t both = dma_loaded[threadIdx.x] & dma_read[threadIdx.x];
+    if (both) atomicAdd(&g_dma_violations, (unsigned long long)__popc(both));
+  }
+  dma_ledger_clear();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+#define QL_DMA_BEGIN() (dma_ledger_clear(), __syncthreads())
+#define QL_DMA_LOADED(p) dma_mark(dma_loaded, (p))
+#define QL_DMA_READ(p) dma_mark(dma_read, (p))
+#define QL_DMA_SETTLE() dma_ledger_settle()
+#else
+#define QL_DMA_BEGIN() ((void)0)
+#define QL_DMA_LOADED(p) ((void)0)
+#define QL_DMA_READ(p) ((void)0)
+#define QL_DMA_SETTLE() ((void)0)
+#endif
+
 // ---- LDS tiles -------------------------------------------------------------------------------
 QL_DEV int swz_chunk(int chunk, int row) { return chunk ^ (((row >> 1) & 3) << 2 | (row & 1) * 3); }
 QL_DEV int tile_off(int row, int chunk) { return row * kRowBytes + swz_chunk(chunk, row) * 16; }
@@ -86,6 +127,7 @@ QL_DEV int tile_off(int row, int chunk) { return row * kRowBytes + swz_chunk(chu
 // addressing row r_j, columns n0 + 4 c .. +3 of a row-major tile, lane i gets column n0 + i
 // of rows r_0 .. r_3 (4 consecutive contraction values of an MFMA operand column).
 QL_DEV uint2 read_tr(const char* p) {
+  QL_DMA_READ(p);
   const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p));
   return __builtin_bit_cast(uint2, r);
 }
@@ -93,6 +135,7 @@ QL_DEV uint2 read_tr(const char* p) {
 // Operand fragment (16 rows x 32 contraction) along the rows of a tile: lane holds row `row`,
 // head-dim values 32 ks + 8 (lane / 16) .. +7.
 QL_DEV uint4 frag_row(const char* __restrict__ t, int row, int ks, int fq) {
+  QL_DMA_READ(t + tile_off(row, 4 * ks + fq));
   return *reinterpret_cast<const uint4*>(t + tile_off(row, 4 * ks + fq));
 }
 
@@ -132,6 +175,7 @@ QL_DEV void dma_b128(const char* sbase, uint32_t voff, char* lds) {
                :
                : "v"(voff), "s"(sbase), "s"(m0)
                : "memory", "m0");
+  QL_DMA_LOADED(lds);  // the 1 KiB this instruction fills: one span (tiles are 1-KiB aligned)
 }
 #pragma clang diagnostic pop
 
@@ -174,6 +218,7 @@ struct TileDma {
 // (__syncthreads would also do, but inline asm keeps the compiler from adding its own waits.)
 QL_DEV void wait_all_barrier() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  QL_DMA_SETTLE();
 }
 
 // Index differences used by the branch-free masks, clamped into int range.
@@ -311,6 +356,7 @@ void attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict_
                      const uint16_t* __restrict__ V, uint16_t* __restrict__ O,
                      float* __restrict__ lse, AttnShape sh, int n_qblocks) {
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // [stage][K, V]
+  QL_DMA_BEGIN();
   const int64_t BH = sh.B * sh.HQ;
   const int qb = n_qblocks - 1 - (int)(blockIdx.x / BH);  // heaviest blocks first
   const int64_t bh = blockIdx.x % BH;
@@ -506,6 +552,7 @@ void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
                    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
                    float* __restrict__ pk, float* __restrict__ pv, BwdShape sh, int n_kblocks) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kBwdStage];
+  QL_DMA_BEGIN();
   const int64_t BH = sh.B * sh.HQ;
   const int kb = (int)(blockIdx.x / BH);  // heaviest (first) key blocks first
   const int64_t bh = blockIdx.x % BH;
@@ -717,6 +764,7 @@ void attn_bwd_dq(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  const float* __restrict__ lse, const float* __restrict__ delta,
                  uint16_t* __restrict__ dQ, BwdShape sh, int n_qblocks) {
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // [stage][K, V]
+  QL_DMA_BEGIN();
   const int64_t BH = sh.B * sh.HQ;
   const int qb = n_qblocks - 1 - (int)(blockIdx.x / BH);  // heaviest blocks first
   const int64_t bh = blockIdx.x % BH;
@@ -895,3 +943,17 @@ extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const
 #undef QL_ATTN_BWD
   return ql_launch_status();
 }
+
+#ifdef QL_DMA_CHECK
+// Debug builds only: the violations the ordering check counted since the last reset.
+extern "C" int qlora_debug_dma_violations(unsigned long long* out, int reset) {
+  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(g_dma_violations), sizeof(*out)) != hipSuccess)
+    return QL_EINVAL;
+  if (reset) {
+    const unsigned long long zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_dma_violations), &zero, sizeof(zero)) != hipSuccess)
+      return QL_EINVAL;
+  }
+  return QL_OK;
+}
+#endif
