@@ -122,6 +122,53 @@ QL_DEV void load_tile(const TileLoader& t, const uint16_t* __restrict__ X, int64
   }
 }
 
+// load_tile with each load written as inline assembly, for the prologue. The compiler's
+// wait-count pass sees the builtin direct-to-LDS loads of one LDS array as possibly
+// overlapping, and waited for all of them (vmcnt(0)) between the A and B loads of each stage
+// and before the first fragment reads: four HBM round trips in a row before the first
+// product. Hidden from it, both stages' loads go out together, and the kernel's own
+// s_waitcnt vmcnt + barrier are the only waits. (s_nop 4: the wait states a write of M0
+// needs before a vector memory instruction reads it; inline assembly gets no hazard padding.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is clobbered on purpose
+QL_DEV void dma_hidden(const char* sbase, uint32_t voff, char* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t)lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int R8 = 8>
+QL_DEV void load_tile_hidden(const TileLoader& t, const uint16_t* __restrict__ X, int64_t ld,
+                             int64_t row0, int64_t rows, int64_t k0, char* __restrict__ lds_tile) {
+#pragma unroll
+  for (int j = 0; j < R8; ++j) {
+    const int r0 = (4 * j + t.wave) * 8;
+    const int64_t grow0 = row0 + r0;
+    const int64_t base_row = grow0 < rows ? grow0 : rows - 1;
+    const int64_t r = (grow0 + t.rsub) < rows ? grow0 + t.rsub : rows - 1;
+    const uint32_t off = (uint32_t)(r - base_row) * (uint32_t)(ld * 2) + t.chunk16;
+    dma_hidden(reinterpret_cast<const char*>(X + base_row * ld + k0), off,
+               lds_tile + r0 * kRowBytes);
+  }
+}
+
+// Prologue step t (second-segment steps first) of a dense tile: 8 + NB hidden loads per wave.
+// A plain function with its operands by value (a capturing lambda left them in memory, and
+// the reloads' waits drained the loads in flight).
+template <int NB>
+QL_DEV void prologue_dense(const TileLoader& la, const uint16_t* A, int64_t lda,
+                           const uint16_t* B, int64_t ldb, const uint16_t* A2, int64_t lda2,
+                           const uint16_t* B2, int64_t ldb2, int nk2, int64_t kb, int64_t m0,
+                           int64_t n0, int64_t M, int64_t N, int t, char* stage) {
+  const bool s2 = t < nk2;
+  const int64_t k0 = s2 ? (int64_t)t * BK : kb + (int64_t)(t - nk2) * BK;
+  load_tile_hidden(la, s2 ? A2 : A, s2 ? lda2 : lda, m0, M, k0, stage);
+  load_tile_hidden<NB>(la, s2 ? B2 : B, s2 ? ldb2 : ldb, n0, N, k0, stage + kATileBytes);
+}
+
 // The same loads for an operand whose row count is a multiple of 8, with the addresses
 // computed once per tile: every 8-row group a load covers is then either wholly inside the
 // operand or wholly past its end (a group past the end re-reads the last 8 rows, tile rows
@@ -639,9 +686,9 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
     auto prologue_load = [&](int t, char* stage) {
       const bool s2 = t < nk2;
       const int64_t k0 = s2 ? (int64_t)t * BK : kb + (int64_t)(t - nk2) * BK;
-      load_tile(la, s2 ? A2 : A, s2 ? lda2 : lda, m0, M, k0, stage);
+      load_tile_hidden(la, s2 ? A2 : A, s2 ? lda2 : lda, m0, M, k0, stage);
       if (!kNf4 || s2) {
-        load_tile<NB>(la, s2 ? B2 : B, s2 ? ldb2 : ldb, n0, N, k0, stage + kATileBytes);
+        load_tile_hidden<NB>(la, s2 ? B2 : B, s2 ? ldb2 : ldb, n0, N, k0, stage + kATileBytes);
       } else if constexpr (kNf4) {
         // step 1's chunks 4..7 are left to the first loop step (K2 <= 64: step 1 is NF4)
         Nf4Row now = brow;
@@ -651,10 +698,21 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
       }
     };
     if constexpr (BQ == kBNf4Nested) __syncthreads();  // code2_lds filled
-    prologue_load(0, smem);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    prologue_load(nk > 1 ? 1 : 0, smem + kStageBytes);
+    if constexpr (!kNf4) {
+      // both stages' loads go out before the first wait, which waits for stage 0 only: the
+      // 8 + NB loads of stage 1 (this wave's share) may stay in flight, since loads complete
+      // in issue order; the first K step's vmcnt(0) covers them before stage 1 is read
+      prologue_dense<NB>(la, A, lda, B, ldb, A2, lda2, B2, ldb2, nk2, kb, m0, n0, M, N, 0, smem);
+      prologue_dense<NB>(la, A, lda, B, ldb, A2, lda2, B2, ldb2, nk2, kb, m0, n0, M, N,
+                         nk > 1 ? 1 : 0, smem + kStageBytes);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 + NB) : "memory");
+      __syncthreads();
+    } else {
+      prologue_load(0, smem);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      prologue_load(nk > 1 ? 1 : 0, smem + kStageBytes);
+    }
     if constexpr (kNf4) {  // B of loop step 0's reload target (step 2), one step ahead
       const int t2 = 2 < nk ? 2 : nk - 1;
       nf4_issue<BQ>(brow, nf4op, kb + (int64_t)(t2 - nk2) * BK);
