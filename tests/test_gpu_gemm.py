@@ -85,9 +85,9 @@ def test_gemm_output_view_with_row_stride():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_gemm_nt_large_tile_edges(M, N, K, dtype):
     """k-contiguous operands with K % 64 == 0 take the large-tile kernel (256 x 256, or
-    256 x 224 / 256 x 288 when N is a multiple of that width and it fills the CUs better: the
-    4096 and 4000 x 3584 cases take 224, the x 4608 cases 288, the 4000-row ones with a ragged
-    last row of tiles); M and N edges are loaded clamped and must never be stored."""
+    256 x 224 when N is a multiple of 224 and it fills the CUs better: the 4096 and 4000 x 3584
+    cases take 224, the 4000-row ones with a ragged last row of tiles); M and N edges are
+    loaded clamped and must never be stored."""
     print(f"gemm_nt M={M} N={N} K={K} {dtype}", flush=True)
     g = torch.Generator().manual_seed(M + 11 * N + K)
     a = torch.randn(M, K, generator=g).to(dtype)
