@@ -417,6 +417,16 @@ def bench_swiglu(torch, res):
         swiglu.swiglu_bwd_lora_down(*views, bt[:16], bt[16:], 1.0, 1.0, dlo, dlo_t)
     _rate("swiglu_bwd_lora_down_4096x18944", _graph_time([fused] * 10, torch, replays=3),
           5 * 2 * n + 2 * 32 * N + 2 * (M * 64 + 32 * M), res)
+    # ... and with both adapters' lora_B gradients in the same pass: plus u^T of both adapters
+    # (0.3 MB) and the two fp32 [18944, 16] gradients (2.4 MB)
+    ut = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=32)
+    ut.copy_(torch.randn(32, M, device="cuda", generator=g).to(torch.bfloat16))
+
+    def fused_db():
+        swiglu.swiglu_bwd_lora(*views, bt[:16], bt[16:], ut[:16], ut[16:32], 1.0, 1.0, 1.0, 1.0,
+                               dlo, dlo_t)
+    _rate("swiglu_bwd_lora_4096x18944", _graph_time([fused_db] * 10, torch, replays=3),
+          5 * 2 * n + 2 * 32 * N + 2 * 32 * M + 2 * (M * 64 + 32 * M) + 2 * 4 * 16 * N, res)
 
 
 def bench_gemms(torch, res):

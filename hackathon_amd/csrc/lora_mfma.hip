@@ -494,6 +494,197 @@ __global__ __launch_bounds__(256) void swiglu_bwd_down_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
+// SwiGLU backward fused with both rank-16 products of its gradients for the gate and up
+// adapters (a LoRA MLP): for d in {dgate, dup} with that adapter's Y [16, K] and u^T [16, M],
+//   du[m, c] (16 columns each)  = alpha * sum_k d[m, k] Y[c, k]    the down-projection
+//   dB[k, c]                    = beta  * sum_m d[m, k] u[m, c]    the lora_B gradient
+// A workgroup owns 256 columns and a range of rows (a multiple of 32) and walks it in tiles
+// of 32 x 256, loading, computing and storing exactly as swiglu_bwd_down_kernel does (the
+// same ql_swiglu.h arithmetic, the same bits) and keeping both gradients of the tile in LDS.
+// After the tile's barrier:
+//  - du: wave w takes row group w / 2 and adapter w % 2: its 8 products over the 256 columns
+//    use that adapter's Y fragments, loaded once per workgroup (the columns are fixed), and
+//    the fp32 partial of the 16 x 16 block goes to ws_du[column block][row][32]; the partials
+//    of the column blocks are summed in order by lora_down_reduce.
+//  - dB: wave w takes 16-column blocks 4w .. 4w + 3 of both adapters; each product reads the
+//    block transposed from LDS (two ds_read_b64_tr_b16: 8 consecutive rows of one column per
+//    lane) against u^T's 32 rows of the tile (rows past M read as zero), accumulating over the
+//    workgroup's rows; at the end the partial goes to ws_db[adapter][row range][K][16], summed
+//    in order by lora_wgrad_reduce.
+// So the gradients are never read back from HBM for either product; the extra traffic is the
+// fp32 partials (M x 32 per column block, K x 32 per row range).
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+// Transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, with lane 4 j + c
+// addressing row r_j, columns n0 + 4 c .. +3 of a row-major 16-bit tile, lane i receives
+// column n0 + i of rows r_0 .. r_3.
+QL_DEV uint2 lds_read_tr(const char* p) {
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+constexpr int kSlRows = 32;                          // rows per tile
+constexpr int kSlCols = 256;                         // columns per workgroup
+constexpr int kSlLdsRow = 2 * kSlCols + 16;          // bytes per LDS row (16 B of padding)
+constexpr int kSlLdsArr = kSlRows * kSlLdsRow;       // one gradient's tile
+constexpr int kSlLdsBuf = 2 * kSlLdsArr;             // dgate + dup
+
+template <int IT>
+__global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
+    const uint16_t* __restrict__ GR, int64_t ldgr, const uint16_t* __restrict__ GA,
+    int64_t ldga, const uint16_t* __restrict__ UP, int64_t ldup, uint16_t* __restrict__ DG,
+    int64_t lddg, uint16_t* __restrict__ DU, int64_t lddu, const uint16_t* __restrict__ YG,
+    const uint16_t* __restrict__ YU, int64_t ldy, const uint16_t* __restrict__ UTG,
+    const uint16_t* __restrict__ UTU, int64_t ldut, int64_t M, int64_t K,
+    int64_t rows_per_split, float* __restrict__ ws_du, float* __restrict__ ws_db) {
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) char lds[2 * kSlLdsBuf];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t k0 = (int64_t)blockIdx.x * kSlCols;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_split;
+  const int64_t r1 = r0 + rows_per_split < M ? r0 + rows_per_split : M;
+  const int lr = tid >> 5, c = tid & 31;
+  // this thread's 16-B chunk: columns past K (the last block) recompute the block's first
+  const int64_t kx = k0 + 8 * c < K ? k0 + 8 * c : k0;
+  const int rg = wave >> 1, qd = wave & 1;  // du: row group and adapter of this wave
+  uint4 yv[kSlCols / 32];
+  {
+    const uint16_t* yq = qd ? YU : YG;
+    const uint32_t oy = (uint32_t)(((lane & 15) * ldy + 8 * (lane >> 4)) * 2);
+#pragma unroll
+    for (int g = 0; g < kSlCols / 32; ++g) {
+      const int64_t kg = k0 + 32 * g;
+      yv[g] = ld16(reinterpret_cast<const char*>(yq + (kg < K ? kg : k0)), oy);
+    }
+  }
+  f32x4_t acc_db[4][2];  // [column block 4 wave + i][adapter]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc_db[i][0] = acc_db[i][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int lds_w = lr * kSlLdsRow + 16 * c;                            // + 8 h rows
+  const int lds_r = (lane & 15) * kSlLdsRow + 16 * (lane >> 4);         // + 16 rg rows + 64 g
+  const int lds_t = (8 * (lane >> 4) + ((lane >> 2) & 3)) * kSlLdsRow + 8 * (lane & 3);
+  int buf = 0;
+  for (int64_t m0 = r0; m0 < r1; m0 += kSlRows) {
+    // rows m0 + lr + 8 h; a row past M (the last tile) works on row M - 1 and stores the
+    // bits row M - 1's owner stores, and is left out of both products
+    uint32_t ogr[4], oga[4], oup[4], odg[4], odu[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t rs = m0 + lr + 8 * h < M ? lr + 8 * h : M - 1 - m0;
+      ogr[h] = (uint32_t)((rs * ldgr + kx) * 2);
+      oga[h] = (uint32_t)((rs * ldga + kx) * 2);
+      oup[h] = (uint32_t)((rs * ldup + kx) * 2);
+      odg[h] = (uint32_t)((rs * lddg + kx) * 2);
+      odu[h] = (uint32_t)((rs * lddu + kx) * 2);
+    }
+    const char* grb = reinterpret_cast<const char*>(GR + m0 * ldgr);
+    const char* gab = reinterpret_cast<const char*>(GA + m0 * ldga);
+    const char* upb = reinterpret_cast<const char*>(UP + m0 * ldup);
+    char* dgb = reinterpret_cast<char*>(DG + m0 * lddg);
+    char* dub = reinterpret_cast<char*>(DU + m0 * lddu);
+    uint4 vgr[4], vga[4], vup[4], uq[2];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) vga[h] = ld16(gab, oga[h]);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      vgr[h] = ld16(grb, ogr[h]);
+      vup[h] = ld16(upb, oup[h]);
+    }
+    // dB's second operand: u^T row lane % 16, tile rows 8 (lane / 16) .. +7
+    const int64_t ur = m0 + 8 * (lane >> 4);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint16_t* ut = (q ? UTU : UTG) + (int64_t)(lane & 15) * ldut;
+      if (ur + 8 <= M) {
+        uq[q] = *reinterpret_cast<const uint4*>(ut + ur);
+      } else {
+        uint16_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ur + i < M ? ut[ur + i] : (uint16_t)0;
+        uq[q] = make_uint4((uint32_t)v[0] | ((uint32_t)v[1] << 16),
+                           (uint32_t)v[2] | ((uint32_t)v[3] << 16),
+                           (uint32_t)v[4] | ((uint32_t)v[5] << 16),
+                           (uint32_t)v[6] | ((uint32_t)v[7] << 16));
+      }
+    }
+    char* lb = lds + buf * kSlLdsBuf;
+    bool fast = true;  // one test of the tile's gate values (ql_swiglu.h)
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      float ga8[8];
+      Vec8<IT>::unpack(vga[h], ga8);
+      fast &= ql_sigmoid_fast_ok8(ga8);
+    }
+    auto rows = [&](auto fast_tag) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        float gr8[8], ga8[8], up8[8], dg8[8], du8[8];
+        Vec8<IT>::unpack(vgr[h], gr8);
+        Vec8<IT>::unpack(vga[h], ga8);
+        Vec8<IT>::unpack(vup[h], up8);
+        ql_swiglu_bwd8_as<decltype(fast_tag)::value>(gr8, ga8, up8, dg8, du8);
+        const uint4 pdg = Vec8<IT>::pack(dg8);
+        const uint4 pdu = Vec8<IT>::pack(du8);
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, pdg),
+                                    reinterpret_cast<u32x4v*>(dgb + odg[h]));
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, pdu),
+                                    reinterpret_cast<u32x4v*>(dub + odu[h]));
+        *reinterpret_cast<uint4*>(lb + lds_w + 8 * h * kSlLdsRow) = pdg;
+        *reinterpret_cast<uint4*>(lb + kSlLdsArr + lds_w + 8 * h * kSlLdsRow) = pdu;
+      }
+    };
+    if (__builtin_expect(fast, 1)) rows(std::true_type{});
+    else rows(std::false_type{});
+    // the one barrier of the tile: this tile's LDS copy is complete, and (double buffering)
+    // every wave has finished reading the copy two tiles back, which the next tile overwrites
+    __syncthreads();
+    {
+      f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int g = 0; g < kSlCols / 32; ++g) {
+        const uint4 f = *reinterpret_cast<const uint4*>(lb + qd * kSlLdsArr + lds_r +
+                                                        16 * rg * kSlLdsRow + 64 * g);
+        if (k0 + 32 * g < K) acc = mfma<IT>(yv[g], f, acc);  // wave-uniform
+      }
+      const int64_t row = m0 + 16 * rg + (lane & 15);
+      if (row < M)
+        *reinterpret_cast<float4*>(ws_du + ((int64_t)blockIdx.x * M + row) * (2 * kRank) +
+                                   kRank * qd + 4 * (lane >> 4)) =
+            make_float4(acc[0], acc[1], acc[2], acc[3]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n0 = 16 * (4 * wave + i);
+      if (k0 + n0 < K) {  // wave-uniform; K % 32 == 0: a 16-column block is all in or out
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const char* p = lb + q * kSlLdsArr + lds_t + 2 * n0;
+          const uint2 a = lds_read_tr(p);                   // rows 8 (lane / 16) + 0 .. 3
+          const uint2 b = lds_read_tr(p + 4 * kSlLdsRow);   // rows 8 (lane / 16) + 4 .. 7
+          acc_db[i][q] = mfma<IT>(make_uint4(a.x, a.y, b.x, b.y), uq[q], acc_db[i][q]);
+        }
+      }
+    }
+    buf ^= 1;
+  }
+  // lane holds dB[n = block + 4 (lane / 16) + e][c = lane % 16]
+  const int S = (int)gridDim.y;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n0 = k0 + 16 * (4 * wave + i);
+    if (n0 >= K) continue;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ws_db[(((int64_t)q * S + blockIdx.y) * K + n0 + 4 * (lane >> 4) + e) * kRank +
+              (lane & 15)] = acc_db[i][q][e];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // 8 x 8 transpose of 16-bit values: in[i] holds row i (8 columns as 4 words, column pairs);
 // out[t] holds column t (8 rows as 4 words, row pairs).
 QL_DEV void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
@@ -1075,6 +1266,82 @@ int ql_swiglu_bwd_down(int dtype, const void* GR, int64_t ldgr, const void* GA, 
   return ql_launch_status();
 }
 
+// SwiGLU backward + both rank-16 products per adapter: one workgroup per 256 columns and
+// row range, the ranges (multiples of 32 rows) chosen so the grid fills at most the two
+// workgroups per CU that fit (more leaves a short second round).
+int64_t ql_swiglu_bwd_lora_rows_per_split(int64_t M, int64_t K) {
+  const int64_t blocks = (K + kSlCols - 1) / kSlCols;
+  int64_t s = 512 / blocks;
+  if (s < 1) s = 1;
+  const int64_t rps = ((M + s - 1) / s + kSlRows - 1) / kSlRows * kSlRows;
+  return rps > 0 ? rps : kSlRows;
+}
+
+int64_t ql_swiglu_bwd_lora_ws_floats(int64_t M, int64_t K) {
+  const int64_t blocks = (K + kSlCols - 1) / kSlCols;
+  const int64_t rps = ql_swiglu_bwd_lora_rows_per_split(M, K);
+  const int64_t splits = (M + rps - 1) / rps;
+  return blocks * M * 2 * kRank + 2 * splits * K * kRank;
+}
+
+int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, int64_t ldga,
+                       const void* UP, int64_t ldup, void* DG, int64_t lddg, void* DU,
+                       int64_t lddu, int64_t M, int64_t K, const void* YG, const void* YU,
+                       int64_t ldy, const void* UTG, const void* UTU, int64_t ldut,
+                       float alpha_g, float alpha_u, float beta_g, float beta_u, void* out,
+                       int64_t ldo, int out_cols, void* out_t, int64_t ldt, float* dbg,
+                       float* dbu, float* ws, int64_t ws_floats, hipStream_t s) {
+  constexpr int NC = 2 * kRank;
+  if (M <= 0 || K <= 0 || K % 32 || out_cols < NC || ldo < out_cols) return QL_EINVAL;
+  if (out_t && ldt < M) return QL_EINVAL;
+  if (ldgr < K || ldga < K || ldup < K || lddg < K || lddu < K || ldy < K || ldut < M)
+    return QL_EINVAL;
+  // per-lane byte offsets within a tile's rows are 32-bit
+  const int64_t lim = int64_t(1) << 31;
+  if (2 * kSlRows * (ldgr > ldga ? (ldgr > ldup ? ldgr : ldup) : (ldga > ldup ? ldga : ldup)) >= lim ||
+      2 * kSlRows * (lddg > lddu ? lddg : lddu) >= lim || 32 * ldy >= lim)
+    return QL_EINVAL;
+  if (!rows16_ok(GR, ldgr) || !rows16_ok(GA, ldga) || !rows16_ok(UP, ldup) ||
+      !rows16_ok(DG, lddg) || !rows16_ok(DU, lddu) || !rows16_ok(YG, ldy) ||
+      !rows16_ok(YU, ldy) || !rows16_ok(UTG, ldut) || !rows16_ok(UTU, ldut))
+    return QL_EALIGN;
+  if (!ql_aligned(dbg, 16) || !ql_aligned(dbu, 16) || !ql_aligned(ws, 16)) return QL_EALIGN;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  if (ws_floats < ql_swiglu_bwd_lora_ws_floats(M, K)) return QL_EINVAL;
+  const int64_t blocks = (K + kSlCols - 1) / kSlCols;
+  const int64_t rps = ql_swiglu_bwd_lora_rows_per_split(M, K);
+  const int splits = (int)((M + rps - 1) / rps);
+  if (blocks > INT32_MAX || splits > 65535) return QL_ESHAPE;
+  float* ws_du = ws;
+  float* ws_db = ws + blocks * M * NC;
+  const dim3 grid((unsigned)blocks, (unsigned)splits);
+#define QL_SWL(IT)                                                                            \
+  do {                                                                                        \
+    hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT>), grid, dim3(256), 0, s,                   \
+                       (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                  \
+                       (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU, lddu,   \
+                       (const uint16_t*)YG, (const uint16_t*)YU, ldy, (const uint16_t*)UTG,   \
+                       (const uint16_t*)UTU, ldut, M, K, rps, ws_du, ws_db);                  \
+    int st = ql_launch_status();                                                              \
+    if (st != QL_OK) return st;                                                               \
+    hipLaunchKernelGGL((lora_down_reduce<IT, IT>), dim3(grid1d(M * out_cols)), dim3(256), 0,  \
+                       s, ws_du, (int)blocks, M, NC, (uint16_t*)out, ldo, out_cols, alpha_g,  \
+                       alpha_u, (uint16_t*)out_t, ldt);                                       \
+  } while (0)
+  if (dtype == QL_BF16) QL_SWL(QL_BF16);
+  else QL_SWL(QL_F16);
+#undef QL_SWL
+  int st = ql_launch_status();
+  if (st != QL_OK) return st;
+  hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s, ws_db,
+                     splits, K, kRank, dbg, beta_g, false);
+  st = ql_launch_status();
+  if (st != QL_OK) return st;
+  hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s,
+                     ws_db + (int64_t)splits * K * kRank, splits, K, kRank, dbu, beta_u, false);
+  return ql_launch_status();
+}
+
 // ---- C-ABI -------------------------------------------------------------------------------
 
 extern "C" int64_t qlora_swiglu_bwd_lora_down_workspace_size(int64_t rows, int64_t cols) {
@@ -1109,6 +1376,41 @@ extern "C" int qlora_swiglu_bwd_lora_down(
                             static_cast<hipStream_t>(stream));
 }
 
+
+extern "C" int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0 || cols % 32) return 0;
+  return ql_swiglu_bwd_lora_ws_floats(rows, cols) * (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_swiglu_bwd_lora(
+    const void* grad, int64_t ldgr, const void* gate, int64_t ldg, const void* up, int64_t ldu,
+    void* dgate, int64_t lddg, void* dup, int64_t lddu, int64_t rows, int64_t cols,
+    const void* bt_gate, const void* bt_up, int64_t ldbt, const void* ut_gate,
+    const void* ut_up, int64_t ldut, float alpha_gate, float alpha_up, float beta_gate,
+    float beta_up, int dtype, void* du, int64_t ldo, int out_cols, void* du_t, int64_t ldt,
+    float* db_gate, float* db_up, void* workspace, int64_t workspace_bytes,
+    ql_stream_t stream) {
+  if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (rows == 0) return QL_OK;
+  if (!grad || !gate || !up || !dgate || !dup || !bt_gate || !bt_up || !ut_gate || !ut_up ||
+      !du || !db_gate || !db_up || !workspace)
+    return QL_EINVAL;
+  // lanes past the last row or column recompute the last one and re-read its inputs after
+  // other lanes stored: outputs that overlap the inputs would be read back modified
+  const void* ins[3] = {grad, gate, up};
+  const int64_t in_ld[3] = {ldgr, ldg, ldu};
+  for (int i = 0; i < 3; ++i)
+    if (ql_spans_overlap(dgate, lddg, ins[i], in_ld[i], rows, cols, 2) ||
+        ql_spans_overlap(dup, lddu, ins[i], in_ld[i], rows, cols, 2))
+      return QL_EINVAL;
+  if (!ql_aligned(du, 2) || (du_t && !ql_aligned(du_t, 2))) return QL_EALIGN;
+  return ql_swiglu_bwd_lora(dtype, grad, ldgr, gate, ldg, up, ldu, dgate, lddg, dup, lddu, rows,
+                            cols, bt_gate, bt_up, ldbt, ut_gate, ut_up, ldut, alpha_gate,
+                            alpha_up, beta_gate, beta_up, du, ldo, out_cols, du_t, ldt, db_gate,
+                            db_up, static_cast<float*>(workspace),
+                            workspace_bytes / (int64_t)sizeof(float),
+                            static_cast<hipStream_t>(stream));
+}
 
 extern "C" int64_t qlora_lora_down_workspace_size(int64_t M, int64_t K, int slots) {
   if (M <= 0 || K <= 0 || slots < 1 || slots > kMaxSlots) return 0;

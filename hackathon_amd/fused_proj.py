@@ -154,10 +154,11 @@ def group_forward(x2, specs, ab):
     return y, (at, bt, ut)
 
 
-def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None):
+def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_given=None):
     """(dx or None, [dA_0, dB_0, dA_1, ...] with None where not needed) for the output
     gradient g [M, sum n_g] (row stride a multiple of 8, unit column stride). `du_dut`, when
-    given, holds the adapters' down-projections of g already (du [M, 64], du^T [16 G, M])."""
+    given, holds the adapters' down-projections of g already (du [M, 64], du^T [16 G, M]);
+    `db_given`, the lora_B gradients [dB_0, dB_1, ..] already computed."""
     dt = x2.dtype
     dev = x2.device
     M, K = x2.shape
@@ -188,8 +189,8 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None):
         if need_ab[2 * i]:
             da = da_all[16 * i:16 * i + 16]
         if need_ab[2 * i + 1]:
-            db = _gemm.lora_wgrad(ut[16 * i:16 * i + 16], g[:, offs[i]:offs[i + 1]],
-                                  alpha=s.scaling)
+            db = db_given[i] if db_given is not None else _gemm.lora_wgrad(
+                ut[16 * i:16 * i + 16], g[:, offs[i]:offs[i + 1]], alpha=s.scaling)
         grads += [da, db]
     return dx, grads
 
@@ -280,20 +281,29 @@ class GateUpSwiGLU(torch.autograd.Function):
         if dh2.stride(-1) != 1 or dh2.stride(0) % 8 or dh2.data_ptr() % 16:
             dh2 = dh2.contiguous()
         g = torch.empty((M, 2 * n), dtype=x2.dtype, device=x2.device)
-        du_dut = None
+        du_dut = db_given = None
+        need_ab = ctx.needs_input_grad[2:]
         if n % 32 == 0:
             # the SwiGLU gradients and, in the same pass, du_gate = s dgate B_gate and
-            # du_up = s dup B_up (the gradients are not read back for the down-projections)
+            # du_up = s dup B_up, plus (when wanted) both lora_B gradients s dgate^T u_gate and
+            # s dup^T u_up: the gradients are not read back from HBM for any of them
             du = torch.empty((M, _PAD), dtype=x2.dtype, device=x2.device)
             dut = _t_buffer(32, M, x2.dtype, x2.device)
             gate_s, up_s = ctx.specs
-            swiglu.swiglu_bwd_lora_down(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:, :n],
-                                        bt[:, n:], gate_s.scaling, up_s.scaling, du, dut)
+            if need_ab[1] or need_ab[3]:
+                db_given = swiglu.swiglu_bwd_lora(
+                    dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:, :n], bt[:, n:], ut[:16],
+                    ut[16:32], gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du,
+                    dut)
+            else:
+                swiglu.swiglu_bwd_lora_down(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:],
+                                            bt[:, :n], bt[:, n:], gate_s.scaling, up_s.scaling,
+                                            du, dut)
             du_dut = (du, dut)
         else:
             swiglu.swiglu_bwd_rows(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:])
         dx, grads = group_backward(g, x2, at, bt, ut, ctx.specs, ctx.needs_input_grad[0],
-                                   ctx.needs_input_grad[2:], du_dut=du_dut)
+                                   need_ab, du_dut=du_dut, db_given=db_given)
         grads = [None if gr is None else gr.to(t) for gr, t in zip(grads, ctx.ab_dtypes)]
         return (None if dx is None else dx.view(ctx.shape)), None, *grads
 

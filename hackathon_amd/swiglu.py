@@ -84,6 +84,35 @@ def swiglu_bwd_lora_down(grad, gate, up, dgate, dup, bt_gate, bt_up, alpha_gate,
               _lib.stream_of(gate))
 
 
+def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, alpha_gate,
+                    alpha_up, beta_gate, beta_up, du, du_t=None):
+    """swiglu_bwd_lora_down plus both adapters' lora_B gradients in the same pass
+    (qlora_swiglu_bwd_lora): returns fp32 (db_gate, db_up) [cols, 16] with
+    db_gate = beta_gate dgate^T ut_gate^T and db_up = beta_up dup^T ut_up^T, where ut_* [16, rows]
+    are the adapters' down-projections of the forward input, transposed."""
+    _lib.require_rows(gate.dtype, grad=grad, gate=gate, up=up, dgate=dgate, dup=dup,
+                      bt_gate=bt_gate, bt_up=bt_up, ut_gate=ut_gate, ut_up=ut_up, du=du,
+                      du_t=du_t)
+    rows, cols = gate.shape
+    if bt_up.stride(0) != bt_gate.stride(0):
+        raise ValueError("bt_gate and bt_up must share a row stride (slices of one B^T buffer)")
+    if ut_up.stride(0) != ut_gate.stride(0):
+        raise ValueError("ut_gate and ut_up must share a row stride (slices of one u^T buffer)")
+    db_gate = torch.empty((cols, 16), dtype=torch.float32, device=gate.device)
+    db_up = torch.empty((cols, 16), dtype=torch.float32, device=gate.device)
+    ws, ws_bytes = _lib.workspace("qlora_swiglu_bwd_lora_workspace_size", rows, cols,
+                                  device=gate.device)
+    _lib.call("qlora_swiglu_bwd_lora", grad.data_ptr(), grad.stride(0), gate.data_ptr(),
+              gate.stride(0), up.data_ptr(), up.stride(0), dgate.data_ptr(), dgate.stride(0),
+              dup.data_ptr(), dup.stride(0), rows, cols, bt_gate.data_ptr(), bt_up.data_ptr(),
+              bt_gate.stride(0), ut_gate.data_ptr(), ut_up.data_ptr(), ut_gate.stride(0),
+              float(alpha_gate), float(alpha_up), float(beta_gate), float(beta_up),
+              _lib.tag(gate.dtype), du.data_ptr(), du.stride(0), du.shape[1], _lib.ptr(du_t),
+              du_t.stride(0) if du_t is not None else 0, db_gate.data_ptr(), db_up.data_ptr(),
+              _lib.ptr(ws), ws_bytes, _lib.stream_of(gate))
+    return db_gate, db_up
+
+
 def patch_qwen2_mlp():
     """Send Qwen2MLP.forward through the fused kernel for GPU inputs (solution/swiglu.py:68-81)."""
     from transformers.models.qwen2 import modeling_qwen2

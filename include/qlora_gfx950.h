@@ -401,6 +401,33 @@ int qlora_swiglu_bwd_lora_down(const void* grad, int64_t ldgr, const void* gate,
                                ql_stream_t stream);
 
 /*
+ * qlora_swiglu_bwd_lora_down plus both adapters' lora_B gradients in the same pass:
+ *   dgate, dup, du, du_t = as qlora_swiglu_bwd_lora_down (du summed in another order: within
+ *                          fp32 rounding of it, not bit for bit)
+ *   db_gate[k, c] = beta_gate * sum_m dgate[m, k] * ut_gate[c, m]    fp32 [cols, 16]
+ *   db_up[k, c]   = beta_up   * sum_m dup[m, k]   * ut_up[c, m]
+ * ut_gate / ut_up [16, rows] (ld ldut >= rows, a multiple of 8) are the adapters'
+ * down-projections of the forward input, transposed (u^T of y = base + s B (A x)), so
+ * db = s (dY)^T u is the lora_B gradient. Each workgroup owns 256 columns and a range of rows,
+ * keeps the tile's gradients on chip for both products and writes fp32 partials: the two
+ * gradients are never read back from HBM. The workspace (16-B aligned, at least
+ * qlora_swiglu_bwd_lora_workspace_size bytes) is required (QL_EINVAL without it); db_gate and
+ * db_up are 16-B aligned. Other rules as qlora_swiglu_bwd_lora_down.
+ * Replaces: solution/swiglu.py:25-37 (the SwiGLU backward) and the lora_B autograd backward
+ * of solution/lora.py:172 for the gate and up projections (both the down-projection of the
+ * output gradient and the weight gradient of B).
+ */
+int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols);
+int qlora_swiglu_bwd_lora(const void* grad, int64_t ldgr, const void* gate, int64_t ldg,
+                          const void* up, int64_t ldu, void* dgate, int64_t lddg, void* dup,
+                          int64_t lddu, int64_t rows, int64_t cols, const void* bt_gate,
+                          const void* bt_up, int64_t ldbt, const void* ut_gate,
+                          const void* ut_up, int64_t ldut, float alpha_gate, float alpha_up,
+                          float beta_gate, float beta_up, int dtype, void* du, int64_t ldo,
+                          int out_cols, void* du_t, int64_t ldt, float* db_gate, float* db_up,
+                          void* workspace, int64_t workspace_bytes, ql_stream_t stream);
+
+/*
  * The compute-dtype operands of one rank-16 adapter, from its fp32 factors A [16, K] and
  * B [N, 16], in one launch (K % 8 == 0, pad >= 16):
  *   a16 [16, K] = A;  at_pad [K, pad] = A^T | 0;  bs_pad [N, pad] = scaling * B | 0;

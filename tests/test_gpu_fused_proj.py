@@ -206,3 +206,52 @@ def test_swiglu_bwd_lora_down(rows, cols, dtype):
         assert torch.all((got - exact).abs() <= bound), q
     assert torch.all(du[:, 32:] == 0)
     assert torch.equal(dut, du[:, :32].t())
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(4096, 18944, torch.bfloat16),
+                                             (37, 1024, torch.bfloat16),
+                                             (300, 96, torch.bfloat16),
+                                             (1000, 2048, torch.float16),
+                                             (4000, 4832, torch.bfloat16)])
+def test_swiglu_bwd_lora(rows, cols, dtype):
+    """qlora_swiglu_bwd_lora: the gradient bits of qlora_swiglu_bwd_rows, the two scaled
+    down-projections of them (fp32 accumulation bound vs fp64, zeros after column 32, the
+    transposed copy exactly) and both lora_B gradients beta d^T u^T (fp32 accumulation bound
+    vs fp64). Row counts that are not a multiple of 32 leave rows of the last tile past M,
+    which must not reach either product; 96 and 4832 columns leave a partial last block of
+    256 columns."""
+    print(f"swiglu_bwd_lora {rows}x{cols} {dtype}", flush=True)
+    from hackathon_amd import gemm
+
+    g = torch.Generator(device="cuda").manual_seed(3 * rows + cols)
+    y = torch.randn(rows, 2 * cols, device="cuda", generator=g).to(dtype)
+    gate, up = y[:, :cols], y[:, cols:]
+    dh = torch.randn(rows, cols, device="cuda", generator=g).to(dtype)
+    bt = (torch.randn(16, 2 * cols, device="cuda", generator=g) * 0.1).to(dtype)
+    ut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+    ut.copy_(torch.randn(32, rows, device="cuda", generator=g).to(dtype))
+    buf = torch.empty(rows, 2 * cols, dtype=dtype, device="cuda")
+    du = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
+    dut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+    db_gate, db_up = swiglu.swiglu_bwd_lora(dh, gate, up, buf[:, :cols], buf[:, cols:],
+                                            bt[:, :cols], bt[:, cols:], ut[:16], ut[16:32],
+                                            2.0, 0.5, 2.0, 0.5, du, dut)
+    ref = torch.empty_like(buf)
+    swiglu.swiglu_bwd_rows(dh, gate, up, ref[:, :cols], ref[:, cols:])
+    assert torch.equal(buf, ref)
+    u = ut.double()
+    for q, (c0, a, db) in enumerate(((0, 2.0, db_gate), (cols, 0.5, db_up))):
+        x = ref[:, c0:c0 + cols].double()
+        w = bt[:, c0:c0 + cols].double()
+        exact = a * (x @ w.t())
+        rnd = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11  # one rounding to the output
+        bound = a * 4 * 2.0**-22 * cols * x.abs().max() * w.abs().max() + rnd * exact.abs()
+        got = du[:, 16 * q:16 * q + 16].double()
+        assert torch.all((got - exact).abs() <= bound), q
+        uq = u[16 * q:16 * q + 16]
+        exact_b = a * (x.t() @ uq.t())
+        bound_b = a * 4 * 2.0**-22 * rows * x.abs().max() * uq.abs().max()
+        assert db.shape == (cols, 16) and db.dtype == torch.float32
+        assert torch.all((db.double() - exact_b).abs() <= bound_b), q
+    assert torch.all(du[:, 32:] == 0)
+    assert torch.equal(dut, du[:, :32].t())
