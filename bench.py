@@ -427,6 +427,27 @@ def bench_swiglu(torch, res):
                                dlo, dlo_t)
     _rate("swiglu_bwd_lora_4096x18944", _graph_time([fused_db] * 10, torch, replays=3),
           5 * 2 * n + 2 * 32 * N + 2 * 32 * M + 2 * (M * 64 + 32 * M) + 2 * 4 * 16 * N, res)
+    # ... and with the down adapter's lora_A gradient du_d^T h too (h recomputed on chip): plus
+    # du_d^T (0.1 MB) and the fp32 [16, 18944] gradient (1.2 MB)
+    udt = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=16)
+    udt.copy_(torch.randn(16, M, device="cuda", generator=g).to(torch.bfloat16))
+
+    def fused_da():
+        swiglu.swiglu_bwd_lora(*views, bt[:16], bt[16:], ut[:16], ut[16:32], 1.0, 1.0, 1.0, 1.0,
+                               dlo, dlo_t, ud_t=udt)
+    _rate("swiglu_bwd_lora_da_4096x18944", _graph_time([fused_da] * 10, torch, replays=3),
+          5 * 2 * n + 2 * 32 * N + 2 * 48 * M + 2 * (M * 64 + 32 * M) + 3 * 4 * 16 * N, res)
+    # the forward fused with the down adapter's u = h A^T: the SwiGLU forward's 465.6 MB plus A
+    # (0.6 MB) and u, u^T (0.7 MB)
+    a16 = (torch.randn(16, N, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    u16 = torch.empty(M, 64, device="cuda", dtype=torch.bfloat16)
+    u16_t = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=16)
+    hv = dg.view(M, N)
+
+    def fused_fwd():
+        swiglu.swiglu_fwd_lora_down(views[1], views[2], hv, a16, u16, u16_t)
+    _rate("swiglu_fwd_lora_down_4096x18944", _graph_time([fused_fwd] * 10, torch, replays=3),
+          3 * 2 * n + 2 * 16 * N + 2 * (M * 64 + 16 * M), res)
 
 
 def bench_gemms(torch, res):

@@ -50,8 +50,11 @@ _SIGNATURES = {
     "qlora_swiglu_bwd_lora": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
                               _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_ptr,
                               _c_ptr, _c_i64, _c_f32, _c_f32, _c_f32, _c_f32, _c_int, _c_ptr,
-                              _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64,
-                              _c_ptr],
+                              _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_f32,
+                              _c_ptr, _c_ptr, _c_i64, _c_ptr],
+    "qlora_swiglu_fwd_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64,
+                                   _c_i64, _c_ptr, _c_i64, _c_f32, _c_int, _c_ptr, _c_i64, _c_int,
+                                   _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_dropout_scale": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64,
                                  _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_scaled_add": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,
@@ -106,7 +109,8 @@ _SIZE_QUERIES = {
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_swiglu_bwd_lora_down_workspace_size": [_c_i64, _c_i64],
-    "qlora_swiglu_bwd_lora_workspace_size": [_c_i64, _c_i64],
+    "qlora_swiglu_bwd_lora_workspace_size": [_c_i64, _c_i64, _c_int],
+    "qlora_swiglu_fwd_lora_down_workspace_size": [_c_i64, _c_i64],
     "qlora_nf4_quantize_workspace_size": [_c_i64, _c_int, _c_int],
     "qlora_attn_bwd_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64],
     "qlora_adamw_chunk_elems": [],

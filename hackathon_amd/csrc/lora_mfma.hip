@@ -513,6 +513,12 @@ __global__ __launch_bounds__(256) void swiglu_bwd_down_kernel(
 //    in order by lora_wgrad_reduce.
 // So the gradients are never read back from HBM for either product; the extra traffic is the
 // fp32 partials (M x 32 per column block, K x 32 per row range).
+// DA: also the lora_A gradient of the next layer's adapter, whose input was h = silu(gate) up:
+//   dA^T[k, c] = sum_m h[m, k] ud[m, c]   (ud = that adapter's du, given as ud^T [16, M])
+// with h recomputed in registers (the bits of the forward) into a third LDS array and read
+// transposed like the gradients. The three arrays take one LDS buffer (with a second barrier
+// per tile before it is refilled) and the Y fragments move from registers to LDS, so two
+// workgroups (at most 256 registers a lane) still fit on a CU.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
@@ -530,16 +536,23 @@ constexpr int kSlLdsRow = 2 * kSlCols + 16;          // bytes per LDS row (16 B 
 constexpr int kSlLdsArr = kSlRows * kSlLdsRow;       // one gradient's tile
 constexpr int kSlLdsBuf = 2 * kSlLdsArr;             // dgate + dup
 
-template <int IT>
-__global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
+template <int IT, bool DA>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void swiglu_bwd_lora_kernel(
     const uint16_t* __restrict__ GR, int64_t ldgr, const uint16_t* __restrict__ GA,
     int64_t ldga, const uint16_t* __restrict__ UP, int64_t ldup, uint16_t* __restrict__ DG,
     int64_t lddg, uint16_t* __restrict__ DU, int64_t lddu, const uint16_t* __restrict__ YG,
     const uint16_t* __restrict__ YU, int64_t ldy, const uint16_t* __restrict__ UTG,
     const uint16_t* __restrict__ UTU, int64_t ldut, int64_t M, int64_t K,
-    int64_t rows_per_split, float* __restrict__ ws_du, float* __restrict__ ws_db) {
+    int64_t rows_per_split, float* __restrict__ ws_du, float* __restrict__ ws_db,
+    const uint16_t* __restrict__ UTD, float* __restrict__ ws_da) {
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-  __shared__ __attribute__((aligned(16))) char lds[2 * kSlLdsBuf];
+  constexpr int NA = DA ? 3 : 2;          // LDS arrays per tile: dgate, dup (, h)
+  constexpr int NBUF = DA ? 1 : 2;        // tiles in LDS
+  constexpr int BUF = NA * kSlLdsArr;
+  // DA: the Y fragments live in LDS (16 rows of 256 columns per adapter, rows padded like the
+  // tiles), not in registers, which keeps the kernel at two waves per SIMD
+  constexpr int YBYTES = DA ? 2 * 16 * kSlLdsRow : 0;
+  __shared__ __attribute__((aligned(16))) char lds[NBUF * BUF + YBYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t k0 = (int64_t)blockIdx.x * kSlCols;
@@ -549,8 +562,19 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
   // this thread's 16-B chunk: columns past K (the last block) recompute the block's first
   const int64_t kx = k0 + 8 * c < K ? k0 + 8 * c : k0;
   const int rg = wave >> 1, qd = wave & 1;  // du: row group and adapter of this wave
-  uint4 yv[kSlCols / 32];
-  {
+  uint4 yv[DA ? 1 : kSlCols / 32];
+  char* const ylds = lds + NBUF * BUF;
+  if constexpr (DA) {  // thread t: rows t / 32 and t / 32 + 8 of both Y, 16 B at column 8 (t % 32)
+    const int64_t col = k0 + 8 * c < K ? k0 + 8 * c : k0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = lr + 8 * i;
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+        *reinterpret_cast<uint4*>(ylds + (a * 16 + r) * kSlLdsRow + 16 * c) =
+            *reinterpret_cast<const uint4*>((a ? YU : YG) + (int64_t)r * ldy + col);
+    }
+  } else {
     const uint16_t* yq = qd ? YU : YG;
     const uint32_t oy = (uint32_t)(((lane & 15) * ldy + 8 * (lane >> 4)) * 2);
 #pragma unroll
@@ -559,9 +583,11 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
       yv[g] = ld16(reinterpret_cast<const char*>(yq + (kg < K ? kg : k0)), oy);
     }
   }
-  f32x4_t acc_db[4][2];  // [column block 4 wave + i][adapter]
+  f32x4_t acc_db[4][NA];  // [column block 4 wave + i][adapter (, dA)]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc_db[i][0] = acc_db[i][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int q = 0; q < NA; ++q) acc_db[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int lds_w = lr * kSlLdsRow + 16 * c;                            // + 8 h rows
   const int lds_r = (lane & 15) * kSlLdsRow + 16 * (lane >> 4);         // + 16 rg rows + 64 g
   const int lds_t = (8 * (lane >> 4) + ((lane >> 2) & 3)) * kSlLdsRow + 8 * (lane & 3);
@@ -584,7 +610,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
     const char* upb = reinterpret_cast<const char*>(UP + m0 * ldup);
     char* dgb = reinterpret_cast<char*>(DG + m0 * lddg);
     char* dub = reinterpret_cast<char*>(DU + m0 * lddu);
-    uint4 vgr[4], vga[4], vup[4], uq[2];
+    uint4 vgr[4], vga[4], vup[4], uq[NA];
 #pragma unroll
     for (int h = 0; h < 4; ++h) vga[h] = ld16(gab, oga[h]);
 #pragma unroll
@@ -592,11 +618,11 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
       vgr[h] = ld16(grb, ogr[h]);
       vup[h] = ld16(upb, oup[h]);
     }
-    // dB's second operand: u^T row lane % 16, tile rows 8 (lane / 16) .. +7
+    // dB's (and dA's) second operand: u^T row lane % 16, tile rows 8 (lane / 16) .. +7
     const int64_t ur = m0 + 8 * (lane >> 4);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint16_t* ut = (q ? UTU : UTG) + (int64_t)(lane & 15) * ldut;
+    for (int q = 0; q < NA; ++q) {
+      const uint16_t* ut = (q == 2 ? UTD : q ? UTU : UTG) + (int64_t)(lane & 15) * ldut;
       if (ur + 8 <= M) {
         uq[q] = *reinterpret_cast<const uint4*>(ut + ur);
       } else {
@@ -609,7 +635,8 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
                            (uint32_t)v[6] | ((uint32_t)v[7] << 16));
       }
     }
-    char* lb = lds + buf * kSlLdsBuf;
+    char* lb = lds + buf * BUF;
+    if (NBUF == 1 && m0 != r0) __syncthreads();  // the previous tile's reads are done
     bool fast = true;  // one test of the tile's gate values (ql_swiglu.h)
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -633,12 +660,18 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
                                     reinterpret_cast<u32x4v*>(dub + odu[h]));
         *reinterpret_cast<uint4*>(lb + lds_w + 8 * h * kSlLdsRow) = pdg;
         *reinterpret_cast<uint4*>(lb + kSlLdsArr + lds_w + 8 * h * kSlLdsRow) = pdu;
+        if constexpr (DA) {
+          float h8[8];
+          ql_swiglu_fwd8_as<decltype(fast_tag)::value>(ga8, up8, h8);
+          *reinterpret_cast<uint4*>(lb + 2 * kSlLdsArr + lds_w + 8 * h * kSlLdsRow) =
+              Vec8<IT>::pack(h8);
+        }
       }
     };
     if (__builtin_expect(fast, 1)) rows(std::true_type{});
     else rows(std::false_type{});
-    // the one barrier of the tile: this tile's LDS copy is complete, and (double buffering)
-    // every wave has finished reading the copy two tiles back, which the next tile overwrites
+    // this tile's LDS copy is complete; with two buffers, every wave has also finished
+    // reading the copy two tiles back, which the next tile overwrites
     __syncthreads();
     {
       f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -646,7 +679,13 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
       for (int g = 0; g < kSlCols / 32; ++g) {
         const uint4 f = *reinterpret_cast<const uint4*>(lb + qd * kSlLdsArr + lds_r +
                                                         16 * rg * kSlLdsRow + 64 * g);
-        if (k0 + 32 * g < K) acc = mfma<IT>(yv[g], f, acc);  // wave-uniform
+        uint4 y;
+        if constexpr (DA)
+          y = *reinterpret_cast<const uint4*>(ylds + (qd * 16 + (lane & 15)) * kSlLdsRow +
+                                              64 * g + 16 * (lane >> 4));
+        else
+          y = yv[g];
+        if (k0 + 32 * g < K) acc = mfma<IT>(y, f, acc);  // wave-uniform
       }
       const int64_t row = m0 + 16 * rg + (lane & 15);
       if (row < M)
@@ -659,7 +698,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
       const int n0 = 16 * (4 * wave + i);
       if (k0 + n0 < K) {  // wave-uniform; K % 32 == 0: a 16-column block is all in or out
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < NA; ++q) {
           const char* p = lb + q * kSlLdsArr + lds_t + 2 * n0;
           const uint2 a = lds_read_tr(p);                   // rows 8 (lane / 16) + 0 .. 3
           const uint2 b = lds_read_tr(p + 4 * kSlLdsRow);   // rows 8 (lane / 16) + 4 .. 7
@@ -667,7 +706,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
         }
       }
     }
-    buf ^= 1;
+    if (NBUF == 2) buf ^= 1;
   }
   // lane holds dB[n = block + 4 (lane / 16) + e][c = lane % 16]
   const int S = (int)gridDim.y;
@@ -681,6 +720,145 @@ __global__ __launch_bounds__(256) void swiglu_bwd_lora_kernel(
       for (int e = 0; e < 4; ++e)
         ws_db[(((int64_t)q * S + blockIdx.y) * K + n0 + 4 * (lane >> 4) + e) * kRank +
               (lane & 15)] = acc_db[i][q][e];
+    if constexpr (DA) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ws_da[((int64_t)blockIdx.y * K + n0 + 4 * (lane >> 4) + e) * kRank + (lane & 15)] =
+            acc_db[i][2][e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// SwiGLU forward fused with the down-projection of its output by the next layer's adapter
+// (the down projection of a LoRA MLP):
+//   h        = silu(gate) * up             stored, the bits of qlora_swiglu_fwd_rows
+//   out[m, c] = alpha * sum_k h[m, k] Y[c, k]   c < 16 (Y = that adapter's A [16, K])
+// The same streaming tile walk as swiglu_bwd_down_kernel (32 x 256 tiles of a row block over
+// a K range, one LDS copy of each tile, one barrier per tile), with two inputs, one output and
+// one product: wave w multiplies k groups 2w and 2w + 1 of both row groups by Y's fragments
+// (from L2, each serving both row groups), and the waves' sums meet in LDS at the end.
+template <int IT, bool PARTIAL>
+__global__ __launch_bounds__(256) void swiglu_fwd_down_kernel(
+    const uint16_t* __restrict__ GA, int64_t ldga, const uint16_t* __restrict__ UP,
+    int64_t ldup, uint16_t* __restrict__ HH, int64_t ldh, const uint16_t* __restrict__ Y,
+    int64_t ldy, int64_t M, int64_t K, int64_t k_per_split, float* __restrict__ ws,
+    uint16_t* __restrict__ out, int64_t ldo, int out_cols, float alpha,
+    uint16_t* __restrict__ out_t, int64_t ldt) {
+  constexpr int RG = kSwRows / 16;
+  constexpr int H = kSwRows / 8;
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  static_assert(kSwLdsBuf >= RG * 4 * 64 * 16, "the wave reduction reuses the tiles");
+  __shared__ __attribute__((aligned(16))) char lds[2 * kSwLdsArr];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t m0 = (int64_t)blockIdx.x * kSwRows;
+  const int64_t kb = (int64_t)blockIdx.y * k_per_split;
+  const int64_t ke = kb + k_per_split < K ? kb + k_per_split : K;
+  const int lr = tid >> 5, c = tid & 31;
+  // rows m0 + lr + 8 h; a row past M works on row M - 1 and stores the bits its owner stores
+  const char* gab = reinterpret_cast<const char*>(GA + m0 * ldga);
+  const char* upb = reinterpret_cast<const char*>(UP + m0 * ldup);
+  char* hb = reinterpret_cast<char*>(HH + m0 * ldh);
+  uint32_t oga[H], oup[H], oh[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const int64_t row = m0 + lr + 8 * h;
+    const int64_t rs = (row < M ? row : M - 1) - m0;
+    oga[h] = (uint32_t)(rs * ldga * 2);
+    oup[h] = (uint32_t)(rs * ldup * 2);
+    oh[h] = (uint32_t)(rs * ldh * 2);
+  }
+  const uint32_t oy = (uint32_t)(((lane & 15) * ldy + 8 * (lane >> 4)) * 2);
+  const int lds_w = lr * kSwLdsRow + 16 * c;
+  const int lds_r = (lane & 15) * kSwLdsRow + 16 * (lane >> 4);
+  f32x4_t acc[RG][2];  // [row group][k group parity]
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) acc[rg][0] = acc[rg][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int buf = 0;
+  for (int64_t k0 = kb; k0 < ke; k0 += kSwK) {
+    // chunks and 32-k groups past ke read the chunk / group at k0: recomputed and stored with
+    // the same bits, and left out of the products
+    const int64_t kx = k0 + 8 * c < ke ? k0 + 8 * c : k0;
+    const uint32_t kxb = (uint32_t)(2 * kx);
+    uint4 vga[H], vup[H], yv[2];
+#pragma unroll
+    for (int h = 0; h < H; ++h) vga[h] = ld16(gab, oga[h] + kxb);
+#pragma unroll
+    for (int h = 0; h < H; ++h) vup[h] = ld16(upb, oup[h] + kxb);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int64_t kg = k0 + 32 * (2 * wave + gi);
+      yv[gi] = ld16(reinterpret_cast<const char*>(Y) + 2 * (kg < ke ? kg : k0), oy);
+    }
+    char* lb = lds + buf * kSwLdsArr;
+    bool fast = true;  // one test of the tile's gate values (ql_swiglu.h)
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      float ga8[8];
+      Vec8<IT>::unpack(vga[h], ga8);
+      fast &= ql_sigmoid_fast_ok8(ga8);
+    }
+    auto rows = [&](auto fast_tag) {
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        float ga8[8], up8[8], h8[8];
+        Vec8<IT>::unpack(vga[h], ga8);
+        Vec8<IT>::unpack(vup[h], up8);
+        ql_swiglu_fwd8_as<decltype(fast_tag)::value>(ga8, up8, h8);
+        const uint4 ph = Vec8<IT>::pack(h8);
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, ph),
+                                    reinterpret_cast<u32x4v*>(hb + oh[h] + kxb));
+        *reinterpret_cast<uint4*>(lb + lds_w + 8 * h * kSwLdsRow) = ph;
+      }
+    };
+    if (__builtin_expect(fast, 1)) rows(std::true_type{});
+    else rows(std::false_type{});
+    __syncthreads();
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        const uint4 f = *reinterpret_cast<const uint4*>(lb + lds_r + 16 * rg * kSwLdsRow +
+                                                        64 * (2 * wave + gi));
+        if (k0 + 32 * (2 * wave + gi) < ke) acc[rg][gi] = mfma<IT>(yv[gi], f, acc[rg][gi]);
+      }
+    }
+    buf ^= 1;
+  }
+  // sum over the waves in wave order through LDS; wave rg < RG finishes row group rg
+  __syncthreads();
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) red[(rg * 4 + wave) * 64 + lane] = acc[rg][0] + acc[rg][1];
+  __syncthreads();
+  const int cc = 4 * (lane >> 4);
+  if (wave < RG) {
+    const int64_t row = m0 + 16 * wave + (lane & 15);
+    if (row < M) {
+      f32x4_t sum = red[(wave * 4) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) sum += red[(wave * 4 + w) * 64 + lane];
+      if constexpr (PARTIAL) {
+        *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * kRank + cc) =
+            make_float4(sum[0], sum[1], sum[2], sum[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint16_t v = Elem<IT>::from_f32(alpha * sum[e]);
+          out[row * ldo + cc + e] = v;
+          if (out_t) out_t[(int64_t)(cc + e) * ldt + row] = v;
+        }
+      }
+    }
+  }
+  if constexpr (!PARTIAL) {
+    const int64_t row = m0 + 16 * (3 - wave) + (lane & 15);  // waves 2, 3: the zero columns
+    if (wave >= 4 - RG && row < M)
+      for (int zc = kRank + cc; zc < out_cols; zc += 16)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (zc + e < out_cols) out[row * ldo + zc + e] = Elem<IT>::from_f32(0.f);
   }
 }
 
@@ -1277,11 +1455,11 @@ int64_t ql_swiglu_bwd_lora_rows_per_split(int64_t M, int64_t K) {
   return rps > 0 ? rps : kSlRows;
 }
 
-int64_t ql_swiglu_bwd_lora_ws_floats(int64_t M, int64_t K) {
+int64_t ql_swiglu_bwd_lora_ws_floats(int64_t M, int64_t K, bool da) {
   const int64_t blocks = (K + kSlCols - 1) / kSlCols;
   const int64_t rps = ql_swiglu_bwd_lora_rows_per_split(M, K);
   const int64_t splits = (M + rps - 1) / rps;
-  return blocks * M * 2 * kRank + 2 * splits * K * kRank;
+  return blocks * M * 2 * kRank + (da ? 3 : 2) * splits * K * kRank;
 }
 
 int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, int64_t ldga,
@@ -1290,8 +1468,10 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
                        int64_t ldy, const void* UTG, const void* UTU, int64_t ldut,
                        float alpha_g, float alpha_u, float beta_g, float beta_u, void* out,
                        int64_t ldo, int out_cols, void* out_t, int64_t ldt, float* dbg,
-                       float* dbu, float* ws, int64_t ws_floats, hipStream_t s) {
+                       float* dbu, const void* UTD, float beta_d, float* dad, float* ws,
+                       int64_t ws_floats, hipStream_t s) {
   constexpr int NC = 2 * kRank;
+  const bool da = UTD != nullptr;
   if (M <= 0 || K <= 0 || K % 32 || out_cols < NC || ldo < out_cols) return QL_EINVAL;
   if (out_t && ldt < M) return QL_EINVAL;
   if (ldgr < K || ldga < K || ldup < K || lddg < K || lddu < K || ldy < K || ldut < M)
@@ -1303,25 +1483,38 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
     return QL_EINVAL;
   if (!rows16_ok(GR, ldgr) || !rows16_ok(GA, ldga) || !rows16_ok(UP, ldup) ||
       !rows16_ok(DG, lddg) || !rows16_ok(DU, lddu) || !rows16_ok(YG, ldy) ||
-      !rows16_ok(YU, ldy) || !rows16_ok(UTG, ldut) || !rows16_ok(UTU, ldut))
+      !rows16_ok(YU, ldy) || !rows16_ok(UTG, ldut) || !rows16_ok(UTU, ldut) ||
+      (da && !rows16_ok(UTD, ldut)))
     return QL_EALIGN;
-  if (!ql_aligned(dbg, 16) || !ql_aligned(dbu, 16) || !ql_aligned(ws, 16)) return QL_EALIGN;
+  if (!ql_aligned(dbg, 16) || !ql_aligned(dbu, 16) || !ql_aligned(ws, 16) ||
+      (da && !ql_aligned(dad, 16)))
+    return QL_EALIGN;
   if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
-  if (ws_floats < ql_swiglu_bwd_lora_ws_floats(M, K)) return QL_EINVAL;
+  if (ws_floats < ql_swiglu_bwd_lora_ws_floats(M, K, da)) return QL_EINVAL;
   const int64_t blocks = (K + kSlCols - 1) / kSlCols;
   const int64_t rps = ql_swiglu_bwd_lora_rows_per_split(M, K);
   const int splits = (int)((M + rps - 1) / rps);
   if (blocks > INT32_MAX || splits > 65535) return QL_ESHAPE;
   float* ws_du = ws;
   float* ws_db = ws + blocks * M * NC;
+  float* ws_da = ws_db + 2 * (int64_t)splits * K * kRank;
   const dim3 grid((unsigned)blocks, (unsigned)splits);
 #define QL_SWL(IT)                                                                            \
   do {                                                                                        \
-    hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT>), grid, dim3(256), 0, s,                   \
-                       (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                  \
-                       (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU, lddu,   \
-                       (const uint16_t*)YG, (const uint16_t*)YU, ldy, (const uint16_t*)UTG,   \
-                       (const uint16_t*)UTU, ldut, M, K, rps, ws_du, ws_db);                  \
+    if (da)                                                                                   \
+      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, true>), grid, dim3(256), 0, s,           \
+                         (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                \
+                         (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU,       \
+                         lddu, (const uint16_t*)YG, (const uint16_t*)YU, ldy,                 \
+                         (const uint16_t*)UTG, (const uint16_t*)UTU, ldut, M, K, rps, ws_du,  \
+                         ws_db, (const uint16_t*)UTD, ws_da);                                 \
+    else                                                                                      \
+      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, false>), grid, dim3(256), 0, s,          \
+                         (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                \
+                         (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU,       \
+                         lddu, (const uint16_t*)YG, (const uint16_t*)YU, ldy,                 \
+                         (const uint16_t*)UTG, (const uint16_t*)UTU, ldut, M, K, rps, ws_du,  \
+                         ws_db, (const uint16_t*)nullptr, (float*)nullptr);                   \
     int st = ql_launch_status();                                                              \
     if (st != QL_OK) return st;                                                               \
     hipLaunchKernelGGL((lora_down_reduce<IT, IT>), dim3(grid1d(M * out_cols)), dim3(256), 0,  \
@@ -1339,6 +1532,54 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
   if (st != QL_OK) return st;
   hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s,
                      ws_db + (int64_t)splits * K * kRank, splits, K, kRank, dbu, beta_u, false);
+  if (!da) return ql_launch_status();
+  st = ql_launch_status();
+  if (st != QL_OK) return st;
+  hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s, ws_da,
+                     splits, K, kRank, dad, beta_d, true);  // [16, K]: A's layout
+  return ql_launch_status();
+}
+
+// SwiGLU forward + the down-projection of h: the backward_down tile walk and split rule.
+int ql_swiglu_fwd_down(int dtype, const void* GA, int64_t ldga, const void* UP, int64_t ldup,
+                       void* HH, int64_t ldh, int64_t M, int64_t K, const void* Y, int64_t ldy,
+                       float alpha, void* out, int64_t ldo, int out_cols, void* out_t,
+                       int64_t ldt, float* ws, int64_t ws_floats, hipStream_t s) {
+  if (M <= 0 || K <= 0 || K % 32 || out_cols < kRank || ldo < out_cols) return QL_EINVAL;
+  if (out_t && ldt < M) return QL_EINVAL;
+  if (ldga < K || ldup < K || ldh < K || ldy < K) return QL_EINVAL;
+  const int64_t lim = int64_t(1) << 31;
+  if (2 * kSwRows * (ldga > ldup ? ldga : ldup) >= lim || 2 * kSwRows * ldh >= lim ||
+      32 * ldy >= lim)
+    return QL_EINVAL;
+  if (!rows16_ok(GA, ldga) || !rows16_ok(UP, ldup) || !rows16_ok(HH, ldh) || !rows16_ok(Y, ldy))
+    return QL_EALIGN;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  int splits = ql_swiglu_bwd_down_splits(M, K);
+  if (ws_floats < (int64_t)splits * M * kRank || !ws) splits = 1;
+  int64_t kps = ((K + splits - 1) / splits + kSwK - 1) / kSwK * kSwK;
+  splits = (int)((K + kps - 1) / kps);
+  const dim3 grid((unsigned)((M + kSwRows - 1) / kSwRows), (unsigned)splits);
+#define QL_SWF(IT)                                                                            \
+  do {                                                                                        \
+    if (splits == 1) {                                                                        \
+      hipLaunchKernelGGL((swiglu_fwd_down_kernel<IT, false>), grid, dim3(256), 0, s,          \
+                         (const uint16_t*)GA, ldga, (const uint16_t*)UP, ldup, (uint16_t*)HH, \
+                         ldh, (const uint16_t*)Y, ldy, M, K, kps, (float*)nullptr,            \
+                         (uint16_t*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);        \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((swiglu_fwd_down_kernel<IT, true>), grid, dim3(256), 0, s,           \
+                         (const uint16_t*)GA, ldga, (const uint16_t*)UP, ldup, (uint16_t*)HH, \
+                         ldh, (const uint16_t*)Y, ldy, M, K, kps, ws, (uint16_t*)out, ldo,    \
+                         out_cols, alpha, (uint16_t*)out_t, ldt);                             \
+      hipLaunchKernelGGL((lora_down_reduce<IT, IT>), dim3(grid1d(M * out_cols)), dim3(256),   \
+                         0, s, ws, splits, M, kRank, (uint16_t*)out, ldo, out_cols, alpha,    \
+                         alpha, (uint16_t*)out_t, ldt);                                       \
+    }                                                                                         \
+  } while (0)
+  if (dtype == QL_BF16) QL_SWF(QL_BF16);
+  else QL_SWF(QL_F16);
+#undef QL_SWF
   return ql_launch_status();
 }
 
@@ -1377,9 +1618,10 @@ extern "C" int qlora_swiglu_bwd_lora_down(
 }
 
 
-extern "C" int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols) {
+extern "C" int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols,
+                                                        int with_da) {
   if (rows <= 0 || cols <= 0 || cols % 32) return 0;
-  return ql_swiglu_bwd_lora_ws_floats(rows, cols) * (int64_t)sizeof(float);
+  return ql_swiglu_bwd_lora_ws_floats(rows, cols, with_da != 0) * (int64_t)sizeof(float);
 }
 
 extern "C" int qlora_swiglu_bwd_lora(
@@ -1388,12 +1630,12 @@ extern "C" int qlora_swiglu_bwd_lora(
     const void* bt_gate, const void* bt_up, int64_t ldbt, const void* ut_gate,
     const void* ut_up, int64_t ldut, float alpha_gate, float alpha_up, float beta_gate,
     float beta_up, int dtype, void* du, int64_t ldo, int out_cols, void* du_t, int64_t ldt,
-    float* db_gate, float* db_up, void* workspace, int64_t workspace_bytes,
-    ql_stream_t stream) {
+    float* db_gate, float* db_up, const void* ud_t, float beta_down, float* da_down,
+    void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
   if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (rows == 0) return QL_OK;
   if (!grad || !gate || !up || !dgate || !dup || !bt_gate || !bt_up || !ut_gate || !ut_up ||
-      !du || !db_gate || !db_up || !workspace)
+      !du || !db_gate || !db_up || !workspace || (!ud_t) != (!da_down))
     return QL_EINVAL;
   // lanes past the last row or column recompute the last one and re-read its inputs after
   // other lanes stored: outputs that overlap the inputs would be read back modified
@@ -1407,7 +1649,35 @@ extern "C" int qlora_swiglu_bwd_lora(
   return ql_swiglu_bwd_lora(dtype, grad, ldgr, gate, ldg, up, ldu, dgate, lddg, dup, lddu, rows,
                             cols, bt_gate, bt_up, ldbt, ut_gate, ut_up, ldut, alpha_gate,
                             alpha_up, beta_gate, beta_up, du, ldo, out_cols, du_t, ldt, db_gate,
-                            db_up, static_cast<float*>(workspace),
+                            db_up, ud_t, beta_down, da_down, static_cast<float*>(workspace),
+                            workspace_bytes / (int64_t)sizeof(float),
+                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t qlora_swiglu_fwd_lora_down_workspace_size(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int s = ql_swiglu_bwd_down_splits(rows, cols);
+  return s > 1 ? (int64_t)s * rows * kRank * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int qlora_swiglu_fwd_lora_down(const void* gate, int64_t ldg, const void* up,
+                                          int64_t ldu, void* h, int64_t ldh, int64_t rows,
+                                          int64_t cols, const void* a, int64_t lda, float alpha,
+                                          int dtype, void* u, int64_t ldo, int out_cols,
+                                          void* u_t, int64_t ldt, void* workspace,
+                                          int64_t workspace_bytes, ql_stream_t stream) {
+  if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
+  if (rows == 0) return QL_OK;
+  if (!gate || !up || !h || !a || !u) return QL_EINVAL;
+  // lanes past the last row or column recompute the last one and re-read its inputs after
+  // other lanes stored: an output that overlaps the inputs would be read back modified
+  if (ql_spans_overlap(h, ldh, gate, ldg, rows, cols, 2) ||
+      ql_spans_overlap(h, ldh, up, ldu, rows, cols, 2))
+    return QL_EINVAL;
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  if (!ql_aligned(u, 2) || (u_t && !ql_aligned(u_t, 2))) return QL_EALIGN;
+  return ql_swiglu_fwd_down(dtype, gate, ldg, up, ldu, h, ldh, rows, cols, a, lda, alpha, u, ldo,
+                            out_cols, u_t, ldt, static_cast<float*>(workspace),
                             workspace_bytes / (int64_t)sizeof(float),
                             static_cast<hipStream_t>(stream));
 }

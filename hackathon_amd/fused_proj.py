@@ -308,6 +308,89 @@ class GateUpSwiGLU(torch.autograd.Function):
         return (None if dx is None else dx.view(ctx.shape)), None, *grads
 
 
+class LoraMLP(torch.autograd.Function):
+    """x -> down_proj(silu(gate_proj(x)) * up_proj(x)) when all three projections are 4-bit
+    LoRA layers: GateUpSwiGLU's gate/up group and the down projection as LoraNF4Linear's two
+    GEMMs, with the down adapter's products on h = silu(gate) up fused into the SwiGLU kernels
+    (solution/swiglu.py:15-37 and solution/lora.py:157-173 math):
+
+      forward   h and u_d = h A_d^T                        qlora_swiglu_fwd_lora_down
+                out = [h | u_d] [W_d | s_d B_d]^T + b_d     qlora_gemm_nt_cat
+      backward  du_d = s_d dY B_d                           qlora_lora_down
+                dh = [dY | du_d] [W_d^T | A_d^T]^T          qlora_gemm_nt_cat
+                dB_d = s_d dY^T u_d                         qlora_lora_wgrad
+                dgate, dup, du_gate, du_up, dB_gate, dB_up  qlora_swiglu_bwd_lora, which also
+                and dA_d = du_d^T h                         recomputes h on chip for dA_d
+                dx, dA_gate, dA_up                          as GateUpSwiGLU
+
+    h is not kept for the backward: it is neither read back for u_d nor stored for dA_d."""
+
+    @staticmethod
+    def forward(ctx, x, specs, dspec, *ab):
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        dt, dev = x2.dtype, x2.device
+        M = x2.shape[0]
+        y, (at, bt, ut) = group_forward(x2, specs, ab[:4])
+        n, N = specs[0].n, dspec.n
+        a16_d, at_d, bs_d, bt_d = _gemm.lora_pack(ab[4], ab[5], dspec.scaling, dt, _PAD)
+        h = torch.empty((M, n), dtype=dt, device=dev)
+        u_d = torch.empty((M, _PAD), dtype=dt, device=dev)
+        ut_d = _gemm.lora_t_buffer(M, dt, dev)
+        swiglu.swiglu_fwd_lora_down(y[:, :n], y[:, n:], h, a16_d, u_d, ut_d)
+        out = torch.empty((M, N), dtype=dt, device=dev)
+        bias = None if dspec.bias is None else dspec.bias.to(dt)
+        if nf4.use_fused_gemm(h, dspec.qs, dspec.packed):  # few rows: W_d dequantised in-GEMM
+            nf4.gemm_nf4(h, dspec.packed, dspec.qs, out=out, a2=u_d, b2=bs_d, bias=bias)
+        else:
+            w = nf4.dequantize_nf4(dspec.packed, dspec.qs, dt)
+            _gemm.gemm_nt_cat(h, w, u_d, bs_d, out, bias=bias)
+            del w
+        del h, u_d
+        ctx.save_for_backward(x2, y, at, bt, ut, at_d, bt_d, ut_d)
+        ctx.specs, ctx.dspec, ctx.shape = specs, dspec, x.shape
+        ctx.ab_dtypes = [t.dtype for t in ab]
+        return out.view(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, dout):
+        x2, y, at, bt, ut, at_d, bt_d, ut_d = ctx.saved_tensors
+        specs, dspec = ctx.specs, ctx.dspec
+        dt, dev = x2.dtype, x2.device
+        M = x2.shape[0]
+        n, N = specs[0].n, dspec.n
+        need = ctx.needs_input_grad  # x, specs, dspec, A_gate, B_gate, A_up, B_up, A_d, B_d
+        dy = dout.reshape(M, N)
+        if dy.dtype != dt:
+            dy = dy.to(dt)
+        if dy.stride(-1) != 1 or dy.stride(0) % 8 or dy.data_ptr() % 16:
+            dy = dy.contiguous()
+        s_d = dspec.scaling
+        du_d = torch.empty((M, _PAD), dtype=dt, device=dev)
+        dut_d = _gemm.lora_t_buffer(M, dt, dev)
+        _gemm.lora_down(dy, bt_d, du_d, alpha=s_d, out_t=dut_d)  # du_d = s_d dY B_d
+        wt = nf4.dequantize_nf4_t(dspec.packed, dspec.qs, dt)    # W_d^T [n, N]
+        dh = torch.empty((M, n), dtype=dt, device=dev)
+        _gemm.gemm_nt_cat(dy, wt, du_d, at_d, dh)
+        del wt, du_d
+        db_d = _gemm.lora_wgrad(ut_d, dy, alpha=s_d) if need[8] else None
+        g = torch.empty((M, 2 * n), dtype=dt, device=dev)
+        du = torch.empty((M, _PAD), dtype=dt, device=dev)
+        dut = _t_buffer(32, M, dt, dev)
+        gate_s, up_s = specs
+        db_g, db_u, da_d = swiglu.swiglu_bwd_lora(
+            dh, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:, :n], bt[:, n:], ut[:16], ut[16:32],
+            gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du, dut, ud_t=dut_d)
+        del dh
+        dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[3:7],
+                                   du_dut=(du, dut), db_given=[db_g, db_u])
+        grads = grads + [da_d if need[7] else None, db_d]
+        grads = [None if gr is None else gr.to(t) for gr, t in zip(grads, ctx.ab_dtypes)]
+        return (None if dx is None else dx.view(ctx.shape)), None, None, *grads
+
+
 def _group(layers, x):
     """(specs, [A_0, B_0, ...]) when every layer of the group is a fused-kernel 4-bit LoRA
     projection of the same input width, else None."""
@@ -370,7 +453,8 @@ def fused_attention(module, hidden_states, position_embeddings, attention_mask,
 
 
 def fused_mlp(module, x):
-    """Qwen2MLP.forward as down_proj(GateUpSwiGLU(x)), or None."""
+    """Qwen2MLP.forward as LoraMLP(x) when the down projection is a fused-kernel 4-bit LoRA
+    layer too, else down_proj(GateUpSwiGLU(x)); None when the gate/up group does not fit."""
     if getattr(getattr(module, "config", None), "hidden_act", "silu") != "silu":
         return None
     if not (_common.on_gpu(x) and x.dtype in (torch.bfloat16, torch.float16)
@@ -380,8 +464,13 @@ def fused_mlp(module, x):
     if group is None:
         return None
     specs, ab = group
-    if specs[0].n != specs[1].n or specs[0].n % 8:
+    n = specs[0].n
+    if specs[1].n != n or n % 8:
         return None
+    down = lora_spec(module.down_proj, x) if n % 32 == 0 else None
+    if down is not None and int(down[0].qs.shape[1]) == n:
+        dspec, a_d, b_d = down
+        return LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
     return module.down_proj(GateUpSwiGLU.apply(x, tuple(specs), *ab))
 
 

@@ -85,23 +85,29 @@ def swiglu_bwd_lora_down(grad, gate, up, dgate, dup, bt_gate, bt_up, alpha_gate,
 
 
 def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, alpha_gate,
-                    alpha_up, beta_gate, beta_up, du, du_t=None):
+                    alpha_up, beta_gate, beta_up, du, du_t=None, ud_t=None, beta_down=1.0):
     """swiglu_bwd_lora_down plus both adapters' lora_B gradients in the same pass
     (qlora_swiglu_bwd_lora): returns fp32 (db_gate, db_up) [cols, 16] with
     db_gate = beta_gate dgate^T ut_gate^T and db_up = beta_up dup^T ut_up^T, where ut_* [16, rows]
-    are the adapters' down-projections of the forward input, transposed."""
+    are the adapters' down-projections of the forward input, transposed. With `ud_t` (the du^T
+    [16, rows] of the adapter of the layer that reads h = silu(gate) up) also that adapter's
+    lora_A gradient da_down = beta_down ud_t h [16, cols], h recomputed on chip: returns
+    (db_gate, db_up, da_down)."""
     _lib.require_rows(gate.dtype, grad=grad, gate=gate, up=up, dgate=dgate, dup=dup,
                       bt_gate=bt_gate, bt_up=bt_up, ut_gate=ut_gate, ut_up=ut_up, du=du,
-                      du_t=du_t)
+                      du_t=du_t, ud_t=ud_t)
     rows, cols = gate.shape
     if bt_up.stride(0) != bt_gate.stride(0):
         raise ValueError("bt_gate and bt_up must share a row stride (slices of one B^T buffer)")
-    if ut_up.stride(0) != ut_gate.stride(0):
-        raise ValueError("ut_gate and ut_up must share a row stride (slices of one u^T buffer)")
-    db_gate = torch.empty((cols, 16), dtype=torch.float32, device=gate.device)
-    db_up = torch.empty((cols, 16), dtype=torch.float32, device=gate.device)
+    if ut_up.stride(0) != ut_gate.stride(0) or (ud_t is not None
+                                                 and ud_t.stride(0) != ut_gate.stride(0)):
+        raise ValueError("ut_gate, ut_up and ud_t must share a row stride")
+    dev = gate.device
+    db_gate = torch.empty((cols, 16), dtype=torch.float32, device=dev)
+    db_up = torch.empty((cols, 16), dtype=torch.float32, device=dev)
+    da_down = None if ud_t is None else torch.empty((16, cols), dtype=torch.float32, device=dev)
     ws, ws_bytes = _lib.workspace("qlora_swiglu_bwd_lora_workspace_size", rows, cols,
-                                  device=gate.device)
+                                  int(ud_t is not None), device=dev)
     _lib.call("qlora_swiglu_bwd_lora", grad.data_ptr(), grad.stride(0), gate.data_ptr(),
               gate.stride(0), up.data_ptr(), up.stride(0), dgate.data_ptr(), dgate.stride(0),
               dup.data_ptr(), dup.stride(0), rows, cols, bt_gate.data_ptr(), bt_up.data_ptr(),
@@ -109,8 +115,24 @@ def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, 
               float(alpha_gate), float(alpha_up), float(beta_gate), float(beta_up),
               _lib.tag(gate.dtype), du.data_ptr(), du.stride(0), du.shape[1], _lib.ptr(du_t),
               du_t.stride(0) if du_t is not None else 0, db_gate.data_ptr(), db_up.data_ptr(),
-              _lib.ptr(ws), ws_bytes, _lib.stream_of(gate))
-    return db_gate, db_up
+              _lib.ptr(ud_t), float(beta_down), _lib.ptr(da_down), _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(gate))
+    return (db_gate, db_up) if ud_t is None else (db_gate, db_up, da_down)
+
+
+def swiglu_fwd_lora_down(gate, up, h, a, u, u_t=None, alpha=1.0):
+    """h = silu(gate) * up (as swiglu_rows) and, in the same pass, the down-projection of h by
+    the next layer's adapter: u[:, :16] = alpha h a^T for a [16, cols] (that adapter's A in the
+    compute dtype), u[:, 16:] = 0, u_t = u[:, :16]^T when given (qlora_swiglu_fwd_lora_down)."""
+    _lib.require_rows(gate.dtype, gate=gate, up=up, h=h, a=a, u=u, u_t=u_t)
+    rows, cols = gate.shape
+    ws, ws_bytes = _lib.workspace("qlora_swiglu_fwd_lora_down_workspace_size", rows, cols,
+                                  device=gate.device)
+    _lib.call("qlora_swiglu_fwd_lora_down", gate.data_ptr(), gate.stride(0), up.data_ptr(),
+              up.stride(0), h.data_ptr(), h.stride(0), rows, cols, a.data_ptr(), a.stride(0),
+              float(alpha), _lib.tag(gate.dtype), u.data_ptr(), u.stride(0), u.shape[1],
+              _lib.ptr(u_t), u_t.stride(0) if u_t is not None else 0, _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(gate))
 
 
 def patch_qwen2_mlp():

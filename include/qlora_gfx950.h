@@ -408,16 +408,22 @@ int qlora_swiglu_bwd_lora_down(const void* grad, int64_t ldgr, const void* gate,
  *   db_up[k, c]   = beta_up   * sum_m dup[m, k]   * ut_up[c, m]
  * ut_gate / ut_up [16, rows] (ld ldut >= rows, a multiple of 8) are the adapters'
  * down-projections of the forward input, transposed (u^T of y = base + s B (A x)), so
- * db = s (dY)^T u is the lora_B gradient. Each workgroup owns 256 columns and a range of rows,
- * keeps the tile's gradients on chip for both products and writes fp32 partials: the two
- * gradients are never read back from HBM. The workspace (16-B aligned, at least
- * qlora_swiglu_bwd_lora_workspace_size bytes) is required (QL_EINVAL without it); db_gate and
- * db_up are 16-B aligned. Other rules as qlora_swiglu_bwd_lora_down.
+ * db = s (dY)^T u is the lora_B gradient. With ud_t and da_down (both or neither), also the
+ * lora_A gradient of the adapter of the layer that reads h = silu(gate) * up (the down
+ * projection of a LoRA MLP), h recomputed on chip with the forward's bits:
+ *   da_down[c, k] = beta_down * sum_m ud_t[c, m] * h[m, k]             fp32 [16, cols]
+ * where ud_t [16, rows] (ld ldut) is that adapter's du^T (du = s dY B). Each workgroup owns
+ * 256 columns and a range of rows, keeps the tile's gradients (and h) on chip for every
+ * product and writes fp32 partials: nothing is read back from HBM. The workspace (16-B
+ * aligned, at least qlora_swiglu_bwd_lora_workspace_size(rows, cols, with_da) bytes) is
+ * required (QL_EINVAL without it); db_gate, db_up and da_down are 16-B aligned. Other rules as
+ * qlora_swiglu_bwd_lora_down.
  * Replaces: solution/swiglu.py:25-37 (the SwiGLU backward) and the lora_B autograd backward
  * of solution/lora.py:172 for the gate and up projections (both the down-projection of the
- * output gradient and the weight gradient of B).
+ * output gradient and the weight gradient of B), and the lora_A weight gradient of the down
+ * projection's adapter (the same line's autograd, du^T h).
  */
-int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols);
+int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols, int with_da);
 int qlora_swiglu_bwd_lora(const void* grad, int64_t ldgr, const void* gate, int64_t ldg,
                           const void* up, int64_t ldu, void* dgate, int64_t lddg, void* dup,
                           int64_t lddu, int64_t rows, int64_t cols, const void* bt_gate,
@@ -425,7 +431,29 @@ int qlora_swiglu_bwd_lora(const void* grad, int64_t ldgr, const void* gate, int6
                           const void* ut_up, int64_t ldut, float alpha_gate, float alpha_up,
                           float beta_gate, float beta_up, int dtype, void* du, int64_t ldo,
                           int out_cols, void* du_t, int64_t ldt, float* db_gate, float* db_up,
-                          void* workspace, int64_t workspace_bytes, ql_stream_t stream);
+                          const void* ud_t, float beta_down, float* da_down, void* workspace,
+                          int64_t workspace_bytes, ql_stream_t stream);
+
+/*
+ * SwiGLU forward fused with the down-projection of its output by the adapter of the layer
+ * that reads it (the down projection of a LoRA MLP):
+ *   h = silu(gate) * up                  the bits of qlora_swiglu_fwd_rows (row-strided)
+ *   u[m, c] = alpha * sum_k h[m, k] * a[c, k]     c < 16, a = that adapter's A [16, cols]
+ *   u[m, c] = 0 for 16 <= c < out_cols;  u_t (optional, [16, ldt >= rows]) = u[:, :16]^T.
+ * The products use an on-chip copy of each tile of h, so h is not read back from HBM.
+ * Workspace (16-B aligned) enables a split over the columns; see the size query. cols % 32 ==
+ * 0; every matrix 16-B aligned with a leading dimension that is a multiple of 8, at least
+ * cols, and below 2^24; dtype QL_BF16 or QL_F16 (u and u_t in it too). Not in place: h must
+ * not meet gate or up (QL_EINVAL otherwise).
+ * Replaces: solution/swiglu.py:15-22 (the SwiGLU forward) together with the first adapter
+ * GEMM of solution/lora.py:172 (lora_A(x)) for the down projection.
+ */
+int64_t qlora_swiglu_fwd_lora_down_workspace_size(int64_t rows, int64_t cols);
+int qlora_swiglu_fwd_lora_down(const void* gate, int64_t ldg, const void* up, int64_t ldu,
+                               void* h, int64_t ldh, int64_t rows, int64_t cols, const void* a,
+                               int64_t lda, float alpha, int dtype, void* u, int64_t ldo,
+                               int out_cols, void* u_t, int64_t ldt, void* workspace,
+                               int64_t workspace_bytes, ql_stream_t stream);
 
 /*
  * The compute-dtype operands of one rank-16 adapter, from its fp32 factors A [16, K] and

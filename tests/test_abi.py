@@ -147,14 +147,27 @@ def test_rejected_arguments_return_codes(lib):
                                               None, 0, None, 0, None) == -1
     # ... and with both lora_B gradients: the workspace is required, and neither output may
     # meet an input
-    assert lib.qlora_swiglu_bwd_lora_workspace_size(4096, 18944) >= 74 * 4096 * 32 * 4
-    assert lib.qlora_swiglu_bwd_lora_workspace_size(4096, 100) == 0  # cols % 32
+    for with_da in (0, 1):  # at least the du partials of the 74 blocks of 256 columns
+        assert lib.qlora_swiglu_bwd_lora_workspace_size(4096, 18944, with_da) > 74 * 4096 * 128
+    assert lib.qlora_swiglu_bwd_lora_workspace_size(4096, 100, 0) == 0  # cols % 32
     assert lib.qlora_swiglu_bwd_lora(gr, 64, ga, 128, up, 128, dg, 128, du, 128, 16, 64, fake,
                                      fake, 128, fake, fake, 16, 1.0, 1.0, 1.0, 1.0, 2, fake, 64,
-                                     64, None, 0, fake, fake, None, 0, None) == -1
+                                     64, None, 0, fake, fake, None, 1.0, None, None, 0,
+                                     None) == -1
     assert lib.qlora_swiglu_bwd_lora(gr, 64, ga, 128, up, 128, ga, 128, du, 128, 16, 64, fake,
                                      fake, 128, fake, fake, 16, 1.0, 1.0, 1.0, 1.0, 2, fake, 64,
-                                     64, None, 0, fake, fake, fake, 1 << 20, None) == -1
+                                     64, None, 0, fake, fake, None, 1.0, None, fake, 1 << 20,
+                                     None) == -1
+    # ... the down adapter's du^T and dA come together or not at all
+    assert lib.qlora_swiglu_bwd_lora(gr, 64, ga, 128, up, 128, dg, 128, du, 128, 16, 64, fake,
+                                     fake, 128, fake, fake, 16, 1.0, 1.0, 1.0, 1.0, 2, fake, 64,
+                                     64, None, 0, fake, fake, fake, 1.0, None, fake, 1 << 20,
+                                     None) == -1
+    # SwiGLU forward + the down adapter's u: columns a multiple of 32, never in place
+    assert lib.qlora_swiglu_fwd_lora_down(ga, 128, up, 128, dg, 128, 16, 48, fake, 48, 1.0, 2,
+                                          fake, 64, 64, None, 0, None, 0, None) == -1
+    assert lib.qlora_swiglu_fwd_lora_down(ga, 128, up, 128, up, 128, 16, 64, fake, 64, 1.0, 2,
+                                          fake, 64, 64, None, 0, None, 0, None) == -1
     # adamw: a table is required when there is work; the bias correction must be positive
     assert lib.qlora_adamw_fp32(None, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 1.0, 1e-8, None) == -1
     assert lib.qlora_adamw_fp32(fake, 1, 1, 1.0, 0.999, 0.1, 0.001, 1e-3, 0.0, 1e-8, None) == -1

@@ -106,6 +106,37 @@ def test_gate_up_swiglu_matches_separate_layers(seq):
         assert _rel(a, b) < 1e-2, (name, _rel(a, b))
 
 
+@pytest.mark.parametrize("seq", [96, 37])
+def test_lora_mlp_matches_separate_layers(seq):
+    """The whole 4-bit LoRA MLP as one autograd function (the down adapter's products on h
+    fused into the SwiGLU kernels, h not kept) against gate, up and down run one by one:
+    output, input gradient and all six adapter gradients."""
+    print(f"fused LoRA MLP seq={seq}", flush=True)
+    cfg, model = _model()
+    mlp = model.model.layers[0].mlp
+    layers = (mlp.gate_proj, mlp.up_proj, mlp.down_proj)
+    params = _params(layers)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16)
+
+    out = mlp.down_proj(swiglu.swiglu(mlp.gate_proj(x), mlp.up_proj(x)))
+    (out.float() * w).sum().backward()
+    ref = out.detach().clone()
+    ref_g = [x.grad.clone()] + [p.grad.clone() for p in params]
+    _zero(params, x)
+
+    specs, ab = fused_proj._group(layers[:2], x)
+    dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
+    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+    (out2.float() * w).sum().backward()
+    assert out2.shape == ref.shape and _rel(out2, ref) < 4e-3
+    got_g = [x.grad] + [p.grad for p in params]
+    for name, a, b in zip(["x", "Ag", "Bg", "Au", "Bu", "Ad", "Bd"], got_g, ref_g):
+        assert _rel(a, b) < 1e-2, (name, _rel(a, b))
+    assert fused_proj.fused_mlp(mlp, x) is not None  # the patched MLP takes this path
+
+
 def test_swiglu_rows_match_the_contiguous_kernels():
     print("swiglu rows", flush=True)
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -127,7 +158,7 @@ def test_decoder_layer_takes_the_fused_path(monkeypatch):
     cfg, model = _model()
     hackathon_amd.apply()
     calls = {"qkv": 0, "mlp": 0}
-    qkv_apply, mlp_apply = fused_proj.QKVRoPE.apply, fused_proj.GateUpSwiGLU.apply
+    qkv_apply, mlp_apply = fused_proj.QKVRoPE.apply, fused_proj.LoraMLP.apply
 
     def count_qkv(*a):
         calls["qkv"] += 1
@@ -138,7 +169,7 @@ def test_decoder_layer_takes_the_fused_path(monkeypatch):
         return mlp_apply(*a)
 
     monkeypatch.setattr(fused_proj.QKVRoPE, "apply", count_qkv)
-    monkeypatch.setattr(fused_proj.GateUpSwiGLU, "apply", count_mlp)
+    monkeypatch.setattr(fused_proj.LoraMLP, "apply", count_mlp)
     ids = torch.randint(0, 1000, (2, 64), device="cuda")
     out = model(input_ids=ids, labels=ids, use_cache=False)
     out.loss.backward()
@@ -211,6 +242,37 @@ def test_swiglu_bwd_lora_down(rows, cols, dtype):
 @pytest.mark.parametrize("rows,cols,dtype", [(4096, 18944, torch.bfloat16),
                                              (37, 1024, torch.bfloat16),
                                              (300, 96, torch.bfloat16),
+                                             (1000, 2048, torch.float16)])
+def test_swiglu_fwd_lora_down(rows, cols, dtype):
+    """qlora_swiglu_fwd_lora_down: h with the bits of qlora_swiglu_fwd_rows, u = alpha h a^T
+    within the fp32 accumulation bound of an fp64 product, zeros after column 16, u_t the exact
+    transpose; ragged row counts exercise rows past M."""
+    print(f"swiglu_fwd_lora_down {rows}x{cols} {dtype}", flush=True)
+    from hackathon_amd import gemm
+
+    g = torch.Generator(device="cuda").manual_seed(5 * rows + cols)
+    y = torch.randn(rows, 2 * cols, device="cuda", generator=g).to(dtype)
+    gate, up = y[:, :cols], y[:, cols:]
+    a = (torch.randn(16, cols, device="cuda", generator=g) * 0.05).to(dtype)
+    h = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    u = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
+    ut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=16)
+    swiglu.swiglu_fwd_lora_down(gate, up, h, a, u, ut, alpha=0.75)
+    ref = torch.empty_like(h)
+    swiglu.swiglu_rows(gate, up, ref)
+    assert torch.equal(h, ref)
+    hd, ad = ref.double(), a.double()
+    exact = 0.75 * (hd @ ad.t())
+    rnd = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    bound = 0.75 * 4 * 2.0**-22 * cols * hd.abs().max() * ad.abs().max() + rnd * exact.abs()
+    assert torch.all((u[:, :16].double() - exact).abs() <= bound)
+    assert torch.all(u[:, 16:] == 0)
+    assert torch.equal(ut, u[:, :16].t())
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(4096, 18944, torch.bfloat16),
+                                             (37, 1024, torch.bfloat16),
+                                             (300, 96, torch.bfloat16),
                                              (1000, 2048, torch.float16),
                                              (4000, 4832, torch.bfloat16)])
 def test_swiglu_bwd_lora(rows, cols, dtype):
@@ -233,14 +295,33 @@ def test_swiglu_bwd_lora(rows, cols, dtype):
     buf = torch.empty(rows, 2 * cols, dtype=dtype, device="cuda")
     du = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
     dut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+    udt = gemm.lora_t_buffer(rows, dtype, "cuda", rows=16)
+    udt.copy_(torch.randn(16, rows, device="cuda", generator=g).to(dtype))
     db_gate, db_up = swiglu.swiglu_bwd_lora(dh, gate, up, buf[:, :cols], buf[:, cols:],
                                             bt[:, :cols], bt[:, cols:], ut[:16], ut[16:32],
                                             2.0, 0.5, 2.0, 0.5, du, dut)
     ref = torch.empty_like(buf)
     swiglu.swiglu_bwd_rows(dh, gate, up, ref[:, :cols], ref[:, cols:])
     assert torch.equal(buf, ref)
+    # with the down adapter's lora_A gradient: the same outputs, plus da = 1.5 ud^T h
+    buf2 = torch.empty_like(buf)
+    du2 = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
+    dut2 = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+    db_gate2, db_up2, da = swiglu.swiglu_bwd_lora(
+        dh, gate, up, buf2[:, :cols], buf2[:, cols:], bt[:, :cols], bt[:, cols:], ut[:16],
+        ut[16:32], 2.0, 0.5, 2.0, 0.5, du2, dut2, ud_t=udt, beta_down=1.5)
+    # (the dB partials come from fewer, longer row ranges here: fp32 rounding apart, checked
+    # against fp64 with the others below)
+    assert torch.equal(buf2, ref) and torch.equal(du2, du) and torch.equal(dut2, dut)
+    h = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    swiglu.swiglu_rows(gate, up, h)
+    hd, udd = h.double(), udt.double()
+    exact_a = 1.5 * (udd @ hd)
+    bound_a = 1.5 * 4 * 2.0**-22 * rows * hd.abs().max() * udd.abs().max()
+    assert da.shape == (16, cols) and torch.all((da.double() - exact_a).abs() <= bound_a)
     u = ut.double()
-    for q, (c0, a, db) in enumerate(((0, 2.0, db_gate), (cols, 0.5, db_up))):
+    for q, (c0, a, db, db2) in enumerate(((0, 2.0, db_gate, db_gate2),
+                                          (cols, 0.5, db_up, db_up2))):
         x = ref[:, c0:c0 + cols].double()
         w = bt[:, c0:c0 + cols].double()
         exact = a * (x @ w.t())
@@ -253,5 +334,6 @@ def test_swiglu_bwd_lora(rows, cols, dtype):
         bound_b = a * 4 * 2.0**-22 * rows * x.abs().max() * uq.abs().max()
         assert db.shape == (cols, 16) and db.dtype == torch.float32
         assert torch.all((db.double() - exact_b).abs() <= bound_b), q
+        assert torch.all((db2.double() - exact_b).abs() <= bound_b), q
     assert torch.all(du[:, 32:] == 0)
     assert torch.equal(dut, du[:, :32].t())
