@@ -625,6 +625,7 @@ def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=20
         model.zero_grad(set_to_none=True)
         qlora_step.patched_mode()
         log(f"[bench] step-0 loss patched {loss_p0:.6f} eager {loss_e0:.6f}")
+    torch.cuda.reset_peak_memory_stats()  # the patched steps' own peak, not the parity runs'
     t_p, loss_p = run(step, steps, warmup)
     log(f"[bench] patched step {t_p * 1e3:.1f} ms loss {loss_p:.4f}")
     peak_p = torch.cuda.max_memory_allocated() / 2**30
