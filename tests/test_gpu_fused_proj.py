@@ -137,6 +137,41 @@ def test_lora_mlp_matches_separate_layers(seq):
     assert fused_proj.fused_mlp(mlp, x) is not None  # the patched MLP takes this path
 
 
+def test_lora_mlp_partial_grads_and_no_grad():
+    """LoraMLP with the down adapter frozen returns no gradient for it and the same gradients
+    for the others as with it trainable; under no_grad it gives the same output."""
+    print("fused LoRA MLP, frozen down adapter", flush=True)
+    cfg, model = _model(seed=1)
+    mlp = model.model.layers[0].mlp
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(2, 64, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(2, 64, 512, device="cuda", generator=g).to(torch.bfloat16)
+    specs, ab = fused_proj._group((mlp.gate_proj, mlp.up_proj), x)
+    dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
+    out = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+    (out.float() * w).sum().backward()
+    ref = [x.grad.clone()] + [t.grad.clone() for t in ab]
+    with torch.no_grad():
+        out0 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+    assert torch.equal(out0, out)
+    x.grad = None
+    for t in ab:
+        t.grad = None
+    a_d.grad = b_d.grad = None
+    a_d.requires_grad_(False)
+    b_d.requires_grad_(False)
+    try:
+        out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+        (out2.float() * w).sum().backward()
+        assert a_d.grad is None and b_d.grad is None
+        got = [x.grad] + [t.grad for t in ab]
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+    finally:
+        a_d.requires_grad_(True)
+        b_d.requires_grad_(True)
+
+
 def test_swiglu_rows_match_the_contiguous_kernels():
     print("swiglu rows", flush=True)
     g = torch.Generator(device="cuda").manual_seed(3)
