@@ -66,6 +66,8 @@ _SIGNATURES = {
                       _c_ptr],
     "qlora_nf4_dequant_t": [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_f32, _c_int,
                             _c_int, _c_ptr, _c_ptr, _c_i64, _c_int, _c_ptr],
+    "qlora_nf4_dequant_group": [_c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_ptr],
+    "qlora_nf4_dequant_t_group": [_c_ptr, _c_int, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr],
     "qlora_transpose16": [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_gemm_nt_cat": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr,
                           _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32,
@@ -225,6 +227,15 @@ def lora_factors(items) -> ctypes.Array:
     for i, (a, b, s) in enumerate(items):
         arr[i] = LoraFactor(a.data_ptr(), b.data_ptr(), b.shape[0], float(s))
     return arr
+
+
+class Nf4Weight(ctypes.Structure):
+    """ql_nf4_weight: one NF4 weight [rows, cols], its scales and its output."""
+    _fields_ = [("packed", ctypes.c_void_p), ("rows", ctypes.c_int64), ("cols", ctypes.c_int64),
+                ("absmax", ctypes.c_void_p), ("code2", ctypes.c_void_p),
+                ("absmax2", ctypes.c_void_p), ("offset", ctypes.c_float),
+                ("blocksize", ctypes.c_int), ("blocksize2", ctypes.c_int),
+                ("out", ctypes.c_void_p)]
 
 
 def workspace(name: str, *sizes, device) -> tuple:

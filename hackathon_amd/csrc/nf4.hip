@@ -72,12 +72,15 @@ QL_DEV float block_scale(int64_t blk, const uint8_t* __restrict__ absmax_q,
   }
 }
 
+// One workgroup's span of the vector path: groups tile * kThreads * UNROLL + [0, kThreads *
+// UNROLL) of one weight.
 template <int OUT_DT, bool NESTED, int UNROLL>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
-    const uint32_t* __restrict__ packed4, int64_t n_groups, const uint8_t* __restrict__ absmax_q,
-    const float* __restrict__ absmax_f, const float* __restrict__ code2,
-    const float* __restrict__ absmax2, float offset, int log2_bs, int log2_bs2,
-    const float* __restrict__ nf4_table, typename Elem<OUT_DT>::T* __restrict__ out) {
+QL_DEV void dequant_vec_span(int64_t tile, const uint32_t* __restrict__ packed4, int64_t n_groups,
+                             const uint8_t* __restrict__ absmax_q,
+                             const float* __restrict__ absmax_f, const float* __restrict__ code2,
+                             const float* __restrict__ absmax2, float offset, int log2_bs,
+                             int log2_bs2, const float* __restrict__ nf4_table,
+                             typename Elem<OUT_DT>::T* __restrict__ out) {
 #pragma clang fp contract(off)
   __shared__ float table[16];
   __shared__ float code2_lds[NESTED ? 256 : 1];
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
   // loads go first because loads complete in issue order.
   const float tab_v = threadIdx.x < 16 ? nf4_table[threadIdx.x] : 0.f;
   const float code2_v = NESTED ? code2[threadIdx.x] : 0.f;  // kThreads == 256
-  const int64_t base = (int64_t)blockIdx.x * (kThreads * UNROLL) + threadIdx.x;
+  const int64_t base = tile * (kThreads * UNROLL) + threadIdx.x;
   uint32_t word[UNROLL];
   uint32_t code[UNROLL];  // absmax code (nested) or the fp32 absmax bits (plain)
   float scale2[UNROLL];   // second-level scale (nested)
@@ -129,6 +132,59 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
   }
 }
 
+template <int OUT_DT, bool NESTED, int UNROLL>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_vec(
+    const uint32_t* __restrict__ packed4, int64_t n_groups, const uint8_t* __restrict__ absmax_q,
+    const float* __restrict__ absmax_f, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, float offset, int log2_bs, int log2_bs2,
+    const float* __restrict__ nf4_table, typename Elem<OUT_DT>::T* __restrict__ out) {
+  dequant_vec_span<OUT_DT, NESTED, UNROLL>(blockIdx.x, packed4, n_groups, absmax_q, absmax_f,
+                                           code2, absmax2, offset, log2_bs, log2_bs2, nf4_table,
+                                           out);
+}
+
+// Several weights in one launch (the q/k/v or gate/up projections of a layer): one launch
+// instead of one per weight, so the small weights' latency-bound ramps overlap with the large
+// ones'. Weight i owns workgroups [tile_begin_i, tile_begin_{i+1}); the descriptor table
+// travels by value in the kernel arguments and each workgroup selects its entry with
+// wave-uniform compares.
+constexpr int kMaxGroup = 4;
+struct DqItem {
+  const uint8_t* packed;
+  const uint8_t* absmax_q;
+  const float* absmax_f;
+  const float* code2;
+  const float* absmax2;
+  void* out;
+  int64_t rows;      // vector path: the weight's 4-byte groups; transposed path: rows
+  int64_t cols;      // transposed path only
+  float offset;
+  int log2_bs, log2_bs2;
+  uint32_t tile_begin;  // first workgroup (x index) of this weight
+};
+struct DqGroup {
+  DqItem item[kMaxGroup];
+  int count;
+};
+
+QL_DEV DqItem pick_item(const DqGroup& grp, uint32_t bx) {
+  DqItem it = grp.item[0];
+#pragma unroll
+  for (int j = 1; j < kMaxGroup; ++j)
+    if (j < grp.count && bx >= grp.item[j].tile_begin) it = grp.item[j];
+  return it;
+}
+
+template <int OUT_DT, bool NESTED, int UNROLL>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_vec_group(
+    const DqGroup grp, const float* __restrict__ nf4_table) {
+  const DqItem it = pick_item(grp, blockIdx.x);
+  dequant_vec_span<OUT_DT, NESTED, UNROLL>(
+      blockIdx.x - it.tile_begin, reinterpret_cast<const uint32_t*>(it.packed), it.rows,
+      it.absmax_q, it.absmax_f, it.code2, it.absmax2, it.offset, it.log2_bs, it.log2_bs2,
+      nf4_table, static_cast<typename Elem<OUT_DT>::T*>(it.out));
+}
+
 // Any even blocksize, any alignment: one thread per packed byte.
 template <int OUT_DT, bool NESTED>
 __global__ __launch_bounds__(kThreads) void nf4_dequant_scalar(
@@ -167,13 +223,14 @@ constexpr int kTRows = 64, kTCols = 128;
 constexpr int kTStride = 36;  // LDS words per k-row of the tile (32 used, 16-B aligned rows)
 constexpr int kTInStride = 17;  // LDS words per packed input row (16 used)
 
+// One 64 x 128 tile (n-tile nt, k-tile kt) of the transposed dequantisation.
 template <int OUT_DT, bool NESTED>
-__global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
-    const uint8_t* __restrict__ packed, int64_t rows, int64_t cols,
-    const uint8_t* __restrict__ absmax_q, const float* __restrict__ absmax_f,
-    const float* __restrict__ code2, const float* __restrict__ absmax2, float offset, int log2_bs,
-    int log2_bs2, const float* __restrict__ nf4_table, uint16_t* __restrict__ outT,
-    int64_t ld_out) {
+QL_DEV void dequant_t_tile(int64_t nt, int64_t kt, const uint8_t* __restrict__ packed,
+                           int64_t rows, int64_t cols, const uint8_t* __restrict__ absmax_q,
+                           const float* __restrict__ absmax_f, const float* __restrict__ code2,
+                           const float* __restrict__ absmax2, float offset, int log2_bs,
+                           int log2_bs2, const float* __restrict__ nf4_table,
+                           uint16_t* __restrict__ outT, int64_t ld_out) {
 #pragma clang fp contract(off)
   __shared__ float table[16];
   __shared__ float code2_lds[NESTED ? 256 : 1];
@@ -181,8 +238,8 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
   __shared__ uint32_t tile_in[kTRows * kTInStride];
   // n-tiles vary fastest: workgroups running together write adjacent 128-B pieces of the same
   // output rows (whole DRAM pages) instead of one piece each of many rows
-  const int64_t n0 = (int64_t)blockIdx.x * kTRows;
-  const int64_t k0 = (int64_t)blockIdx.y * kTCols;
+  const int64_t n0 = nt * kTRows;
+  const int64_t k0 = kt * kTCols;
   {  // packed input: thread t loads 16 B of row t / 4 (chunk t % 4)
     const int r = threadIdx.x >> 2, c = threadIdx.x & 3;
     if (n0 + r < rows) {
@@ -235,6 +292,32 @@ __global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
       __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(outT + (k0 + kr) * ld_out + n));
     }
   }
+}
+
+template <int OUT_DT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_t_kernel(
+    const uint8_t* __restrict__ packed, int64_t rows, int64_t cols,
+    const uint8_t* __restrict__ absmax_q, const float* __restrict__ absmax_f,
+    const float* __restrict__ code2, const float* __restrict__ absmax2, float offset, int log2_bs,
+    int log2_bs2, const float* __restrict__ nf4_table, uint16_t* __restrict__ outT,
+    int64_t ld_out) {
+  dequant_t_tile<OUT_DT, NESTED>(blockIdx.x, blockIdx.y, packed, rows, cols, absmax_q, absmax_f,
+                                 code2, absmax2, offset, log2_bs, log2_bs2, nf4_table, outT,
+                                 ld_out);
+}
+
+// Grouped transposed dequantisation: weight i's n-tiles are x indices [tile_begin_i, ..) and
+// its output block starts at item.out (its column offset in the shared out_t); the k-tiles
+// (y) run to the widest weight and a narrower weight's surplus workgroups exit at once.
+template <int OUT_DT, bool NESTED>
+__global__ __launch_bounds__(kThreads) void nf4_dequant_t_group(
+    const DqGroup grp, const float* __restrict__ nf4_table, int64_t ld_out) {
+  const DqItem it = pick_item(grp, blockIdx.x);
+  if ((int64_t)blockIdx.y * kTCols >= it.cols) return;  // whole workgroup, before any barrier
+  dequant_t_tile<OUT_DT, NESTED>(blockIdx.x - it.tile_begin, blockIdx.y, it.packed, it.rows,
+                                 it.cols, it.absmax_q, it.absmax_f, it.code2, it.absmax2,
+                                 it.offset, it.log2_bs, it.log2_bs2, nf4_table,
+                                 static_cast<uint16_t*>(it.out), ld_out);
 }
 
 int ilog2_exact(int64_t v) {  // log2 of a power of two, else -1
@@ -335,5 +418,111 @@ extern "C" int qlora_nf4_dequant_t(const uint8_t* packed, int64_t rows, int64_t 
     if (nested) QL_DQT(QL_F16, true); else QL_DQT(QL_F16, false);
   }
 #undef QL_DQT
+  return ql_launch_status();
+}
+
+namespace {
+
+// Checks one weight of a group as the single-weight entries check theirs and fills its scale
+// fields; `transposed` applies qlora_nf4_dequant_t's extra shape rules.
+int group_item(const ql_nf4_weight& w, int nested, bool transposed, int64_t ld_out,
+               DqItem* it) {
+  if (w.rows < 0 || w.cols < 0) return QL_EINVAL;
+  if (w.rows == 0 || w.cols == 0) return QL_OK;
+  if (!w.packed || !w.absmax || !w.out) return QL_EINVAL;
+  if (nested && (!w.code2 || !w.absmax2)) return QL_EINVAL;
+  it->packed = w.packed;
+  it->absmax_q = nested ? static_cast<const uint8_t*>(w.absmax) : nullptr;
+  it->absmax_f = nested ? nullptr : static_cast<const float*>(w.absmax);
+  it->code2 = nested ? w.code2 : nullptr;
+  it->absmax2 = nested ? w.absmax2 : nullptr;
+  it->offset = nested ? w.offset : 0.f;
+  it->out = w.out;
+  it->cols = w.cols;
+  it->log2_bs = ilog2_exact(w.blocksize);
+  it->log2_bs2 = nested ? ilog2_exact(w.blocksize2) : 0;
+  if (transposed) {
+    if (it->log2_bs < 4 || it->log2_bs2 < 0) return QL_EINVAL;
+    if (ld_out < w.rows) return QL_EINVAL;
+    if (w.cols % kTCols || w.rows % 8) return QL_ESHAPE;
+    if (!ql_aligned(w.packed, 16) || !ql_aligned(w.out, 16)) return QL_EALIGN;
+    it->rows = w.rows;
+  } else {
+    if (w.cols > INT64_MAX / w.rows) return QL_EINVAL;
+    const int64_t n = w.rows * w.cols;
+    if (it->log2_bs < 3 || it->log2_bs2 < 0) return QL_EINVAL;  // powers of two, blocksize >= 8
+    if (n % 8) return QL_ESHAPE;
+    if (!ql_aligned(w.packed, 4) || !ql_aligned(w.out, 16)) return QL_EALIGN;
+    it->rows = n / 8;  // 4-byte groups
+  }
+  return QL_OK;
+}
+
+template <int OUT_DT, bool NESTED>
+void launch_group(const DqGroup& grp, uint32_t tiles, const float* table, hipStream_t s) {
+  hipLaunchKernelGGL((nf4_dequant_vec_group<OUT_DT, NESTED, 2>), dim3(tiles), dim3(kThreads), 0,
+                     s, grp, table);
+}
+
+}  // namespace
+
+extern "C" int qlora_nf4_dequant_group(const ql_nf4_weight* weights, int count, int nested,
+                                       const float* nf4_table, int out_dtype,
+                                       ql_stream_t stream) {
+  if (count < 1 || count > kMaxGroup || !weights || !nf4_table) return QL_EINVAL;
+  DqGroup grp{};
+  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    DqItem it{};
+    const int st = group_item(weights[i], nested, false, 0, &it);
+    if (st != QL_OK) return st;
+    if (it.rows == 0 || weights[i].rows == 0 || weights[i].cols == 0) continue;
+    it.tile_begin = (uint32_t)tiles;
+    tiles += (it.rows + kThreads * 2 - 1) / (kThreads * 2);
+    if (tiles > INT32_MAX) return QL_ESHAPE;
+    grp.item[grp.count++] = it;
+  }
+  if (grp.count == 0) return QL_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nested) {
+    QL_DISPATCH_DTYPE(out_dtype, DT, launch_group<DT, true>(grp, (uint32_t)tiles, nf4_table, s));
+  } else {
+    QL_DISPATCH_DTYPE(out_dtype, DT, launch_group<DT, false>(grp, (uint32_t)tiles, nf4_table, s));
+  }
+  return ql_launch_status();
+}
+
+extern "C" int qlora_nf4_dequant_t_group(const ql_nf4_weight* weights, int count, int nested,
+                                         const float* nf4_table, int64_t ld_out, int out_dtype,
+                                         ql_stream_t stream) {
+  if (count < 1 || count > kMaxGroup || !weights || !nf4_table) return QL_EINVAL;
+  if (out_dtype != QL_BF16 && out_dtype != QL_F16) return QL_EDTYPE;
+  if (ld_out % 8) return QL_ESHAPE;
+  DqGroup grp{};
+  int64_t tiles = 0, max_cols = 0;
+  for (int i = 0; i < count; ++i) {
+    DqItem it{};
+    const int st = group_item(weights[i], nested, true, ld_out, &it);
+    if (st != QL_OK) return st;
+    if (weights[i].rows == 0 || weights[i].cols == 0) continue;
+    it.tile_begin = (uint32_t)tiles;
+    tiles += (it.rows + kTRows - 1) / kTRows;
+    if (tiles > INT32_MAX) return QL_ESHAPE;
+    max_cols = it.cols > max_cols ? it.cols : max_cols;
+    grp.item[grp.count++] = it;
+  }
+  if (grp.count == 0) return QL_OK;
+  if (max_cols / kTCols > 65535) return QL_ESHAPE;
+  const dim3 grid((unsigned)tiles, (unsigned)(max_cols / kTCols));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define QL_DQTG(DT, NST)                                                                      \
+  hipLaunchKernelGGL((nf4_dequant_t_group<DT, NST>), grid, dim3(kThreads), 0, s, grp, nf4_table, \
+                     ld_out)
+  if (out_dtype == QL_BF16) {
+    if (nested) QL_DQTG(QL_BF16, true); else QL_DQTG(QL_BF16, false);
+  } else {
+    if (nested) QL_DQTG(QL_F16, true); else QL_DQTG(QL_F16, false);
+  }
+#undef QL_DQTG
   return ql_launch_status();
 }

@@ -145,8 +145,8 @@ def group_forward(x2, specs, ab):
                          bias=None if bias is None else bias[c0:c1])
         return y, (at, bt, ut)
     w = torch.empty((offs[-1], K), dtype=dt, device=dev)
-    for g, s in enumerate(specs):
-        nf4.dequantize_nf4(s.packed, s.qs, dt, out=w[offs[g]:offs[g + 1]])
+    nf4.dequantize_nf4_group([(s.packed, s.qs) for s in specs], dt,
+                             [w[offs[g]:offs[g + 1]] for g in range(G)])
     for p0, p1 in _column_blocks(specs):
         c0, c1 = offs[p0], offs[p1]
         _gemm.gemm_nt_cat(x2, w[c0:c1], u, bs[c0:c1], y[:, c0:c1],
@@ -175,8 +175,8 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
     dx = None
     if need_dx:
         wt = torch.empty((K, offs[-1]), dtype=dt, device=dev)
-        for i, s in enumerate(specs):
-            nf4.dequantize_nf4_t(s.packed, s.qs, dt, out=wt[:, offs[i]:offs[i + 1]])
+        nf4.dequantize_nf4_t_group([(s.packed, s.qs) for s in specs], dt,
+                                   [wt[:, offs[i]:offs[i + 1]] for i in range(G)])
         dx = torch.empty((M, K), dtype=dt, device=dev)
         _gemm.gemm_nt_cat(g, wt, du, at, dx)
         del wt

@@ -111,6 +111,79 @@ def dequantize_nf4_t(packed, quant_state, dtype=torch.bfloat16, out=None):
     return out
 
 
+def _pow2_at_least(v, lo):
+    v = int(v)
+    return v >= lo and v & (v - 1) == 0
+
+
+def _groupable(items, outs, transposed):
+    """Whether qlora_nf4_dequant_group / _t_group take these weights and outputs."""
+    if not 2 <= len(items) <= 4 or len({bool(qs.nested) for _, qs in items}) != 1:
+        return False
+    lds = set()
+    for (packed, qs), out in zip(items, outs):
+        rows, cols = (int(v) for v in qs.shape)
+        align = 16 if transposed else 4
+        if (not packed.is_cuda or not packed.is_contiguous() or packed.device != out.device
+                or packed.data_ptr() % align
+                or out.data_ptr() % 16 or not _pow2_at_least(qs.blocksize, 16 if transposed else 8)
+                or (qs.nested and not _pow2_at_least(qs.state2.blocksize, 1))
+                or packed.numel() * 2 < rows * cols):
+            return False
+        if transposed:
+            if (cols % 128 or rows % 8 or out.dtype not in (torch.bfloat16, torch.float16)
+                    or tuple(out.shape) != (cols, rows) or out.stride(1) != 1):
+                return False
+            lds.add(out.stride(0))
+        elif (rows * cols) % 8 or out.numel() != rows * cols or not out.is_contiguous():
+            return False
+    return not transposed or (len(lds) == 1 and lds.pop() % 8 == 0)
+
+
+def _group_call(name, items, outs, dtype, *extra):
+    keep = []  # the scale tensors _scale_args made stay alive until the launch is queued
+    arr = (_lib.Nf4Weight * len(items))()
+    for i, ((packed, qs), out) in enumerate(zip(items, outs)):
+        absmax, nested, code2, absmax2, offset, blocksize2 = _scale_args(qs)
+        keep += [absmax, code2, absmax2]
+        rows, cols = (int(v) for v in qs.shape)
+        arr[i] = _lib.Nf4Weight(packed.data_ptr(), rows, cols, absmax.data_ptr(), _lib.ptr(code2),
+                                _lib.ptr(absmax2), offset, int(qs.blocksize), blocksize2,
+                                out.data_ptr())
+    device = outs[0].device
+    _lib.call(name, arr, len(items), int(bool(items[0][1].nested)), _nf4_table(device).data_ptr(),
+              *extra, _lib.tag(dtype), _lib.stream_of(outs[0]))
+
+
+def dequantize_nf4_group(items, dtype, outs):
+    """Dequantise the weights `items` = [(packed, quant_state), ...] into `outs` (one
+    contiguous [out_features, in_features] tensor of `dtype` each): one launch for up to four
+    weights of the same nesting (qlora_nf4_dequant_group), else one dequantize_nf4 each.
+    Bit-identical either way."""
+    for out in outs:
+        _lib.require_device(out)
+    if _groupable(items, outs, False) and all(o.dtype == dtype for o in outs):
+        _group_call("qlora_nf4_dequant_group", items, outs, dtype)
+    else:
+        for (packed, qs), out in zip(items, outs):
+            dequantize_nf4(packed, qs, dtype, out=out)
+    return outs
+
+
+def dequantize_nf4_t_group(items, dtype, outs):
+    """The transposed weights of `items` into `outs` ([in_features, out_features] column blocks
+    of one buffer, sharing its row stride): one launch (qlora_nf4_dequant_t_group) when the
+    weights qualify, else one dequantize_nf4_t each. Bit-identical either way."""
+    for out in outs:
+        _lib.require_device(out)
+    if _groupable(items, outs, True) and all(o.dtype == dtype for o in outs):
+        _group_call("qlora_nf4_dequant_t_group", items, outs, dtype, outs[0].stride(0))
+    else:
+        for (packed, qs), out in zip(items, outs):
+            dequantize_nf4_t(packed, qs, dtype, out=out)
+    return outs
+
+
 # Token rows up to which the forward GEMM dequantises W inside the GEMM (gemm_nf4) instead of
 # writing a dense 16-bit W first. Measured on MI355X at the Qwen2.5-7B projection shapes: the
 # fused GEMM is 1.12-1.28x faster at 64 and 256 rows (W's dense write and re-read dominate),

@@ -272,6 +272,49 @@ int qlora_nf4_dequant_t(const uint8_t* packed, int64_t rows, int64_t cols, const
                         int64_t ld_out, int out_dtype, ql_stream_t stream);
 
 /*
+ * Several NF4 weights dequantised in ONE launch: the projections that read the same input
+ * (q/k/v, gate/up). Each entry describes one weight W_i [rows, cols] with the arguments of
+ * qlora_nf4_dequant (n_weights = rows * cols; absmax, code2, absmax2, offset, blocksize,
+ * blocksize2) and its own output `out`; `nested` and `out_dtype` are shared. Results are
+ * bit-identical to one qlora_nf4_dequant call per entry.
+ * Replaces: solution/nf4.py:71-92 (dequantize_nf4) called once per projection; the
+ * grouping itself has no reference counterpart.
+ * 1 <= count <= 4. Every entry needs rows * cols % 8 == 0, blocksize a power of two >= 8
+ * (blocksize2 a power of two when nested), packed 4-B and out 16-B aligned (else QL_ESHAPE /
+ * QL_EINVAL / QL_EALIGN); weights outside these rules go through qlora_nf4_dequant. The
+ * outputs must not overlap one another.
+ */
+typedef struct ql_nf4_weight {
+  const uint8_t* packed;
+  int64_t rows;
+  int64_t cols;
+  const void* absmax;
+  const float* code2;
+  const float* absmax2;
+  float offset;
+  int blocksize;
+  int blocksize2;
+  void* out;
+} ql_nf4_weight;
+int qlora_nf4_dequant_group(const ql_nf4_weight* weights, int count, int nested,
+                            const float* nf4_table, int out_dtype, ql_stream_t stream);
+
+/*
+ * The transposed form of qlora_nf4_dequant_group: entry i writes W_i^T with the layout of
+ * qlora_nf4_dequant_t, out_i[k * ld_out + n] = W_i[n][k], where out_i is normally the
+ * column block of a shared [cols, ld_out] buffer (out_t + first output column of W_i), as
+ * the backward of the fused projections wants dY_cat @ W_cat. Bit-identical to one
+ * qlora_nf4_dequant_t call per entry. Each entry follows qlora_nf4_dequant_t's rules (cols %
+ * 128 == 0, rows % 8 == 0, ld_out >= rows, blocksize a power of two >= 16, 16-B aligned
+ * packed and out); ld_out % 8 == 0; out_dtype QL_BF16 or QL_F16; 1 <= count <= 4; the
+ * column blocks must not overlap.
+ * Replaces: solution/nf4.py:110 (the backward's re-dequantisation) once per projection.
+ */
+int qlora_nf4_dequant_t_group(const ql_nf4_weight* weights, int count, int nested,
+                              const float* nf4_table, int64_t ld_out, int out_dtype,
+                              ql_stream_t stream);
+
+/*
  * 16-bit transpose: out[c * ld_out + r] = in[r * ld_in + c] for r < rows, c < cols.
  * Lays out k-contiguous operands: the frozen lm_head weight for dz @ W
  * (solution/cross_entropy.py:123, solution/fused_ce.py:143) and the LoRA factors.

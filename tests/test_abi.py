@@ -82,6 +82,30 @@ def test_rejected_arguments_return_codes(lib):
     # unknown output dtype
     assert lib.qlora_nf4_dequant(fake, 64, fake, 0, None, None, 0.0, 64, 1, fake, fake, 7,
                                  None) == -2
+    # grouped dequant: empty or oversized group, a weight the vector path cannot take, a
+    # 32-bit transposed output, a misaligned output block
+    W = _lib.Nf4Weight
+    one = (W * 1)(W(0x1000, 64, 64, 0x1000, 0x1000, 0x1000, 0.0, 64, 256, 0x1000))
+    assert lib.qlora_nf4_dequant_group(one, 0, 1, fake, 2, None) == -1
+    assert lib.qlora_nf4_dequant_group((W * 5)(*([one[0]] * 5)), 5, 1, fake, 2, None) == -1
+    assert lib.qlora_nf4_dequant_group(one, 1, 1, None, 2, None) == -1
+    assert lib.qlora_nf4_dequant_group((W * 1)(W(0x1000, 3, 6, 0x1000, 0x1000, 0x1000, 0.0, 64,
+                                                 256, 0x1000)), 1, 1, fake, 2, None) == -4
+    assert lib.qlora_nf4_dequant_group((W * 1)(W(0x1000, 64, 64, 0x1000, 0x1000, 0x1000, 0.0, 6,
+                                                 256, 0x1000)), 1, 1, fake, 2, None) == -1
+    assert lib.qlora_nf4_dequant_group((W * 1)(W(0x1000, 64, 64, 0x1000, None, 0x1000, 0.0, 64,
+                                                 256, 0x1000)), 1, 1, fake, 2, None) == -1
+    assert lib.qlora_nf4_dequant_group(one, 1, 1, fake, 7, None) == -2
+    t_one = (W * 1)(W(0x1000, 64, 128, 0x1000, 0x1000, 0x1000, 0.0, 64, 256, 0x1000))
+    assert lib.qlora_nf4_dequant_t_group(t_one, 1, 1, fake, 64, 0, None) == -2
+    assert lib.qlora_nf4_dequant_t_group(t_one, 1, 1, fake, 60, 2, None) == -4
+    assert lib.qlora_nf4_dequant_t_group(t_one, 1, 1, fake, 8, 2, None) == -1  # ld_out < rows
+    assert lib.qlora_nf4_dequant_t_group((W * 1)(W(0x1000, 64, 96, 0x1000, 0x1000, 0x1000, 0.0,
+                                                   64, 256, 0x1000)), 1, 1, fake, 64, 2,
+                                         None) == -4
+    assert lib.qlora_nf4_dequant_t_group((W * 1)(W(0x1000, 64, 128, 0x1000, 0x1000, 0x1000, 0.0,
+                                                   64, 256, 0x1008)), 1, 1, fake, 64, 2,
+                                         None) == -3
     # rmsnorm: bad dtype, zero columns
     assert lib.qlora_rmsnorm_fwd(fake, 9, 8, fake, 2, fake, 2, 8, fake, 4, 8, 1e-6, None) == -2
     assert lib.qlora_rmsnorm_fwd(fake, 2, 8, fake, 2, fake, 2, 8, fake, 4, 0, 1e-6, None) == -1

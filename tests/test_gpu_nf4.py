@@ -103,3 +103,71 @@ def test_transposed_dequant_bit_exact(shape, nested, blocksize):
     assert out_t.shape == (shape[1], shape[0])
     want_t = want_bf16.reshape(shape).T
     np.testing.assert_array_equal(bits16(out_t).cpu().numpy().view(np.uint16), want_t)
+
+
+def _concat_rows(outs_shapes, dtype):
+    rows = sum(r for r, _ in outs_shapes)
+    w = torch.empty((rows, outs_shapes[0][1]), dtype=dtype, device="cuda")
+    offs = np.cumsum([0] + [r for r, _ in outs_shapes])
+    return w, [w[offs[i]:offs[i + 1]] for i in range(len(outs_shapes))], offs
+
+
+@pytest.mark.parametrize("shapes,nested,blocksize,dtype", [
+    ([(96, 320), (40, 320), (8, 320)], True, 64, torch.bfloat16),
+    ([(64, 256), (72, 256), (128, 256), (8, 256)], False, 128, torch.float32),
+    ([(3584, 3584), (512, 3584), (512, 3584)], True, 64, torch.bfloat16),  # Qwen2.5-7B q/k/v
+])
+def test_grouped_dequant_bit_exact(shapes, nested, blocksize, dtype):
+    """One qlora_nf4_dequant_group launch writes every weight with the oracle's bits."""
+    print(f"nf4 dequant group {shapes} nested={nested} bs={blocksize} {dtype}", flush=True)
+    cases = [_case(sh, nested, blocksize, seed=20 + i) for i, sh in enumerate(shapes)]
+    w, outs, _ = _concat_rows(shapes, dtype)
+    items = [(c[0], c[1]) for c in cases]
+    assert nf4._groupable(items, outs, False)
+    nf4.dequantize_nf4_group(items, dtype, outs)
+    for c, out in zip(cases, outs):
+        if dtype == torch.float32:
+            np.testing.assert_array_equal(out.cpu().numpy().reshape(-1), c[3])
+        else:
+            np.testing.assert_array_equal(bits16(out).cpu().numpy().reshape(-1).view(np.uint16),
+                                          c[2])
+
+
+@pytest.mark.parametrize("shapes,nested,blocksize", [
+    ([(128, 256), (64, 256), (72, 256)], True, 64),       # a partial 64-row tile
+    ([(64, 512), (136, 256)], False, 64),                 # narrower second weight
+    ([(3584, 3584), (512, 3584), (512, 3584)], True, 64),  # Qwen2.5-7B q/k/v
+])
+def test_grouped_transposed_dequant_bit_exact(shapes, nested, blocksize):
+    """One qlora_nf4_dequant_t_group launch writes each W_i^T into its column block of a shared
+    [in_features, sum out_features] buffer with the oracle's bits, and leaves the rest alone."""
+    print(f"nf4 dequant_t group {shapes} nested={nested} bs={blocksize}", flush=True)
+    cases = [_case(sh, nested, blocksize, seed=30 + i) for i, sh in enumerate(shapes)]
+    kmax = max(c for _, c in shapes)
+    offs = np.cumsum([0] + [r for r, _ in shapes])
+    sentinel = torch.full((kmax, int(offs[-1])), 7.0, dtype=torch.bfloat16, device="cuda")
+    wt = sentinel.clone()
+    outs = [wt[:c, offs[i]:offs[i + 1]] for i, (_, c) in enumerate(shapes)]
+    items = [(c[0], c[1]) for c in cases]
+    assert nf4._groupable(items, outs, True)
+    nf4.dequantize_nf4_t_group(items, torch.bfloat16, outs)
+    for (r, c), case, out in zip(shapes, cases, outs):
+        want_t = case[2].reshape(r, c).T
+        np.testing.assert_array_equal(bits16(out).cpu().numpy().view(np.uint16), want_t)
+    mask = torch.ones_like(wt, dtype=torch.bool)
+    for i, (_, c) in enumerate(shapes):
+        mask[:c, offs[i]:offs[i + 1]] = False
+    assert torch.equal(wt[mask], sentinel[mask])
+
+
+def test_grouped_dequant_falls_back_for_mixed_nesting():
+    """Weights of different nesting are dequantised one launch each, with the same bits."""
+    print("nf4 dequant group mixed nesting", flush=True)
+    a = _case((64, 256), True, 64, seed=40)
+    b = _case((32, 256), False, 64, seed=41)
+    items = [(a[0], a[1]), (b[0], b[1])]
+    _, outs, _ = _concat_rows([(64, 256), (32, 256)], torch.bfloat16)
+    assert not nf4._groupable(items, outs, False)
+    nf4.dequantize_nf4_group(items, torch.bfloat16, outs)
+    for c, out in zip((a, b), outs):
+        np.testing.assert_array_equal(bits16(out).cpu().numpy().reshape(-1).view(np.uint16), c[2])
