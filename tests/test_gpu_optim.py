@@ -66,3 +66,35 @@ def test_fused_adamw_grads_set_to_none_and_other_dtypes():
         opt_fus.zero_grad(set_to_none=True)
     for a, b in zip(p_ref, p_fus):
         torch.testing.assert_close(b, a, rtol=2e-6, atol=1e-7)
+
+
+def test_fused_adamw_step_counters_skipped_grads_and_state_dict():
+    """The step counters (0-dim views of one buffer) advance only for parameters that have a
+    gradient, in mixed groups the kernel and torch's step share, and survive a state-dict round
+    trip into a new optimizer; values and counts stay torch's."""
+    print("fused adamw counters", flush=True)
+    base = _params(3)[:4]
+    p_ref = [torch.nn.Parameter(t.clone()) for t in base] + [
+        torch.nn.Parameter(torch.randn(9, device="cuda", dtype=torch.bfloat16))]
+    p_fus = [torch.nn.Parameter(t.detach().clone()) for t in p_ref]
+    opt_ref = torch.optim.AdamW(p_ref, lr=2e-3, weight_decay=0.01, foreach=False)
+    opt_fus = FusedAdamW(p_fus, lr=2e-3, weight_decay=0.01)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    for step in range(6):
+        if step == 3:  # continue in a new optimizer from the saved state
+            sd = opt_fus.state_dict()
+            opt_fus = FusedAdamW(p_fus, lr=2e-3, weight_decay=0.01)
+            opt_fus.load_state_dict(sd)
+        for i, (a, b) in enumerate(zip(p_ref, p_fus)):
+            skip = (i == 1 and step in (1, 4)) or (i == 4 and step == 2)
+            grad = None if skip else torch.randn(a.shape, device="cuda", generator=g,
+                                                 dtype=torch.float32).to(a.dtype)
+            a.grad = None if grad is None else grad.clone()
+            b.grad = None if grad is None else grad.clone()
+        opt_ref.step()
+        opt_fus.step()
+        for a, b in zip(p_ref, p_fus):
+            assert float(opt_fus.state[b]["step"]) == float(opt_ref.state[a]["step"])
+            tol = dict(rtol=2e-6, atol=1e-7) if a.dtype == torch.float32 else {}
+            torch.testing.assert_close(b, a, **tol)
+    assert [float(opt_fus.state[b]["step"]) for b in p_fus] == [6.0, 4.0, 6.0, 6.0, 5.0]

@@ -23,9 +23,10 @@ def test_groups_cover_rows_within_budget(n, vocab, chunk):
         assert groups[-1][1] - groups[-1][0] <= groups[0][1] - groups[0][0]
 
 
-def test_qwen_shapes_run_as_one_group():
-    # 8192 x 151936 (2.49 GB of bf16 logits) and the 7B step's 4096 x 152064 fit the budget
-    assert vocab_pass.plan_groups(8192, 151936, 512) == [(0, 8192)]
+def test_qwen_shapes_group_sizes():
+    # 8192 x 151936 (2.49 GB of bf16 logits) never lives whole: two groups of 4096 rows; the 7B
+    # step's 4096 x 152064 (1.25 GB) is one group
+    assert vocab_pass.plan_groups(8192, 151936, 512) == [(0, 4096), (4096, 8192)]
     assert vocab_pass.plan_groups(4096, 152064, 512) == [(0, 4096)]
     # a budget of one chunk gives the reference's 512-row chunks
     assert vocab_pass.plan_groups(2000, 151936, 512, budget=1) == \
