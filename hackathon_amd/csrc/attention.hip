@@ -221,6 +221,14 @@ QL_DEV void wait_all_barrier() {
   QL_DMA_SETTLE();
 }
 
+// This thread's ordinary global loads (the fragments a kernel keeps in registers across its
+// block loop) have landed, said with a wait the compiler's wait-count pass sees. That pass
+// cannot read wait_all_barrier's assembly: without this it counts those loads as pending in
+// every block and waits for each before its first use there, and since vmcnt completes in
+// issue order, each such wait also drains the next block's DMA issued since, so the prefetch
+// no longer runs under the block's math.
+QL_DEV void wait_vm_visible() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
 // Index differences used by the branch-free masks, clamped into int range.
 QL_DEV int clamp_rel(int64_t x) { return (int)(x < -4096 ? -4096 : x > 4096 ? 4096 : x); }
 
@@ -395,6 +403,7 @@ void attn_fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict_
   vdma.init(sh.vs_s, wave, lane);
   kdma.issue(kbase, sh.ks_s, 0, S, smem);
   vdma.issue(vbase, sh.vs_s, 0, S, smem + kTileBytes);
+  wait_vm_visible();  // the q fragments
   for (int j = 0; j < nkv; ++j) {
     // block j's tiles are in LDS, and every wave is past block j - 1, whose stage the DMA
     // issued in this step overwrites
@@ -588,16 +597,22 @@ void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
   TileDma qdma, odma;
   qdma.init(sh.qs_s, wave, lane);
   odma.init(sh.os_s, wave, lane);
-  // lse * log2e and Delta of a query block: thread t < 128 stages row t & 63 of one of them
+  // lse * log2e and Delta of a query block: thread t < 128 stages row t & 63 of one of them.
+  // The load goes out before the block's math and the lse is scaled only where it is staged,
+  // after that math, so no wave waits on the load's latency inside the block.
   const int t = threadIdx.x;
   auto row_stat = [&](int qb) -> float {
     const int64_t q = (int64_t)qb * kRows + (t & 63);
     const int64_t qc = q < S ? q : S - 1;
-    return t < 64 ? lse_row[qc] * kLog2e : dl_row[qc];
+    return t < 64 ? lse_row[qc] : dl_row[qc];
+  };
+  auto stage_stat = [&](char* stage, float v) {
+    reinterpret_cast<float*>(stage + 2 * kTileBytes)[t] = t < 64 ? v * kLog2e : v;
   };
   qdma.issue(qbase, sh.qs_s, (int64_t)kb * kRows, S, smem);
   odma.issue(obase, sh.os_s, (int64_t)kb * kRows, S, smem + kTileBytes);
-  if (t < 128) reinterpret_cast<float*>(smem + 2 * kTileBytes)[t] = row_stat(kb);
+  if (t < 128) stage_stat(smem, row_stat(kb));
+  wait_vm_visible();  // the k and v fragments
   for (int qb = kb; qb < n_qb; ++qb) {
     wait_all_barrier();
     const int it = qb - kb;
@@ -612,7 +627,7 @@ void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
     const int qlim = clamp_rel(S - (qrow0 + 4 * fq));
     dkdv_block<DT>(st, cur, nxt, more, qdma, odma, qbase, obase, sh.qs_s, sh.os_s, qrow0, S,
                    need_mask, kq_rel, qlim, sl2, lane);
-    if (more && t < 128) reinterpret_cast<float*>(nxt + 2 * kTileBytes)[t] = stat;
+    if (more && t < 128) stage_stat(nxt, stat);
   }
 
   const int64_t key = key0w + fr;
@@ -804,6 +819,7 @@ void attn_bwd_dq(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   vdma.init(sh.vs_s, wave, lane);
   kdma.issue(kbase, sh.ks_s, 0, S, smem);
   vdma.issue(vbase, sh.vs_s, 0, S, smem + kTileBytes);
+  wait_vm_visible();  // the q and dO fragments, lse and Delta
   for (int j = 0; j < nkv; ++j) {
     wait_all_barrier();
     char* cur = smem + (j & 1) * 2 * kTileBytes;
