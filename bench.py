@@ -504,6 +504,156 @@ def bench_ce(torch, res, reps=3):
                                            frac_mfma=round(fl / t / 1e12 / BF16_PEAK_TFLOPS, 3))
 
 
+def _event_time(fn, torch, calls=20, warm=3):
+    """Seconds per call of `fn`, timed with events around `calls` back-to-back calls (for calls
+    that allocate their outputs, which a captured graph would keep fixed)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(calls):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / calls
+
+
+def _flops(name, t, flop, res):
+    res[name] = dict(us=round(t * 1e6, 2), tflops=round(flop / t / 1e12, 1),
+                     frac_mfma=round(flop / t / 1e12 / BF16_PEAK_TFLOPS, 3))
+
+
+def bench_next_rows(torch, res):
+    """The kernels beside the six, at the shapes the Qwen2.5-7B step runs them:
+    - causal flash attention, 2 x 2048 tokens, 28 query / 4 kv heads, head_dim 128, bf16:
+      forward 4 B HQ S^2 D / 2 FLOP, backward 2.5x that (the algorithmic count; the kernels
+      recompute P in both backward passes); inputs resident (29 MB of q);
+    - the residual-add RMSNorm forward and the backward with the residual gradient, 4096 x
+      3584 bf16, rotated sets;
+    - the grouped NF4 dequant of the q|k|v weights (3584 + 512 + 512 rows x 3584), plain and
+      transposed, rotated sets;
+    - the GPU NF4 quantiser (18944 x 3584 bf16 -> NF4 bs64 with double-quant absmax);
+    - the fused AdamW over the 7B adapter set (392 fp32 tensors, 40.4 M values: p, g, m, v
+      read and p, m, v written, 28 B a value)."""
+    import math as _m
+
+    from hackathon_amd import _lib, attention, nf4, quant, qlora_step
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    B, S, HQ, HK, D = 2, 2048, 28, 4, 128
+    q = torch.randn(B, S, HQ, D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+    k = torch.randn(B, S, HK, D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn(B, S, HK, D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+    do = torch.randn(B, S, HQ, D, device=dev, generator=g).to(torch.bfloat16)
+    scale = 1.0 / _m.sqrt(D)
+    o, lse = attention.attn_fwd(q, k, v, scale)
+    fl = 4 * B * HQ * S * S * D / 2
+    _flops("attn_fwd_2x2048x28q4kvx128", _event_time(lambda: attention.attn_fwd(q, k, v, scale),
+                                                     torch), fl, res)
+    _flops("attn_bwd_2x2048x28q4kvx128",
+           _event_time(lambda: attention.attn_bwd(q, k, v, o, lse, do, scale), torch), 2.5 * fl,
+           res)
+    del q, k, v, do, o, lse
+
+    M, N = 4096, 3584
+    w = (1 + 0.1 * torch.randn(N, device=dev, generator=g)).to(torch.bfloat16)
+    fwd_bytes = 4 * M * N * 2 + N * 2 + M * 4        # x, d in; h, y out
+    bwd_bytes = 4 * M * N * 2 + N * 2 + M * 4        # dy, x, dres in; dx out
+    sets = _rotated_sets(bwd_bytes)
+    bufs = [tuple(torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16) for _ in range(4))
+            + (torch.rand(M, device=dev, generator=g) + 0.5, torch.empty(M, N, device=dev,
+                                                                        dtype=torch.bfloat16))
+            for _ in range(sets)]
+
+    def fwd(b):
+        x, d, h, y, rstd, _ = b
+        _lib.call("qlora_add_rmsnorm_fwd", x.data_ptr(), d.data_ptr(), 2, N, N, w.data_ptr(), 2,
+                  h.data_ptr(), N, y.data_ptr(), 2, N, rstd.data_ptr(), M, N, 1e-6,
+                  _lib.stream_of(x))
+
+    def bwd(b):
+        dy, x, dres, _, rstd, dx = b
+        _lib.call("qlora_rmsnorm_bwd_residual", dy.data_ptr(), 2, N, x.data_ptr(), 2, N,
+                  w.data_ptr(), 2, rstd.data_ptr(), dres.data_ptr(), N, dx.data_ptr(), N, M, N,
+                  _lib.stream_of(x))
+    calls = 2 * sets
+    _rate("add_rmsnorm_fwd_4096x3584", _graph_time(
+        [lambda b=bufs[i % sets]: fwd(b) for i in range(calls)], torch, 3), fwd_bytes, res)
+    _rate("rmsnorm_bwd_residual_4096x3584", _graph_time(
+        [lambda b=bufs[i % sets]: bwd(b) for i in range(calls)], torch, 3), bwd_bytes, res)
+    for name in ("add_rmsnorm_fwd_4096x3584", "rmsnorm_bwd_residual_4096x3584"):
+        res[name]["rotated_sets"] = sets
+    del bufs
+
+    shapes = [(3584, 3584), (512, 3584), (512, 3584)]
+    rows = sum(r for r, _ in shapes)
+    items = [quant.quantize_nf4(torch.randn(sh, device=dev, generator=g) * 0.02, 64, True)
+             for sh in shapes]
+    nbytes = sum(nf4_algorithmic_bytes(r * c) for r, c in shapes)
+    sets = _rotated_sets(nbytes, minimum=4)
+    wsets = [(torch.empty(rows, N, device=dev, dtype=torch.bfloat16),
+              torch.empty(N, rows, device=dev, dtype=torch.bfloat16)) for _ in range(sets)]
+    offs = [0, 3584, 4096, 4608]
+
+    def plain(i):
+        wb = wsets[i % sets][0]
+        nf4.dequantize_nf4_group(items, torch.bfloat16, [wb[offs[j]:offs[j + 1]] for j in range(3)])
+
+    def trans(i):
+        wt = wsets[i % sets][1]
+        nf4.dequantize_nf4_t_group(items, torch.bfloat16,
+                                   [wt[:, offs[j]:offs[j + 1]] for j in range(3)])
+    _rate("nf4_dequant_group_qkv_7b", _graph_time([lambda i=i: plain(i) for i in range(2 * sets)],
+                                                   torch, 3), nbytes, res)
+    _rate("nf4_dequant_t_group_qkv_7b", _graph_time([lambda i=i: trans(i) for i in range(2 * sets)],
+                                                     torch, 3), nbytes, res)
+    del wsets, items
+
+    n = 18944 * 3584
+    wq = (torch.randn(n, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    packed = torch.empty(n // 2, dtype=torch.uint8, device=dev)
+    nb = n // 64
+    absmax = torch.empty(nb, dtype=torch.uint8, device=dev)
+    absmax2 = torch.empty(_m.ceil(nb / 256), dtype=torch.float32, device=dev)
+    offset = torch.empty((), dtype=torch.float32, device=dev)
+    code, code2 = quant.nf4_code(dev), quant.dynamic_map(True).to(dev)
+    ws, ws_bytes = _lib.workspace("qlora_nf4_quantize_workspace_size", n, 64, 1, device=dev)
+
+    def qz():
+        _lib.call("qlora_nf4_quantize", wq.data_ptr(), 2, n, 64, 1, 256, code.data_ptr(),
+                  code2.data_ptr(), packed.data_ptr(), absmax.data_ptr(), absmax2.data_ptr(),
+                  offset.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_of(wq))
+    qbytes = 2 * n + n // 2 + nb + 4 * _m.ceil(nb / 256)
+    _rate("nf4_quantize_18944x3584", _event_time(qz, torch), qbytes, res)
+    del wq, packed, absmax, ws
+
+    cfg = qlora_step.qwen2_config()
+    H, I, KV = cfg.hidden_size, cfg.intermediate_size, cfg.num_key_value_heads * 128
+    shapes = []
+    for _ in range(cfg.num_hidden_layers):
+        for out_f, in_f in ((H, H), (KV, H), (KV, H), (H, H), (I, H), (I, H), (H, I)):
+            shapes += [(16, in_f), (out_f, 16)]
+    tensors = [[torch.randn(sh, device=dev, generator=g) * 0.01 for _ in range(4)]
+               for sh in shapes]
+    for t in tensors:
+        t[3].abs_()
+    chunk = int(_lib.load().qlora_adamw_chunk_elems())
+    table, first = [], 0
+    for p_, g_, m_, v_ in tensors:
+        table.append([p_.data_ptr(), g_.data_ptr(), m_.data_ptr(), v_.data_ptr(), p_.numel(), first])
+        first += (p_.numel() + chunk - 1) // chunk
+    table_d = torch.tensor(table, dtype=torch.int64).to(dev)
+    values = sum(t[0].numel() for t in tensors)
+
+    def adamw():
+        _lib.call("qlora_adamw_fp32", table_d.data_ptr(), len(tensors), first, 1.0, 0.999, 0.1,
+                  0.001, 1e-4, 0.05, 1e-8, _lib.stream_of(table_d))
+    _rate("adamw_fp32_7b_adapters", _graph_time([adamw] * 10, torch, 3), 28 * values, res)
+    res["adamw_fp32_7b_adapters"]["values"] = values
+
+
 def bench_kernels(torch):
     """Device time per call and roofline fraction of the other kernels at their configs."""
     res = {}
@@ -513,6 +663,7 @@ def bench_kernels(torch):
     bench_gemms(torch, res)
     bench_ce(torch, res)
     res["qwen25_7b_mlp_lora_4096tok"] = bench_mlp(torch)
+    bench_next_rows(torch, res)
     return res
 
 
@@ -524,6 +675,7 @@ WORKLOADS = {
     "ce": lambda torch, res: bench_ce(torch, res),
     "mlp": lambda torch, res: res.update(qwen25_7b_mlp_lora_4096tok=bench_mlp(torch)),
     "nf4_small": lambda torch, res: res.update(nf4_4864x896=bench_nf4_small(torch)),
+    "next": lambda torch, res: bench_next_rows(torch, res),
 }
 
 

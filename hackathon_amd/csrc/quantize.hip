@@ -2,7 +2,8 @@
 // feeds the dequant kernel (the weight format of solution/nf4.py:73-86, which the reference
 // takes from bitsandbytes' quantize_4bit; this kernel produces the same layout without it).
 //
-//   stage 1  one thread per NF4 block of `blocksize` weights: absmax = max |w|, codes =
+//   stage 1  per NF4 block of `blocksize` weights (the lanes of a wave sharing each block when
+//            blocksize is a power of two from 16 to 512, else one thread a block): absmax = max |w|, codes =
 //            nearest NF4 level of w * (1 / absmax) (fp32 multiply by the correctly rounded
 //            reciprocal; ties go to the lower level, i.e. the count of level midpoints
 //            strictly below the value), two codes per byte, high nibble first.
@@ -51,6 +52,63 @@ __global__ __launch_bounds__(kThreads) void nf4_quantize_blocks(
     packed[j / 2] = (uint8_t)((hi << 4) | lo);
   }
   absmax[b] = am;
+}
+
+// Stage 1 with the lanes of a wave sharing the blocks (blocksize = 8 LPB, a power of two from
+// 16 to 512): lane l takes the 8 consecutive weights of group g0 + l (one 16-B load of 16-bit
+// weights, so a wave's load instruction reads 1 KiB contiguous), the LPB lanes of a block
+// combine their maxima with butterflies, and each lane writes its 8 codes as one 32-bit word.
+// The per-weight arithmetic is nf4_quantize_blocks': the same absmax, reciprocal, product and
+// count of midpoints strictly below (counted by 15 comparisons, which equals the binary
+// search's lower bound on the sorted midpoints, NaN included), so the bytes are identical.
+template <int IT, int LPB>
+__global__ __launch_bounds__(kThreads) void nf4_quantize_lanes(
+    const typename Elem<IT>::T* __restrict__ w, int64_t n, int64_t n_blocks,
+    const float* __restrict__ nf4_code, uint8_t* __restrict__ packed, float* __restrict__ absmax) {
+#pragma clang fp contract(off)
+  float mid[15];
+#pragma unroll
+  for (int k = 0; k < 15; ++k) mid[k] = (nf4_code[k] + nf4_code[k + 1]) * 0.5f;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t n_waves = (int64_t)gridDim.x * (kThreads / 64);
+  const int64_t n_groups = (n + 7) / 8;
+  for (int64_t g0 = wave * 64; g0 < n_groups; g0 += n_waves * 64) {  // wave-uniform bounds
+    const int64_t grp = g0 + lane;
+    const int64_t j0 = 8 * grp;
+    const bool whole = j0 + 8 <= n;
+    float x[8];
+    if (whole) {
+      Vec8<IT>::load(w + j0, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = j0 + e < n ? Elem<IT>::load(w, j0 + e) : 0.f;
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[e]));
+#pragma unroll
+    for (int off = 1; off < LPB; off <<= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float inv = am > 0.f ? 1.0f / am : 0.f;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = x[e] * inv;
+      uint32_t c = 0;
+#pragma unroll
+      for (int k = 0; k < 15; ++k) c += mid[k] < v ? 1u : 0u;
+      word |= c << (8 * (e >> 1) + ((e & 1) ? 0 : 4));  // weight 2i: high nibble of byte i
+    }
+    if (whole) {
+      *reinterpret_cast<uint32_t*>(packed + 4 * grp) = word;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (j0 + 2 * i < n) packed[4 * grp + i] = (uint8_t)(word >> (8 * i));
+    }
+    const int64_t blk = grp / LPB;
+    if (lane % LPB == 0 && blk < n_blocks) absmax[blk] = am;
+  }
 }
 
 // fp64 partial sums of x[0..n): one per workgroup.
@@ -126,11 +184,34 @@ extern "C" int qlora_nf4_quantize(const void* w, int w_dtype, int64_t n, int blo
     return QL_EINVAL;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* am = nested ? static_cast<float*>(workspace) : static_cast<float*>(absmax);
-  const dim3 g1((unsigned)((nb + kThreads - 1) / kThreads));
-  QL_DISPATCH_DTYPE(w_dtype, DT,
-                    hipLaunchKernelGGL((nf4_quantize_blocks<DT>), g1, dim3(kThreads), 0, s,
-                                       static_cast<const typename Elem<DT>::T*>(w), n,
-                                       (int64_t)blocksize, nb, nf4_code, packed, am));
+  const int lpb = blocksize / 8;
+  const bool lanes = (blocksize & (blocksize - 1)) == 0 && blocksize >= 16 && blocksize <= 512 &&
+                     ql_aligned(w, 16) && ql_aligned(packed, 4);
+  if (lanes) {
+    const int64_t waves = (n / 8 + 64) / 64;
+    const int64_t wgs = (waves + kThreads / 64 - 1) / (kThreads / 64);
+    const dim3 g1((unsigned)(wgs < 65536 ? wgs : 65536));
+#define QL_QZ(LPB)                                                                               \
+  QL_DISPATCH_DTYPE(w_dtype, DT,                                                                 \
+                    hipLaunchKernelGGL((nf4_quantize_lanes<DT, LPB>), g1, dim3(kThreads), 0, s,  \
+                                       static_cast<const typename Elem<DT>::T*>(w), n, nb,       \
+                                       nf4_code, packed, am))
+    switch (lpb) {
+      case 2: QL_QZ(2); break;
+      case 4: QL_QZ(4); break;
+      case 8: QL_QZ(8); break;
+      case 16: QL_QZ(16); break;
+      case 32: QL_QZ(32); break;
+      default: QL_QZ(64); break;
+    }
+#undef QL_QZ
+  } else {
+    const dim3 g1((unsigned)((nb + kThreads - 1) / kThreads));
+    QL_DISPATCH_DTYPE(w_dtype, DT,
+                      hipLaunchKernelGGL((nf4_quantize_blocks<DT>), g1, dim3(kThreads), 0, s,
+                                         static_cast<const typename Elem<DT>::T*>(w), n,
+                                         (int64_t)blocksize, nb, nf4_code, packed, am));
+  }
   if (!nested) return ql_launch_status();
   double* part = reinterpret_cast<double*>(static_cast<char*>(workspace) +
                                            align256(nb * (int64_t)sizeof(float)));

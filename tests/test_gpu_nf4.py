@@ -70,6 +70,9 @@ def test_dequant_full_qwen25_7b_gate_shape_bit_exact():
     ((96, 320), torch.float16, False, 64),
     ((33, 70), torch.float32, True, 6),           # partial last block, odd blocksize multiple
     ((7, 6), torch.bfloat16, True, 64),           # fewer weights than one block
+    ((65, 130), torch.bfloat16, True, 128),       # partial last block of the lane-shared path
+    ((40, 24), torch.float16, False, 16),         # two lanes a block
+    ((96, 96), torch.float32, True, 512),         # 64 lanes a block, a partial last block
 ])
 def test_quantizer_kernel_matches_cpu_bytes(shape, dtype, nested, bs):
     """The GPU quantiser kernel and the CPU torch quantiser give identical packed codes, absmax
