@@ -58,56 +58,85 @@ __global__ __launch_bounds__(kThreads) void nf4_quantize_blocks(
 // 16 to 512): lane l takes the 8 consecutive weights of group g0 + l (one 16-B load of 16-bit
 // weights, so a wave's load instruction reads 1 KiB contiguous), the LPB lanes of a block
 // combine their maxima with butterflies, and each lane writes its 8 codes as one 32-bit word.
-// The per-weight arithmetic is nf4_quantize_blocks': the same absmax, reciprocal, product and
-// count of midpoints strictly below (counted by 15 comparisons, which equals the binary
-// search's lower bound on the sorted midpoints, NaN included), so the bytes are identical.
+// The per-weight arithmetic is nf4_quantize_blocks': the same absmax, reciprocal and product,
+// and the same count of midpoints strictly below the product v, found by table: the 256
+// buckets [i / 128 - 1, (i + 1) / 128 - 1) each hold at most one midpoint (the midpoints are
+// more than 1/128 apart), so the count is the number of midpoints below the bucket plus
+// whether the bucket's own midpoint is below v. The bucket is floor(128 v), exact in fp32,
+// clamped to the table (|v| exceeds 1 by at most rounding; NaN goes to bucket 0 and count 0,
+// as in the binary search), so the bytes are identical; the GPU tests check them at every
+// bucket edge and midpoint and one ulp either side.
+static_assert(kThreads == 256, "nf4_quantize_lanes builds its 256-bucket table one bucket a thread");
+
 template <int IT, int LPB>
 __global__ __launch_bounds__(kThreads) void nf4_quantize_lanes(
     const typename Elem<IT>::T* __restrict__ w, int64_t n, int64_t n_blocks,
     const float* __restrict__ nf4_code, uint8_t* __restrict__ packed, float* __restrict__ absmax) {
 #pragma clang fp contract(off)
-  float mid[15];
+  __shared__ float2 lut[256];  // {the bucket's midpoint or +inf, midpoints below the bucket}
+  {
+    float mid[15];
 #pragma unroll
-  for (int k = 0; k < 15; ++k) mid[k] = (nf4_code[k] + nf4_code[k + 1]) * 0.5f;
+    for (int k = 0; k < 15; ++k) mid[k] = (nf4_code[k] + nf4_code[k + 1]) * 0.5f;
+    const int t = threadIdx.x;  // kThreads == 256: one bucket a thread
+    const float lo = (float)t / 128.f - 1.f, hi = (float)(t + 1) / 128.f - 1.f;
+    float below = 0.f, m = INFINITY;
+#pragma unroll
+    for (int k = 0; k < 15; ++k) {
+      below += mid[k] < lo ? 1.f : 0.f;
+      if (mid[k] >= lo && mid[k] < hi) m = mid[k];
+    }
+    lut[t] = make_float2(m, below);
+  }
+  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
   const int64_t n_waves = (int64_t)gridDim.x * (kThreads / 64);
   const int64_t n_groups = (n + 7) / 8;
-  for (int64_t g0 = wave * 64; g0 < n_groups; g0 += n_waves * 64) {  // wave-uniform bounds
-    const int64_t grp = g0 + lane;
-    const int64_t j0 = 8 * grp;
-    const bool whole = j0 + 8 <= n;
-    float x[8];
-    if (whole) {
-      Vec8<IT>::load(w + j0, x);
-    } else {
+  // two 64-group spans a step, both loaded before either is coded
+  for (int64_t g0 = wave * 128; g0 < n_groups; g0 += n_waves * 128) {  // wave-uniform bounds
+    float xs[2][8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = j0 + e < n ? Elem<IT>::load(w, j0 + e) : 0.f;
+    for (int u = 0; u < 2; ++u) {
+      const int64_t j0 = 8 * (g0 + 64 * u + lane);
+      if (j0 + 8 <= n) {
+        Vec8<IT>::load(w + j0, xs[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xs[u][e] = j0 + e < n ? Elem<IT>::load(w, j0 + e) : 0.f;
+      }
     }
-    float am = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[e]));
+    for (int u = 0; u < 2; ++u) {
+      const int64_t grp = g0 + 64 * u + lane;
+      const int64_t j0 = 8 * grp;
+      const bool whole = j0 + 8 <= n;
+      const float* x = xs[u];
+      float am = 0.f;
 #pragma unroll
-    for (int off = 1; off < LPB; off <<= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
-    const float inv = am > 0.f ? 1.0f / am : 0.f;
-    uint32_t word = 0;
+      for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[e]));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = x[e] * inv;
-      uint32_t c = 0;
+      for (int off = 1; off < LPB; off <<= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+      const float inv = am > 0.f ? 1.0f / am : 0.f;
+      uint32_t word = 0;
 #pragma unroll
-      for (int k = 0; k < 15; ++k) c += mid[k] < v ? 1u : 0u;
-      word |= c << (8 * (e >> 1) + ((e & 1) ? 0 : 4));  // weight 2i: high nibble of byte i
+      for (int e = 0; e < 8; ++e) {
+        const float v = x[e] * inv;
+        const float f = fminf(fmaxf(floorf(v * 128.f), -128.f), 127.f);
+        const float2 b = lut[(int)f + 128];
+        const uint32_t c = (uint32_t)b.y + (b.x < v ? 1u : 0u);
+        word |= c << (8 * (e >> 1) + ((e & 1) ? 0 : 4));  // weight 2i: high nibble of byte i
+      }
+      if (whole) {
+        *reinterpret_cast<uint32_t*>(packed + 4 * grp) = word;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (j0 + 2 * i < n) packed[4 * grp + i] = (uint8_t)(word >> (8 * i));
+      }
+      const int64_t blk = grp / LPB;
+      if (lane % LPB == 0 && blk < n_blocks) absmax[blk] = am;
     }
-    if (whole) {
-      *reinterpret_cast<uint32_t*>(packed + 4 * grp) = word;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (j0 + 2 * i < n) packed[4 * grp + i] = (uint8_t)(word >> (8 * i));
-    }
-    const int64_t blk = grp / LPB;
-    if (lane % LPB == 0 && blk < n_blocks) absmax[blk] = am;
   }
 }
 
@@ -126,13 +155,15 @@ __global__ __launch_bounds__(kThreads) void sum_f64_partials(const float* __rest
   if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
 }
 
-// offset = (float)(sum(part) / n), one thread.
-__global__ void mean_from_partials(const double* __restrict__ part, int n_part, int64_t n,
-                                   float* __restrict__ offset) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// offset = (float)(sum(part) / n), one wave (the fp64 sum is exact, so in any order).
+__global__ __launch_bounds__(64) void mean_from_partials(const double* __restrict__ part,
+                                                         int n_part, int64_t n,
+                                                         float* __restrict__ offset) {
   double s = 0.0;
-  for (int i = 0; i < n_part; ++i) s += part[i];
-  offset[0] = (float)(s / (double)n);
+  for (int i = threadIdx.x; i < n_part; i += 64) s += part[i];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (threadIdx.x == 0) offset[0] = (float)(s / (double)n);
 }
 
 // One workgroup per block of 256 values of (absmax - offset): dynamic-map codes + absmax2.
@@ -188,7 +219,7 @@ extern "C" int qlora_nf4_quantize(const void* w, int w_dtype, int64_t n, int blo
   const bool lanes = (blocksize & (blocksize - 1)) == 0 && blocksize >= 16 && blocksize <= 512 &&
                      ql_aligned(w, 16) && ql_aligned(packed, 4);
   if (lanes) {
-    const int64_t waves = (n / 8 + 64) / 64;
+    const int64_t waves = (n / 8 + 128) / 128;
     const int64_t wgs = (waves + kThreads / 64 - 1) / (kThreads / 64);
     const dim3 g1((unsigned)(wgs < 65536 ? wgs : 65536));
 #define QL_QZ(LPB)                                                                               \

@@ -90,6 +90,27 @@ def test_quantizer_kernel_matches_cpu_bytes(shape, dtype, nested, bs):
         assert torch.equal(s_cpu.state2.code, s_gpu.state2.code.cpu())
 
 
+@pytest.mark.parametrize("nested", [False, True])
+def test_quantizer_codes_at_bucket_edges_and_midpoints(nested):
+    """The GPU quantiser finds each code through a 256-bucket table (floor(128 v) picks the
+    bucket, one midpoint at most per bucket). Products exactly on a bucket edge or an NF4
+    midpoint, and one ulp either side, give the CPU quantiser's bytes: every block holds 1.0
+    (absmax 1, so v is the weight itself) and 63 such values."""
+    print(f"nf4 quantize edges nested={nested}", flush=True)
+    code = np.array(quant.NF4_CODE, dtype=np.float32)
+    mids = ((code[:-1] + code[1:]) * np.float32(0.5)).astype(np.float32)
+    edges = (np.arange(257, dtype=np.float32) / np.float32(128) - np.float32(1)).astype(np.float32)
+    pts = np.concatenate([edges, mids, np.float32([0.0, -0.0])])
+    vals = np.concatenate([pts, np.nextafter(pts, np.float32(-2)), np.nextafter(pts, np.float32(2))])
+    vals = np.clip(vals, -1, 1).astype(np.float32)
+    vals = np.concatenate([vals, np.zeros((-len(vals)) % 63, np.float32)]).reshape(-1, 63)
+    w = torch.from_numpy(np.concatenate([np.ones((len(vals), 1), np.float32), vals], axis=1))
+    p_cpu, s_cpu = quant.quantize_nf4(w, 64, compress_statistics=nested)
+    p_gpu, s_gpu = quant.quantize_nf4(w.cuda(), 64, compress_statistics=nested)
+    assert torch.equal(p_cpu, p_gpu.cpu())
+    assert torch.equal(s_cpu.absmax, s_gpu.absmax.cpu())
+
+
 @pytest.mark.parametrize("shape,nested,blocksize", [
     ((384, 256), True, 64),
     ((136, 512), True, 64),       # a partial 64-row tile
