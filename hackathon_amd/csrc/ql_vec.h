@@ -71,6 +71,37 @@ template <> struct Vec8<QL_F32> {
   }
 };
 
+// The register image of 8 elements as loaded (16 B for 16-bit types, 32 B for fp32), kept
+// packed until it is unpacked: a kernel can issue every load of a row before its first use
+// and hold the row in half the registers 8 floats a chunk would take.
+template <int DT> struct Raw8 {
+  uint4 r;
+  QL_DEV void load(const uint16_t* p) { r = *reinterpret_cast<const uint4*>(p); }
+  QL_DEV void load_bytes(const char* p) { r = *reinterpret_cast<const uint4*>(p); }
+  QL_DEV void store_bytes(char* p) const { *reinterpret_cast<uint4*>(p) = r; }
+  QL_DEV void unpack(float* v) const { Vec8<DT>::unpack(r, v); }
+  // An empty register barrier: the value is unchanged, but the compiler must unpack it again
+  // afterwards instead of keeping an earlier unpacked copy (8 registers a chunk) alive.
+  QL_DEV void opaque() { asm volatile("" : "+v"(r.x), "+v"(r.y), "+v"(r.z), "+v"(r.w)); }
+};
+template <> struct Raw8<QL_F32> {
+  float4 a, b;
+  QL_DEV void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  QL_DEV void load_bytes(const char* p) { load(reinterpret_cast<const float*>(p)); }
+  QL_DEV void store_bytes(char* p) const {
+    reinterpret_cast<float4*>(p)[0] = a;
+    reinterpret_cast<float4*>(p)[1] = b;
+  }
+  QL_DEV void unpack(float* v) const {
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  QL_DEV void opaque() {}  // already 8 registers of fp32: nothing to save
+};
+
 // Scalar access with a runtime dtype tag (uniform across the wave: no divergence).
 QL_DEV float load_any(const void* p, int dt, int64_t i) {
   if (dt == QL_F32) return static_cast<const float*>(p)[i];
