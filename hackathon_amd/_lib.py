@@ -77,6 +77,9 @@ _SIGNATURES = {
     "qlora_gemm_nf4": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_ptr,
                        _c_ptr, _c_f32, _c_int, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr,
                        _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_f32, _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_wgrad_diag": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                              _c_i64p, ctypes.POINTER(ctypes.c_float), _c_ptr, _c_ptr, _c_i64,
+                              _c_ptr],
     "qlora_lora_wgrad": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
                          _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_wgrad_noalloc": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
@@ -110,6 +113,7 @@ _SIZE_QUERIES = {
     "qlora_gemm_nf4_workspace_size": [_c_i64, _c_i64, _c_i64],
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64, _c_int],
+    "qlora_lora_wgrad_diag_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_swiglu_bwd_lora_down_workspace_size": [_c_i64, _c_i64],
     "qlora_swiglu_bwd_lora_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_swiglu_fwd_lora_down_workspace_size": [_c_i64, _c_i64],
@@ -126,7 +130,7 @@ class KernelLibraryMissing(RuntimeError):
     pass
 
 
-ABI_VERSION = 2  # qlora_abi_version() of the library these signatures describe
+ABI_VERSION = 3  # qlora_abi_version() of the library these signatures describe
 
 
 def load():

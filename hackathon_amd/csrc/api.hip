@@ -1,7 +1,7 @@
 // Library identification and status text for the C-ABI.
 #include "ql_common.h"
 
-extern "C" int qlora_abi_version(void) { return 2; }
+extern "C" int qlora_abi_version(void) { return 3; }
 
 extern "C" const char* qlora_strerror(int status) {
   switch (status) {

@@ -1085,6 +1085,38 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict
   }
 }
 
+// The diagonal blocks of a multi-slot weight gradient: out[n, c] = alpha_q * sum over splits
+// (in split order) of ws[split][n][16 q + c], for the slot q whose columns [off_q, off_{q+1})
+// hold n. With Q the concatenated output gradient of several adapters and P^T their stacked
+// u^T, that is each adapter's lora_B gradient s_q g_q^T u_q, stacked as [N, 16].
+struct WgradDiag {
+  int64_t off[kMaxSlots + 1];
+  float alpha[kMaxSlots];
+  int slots;
+};
+
+__global__ __launch_bounds__(256) void lora_wgrad_reduce_diag(const float* __restrict__ ws,
+                                                              int splits, int64_t N,
+                                                              const WgradDiag d,
+                                                              float* __restrict__ out) {
+  const int nc = kRank * d.slots;
+  const int64_t total4 = N * kRank / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total4;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t n = (4 * i) / kRank, c = 4 * i - n * kRank;
+    int q = 0;
+    while (q + 1 < d.slots && n >= d.off[q + 1]) ++q;
+    const float* src = ws + n * nc + kRank * q + c;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < splits; ++z) {
+      const float4 t = *reinterpret_cast<const float4*>(src + (int64_t)z * N * nc);
+      v.x += t.x; v.y += t.y; v.z += t.z; v.w += t.w;
+    }
+    const float a = d.alpha[q];
+    reinterpret_cast<float4*>(out)[i] = make_float4(a * v.x, a * v.y, a * v.z, a * v.w);
+  }
+}
+
 // The compute-dtype forms of one adapter's fp32 factors A [16, K] and B [N, 16], in one pass:
 //   a16 [16, K]  = A                    (the Y operand of u = x A^T)
 //   at  [K, 64]  = A^T | 0              (the second K segment of the backward dX GEMM)
@@ -1180,10 +1212,14 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
       T* row = bs + n * pad;
       float b[kRank];
 #pragma unroll
-      for (int r = 0; r < kRank; ++r) {
-        b[r] = p.B[g][ln * kRank + r];
-        bt[(int64_t)r * N + n] = Elem<OT>::from_f32(b[r]);
-      }
+      for (int r = 0; r < kRank; ++r) b[r] = p.B[g][ln * kRank + r];
+      // bt [16 G, N] block-diagonal: column n holds B_g^T in rows 16 g .. 16 g + 15 and zeros
+      // in the other slots' rows, so one multi-slot lora_down over all N columns gives every
+      // adapter's du at once
+      for (int q = 0; q < p.G; ++q)
+#pragma unroll
+        for (int r = 0; r < kRank; ++r)
+          bt[(int64_t)(kRank * q + r) * N + n] = Elem<OT>::from_f32(q == g ? b[r] : 0.f);
       for (int c0 = 0; c0 < pad; c0 += 8) {
         float v[8];
         const bool mine = c0 / kRank == g;
@@ -1725,6 +1761,80 @@ extern "C" int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int
   return ql_lora_wgrad(in_dtype, PT, ldpt, Q, ldq, M, N, slots, out, out_transposed, alpha,
                        static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
                        static_cast<hipStream_t>(stream));
+}
+
+// Weight gradients of several adapters whose outputs are concatenated, as one multi-slot
+// pass over the concatenated output gradient (every slot's products over every column, the
+// unused ones discarded by lora_wgrad_reduce_diag): one read of Q and two launches instead of
+// two per adapter.
+static int64_t wgrad_diag_floats(int64_t M, int64_t N, int slots) {
+  return (int64_t)ql_lora_wgrad_splits(M, N, slots) * N * kRank * slots;
+}
+
+extern "C" int64_t qlora_lora_wgrad_diag_workspace_size(int64_t M, int64_t N, int slots) {
+  if (M <= 0 || N <= 0 || slots < 1 || slots > kMaxSlots) return 0;
+  return wgrad_diag_floats(M, N, slots) * (int64_t)sizeof(float);
+}
+
+extern "C" int qlora_lora_wgrad_diag(const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
+                                     int64_t M, int64_t N, int slots, int in_dtype,
+                                     const int64_t* col_offsets, const float* alphas,
+                                     float* out, void* workspace, int64_t workspace_bytes,
+                                     ql_stream_t stream) {
+  if (M <= 0 || N < 0 || slots < 1 || slots > kMaxSlots) return QL_EINVAL;
+  if (N == 0) return QL_OK;
+  if (!PT || !Q || !out || !col_offsets || !alphas || !workspace) return QL_EINVAL;
+  WgradDiag d{};
+  d.slots = slots;
+  for (int q = 0; q <= slots; ++q) d.off[q] = col_offsets[q];
+  if (d.off[0] != 0 || d.off[slots] != N) return QL_ESHAPE;
+  for (int q = 0; q < slots; ++q) {
+    if (d.off[q + 1] < d.off[q]) return QL_ESHAPE;
+    d.alpha[q] = alphas[q];
+  }
+  const int nc = kRank * slots;
+  if (N % 8 || ldpt < M || ldq < N) return QL_EINVAL;
+  if (64 * ldq >= (int64_t(1) << 31) || 2 * nc * ldpt >= (int64_t(1) << 31)) return QL_EINVAL;
+  if (ldq % 8 || ldpt % 8 || !ql_aligned(Q, 16) || !ql_aligned(PT, 16) || !ql_aligned(out, 16) ||
+      !ql_aligned(workspace, 16))
+    return QL_EALIGN;
+  if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
+  if (workspace_bytes < wgrad_diag_floats(M, N, slots) * (int64_t)sizeof(float)) return QL_EINVAL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* ws = static_cast<float*>(workspace);
+  int splits = ql_lora_wgrad_splits(M, N, slots);
+  const int64_t mps = ((M + splits - 1) / splits + 127) / 128 * 128;
+  splits = (int)((M + mps - 1) / mps);
+  const dim3 grid((unsigned)((N + 127) / 128), (unsigned)splits);
+  const int64_t per_wave = mps / 128;
+  const int unroll = (slots == 1 && per_wave % 4 == 0) ? 4 : (per_wave % 2 == 0 ? 2 : 1);
+#define QL_WD_GU(IT, G, U)                                                                     \
+  hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U>), grid, dim3(kThreads), 0, s,          \
+                     (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,         \
+                     (float*)nullptr, 0.f, false)
+#define QL_WD_G(IT, G)                                     \
+  do {                                                     \
+    if (unroll == 4) QL_WD_GU(IT, G, (G == 1 ? 4 : 2));    \
+    else if (unroll == 2) QL_WD_GU(IT, G, 2);              \
+    else QL_WD_GU(IT, G, 1);                               \
+  } while (0)
+#define QL_WD(IT)                            \
+  do {                                       \
+    switch (slots) {                         \
+      case 1: QL_WD_G(IT, 1); break;         \
+      case 2: QL_WD_G(IT, 2); break;         \
+      case 3: QL_WD_G(IT, 3); break;         \
+      default: QL_WD_G(IT, 4); break;        \
+    }                                        \
+  } while (0)
+  if (in_dtype == QL_BF16) QL_WD(QL_BF16);
+  else QL_WD(QL_F16);
+#undef QL_WD
+#undef QL_WD_G
+#undef QL_WD_GU
+  hipLaunchKernelGGL(lora_wgrad_reduce_diag, dim3(grid1d(N * kRank / 4)), dim3(256), 0, s, ws,
+                     splits, N, d, out);
+  return ql_launch_status();
 }
 
 // ---- qlora_lora_wgrad without a caller workspace -------------------------------------------

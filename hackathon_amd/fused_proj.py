@@ -164,12 +164,17 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
     M, K = x2.shape
     G = len(specs)
     offs = _offsets(specs)
+    same_scaling = len({s.scaling for s in specs}) == 1
     if du_dut is None:
         du = torch.empty((M, _PAD), dtype=dt, device=dev)
         dut = _t_buffer(16 * G, M, dt, dev)
-        for i, s in enumerate(specs):
-            _gemm.lora_down(g[:, offs[i]:offs[i + 1]], bt[:, offs[i]:offs[i + 1]],
-                            du[:, 16 * i:], alpha=s.scaling, out_t=dut[16 * i:16 * i + 16])
+        if same_scaling:  # bt is block-diagonal: every adapter's du in one pass over g
+            _gemm.lora_down(g, bt, du, alpha=specs[0].scaling, out_t=dut)
+        else:
+            for i, s in enumerate(specs):
+                _gemm.lora_down(g[:, offs[i]:offs[i + 1]],
+                                bt[16 * i:16 * i + 16, offs[i]:offs[i + 1]], du[:, 16 * i:],
+                                alpha=s.scaling, out_t=dut[16 * i:16 * i + 16])
     else:
         du, dut = du_dut
     dx = None
@@ -184,13 +189,21 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
     da_all = None
     if any(need_ab[0::2]):  # dA_g^T for every slot in one pass over x: [16 G, K]
         da_all = _gemm.lora_wgrad(dut, x2, transposed=True)
+    db_all = None
+    if db_given is None and sum(need_ab[1::2]) > 1:  # every dB_g in one pass over g
+        db_all = _gemm.lora_wgrad_diag(ut[:16 * G], g, offs, [s.scaling for s in specs])
     for i, s in enumerate(specs):
         da = db = None
         if need_ab[2 * i]:
             da = da_all[16 * i:16 * i + 16]
         if need_ab[2 * i + 1]:
-            db = db_given[i] if db_given is not None else _gemm.lora_wgrad(
-                ut[16 * i:16 * i + 16], g[:, offs[i]:offs[i + 1]], alpha=s.scaling)
+            if db_given is not None:
+                db = db_given[i]
+            elif db_all is not None:
+                db = db_all[offs[i]:offs[i + 1]]
+            else:
+                db = _gemm.lora_wgrad(ut[16 * i:16 * i + 16], g[:, offs[i]:offs[i + 1]],
+                                      alpha=s.scaling)
         grads += [da, db]
     return dx, grads
 
@@ -292,12 +305,12 @@ class GateUpSwiGLU(torch.autograd.Function):
             gate_s, up_s = ctx.specs
             if need_ab[1] or need_ab[3]:
                 db_given = swiglu.swiglu_bwd_lora(
-                    dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:, :n], bt[:, n:], ut[:16],
+                    dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:16, :n], bt[16:32, n:], ut[:16],
                     ut[16:32], gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du,
                     dut)
             else:
                 swiglu.swiglu_bwd_lora_down(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:],
-                                            bt[:, :n], bt[:, n:], gate_s.scaling, up_s.scaling,
+                                            bt[:16, :n], bt[16:32, n:], gate_s.scaling, up_s.scaling,
                                             du, dut)
             du_dut = (du, dut)
         else:
@@ -381,7 +394,7 @@ class LoraMLP(torch.autograd.Function):
         dut = _t_buffer(32, M, dt, dev)
         gate_s, up_s = specs
         db_g, db_u, da_d = swiglu.swiglu_bwd_lora(
-            dh, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:, :n], bt[:, n:], ut[:16], ut[16:32],
+            dh, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:16, :n], bt[16:32, n:], ut[:16], ut[16:32],
             gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du, dut, ud_t=dut_d)
         del dh
         dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[3:7],

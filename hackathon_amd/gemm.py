@@ -8,6 +8,8 @@ bf16 or fp16 on a GPU; they are made unit-stride along their contiguous dimensio
 
 from __future__ import annotations
 
+import ctypes
+
 import weakref
 
 import torch
@@ -185,6 +187,27 @@ def lora_t_buffer(m: int, dtype, device, rows: int = 16) -> torch.Tensor:
     return torch.empty((rows, (m + 7) // 8 * 8), dtype=dtype, device=device)[:, :m]
 
 
+def lora_wgrad_diag(pt: torch.Tensor, q: torch.Tensor, col_offsets, alphas) -> torch.Tensor:
+    """The lora_B gradients of G adapters with concatenated outputs from one pass: fp32 [N, 16]
+    whose rows off_i .. off_{i+1} - 1 are alphas[i] * q[:, off_i:off_{i+1}]^T pt[16 i:16 i + 16]^T
+    (pt = the adapters' stacked u^T [16 G, M], q = their concatenated output gradient [M, N])
+    (qlora_lora_wgrad_diag)."""
+    _lib.require_rows(q.dtype, pt=pt, q=q)
+    M, N = q.shape
+    G = _slots(pt.shape[0], "pt")
+    if len(col_offsets) != G + 1 or len(alphas) != G:
+        raise ValueError("col_offsets needs G + 1 entries and alphas G")
+    out = torch.empty((N, 16), dtype=torch.float32, device=q.device)
+    ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_diag_workspace_size", M, N, G,
+                                  device=q.device)
+    offs = _lib.i64_array(col_offsets)
+    al = (ctypes.c_float * G)(*[float(a) for a in alphas])
+    _lib.call("qlora_lora_wgrad_diag", pt.data_ptr(), pt.stride(0), q.data_ptr(), q.stride(0), M,
+              N, G, _lib.tag(q.dtype), offs, al, out.data_ptr(), _lib.ptr(ws), ws_bytes,
+              _lib.stream_of(q))
+    return out
+
+
 def lora_wgrad(pt: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
                transposed: bool = False) -> torch.Tensor:
     """fp32 alpha * q^T @ pt^T for q [M, N] and pt [16G, M] (token-contiguous, as lora_down's
@@ -221,9 +244,10 @@ def lora_pack(a: torch.Tensor, b: torch.Tensor, scaling: float, dtype, pad: int 
 
 
 def lora_pack_group(factors, dtype, pad: int = 64):
-    """(a16 [16G, K], at_pad [K, pad], bs_pad [N, pad], bt [16, N]) in `dtype` for G <= 4
+    """(a16 [16G, K], at_pad [K, pad], bs_pad [N, pad], bt [16G, N]) in `dtype` for G <= 4
     adapters (a_g [16, K], b_g [n_g, 16], scaling_g) that read the same input, adapter g in
-    columns 16g .. 16g+15 and output rows off_g .. off_g + n_g - 1, N = sum n_g
+    columns 16g .. 16g+15 and output rows off_g .. off_g + n_g - 1, N = sum n_g; bt is
+    block-diagonal (B_g^T in rows 16g .. 16g+15 of adapter g's columns, zeros elsewhere)
     (qlora_lora_pack_group, one launch)."""
     items = []
     for a, b, s in factors:
@@ -236,7 +260,7 @@ def lora_pack_group(factors, dtype, pad: int = 64):
     a16 = torch.empty((16 * G, K), dtype=dtype, device=dev)
     at = torch.empty((K, pad), dtype=dtype, device=dev)
     bs = torch.empty((N, pad), dtype=dtype, device=dev)
-    bt = torch.empty((16, N), dtype=dtype, device=dev)
+    bt = torch.empty((16 * G, N), dtype=dtype, device=dev)
     _lib.call("qlora_lora_pack_group", _lib.lora_factors(items), G, K, _lib.tag(dtype),
               a16.data_ptr(), at.data_ptr(), bs.data_ptr(), bt.data_ptr(), pad,
               _lib.stream_of(a16))

@@ -37,8 +37,9 @@ enum {
 
 typedef void* ql_stream_t; /* hipStream_t */
 
-/* Library identification and error text. qlora_abi_version() is 2 for the signatures in this
- * file (version 1 had no `slots` argument in the qlora_lora_down / qlora_lora_wgrad family). */
+/* Library identification and error text. qlora_abi_version() is 3 for the signatures in this
+ * file (version 1 had no `slots` argument in the qlora_lora_down / qlora_lora_wgrad family;
+ * version 2 wrote qlora_lora_pack_group's bt as [16, N] instead of [16 count, N]). */
 int qlora_abi_version(void);
 const char* qlora_strerror(int status);
 
@@ -403,6 +404,24 @@ int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, i
                      void* workspace, int64_t workspace_bytes, ql_stream_t stream);
 
 /*
+ * The lora_B weight gradients of `slots` = G adapters whose outputs are concatenated (the
+ * q/k/v projections), from one multi-slot pass over the concatenated output gradient:
+ *   out[n, c] = alphas[q] * sum_m Q[m, n] * PT[16 q + c, m]    for off_q <= n < off_{q+1}
+ * (fp32 [N, 16]: adapter q's dB = s_q g_q^T u_q in rows off_q .. off_{q+1} - 1). col_offsets
+ * (host, G + 1 values: 0 = off_0 <= .. <= off_G = N) and alphas (host, G) are read at the
+ * call. The other slots' products over a column are computed and discarded. Same Q / PT
+ * requirements as qlora_lora_wgrad; out and the workspace (qlora_lora_wgrad_diag_workspace_size
+ * bytes, required) 16-B aligned. Deterministic: the partial sums are added in a fixed order.
+ * Replaces: the autograd lora_B gradients of solution/lora.py:172 for projections fused into
+ * one GEMM (no reference counterpart for the fused layout itself).
+ */
+int64_t qlora_lora_wgrad_diag_workspace_size(int64_t M, int64_t N, int slots);
+int qlora_lora_wgrad_diag(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M,
+                          int64_t N, int slots, int in_dtype, const int64_t* col_offsets,
+                          const float* alphas, float* out, void* workspace,
+                          int64_t workspace_bytes, ql_stream_t stream);
+
+/*
  * qlora_lora_wgrad without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving or training loops, C hosts without an
  * allocator). No counterpart in the reference. Same arguments, results and rules as
@@ -518,7 +537,9 @@ int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float 
  *   a16 [16 count, K]: rows 16g .. 16g+15 = A_g;
  *   at_pad [K, pad]:   columns 16g .. 16g+15 = A_g^T, the rest 0;
  *   bs_pad [N, pad]:   row off_g + n: columns 16g .. 16g+15 = s_g B_g[n], the rest 0;
- *   bt [16, N]:        columns off_g .. = B_g^T.
+ *   bt [16 count, N]:  block-diagonal: rows 16g .. 16g+15, columns off_g .. off_g + n_g - 1
+ *                      = B_g^T, every other entry 0 (so qlora_lora_down with `slots` = count
+ *                      over all N columns gives each adapter's du = g_g B_g in slot g).
  * out_dtype QL_BF16 or QL_F16, round to nearest even; K % 8 == 0.
  * Replaces: the per-projection casts of solution/lora.py:172 for projections fused into one
  * GEMM (no reference counterpart for the fused layout itself).

@@ -106,6 +106,19 @@ def test_rejected_arguments_return_codes(lib):
     assert lib.qlora_nf4_dequant_t_group((W * 1)(W(0x1000, 64, 128, 0x1000, 0x1000, 0x1000, 0.0,
                                                    64, 256, 0x1008)), 1, 1, fake, 64, 2,
                                          None) == -3
+    # diagonal weight gradient: offsets not ending at N, no workspace, bad dtype
+    offs = _lib.i64_array((0, 64, 128))
+    al = (ctypes.c_float * 2)(1.0, 1.0)
+    assert lib.qlora_lora_wgrad_diag(fake, 64, fake, 256, 64, 256, 2, 2, offs, al, fake, fake,
+                                     1 << 20, None) == -4
+    offs = _lib.i64_array((0, 64, 256))
+    assert lib.qlora_lora_wgrad_diag(fake, 64, fake, 256, 64, 256, 2, 2, offs, al, fake, None,
+                                     1 << 20, None) == -1
+    assert lib.qlora_lora_wgrad_diag(fake, 64, fake, 256, 64, 256, 2, 0, offs, al, fake, fake,
+                                     1 << 20, None) == -2
+    assert lib.qlora_lora_wgrad_diag(fake, 64, fake, 256, 64, 256, 2, 2, offs, al, fake, fake,
+                                     16, None) == -1  # workspace too small
+    assert lib.qlora_lora_wgrad_diag_workspace_size(64, 256, 5) == 0
     # rmsnorm: bad dtype, zero columns
     assert lib.qlora_rmsnorm_fwd(fake, 9, 8, fake, 2, fake, 2, 8, fake, 4, 8, 1e-6, None) == -2
     assert lib.qlora_rmsnorm_fwd(fake, 2, 8, fake, 2, fake, 2, 8, fake, 4, 0, 1e-6, None) == -1

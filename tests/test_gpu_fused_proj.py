@@ -233,9 +233,47 @@ def test_lora_pack_group_matches_the_single_packs():
         others = torch.ones(64, dtype=torch.bool, device="cuda")
         others[cols] = False
         assert torch.all(bs[rows][:, others] == 0)
-        assert torch.equal(bt[:, rows], bt1)
+        assert torch.equal(bt[cols, rows], bt1)
+        other_slots = torch.ones(48, dtype=torch.bool, device="cuda")
+        other_slots[cols] = False
+        assert torch.all(bt[other_slots][:, rows] == 0)  # block-diagonal
         off += n
+    assert bt.shape == (48, sum(ns))
     assert torch.all(at[:, 48:] == 0)
+
+
+@pytest.mark.parametrize("M,ns,scales", [
+    (4096, (3584, 512, 512), (2.0, 2.0, 2.0)),   # Qwen2.5-7B q/k/v
+    (300, (64, 128, 8, 40), (0.5, 1.0, 2.0, 3.0)),  # ragged tokens, four slots, unequal scalings
+    (96, (256,), (1.5,)),
+])
+def test_lora_wgrad_diag_matches_per_adapter(M, ns, scales):
+    """qlora_lora_wgrad_diag (one multi-slot pass over the concatenated output gradient) gives
+    each adapter's lora_B gradient s_q g_q^T u_q: against the fp64 product within an fp32
+    accumulation bound, as the per-adapter lora_wgrad is (the two sum in different orders)."""
+    print(f"lora_wgrad_diag M={M} ns={ns}", flush=True)
+    from hackathon_amd import gemm
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    G, N = len(ns), sum(ns)
+    q = torch.randn(M, N, device="cuda", generator=g).to(torch.bfloat16)
+    pt = gemm.lora_t_buffer(M, torch.bfloat16, "cuda", rows=16 * G)
+    pt.copy_(torch.randn(16 * G, M, device="cuda", generator=g).to(torch.bfloat16))
+    offs = [0]
+    for n in ns:
+        offs.append(offs[-1] + n)
+    out = gemm.lora_wgrad_diag(pt, q, offs, scales)
+    assert out.shape == (N, 16) and out.dtype == torch.float32
+    for i, s in enumerate(scales):
+        qi, pti = q[:, offs[i]:offs[i + 1]], pt[16 * i:16 * i + 16]
+        ref = s * (qi.double().t() @ pti.double().t())
+        got = out[offs[i]:offs[i + 1]].double()
+        bound = 4e-6 * M ** 0.5 * s * (qi.double().t().abs() @ pti.double().t().abs()) + 1e-6
+        assert torch.all((got - ref).abs() <= bound)
+        # the per-adapter call sums in another order: both within the bound of the exact value
+        sep = gemm.lora_wgrad(pti, qi, alpha=s).double()
+        assert torch.all((sep - ref).abs() <= bound)
+        assert torch.all((got - sep).abs() <= 2 * bound)
 
 
 @pytest.mark.parametrize("rows,cols,dtype", [(4096, 18944, torch.bfloat16),
