@@ -229,8 +229,14 @@ QL_DEV void wait_all_barrier() {
 // no longer runs under the block's math.
 QL_DEV void wait_vm_visible() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-// Index differences used by the branch-free masks, clamped into int range.
-QL_DEV int clamp_rel(int64_t x) { return (int)(x < -4096 ? -4096 : x > 4096 ? 4096 : x); }
+// Index differences used by the masks, clamped into int range. The empty register barrier
+// keeps the compiler from comparing the unclamped 64-bit value instead (an equivalent test,
+// but two 64-bit compares per element of every masked block).
+QL_DEV int clamp_rel(int64_t x) {
+  int v = (int)(x < -4096 ? -4096 : x > 4096 ? 4096 : x);
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 struct AttnShape {
   int64_t B, HQ, HK, S;
@@ -512,19 +518,28 @@ QL_DEV void dkdv_block(DkdvState<DT>& st, const char* __restrict__ cur, char* __
     }
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
-    const int r4 = 16 * qt + 4 * fq;
-    const float4 l4 = *reinterpret_cast<const float4*>(lse2 + r4);
-    const float4 d4 = *reinterpret_cast<const float4*>(dlt + r4);
+    const float4 l4 = *reinterpret_cast<const float4*>(lse2 + 16 * qt + 4 * fq);
     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      sp[qt][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][e], sl2, -lv[e]));
+  }
+  // Only the diagonal block and a block past the end have masked entries: a wave-uniform
+  // branch, so the other blocks skip the tests. key - q = kq_rel - 16 qt - e; rows at or past
+  // the end: 16 qt + e >= qlim.
+  if (__builtin_expect(need_mask, 0)) {
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (kq_rel - 16 * qt - e > 0 || 16 * qt + e >= qlim) sp[qt][e] = 0.f;
+  }
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    const float4 d4 = *reinterpret_cast<const float4*>(dlt + 16 * qt + 4 * fq);
     const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][e], sl2, -lv[e]));
-      // key - q = kq_rel - 16 qt - e; rows at or past the end: 16 qt + e >= qlim
-      if (need_mask) p = (kq_rel - 16 * qt - e > 0 || 16 * qt + e >= qlim) ? 0.f : p;
-      sp[qt][e] = p;
-      dp[qt][e] = p * (dp[qt][e] - dv[e]);
-    }
+    for (int e = 0; e < 4; ++e) dp[qt][e] = sp[qt][e] * (dp[qt][e] - dv[e]);
   }
   uint4 pb[2], sb[2];
 #pragma unroll
@@ -739,18 +754,31 @@ QL_DEV void dq_block(DqState<DT>& st, const char* __restrict__ kl, const char* _
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          sp[qt][kk][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][kk][e], sl2, -st.l2[qt]));
+    if (__builtin_expect(need_mask, 0)) {  // wave-uniform: the diagonal and end blocks only
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int rel = 32 * h + 16 * kk + e;
+            if (kq_rel + rel - 16 * qt > 0 || rel >= klim) sp[qt][kk][e] = 0.f;
+          }
+    }
     uint4 sb[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][kk][e], sl2, -st.l2[qt]));
-          const int rel = 32 * h + 16 * kk + e;
-          if (need_mask) p = (kq_rel + rel - 16 * qt > 0 || rel >= klim) ? 0.f : p;
-          dp[qt][kk][e] = p * (dp[qt][kk][e] - st.dl[qt]);
-        }
+        for (int e = 0; e < 4; ++e) dp[qt][kk][e] = sp[qt][kk][e] * (dp[qt][kk][e] - st.dl[qt]);
       sb[qt] = pack_pair<DT>(dp[qt][0], dp[qt][1]);
     }
     __builtin_amdgcn_sched_barrier(0);
