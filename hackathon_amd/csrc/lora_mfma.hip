@@ -1123,7 +1123,9 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce_diag(const float* __res
 //   bs  [N, 64]  = s B | 0              (the second K segment of the forward GEMM)
 //   bt  [16, N]  = B^T                  (the Y operand of du = s g B)
 // Thread t of the flat range handles one row of at (t < K), then one row of bs and one
-// column of bt (K <= t < K + N), then 8 elements of a16.
+// column of bt (K <= t < K + N), then 8 elements of a16. qlora_lora_pack uses this form only
+// for a pad that is not a multiple of 8 or rows that are not 16-B aligned; otherwise it runs
+// the one-slot group packing, which writes whole 16-B chunks.
 template <int OT>
 __global__ __launch_bounds__(256) void lora_pack_kernel(const float* __restrict__ A,
                                                         const float* __restrict__ B, int64_t K,
@@ -1164,8 +1166,14 @@ __global__ __launch_bounds__(256) void lora_pack_kernel(const float* __restrict_
 // The compute-dtype operands of up to four rank-16 adapters that share an input (the q/k/v or
 // gate/up projections of one layer) for one fused GEMM per direction: adapter g owns columns
 // 16g .. 16g+15 of the padded operands and rows off[g] .. off[g+1]-1 of the concatenated
-// outputs. Work items: t < K: row t of at (all pad columns); K <= t < K + N: row n of bs and
-// column n of bt; then 8 elements of a16 per item.
+// outputs. The padded rows of at and bs are written one 16-B chunk per work item, so the 8
+// consecutive lanes of one 128-B row (pad 64) write it whole and every item needs one round of
+// loads; a thread per row walking its chunks (or storing 2 B per column) cost 6-8 us per launch
+// at the 7B shapes, almost all of it store issue and serial load waits. Work items, in order:
+//   [0, K ch)            chunk t % ch of row t / ch of at  (ch = pad / 8)
+//   [.., + N ch)         the same for the rows of bs
+//   [.., + N)            column n of bt (every slot's 16 rows)
+//   then 8 elements of a16 per item.
 constexpr int kMaxGroup = 4;
 struct PackGroupArgs {
   const float* A[kMaxGroup];  // [16, K]
@@ -1182,53 +1190,64 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
                                                               typename Elem<OT>::T* __restrict__ bs,
                                                               typename Elem<OT>::T* __restrict__ bt,
                                                               int pad) {
-  using T = typename Elem<OT>::T;
   const int64_t N = p.off[p.G];
+  const int ch = pad / 8;
+  const int64_t n_at = K * ch, n_bs = N * ch;
   const int64_t n_a16 = (int64_t)kRank * p.G * K / 8;
-  const int64_t total = K + N + n_a16;
+  const int64_t total = n_at + n_bs + N + n_a16;
+  auto slot_of = [&](int64_t n) {
+    int g = 0;
+    while (g + 1 < p.G && n >= p.off[g + 1]) ++g;
+    return g;
+  };
   for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * 256) {
-    if (t < K) {
-      // row t of at: 8 columns (one 16-B store) at a time
-      T* row = at + t * pad;
-      for (int c0 = 0; c0 < pad; c0 += 8) {
-        const int g = c0 / kRank;
-        float v[8];
-        if (g < p.G) {
-          const float* a = p.A[g] + (int64_t)(c0 & (kRank - 1)) * K + t;
+    if (t < n_at) {
+      // at [K, pad]: column 16 g + r of row k holds A_g[r][k]
+      const int64_t k = t / ch;
+      const int c0 = 8 * (int)(t - k * ch);
+      const int g = c0 / kRank;
+      float v[8];
+      if (g < p.G) {
+        const float* a = p.A[g] + (int64_t)(c0 & (kRank - 1)) * K + k;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = a[(int64_t)e * K];
-        } else {
+        for (int e = 0; e < 8; ++e) v[e] = a[(int64_t)e * K];
+      } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = 0.f;
-        }
-        Vec8<OT>::store(row + c0, v);
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
       }
-    } else if (t < K + N) {
-      const int64_t n = t - K;
-      int g = 0;
-      while (g + 1 < p.G && n >= p.off[g + 1]) ++g;
-      const int64_t ln = n - p.off[g];
-      T* row = bs + n * pad;
-      float b[kRank];
+      Vec8<OT>::store(at + k * pad + c0, v);
+    } else if (t < n_at + n_bs) {
+      // bs [N, pad]: row n of slot g holds scale_g B_g[n - off_g] in columns 16 g .. 16 g + 15
+      const int64_t u = t - n_at;
+      const int64_t n = u / ch;
+      const int c0 = 8 * (int)(u - n * ch);
+      const int g = slot_of(n);
+      float v[8];
+      if (c0 / kRank == g) {
+        const float* b = p.B[g] + (n - p.off[g]) * kRank + (c0 & (kRank - 1));
 #pragma unroll
-      for (int r = 0; r < kRank; ++r) b[r] = p.B[g][ln * kRank + r];
+        for (int e = 0; e < 8; ++e) v[e] = p.scale[g] * b[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+      Vec8<OT>::store(bs + n * pad + c0, v);
+    } else if (t < n_at + n_bs + N) {
       // bt [16 G, N] block-diagonal: column n holds B_g^T in rows 16 g .. 16 g + 15 and zeros
       // in the other slots' rows, so one multi-slot lora_down over all N columns gives every
       // adapter's du at once
+      const int64_t n = t - n_at - n_bs;
+      const int g = slot_of(n);
+      float b[kRank];
+#pragma unroll
+      for (int r = 0; r < kRank; ++r) b[r] = p.B[g][(n - p.off[g]) * kRank + r];
       for (int q = 0; q < p.G; ++q)
 #pragma unroll
         for (int r = 0; r < kRank; ++r)
           bt[(int64_t)(kRank * q + r) * N + n] = Elem<OT>::from_f32(q == g ? b[r] : 0.f);
-      for (int c0 = 0; c0 < pad; c0 += 8) {
-        float v[8];
-        const bool mine = c0 / kRank == g;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = mine ? p.scale[g] * b[(c0 & (kRank - 1)) + e] : 0.f;
-        Vec8<OT>::store(row + c0, v);
-      }
     } else {
-      const int64_t i = (t - K - N) * 8;  // into a16 [16 G, K]
+      const int64_t i = (t - n_at - n_bs - N) * 8;  // into a16 [16 G, K]
       const int64_t gr = i / K, col = i - gr * K;
       const int g = (int)(gr / kRank), r = (int)(gr - (int64_t)g * kRank);
 #pragma unroll
@@ -1898,6 +1917,23 @@ extern "C" int qlora_lora_wgrad_noalloc(const void* PT, int64_t ldpt, const void
                           need, stream);
 }
 
+namespace {
+// pad % 8 == 0, pad >= 16 G, K % 8 == 0, at and bs 16-B aligned (checked by the callers)
+int launch_pack_group(const PackGroupArgs& p, int64_t K, int out_dtype, void* a16, void* at_pad,
+                      void* bs_pad, void* bt, int pad, hipStream_t s) {
+  const int64_t N = p.off[p.G];
+  const int64_t total = (K + N) * (pad / 8) + N + (int64_t)kRank * p.G * K / 8;
+  if (total == 0) return QL_OK;
+  if (out_dtype == QL_BF16)
+    hipLaunchKernelGGL((lora_pack_group_kernel<QL_BF16>), dim3(grid1d(total)), dim3(256), 0, s, p,
+                       K, (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
+  else
+    hipLaunchKernelGGL((lora_pack_group_kernel<QL_F16>), dim3(grid1d(total)), dim3(256), 0, s, p,
+                       K, (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
+  return ql_launch_status();
+}
+}  // namespace
+
 extern "C" int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_t N, float scaling,
                                int out_dtype, void* a16, void* at_pad, void* bs_pad, void* bt,
                                int pad, ql_stream_t stream) {
@@ -1905,9 +1941,20 @@ extern "C" int qlora_lora_pack(const float* A, const float* B, int64_t K, int64_
   if (K == 0 && N == 0) return QL_OK;
   if (!A || !B || !a16 || !at_pad || !bs_pad || !bt) return QL_EINVAL;
   if (out_dtype != QL_BF16 && out_dtype != QL_F16) return QL_EDTYPE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pad % 8 == 0 && ql_aligned(at_pad, 16) && ql_aligned(bs_pad, 16)) {
+    // the one-slot case of the group packing: the same values, 16-B chunks per item
+    PackGroupArgs p{};
+    p.G = 1;
+    p.A[0] = A;
+    p.B[0] = B;
+    p.scale[0] = scaling;
+    p.off[0] = 0;
+    p.off[1] = N;
+    return launch_pack_group(p, K, out_dtype, a16, at_pad, bs_pad, bt, pad, s);
+  }
   const int64_t total = K + N + kRank * K / 8;
   const dim3 grid(grid1d(total));
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (out_dtype == QL_BF16)
     hipLaunchKernelGGL((lora_pack_kernel<QL_BF16>), grid, dim3(256), 0, s, A, B, K, N, scaling,
                        (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
@@ -1935,14 +1982,6 @@ extern "C" int qlora_lora_pack_group(const ql_lora_factor* factors, int count, i
     p.scale[g] = factors[g].scaling;
     p.off[g + 1] = p.off[g] + factors[g].n;
   }
-  const int64_t total = K + p.off[count] + (int64_t)kRank * count * K / 8;
-  if (total == 0) return QL_OK;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (out_dtype == QL_BF16)
-    hipLaunchKernelGGL((lora_pack_group_kernel<QL_BF16>), dim3(grid1d(total)), dim3(256), 0, s, p,
-                       K, (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
-  else
-    hipLaunchKernelGGL((lora_pack_group_kernel<QL_F16>), dim3(grid1d(total)), dim3(256), 0, s, p,
-                       K, (uint16_t*)a16, (uint16_t*)at_pad, (uint16_t*)bs_pad, (uint16_t*)bt, pad);
-  return ql_launch_status();
+  return launch_pack_group(p, K, out_dtype, a16, at_pad, bs_pad, bt, pad,
+                           static_cast<hipStream_t>(stream));
 }

@@ -222,6 +222,7 @@ def test_lora_pack_group_matches_the_single_packs():
     facs = [(torch.randn(16, K, device="cuda", generator=g),
              torch.randn(n, 16, device="cuda", generator=g), s) for n, s in zip(ns, scales)]
     a16, at, bs, bt = gemm.lora_pack_group(facs, torch.bfloat16)
+    assert torch.all(at[:, 48:] == 0)  # columns past the last slot
     off = 0
     for i, ((a, b, s), n) in enumerate(zip(facs, ns)):
         a1, at1, bs1, bt1 = gemm.lora_pack(a, b, s, torch.bfloat16, 64)

@@ -288,17 +288,20 @@ def test_lora_wgrad_slots(M, N, G):
     assert torch.equal(gemm.lora_wgrad(pt_dev, qd, alpha=0.5, transposed=True), out.t())
 
 
-@pytest.mark.parametrize("K,N", [(3584, 512), (256, 18944), (8, 8)])
-def test_lora_pack_is_exact(K, N):
+@pytest.mark.parametrize("pad", [64, 24, 20])  # 16-B chunks per item; 20: the per-row form
+@pytest.mark.parametrize("K,N", [(3584, 512), (256, 18944), (18944, 3584), (8, 8)])
+def test_lora_pack_is_exact(K, N, pad):
     """The packed adapter operands equal torch's own casts of A, A^T, s*B and B^T (RNE)."""
+    print(f"lora_pack K={K} N={N} pad={pad}", flush=True)
     g = torch.Generator().manual_seed(K + N)
     a = torch.randn(16, K, generator=g) * 0.25
     b = torch.randn(N, 16, generator=g) * 0.01
-    a16, at, bs, bt = gemm.lora_pack(a.cuda(), b.cuda(), 2.0, torch.bfloat16)
-    assert torch.equal(a16.cpu(), a.to(torch.bfloat16))
-    assert torch.equal(at[:, :16].cpu(), a.t().to(torch.bfloat16)) and torch.all(at[:, 16:] == 0)
-    assert torch.equal(bs[:, :16].cpu(), (2.0 * b).to(torch.bfloat16)) and torch.all(bs[:, 16:] == 0)
-    assert torch.equal(bt.cpu(), b.t().to(torch.bfloat16))
+    for dt in (torch.bfloat16, torch.float16):
+        a16, at, bs, bt = gemm.lora_pack(a.cuda(), b.cuda(), 2.0, dt, pad=pad)
+        assert torch.equal(a16.cpu(), a.to(dt))
+        assert torch.equal(at[:, :16].cpu(), a.t().to(dt)) and torch.all(at[:, 16:] == 0)
+        assert torch.equal(bs[:, :16].cpu(), (2.0 * b).to(dt)) and torch.all(bs[:, 16:] == 0)
+        assert torch.equal(bt.cpu(), b.t().to(dt))
 
 
 @pytest.mark.parametrize("M,N", [(4096, 3584), (100, 520)])
