@@ -1877,17 +1877,17 @@ float* g_scratch[kMaxDevices];  // device address of lora_wgrad_scratch per devi
 int wgrad_scratch_of(hipStream_t stream, float** out) {
   int dev = 0;
   hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
-  if (e != hipSuccess) return (int)e;
+  if (e != hipSuccess) return ql_hip_status(e);
   if (dev < 0 || dev >= kMaxDevices) return QL_EINVAL;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch[dev]) {
     int cur = 0;
-    if ((e = hipGetDevice(&cur)) != hipSuccess) return (int)e;
-    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return ql_hip_status(e);
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return ql_hip_status(e);
     void* p = nullptr;
     const hipError_t got = hipGetSymbolAddress(&p, HIP_SYMBOL(lora_wgrad_scratch));
-    if (cur != dev && (e = hipSetDevice(cur)) != hipSuccess) return (int)e;
-    if (got != hipSuccess) return (int)got;
+    if (cur != dev && (e = hipSetDevice(cur)) != hipSuccess) return ql_hip_status(e);
+    if (got != hipSuccess) return ql_hip_status(got);
     if (!p || !ql_aligned(p, 256)) return QL_EALIGN;
     g_scratch[dev] = static_cast<float*>(p);
   }

@@ -21,6 +21,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib, head_hooks, vocab_pass
+from . import gemm as _gemm
 
 CHUNK = 512  # rows of logits per chunk, the unit of the logits budget (solution/fused_ce.py:33)
 IGNORE = -100
@@ -128,7 +129,9 @@ def fused_head_loss(hidden, weight, labels, attention_mask, num_items_in_batch):
         attention_mask = attention_mask.to(device)
     rows, n_labelled = _row_order(targets, attention_mask)
     denominator = _denominator(num_items_in_batch, n_labelled, device)
-    head = weight if weight.dtype == torch.float16 else weight.detach().to(torch.float16)
+    # the fp16 head (solution/fused_ce.py:202), cast once per frozen weight and kept while the
+    # weight is unchanged, so its transpose for dz @ W is kept with it
+    head = _gemm.frozen_as(weight, torch.float16)
     loss, row_loss, row_entropy, row_correct = FusedLinearCE.apply(
         hidden.reshape(-1, width)[rows], head, targets[rows], n_labelled, denominator)
     with torch.no_grad():

@@ -136,7 +136,7 @@ def group_forward(x2, specs, ab):
     _gemm.lora_down(x2, a16, u, out_t=ut)  # every slot in one pass over x
     y = torch.empty((M, offs[-1]), dtype=dt, device=dev)
     bias = _bias_cat(specs, dt, dev)
-    if all(nf4.use_fused_gemm(x2, s.qs, s.packed) for s in specs):
+    if all(nf4.use_fused_gemm(x2, s.qs, s.packed, a2=u) for s in specs):
         # few rows: each projection's W dequantised inside its GEMM (bs rows of projection g
         # are zero outside slot g, so u's other slots add nothing)
         for g, s in enumerate(specs):
@@ -355,7 +355,7 @@ class LoraMLP(torch.autograd.Function):
         swiglu.swiglu_fwd_lora_down(y[:, :n], y[:, n:], h, a16_d, u_d, ut_d)
         out = torch.empty((M, N), dtype=dt, device=dev)
         bias = None if dspec.bias is None else dspec.bias.to(dt)
-        if nf4.use_fused_gemm(h, dspec.qs, dspec.packed):  # few rows: W_d dequantised in-GEMM
+        if nf4.use_fused_gemm(h, dspec.qs, dspec.packed, a2=u_d):  # W_d dequantised in-GEMM
             nf4.gemm_nf4(h, dspec.packed, dspec.qs, out=out, a2=u_d, b2=bs_d, bias=bias)
         else:
             w = nf4.dequantize_nf4(dspec.packed, dspec.qs, dt)

@@ -104,15 +104,21 @@ class _Seeds:
 class LoRALinearFn(torch.autograd.Function):
     """lo = (xd @ A^T) @ B^T on the MFMA GEMM, with the adapter weight gradients:
         u = xd A^T;  lo = u B^T;   dB = dlo^T u;  du = dlo B;  dA = du^T xd;  dxd = du A
-    (the nn.Linear pair of solution/lora.py:172 and what autograd computes for it)."""
+    (the nn.Linear pair of solution/lora.py:172 and what autograd computes for it).
+    The MFMA GEMM takes 16-bit operands; with an fp32 compute dtype the same six products run
+    on torch's fp32 GEMM, which is what the reference's nn.Linear pair runs in any dtype."""
 
     @staticmethod
     def forward(ctx, xd, a_weight, b_weight):
         x2 = _rows(xd)
         a = a_weight.to(x2.dtype)
         b = b_weight.to(x2.dtype)
-        u = _gemm.gemm(x2, a)
-        lo = _gemm.gemm(u, b)
+        if x2.dtype == torch.float32:
+            u = x2 @ a.t()
+            lo = u @ b.t()
+        else:
+            u = _gemm.gemm(x2, a)
+            lo = _gemm.gemm(u, b)
         ctx.save_for_backward(x2, u, a, b)
         ctx.shape, ctx.wdtypes = xd.shape, (a_weight.dtype, b_weight.dtype)
         return lo.view(*xd.shape[:-1], b.shape[0])
@@ -122,6 +128,15 @@ class LoRALinearFn(torch.autograd.Function):
         x2, u, a, b = ctx.saved_tensors
         d2 = _rows(dlo).to(x2.dtype)
         da = db = dx = None
+        if x2.dtype == torch.float32:
+            du = d2 @ b                                                 # [M, r]
+            if ctx.needs_input_grad[2]:
+                db = (d2.t() @ u).to(ctx.wdtypes[1])
+            if ctx.needs_input_grad[1]:
+                da = (du.t() @ x2).to(ctx.wdtypes[0])
+            if ctx.needs_input_grad[0]:
+                dx = (du @ a).view(ctx.shape)
+            return dx, da, db
         du = _gemm.gemm(d2, b, b_kn=True)                               # [M, r]
         if ctx.needs_input_grad[2]:
             db = _gemm.matmul_tn(d2, u, out_dtype=torch.float32).to(ctx.wdtypes[1])
@@ -164,7 +179,7 @@ class LoraNF4Linear(torch.autograd.Function):
         _gemm.lora_down(x2, a16, u, out_t=ut)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
         b16 = None if bias is None else bias.to(dt)
-        if nf4.use_fused_gemm(x2, quant_state, packed):   # few rows: W dequantised in the GEMM
+        if nf4.use_fused_gemm(x2, quant_state, packed, a2=u):  # few rows: W dequantised in-GEMM
             nf4.gemm_nf4(x2, packed, quant_state, out=y, a2=u, b2=bs, bias=b16)
         else:
             w = nf4.dequantize_nf4(packed, quant_state, dt)

@@ -4,9 +4,10 @@ Every 4-bit layer call rebuilds the weight from the packed NF4 nibbles and the
 double-quantised block scales (solution/nf4.py:1-16); here that rebuild is the gfx950 kernel
 `qlora_nf4_dequant`, with the scale dequantisation `code2[q] * absmax2 + offset` folded in and
 evaluated with the same fp32 operation order, so the weights come out bit-identical to the
-reference's formula. The contraction runs in the library's bf16/fp16 MFMA GEMM
-(`qlora_gemm`), and the backward re-dequantises (nothing dense is kept between forward and
-backward, solution/nf4.py:95-112).
+reference's formula. A bf16/fp16 contraction runs in the library's MFMA GEMM (`qlora_gemm`);
+an fp32 one (bitsandbytes' default compute dtype) runs in torch's fp32 GEMM on the kernel's
+fp32 weight, as the reference does. The backward re-dequantises (nothing dense is kept
+between forward and backward, solution/nf4.py:95-112).
 
 Signatures kept from the reference: `dequantize_nf4(packed, quant_state, dtype)`,
 `supported(qs)`, `NF4Linear.apply(x, packed, quant_state, bias)`, `_prepare(module, x)`,
@@ -46,14 +47,16 @@ def _offset_value(quant_state):
     """The double-quant offset as a Python float. Reading it from a device tensor
     synchronises the host (solution/nf4.py:81 does so on every call, 392 times per 7B step)
     and is not allowed under graph capture, so the value is read once per offset tensor and
-    cached on the state; assigning a new offset tensor invalidates the cache."""
+    cached on the state; assigning a new offset tensor, or changing it in place (which bumps
+    its version counter), invalidates the cache."""
     off = quant_state.offset
+    version = getattr(off, "_version", None)
     cached = getattr(quant_state, "_ql_offset", None)
-    if cached is not None and cached[0] is off:
-        return cached[1]
+    if cached is not None and cached[0] is off and cached[1] == version:
+        return cached[2]
     value = float(off)
     try:
-        quant_state._ql_offset = (off, value)
+        quant_state._ql_offset = (off, version, value)
     except AttributeError:  # a state object that takes no new attributes
         pass
     return value
@@ -191,16 +194,23 @@ def dequantize_nf4_t_group(items, dtype, outs):
 FUSED_GEMM_MAX_ROWS = 256
 
 
-def use_fused_gemm(x2, quant_state, packed):
-    """Whether the forward of x2 [M, K] against this NF4 weight takes gemm_nf4."""
-    return x2.shape[0] <= FUSED_GEMM_MAX_ROWS and fused_gemm_ok(quant_state, packed, x2)
+def use_fused_gemm(x2, quant_state, packed, a2=None):
+    """Whether the forward of x2 [M, K] (with the rank-16 segment a2 when given) against this
+    NF4 weight takes gemm_nf4."""
+    return x2.shape[0] <= FUSED_GEMM_MAX_ROWS and fused_gemm_ok(quant_state, packed, x2, a2)
 
 
-def fused_gemm_ok(quant_state, packed, x=None):
-    """Whether gemm_nf4 takes this weight (and input x [M, K] when given): in_features a
-    multiple of 64, blocksize a power of two >= 64 dividing it (blocksize2 a power of two),
-    packed codes 16-B aligned; x 16-bit, 16-B aligned rows of unit stride."""
+GEMM_NF4_MAX_K2 = 64  # the second K segment is one K step of the tile (qlora_gemm_nf4)
+
+
+def fused_gemm_ok(quant_state, packed, x=None, a2=None):
+    """Whether gemm_nf4 takes this weight (and input x [M, K], segment a2 [M, K2] when given):
+    in_features a multiple of 64, blocksize a power of two >= 64 dividing it (blocksize2 a
+    power of two), packed codes 16-B aligned; x 16-bit, 16-B aligned rows of unit stride;
+    K2 a multiple of 64 and at most 64."""
     if packed.data_ptr() % 16:
+        return False
+    if a2 is not None and (a2.shape[1] % 64 or a2.shape[1] > GEMM_NF4_MAX_K2):
         return False
     _, cols = tuple(quant_state.shape)
     bs = int(quant_state.blocksize)
@@ -222,7 +232,7 @@ def gemm_nf4(x, packed, quant_state, out=None, a2=None, b2=None, bias=None, alph
     """out = alpha * (x @ W^T + a2 @ b2^T) (+ bias) with W [N, K] the NF4 weight of
     `quant_state`, dequantised inside the GEMM to x's dtype (bit-identical to the GEMM on
     dequantize_nf4(packed, quant_state, x.dtype)); a2 [M, K2] and b2 [N, K2] are the optional
-    rank-16 segment (K2 <= 128) (qlora_gemm_nf4). x [M, K] 2-D."""
+    rank-16 segment (K2 = 64: one K step) (qlora_gemm_nf4). x [M, K] 2-D."""
     _lib.require_device(x, packed)
     N, K = tuple(quant_state.shape)
     M = x.shape[0]
@@ -271,6 +281,11 @@ class NF4Linear(torch.autograd.Function):
             out = gemm_nf4(x2, packed, quant_state, bias=bias)  # W dequantised in the GEMM
             return out.view(*x.shape[:-1], out.shape[-1])
         weight = dequantize_nf4(packed, quant_state, x.dtype)
+        if x.dtype == torch.float32:
+            # fp32 compute (bitsandbytes' default compute dtype): the library's MFMA GEMMs take
+            # 16-bit operands, so the fp32 product is torch's, on the kernel's fp32 W, as in
+            # solution/nf4.py:100-102
+            return torch.nn.functional.linear(x, weight, bias)
         return _gemm.linear(x, weight, bias)
 
     @staticmethod
@@ -279,7 +294,10 @@ class NF4Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             qs = ctx.quant_state
             rows = tuple(qs.shape)[0]
-            if grad_out.dtype in (torch.bfloat16, torch.float16) \
+            if grad_out.dtype == torch.float32:
+                weight = dequantize_nf4(ctx.packed, qs, torch.float32)
+                grad_x = torch.matmul(grad_out, weight)                # solution/nf4.py:110-111
+            elif grad_out.dtype in (torch.bfloat16, torch.float16) \
                     and transposed_dequant_ok(qs, ctx.packed) and rows % 64 == 0:
                 # dY @ W as an NT GEMM against W^T, dequantised straight into that layout
                 weight_t = dequantize_nf4_t(ctx.packed, qs, grad_out.dtype)
@@ -293,7 +311,8 @@ class NF4Linear(torch.autograd.Function):
 def _prepare(module, x):
     """The part of a 4-bit layer's forward before the matmul (solution/nf4.py:115-138):
     returns (x, bias, input dtype), or None when this layer should take the original path.
-    bf16 compute is accepted here (the reference accepted fp16/fp32 only, :131-132)."""
+    bf16 compute is accepted here (the reference accepted fp16/fp32 only, :131-132); fp32
+    compute runs NF4Linear's fp32 branch (the kernel's fp32 W and torch's fp32 GEMM)."""
     quant_state = getattr(module.weight, "quant_state", None)
     if (not x.is_cuda or not supported(quant_state) or module.weight.requires_grad
             or (module.bias is not None and module.bias.requires_grad)):

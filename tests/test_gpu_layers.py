@@ -153,3 +153,75 @@ def test_fused_and_unfused_lora_layer_agree(in_f, out_f):
     for a, b in zip(*results):
         s = b.abs().max().item()
         torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2 * s)
+
+
+def _deq_f32(packed, st):
+    """The oracle's fp32 dequantised weight (what the kernel's fp32 output must equal)."""
+    w = onf4.dequant_state(packed, st, TABLE, out="f32")
+    return torch.from_numpy(w).view(tuple(st.shape))
+
+
+def _close_f32(got, want, K, amax, bmax):
+    # fp32 products and sums (any order) of K terms, plus the output rounding
+    bound = 2 * K * 2.0**-24 * amax * bmax + 2.0**-23 * want.abs() + 1e-30
+    assert torch.all((got.double() - want).abs() <= bound), \
+        float(((got.double() - want).abs() / bound).max())
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_linear4bit_fp32_compute(bias):
+    """bitsandbytes' default: no compute dtype set, fp32 input, so the layer computes in fp32
+    (solution/nf4.py:100-104,131-132): dequant kernel to fp32 W, then an fp32 GEMM. Output and
+    input gradient against F.linear on the oracle's fp32 W, in fp64."""
+    print(f"Linear4bit fp32 compute bias={bias}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    M, N, K = 96, 320, 512
+    w = torch.randn(N, K, generator=g) * 0.02
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    layer = quant.Linear4bit.from_weight(w, bias=b).cuda()
+    assert layer.compute_dtype is None
+    wq = _deq_f32(layer.weight.data.cpu(), layer.weight.quant_state).double()
+    # the kernel's fp32 W is the oracle's, bit for bit
+    wk = nf4.dequantize_nf4(layer.weight.data, layer.weight.quant_state, torch.float32)
+    assert torch.equal(wk.cpu(), wq.float())
+    x = torch.randn(M, K, generator=g)
+    xg = x.cuda().requires_grad_()
+    y = layer(xg)
+    assert y.dtype == torch.float32 and layer.compute_dtype == torch.float32
+    y_ref = x.double() @ wq.t() + (b.double() if bias else 0)
+    _close_f32(y.detach().cpu(), y_ref, K, x.abs().max().item(), wq.abs().max().item())
+    dy = torch.randn(M, N, generator=g)
+    y.backward(dy.cuda())
+    _close_f32(xg.grad.cpu(), dy.double() @ wq, N, dy.abs().max().item(), wq.abs().max().item())
+
+
+def test_lora_layer_fp32_compute():
+    """LoraLinear4bit(compute_dtype=float32) on an fp32-compute base: base(x) + 2 B(A(x)) and
+    the gradients to x, A and B, against fp64 on the oracle's fp32 W."""
+    g = torch.Generator().manual_seed(22)
+    M, in_f, out_f = 128, 256, 192
+    w = torch.randn(out_f, in_f, generator=g) * 0.02
+    base = quant.Linear4bit.from_weight(w, compute_dtype=torch.float32)
+    layer = lora.LoraLinear4bit(base, r=16, lora_alpha=32, compute_dtype=torch.float32)
+    with torch.no_grad():
+        layer.lora_A["default"].weight.normal_(0, 0.25, generator=g)
+        layer.lora_B["default"].weight.normal_(0, 0.01, generator=g)
+    A = layer.lora_A["default"].weight.detach().clone().double()
+    B = layer.lora_B["default"].weight.detach().clone().double()
+    wq = _deq_f32(base.weight.data, base.weight.quant_state).double()
+    layer = layer.cuda()
+    x = torch.randn(M, in_f, generator=g)
+    dy = torch.randn(M, out_f, generator=g)
+    xg = x.cuda().requires_grad_()
+    y = layer(xg)
+    assert y.dtype == torch.float32
+    y.backward(dy.cuda())
+    xd = x.double().requires_grad_()
+    Ad, Bd = A.clone().requires_grad_(), B.clone().requires_grad_()
+    y_ref = xd @ wq.t() + 2.0 * ((xd @ Ad.t()) @ Bd.t())
+    y_ref.backward(dy.double())
+    for got, want in ((y.detach(), y_ref.detach()), (xg.grad, xd.grad),
+                      (layer.lora_A["default"].weight.grad, Ad.grad),
+                      (layer.lora_B["default"].weight.grad, Bd.grad)):
+        s = want.abs().max().item()
+        torch.testing.assert_close(got.cpu().double(), want, rtol=1e-4, atol=1e-5 * s)

@@ -7,8 +7,17 @@ activations and GEMMs). The bf16 paths differ from it by rounding alone, and at 
 bf16 paths sit a few percent from it. The bar:
   - loss within 1e-4 relative of the fp32 reference (and within 2e-3 of eager bf16);
   - every adapter gradient at least as close to the fp32 reference as the eager bf16 path's
-    (relative Frobenius error <= 1.25 x eager's + 1e-3).
+    (relative Frobenius error <= 1.25 x eager's + 1e-3);
+  - at two layers, every adapter gradient within a fixed relative Frobenius error of the fp32
+    reference: the tightest round value the eager bf16 path meets on every tensor (measured on
+    MI355X: eager 1.1e-2 .. 2.0e-2, patched 1.0e-2 .. 1.9e-2 at the tiny shape; eager
+    3.5e-2 .. 7.9e-2, patched 3.0e-2 .. 7.0e-2 at the 7B shape).
+The per-layer check with a tight bar is tests/test_gpu_decoder_7b.py (one 7B decoder layer against
+fp64, about 1e-2) and tests/test_gpu_mlp_7b.py (the 7B LoRA MLP against fp64, about 4e-3).
 """
+
+# fixed per-tensor bars on the relative Frobenius error of the adapter gradients at two layers
+ABS_BAR = {"tiny": 2.5e-2, "qwen25_7b_2layers": 8e-2}
 
 import copy
 
@@ -60,10 +69,14 @@ def test_patched_step_matches_fp32_reference(shape):
     assert torch.isfinite(loss_p)
     assert abs(loss_p.item() - loss_32.item()) <= 1e-4 * abs(loss_32.item()), (loss_p, loss_32)
     assert abs(loss_p.item() - loss_e.item()) <= 2e-3 * abs(loss_e.item()), (loss_p, loss_e)
-    for a, b, c in zip(g_p, g_e, g_32):
-        err_p = ((a - c).norm() / c.norm()).item()
-        err_e = ((b - c).norm() / c.norm()).item()
+    errs = [(((a - c).norm() / c.norm()).item(), ((b - c).norm() / c.norm()).item())
+            for a, b, c in zip(g_p, g_e, g_32)]
+    print(f"{shape}: loss fp32 {loss_32.item():.7f} patched {loss_p.item():.7f} eager "
+          f"{loss_e.item():.7f}; adapter grad errors (patched, eager): "
+          + " ".join(f"{p:.2e},{e:.2e}" for p, e in errs), flush=True)
+    for err_p, err_e in errs:
         assert err_p <= 1.25 * err_e + 1e-3, (err_p, err_e)
+        assert err_p <= ABS_BAR[shape], (err_p, ABS_BAR[shape])
 
 
 def _rel(a, b):

@@ -205,3 +205,36 @@ def test_rank16_wrappers_check_dtype_layout_and_device():
                 return bad.stride(i)
         with pytest.raises(err):
             _lib.require_rows(torch.bfloat16, y=Fake())
+
+
+def test_offset_cache_follows_in_place_updates():
+    """The double-quant offset is read from its tensor once and cached on the state; a new
+    tensor or an in-place change of the same one is seen on the next call."""
+    _, st = quant.quantize_nf4(torch.randn(64, 128) * 0.02, 64)
+    first = nf4._offset_value(st)
+    assert first == float(st.offset)
+    st.offset.add_(0.25)                       # in place: same object, new version
+    assert nf4._offset_value(st) == float(st.offset) != first
+    st.offset = torch.tensor(1.5)
+    assert nf4._offset_value(st) == 1.5
+
+
+def test_fused_gemm_guard_checks_the_segment_width():
+    packed, st = quant.quantize_nf4(torch.randn(128, 256) * 0.02, 64)
+    x = torch.zeros(8, 256, dtype=torch.bfloat16)
+    assert nf4.fused_gemm_ok(st, packed, x)
+    assert nf4.fused_gemm_ok(st, packed, x, torch.zeros(8, 64, dtype=torch.bfloat16))
+    assert not nf4.fused_gemm_ok(st, packed, x, torch.zeros(8, 128, dtype=torch.bfloat16))
+    assert not nf4.use_fused_gemm(x, st, packed, torch.zeros(8, 128, dtype=torch.bfloat16))
+
+
+def test_frozen_head_cast_is_kept():
+    """An fp32 head weight is cast to the fused head's fp16 once and reused while unchanged."""
+    from hackathon_amd import gemm
+
+    w = torch.randn(64, 32)
+    h1 = gemm.frozen_as(w, torch.float16)
+    assert h1.dtype == torch.float16 and gemm.frozen_as(w, torch.float16) is h1
+    w.mul_(2.0)                                # a change of the weight makes a new copy
+    h2 = gemm.frozen_as(w, torch.float16)
+    assert h2 is not h1 and torch.equal(h2, w.to(torch.float16))
