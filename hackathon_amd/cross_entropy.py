@@ -28,7 +28,9 @@ from . import _common, _lib, head_hooks, vocab_pass
 from . import gemm as _gemm
 
 IGNORE_INDEX = -100
-CHUNK_ROWS = 512  # rows of logits per chunk, the unit of the logits budget
+# rows of logits per chunk (solution/cross_entropy.py:37): as the default argument, the unit of
+# the engine's logits budget; passed explicitly, the bound on the live logits
+CHUNK_ROWS = vocab_pass.EngineRows(512)
 BLOCK_V = 4096  # the reference's vocab block (solution/cross_entropy.py:39); tiles are internal
 GRAD_GAIN = 65536.0  # power of two: scaling dz by it and dividing it out in fp32 is exact
 STEP_ATTR = head_hooks.STEP_ATTR

@@ -23,7 +23,9 @@ import torch
 from . import _lib, head_hooks, vocab_pass
 from . import gemm as _gemm
 
-CHUNK = 512  # rows of logits per chunk, the unit of the logits budget (solution/fused_ce.py:33)
+# rows of logits per chunk (solution/fused_ce.py:33): left as it is, the unit of the engine's
+# logits budget; set to another value (a plain int, 512 included), the bound on the live logits
+CHUNK = vocab_pass.EngineRows(512)
 IGNORE = -100
 STEP_ATTR = head_hooks.STEP_ATTR
 VARIANT = "fused_ce"

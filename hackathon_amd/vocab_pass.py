@@ -13,12 +13,15 @@ For each group of rows, three launches on the stream of the hidden states:
                                contiguous reduction), fp32 out, for the rows that need it
 
 Grouping. The reference bounds the live logits at `chunk_rows` rows (512 x 151936 x 2 B =
-155 MB). An MI355X has 288 GB of HBM, so the engine runs as many whole chunks per GEMM as fit
+155 MB). An MI355X has 288 GB of HBM, so with the callers' default chunk size (`EngineRows`,
+the value 512 marked as the default) the engine runs as many whole chunks per GEMM as fit
 `LOGITS_BUDGET` bytes of logits (still a fixed bound, independent of the batch): W (467 MB at
-151936 x 1536 bf16) is streamed once per group rather than once per chunk, and dz @ W becomes one tall GEMM instead of sixteen skinny
-split-K ones. The groups are balanced and the row count of each a multiple of 256 (one GEMM
-tile) where possible. Per-row results do not depend on the grouping: each row's statistics
-come from its own logits, and each row of grad_h from its own dz.
+151936 x 1536 bf16) is streamed once per group rather than once per chunk, and dz @ W becomes
+one tall GEMM instead of sixteen skinny split-K ones. A chunk size a caller passes explicitly
+(any plain int, 512 included) is the reference's hard bound: groups of at most that many rows.
+The groups are balanced and the row count of each a multiple of 256 (one GEMM tile) where
+possible. Per-row results do not depend on the grouping: each row's statistics come from its
+own logits, and each row of grad_h from its own dz.
 """
 
 from __future__ import annotations
@@ -36,6 +39,24 @@ from . import gemm as _gemm
 # 2048 8.13-8.27 ms, eight of 1024 8.97-9.11 ms.
 LOGITS_BUDGET = 5 << 28
 TILE_ROWS = 256          # the NT GEMM's M tile
+
+
+
+class EngineRows(int):
+    """The reference's default chunk size (512 rows) as the façades' default argument: passed
+    as is, the engine groups whole chunks up to LOGITS_BUDGET; any other value, a plain 512
+    included, bounds the live logits at that many rows, as solution/cross_entropy.py:37-38 and
+    solution/fused_ce.py:33 do."""
+
+    def __repr__(self):
+        return int.__repr__(self)
+
+
+def budget_for(chunk_rows):
+    """Bytes of live logits a group may hold for this chunk argument: LOGITS_BUDGET for the
+    default (EngineRows), else 0, which plan_groups turns into one chunk per group."""
+    return LOGITS_BUDGET if isinstance(chunk_rows, EngineRows) else 0
+
 
 IGNORE_NEGATIVE = 0      # a row is labelled when its target is >= 0 (solution/fused_ce.py:48)
 IGNORE_MINUS_100 = 1     # a row is labelled when its target is not -100 (cross_entropy.py:54)
@@ -96,12 +117,14 @@ def run(hidden, weight, target, out, *, ignore_mode, chunk_rows, grad=None, grad
     """One pass of `hidden` [n, H] (the matmul dtype, unit stride along H) through the frozen
     head `weight` [V, H] (same dtype): per-row statistics into `out` (a RowResults of n rows)
     and, when `grad` (fp32 [n, H]) is given, grad[r] = dz[r] @ W for the rows r < grad_rows;
-    rows from grad_rows on are left untouched in `grad`. `target` is int64 [n] on the device."""
+    rows from grad_rows on are left untouched in `grad`. `target` is int64 [n] on the device.
+    `chunk_rows`: an EngineRows lets groups grow to LOGITS_BUDGET; a plain int is the bound on
+    the rows of live logits."""
     n, vocab = hidden.shape[0], weight.shape[0]
     if hidden.dtype != weight.dtype or weight.dtype not in (torch.float16, torch.bfloat16):
         raise TypeError("the head GEMMs take fp16 or bf16 operands of one dtype, got "
                         f"{hidden.dtype} and {weight.dtype}")
-    groups = plan_groups(n, vocab, chunk_rows, weight.element_size())
+    groups = plan_groups(n, vocab, chunk_rows, weight.element_size(), budget_for(chunk_rows))
     if not groups:
         return
     want_grad = grad is not None and grad_rows > 0

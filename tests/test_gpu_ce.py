@@ -193,3 +193,48 @@ def test_fused_ce_full_qwen25_shape_rows_vs_oracle():
           f"1e-4 (within one logit ulp): {boundary_rows}", flush=True)
     assert abs(float(loss) - total_r / float(denom)) <= 1e-4 * abs(total_r / float(denom))
     assert ulp_ties <= n // 100 and boundary_rows <= n // 100
+
+
+@pytest.mark.parametrize("variant", ["cross_entropy", "fused_ce"])
+def test_explicit_chunk_rows_bounds_live_logits(variant, monkeypatch):
+    """At 4096 tokens x 1536 x 151936 (1.25 GB of bf16 logits), the default chunk argument lets
+    the engine hold one group of 4096 rows; an explicit chunk of 512 rows (the reference's
+    bound) keeps the extra memory of the call near one 512-row chunk (156 MB) plus the hidden
+    gradient, with the same per-row results."""
+    print(f"chunk_rows bound, {variant}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    n, H, V = 4096, 1536, 151936
+    hidden = torch.randn(n, H, generator=g).to(torch.bfloat16).cuda()
+    weight = (torch.randn(V, H, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    labels = torch.randint(0, V, (1, n), generator=g).cuda()
+
+    def call(chunk):
+        hg = hidden.clone().requires_grad_()
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        if variant == "cross_entropy":
+            kw = {} if chunk is None else {"chunk_rows": chunk}
+            loss, step = cross_entropy.fused_causal_lm_loss(hg[None], weight, labels, **kw)
+            tok = step.token_loss
+        else:
+            if chunk is not None:
+                monkeypatch.setattr(fused_ce, "CHUNK", chunk)
+            loss, stats = fused_ce.fused_head_loss(hg[None], weight, labels, None, None)
+            tok = stats.token_loss
+        loss.backward()
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - base
+        monkeypatch.setattr(fused_ce, "CHUNK", cross_entropy.CHUNK_ROWS)
+        return peak, loss.detach(), tok.detach(), hg.grad
+
+    call(None)  # caches the transposed head weight for dz @ W
+    peak_default, loss_d, tok_d, grad_d = call(None)
+    peak_512, loss_b, tok_b, grad_b = call(512)
+    print(f"extra memory of the call: default {peak_default / 2**20:.0f} MiB, chunk_rows=512 "
+          f"{peak_512 / 2**20:.0f} MiB", flush=True)
+    assert peak_default >= n * V * 2
+    assert peak_512 <= 512 * V * 2 + 160 * 2**20
+    assert torch.equal(tok_d, tok_b)
+    assert torch.equal(loss_d, loss_b)
+    torch.testing.assert_close(grad_b, grad_d, rtol=1e-2, atol=1e-2 * grad_d.abs().max().item())

@@ -57,3 +57,23 @@ def test_fp32_model_keeps_its_own_forward():
     dt = cross_entropy._matmul_dtype(cross_entropy._hidden_dtype(lm), lm.lm_head.weight.dtype)
     assert dt not in cross_entropy.MATMUL_DTYPES
     assert not cross_entropy._head_ok(lm)  # on the CPU it is refused for the device as well
+
+
+def test_explicit_chunk_rows_bound_the_live_logits():
+    """The default chunk argument lets groups grow to the engine's budget; an explicitly passed
+    chunk size (a plain int, 512 included) bounds every group at that many rows, as the
+    reference's chunk loop does."""
+    import inspect
+
+    from hackathon_amd import fused_ce
+
+    default = inspect.signature(cross_entropy.fused_causal_lm_loss).parameters["chunk_rows"].default
+    assert default == 512 and repr(default) == "512"
+    assert vocab_pass.budget_for(default) == vocab_pass.LOGITS_BUDGET
+    assert vocab_pass.budget_for(fused_ce.CHUNK) == vocab_pass.LOGITS_BUDGET
+    for chunk in (512, 256, 1000):
+        groups = vocab_pass.plan_groups(8192, 151936, chunk, 2, vocab_pass.budget_for(chunk))
+        assert max(b - a for a, b in groups) <= chunk
+        assert [r for a, b in groups for r in range(a, b)] == list(range(8192))
+    groups = vocab_pass.plan_groups(8192, 151936, default, 2, vocab_pass.budget_for(default))
+    assert groups == [(0, 4096), (4096, 8192)]
