@@ -24,6 +24,7 @@ Also reported in the same line:
                  and the Qwen2.5-7B LoRA MLP forward + backward at 4096 tokens (patched vs
                  eager, TFLOP/s against 3.364 TFLOP of work)
   qlora_step     Qwen2.5-7B-shaped QLoRA training step tokens/s, patched vs PyTorch eager
+  qlora_step_dropout  the same step with LoRA dropout 0.05 on every adapter
 
 `python bench.py --gpus N --steps K --warmup W`; N > 1 is not run (one GPU only).
 """
@@ -809,14 +810,17 @@ def bench_mlp(torch, tokens=4096, reps=3):
 
 # ---------------------------------------------------------------------------------------------
 def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=2048,
-               parity=True):
-    """Qwen2.5-7B-shaped QLoRA step (28 layers unless `layers`), tokens/s patched and eager."""
+               parity=True, dropout=0.0):
+    """Qwen2.5-7B-shaped QLoRA step (28 layers unless `layers`), tokens/s patched and eager.
+    With `dropout` > 0 every LoRA adapter drops its input with that probability (the
+    reference's training regime, p = 0.05): the patched layers draw the mask from the package's
+    Philox stream and eager from torch's RNG, so the step-0 losses differ by the masks."""
     from hackathon_amd import qlora_step
 
     over = {} if layers is None else {"num_hidden_layers": layers}
     cfg = qlora_step.qwen2_config(**over)
     t0 = time.perf_counter()
-    model = qlora_step.build_qlora_model(cfg, "cuda")
+    model = qlora_step.build_qlora_model(cfg, "cuda", dropout=dropout)
     torch.cuda.synchronize()
     log(f"[bench] model built in {time.perf_counter() - t0:.1f} s")
     ids, labels = qlora_step.make_batch(batch, seq, cfg.vocab_size)
@@ -855,7 +859,8 @@ def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=20
                tokens_per_s=round(tokens / t_p, 1), loss=round(loss_p, 5),
                step0_loss_patched=round(loss_p0, 6), step0_loss_eager=round(loss_e0, 6),
                step0_loss_rel_diff=round(abs(loss_p0 - loss_e0) / abs(loss_e0), 7),
-               peak_mem_gib=round(peak_p, 1), layers=cfg.num_hidden_layers)
+               peak_mem_gib=round(peak_p, 1), layers=cfg.num_hidden_layers,
+               lora_dropout=dropout)
     if eager_steps:
         with qlora_step.eager_mode(model):
             step_e = qlora_step.QLoRAStep(model, fused_head=False)
@@ -1002,6 +1007,8 @@ def main():
     ap.add_argument("--no-cpu-configs", action="store_true",
                     help="skip the host CPU baselines of the other configs")
     ap.add_argument("--step-steps", type=int, default=5)
+    ap.add_argument("--no-dropout-step", action="store_true",
+                    help="skip the step with LoRA dropout 0.05")
     ap.add_argument("--step-layers", type=int, default=None)
     ap.add_argument("--eager-steps", type=int, default=2,
                     help="timed steps of the eager baseline (0: skip it and the parity check)")
@@ -1086,6 +1093,11 @@ def main():
     if not args.no_step:
         line["qlora_step"] = bench_step(torch, args.step_steps, 2, eager_steps=args.eager_steps,
                                         layers=args.step_layers, parity=args.eager_steps > 0)
+        if not args.no_dropout_step:
+            torch.cuda.empty_cache()
+            line["qlora_step_dropout"] = bench_step(
+                torch, args.step_steps, 2, eager_steps=args.eager_steps, layers=args.step_layers,
+                parity=args.eager_steps > 0, dropout=0.05)
     line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     line["cpu_baseline"]["host_cpu"] = _cpu_model()
     line["cpu_baseline_c_1thread"] = cpu_baseline_nf4_c(min(args.cpu_seconds, 5.0))

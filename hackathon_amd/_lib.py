@@ -59,6 +59,10 @@ _SIGNATURES = {
                                  _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_scaled_add": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,
                               _c_i64, _c_i64, _c_i64, _c_f32, _c_ptr],
+    "qlora_lora_dropout_scale_bits": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64,
+                                      _c_i64, _c_int, _c_u64, _c_f32, _c_f32, _c_ptr],
+    "qlora_lora_up_masked_add": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+                                 _c_i64, _c_i64, _c_int, _c_f32, _c_ptr],
     "qlora_gemm": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int,
                    _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32, _c_f32, _c_ptr],
     "qlora_gemm_ws": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,

@@ -78,6 +78,70 @@ __global__ __launch_bounds__(kThreads) void dropout_scale_kernel(
   }
 }
 
+// The dropout forward for the fused 4-bit LoRA layer: the same OUT = IN * keep * scale as
+// dropout_scale_kernel (vector rows only), plus the keep mask as bits, byte c / 8 of row `row`
+// holding columns c .. c + 7 (bit j = column c + j), so the backward needs no second Philox pass.
+template <int IT, int OT>
+__global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
+    const typename Elem<IT>::T* __restrict__ in, int64_t in_rs, typename Elem<OT>::T* __restrict__ out,
+    int64_t out_rs, uint8_t* __restrict__ bits, int64_t bits_rs, int64_t n_cols, uint64_t seed,
+    float p, float scale) {
+  const int64_t row = blockIdx.x;
+  const auto* src = in + row * in_rs;
+  auto* dst = out + row * out_rs;
+  for (int64_t c = 8 * (int64_t)threadIdx.x; c < n_cols; c += 8 * kThreads) {
+    float v[8];
+    Vec8<IT>::load(src + c, v);
+    uint32_t b = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t flat = (uint32_t)(row * n_cols + c + j);
+      const bool keep = uniform_from_word(philox_word0(flat, seed)) > p;
+      v[j] = keep ? v[j] * scale : 0.0f;
+      b |= (uint32_t)keep << j;
+    }
+    Vec8<OT>::store(dst + c, v);
+    bits[row * bits_rs + c / 8] = (uint8_t)b;
+  }
+}
+
+// The dropout backward of the adapter's input gradient, added to the base gradient:
+//   dx[m, k] += keep(m, k) ? scale * sum_{r < 16} du[m, r] * A[r, k] : 0
+// (du = s g B [M, >= 16], A [16, K] in dx's dtype; keep from the forward's bits). The rank-16
+// sum runs in fp32 in order r = 0 .. 15 and dx is rounded once. Each thread owns 8 consecutive
+// columns (A's 16 x 8 values stay in registers) and walks kRowsPerGroup rows.
+constexpr int kUpRows = 16;
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void up_masked_add_kernel(
+    typename Elem<DT>::T* __restrict__ dx, int64_t dx_rs, const typename Elem<DT>::T* __restrict__ du,
+    int64_t du_rs, const typename Elem<DT>::T* __restrict__ A, int64_t a_rs,
+    const uint8_t* __restrict__ bits, int64_t bits_rs, int64_t M, int64_t K, float scale) {
+#pragma clang fp contract(off)
+  const int64_t c = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 8;
+  if (c >= K) return;
+  float a[16][8];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) Vec8<DT>::load(A + r * a_rs + c, a[r]);
+  const int64_t m0 = (int64_t)blockIdx.y * kUpRows;
+  const int64_t m1 = m0 + kUpRows < M ? m0 + kUpRows : M;
+  for (int64_t m = m0; m < m1; ++m) {
+    float d[16], v[8];
+    Vec8<DT>::load(du + m * du_rs, d);
+    Vec8<DT>::load(du + m * du_rs + 8, d + 8);
+    Vec8<DT>::load(dx + m * dx_rs + c, v);
+    const uint32_t b = bits[m * bits_rs + c / 8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float t = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) t = __builtin_fmaf(d[r], a[r][j], t);
+      if ((b >> j) & 1u) v[j] = v[j] + scale * t;
+    }
+    Vec8<DT>::store(dx + m * dx_rs + c, v);
+  }
+}
+
 template <int BT, int LT, int OT, bool VEC>
 __global__ __launch_bounds__(kThreads) void scaled_add_kernel(
     const typename Elem<BT>::T* __restrict__ base, int64_t b_rs, const typename Elem<LT>::T* __restrict__ lo,
@@ -180,4 +244,60 @@ extern "C" int qlora_lora_scaled_add(const void* base, int base_dtype, int64_t b
                                                out_row_stride, n_rows, n_cols, scaling, vec,
                                                static_cast<hipStream_t>(stream)));
   return QL_EDTYPE;
+}
+
+extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* out,
+                                             int64_t out_row_stride, uint8_t* bits,
+                                             int64_t bits_row_stride, int64_t n_rows,
+                                             int64_t n_cols, int dtype, uint64_t seed, float p,
+                                             float scale, ql_stream_t stream) {
+  if (n_rows < 0 || n_cols < 0 || n_rows > UINT32_MAX || !(p > 0.0f) || !(p < 1.0f))
+    return QL_EINVAL;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  if (n_rows == 0 || n_cols == 0) return QL_OK;
+  if (!in || !out || !bits) return QL_EINVAL;
+  if (n_cols % 8 || bits_row_stride < n_cols / 8) return QL_ESHAPE;
+  if (!rows_vec_ok(in, in_row_stride, dtype, n_cols) || !rows_vec_ok(out, out_row_stride, dtype, n_cols))
+    return QL_EALIGN;
+  const dim3 grid((unsigned)n_rows);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  using B = typename Elem<QL_BF16>::T;
+  if (dtype == QL_BF16)
+    hipLaunchKernelGGL((dropout_bits_kernel<QL_BF16, QL_BF16>), grid, dim3(kThreads), 0, s,
+                       (const B*)in, in_row_stride, (B*)out, out_row_stride, bits,
+                       bits_row_stride, n_cols, seed, p, scale);
+  else
+    hipLaunchKernelGGL((dropout_bits_kernel<QL_F16, QL_F16>), grid, dim3(kThreads), 0, s,
+                       (const B*)in, in_row_stride, (B*)out, out_row_stride, bits,
+                       bits_row_stride, n_cols, seed, p, scale);
+  return ql_launch_status();
+}
+
+extern "C" int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
+                                        int64_t du_row_stride, const void* A, int64_t a_row_stride,
+                                        const uint8_t* bits, int64_t bits_row_stride, int64_t M,
+                                        int64_t K, int dtype, float scale, ql_stream_t stream) {
+  if (M < 0 || K < 0) return QL_EINVAL;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  if (M == 0 || K == 0) return QL_OK;
+  if (!dx || !du || !A || !bits) return QL_EINVAL;
+  if (K % 8 || bits_row_stride < K / 8 || du_row_stride < 16 || a_row_stride < K)
+    return QL_ESHAPE;
+  if (!rows_vec_ok(dx, dx_row_stride, dtype, K) || !rows_vec_ok(A, a_row_stride, dtype, K) ||
+      !rows_vec_ok(du, du_row_stride, dtype, 16))
+    return QL_EALIGN;
+  const int64_t gx = (K / 8 + kThreads - 1) / kThreads, gy = (M + kUpRows - 1) / kUpRows;
+  if (gx > INT32_MAX || gy > 65535) return QL_ESHAPE;
+  const dim3 grid((unsigned)gx, (unsigned)gy);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  using B = typename Elem<QL_BF16>::T;
+  if (dtype == QL_BF16)
+    hipLaunchKernelGGL((up_masked_add_kernel<QL_BF16>), grid, dim3(kThreads), 0, s, (B*)dx,
+                       dx_row_stride, (const B*)du, du_row_stride, (const B*)A, a_row_stride, bits,
+                       bits_row_stride, M, K, scale);
+  else
+    hipLaunchKernelGGL((up_masked_add_kernel<QL_F16>), grid, dim3(kThreads), 0, s, (B*)dx,
+                       dx_row_stride, (const B*)du, du_row_stride, (const B*)A, a_row_stride, bits,
+                       bits_row_stride, M, K, scale);
+  return ql_launch_status();
 }

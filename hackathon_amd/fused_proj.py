@@ -64,6 +64,8 @@ def lora_spec(layer, x):
         return None
     drop = layer.lora_dropout[adapter]
     p = float(drop.p) if isinstance(drop, torch.nn.Dropout) and drop.training else 0.0
+    if p != 0:  # each adapter of a group would need its own mask of the shared input
+        return None
     fused = lora._fused_base(layer, adapter, x, compute_dtype, p)
     if fused is None:
         return None

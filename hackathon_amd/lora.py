@@ -150,22 +150,41 @@ class LoRALinearFn(torch.autograd.Function):
 _PAD = 64  # rank-16 factors are zero-padded to one 64-wide K step of the NT GEMM
 
 
-class LoraNF4Linear(torch.autograd.Function):
-    """The whole 4-bit LoRA linear (p = 0, rank 16) as one MFMA GEMM per direction:
+def dropout_with_bits(x2, p, seed):
+    """(x2 * keep / (1 - p), keep bits [M, K / 8] uint8) in x2's dtype, the mask of
+    DropoutCast(x2, p, seed) (qlora_lora_dropout_scale_bits)."""
+    M, K = x2.shape
+    if x2.data_ptr() % 16 or x2.stride(0) % 8:
+        x2 = x2.contiguous() if x2.stride(0) % 8 else x2.clone()
+    xd = torch.empty((M, K), dtype=x2.dtype, device=x2.device)
+    bits = torch.empty((M, K // 8), dtype=torch.uint8, device=x2.device)
+    _lib.call("qlora_lora_dropout_scale_bits", x2.data_ptr(), x2.stride(0), xd.data_ptr(),
+              xd.stride(0), bits.data_ptr(), bits.stride(0), M, K, _lib.tag(x2.dtype),
+              int(seed) & 0xFFFF_FFFF_FFFF_FFFF, float(p), 1.0 / (1.0 - p), _lib.stream_of(x2))
+    return xd, bits
 
-        forward   u = x A^T                       qlora_lora_down  -> [M, 64], cols >= 16 zero
+
+class LoraNF4Linear(torch.autograd.Function):
+    """The whole 4-bit LoRA linear (rank 16) as one MFMA GEMM per direction:
+
+        forward   u = xd A^T                      qlora_lora_down  -> [M, 64], cols >= 16 zero
                   y = [x | u] [W | s B]^T + bias   qlora_gemm_nt_cat (W dequantised first)
         backward  du = s g B                      qlora_lora_down  (Y = B^T)
                   dx = [g | du] [W^T | A^T]^T      qlora_gemm_nt_cat (W^T dequantised directly)
-                  dB = s g^T u,  dA = du^T x       qlora_lora_wgrad (reductions over tokens)
+                  dB = s g^T u,  dA = du^T xd      qlora_lora_wgrad (reductions over tokens)
 
-    The same sums as base_layer(x) + ScaledAdd(B(A(x))) of solution/lora.py:157-173 with the
-    adapter term accumulated in fp32 inside the base GEMM instead of rounded to the compute
-    dtype and added in a separate pass; u, du and s*B are the compute-dtype values the
+    with xd = x when p = 0. With dropout (p > 0, the reference's training regime) xd =
+    x * keep / (1 - p) comes from qlora_lora_dropout_scale_bits (the mask of DropoutCast with
+    the same seed, kept as bits), the dX GEMM runs on the base term alone and
+    qlora_lora_up_masked_add adds keep * (du A) / (1 - p).
+
+    The same sums as base_layer(x) + ScaledAdd(B(A(dropout(x)))) of solution/lora.py:157-173
+    with the adapter term accumulated in fp32 inside the base GEMM instead of rounded to the
+    compute dtype and added in a separate pass; u, du and s*B are the compute-dtype values the
     reference's autocast GEMMs see (s = alpha / r = 2 scales B exactly)."""
 
     @staticmethod
-    def forward(ctx, x, a_weight, b_weight, packed, quant_state, bias, scaling):
+    def forward(ctx, x, a_weight, b_weight, packed, quant_state, bias, scaling, p, seed):
         from . import nf4
 
         x2 = x.reshape(-1, x.shape[-1]).contiguous()
@@ -174,9 +193,10 @@ class LoraNF4Linear(torch.autograd.Function):
         N = int(quant_state.shape[0])
         # A, A^T|0, s*B|0 and B^T in the compute dtype, one launch (kept for the backward)
         a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
+        xd, bits = dropout_with_bits(x2, p, seed) if p > 0 else (x2, None)
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
         ut = _gemm.lora_t_buffer(M, dt, x2.device)                     # u^T, for dB
-        _gemm.lora_down(x2, a16, u, out_t=ut)
+        _gemm.lora_down(xd, a16, u, out_t=ut)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
         b16 = None if bias is None else bias.to(dt)
         if nf4.use_fused_gemm(x2, quant_state, packed, a2=u):  # few rows: W dequantised in-GEMM
@@ -186,8 +206,9 @@ class LoraNF4Linear(torch.autograd.Function):
             _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=b16)
             del w
         del u
-        ctx.save_for_backward(x2, ut, at, bt)
+        ctx.save_for_backward(xd, ut, at, bt, a16 if p > 0 else None, bits)
         ctx.packed, ctx.quant_state, ctx.scaling = packed, quant_state, float(scaling)
+        ctx.p = float(p)
         ctx.shape, ctx.wdtypes = x.shape, (a_weight.dtype, b_weight.dtype)
         return y.view(*x.shape[:-1], N)
 
@@ -195,9 +216,9 @@ class LoraNF4Linear(torch.autograd.Function):
     def backward(ctx, g):
         from . import nf4
 
-        x2, ut, at, bt = ctx.saved_tensors
-        dt = x2.dtype
-        M, K = x2.shape
+        xd, ut, at, bt, a16, bits = ctx.saved_tensors
+        dt = xd.dtype
+        M, K = xd.shape
         g2 = _rows(g)
         if g2.dtype != dt:
             g2 = g2.to(dt)
@@ -210,26 +231,36 @@ class LoraNF4Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             wt = nf4.dequantize_nf4_t(ctx.packed, ctx.quant_state, dt)  # [K, N]
             dx = torch.empty((M, K), dtype=dt, device=g2.device)
-            _gemm.gemm_nt_cat(g2, wt, du, at, dx)
+            if bits is None:
+                _gemm.gemm_nt_cat(g2, wt, du, at, dx)
+            else:
+                _gemm.gemm_nt_cat(g2, wt, None, None, dx)
+                _lib.call("qlora_lora_up_masked_add", dx.data_ptr(), dx.stride(0), du.data_ptr(),
+                          du.stride(0), a16.data_ptr(), a16.stride(0), bits.data_ptr(),
+                          bits.stride(0), M, K, _lib.tag(dt), 1.0 / (1.0 - ctx.p),
+                          _lib.stream_of(dx))
             del wt
             dx = dx.view(ctx.shape)
         if ctx.needs_input_grad[1]:
-            da = _gemm.lora_wgrad(dut, x2, transposed=True)             # [16, K] = du^T x
+            da = _gemm.lora_wgrad(dut, xd, transposed=True)             # [16, K] = du^T xd
             if da.dtype != ctx.wdtypes[0]:
                 da = da.to(ctx.wdtypes[0])
         if ctx.needs_input_grad[2]:
             db = _gemm.lora_wgrad(ut, g2, alpha=s)                     # [N, 16] = s g^T u
             if db.dtype != ctx.wdtypes[1]:
                 db = db.to(ctx.wdtypes[1])
-        return dx, da, db, None, None, None, None
+        return dx, da, db, None, None, None, None, None, None
 
 
 def _fused_base(layer, adapter, x, compute_dtype, p):
-    """(packed, quant_state, bias) when the layer can run as LoraNF4Linear, else None:
-    dropout off, rank 16, a frozen NF4 base whose shapes the k-contiguous kernels take."""
+    """(packed, quant_state, bias) when the layer can run as LoraNF4Linear, else None: rank
+    16, a frozen NF4 base whose shapes the k-contiguous kernels take, dropout off or drawn
+    from this package's Philox stream (not torch's RNG, TORCH_DROPOUT_RNG)."""
     from . import nf4
 
-    if p != 0 or compute_dtype not in (torch.bfloat16, torch.float16):
+    if compute_dtype not in (torch.bfloat16, torch.float16):
+        return None
+    if p != 0 and (TORCH_DROPOUT_RNG or not 0 < p < 1):
         return None
     base = layer.base_layer
     weight = getattr(base, "weight", None)
@@ -287,7 +318,8 @@ def lora_forward(self, x, *args, **kwargs):
         xc = x if x.dtype == compute_dtype else x.to(compute_dtype)
         with torch.autocast("cuda", enabled=False):
             y = LoraNF4Linear.apply(xc, self.lora_A[adapter].weight, self.lora_B[adapter].weight,
-                                    weight, qs, bias, self.scaling[adapter])
+                                    weight, qs, bias, self.scaling[adapter], p,
+                                    _Seeds.next() if p > 0 else 0)
         out_dtype = torch.promote_types(x.dtype, compute_dtype)
         return y if y.dtype == out_dtype else y.to(out_dtype)
     result = self.base_layer(x)

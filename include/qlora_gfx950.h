@@ -201,6 +201,33 @@ int qlora_lora_scaled_add(const void* base, int base_dtype, int64_t base_row_str
                           float scaling, ql_stream_t stream);
 
 /*
+ * LoRA dropout forward that also keeps the mask: out = in * keep * scale (the bits of
+ * qlora_lora_dropout_scale with p > 0, the same Philox uniform), and bits[row][c / 8] bit
+ * c % 8 = keep(row, c). in and out share dtype QL_BF16 or QL_F16; n_cols % 8 == 0 and 16-B
+ * aligned rows (QL_ESHAPE / QL_EALIGN otherwise); 0 < p < 1 (QL_EINVAL otherwise).
+ * Replaces: solution/lora.py:29-46 + :84-89 (DropoutCast.forward) for the fused 4-bit LoRA
+ * layer, whose backward reads the bits instead of regenerating the mask (:90-93).
+ */
+int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* out,
+                                  int64_t out_row_stride, uint8_t* bits, int64_t bits_row_stride,
+                                  int64_t n_rows, int64_t n_cols, int dtype, uint64_t seed,
+                                  float p, float scale, ql_stream_t stream);
+
+/*
+ * The adapter's input gradient through the dropout, added to the base layer's:
+ *   dx[m][k] += keep(m, k) ? scale * sum_{r<16} du[m][r] * A[r][k] : 0
+ * du = s g B [M, >= 16], A [16, K] (rank 16), dx [M, K], all dtype (QL_BF16 / QL_F16); keep from
+ * qlora_lora_dropout_scale_bits' bits. fp32 sum in r order, dx rounded once. K % 8 == 0 and
+ * 16-B aligned rows (QL_ESHAPE / QL_EALIGN otherwise).
+ * Replaces: solution/lora.py:90-93 (DropoutCast.backward) applied to lora_A's input gradient
+ * (the autograd of :172), and autograd's sum with the base layer's gradient.
+ */
+int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
+                             int64_t du_row_stride, const void* A, int64_t a_row_stride,
+                             const uint8_t* bits, int64_t bits_row_stride, int64_t M, int64_t K,
+                             int dtype, float scale, ql_stream_t stream);
+
+/*
  * Per-row cross-entropy statistics over a chunk of logits, optionally overwriting the
  * logits IN PLACE with the gradient.
  * Replaces: solution/fused_ce.py:42-96 (ce_row_kernel) + :99-109 (ce_rows) and

@@ -225,3 +225,69 @@ def test_lora_layer_fp32_compute():
                       (layer.lora_B["default"].weight.grad, Bd.grad)):
         s = want.abs().max().item()
         torch.testing.assert_close(got.cpu().double(), want, rtol=1e-4, atol=1e-5 * s)
+
+
+def test_dropout_bits_match_the_reference_mask():
+    """The fused layer's dropout: xd bit-identical to the oracle's DropoutCast output for the
+    same seed and the kept bits equal to the oracle's Philox keep mask (bit j of byte c / 8 is
+    column c + j)."""
+    from oracle import philox
+
+    g = torch.Generator().manual_seed(5)
+    M, K, p, seed = 300, 1024, 0.05, 123456789
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    xd, bits = lora.dropout_with_bits(x.cuda(), p, seed)
+    want = ops.dropout_scale(x, p, seed, 1 / (1 - p), torch.bfloat16)
+    assert torch.equal(xd.cpu().view(torch.int16), want.view(torch.int16))
+    keep = philox.keep_mask(seed, M, K, p)
+    assert np.array_equal(bits.cpu().numpy(), np.packbits(keep, axis=1, bitorder="little"))
+
+
+def test_lora_layer_dropout_takes_the_fused_path_vs_fp64(monkeypatch):
+    """The reference's training regime, LoRA dropout 0.05, at 4096 x 3584 -> 512: the layer runs
+    as LoraNF4Linear (one GEMM per direction, the mask in the dropout kernel's bits) and matches
+    an fp64 reference built with the oracle's keep mask for the same seed: output and the
+    gradients to x, A and B (rtol 2e-2, atol 2e-2 * max|ref|, relative Frobenius <= 1e-2)."""
+    from oracle import philox
+
+    print("LoRA layer dropout 0.05 4096x3584->512", flush=True)
+    M, in_f, out_f, p = 4096, 3584, 512, 0.05
+    layer = _lora_layer(in_f, out_f, seed=17, dropout=p)
+    wq = _deq_ref(layer.base_layer.weight.data, layer.base_layer.weight.quant_state,
+                  torch.bfloat16).double()
+    A = layer.lora_A["default"].weight.detach().clone()
+    B = layer.lora_B["default"].weight.detach().clone()
+    layer = layer.cuda().train()
+    calls = {"n": 0}
+    fused_apply = lora.LoraNF4Linear.apply
+
+    def counted(*a):
+        calls["n"] += 1
+        return fused_apply(*a)
+
+    monkeypatch.setattr(lora.LoraNF4Linear, "apply", counted)
+    lora._Seeds.gen = torch.Generator().manual_seed(7)
+    seed = int(torch.randint(0, 2**31 - 1, (1,), generator=torch.Generator().manual_seed(7)))
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(M, in_f, generator=g).to(torch.bfloat16)
+    dy = torch.randn(M, out_f, generator=g).to(torch.bfloat16)
+    xg = x.cuda().requires_grad_()
+    y = layer(xg)
+    y.backward(dy.cuda())
+    assert calls["n"] == 1
+    keep = torch.from_numpy(philox.keep_mask(seed, M, in_f, p)).double()
+    xd = x.double().requires_grad_()
+    Ad = A.to(torch.bfloat16).double().requires_grad_()
+    Bd = B.to(torch.bfloat16).double().requires_grad_()
+    dropped = xd * keep / (1 - p)
+    y_ref = xd @ wq.t() + 2.0 * ((dropped @ Ad.t()) @ Bd.t())
+    y_ref.backward(dy.double())
+    for name, got, want in (("y", y.detach(), y_ref.detach()), ("dx", xg.grad, xd.grad),
+                            ("dA", layer.lora_A["default"].weight.grad, Ad.grad),
+                            ("dB", layer.lora_B["default"].weight.grad, Bd.grad)):
+        got = got.cpu().double()
+        s = want.abs().max().item()
+        torch.testing.assert_close(got, want, rtol=2e-2, atol=2e-2 * s, msg=name)
+        rel = ((got - want).norm() / want.norm()).item()
+        print(f"{name}: relative Frobenius error {rel:.2e}", flush=True)
+        assert rel <= 1e-2, (name, rel)
