@@ -93,7 +93,7 @@ def test_decoder_layer_qwen25_7b_shape_vs_fp64(monkeypatch):
             return _orig(*a)
 
         monkeypatch.setattr(cls, "apply", counted)
-    rot = Qwen2RotaryEmbedding(cfg, device="cuda")
+    rot = Qwen2RotaryEmbedding(cfg).to("cuda")
     x = torch.randn(B, S, cfg.hidden_size, device="cuda", generator=gen).to(torch.bfloat16)
     dy = torch.randn(B, S, cfg.hidden_size, device="cuda", generator=gen).to(torch.bfloat16)
     pos = torch.arange(S, device="cuda")[None]
