@@ -582,7 +582,38 @@ def bench_next_rows(torch, res):
     _flops("attn_bwd_2x2048x28q4kvx128",
            _event_time(lambda: attention.attn_bwd(q, k, v, o, lse, do, scale), torch), 2.5 * fl,
            res)
-    del q, k, v, do, o, lse
+    # torch's SDPA on the same inputs, called as transformers' eager path calls it (kv heads
+    # repeated, is_causal): the forward alone, and forward + backward through autograd
+    rep = HQ // HK
+    kr = k.repeat_interleave(rep, dim=1).contiguous().requires_grad_()
+    vr = v.repeat_interleave(rep, dim=1).contiguous().requires_grad_()
+    qr = q.contiguous().requires_grad_()
+    do_t = do.transpose(1, 2).contiguous()
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    # the fused backends only: the math fallback would run batched bf16 products on
+    # transposed views
+    fused_backends = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+
+    def sdpa(*a, **kw):
+        with sdpa_kernel(fused_backends):
+            return torch.nn.functional.scaled_dot_product_attention(*a, **kw)
+
+    def sdpa_fwd():
+        with torch.no_grad():
+            sdpa(qr, kr, vr, is_causal=True, scale=scale)
+
+    def sdpa_fwd_bwd():
+        out = sdpa(qr, kr, vr, is_causal=True, scale=scale)
+        torch.autograd.grad(out, (qr, kr, vr), do_t)
+
+    t_f = _event_time(sdpa_fwd, torch)
+    t_fb = _event_time(sdpa_fwd_bwd, torch)
+    res["torch_sdpa_2x2048x28q4kvx128"] = dict(
+        fwd_us=round(t_f * 1e6, 1), fwd_tflops=round(fl / t_f / 1e12, 1),
+        bwd_us=round((t_fb - t_f) * 1e6, 1), bwd_tflops=round(2.5 * fl / (t_fb - t_f) / 1e12, 1),
+        note="forward + backward minus forward; kv heads repeated as transformers does")
+    del q, k, v, do, o, lse, qr, kr, vr, do_t
 
     M, N = 4096, 3584
     w = (1 + 0.1 * torch.randn(N, device=dev, generator=g)).to(torch.bfloat16)

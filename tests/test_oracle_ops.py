@@ -241,3 +241,23 @@ def test_scaled_add_crafted_cases():
                         ([0.5], [3.0], 2.0, f32), ([1.0], [2.0 ** -8], 1 + 2.0 ** -22, bf)):
         bt, vt = torch.tensor(b, dtype=dt), torch.tensor(v, dtype=dt)
         assert torch.equal(ops.scaled_add(bt, vt, s), _exact_scaled_add(bt, vt, s, dt))
+
+
+@pytest.mark.parametrize("batch,seq,dim,theta,dtype", [(1, 2048, 128, 1e6, torch.float32),
+                                                        (2, 77, 64, 1e4, torch.bfloat16),
+                                                        (1, 512, 128, 1e6, torch.float16)])
+def test_qwen_cos_sin_is_qwen2_rotary_embedding(batch, seq, dim, theta, dtype):
+    """The oracle's rotary tables equal transformers' Qwen2RotaryEmbedding (the tables the
+    model feeds RoPE) for the same head dim, theta and positions 0 .. seq - 1, in every dtype."""
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RotaryEmbedding
+
+    cfg = Qwen2Config(hidden_size=dim * 4, num_attention_heads=4, num_key_value_heads=2,
+                      rope_theta=theta, max_position_embeddings=max(seq, 32))
+    rot = Qwen2RotaryEmbedding(cfg)
+    x = torch.zeros(batch, seq, dim, dtype=dtype)
+    pos = torch.arange(seq)[None].expand(batch, -1)
+    want_cos, want_sin = rot(x, pos)
+    cos, sin = ops.qwen_cos_sin(batch, seq, dim, theta=theta, dtype=dtype)
+    assert cos.shape == want_cos.shape and cos.dtype == want_cos.dtype
+    assert torch.equal(cos, want_cos) and torch.equal(sin, want_sin)
