@@ -909,7 +909,7 @@ def bench_step(torch, steps, warmup, eager_steps=2, layers=None, batch=2, seq=20
 def _trace_category(name):
     """Step-breakdown category of a kernel name from a rocprofv3 kernel trace."""
     table = (("attn_fwd_kernel", "attention fwd (flash)"), ("attn_bwd_dkdv", "attention dK/dV"),
-             ("attn_bwd_dq", "attention dQ"), ("attn_bwd_delta", "attention Delta"),
+             ("attn_bwd_dq", "attention dQ (with Delta)"),
              ("attn_bwd_reduce", "attention dK/dV head sum"),
              ("gemm_nt_kernel", "NT GEMM (incl. the LoRA K segment)"),
              ("splitk_reduce", "GEMM split-K reduce"), ("gemm_mfma_kernel", "GEMM (general)"),

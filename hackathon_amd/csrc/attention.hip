@@ -4,8 +4,9 @@
 // (transformers/models/qwen2/modeling_qwen2.py:220, the SDPA path of Qwen2Attention); these
 // kernels are the native replacement: O = softmax(Q K^T * scale, causal) V with grouped-query
 // heads, 16-bit in and out, fp32 accumulation and softmax, and the row log-sum-exp kept for
-// the backward. The backward follows the FlashAttention-2 split: Delta = rowsum(dO * O), then
-// dK, dV per key block and dQ per query block, each recomputing P from Q, K and the lse.
+// the backward. The backward follows the FlashAttention-2 split: dQ per query block, which also
+// forms Delta = rowsum(dO * O) for its rows, then dK, dV per key block, each recomputing P from
+// Q, K and the lse.
 //
 // Building blocks shared by every kernel:
 //  - v_mfma_f32_16x16x32 (bf16 or fp16). A pair of C tiles stacked along their rows is itself
@@ -452,29 +453,6 @@ struct BwdShape {
   float scale;
 };
 
-// Delta[bh, s] = sum_d dO[s, d] * O[s, d]: 16 lanes per row, 8 d each.
-template <int DT>
-__global__ __launch_bounds__(256) void attn_bwd_delta(const uint16_t* __restrict__ O,
-                                                       const uint16_t* __restrict__ dO,
-                                                       float* __restrict__ delta, BwdShape sh) {
-  const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (b, hq, s) row id
-  const int part = threadIdx.x & 15;
-  const int64_t total = sh.B * sh.HQ * sh.S;
-  const int64_t rc = r < total ? r : total - 1;
-  const int64_t bh = rc / sh.S, srow = rc - bh * sh.S;
-  const int64_t b = bh / sh.HQ, h = bh - b * sh.HQ;
-  const int64_t off = b * sh.os_b + h * sh.os_h + srow * sh.os_s + 8 * part;
-  float o8[8], d8[8];
-  Vec8<DT>::load(O + off, o8);
-  Vec8<DT>::load(dO + off, d8);
-  float acc = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc += o8[j] * d8[j];
-#pragma unroll
-  for (int m = 8; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
-  if (part == 0 && r < total) delta[r] = acc;
-}
-
 // ---- dK, dV: one workgroup per (b, hq, 64-key block), heaviest (first) key blocks first; wave
 // w owns keys 16 w .. +15 of the block. Per 64-row query block at or below the diagonal:
 //   S = Q K^T, dP = dO V^T      Q, dO row fragments from LDS; K, V fragments in registers
@@ -803,9 +781,10 @@ QL_DEV void dq_block(DqState<DT>& st, const char* __restrict__ kl, const char* _
 template <int DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_bwd_dq(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                 const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
-                 const float* __restrict__ lse, const float* __restrict__ delta,
-                 uint16_t* __restrict__ dQ, BwdShape sh, int n_qblocks) {
+                 const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
+                 const uint16_t* __restrict__ dO, const float* __restrict__ lse,
+                 float* __restrict__ delta, uint16_t* __restrict__ dQ, BwdShape sh,
+                 int n_qblocks) {
   __shared__ __attribute__((aligned(1024))) char smem[4 * kTileBytes];  // [stage][K, V]
   QL_DMA_BEGIN();
   const int64_t BH = sh.B * sh.HQ;
@@ -823,17 +802,40 @@ void attn_bwd_dq(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   DqState<DT> st;
   const uint16_t* qbase = Q + b * sh.qs_b + hq * sh.qs_h;
   const uint16_t* dobase = dO + b * sh.os_b + hq * sh.os_h;
+  const uint16_t* obase = O + b * sh.os_b + hq * sh.os_h;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int64_t q = q0 + 16 * qt + fr;
     const int64_t qc = q < S ? q : S - 1;
+    uint4 of[4];
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
       st.qf[qt][ds] = *reinterpret_cast<const uint4*>(qbase + qc * sh.qs_s + 32 * ds + 8 * fq);
       st.df[qt][ds] = *reinterpret_cast<const uint4*>(dobase + qc * sh.os_s + 32 * ds + 8 * fq);
+      of[ds] = *reinterpret_cast<const uint4*>(obase + qc * sh.os_s + 32 * ds + 8 * fq);
     }
     st.l2[qt] = lse[bh * S + qc] * kLog2e;
-    st.dl[qt] = delta[bh * S + qc];
+    // Delta = rowsum(dO * O) of this lane's row (the FlashAttention-2 backward's D), in a fixed
+    // order: 16 parts of 8 consecutive d (part p = 4 ds + fq holds d = 8 p .. 8 p + 7, an fma
+    // chain), combined by a butterfly over p ^ 8, p ^ 4, p ^ 2, p ^ 1; the first two flip ds
+    // (within this lane), the last two fq (lanes ^ 32 and ^ 16), so every lane of the row ends
+    // with the same value. The dQ kernel runs first and stores it for the dK/dV kernel.
+    float part[4];
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      float o8[8], d8[8];
+      Vec8<DT>::unpack(of[ds], o8);
+      Vec8<DT>::unpack(st.df[qt][ds], d8);
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(o8[j], d8[j], acc);
+      part[ds] = acc;
+    }
+    float dl = (part[0] + part[2]) + (part[1] + part[3]);
+    dl += __shfl_xor(dl, 32, 64);
+    dl += __shfl_xor(dl, 16, 64);
+    st.dl[qt] = dl;
+    if (fq == 0 && q < S) delta[bh * S + q] = dl;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) st.dq[qt][dt] = zero4();
   }
@@ -847,7 +849,7 @@ void attn_bwd_dq(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   vdma.init(sh.vs_s, wave, lane);
   kdma.issue(kbase, sh.ks_s, 0, S, smem);
   vdma.issue(vbase, sh.vs_s, 0, S, smem + kTileBytes);
-  wait_vm_visible();  // the q and dO fragments, lse and Delta
+  wait_vm_visible();  // the q and dO fragments and lse (Delta is computed above)
   for (int j = 0; j < nkv; ++j) {
     wait_all_barrier();
     char* cur = smem + (j & 1) * 2 * kTileBytes;
@@ -961,16 +963,17 @@ extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const
     pk = reinterpret_cast<float*>(ws + align256(B * HQ * S * (int64_t)sizeof(float)));
     pv = reinterpret_cast<float*>(reinterpret_cast<char*>(pk) + part_bytes);
   }
-  const int64_t rows = B * HQ * S;
   const int n_kblocks = (int)((S + kRows - 1) / kRows);
   const int n_qblocks = (int)((S + BQ - 1) / BQ);
-  if (B * HQ * n_kblocks > INT32_MAX || (rows * 16 + 255) / 256 > INT32_MAX ||
+  if (B * HQ * n_kblocks > INT32_MAX || B * HQ * n_qblocks > INT32_MAX ||
       (B * HK * S * 16 + 255) / 256 > INT32_MAX)
     return QL_EINVAL;
 #define QL_ATTN_BWD(DTC)                                                                          \
   do {                                                                                            \
-    hipLaunchKernelGGL((attn_bwd_delta<DTC>), dim3((unsigned)((rows * 16 + 255) / 256)), dim3(256), \
-                       0, s, (const uint16_t*)o, (const uint16_t*)d_o, delta, sh);                \
+    hipLaunchKernelGGL((attn_bwd_dq<DTC>), dim3((unsigned)(B * HQ * n_qblocks)), dim3(kThreads),  \
+                       0, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,          \
+                       (const uint16_t*)o, (const uint16_t*)d_o, lse, delta, (uint16_t*)dq, sh,   \
+                       n_qblocks);                                                                \
     hipLaunchKernelGGL((attn_bwd_dkdv<DTC>), dim3((unsigned)(B * HQ * n_kblocks)), dim3(kThreads), \
                        0, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,          \
                        (const uint16_t*)d_o, lse, delta, (uint16_t*)dk, (uint16_t*)dv, pk, pv,    \
@@ -978,9 +981,6 @@ extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const
     if (pk)                                                                                       \
       hipLaunchKernelGGL((attn_bwd_reduce<DTC>), dim3((unsigned)((B * HK * S * 16 + 255) / 256)), \
                          dim3(256), 0, s, pk, pv, (uint16_t*)dk, (uint16_t*)dv, sh);              \
-    hipLaunchKernelGGL((attn_bwd_dq<DTC>), dim3((unsigned)(B * HQ * n_qblocks)), dim3(kThreads),  \
-                       0, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,          \
-                       (const uint16_t*)d_o, lse, delta, (uint16_t*)dq, sh, n_qblocks);           \
   } while (0)
   if (dtype == QL_BF16) QL_ATTN_BWD(QL_BF16);
   else QL_ATTN_BWD(QL_F16);
