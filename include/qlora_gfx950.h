@@ -217,7 +217,8 @@ int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* o
  * The adapter's input gradient through the dropout, added to the base layer's:
  *   dx[m][k] += keep(m, k) ? scale * sum_{r<16} du[m][r] * A[r][k] : 0
  * du = s g B [M, >= 16], A [16, K] (rank 16), dx [M, K], all dtype (QL_BF16 / QL_F16); keep from
- * qlora_lora_dropout_scale_bits' bits. fp32 sum in r order, dx rounded once. K % 8 == 0 and
+ * qlora_lora_dropout_scale_bits' bits. The rank-16 sum is 8 two-term dot products of the 16-bit
+ * values accumulated in fp32, dx rounded once. K % 8 == 0 and
  * 16-B aligned rows (QL_ESHAPE / QL_EALIGN otherwise).
  * Replaces: solution/lora.py:90-93 (DropoutCast.backward) applied to lora_A's input gradient
  * (the autograd of :172), and autograd's sum with the base layer's gradient.

@@ -291,3 +291,33 @@ def test_lora_layer_dropout_takes_the_fused_path_vs_fp64(monkeypatch):
         rel = ((got - want).norm() / want.norm()).item()
         print(f"{name}: relative Frobenius error {rel:.2e}", flush=True)
         assert rel <= 1e-2, (name, rel)
+
+
+@pytest.mark.parametrize("M,K,dtype", [(4096, 3584, torch.bfloat16), (37, 200, torch.float16),
+                                       (1000, 2056, torch.bfloat16)])
+def test_up_masked_add_vs_fp64(M, K, dtype):
+    """qlora_lora_up_masked_add: dx + keep * scale * (du[:, :16] A) against fp64 on the same
+    16-bit values, with a random keep mask in the bit layout of the dropout kernel; within the
+    fp32-sum bound plus one rounding of dx."""
+    from hackathon_amd import _lib
+
+    print(f"up_masked_add M={M} K={K} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M + K)
+    dx = torch.randn(M, K, generator=g).to(dtype)
+    du = torch.zeros(M, 64, dtype=dtype)
+    du[:, :16] = (torch.randn(M, 16, generator=g) * 0.5).to(dtype)
+    A = (torch.randn(16, K, generator=g) * 0.25).to(dtype)
+    keep = torch.rand(M, K, generator=g) > 0.05
+    bits = torch.from_numpy(np.packbits(keep.numpy(), axis=1, bitorder="little"))
+    scale = 1 / 0.95
+    dxg, dug, Ag, bitsg = dx.cuda(), du.cuda(), A.cuda(), bits.cuda()
+    _lib.call("qlora_lora_up_masked_add", dxg.data_ptr(), dxg.stride(0), dug.data_ptr(),
+              dug.stride(0), Ag.data_ptr(), Ag.stride(0), bitsg.data_ptr(), bitsg.stride(0), M, K,
+              _lib.tag(dtype), scale, _lib.stream_of(dxg))
+    term = (du[:, :16].double() @ A.double()) * scale
+    want = dx.double() + keep.double() * term
+    mag = (du[:, :16].double().abs() @ A.double().abs()) * scale
+    eps = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    bound = 16 * 2.0**-24 * mag + eps * want.abs() + 1e-30
+    err = (dxg.cpu().double() - want).abs()
+    assert torch.all(err <= bound), float((err / bound).max())
