@@ -919,6 +919,10 @@ def _trace_category(name):
              ("rope", "RoPE"), ("ce_rows", "CE rows"), ("transpose16", "transpose"),
              ("Cijk", "hipBLASLt"), ("multi_tensor_apply", "torch AdamW (foreach)"),
              ("adamw_multi_fp32", "AdamW (fused)"),
+             ("dropout_bits_kernel", "LoRA dropout (Philox mask + bits)"),
+             ("dropout_scale_kernel", "LoRA dropout / cast"),
+             ("up_masked_add", "LoRA dropout backward (masked rank-16 add)"),
+             ("scaled_add", "LoRA scaled add"),
              ("CUDAFunctor_add", "torch add"))
     for key, cat in table:
         if key in name:
@@ -1040,6 +1044,9 @@ def main():
     ap.add_argument("--step-steps", type=int, default=5)
     ap.add_argument("--no-dropout-step", action="store_true",
                     help="skip the step with LoRA dropout 0.05")
+    ap.add_argument("--step-dropout", type=float, default=0.0,
+                    help="LoRA dropout of the main step entry (default 0; with it set, the "
+                         "separate dropout-0.05 entry is not run)")
     ap.add_argument("--step-layers", type=int, default=None)
     ap.add_argument("--eager-steps", type=int, default=2,
                     help="timed steps of the eager baseline (0: skip it and the parity check)")
@@ -1123,8 +1130,9 @@ def main():
         log(f"[bench] kernels: {json.dumps(line['kernels'])}")
     if not args.no_step:
         line["qlora_step"] = bench_step(torch, args.step_steps, 2, eager_steps=args.eager_steps,
-                                        layers=args.step_layers, parity=args.eager_steps > 0)
-        if not args.no_dropout_step:
+                                        layers=args.step_layers, parity=args.eager_steps > 0,
+                                        dropout=args.step_dropout)
+        if not args.no_dropout_step and args.step_dropout == 0:
             torch.cuda.empty_cache()
             line["qlora_step_dropout"] = bench_step(
                 torch, args.step_steps, 2, eager_steps=args.eager_steps, layers=args.step_layers,

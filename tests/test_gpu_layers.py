@@ -321,3 +321,25 @@ def test_up_masked_add_vs_fp64(M, K, dtype):
     bound = 16 * 2.0**-24 * mag + eps * want.abs() + 1e-30
     err = (dxg.cpu().double() - want).abs()
     assert torch.all(err <= bound), float((err / bound).max())
+
+
+def test_torch_dropout_rng_keeps_the_unfused_path(monkeypatch):
+    """With TORCH_DROPOUT_RNG the mask must come from torch's own dropout, so a layer with
+    dropout takes the unfused structure (torch's Dropout, then the cast and the adapter GEMMs);
+    with it off the same layer takes the fused path."""
+    layer = _lora_layer(256, 128, seed=4, dropout=0.05).cuda().train()
+    x = torch.randn(16, 256, device="cuda")
+    calls = {"n": 0}
+    fused_apply = lora.LoraNF4Linear.apply
+
+    def counted(*a):
+        calls["n"] += 1
+        return fused_apply(*a)
+
+    monkeypatch.setattr(lora.LoraNF4Linear, "apply", counted)
+    monkeypatch.setattr(lora, "TORCH_DROPOUT_RNG", True)
+    y = layer(x)
+    assert calls["n"] == 0 and torch.isfinite(y).all()
+    monkeypatch.setattr(lora, "TORCH_DROPOUT_RNG", False)
+    layer(x)
+    assert calls["n"] == 1
