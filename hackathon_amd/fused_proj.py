@@ -17,7 +17,20 @@ up. Here each group runs as one fused computation with the same sums:
             dB_g = s_g dY_g^T u_g                           qlora_lora_wgrad per projection
 
 so the gradient that autograd would otherwise assemble from one dX GEMM per projection plus the
-element-wise adds becomes one fp32 accumulation. The attention group also applies RoPE (the q
+element-wise adds becomes one fp32 accumulation.
+
+With LoRA dropout (p > 0, the same p on every projection of the group) each adapter draws its
+own mask of x from its own seed, as the layers one by one do (solution/lora.py:29-46,157-173):
+
+  forward   xd_g = x * keep_g / (1 - p)                      qlora_lora_dropout_scale_bits per
+                                                            adapter (keep_g also kept as bits)
+            u_g = xd_g A_g^T                                 qlora_lora_down per adapter
+            y = [x | u] [W_cat | sB_cat]^T + b               as above
+  backward  dx = dY_cat W_cat + sum_g keep_g (du_g A_g)/(1-p)  the GEMM on the base term, then
+                                                            qlora_lora_up_masked_add per adapter
+            dA_g = du_g^T xd_g                              qlora_lora_wgrad per adapter
+
+and du_g, dB_g as above (neither depends on the mask). The attention group also applies RoPE (the q
 and k slices of the output feed the rotation kernel directly and its backward writes the
 pre-rotation gradients straight into the slices of the gradient buffer), and the MLP group
 applies SwiGLU on the two halves of its output (row-strided kernels). Zero columns of the padded
@@ -42,16 +55,18 @@ _PAD = 64  # padded LoRA K segment: up to 4 adapters of rank 16
 
 class _Spec:
     """One projection: packed NF4 weight, quant state, frozen bias, adapter scaling."""
-    __slots__ = ("packed", "qs", "bias", "scaling", "n")
+    __slots__ = ("packed", "qs", "bias", "scaling", "n", "p")
 
-    def __init__(self, packed, qs, bias, scaling):
+    def __init__(self, packed, qs, bias, scaling, p=0.0):
         self.packed, self.qs, self.bias, self.scaling = packed, qs, bias, float(scaling)
         self.n = int(qs.shape[0])
+        self.p = float(p)  # LoRA dropout probability (0: off)
 
 
 def lora_spec(layer, x):
-    """(_Spec, A, B) of a 4-bit LoRA projection the fused kernels take for input x (dropout
-    off, rank 16, NF4 base, compute dtype = x's dtype), else None."""
+    """(_Spec, A, B) of a 4-bit LoRA projection the fused kernels take for input x (rank 16,
+    NF4 base, compute dtype = x's dtype, dropout off or drawn from this package's Philox
+    stream), else None."""
     if not hasattr(layer, "lora_A") or not hasattr(layer, "base_layer"):
         return None
     if "forward" in getattr(layer, "__dict__", {}):  # an instance-level forward (the eager path)
@@ -64,13 +79,11 @@ def lora_spec(layer, x):
         return None
     drop = layer.lora_dropout[adapter]
     p = float(drop.p) if isinstance(drop, torch.nn.Dropout) and drop.training else 0.0
-    if p != 0:  # each adapter of a group would need its own mask of the shared input
-        return None
     fused = lora._fused_base(layer, adapter, x, compute_dtype, p)
     if fused is None:
         return None
     weight, qs, bias = fused
-    return (_Spec(weight, qs, bias, layer.scaling[adapter]), layer.lora_A[adapter].weight,
+    return (_Spec(weight, qs, bias, layer.scaling[adapter], p), layer.lora_A[adapter].weight,
             layer.lora_B[adapter].weight)
 
 
@@ -124,8 +137,9 @@ def _column_blocks(specs):
     return blocks
 
 
-def group_forward(x2, specs, ab):
-    """y [M, sum n_g] = x2 W_cat^T + u sB_cat^T + bias and the state the backward needs."""
+def group_forward(x2, specs, ab, seeds=None):
+    """y [M, sum n_g] = x2 W_cat^T + u sB_cat^T + bias, the state the backward needs and, with
+    dropout (specs' p > 0, one seed per adapter), (p, a16, [xd_g], [keep bits_g]), else None."""
     dt = x2.dtype
     dev = x2.device
     M, K = x2.shape
@@ -135,7 +149,21 @@ def group_forward(x2, specs, ab):
         [(ab[2 * g], ab[2 * g + 1], specs[g].scaling) for g in range(G)], dt, _PAD)
     u = torch.empty((M, _PAD), dtype=dt, device=dev)
     ut = _t_buffer(16 * G, M, dt, dev)
-    _gemm.lora_down(x2, a16, u, out_t=ut)  # every slot in one pass over x
+    drop = None
+    p = specs[0].p
+    if p > 0:
+        # each adapter's own mask of x; slot g's lora_down writes u columns 16 g .. 16 g + 15
+        # and zeros after them, which the later slots overwrite
+        xds, bitss = [], []
+        for g in range(G):
+            xd, bits = lora.dropout_with_bits(x2, p, seeds[g])
+            _gemm.lora_down(xd, a16[16 * g:16 * g + 16], u[:, 16 * g:],
+                            out_t=ut[16 * g:16 * g + 16])
+            xds.append(xd)
+            bitss.append(bits)
+        drop = (p, a16, xds, bitss)
+    else:
+        _gemm.lora_down(x2, a16, u, out_t=ut)  # every slot in one pass over x
     y = torch.empty((M, offs[-1]), dtype=dt, device=dev)
     bias = _bias_cat(specs, dt, dev)
     if all(nf4.use_fused_gemm(x2, s.qs, s.packed, a2=u) for s in specs):
@@ -145,7 +173,7 @@ def group_forward(x2, specs, ab):
             c0, c1 = offs[g], offs[g + 1]
             nf4.gemm_nf4(x2, s.packed, s.qs, out=y[:, c0:c1], a2=u, b2=bs[c0:c1],
                          bias=None if bias is None else bias[c0:c1])
-        return y, (at, bt, ut)
+        return y, (at, bt, ut), drop
     w = torch.empty((offs[-1], K), dtype=dt, device=dev)
     nf4.dequantize_nf4_group([(s.packed, s.qs) for s in specs], dt,
                              [w[offs[g]:offs[g + 1]] for g in range(G)])
@@ -153,17 +181,20 @@ def group_forward(x2, specs, ab):
         c0, c1 = offs[p0], offs[p1]
         _gemm.gemm_nt_cat(x2, w[c0:c1], u, bs[c0:c1], y[:, c0:c1],
                           bias=None if bias is None else bias[c0:c1])
-    return y, (at, bt, ut)
+    return y, (at, bt, ut), drop
 
 
-def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_given=None):
+def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_given=None,
+                   drop=None):
     """(dx or None, [dA_0, dB_0, dA_1, ...] with None where not needed) for the output
     gradient g [M, sum n_g] (row stride a multiple of 8, unit column stride). `du_dut`, when
     given, holds the adapters' down-projections of g already (du [M, 64], du^T [16 G, M]);
-    `db_given`, the lora_B gradients [dB_0, dB_1, ..] already computed."""
-    dt = x2.dtype
-    dev = x2.device
-    M, K = x2.shape
+    `db_given`, the lora_B gradients [dB_0, dB_1, ..] already computed; `drop`, group_forward's
+    dropout state (x2 is then not needed and may be None)."""
+    dt = g.dtype
+    dev = g.device
+    M = g.shape[0]
+    K = int(specs[0].qs.shape[1])
     G = len(specs)
     offs = _offsets(specs)
     same_scaling = len({s.scaling for s in specs}) == 1
@@ -185,19 +216,30 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
         nf4.dequantize_nf4_t_group([(s.packed, s.qs) for s in specs], dt,
                                    [wt[:, offs[i]:offs[i + 1]] for i in range(G)])
         dx = torch.empty((M, K), dtype=dt, device=dev)
-        _gemm.gemm_nt_cat(g, wt, du, at, dx)
+        if drop is None:
+            _gemm.gemm_nt_cat(g, wt, du, at, dx)
+        else:
+            p, a16, _, bitss = drop
+            _gemm.gemm_nt_cat(g, wt, None, None, dx)
+            for i in range(G):
+                lora.up_masked_add(dx, du[:, 16 * i:16 * i + 16], a16[16 * i:16 * i + 16],
+                                   bitss[i], p)
         del wt
     grads = []
     da_all = None
-    if any(need_ab[0::2]):  # dA_g^T for every slot in one pass over x: [16 G, K]
+    if drop is not None:  # dA_g^T = du_g^T xd_g, each adapter on its own dropped input
+        da_all = [_gemm.lora_wgrad(dut[16 * i:16 * i + 16], drop[2][i], transposed=True)
+                  if need_ab[2 * i] else None for i in range(G)]
+    elif any(need_ab[0::2]):  # dA_g^T for every slot in one pass over x: [16 G, K]
         da_all = _gemm.lora_wgrad(dut, x2, transposed=True)
+        da_all = [da_all[16 * i:16 * i + 16] for i in range(G)]
     db_all = None
     if db_given is None and sum(need_ab[1::2]) > 1:  # every dB_g in one pass over g
         db_all = _gemm.lora_wgrad_diag(ut[:16 * G], g, offs, [s.scaling for s in specs])
     for i, s in enumerate(specs):
         da = db = None
         if need_ab[2 * i]:
-            da = da_all[16 * i:16 * i + 16]
+            da = da_all[i]
         if need_ab[2 * i + 1]:
             if db_given is not None:
                 db = db_given[i]
@@ -210,18 +252,39 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
     return dx, grads
 
 
+def _save(ctx, x2, drop, *tensors):
+    """save_for_backward of a group's state: x2 without dropout, else the dropout state (the
+    dropped inputs replace x2 for the lora_A gradients)."""
+    if drop is None:
+        ctx.save_for_backward(x2, *tensors)
+        ctx.n_drop, ctx.p = 0, 0.0
+    else:
+        p, a16, xds, bitss = drop
+        ctx.save_for_backward(a16, *xds, *bitss, *tensors)
+        ctx.n_drop, ctx.p = len(xds), p
+
+
+def _saved(ctx):
+    """(x2 or None, dropout state or None, the other saved tensors) as _save stored them."""
+    t = ctx.saved_tensors
+    G = ctx.n_drop
+    if G == 0:
+        return t[0], None, t[1:]
+    return None, (ctx.p, t[0], list(t[1:1 + G]), list(t[1 + G:1 + 2 * G])), t[1 + 2 * G:]
+
+
 class QKVRoPE(torch.autograd.Function):
     """x [B, S, K] -> (q, k, v) in the (B, H, S, D) layout of Qwen2Attention: the q/k/v LoRA
     projections as one GEMM, then RoPE on q and k (solution/rope.py:82-104 math). v is a view
-    of the projection output."""
+    of the projection output. `seeds`: one dropout seed per adapter when the specs' p > 0."""
 
     @staticmethod
-    def forward(ctx, x, cos, sin, hq, hk, specs, *ab):
+    def forward(ctx, x, cos, sin, hq, hk, specs, seeds, *ab):
         B, S, K = x.shape
         x2 = x.reshape(-1, K)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        y, (at, bt, ut) = group_forward(x2, specs, ab)
+        y, (at, bt, ut), drop = group_forward(x2, specs, ab, seeds)
         d = specs[0].n // hq
         y4 = y.view(B, S, hq + 2 * hk, d)
         q_pre = y4[:, :, :hq].transpose(1, 2)
@@ -232,17 +295,17 @@ class QKVRoPE(torch.autograd.Function):
         q = torch.empty((B, S, hq, d), dtype=x.dtype, device=x.device).transpose(1, 2)
         k = torch.empty((B, S, hk, d), dtype=x.dtype, device=x.device).transpose(1, 2)
         rope._launch(q_pre, k_pre, cos3, sin3, q, k, backward=False)
-        ctx.save_for_backward(x2, at, bt, ut, cos3, sin3)
+        _save(ctx, x2, drop, at, bt, ut, cos3, sin3)
         ctx.specs, ctx.dims = specs, (B, S, K, hq, hk, d)
         ctx.ab_dtypes = [t.dtype for t in ab]
         return q, k, v
 
     @staticmethod
     def backward(ctx, dq, dk, dv):
-        x2, at, bt, ut, cos3, sin3 = ctx.saved_tensors
+        x2, drop, (at, bt, ut, cos3, sin3) = _saved(ctx)
         B, S, K, hq, hk, d = ctx.dims
-        dt = x2.dtype
-        g = torch.empty((B * S, (hq + 2 * hk) * d), dtype=dt, device=x2.device)
+        dt, dev = at.dtype, at.device
+        g = torch.empty((B * S, (hq + 2 * hk) * d), dtype=dt, device=dev)
         g4 = g.view(B, S, hq + 2 * hk, d)
         gq = g4[:, :, :hq].transpose(1, 2)
         gk = g4[:, :, hq:hq + hk].transpose(1, 2)
@@ -250,7 +313,7 @@ class QKVRoPE(torch.autograd.Function):
 
         def unit(t, h):
             if t is None:
-                return torch.zeros((B, h, S, d), dtype=dt, device=x2.device)
+                return torch.zeros((B, h, S, d), dtype=dt, device=dev)
             t = t if t.dtype == dt else t.to(dt)
             return t if t.stride(-1) == 1 else t.contiguous()
 
@@ -259,51 +322,54 @@ class QKVRoPE(torch.autograd.Function):
             gv.zero_()
         else:
             gv.copy_(dv)
-        need_ab = ctx.needs_input_grad[6:]
+        need_ab = ctx.needs_input_grad[7:]
         dx, grads = group_backward(g, x2, at, bt, ut, ctx.specs, ctx.needs_input_grad[0],
-                                   need_ab)
+                                   need_ab, drop=drop)
         grads = [None if gr is None else gr.to(t) for gr, t in zip(grads, ctx.ab_dtypes)]
-        return (None if dx is None else dx.view(B, S, K)), None, None, None, None, None, *grads
+        return ((None if dx is None else dx.view(B, S, K)), None, None, None, None, None, None,
+                *grads)
 
 
 class GateUpSwiGLU(torch.autograd.Function):
     """x [.., K] -> silu(gate_proj(x)) * up_proj(x): the two LoRA projections as one GEMM, then
-    SwiGLU on the two halves of its output (solution/swiglu.py:15-37 math)."""
+    SwiGLU on the two halves of its output (solution/swiglu.py:15-37 math). `seeds`: one
+    dropout seed per adapter when the specs' p > 0."""
 
     @staticmethod
-    def forward(ctx, x, specs, *ab):
+    def forward(ctx, x, specs, seeds, *ab):
         K = x.shape[-1]
         x2 = x.reshape(-1, K)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        y, (at, bt, ut) = group_forward(x2, specs, ab)
+        y, (at, bt, ut), drop = group_forward(x2, specs, ab, seeds)
         n = specs[0].n
         h = torch.empty((x2.shape[0], n), dtype=x.dtype, device=x.device)
         swiglu.swiglu_rows(y[:, :n], y[:, n:], h)
-        ctx.save_for_backward(x2, y, at, bt, ut)
+        _save(ctx, x2, drop, y, at, bt, ut)
         ctx.specs, ctx.shape = specs, x.shape
         ctx.ab_dtypes = [t.dtype for t in ab]
         return h.view(*x.shape[:-1], n)
 
     @staticmethod
     def backward(ctx, dh):
-        x2, y, at, bt, ut = ctx.saved_tensors
+        x2, drop, (y, at, bt, ut) = _saved(ctx)
         n = ctx.specs[0].n
-        M = x2.shape[0]
+        M = y.shape[0]
+        dt, dev = y.dtype, y.device
         dh2 = dh.reshape(M, n)
-        if dh2.dtype != x2.dtype:
-            dh2 = dh2.to(x2.dtype)
+        if dh2.dtype != dt:
+            dh2 = dh2.to(dt)
         if dh2.stride(-1) != 1 or dh2.stride(0) % 8 or dh2.data_ptr() % 16:
             dh2 = dh2.contiguous()
-        g = torch.empty((M, 2 * n), dtype=x2.dtype, device=x2.device)
+        g = torch.empty((M, 2 * n), dtype=dt, device=dev)
         du_dut = db_given = None
-        need_ab = ctx.needs_input_grad[2:]
+        need_ab = ctx.needs_input_grad[3:]
         if n % 32 == 0:
             # the SwiGLU gradients and, in the same pass, du_gate = s dgate B_gate and
             # du_up = s dup B_up, plus (when wanted) both lora_B gradients s dgate^T u_gate and
             # s dup^T u_up: the gradients are not read back from HBM for any of them
-            du = torch.empty((M, _PAD), dtype=x2.dtype, device=x2.device)
-            dut = _t_buffer(32, M, x2.dtype, x2.device)
+            du = torch.empty((M, _PAD), dtype=dt, device=dev)
+            dut = _t_buffer(32, M, dt, dev)
             gate_s, up_s = ctx.specs
             if need_ab[1] or need_ab[3]:
                 db_given = swiglu.swiglu_bwd_lora(
@@ -318,9 +384,9 @@ class GateUpSwiGLU(torch.autograd.Function):
         else:
             swiglu.swiglu_bwd_rows(dh2, y[:, :n], y[:, n:], g[:, :n], g[:, n:])
         dx, grads = group_backward(g, x2, at, bt, ut, ctx.specs, ctx.needs_input_grad[0],
-                                   need_ab, du_dut=du_dut, db_given=db_given)
+                                   need_ab, du_dut=du_dut, db_given=db_given, drop=drop)
         grads = [None if gr is None else gr.to(t) for gr, t in zip(grads, ctx.ab_dtypes)]
-        return (None if dx is None else dx.view(ctx.shape)), None, *grads
+        return (None if dx is None else dx.view(ctx.shape)), None, None, *grads
 
 
 class LoraMLP(torch.autograd.Function):
@@ -348,7 +414,7 @@ class LoraMLP(torch.autograd.Function):
             x2 = x2.contiguous()
         dt, dev = x2.dtype, x2.device
         M = x2.shape[0]
-        y, (at, bt, ut) = group_forward(x2, specs, ab[:4])
+        y, (at, bt, ut), _ = group_forward(x2, specs, ab[:4])  # dropout off (fused_mlp)
         n, N = specs[0].n, dspec.n
         a16_d, at_d, bs_d, bt_d = _gemm.lora_pack(ab[4], ab[5], dspec.scaling, dt, _PAD)
         h = torch.empty((M, n), dtype=dt, device=dev)
@@ -420,7 +486,15 @@ def _group(layers, x):
             return None
         specs.append(spec)
         ab += [a, b]
+    if len({s.p for s in specs}) > 1:  # the group's dropout state takes one p
+        return None
     return specs, ab
+
+
+def _seeds(specs):
+    """One dropout seed per adapter, drawn in projection order from the stream the layers one
+    by one draw from, or None with dropout off."""
+    return tuple(lora._Seeds.next() for _ in specs) if specs[0].p > 0 else None
 
 
 def _rows_ok(x):
@@ -461,7 +535,7 @@ def fused_attention(module, hidden_states, position_embeddings, attention_mask,
         return None
     cos = cos if cos.stride(-1) == 1 else cos.contiguous()
     sin = sin if sin.stride(-1) == 1 else sin.contiguous()
-    q, k, v = QKVRoPE.apply(hidden_states, cos, sin, hq, hk, tuple(specs), *ab)
+    q, k, v = QKVRoPE.apply(hidden_states, cos, sin, hq, hk, tuple(specs), _seeds(specs), *ab)
     scale = getattr(module, "scaling", 1.0 / math.sqrt(d))
     attn = attention.flash_attention(q, k, v, scale)  # [B, S, HQ, D]
     return module.o_proj(attn.reshape(B, S, -1)), None
@@ -482,11 +556,12 @@ def fused_mlp(module, x):
     n = specs[0].n
     if specs[1].n != n or n % 8:
         return None
-    down = lora_spec(module.down_proj, x) if n % 32 == 0 else None
-    if down is not None and int(down[0].qs.shape[1]) == n:
+    down = lora_spec(module.down_proj, x) if n % 32 == 0 and specs[0].p == 0 else None
+    if down is not None and down[0].p == 0 and int(down[0].qs.shape[1]) == n:
         dspec, a_d, b_d = down
         return LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
-    return module.down_proj(GateUpSwiGLU.apply(x, tuple(specs), *ab))
+    # with dropout the down adapter's input is its own mask of h: down_proj runs as its layer
+    return module.down_proj(GateUpSwiGLU.apply(x, tuple(specs), _seeds(specs), *ab))
 
 
 def patch():

@@ -164,6 +164,16 @@ def dropout_with_bits(x2, p, seed):
     return xd, bits
 
 
+def up_masked_add(dx, du, a16, bits, p):
+    """dx += keep * (du a16) / (1 - p) in place: the input gradient of the adapter term of a
+    dropped input (du [M, 16] and a16 [16, K] in dx's dtype, row strides >= 16 and >= K; bits
+    from dropout_with_bits) (qlora_lora_up_masked_add)."""
+    M, K = dx.shape
+    _lib.call("qlora_lora_up_masked_add", dx.data_ptr(), dx.stride(0), du.data_ptr(),
+              du.stride(0), a16.data_ptr(), a16.stride(0), bits.data_ptr(), bits.stride(0), M, K,
+              _lib.tag(dx.dtype), 1.0 / (1.0 - p), _lib.stream_of(dx))
+
+
 class LoraNF4Linear(torch.autograd.Function):
     """The whole 4-bit LoRA linear (rank 16) as one MFMA GEMM per direction:
 
@@ -235,10 +245,7 @@ class LoraNF4Linear(torch.autograd.Function):
                 _gemm.gemm_nt_cat(g2, wt, du, at, dx)
             else:
                 _gemm.gemm_nt_cat(g2, wt, None, None, dx)
-                _lib.call("qlora_lora_up_masked_add", dx.data_ptr(), dx.stride(0), du.data_ptr(),
-                          du.stride(0), a16.data_ptr(), a16.stride(0), bits.data_ptr(),
-                          bits.stride(0), M, K, _lib.tag(dt), 1.0 / (1.0 - ctx.p),
-                          _lib.stream_of(dx))
+                up_masked_add(dx, du, a16, bits, ctx.p)
             del wt
             dx = dx.view(ctx.shape)
         if ctx.needs_input_grad[1]:

@@ -4,21 +4,28 @@ by one (each its own LoraNF4Linear, then HipRoPE / SwiGLU, gradients summed by a
 Both compute every sum in fp32 from the same bf16 operands; they differ in the order of the fp32
 accumulation (split-K of the narrow k/v outputs, one dX GEMM instead of three added in bf16),
 so outputs agree to bf16 rounding and gradients to a small relative error (tolerances below).
+With LoRA dropout both paths draw the same seeds (the seed stream restarted before each), so
+they drop the same elements and agree to the same tolerances.
 """
 
 import pytest
 import torch
 
 import hackathon_amd
-from hackathon_amd import fused_proj, qlora_step, rope, swiglu
+from hackathon_amd import fused_proj, lora, qlora_step, rope, swiglu
 
 pytestmark = pytest.mark.gpu
 
 
-def _model(seed=0):
+def _model(seed=0, dropout=0.0):
     cfg = qlora_step.qwen2_config(hidden_size=512, intermediate_size=1024, num_hidden_layers=1,
                                   num_attention_heads=4, num_key_value_heads=2, vocab_size=1000)
-    return cfg, qlora_step.build_qlora_model(cfg, "cuda", seed=seed)
+    return cfg, qlora_step.build_qlora_model(cfg, "cuda", seed=seed, dropout=dropout)
+
+
+def _reseed(seed):
+    """Restart the adapters' dropout seed stream, so two runs draw the same masks."""
+    lora._Seeds.gen = torch.Generator().manual_seed(seed)
 
 
 def _rel(a, b):
@@ -68,7 +75,7 @@ def test_qkv_rope_matches_separate_layers(seq):
     _zero(params, x)
 
     specs, ab = fused_proj._group(layers, x)
-    q2, k2, v2 = fused_proj.QKVRoPE.apply(x, cos, sin, hq, hk, tuple(specs), *ab)
+    q2, k2, v2 = fused_proj.QKVRoPE.apply(x, cos, sin, hq, hk, tuple(specs), None, *ab)
     loss_of(q2, k2, v2).backward()
     for a, b in zip((q2, k2, v2), ref):
         assert a.shape == b.shape
@@ -98,7 +105,7 @@ def test_gate_up_swiglu_matches_separate_layers(seq):
     _zero(params, x)
 
     specs, ab = fused_proj._group(layers, x)
-    h2 = fused_proj.GateUpSwiGLU.apply(x, tuple(specs), *ab)
+    h2 = fused_proj.GateUpSwiGLU.apply(x, tuple(specs), None, *ab)
     (h2.float() * w).sum().backward()
     assert h2.shape == ref.shape and _rel(h2, ref) < 4e-3
     got_g = [x.grad] + [p.grad for p in params]
@@ -170,6 +177,110 @@ def test_lora_mlp_partial_grads_and_no_grad():
     finally:
         a_d.requires_grad_(True)
         b_d.requires_grad_(True)
+
+
+@pytest.mark.parametrize("seq", [64, 37])
+def test_qkv_rope_with_dropout_matches_separate_layers(seq):
+    """LoRA dropout 0.05 on q, k and v: the group draws each adapter's own mask from the seed
+    the layer one by one would draw (the same seed stream, in projection order), so the two
+    paths drop the same elements; outputs and all gradients agree as without dropout. A run on
+    other seeds gives other outputs (the masks are applied)."""
+    print(f"fused qkv with dropout seq={seq}", flush=True)
+    cfg, model = _model(dropout=0.05)
+    attn = model.model.layers[0].self_attn
+    layers = (attn.q_proj, attn.k_proj, attn.v_proj)
+    params = _params(layers)
+    g = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    pos = torch.arange(seq, device="cuda")[None]
+    cos, sin = model.model.rotary_emb(x, pos)
+    hq, hk, d = 4, 2, 128
+    w = [torch.randn(2, h, seq, d, device="cuda", generator=g).to(torch.bfloat16)
+         for h in (hq, hk, hk)]
+
+    def loss_of(*qkv):
+        return sum((t.float() * wt).sum() for t, wt in zip(qkv, w))
+
+    _reseed(5)
+    q = attn.q_proj(x).view(2, seq, hq, d).transpose(1, 2)
+    k = attn.k_proj(x).view(2, seq, hk, d).transpose(1, 2)
+    v = attn.v_proj(x).view(2, seq, hk, d).transpose(1, 2)
+    q, k = rope.HipRoPE.apply(q, k, cos, sin)
+    loss_of(q, k, v).backward()
+    ref = [t.detach().clone() for t in (q, k, v)]
+    ref_g = [x.grad.clone()] + [p.grad.clone() for p in params]
+    _zero(params, x)
+
+    specs, ab = fused_proj._group(layers, x)
+    assert [s.p for s in specs] == [0.05] * 3
+    _reseed(5)
+    q2, k2, v2 = fused_proj.QKVRoPE.apply(x, cos, sin, hq, hk, tuple(specs),
+                                          fused_proj._seeds(specs), *ab)
+    loss_of(q2, k2, v2).backward()
+    for a, b in zip((q2, k2, v2), ref):
+        assert _rel(a, b) < 4e-3
+    got_g = [x.grad] + [p.grad for p in params]
+    for name, a, b in zip(["x", "Aq", "Bq", "Ak", "Bk", "Av", "Bv"], got_g, ref_g):
+        assert a is not None and a.dtype == b.dtype, name
+        assert _rel(a, b) < 1e-2, (name, _rel(a, b))
+    _reseed(6)
+    with torch.no_grad():
+        q3, _, _ = fused_proj.QKVRoPE.apply(x, cos, sin, hq, hk, tuple(specs),
+                                            fused_proj._seeds(specs), *ab)
+    assert _rel(q3, ref[0]) > 1e-3
+
+
+@pytest.mark.parametrize("seq", [96, 37])
+def test_gate_up_swiglu_with_dropout_matches_separate_layers(seq):
+    print(f"fused gate/up with dropout seq={seq}", flush=True)
+    cfg, model = _model(dropout=0.05)
+    mlp = model.model.layers[0].mlp
+    layers = (mlp.gate_proj, mlp.up_proj)
+    params = _params(layers)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(2, seq, 1024, device="cuda", generator=g).to(torch.bfloat16)
+
+    _reseed(3)
+    h = swiglu.swiglu(mlp.gate_proj(x), mlp.up_proj(x))
+    (h.float() * w).sum().backward()
+    ref = h.detach().clone()
+    ref_g = [x.grad.clone()] + [p.grad.clone() for p in params]
+    _zero(params, x)
+
+    specs, ab = fused_proj._group(layers, x)
+    _reseed(3)
+    h2 = fused_proj.GateUpSwiGLU.apply(x, tuple(specs), fused_proj._seeds(specs), *ab)
+    (h2.float() * w).sum().backward()
+    assert _rel(h2, ref) < 4e-3
+    got_g = [x.grad] + [p.grad for p in params]
+    for name, a, b in zip(["x", "Ag", "Bg", "Au", "Bu"], got_g, ref_g):
+        assert _rel(a, b) < 1e-2, (name, _rel(a, b))
+
+
+def test_decoder_layer_with_dropout_takes_the_groups(monkeypatch):
+    """With dropout the patched layer runs q/k/v and gate/up as groups and the down projection
+    as its own layer (its input is its own mask of h), not the fused LoRA MLP."""
+    print("fused routing with dropout", flush=True)
+    cfg, model = _model(dropout=0.05)
+    hackathon_amd.apply()
+    calls = {"qkv": 0, "gate_up": 0, "mlp": 0}
+    orig = {n: c.apply for n, c in (("qkv", fused_proj.QKVRoPE),
+                                     ("gate_up", fused_proj.GateUpSwiGLU),
+                                     ("mlp", fused_proj.LoraMLP))}
+    for name, cls in (("qkv", fused_proj.QKVRoPE), ("gate_up", fused_proj.GateUpSwiGLU),
+                      ("mlp", fused_proj.LoraMLP)):
+        def counted(*a, _name=name):
+            calls[_name] += 1
+            return orig[_name](*a)
+
+        monkeypatch.setattr(cls, "apply", counted)
+    ids = torch.randint(0, 1000, (2, 64), device="cuda")
+    out = model(input_ids=ids, labels=ids, use_cache=False)
+    out.loss.backward()
+    assert calls == {"qkv": 1, "gate_up": 1, "mlp": 0}
+    assert all(p.grad is not None and torch.isfinite(p.grad).all()
+               for p in qlora_step.lora_parameters(model))
 
 
 def test_swiglu_rows_match_the_contiguous_kernels():
