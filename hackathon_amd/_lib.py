@@ -63,6 +63,9 @@ _SIGNATURES = {
                                       _c_i64, _c_int, _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_up_masked_add": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
                                  _c_i64, _c_i64, _c_int, _c_f32, _c_ptr],
+    "qlora_lora_up_masked_add_slots": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+                                       ctypes.POINTER(ctypes.c_void_p), _c_i64, _c_int, _c_i64,
+                                       _c_i64, _c_int, _c_f32, _c_ptr],
     "qlora_gemm": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int,
                    _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32, _c_f32, _c_ptr],
     "qlora_gemm_ws": [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,

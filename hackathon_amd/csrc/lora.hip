@@ -109,14 +109,18 @@ __global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
   }
 }
 
-// The dropout backward of the adapter's input gradient, added to the base gradient:
-//   dx[m, k] += keep(m, k) ? scale * sum_{r < 16} du[m, r] * A[r, k] : 0
-// (du = s g B [M, >= 16], A [16, K] in dx's dtype; keep from the forward's bits). The rank-16
-// sum is 8 two-term dot products (v_dot2_f32_bf16 / _f16: exact 16-bit products summed in fp32)
-// over r = 0 .. 15, and dx is rounded once. Each thread owns 8 consecutive columns (A's pairs
-// (A[2i][k], A[2i + 1][k]) stay in registers) and walks `rows` rows: 4 when the columns take at
-// most 3 blocks of 2048 (the grid stays large), else 16 (fewer reloads of A's pairs). Measured
-// on MI355X: 4096 x 3584 15.6 us (16 rows: 16.6), 4096 x 18944 77.6 us (4 rows: 92.7).
+// The dropout backward of G adapters' input gradients (the adapters of a group that read the
+// same input, each with its own mask), added to the base gradient in one pass:
+//   dx[m, k] += scale * sum_{g < G, keep_g(m, k)} sum_{r < 16} du[m, 16 g + r] * A[16 g + r, k]
+// (du = s g B [M, >= 16 G], A [16 G, K] in dx's dtype; keep_g from adapter g's forward bits).
+// Each rank-16 sum is 8 two-term dot products (v_dot2_f32_bf16 / _f16: exact 16-bit products
+// summed in fp32) over r = 0 .. 15; the kept adapters' sums are added in fp32 in slot order and
+// dx is rounded once (an element no adapter keeps is left as it is). Each thread owns CW
+// consecutive columns, with A's pairs (A[16 g + 2i][k], A[16 g + 2i + 1][k]) in registers: 64
+// of them a slot at CW = 8 (G <= 2), 32 at CW = 4 (G = 3, 4); and walks `rows` rows: 4 when the
+// columns take at most 3 blocks of 256 threads (the grid stays large), else 16 (fewer reloads
+// of A's pairs). Measured on MI355X at G = 1: 4096 x 3584 15.6 us (16 rows: 16.6), 4096 x 18944
+// 77.6 us (4 rows: 92.7).
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_t;
@@ -131,44 +135,89 @@ template <> QL_DEV float dot2_acc<QL_F16>(uint32_t a, uint32_t b, float c) {
                                 false);
 }
 
-template <int DT>
+// CW consecutive 16-bit values of a row as floats (CW = 8: one 16-B access, CW = 4: 8 B).
+template <int DT, int CW> struct Cols;
+template <int DT> struct Cols<DT, 8> {
+  static QL_DEV void words(const uint16_t* p, uint32_t* w) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
+  }
+  static QL_DEV void load(const uint16_t* p, float* v) { Vec8<DT>::load(p, v); }
+  static QL_DEV void store(uint16_t* p, const float* v) { Vec8<DT>::store(p, v); }
+};
+template <int DT> struct Cols<DT, 4> {
+  static QL_DEV void words(const uint16_t* p, uint32_t* w) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    w[0] = r.x; w[1] = r.y;
+  }
+  static QL_DEV void load(const uint16_t* p, float* v) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    float t[8];
+    Vec8<DT>::unpack(make_uint4(r.x, r.y, 0u, 0u), t);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = t[j];
+  }
+  static QL_DEV void store(uint16_t* p, const float* v) {
+    const float t[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
+    const uint4 r = Vec8<DT>::pack(t);
+    *reinterpret_cast<uint2*>(p) = make_uint2(r.x, r.y);
+  }
+};
+
+struct SlotBits {
+  const uint8_t* p[4];  // adapter g's keep bits [M, >= K / 8], one row stride for all
+};
+
+template <int DT, int G, int CW>
 __global__ __launch_bounds__(kThreads) void up_masked_add_kernel(
     typename Elem<DT>::T* __restrict__ dx, int64_t dx_rs, const typename Elem<DT>::T* __restrict__ du,
-    int64_t du_rs, const typename Elem<DT>::T* __restrict__ A, int64_t a_rs,
-    const uint8_t* __restrict__ bits, int64_t bits_rs, int64_t M, int64_t K, float scale,
-    int rows) {
+    int64_t du_rs, const typename Elem<DT>::T* __restrict__ A, int64_t a_rs, SlotBits bits,
+    int64_t bits_rs, int64_t M, int64_t K, float scale, int rows) {
 #pragma clang fp contract(off)
-  const int64_t c = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 8;
+  const int64_t c = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * CW;
   if (c >= K) return;
-  uint32_t ap[8][8];  // [pair i][column j]: A[2i][c + j] in the low half, A[2i + 1][c + j] high
+  uint32_t ap[G][8][CW];  // [slot][pair i][column j]: A[16 g + 2i][c + j] low, A[.. + 1] high
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint4 lo = *reinterpret_cast<const uint4*>(A + (2 * i) * a_rs + c);
-    const uint4 hi = *reinterpret_cast<const uint4*>(A + (2 * i + 1) * a_rs + c);
-    const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w}, hw[4] = {hi.x, hi.y, hi.z, hi.w};
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      ap[i][2 * w] = __builtin_amdgcn_perm(hw[w], lw[w], 0x05040100u);
-      ap[i][2 * w + 1] = __builtin_amdgcn_perm(hw[w], lw[w], 0x07060302u);
+    for (int i = 0; i < 8; ++i) {
+      uint32_t lw[CW / 2], hw[CW / 2];
+      Cols<DT, CW>::words(A + (16 * g + 2 * i) * a_rs + c, lw);
+      Cols<DT, CW>::words(A + (16 * g + 2 * i + 1) * a_rs + c, hw);
+#pragma unroll
+      for (int w = 0; w < CW / 2; ++w) {
+        ap[g][i][2 * w] = __builtin_amdgcn_perm(hw[w], lw[w], 0x05040100u);
+        ap[g][i][2 * w + 1] = __builtin_amdgcn_perm(hw[w], lw[w], 0x07060302u);
+      }
     }
-  }
+  const int shift = (int)(c & 7);  // 0, or 4 for the second half-byte at CW = 4
   const int64_t m0 = (int64_t)blockIdx.y * rows;
   const int64_t m1 = m0 + rows < M ? m0 + rows : M;
   for (int64_t m = m0; m < m1; ++m) {
-    const uint4 d0 = *reinterpret_cast<const uint4*>(du + m * du_rs);
-    const uint4 d1 = *reinterpret_cast<const uint4*>(du + m * du_rs + 8);
-    const uint32_t dp[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};  // (du[2i], du[2i+1])
-    float v[8];
-    Vec8<DT>::load(dx + m * dx_rs + c, v);
-    const uint32_t b = bits[m * bits_rs + c / 8];
+    float v[CW], sum[CW] = {};
+    uint32_t kept = 0;
+    Cols<DT, CW>::load(dx + m * dx_rs + c, v);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float t = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      const uint4 d0 = *reinterpret_cast<const uint4*>(du + m * du_rs + 16 * g);
+      const uint4 d1 = *reinterpret_cast<const uint4*>(du + m * du_rs + 16 * g + 8);
+      const uint32_t dp[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      const uint32_t b = (uint32_t)bits.p[g][m * bits_rs + c / 8] >> shift;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) t = dot2_acc<DT>(dp[i], ap[i][j], t);
-      if ((b >> j) & 1u) v[j] = v[j] + scale * t;
+      for (int j = 0; j < CW; ++j) {
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t = dot2_acc<DT>(dp[i], ap[g][i][j], t);
+        if ((b >> j) & 1u) {
+          sum[j] = (kept >> j) & 1u ? sum[j] + t : t;
+          kept |= 1u << j;
+        }
+      }
     }
-    Vec8<DT>::store(dx + m * dx_rs + c, v);
+#pragma unroll
+    for (int j = 0; j < CW; ++j)
+      if ((kept >> j) & 1u) v[j] = v[j] + scale * sum[j];
+    Cols<DT, CW>::store(dx + m * dx_rs + c, v);
   }
 }
 
@@ -303,33 +352,70 @@ extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stri
   return ql_launch_status();
 }
 
-extern "C" int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
-                                        int64_t du_row_stride, const void* A, int64_t a_row_stride,
-                                        const uint8_t* bits, int64_t bits_row_stride, int64_t M,
-                                        int64_t K, int dtype, float scale, ql_stream_t stream) {
-  if (M < 0 || K < 0) return QL_EINVAL;
+template <int DT, int G>
+void launch_masked_add(void* dx, int64_t dx_rs, const void* du, int64_t du_rs, const void* A,
+                       int64_t a_rs, const SlotBits& bits, int64_t bits_rs, int64_t M, int64_t K,
+                       float scale, dim3 grid, int rows, hipStream_t s) {
+  constexpr int CW = G <= 2 ? 8 : 4;
+  using T = typename Elem<DT>::T;
+  hipLaunchKernelGGL((up_masked_add_kernel<DT, G, CW>), grid, dim3(kThreads), 0, s, (T*)dx, dx_rs,
+                     (const T*)du, du_rs, (const T*)A, a_rs, bits, bits_rs, M, K, scale, rows);
+}
+
+template <int DT>
+void launch_masked_add_g(int slots, void* dx, int64_t dx_rs, const void* du, int64_t du_rs,
+                         const void* A, int64_t a_rs, const SlotBits& bits, int64_t bits_rs,
+                         int64_t M, int64_t K, float scale, dim3 grid, int rows, hipStream_t s) {
+  switch (slots) {
+    case 1: launch_masked_add<DT, 1>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
+    case 2: launch_masked_add<DT, 2>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
+    case 3: launch_masked_add<DT, 3>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
+    default: launch_masked_add<DT, 4>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
+  }
+}
+
+extern "C" int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* du,
+                                              int64_t du_row_stride, const void* A,
+                                              int64_t a_row_stride, const uint8_t* const* bits,
+                                              int64_t bits_row_stride, int slots, int64_t M,
+                                              int64_t K, int dtype, float scale,
+                                              ql_stream_t stream) {
+  if (M < 0 || K < 0 || slots < 1 || slots > 4) return QL_EINVAL;
   if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
   if (M == 0 || K == 0) return QL_OK;
   if (!dx || !du || !A || !bits) return QL_EINVAL;
-  if (K % 8 || bits_row_stride < K / 8 || du_row_stride < 16 || a_row_stride < K)
+  SlotBits sb{};
+  for (int g = 0; g < slots; ++g) {
+    if (!bits[g]) return QL_EINVAL;
+    sb.p[g] = bits[g];
+  }
+  if (K % 8 || bits_row_stride < K / 8 || du_row_stride < 16 * slots || a_row_stride < K)
     return QL_ESHAPE;
   if (!rows_vec_ok(dx, dx_row_stride, dtype, K) || !rows_vec_ok(A, a_row_stride, dtype, K) ||
       !rows_vec_ok(du, du_row_stride, dtype, 16))
     return QL_EALIGN;
-  const int64_t gx = (K / 8 + kThreads - 1) / kThreads;
+  const int cw = slots <= 2 ? 8 : 4;
+  const int64_t gx = (K / cw + kThreads - 1) / kThreads;
   const int rows = gx <= 3 ? 4 : 16;
   const int64_t gy = (M + rows - 1) / rows;
   if (gx > INT32_MAX || gy > 65535) return QL_ESHAPE;
   const dim3 grid((unsigned)gx, (unsigned)gy);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  using B = typename Elem<QL_BF16>::T;
   if (dtype == QL_BF16)
-    hipLaunchKernelGGL((up_masked_add_kernel<QL_BF16>), grid, dim3(kThreads), 0, s, (B*)dx,
-                       dx_row_stride, (const B*)du, du_row_stride, (const B*)A, a_row_stride, bits,
-                       bits_row_stride, M, K, scale, rows);
+    launch_masked_add_g<QL_BF16>(slots, dx, dx_row_stride, du, du_row_stride, A, a_row_stride, sb,
+                                 bits_row_stride, M, K, scale, grid, rows, s);
   else
-    hipLaunchKernelGGL((up_masked_add_kernel<QL_F16>), grid, dim3(kThreads), 0, s, (B*)dx,
-                       dx_row_stride, (const B*)du, du_row_stride, (const B*)A, a_row_stride, bits,
-                       bits_row_stride, M, K, scale, rows);
+    launch_masked_add_g<QL_F16>(slots, dx, dx_row_stride, du, du_row_stride, A, a_row_stride, sb,
+                                bits_row_stride, M, K, scale, grid, rows, s);
   return ql_launch_status();
+}
+
+extern "C" int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
+                                        int64_t du_row_stride, const void* A, int64_t a_row_stride,
+                                        const uint8_t* bits, int64_t bits_row_stride, int64_t M,
+                                        int64_t K, int dtype, float scale, ql_stream_t stream) {
+  if (!bits && M > 0 && K > 0) return QL_EINVAL;
+  const uint8_t* one[1] = {bits};
+  return qlora_lora_up_masked_add_slots(dx, dx_row_stride, du, du_row_stride, A, a_row_stride, one,
+                                        bits_row_stride, 1, M, K, dtype, scale, stream);
 }

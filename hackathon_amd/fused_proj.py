@@ -27,7 +27,7 @@ own mask of x from its own seed, as the layers one by one do (solution/lora.py:2
             u_g = xd_g A_g^T                                 qlora_lora_down per adapter
             y = [x | u] [W_cat | sB_cat]^T + b               as above
   backward  dx = dY_cat W_cat + sum_g keep_g (du_g A_g)/(1-p)  the GEMM on the base term, then
-                                                            qlora_lora_up_masked_add per adapter
+                                                            qlora_lora_up_masked_add_slots
             dA_g = du_g^T xd_g                              qlora_lora_wgrad per adapter
 
 and du_g, dB_g as above (neither depends on the mask). The attention group also applies RoPE (the q
@@ -221,9 +221,7 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
         else:
             p, a16, _, bitss = drop
             _gemm.gemm_nt_cat(g, wt, None, None, dx)
-            for i in range(G):
-                lora.up_masked_add(dx, du[:, 16 * i:16 * i + 16], a16[16 * i:16 * i + 16],
-                                   bitss[i], p)
+            lora.up_masked_add_slots(dx, du, a16, bitss, p)  # every adapter in one pass
         del wt
     grads = []
     da_all = None

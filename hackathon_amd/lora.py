@@ -19,6 +19,7 @@ scaling, active_adapters, disable_adapters, merged) and always runs the patched 
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -171,6 +172,20 @@ def up_masked_add(dx, du, a16, bits, p):
     M, K = dx.shape
     _lib.call("qlora_lora_up_masked_add", dx.data_ptr(), dx.stride(0), du.data_ptr(),
               du.stride(0), a16.data_ptr(), a16.stride(0), bits.data_ptr(), bits.stride(0), M, K,
+              _lib.tag(dx.dtype), 1.0 / (1.0 - p), _lib.stream_of(dx))
+
+
+def up_masked_add_slots(dx, du, a16, bitss, p):
+    """up_masked_add for the G <= 4 adapters of a group in one pass over dx: adapter g's du in
+    columns 16 g .. 16 g + 15 of du, its A in rows 16 g .. of a16, its mask bitss[g] (one row
+    stride for all) (qlora_lora_up_masked_add_slots)."""
+    M, K = dx.shape
+    G = len(bitss)
+    if len({b.stride(0) for b in bitss}) != 1:
+        raise ValueError("the masks' bits must share one row stride")
+    ptrs = (ctypes.c_void_p * G)(*[b.data_ptr() for b in bitss])
+    _lib.call("qlora_lora_up_masked_add_slots", dx.data_ptr(), dx.stride(0), du.data_ptr(),
+              du.stride(0), a16.data_ptr(), a16.stride(0), ptrs, bitss[0].stride(0), G, M, K,
               _lib.tag(dx.dtype), 1.0 / (1.0 - p), _lib.stream_of(dx))
 
 

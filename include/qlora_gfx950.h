@@ -229,6 +229,25 @@ int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
                              int dtype, float scale, ql_stream_t stream);
 
 /*
+ * The same for the 1 <= slots <= 4 adapters of a group that read one input (q/k/v, gate/up),
+ * each with its own mask, in one pass over dx:
+ *   dx[m][k] += scale * sum_{g < slots, keep_g(m, k)} sum_{r<16} du[m][16 g + r] * A[16 g + r][k]
+ * du [M, >= 16 slots] (adapter g in columns 16 g ..), A [16 slots, K] (adapter g in rows 16 g ..),
+ * bits: a host array of `slots` device pointers, adapter g's bits [M, >= K / 8] at bits[g], all
+ * with bits_row_stride. The kept adapters' sums are added in fp32 in slot order and dx is
+ * rounded once (so slots = 1 is qlora_lora_up_masked_add, bit for bit). QL_EINVAL for slots
+ * outside 1 .. 4 or a null pointer; shapes and alignment as above.
+ * Replaces: solution/lora.py:90-93 (DropoutCast.backward) of each adapter of the group, applied
+ * to its lora_A input gradient (the autograd of :172), and autograd's sums of those gradients
+ * with each other and the base layers'.
+ */
+int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* du,
+                                   int64_t du_row_stride, const void* A, int64_t a_row_stride,
+                                   const uint8_t* const* bits, int64_t bits_row_stride, int slots,
+                                   int64_t M, int64_t K, int dtype, float scale,
+                                   ql_stream_t stream);
+
+/*
  * Per-row cross-entropy statistics over a chunk of logits, optionally overwriting the
  * logits IN PLACE with the gradient.
  * Replaces: solution/fused_ce.py:42-96 (ce_row_kernel) + :99-109 (ce_rows) and

@@ -323,6 +323,50 @@ def test_up_masked_add_vs_fp64(M, K, dtype):
     assert torch.all(err <= bound), float((err / bound).max())
 
 
+@pytest.mark.parametrize("M,K,slots,dtype", [
+    (4096, 3584, 3, torch.bfloat16),   # the q/k/v group's dx
+    (4096, 3584, 2, torch.bfloat16),   # gate/up
+    (300, 776, 4, torch.float16),      # ragged, four adapters, CW = 4 half-bytes
+    (37, 264, 1, torch.bfloat16),
+])
+def test_up_masked_add_slots_vs_fp64(M, K, slots, dtype):
+    """qlora_lora_up_masked_add_slots: dx + scale * sum over the adapters that keep an element
+    of du_g A_g, in one pass, against fp64 on the same 16-bit values (independent random masks
+    per adapter, including elements no adapter keeps); within the fp32-sum bound plus one
+    rounding of dx. One adapter gives qlora_lora_up_masked_add's bits exactly."""
+    from hackathon_amd import lora as lora_mod
+
+    print(f"up_masked_add_slots M={M} K={K} slots={slots} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M + K + slots)
+    dx = torch.randn(M, K, generator=g).to(dtype)
+    du = torch.zeros(M, 64, dtype=dtype)
+    du[:, :16 * slots] = (torch.randn(M, 16 * slots, generator=g) * 0.5).to(dtype)
+    A = (torch.randn(16 * slots, K, generator=g) * 0.25).to(dtype)
+    keeps = [torch.rand(M, K, generator=g) > 0.3 for _ in range(slots)]
+    bitss = [torch.from_numpy(np.packbits(k.numpy(), axis=1, bitorder="little")).cuda()
+             for k in keeps]
+    p = 0.05
+    scale = 1 / (1 - p)
+    dxg = dx.cuda()
+    lora_mod.up_masked_add_slots(dxg, du.cuda(), A.cuda(), bitss, p)
+    want = dx.double().clone()
+    mag = torch.zeros(M, K, dtype=torch.float64)
+    for i, keep in enumerate(keeps):
+        d, a = du[:, 16 * i:16 * i + 16].double(), A[16 * i:16 * i + 16].double()
+        want += keep.double() * (d @ a) * scale
+        mag += keep.double() * (d.abs() @ a.abs()) * scale
+    eps = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    bound = 16 * slots * 2.0**-24 * mag + eps * want.abs() + 1e-30
+    err = (dxg.cpu().double() - want).abs()
+    assert torch.all(err <= bound), float((err / bound).max())
+    untouched = ~torch.stack(keeps).any(0)
+    assert untouched.any() and torch.equal(dxg.cpu()[untouched], dx[untouched])
+    if slots == 1:
+        dx1 = dx.cuda()
+        lora_mod.up_masked_add(dx1, du.cuda(), A.cuda(), bitss[0], p)
+        assert torch.equal(dx1, dxg)
+
+
 def test_torch_dropout_rng_keeps_the_unfused_path(monkeypatch):
     """With TORCH_DROPOUT_RNG the mask must come from torch's own dropout, so a layer with
     dropout takes the unfused structure (torch's Dropout, then the cast and the adapter GEMMs);
