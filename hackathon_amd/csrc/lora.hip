@@ -113,112 +113,165 @@ __global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
 // same input, each with its own mask), added to the base gradient in one pass:
 //   dx[m, k] += scale * sum_{g < G, keep_g(m, k)} sum_{r < 16} du[m, 16 g + r] * A[16 g + r, k]
 // (du = s g B [M, >= 16 G], A [16 G, K] in dx's dtype; keep_g from adapter g's forward bits).
-// Each rank-16 sum is 8 two-term dot products (v_dot2_f32_bf16 / _f16: exact 16-bit products
-// summed in fp32) over r = 0 .. 15; the kept adapters' sums are added in fp32 in slot order and
-// dx is rounded once (an element no adapter keeps is left as it is). Each thread owns CW
-// consecutive columns, with A's pairs (A[16 g + 2i][k], A[16 g + 2i + 1][k]) in registers: 64
-// of them a slot at CW = 8 (G <= 2), 32 at CW = 4 (G = 3, 4); and walks `rows` rows: 4 when the
-// columns take at most 3 blocks of 256 threads (the grid stays large), else 16 (fewer reloads
-// of A's pairs). Measured on MI355X at G = 1: 4096 x 3584 15.6 us (16 rows: 16.6), 4096 x 18944
-// 77.6 us (4 rows: 92.7).
+// A wave owns 64 columns and walks `row_blocks` blocks of 16 rows:
+//  - products: each rank-16 sum is one v_mfma_f32_16x16x16 per 16 x 16 block and adapter
+//    (exact 16-bit products summed in fp32), computed transposed, (du A)^T = A^T du^T, so a
+//    lane's four results are four consecutive columns of one row; they go to the wave's LDS
+//    area as one 16-B store, one adapter at a time (A's fragments for the 64 columns stay in
+//    registers);
+//  - the add: lane l takes 8 consecutive columns of row l / 8 (and l / 8 + 8), so every dx
+//    access is 16 B and 8 lanes cover a 128-B row piece: the kept adapters' products are added
+//    in fp32 in slot order from -0.0 (the additive identity of every float: an element no
+//    adapter keeps gets dx + scale * -0.0 = dx exactly) and dx is rounded once.
+// dx and the masks of the next row block are loaded while this one is computed. Measured on
+// MI355X at 4096 x 3584: three adapters with 8 v_dot2_f32_bf16 per element and adapter took
+// 34.5 us (the dot products are the bound); products straight from the MFMA registers to dx,
+// as 8-B pieces of 16 rows per instruction, 53 us; all adapters' products in LDS at once (52 KB
+// a workgroup at G = 3) 32 us.
 
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
-typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
-template <int DT> QL_DEV float dot2_acc(uint32_t a, uint32_t b, float c);
-template <> QL_DEV float dot2_acc<QL_BF16>(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+template <int DT> QL_DEV f32x4_t mfma16(const uint2& a, const uint2& b);
+template <> QL_DEV f32x4_t mfma16<QL_BF16>(const uint2& a, const uint2& b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4i16_t, a),
+                                                  __builtin_bit_cast(v4i16_t, b),
+                                                  f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 }
-template <> QL_DEV float dot2_acc<QL_F16>(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c,
-                                false);
+template <> QL_DEV f32x4_t mfma16<QL_F16>(const uint2& a, const uint2& b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                              __builtin_bit_cast(f16x4_t, b),
+                                              f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 }
-
-// CW consecutive 16-bit values of a row as floats (CW = 8: one 16-B access, CW = 4: 8 B).
-template <int DT, int CW> struct Cols;
-template <int DT> struct Cols<DT, 8> {
-  static QL_DEV void words(const uint16_t* p, uint32_t* w) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
-    w[0] = r.x; w[1] = r.y; w[2] = r.z; w[3] = r.w;
-  }
-  static QL_DEV void load(const uint16_t* p, float* v) { Vec8<DT>::load(p, v); }
-  static QL_DEV void store(uint16_t* p, const float* v) { Vec8<DT>::store(p, v); }
-};
-template <int DT> struct Cols<DT, 4> {
-  static QL_DEV void words(const uint16_t* p, uint32_t* w) {
-    const uint2 r = *reinterpret_cast<const uint2*>(p);
-    w[0] = r.x; w[1] = r.y;
-  }
-  static QL_DEV void load(const uint16_t* p, float* v) {
-    const uint2 r = *reinterpret_cast<const uint2*>(p);
-    float t[8];
-    Vec8<DT>::unpack(make_uint4(r.x, r.y, 0u, 0u), t);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = t[j];
-  }
-  static QL_DEV void store(uint16_t* p, const float* v) {
-    const float t[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
-    const uint4 r = Vec8<DT>::pack(t);
-    *reinterpret_cast<uint2*>(p) = make_uint2(r.x, r.y);
-  }
-};
 
 struct SlotBits {
   const uint8_t* p[4];  // adapter g's keep bits [M, >= K / 8], one row stride for all
 };
 
-template <int DT, int G, int CW>
-__global__ __launch_bounds__(kThreads) void up_masked_add_kernel(
-    typename Elem<DT>::T* __restrict__ dx, int64_t dx_rs, const typename Elem<DT>::T* __restrict__ du,
-    int64_t du_rs, const typename Elem<DT>::T* __restrict__ A, int64_t a_rs, SlotBits bits,
-    int64_t bits_rs, int64_t M, int64_t K, float scale, int rows) {
+constexpr int kMaskedCols = 64;      // columns per wave (four 16-column blocks)
+constexpr int kMaskedPitch = 64 + 4;  // floats per LDS row (padding spreads the 16-B stores)
+
+template <int DT, int G>
+__device__ __forceinline__ void up_masked_add_body(
+    uint16_t* __restrict__ dx, int64_t dx_rs, const uint16_t* __restrict__ du, int64_t du_rs,
+    const uint16_t* __restrict__ A, int64_t a_rs, const SlotBits& bits, int64_t bits_rs,
+    int64_t M, int64_t K, float scale, int row_blocks,
+    float (*__restrict__ prod)[16 * kMaskedPitch]) {
 #pragma clang fp contract(off)
-  const int64_t c = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * CW;
-  if (c >= K) return;
-  uint32_t ap[G][8][CW];  // [slot][pair i][column j]: A[16 g + 2i][c + j] low, A[.. + 1] high
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int fr = lane & 15, fq = lane >> 4;
+  const int64_t k0 = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * kMaskedCols;
+  const bool wave_on = k0 < K;  // wave-uniform; every wave still meets the barriers
+  // A^T fragments of block t, adapter g: A[16 g + 4 fq + i][k0 + 16 t + fr], i = 0 .. 3 (zero
+  // past K: those products are never added)
+  uint2 af[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t lw[CW / 2], hw[CW / 2];
-      Cols<DT, CW>::words(A + (16 * g + 2 * i) * a_rs + c, lw);
-      Cols<DT, CW>::words(A + (16 * g + 2 * i + 1) * a_rs + c, hw);
+    for (int t = 0; t < 4; ++t) {
+      const int64_t k = k0 + 16 * t + fr;
+      uint16_t h[4] = {0, 0, 0, 0};
+      if (wave_on && k < K) {
 #pragma unroll
-      for (int w = 0; w < CW / 2; ++w) {
-        ap[g][i][2 * w] = __builtin_amdgcn_perm(hw[w], lw[w], 0x05040100u);
-        ap[g][i][2 * w + 1] = __builtin_amdgcn_perm(hw[w], lw[w], 0x07060302u);
+        for (int i = 0; i < 4; ++i) h[i] = A[(16 * g + 4 * fq + i) * a_rs + k];
       }
+      af[g][t] = make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
     }
-  const int shift = (int)(c & 7);  // 0, or 4 for the second half-byte at CW = 4
-  const int64_t m0 = (int64_t)blockIdx.y * rows;
-  const int64_t m1 = m0 + rows < M ? m0 + rows : M;
-  for (int64_t m = m0; m < m1; ++m) {
-    float v[CW], sum[CW] = {};
-    uint32_t kept = 0;
-    Cols<DT, CW>::load(dx + m * dx_rs + c, v);
+  const int64_t mb0 = (int64_t)blockIdx.y * row_blocks * 16;
+  int nb = row_blocks;
+  if (mb0 + 16 * (int64_t)nb > M) nb = (int)((M - mb0 + 15) / 16);
+  // the add's share of a block: rows hr and hr + 8, columns k0 + c8 .. +7
+  const int hr = lane >> 3, c8 = (lane & 7) * 8;
+  const bool col_ok = wave_on && k0 + c8 < K;  // K % 8 == 0: all 8 columns or none
+  auto load_add = [&](int64_t mb, uint4* xv, uint32_t* bv) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t m = mb + hr + 8 * h < M ? mb + hr + 8 * h : M - 1;
+      xv[h] = col_ok ? *reinterpret_cast<const uint4*>(dx + m * dx_rs + k0 + c8)
+                     : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        bv[2 * g + h] = col_ok ? bits.p[g][m * bits_rs + (k0 + c8) / 8] : 0u;
+    }
+  };
+  uint4 xv[2];
+  uint32_t bv[2 * G];
+  load_add(mb0, xv, bv);
+  for (int rb = 0; rb < nb; ++rb) {
+    const int64_t mb = mb0 + 16 * rb;
+    uint4 xn[2];
+    uint32_t bn[2 * G];
+    load_add(rb + 1 < nb ? mb + 16 : mb, xn, bn);
+    const int64_t mp = mb + fr < M ? mb + fr : M - 1;  // the products' row (clamped)
+    float sum[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum[h][j] = -0.0f;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const uint4 d0 = *reinterpret_cast<const uint4*>(du + m * du_rs + 16 * g);
-      const uint4 d1 = *reinterpret_cast<const uint4*>(du + m * du_rs + 16 * g + 8);
-      const uint32_t dp[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-      const uint32_t b = (uint32_t)bits.p[g][m * bits_rs + c / 8] >> shift;
+      // adapter g's products of this block into the wave's LDS area: row fr, columns
+      // 16 t + 4 fq .. +3
+      const uint2 dv = wave_on ? *reinterpret_cast<const uint2*>(du + mp * du_rs + 16 * g + 4 * fq)
+                               : make_uint2(0, 0);
 #pragma unroll
-      for (int j = 0; j < CW; ++j) {
-        float t = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t = dot2_acc<DT>(dp[i], ap[g][i][j], t);
-        if ((b >> j) & 1u) {
-          sum[j] = (kept >> j) & 1u ? sum[j] + t : t;
-          kept |= 1u << j;
-        }
+      for (int t = 0; t < 4; ++t) {
+        const f32x4_t p = mfma16<DT>(af[g][t], dv);
+        *reinterpret_cast<f32x4_t*>(&prod[wave][fr * kMaskedPitch + 16 * t + 4 * fq]) = p;
       }
+      __syncthreads();  // the products are in LDS
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float* pr = &prod[wave][(hr + 8 * h) * kMaskedPitch + c8];
+        const f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(pr);
+        const f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(pr + 4);
+        const float pv[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+        const uint32_t b = bv[2 * g + h];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum[h][j] = sum[h][j] + ((b >> j) & 1u ? pv[j] : -0.0f);
+      }
+      __syncthreads();  // every read of these products is done before the next writes
     }
 #pragma unroll
-    for (int j = 0; j < CW; ++j)
-      if ((kept >> j) & 1u) v[j] = v[j] + scale * sum[j];
-    Cols<DT, CW>::store(dx + m * dx_rs + c, v);
+    for (int h = 0; h < 2; ++h) {
+      float v[8];
+      Vec8<DT>::unpack(xv[h], v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = v[j] + scale * sum[h][j];
+      if (col_ok && mb + hr + 8 * h < M)
+        *reinterpret_cast<uint4*>(dx + (mb + hr + 8 * h) * dx_rs + k0 + c8) = Vec8<DT>::pack(v);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xv[h] = xn[h];
+#pragma unroll
+    for (int i = 0; i < 2 * G; ++i) bv[i] = bn[i];
   }
+}
+
+// One to three adapters (the groups of a Qwen2 layer) fit 128 registers: four waves a SIMD, so
+// the 4096 x 3584 grid runs in one round. Four adapters need more and get their own kernel.
+template <int DT, int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void up_masked_add_kernel(uint16_t* __restrict__ dx, int64_t dx_rs,
+                          const uint16_t* __restrict__ du, int64_t du_rs,
+                          const uint16_t* __restrict__ A, int64_t a_rs, SlotBits bits,
+                          int64_t bits_rs, int64_t M, int64_t K, float scale, int row_blocks) {
+  __shared__ __attribute__((aligned(16))) float prod[kThreads / 64][16 * kMaskedPitch];
+  up_masked_add_body<DT, G>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale,
+                            row_blocks, prod);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads)
+void up_masked_add4_kernel(uint16_t* __restrict__ dx, int64_t dx_rs,
+                           const uint16_t* __restrict__ du, int64_t du_rs,
+                           const uint16_t* __restrict__ A, int64_t a_rs, SlotBits bits,
+                           int64_t bits_rs, int64_t M, int64_t K, float scale, int row_blocks) {
+  __shared__ __attribute__((aligned(16))) float prod[kThreads / 64][16 * kMaskedPitch];
+  up_masked_add_body<DT, 4>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale,
+                            row_blocks, prod);
 }
 
 template <int BT, int LT, int OT, bool VEC>
@@ -355,11 +408,15 @@ extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stri
 template <int DT, int G>
 void launch_masked_add(void* dx, int64_t dx_rs, const void* du, int64_t du_rs, const void* A,
                        int64_t a_rs, const SlotBits& bits, int64_t bits_rs, int64_t M, int64_t K,
-                       float scale, dim3 grid, int rows, hipStream_t s) {
-  constexpr int CW = G <= 2 ? 8 : 4;
-  using T = typename Elem<DT>::T;
-  hipLaunchKernelGGL((up_masked_add_kernel<DT, G, CW>), grid, dim3(kThreads), 0, s, (T*)dx, dx_rs,
-                     (const T*)du, du_rs, (const T*)A, a_rs, bits, bits_rs, M, K, scale, rows);
+                       float scale, dim3 grid, int row_blocks, hipStream_t s) {
+  if constexpr (G == 4)
+    hipLaunchKernelGGL((up_masked_add4_kernel<DT>), grid, dim3(kThreads), 0, s, (uint16_t*)dx,
+                       dx_rs, (const uint16_t*)du, du_rs, (const uint16_t*)A, a_rs, bits, bits_rs,
+                       M, K, scale, row_blocks);
+  else
+    hipLaunchKernelGGL((up_masked_add_kernel<DT, G>), grid, dim3(kThreads), 0, s, (uint16_t*)dx,
+                       dx_rs, (const uint16_t*)du, du_rs, (const uint16_t*)A, a_rs, bits, bits_rs,
+                       M, K, scale, row_blocks);
 }
 
 template <int DT>
@@ -394,10 +451,10 @@ extern "C" int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, c
   if (!rows_vec_ok(dx, dx_row_stride, dtype, K) || !rows_vec_ok(A, a_row_stride, dtype, K) ||
       !rows_vec_ok(du, du_row_stride, dtype, 16))
     return QL_EALIGN;
-  const int cw = slots <= 2 ? 8 : 4;
-  const int64_t gx = (K / cw + kThreads - 1) / kThreads;
-  const int rows = gx <= 3 ? 4 : 16;
-  const int64_t gy = (M + rows - 1) / rows;
+  const int64_t cols_per_block = (int64_t)(kThreads / 64) * kMaskedCols;
+  const int64_t gx = (K + cols_per_block - 1) / cols_per_block;
+  const int rows = 4;  // row blocks of 16 per workgroup
+  const int64_t gy = (M + 16 * rows - 1) / (16 * rows);
   if (gx > INT32_MAX || gy > 65535) return QL_ESHAPE;
   const dim3 grid((unsigned)gx, (unsigned)gy);
   hipStream_t s = static_cast<hipStream_t>(stream);
