@@ -10,11 +10,13 @@ layer), the fp32 copy takes the unfused path (the dropout + cast kernel, then to
 GEMMs), so the masks are identical and the two differ by bf16 rounding alone. The eager path
 cannot be a second reference here: torch's dropout draws other masks.
 
-Bars as the dropout-free step test: loss within 1e-4 relative of fp32; every adapter gradient
-within the same fixed relative Frobenius error of fp32 (measured on MI355X: loss 4.2e-5 and
-gradients 1.0e-2 .. 2.0e-2 at the tiny shape, loss 2.9e-5 and gradients 3.3e-2 .. 7.2e-2 at the
-7B shape, as without dropout). Another seed stream must move the loss by more than the loss bar
-(it moved 1.4e-3 and 2.6e-3), so a path that ignored the masks would fail.
+Bars as the dropout-free step tests: loss within 1e-4 relative of fp32; every adapter gradient
+within the same fixed relative Frobenius error of fp32. Measured on MI355X, bf16: loss 4.2e-5
+and gradients 1.0e-2 .. 2.0e-2 at the tiny shape, loss 2.9e-5 and gradients 3.3e-2 .. 7.2e-2 at
+the 7B shape, as without dropout. fp16 with the loss scaled by 2^16 for the backward (the
+reference's regime: fp16 autocast, a GradScaler and dropout 0.05): loss 4.4e-6 / 6.0e-6,
+gradients 1.1e-3 .. 2.3e-3 / 4.1e-3 .. 9.1e-3. Another seed stream must move the loss by more
+than the loss bar (it moved 1.4e-3 .. 2.7e-3), so a path that ignored the masks would fail.
 """
 
 import copy
@@ -27,6 +29,9 @@ from hackathon_amd import lora, qlora_step, quant
 pytestmark = pytest.mark.gpu
 
 ABS_BAR = {"tiny": 2.5e-2, "qwen25_7b_2layers": 8e-2}
+# fp16 compute with the loss scaled by 2^16 for the backward (a GradScaler's start), the bars of
+# the dropout-free fp16 step test
+ABS_BAR_FP16 = {"tiny": 3e-3, "qwen25_7b_2layers": 1e-2}
 
 
 def _grads(model):
@@ -41,9 +46,27 @@ def _fp32_copy(model):
     return m32
 
 
+def _fwd_bwd(model, ids, labels, fused_head, scale):
+    """forward + backward with the loss scaled by `scale` for the backward; the unscaled loss
+    and the unscaled fp32 adapter gradients."""
+    from hackathon_amd import cross_entropy
+
+    if fused_head:
+        cross_entropy.STATE.armed = True
+    try:
+        out = model(input_ids=ids, labels=labels, use_cache=False)
+    finally:
+        cross_entropy.STATE.armed = False
+    (out.loss * scale).backward()
+    grads = [g / scale for g in _grads(model)]
+    model.zero_grad(set_to_none=True)
+    return out.loss.detach().float(), grads
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape", ["tiny", "qwen25_7b_2layers"])
-def test_dropout_step_matches_fp32_reference_with_the_same_masks(shape):
-    print(f"qlora step with dropout 0.05, {shape}", flush=True)
+def test_dropout_step_matches_fp32_reference_with_the_same_masks(shape, dtype):
+    print(f"qlora step with dropout 0.05, {shape}, {dtype}", flush=True)
     if shape == "tiny":
         cfg = qlora_step.qwen2_config(hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                                       num_attention_heads=4, num_key_value_heads=2,
@@ -52,27 +75,27 @@ def test_dropout_step_matches_fp32_reference_with_the_same_masks(shape):
     else:
         cfg = qlora_step.qwen2_config(num_hidden_layers=2)
         batch, seq = 2, 2048
-    model = qlora_step.build_qlora_model(cfg, "cuda", seed=0, dropout=0.05)
+    model = qlora_step.build_qlora_model(cfg, "cuda", seed=0, dropout=0.05, compute_dtype=dtype)
     ids, labels = qlora_step.make_batch(batch, seq, cfg.vocab_size)
     qlora_step.patched_mode()
     m32 = _fp32_copy(model)
     lora._Seeds.gen = torch.Generator().manual_seed(17)
-    loss_32 = qlora_step.QLoRAStep(m32, fused_head=False).forward_backward(ids, labels)
-    g_32 = _grads(m32)
+    loss_32, g_32 = _fwd_bwd(m32, ids, labels, False, 1.0)
     del m32
     torch.cuda.empty_cache()
+    scale = 2.0 ** 16 if dtype == torch.float16 else 1.0
     lora._Seeds.gen = torch.Generator().manual_seed(17)
-    loss_p = qlora_step.QLoRAStep(model, fused_head=True).forward_backward(ids, labels)
-    g_p = _grads(model)
+    loss_p, g_p = _fwd_bwd(model, ids, labels, True, scale)
     lora._Seeds.gen = torch.Generator().manual_seed(18)  # other masks: another loss
     with torch.no_grad():
-        loss_o = model(input_ids=ids, labels=labels, use_cache=False).loss
+        loss_o = model(input_ids=ids, labels=labels, use_cache=False).loss.float()
     errs = [((a - c).norm() / c.norm()).item() for a, c in zip(g_p, g_32)]
-    print(f"dropout {shape}: loss fp32 {loss_32.item():.7f} patched {loss_p.item():.7f} "
+    print(f"dropout {shape} {dtype}: loss fp32 {loss_32.item():.7f} patched {loss_p.item():.7f} "
           f"(other masks {loss_o.item():.7f}); adapter grad errors: "
           + " ".join(f"{e:.2e}" for e in errs), flush=True)
-    assert torch.isfinite(loss_p)
+    assert torch.isfinite(loss_p) and all(torch.isfinite(g).all() for g in g_p)
     assert abs(loss_p.item() - loss_32.item()) <= 1e-4 * abs(loss_32.item()), (loss_p, loss_32)
     assert abs(loss_o.item() - loss_32.item()) > 1e-4 * abs(loss_32.item())
+    bar = (ABS_BAR if dtype == torch.bfloat16 else ABS_BAR_FP16)[shape]
     for e in errs:
-        assert e <= ABS_BAR[shape], (e, ABS_BAR[shape])
+        assert e <= bar, (e, bar)
