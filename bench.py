@@ -768,6 +768,36 @@ def bench_gemm_data(torch, res, reps=20, sets=3):
             entry[kind] = dict(us=round(t * 1e6, 1), tflops=round(fl / t / 1e12, 1))
             del bufs, fns
         res[f"gemm_data_{Mm}x{Nn}x{Kk}"] = entry
+    # the matrix cores without global memory traffic (qlora_mfma_probe: the GEMM's 4 x 4
+    # product pattern, one wave per SIMD; mode 0 fragments in registers, mode 1 read from LDS)
+    # on the same kinds of data
+    from hackathon_amd import _lib
+
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(256 * n_cu, dtype=torch.float32, device=dev)
+    src = torch.randn(2 << 19, device=dev).to(torch.bfloat16)  # 2 MiB for mode 2's loads
+    iters = 2000
+    for mode, name in ((0, "registers"), (1, "lds_fragments"), (2, "lds_fragments_dma"),
+                       (3, "lds_fragments_vgpr_loads")):
+        probe = {}
+        for kind in ("randn", "zeros", "int"):
+            g = torch.Generator(device=dev).manual_seed(2)
+            n_el = 1024 * 8  # 1024 uint4 of 16-bit values
+            if kind == "zeros":
+                ops = torch.zeros(n_el, dtype=torch.bfloat16, device=dev)
+            elif kind == "int":
+                ops = torch.randint(-2, 3, (n_el,), device=dev, generator=g).to(torch.bfloat16)
+            else:
+                ops = torch.randn(n_el, device=dev, generator=g).to(torch.bfloat16)
+
+            def run(o=ops, m=mode):
+                _lib.call("qlora_mfma_probe", o.data_ptr(), _lib.tag(torch.bfloat16), m, iters,
+                          n_cu, out.data_ptr(), src.data_ptr(), _lib.stream_of(out))
+
+            t = _event_time(run, torch, calls=5, warm=2)
+            fl = n_cu * 4 * (iters // 2 * 2 if mode >= 2 else iters) * 32 * 32768.0
+            probe[kind] = dict(us=round(t * 1e6, 1), tflops=round(fl / t / 1e12, 1))
+        res[f"mfma_probe_32x32x16_bf16_{name}"] = probe
 
 
 WORKLOADS = {

@@ -81,6 +81,7 @@ _SIGNATURES = {
                           _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
                         _c_i64, _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
+    "qlora_mfma_probe": [_c_ptr, _c_int, _c_int, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr],
     "qlora_gemm_nf4": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_int, _c_ptr,
                        _c_ptr, _c_f32, _c_int, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr,
                        _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_f32, _c_ptr, _c_i64, _c_ptr],

@@ -1078,3 +1078,184 @@ extern "C" int qlora_gemm_nf4(int64_t M, int64_t N, int64_t K, const void* A, in
   QL_NF4_LAUNCH(QL_F16, kBNf4Plain);
 #undef QL_NF4_LAUNCH
 }
+
+// ---------------------------------------------------------------------------------------------
+// The matrix-core rate with no memory traffic: each wave of one 4-wave workgroup per CU (one
+// wave per SIMD, as the GEMM runs) issues the GEMM's inner product pattern, a 4 x 4 grid of
+// v_mfma_f32_32x32x16 into 16 accumulators, twice per round (two fragment sets), `iters`
+// rounds. Mode 0 keeps both sets of 4 A and 4 B fragments of the given data in registers; mode
+// 1 reads every set's 8 fragments from a 64 KiB LDS tile of that data (one ds_read_b128 each,
+// conflict-free, the next set's reads issued before the current set's products), the GEMM's
+// fragment traffic without its global loads; mode 2 adds the GEMM's K-loop pipeline (two 64 KiB
+// stages, one barrier and 16 direct-to-LDS loads of 1 KiB per wave per 64-k step, from a 2 MiB
+// source that stays in L2), without tile edges or output; mode 3 is mode 2 with those loads
+// staged through registers (global_load_dwordx4, then ds_write_b128 after the step's products).
+// The rate on N(0,1) against all-zero
+// operands is the power/clock ceiling of this part for that data; each mode against the one
+// before is what that layer of the GEMM's pipeline costs. Measurement only; nothing in the
+// QLoRA step calls it.
+namespace {
+
+constexpr int kProbeTile = 4096;  // uint4 in the mode-1 LDS tile (64 KiB)
+typedef int probe_v4_t __attribute__((ext_vector_type(4)));
+constexpr int64_t kProbeSrcBytes = 2 << 20;  // mode-2 source: 2 MiB, resident in each XCD's L2
+
+template <int DT, int MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void mfma_probe_kernel(const uint4* __restrict__ ops, int64_t iters, float* __restrict__ out,
+                       const char* __restrict__ src) {
+  __shared__ __attribute__((aligned(1024))) uint4 tile[MODE == 0 ? 1 : MODE == 1 ? kProbeTile
+                                                                                : 2 * kProbeTile];
+  const int lane = threadIdx.x & 63;
+  f32x16_t acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = f32x16_t{};
+  if constexpr (MODE == 0) {
+    uint4 a[2][4], b[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[s][i] = ops[(s * 8 + i) * 64 + lane];
+        b[s][i] = ops[(s * 8 + 4 + i) * 64 + lane];
+      }
+    for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[4 * i + j] = mfma<DT>(a[s][i], b[s][j], acc[4 * i + j]);
+    }
+  } else if constexpr (MODE == 2) {
+    // the GEMM's K loop without its tile edges: two 64 KiB stages; per 64-k step every wave
+    // waits for the step's loads, meets the others at one barrier, issues 16 direct-to-LDS
+    // loads of 1 KiB into the other stage (from the L2-resident source) and runs 4 sub-steps
+    // of 8 fragment reads and 16 products on this stage
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (int t = threadIdx.x; t < kProbeTile; t += 256) tile[t] = ops[t % 1024];
+    const int64_t steps = iters / 2 > 0 ? iters / 2 : 1;  // 64 products a wave per step
+    for (int64_t st = 0; st < steps; ++st) {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const uint4* cur = tile + (st & 1) * kProbeTile;
+      char* nxt = reinterpret_cast<char*>(tile + ((st + 1) & 1) * kProbeTile);
+      const int64_t soff = ((st + 1) * 65536 + wave * 16384) % kProbeSrcBytes;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        dma_hidden(src + soff + j * 1024, (uint32_t)(lane * 16), nxt + wave * 16384 + j * 1024);
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        uint4 a[4], b[4];
+        const int base = sub * 1024 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = cur[base + 64 * i];
+          b[i] = cur[base + 64 * (4 + i)];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[4 * i + j] = mfma<DT>(a[i], b[j], acc[4 * i + j]);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else if constexpr (MODE == 3) {
+    // mode 2 with the loads staged through registers: 16 global_load_dwordx4 per wave at the
+    // step's start, written to the other stage with ds_write_b128 after the step's products
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (int t = threadIdx.x; t < kProbeTile; t += 256) tile[t] = ops[t % 1024];
+    const int64_t steps = iters / 2 > 0 ? iters / 2 : 1;
+    for (int64_t st = 0; st < steps; ++st) {
+      __syncthreads();
+      const uint4* cur = tile + (st & 1) * kProbeTile;
+      uint4* nxt = tile + ((st + 1) & 1) * kProbeTile;
+      const int64_t soff = ((st + 1) * 65536 + wave * 16384) % kProbeSrcBytes;
+      const uint4* sp = reinterpret_cast<const uint4*>(src + soff);
+      // the loads go out before the products and are waited for only before their stores
+      // (as inline assembly: left to itself the compiler sinks them to the stores)
+      probe_v4_t stage[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(stage[j]) : "v"(sp + j * 64 + lane));
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        uint4 a[4], b[4];
+        const int base = sub * 1024 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = cur[base + 64 * i];
+          b[i] = cur[base + 64 * (4 + i)];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[4 * i + j] = mfma<DT>(a[i], b[j], acc[4 * i + j]);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        nxt[wave * 1024 + j * 64 + lane] = __builtin_bit_cast(uint4, stage[j]);
+    }
+  } else {
+    for (int t = threadIdx.x; t < kProbeTile; t += 256) tile[t] = ops[t % 1024];
+    __syncthreads();
+    // set n reads 8 fragments of 1 KiB (64 lanes x 16 B, contiguous) from 8 KiB slice n % 8
+    auto load_set = [&](int64_t n, uint4* a, uint4* b) {
+      const int base = (int)(n & 7) * 512 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = tile[base + 64 * i];
+        b[i] = tile[base + 64 * (4 + i)];
+      }
+    };
+    uint4 a[4], b[4], an[4], bn[4];
+    load_set(0, a, b);
+    for (int64_t n = 0; n < 2 * iters; ++n) {
+      load_set(n + 1, an, bn);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[4 * i + j] = mfma<DT>(a[i], b[j], acc[4 * i + j]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = an[i];
+        b[i] = bn[i];
+      }
+    }
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) t += acc[i][e];
+  out[(int64_t)blockIdx.x * 256 + threadIdx.x] = t;
+}
+
+}  // namespace
+
+extern "C" int qlora_mfma_probe(const void* operands, int dtype, int mode, int64_t iters,
+                                int workgroups, float* out, const void* source,
+                                ql_stream_t stream) {
+  if (!operands || !out || iters <= 0 || workgroups <= 0 || workgroups > 65535) return QL_EINVAL;
+  if (mode < 0 || mode > 3 || (mode >= 2 && (!source || !ql_aligned(source, 16))))
+    return QL_EINVAL;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  if (!ql_aligned(operands, 16)) return QL_EALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define QL_PROBE(DTC, MC)                                                                      \
+  hipLaunchKernelGGL((mfma_probe_kernel<DTC, MC>), dim3(workgroups), dim3(256), 0, s,          \
+                     (const uint4*)operands, iters, out, (const char*)source)
+  if (dtype == QL_BF16) {
+    if (mode == 0) QL_PROBE(QL_BF16, 0);
+    else if (mode == 1) QL_PROBE(QL_BF16, 1);
+    else if (mode == 2) QL_PROBE(QL_BF16, 2);
+    else QL_PROBE(QL_BF16, 3);
+  } else {
+    if (mode == 0) QL_PROBE(QL_F16, 0);
+    else if (mode == 1) QL_PROBE(QL_F16, 1);
+    else if (mode == 2) QL_PROBE(QL_F16, 2);
+    else QL_PROBE(QL_F16, 3);
+  }
+#undef QL_PROBE
+  return ql_launch_status();
+}

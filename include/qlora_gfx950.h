@@ -248,6 +248,21 @@ int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* 
                                    ql_stream_t stream);
 
 /*
+ * Measurement only (no counterpart in the reference; nothing in the step calls it): the
+ * matrix-core rate under layers of the NT GEMM's pipeline. One workgroup of 4 waves per CU (one
+ * wave per SIMD, as the GEMM runs) issues the GEMM's 4 x 4 grid of v_mfma_f32_32x32x16 on the
+ * data of `operands` (16 x 64 uint4, dtype QL_BF16 / QL_F16, 16-B aligned):
+ * workgroups * 4 * iters * 32 * 32768 FLOP. mode 0: fragments in registers; mode 1: every
+ * fragment read from LDS; mode 2: also the K loop's two 64 KiB stages with one barrier and 16
+ * direct-to-LDS loads of 1 KiB per wave per 64-k step, from `source` (2 MiB, 16-B aligned,
+ * ignored by modes 0 and 1); mode 3: mode 2 with those loads staged through registers. out (>= 256 * workgroups floats) receives a sum of each lane's
+ * accumulators. QL_EINVAL for iters <= 0, workgroups outside 1 .. 65535, another mode or a
+ * missing source.
+ */
+int qlora_mfma_probe(const void* operands, int dtype, int mode, int64_t iters, int workgroups,
+                     float* out, const void* source, ql_stream_t stream);
+
+/*
  * Per-row cross-entropy statistics over a chunk of logits, optionally overwriting the
  * logits IN PLACE with the gradient.
  * Replaces: solution/fused_ce.py:42-96 (ce_row_kernel) + :99-109 (ce_rows) and
