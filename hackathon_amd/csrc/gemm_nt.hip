@@ -1130,8 +1130,9 @@ void mfma_probe_kernel(const uint4* __restrict__ ops, int64_t iters, float* __re
   } else if constexpr (MODE == 2) {
     // the GEMM's K loop without its tile edges: two 64 KiB stages; per 64-k step every wave
     // waits for the step's loads, meets the others at one barrier, issues 16 direct-to-LDS
-    // loads of 1 KiB into the other stage (from the L2-resident source) and runs 4 sub-steps
-    // of 8 fragment reads and 16 products on this stage
+    // loads of 1 KiB into the other stage (from the L2-resident source; workgroups start at
+    // different 64 KiB windows of it, as the GEMM's tiles read different rows) and runs 4
+    // sub-steps of 8 fragment reads and 16 products on this stage
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int t = threadIdx.x; t < kProbeTile; t += 256) tile[t] = ops[t % 1024];
     const int64_t steps = iters / 2 > 0 ? iters / 2 : 1;  // 64 products a wave per step
@@ -1139,7 +1140,7 @@ void mfma_probe_kernel(const uint4* __restrict__ ops, int64_t iters, float* __re
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       const uint4* cur = tile + (st & 1) * kProbeTile;
       char* nxt = reinterpret_cast<char*>(tile + ((st + 1) & 1) * kProbeTile);
-      const int64_t soff = ((st + 1) * 65536 + wave * 16384) % kProbeSrcBytes;
+      const int64_t soff = ((st + 1 + blockIdx.x) * 65536 + wave * 16384) % kProbeSrcBytes;
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         dma_hidden(src + soff + j * 1024, (uint32_t)(lane * 16), nxt + wave * 16384 + j * 1024);
@@ -1169,7 +1170,7 @@ void mfma_probe_kernel(const uint4* __restrict__ ops, int64_t iters, float* __re
       __syncthreads();
       const uint4* cur = tile + (st & 1) * kProbeTile;
       uint4* nxt = tile + ((st + 1) & 1) * kProbeTile;
-      const int64_t soff = ((st + 1) * 65536 + wave * 16384) % kProbeSrcBytes;
+      const int64_t soff = ((st + 1 + blockIdx.x) * 65536 + wave * 16384) % kProbeSrcBytes;
       const uint4* sp = reinterpret_cast<const uint4*>(src + soff);
       // the loads go out before the products and are waited for only before their stores
       // (as inline assembly: left to itself the compiler sinks them to the stores)
