@@ -166,6 +166,8 @@ def load():
             fn.restype = ctypes.c_int64
         lib.qlora_abi_version.argtypes = []
         lib.qlora_abi_version.restype = ctypes.c_int
+        lib.qlora_dropout_keep_threshold.argtypes = [ctypes.c_float]
+        lib.qlora_dropout_keep_threshold.restype = ctypes.c_uint32
         version = lib.qlora_abi_version()
         if version != ABI_VERSION:
             raise KernelLibraryMissing(
@@ -177,8 +179,8 @@ def load():
 
 def exported_symbols():
     """Names the binding expects the library to export (used by the ABI tests)."""
-    return sorted(list(_SIGNATURES) + list(_SIZE_QUERIES) + ["qlora_strerror",
-                                                             "qlora_abi_version"])
+    return sorted(list(_SIGNATURES) + list(_SIZE_QUERIES) + [
+        "qlora_strerror", "qlora_abi_version", "qlora_dropout_keep_threshold"])
 
 
 def check(status: int, what: str) -> None:

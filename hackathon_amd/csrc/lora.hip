@@ -6,49 +6,25 @@
 //   solution/lora.py:49-60  OUT = BASE + LO * scaling in fp32.
 //
 // The dropout mask is regenerated (never stored): keep = U(seed, row*N + col) > p, with U the
-// uniform of Philox4x32-10 (Salmon et al., "Parallel Random Numbers: As Easy as 1, 2, 3",
-// SC'11) on counter {flat index, 0, 0, 0} and key {seed_lo, seed_hi}; word 0 is folded to a
-// non-negative int32 (x < 0 -> -x-1) and scaled by 4.6566127342e-10f. That is the uniform
-// Triton's tl.rand(seed, int32 offset) draws, so a seed gives the reference's mask.
+// Philox4x32-10 uniform Triton's tl.rand(seed, int32 offset) draws (ql_philox.h), so a seed
+// gives the reference's mask. The kernels test the equivalent integer condition on the folded
+// Philox word against a threshold the host derives from p.
 //
 // HBM-bound. One workgroup per row; each thread moves 8 consecutive elements per step.
+#include "ql_philox.h"
 #include "ql_vec.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 
-// Each round's two 32 x 32 -> 64-bit products are written as 64-bit multiplies, so that each
-// becomes one v_mad_u64_u32 instead of a v_mul_hi_u32 and a v_mul_lo_u32 (the 32-bit integer
-// multiplies are the kernel's bound): 15% faster at 4096 x 3584, the same bits.
-QL_DEV uint32_t philox_word0(uint32_t ctr, uint64_t seed) {
-  uint32_t c0 = ctr, c1 = 0u, c2 = 0u, c3 = 0u;
-  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
-    const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
-    const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
-    c0 = hi1 ^ c1 ^ k0;
-    c1 = lo1;
-    c2 = hi0 ^ c3 ^ k1;
-    c3 = lo0;
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-  return c0;
-}
-
-QL_DEV float uniform_from_word(uint32_t w) {
-  int32_t x = (int32_t)w;
-  x = x < 0 ? ~x : x;  // -x - 1 in two's complement, also for INT32_MIN
-  return (float)x * 4.6566127342e-10f;
-}
+using ql_philox::keep_word;
+using ql_philox::philox_word0;
 
 template <int IT, int OT, bool DROPOUT, bool VEC>
 __global__ __launch_bounds__(kThreads) void dropout_scale_kernel(
     const typename Elem<IT>::T* __restrict__ in, int64_t in_rs, typename Elem<OT>::T* __restrict__ out,
-    int64_t out_rs, int64_t n_cols, uint64_t seed, float p, float scale) {
+    int64_t out_rs, int64_t n_cols, uint64_t seed, uint32_t thr, float scale) {
   const int64_t row = blockIdx.x;
   const auto* src = in + row * in_rs;
   auto* dst = out + row * out_rs;
@@ -60,7 +36,7 @@ __global__ __launch_bounds__(kThreads) void dropout_scale_kernel(
       for (int j = 0; j < 8; ++j) {
         if constexpr (DROPOUT) {
           const uint32_t flat = (uint32_t)(row * n_cols + c + j);
-          const bool keep = uniform_from_word(philox_word0(flat, seed)) > p;
+          const bool keep = keep_word(philox_word0(flat, seed), thr);
           v[j] = keep ? v[j] * scale : 0.0f;
         } else {
           v[j] = v[j] * scale;
@@ -73,7 +49,7 @@ __global__ __launch_bounds__(kThreads) void dropout_scale_kernel(
       float v = Elem<IT>::to_f32(src[c]);
       if constexpr (DROPOUT) {
         const uint32_t flat = (uint32_t)(row * n_cols + c);
-        v = uniform_from_word(philox_word0(flat, seed)) > p ? v * scale : 0.0f;
+        v = keep_word(philox_word0(flat, seed), thr) ? v * scale : 0.0f;
       } else {
         v = v * scale;
       }
@@ -89,7 +65,7 @@ template <int IT, int OT>
 __global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
     const typename Elem<IT>::T* __restrict__ in, int64_t in_rs, typename Elem<OT>::T* __restrict__ out,
     int64_t out_rs, uint8_t* __restrict__ bits, int64_t bits_rs, int64_t n_cols, uint64_t seed,
-    float p, float scale) {
+    uint32_t thr, float scale) {
   const int64_t row = blockIdx.x;
   const auto* src = in + row * in_rs;
   auto* dst = out + row * out_rs;
@@ -100,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t flat = (uint32_t)(row * n_cols + c + j);
-      const bool keep = uniform_from_word(philox_word0(flat, seed)) > p;
+      const bool keep = keep_word(philox_word0(flat, seed), thr);
       v[j] = keep ? v[j] * scale : 0.0f;
       b |= (uint32_t)keep << j;
     }
@@ -310,7 +286,8 @@ int launch_dropout(const void* in, int64_t in_rs, void* out, int64_t out_rs, int
   const bool drop = p > 0.0f;
 #define QL_DROP(D, V)                                                                        \
   hipLaunchKernelGGL((dropout_scale_kernel<IT, OT, D, V>), grid, dim3(kThreads), 0, s,       \
-                     (const I*)in, in_rs, (O*)out, out_rs, n_cols, seed, p, scale)
+                     (const I*)in, in_rs, (O*)out, out_rs, n_cols, seed, thr, scale)
+  const uint32_t thr = drop ? ql_philox::keep_threshold(p) : 0u;
   if (drop) {
     if (vec) QL_DROP(true, true); else QL_DROP(true, false);
   } else {
@@ -378,6 +355,10 @@ extern "C" int qlora_lora_scaled_add(const void* base, int base_dtype, int64_t b
   return QL_EDTYPE;
 }
 
+extern "C" uint32_t qlora_dropout_keep_threshold(float p) {
+  return ql_philox::keep_threshold(p);
+}
+
 extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* out,
                                              int64_t out_row_stride, uint8_t* bits,
                                              int64_t bits_row_stride, int64_t n_rows,
@@ -393,15 +374,16 @@ extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stri
     return QL_EALIGN;
   const dim3 grid((unsigned)n_rows);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t thr = ql_philox::keep_threshold(p);
   using B = typename Elem<QL_BF16>::T;
   if (dtype == QL_BF16)
     hipLaunchKernelGGL((dropout_bits_kernel<QL_BF16, QL_BF16>), grid, dim3(kThreads), 0, s,
                        (const B*)in, in_row_stride, (B*)out, out_row_stride, bits,
-                       bits_row_stride, n_cols, seed, p, scale);
+                       bits_row_stride, n_cols, seed, thr, scale);
   else
     hipLaunchKernelGGL((dropout_bits_kernel<QL_F16, QL_F16>), grid, dim3(kThreads), 0, s,
                        (const B*)in, in_row_stride, (B*)out, out_row_stride, bits,
-                       bits_row_stride, n_cols, seed, p, scale);
+                       bits_row_stride, n_cols, seed, thr, scale);
   return ql_launch_status();
 }
 

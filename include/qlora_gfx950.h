@@ -214,12 +214,22 @@ int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* o
                                   float p, float scale, ql_stream_t stream);
 
 /*
+ * The integer form of the dropout test, host only (no GPU call): with x the Philox word folded
+ * to [0, 2^31) (x < 0 -> -x-1), the uniform (float)x * 4.6566127342e-10f is > p exactly when
+ * x >= qlora_dropout_keep_threshold(p) (2^31: nothing is kept; NaN p keeps nothing). The
+ * dropout kernels compare against this value instead of forming the uniform.
+ * No counterpart in the reference (solution/lora.py:41-44 forms the float uniform); exported so
+ * that the equivalence can be checked without a GPU.
+ */
+uint32_t qlora_dropout_keep_threshold(float p);
+
+/*
  * The adapter's input gradient through the dropout, added to the base layer's:
  *   dx[m][k] += keep(m, k) ? scale * sum_{r<16} du[m][r] * A[r][k] : 0
  * du = s g B [M, >= 16], A [16, K] (rank 16), dx [M, K], all dtype (QL_BF16 / QL_F16); keep from
- * qlora_lora_dropout_scale_bits' bits. The rank-16 sum is 8 two-term dot products of the 16-bit
- * values accumulated in fp32, dx rounded once. K % 8 == 0 and
- * 16-B aligned rows (QL_ESHAPE / QL_EALIGN otherwise).
+ * qlora_lora_dropout_scale_bits' bits. The rank-16 products run on the matrix cores (16-bit
+ * operands, fp32 sums), dx is rounded once. K % 8 == 0 and 16-B aligned rows (QL_ESHAPE /
+ * QL_EALIGN otherwise).
  * Replaces: solution/lora.py:90-93 (DropoutCast.backward) applied to lora_A's input gradient
  * (the autograd of :172), and autograd's sum with the base layer's gradient.
  */

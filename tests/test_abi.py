@@ -247,3 +247,31 @@ def test_noalloc_wgrad_rejects_scratch_beyond_its_array(lib):
                                         1.0, None) == -1  # null operand
     assert lib.qlora_lora_wgrad_noalloc(fake, 4096, fake, 512, -1, 512, 1, 2, fake, 0,
                                         1.0, None) == -1  # negative size
+
+
+def test_dropout_keep_threshold_is_the_float_test(lib):
+    """The kernels keep an element when its folded Philox word x is >= the threshold; the
+    reference keeps it when (float)x * 4.6566127342e-10f > p. The two agree on every word: the
+    float test is monotone in x, so checking the words around the threshold, the ends of the
+    range and a spread of others pins it (numpy's int32 -> float32 conversion and float32
+    product round as the reference's do)."""
+    import numpy as np
+
+    from oracle import philox
+
+    rng = np.random.default_rng(7)
+    spread = np.concatenate([rng.integers(0, 1 << 31, 200_000, dtype=np.int64),
+                             np.arange(0, 1 << 31, (1 << 31) // 4096, dtype=np.int64),
+                             np.array([0, 1, (1 << 31) - 1], dtype=np.int64)])
+    ps = [0.05, 0.1, 0.2, 0.5, 0.75, 0.9, 1e-9, 0.0, 0.99999994, 1.0, 1.5, -0.25, float("nan"),
+          float(np.nextafter(np.float32(0.05), np.float32(1)))]
+    for p in ps:
+        t = int(lib.qlora_dropout_keep_threshold(ctypes.c_float(p)))
+        assert 0 <= t <= 1 << 31
+        x = np.concatenate([spread, np.arange(t - 3, t + 4, dtype=np.int64)])
+        x = x[(x >= 0) & (x < 1 << 31)]
+        u = x.astype(np.int32).astype(np.float32) * philox.SCALE
+        want = u > np.float32(p)
+        assert np.array_equal(x >= t, want), p
+    # the mask's own rate: at p = 0.05 the threshold sits at 5% of the range
+    assert abs(int(lib.qlora_dropout_keep_threshold(0.05)) / 2**31 - 0.05) < 1e-6
