@@ -952,6 +952,7 @@ def _trace_category(name):
              ("rope", "RoPE"), ("ce_rows", "CE rows"), ("transpose16", "transpose"),
              ("Cijk", "hipBLASLt"), ("multi_tensor_apply", "torch AdamW (foreach)"),
              ("adamw_multi_fp32", "AdamW (fused)"),
+             ("dropout_down_kernel", "LoRA dropout + down-projection (mask, bits, u)"),
              ("dropout_bits_kernel", "LoRA dropout (Philox mask + bits)"),
              ("dropout_scale_kernel", "LoRA dropout / cast"),
              ("up_masked_add", "LoRA dropout backward (masked rank-16 add)"),

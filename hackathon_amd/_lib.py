@@ -59,6 +59,11 @@ _SIGNATURES = {
                                  _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_scaled_add": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,
                               _c_i64, _c_i64, _c_i64, _c_f32, _c_ptr],
+    "qlora_lora_dropout_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                ctypes.POINTER(ctypes.c_uint64), _c_f32, _c_f32,
+                                ctypes.POINTER(ctypes.c_void_p), _c_i64,
+                                ctypes.POINTER(ctypes.c_void_p), _c_i64, _c_ptr, _c_i64, _c_int,
+                                _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_dropout_scale_bits": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64,
                                       _c_i64, _c_int, _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_up_masked_add": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
@@ -120,6 +125,7 @@ _SIZE_QUERIES = {
     "qlora_gemm_nt_cat_workspace_size": [_c_i64, _c_i64, _c_i64],
     "qlora_gemm_nf4_workspace_size": [_c_i64, _c_i64, _c_i64],
     "qlora_lora_down_workspace_size": [_c_i64, _c_i64, _c_int],
+    "qlora_lora_dropout_down_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_lora_wgrad_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_lora_wgrad_diag_workspace_size": [_c_i64, _c_i64, _c_int],
     "qlora_swiglu_bwd_lora_down_workspace_size": [_c_i64, _c_i64],

@@ -42,6 +42,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "ql_philox.h"
 #include "ql_swiglu.h"
 #include "ql_vec.h"
 #include "lora_mfma.h"
@@ -1256,6 +1257,174 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// LoRA dropout fused with the adapters' down-projections (the forward with p > 0) for the
+// G <= 4 adapters of a group that read one input, each with its own mask and seed:
+//   xd_g = x * keep_g * scale (rounded to the input type)   stored: lora_A's gradient reads it
+//   bits_g[m, k / 8] bit k % 8 = keep_g(m, k)                stored: the dx pass reads it
+//   u[m, 16 g + c] = sum_k xd_g[m, k] A[16 g + c, k]
+// in one pass over x. keep_g is the Philox test of ql_philox.h at flat index m * K + k with
+// seed_g, computed as the dropout kernels compute it, so xd_g and bits_g equal theirs bit for
+// bit. A workgroup of 8 waves takes 16 rows and a range of 64-k chunks (blockIdx.y: the K
+// split); wave w walks chunks w, w + 8, ... of the range. Lane l
+// holds row l % 16 and k = 64 j + 32 h + 8 (l / 16) .. +7 (h = 0, 1), the v_mfma_f32_16x16x32
+// operand layout, so the dropped values reach the matrix cores from the registers that formed
+// them; each adapter's A fragment for the same k comes from L2. The waves' sums are added
+// through LDS in wave order, the splits' by lora_down_reduce in split order (deterministic).
+// Like the dropout kernels, the kernel is bound by the Philox rounds' integer multiplies; the
+// products and the stores ride along. The K split is there for occupancy: the rounds of one
+// element are a dependent chain, and a workgroup per 16 rows alone leaves two waves a SIMD.
+constexpr int kDdWaves = 8;
+
+// 16 B of lane src_byte / 4's fragment h0 or h1 (hi), moved with one ds_bpermute per dword
+// and fragment.
+QL_DEV uint4 from_fragments(const uint4& h0, const uint4& h1, int src_byte, bool hi) {
+  const uint4 a = to_mfma_layout(h0, src_byte);
+  const uint4 b = to_mfma_layout(h1, src_byte);
+  return hi ? b : a;
+}
+
+struct DropDownSlots {
+  uint64_t seed[kMaxSlots];
+  uint16_t* xd[kMaxSlots];  // [M, >= K] with one row stride for all slots
+  uint8_t* bits[kMaxSlots]; // [M, >= K / 8] with one row stride for all slots
+};
+
+template <int DT, int G, bool PARTIAL>
+__global__ __launch_bounds__(64 * kDdWaves) void dropout_down_kernel(
+    const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ A, int64_t lda,
+    int64_t M, int64_t K, int64_t chunks_per_split, DropDownSlots sl, int64_t xd_rs,
+    int64_t bits_rs, uint32_t thr, float scale, float* __restrict__ ws,
+    uint16_t* __restrict__ out, int64_t ldo, int out_cols, uint16_t* __restrict__ out_t,
+    int64_t ldt) {
+  __shared__ f32x4_t red[G * kDdWaves * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t row = (int64_t)blockIdx.x * 16 + r;
+  const bool live = row < M;
+  // Lanes of rows past M redo row M - 1 (its x, its counters, its stores of the same values),
+  // so the loop's stores need no branch: a branch around them makes the wait-count pass assume
+  // the path without stores and wait for every store before the next chunk's loads.
+  const int64_t srow = live ? row : M - 1;
+  const uint16_t* xr = X + srow * ldx + 8 * q;
+  const uint16_t* ar = A + (int64_t)r * lda + 8 * q;
+  // store layout (see the stores below): lane l writes row 8 t + l / 8 of the block, taken from
+  // the fragment lane of that row and k group (l % 8) & 3, fragment h = (l % 8) / 4
+  int perm_src[2];
+  int64_t srow_t[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    perm_src[t] = 4 * (8 * t + (lane >> 3) + 16 * (lane & 3));  // ds_bpermute byte address
+    const int64_t tr = (int64_t)blockIdx.x * 16 + 8 * t + (lane >> 3);
+    srow_t[t] = tr < M ? tr : M - 1;  // the source lane redid row M - 1 for rows past M
+  }
+  const bool perm_hi = (lane >> 2) & 1;
+  // the reference's offsets are int32 (row * K + k): the counter is their low 32 bits
+  const uint32_t flat_row = (uint32_t)((uint64_t)srow * (uint64_t)K) + 8u * (uint32_t)q;
+  f32x4_t acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int64_t jb = (int64_t)blockIdx.y * chunks_per_split;
+  const int64_t je = jb + chunks_per_split < K / 64 ? jb + chunks_per_split : K / 64;
+  // One chunk of loads in flight ahead of the arithmetic: the next chunk's x and A fragments
+  // are issued before this chunk's stores, so waiting for them never waits for the stores
+  // (vmcnt counts loads and stores in issue order). The last chunk reloads itself.
+  uint4 xv[2], av[G][2];
+  auto load_chunk = [&](int64_t j, uint4 (&xo)[2], uint4 (&ao)[G][2]) {
+    const int64_t c0 = 64 * j;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      xo[h] = *reinterpret_cast<const uint4*>(xr + c0 + 32 * h);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        ao[g][h] = *reinterpret_cast<const uint4*>(ar + (int64_t)16 * g * lda + c0 + 32 * h);
+    }
+  };
+  const int64_t j0 = jb + wave;
+  if (j0 < je) load_chunk(j0, xv, av);
+  for (int64_t j = j0; j < je; j += kDdWaves) {
+    uint4 xn[2], an[G][2];
+    load_chunk(j + kDdWaves < je ? j + kDdWaves : j, xn, an);
+    // keep the next chunk's loads ahead of this chunk's stores (the scheduler would sink them
+    // past the arithmetic, after the stores, and the next wait would then cover the stores)
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t c0 = 64 * j;
+    float xf[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) Vec8<DT>::unpack(xv[h], xf[h]);
+    const int64_t c = c0 + 8 * (lane & 7);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {  // one adapter at a time: its mask, product and stores
+      uint4 dv[2];
+      uint32_t bw[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t base = flat_row + (uint32_t)(c0 + 32 * h);
+        float v[8];
+        uint32_t b = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool keep = ql_philox::keep_word(ql_philox::philox_word0(base + e, sl.seed[g]), thr);
+          v[e] = keep ? xf[h][e] * scale : 0.0f;
+          b |= (uint32_t)keep << e;
+        }
+        dv[h] = Vec8<DT>::pack(v);
+        bw[h] = b;
+      }
+      acc[g] = mfma<DT>(av[g][0], dv[0], acc[g]);
+      acc[g] = mfma<DT>(av[g][1], dv[1], acc[g]);
+      // Stores: lane permutes turn the two fragments (16 rows x 32 k each) into two
+      // row-major 8 x 64 tiles, lane l holding row 8 t + l / 8, k = c0 + 8 (l % 8) .. +7, so
+      // each store instruction writes 8 whole 128-B row pieces instead of 16 half lines.
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 o = from_fragments(dv[0], dv[1], perm_src[t], perm_hi);
+        const uint32_t b0 = (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src[t], (int)bw[0]);
+        const uint32_t b1 = (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src[t], (int)bw[1]);
+        *reinterpret_cast<uint4*>(sl.xd[g] + srow_t[t] * xd_rs + c) = o;
+        sl.bits[g][srow_t[t] * bits_rs + c / 8] = (uint8_t)(perm_hi ? b1 : b0);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      xv[h] = xn[h];
+#pragma unroll
+      for (int g = 0; g < G; ++g) av[g][h] = an[g][h];
+    }
+  }
+  // acc[g]: lane l holds u[row m0 + l % 16][16 g + 4 (l / 16) .. +3] of this wave's chunks
+#pragma unroll
+  for (int g = 0; g < G; ++g) red[(g * kDdWaves + wave) * 64 + lane] = acc[g];
+  __syncthreads();
+  if (!live) return;
+  const int c = 4 * q;
+  using T = typename Elem<DT>::T;
+  if (wave < G) {  // wave g finishes slot g
+    const int g = wave;
+    f32x4_t s = red[g * kDdWaves * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < kDdWaves; ++w) s += red[(g * kDdWaves + w) * 64 + lane];
+    const int col = kRank * g + c;
+    if constexpr (PARTIAL) {  // this split's sums, added in split order by lora_down_reduce
+      *reinterpret_cast<float4*>(ws + ((int64_t)blockIdx.y * M + row) * (kRank * G) + col) =
+          make_float4(s[0], s[1], s[2], s[3]);
+      return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[row * ldo + col + e] = Elem<DT>::from_f32(s[e]);
+    if (out_t) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out_t[(int64_t)(col + e) * ldt + row] = Elem<DT>::from_f32(s[e]);
+    }
+  } else if (!PARTIAL && wave == kDdWaves - 1) {  // the zero columns 16 G .. out_cols - 1
+    for (int zc = kRank * G + c; zc < out_cols; zc += 16)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (zc + e < out_cols) out[row * ldo + zc + e] = (T)0;
+  }
+}
+
 unsigned grid1d(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 4096) g = 4096;
@@ -1755,6 +1924,104 @@ extern "C" int qlora_lora_down(const void* X, int64_t ldx, const void* Y, int64_
                       alpha, out_t, ldt, static_cast<float*>(workspace),
                       workspace_bytes / (int64_t)sizeof(float),
                       static_cast<hipStream_t>(stream));
+}
+
+// K split of the fused dropout + down-projection: up to 1024 workgroups of 8 waves, keeping at
+// least four chunks per wave in every split. Measured at 4096 rows (bf16, one adapter): K =
+// 18944 126-128 us split 4 against 135-136 us unsplit; at K = 3584 the split (then 4 x 14
+// chunks) cost 4-24 us more than it saved (the partials and their reduce), so it stays unsplit.
+static int ql_dropout_down_splits(int64_t M, int64_t K) {
+  const int64_t blocks = (M + 15) / 16, nch = K / 64;
+  int s = 1;
+  while (blocks * s < 1024 && nch / (2 * s) >= 4 * kDdWaves && s < 64) s *= 2;
+  return s;
+}
+
+static int64_t ql_dropout_down_workspace_bytes(int64_t M, int64_t K, int slots) {
+  const int s = ql_dropout_down_splits(M, K);
+  return s > 1 ? (int64_t)s * M * kRank * slots * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int64_t qlora_lora_dropout_down_workspace_size(int64_t M, int64_t K, int slots) {
+  if (M <= 0 || K <= 0 || K % 64 || slots < 1 || slots > kMaxSlots) return 0;
+  return ql_dropout_down_workspace_bytes(M, K, slots);
+}
+
+extern "C" int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, const void* A,
+                                       int64_t a_row_stride, int64_t M, int64_t K, int slots,
+                                       int dtype, const uint64_t* seeds, float p, float scale,
+                                       void* const* xd, int64_t xd_row_stride,
+                                       uint8_t* const* bits, int64_t bits_row_stride, void* u,
+                                       int64_t u_row_stride, int u_cols, void* u_t,
+                                       int64_t u_t_row_stride, void* workspace,
+                                       int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || K < 0 || slots < 1 || slots > kMaxSlots || !(p > 0.0f) || !(p < 1.0f) ||
+      workspace_bytes < 0)
+    return QL_EINVAL;
+  if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
+  if (M == 0 || K == 0) return QL_OK;
+  if (!x || !A || !seeds || !xd || !bits || !u) return QL_EINVAL;
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  DropDownSlots sl{};
+  for (int g = 0; g < slots; ++g) {
+    if (!xd[g] || !bits[g]) return QL_EINVAL;
+    if (!ql_aligned(xd[g], 16)) return QL_EALIGN;
+    sl.seed[g] = seeds[g];
+    sl.xd[g] = static_cast<uint16_t*>(xd[g]);
+    sl.bits[g] = bits[g];
+  }
+  const int nc = kRank * slots;
+  if (K % 64 || x_row_stride < K || a_row_stride < K || xd_row_stride < K ||
+      bits_row_stride < K / 8 || u_cols < nc || u_row_stride < u_cols ||
+      (u_t && u_t_row_stride < M))
+    return QL_ESHAPE;
+  if (x_row_stride % 8 || a_row_stride % 8 || xd_row_stride % 8 || !ql_aligned(x, 16) ||
+      !ql_aligned(A, 16) || !ql_aligned(u, 2) || (u_t && !ql_aligned(u_t, 2)))
+    return QL_EALIGN;
+  const int64_t gx = (M + 15) / 16;
+  if (gx > INT32_MAX) return QL_ESHAPE;
+  int splits = ql_dropout_down_splits(M, K);
+  if (workspace_bytes < ql_dropout_down_workspace_bytes(M, K, slots) || !workspace) splits = 1;
+  const int64_t nch = K / 64;
+  const int64_t cps = (nch + splits - 1) / splits;
+  splits = (int)((nch + cps - 1) / cps);
+  const uint32_t thr = ql_philox::keep_threshold(p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* ws = static_cast<float*>(workspace);
+  const dim3 grid((unsigned)gx, (unsigned)splits);
+#define QL_DD(DT, G)                                                                          \
+  do {                                                                                        \
+    if (splits == 1) {                                                                        \
+      hipLaunchKernelGGL((dropout_down_kernel<DT, G, false>), grid, dim3(64 * kDdWaves), 0, s, \
+                         (const uint16_t*)x, x_row_stride, (const uint16_t*)A, a_row_stride,  \
+                         M, K, cps, sl, xd_row_stride, bits_row_stride, thr, scale,           \
+                         (float*)nullptr, (uint16_t*)u, u_row_stride, u_cols,                 \
+                         (uint16_t*)u_t, u_t_row_stride);                                     \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((dropout_down_kernel<DT, G, true>), grid, dim3(64 * kDdWaves), 0, s,  \
+                         (const uint16_t*)x, x_row_stride, (const uint16_t*)A, a_row_stride,  \
+                         M, K, cps, sl, xd_row_stride, bits_row_stride, thr, scale, ws,       \
+                         (uint16_t*)u, u_row_stride, u_cols, (uint16_t*)u_t, u_t_row_stride); \
+      hipLaunchKernelGGL((lora_down_reduce<DT, DT>), dim3(grid1d(M * u_cols)), dim3(256), 0,   \
+                         s, ws, splits, M, nc, (typename Elem<DT>::T*)u, u_row_stride, u_cols, \
+                         1.0f, 1.0f, (uint16_t*)u_t, u_t_row_stride);                         \
+    }                                                                                         \
+  } while (0)
+#define QL_DD_G(DT)                \
+  switch (slots) {                 \
+    case 1: QL_DD(DT, 1); break;   \
+    case 2: QL_DD(DT, 2); break;   \
+    case 3: QL_DD(DT, 3); break;   \
+    default: QL_DD(DT, 4); break;  \
+  }
+  if (dtype == QL_BF16) {
+    QL_DD_G(QL_BF16)
+  } else {
+    QL_DD_G(QL_F16)
+  }
+#undef QL_DD_G
+#undef QL_DD
+  return ql_launch_status();
 }
 
 extern "C" int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N, int slots) {

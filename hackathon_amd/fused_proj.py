@@ -151,9 +151,13 @@ def group_forward(x2, specs, ab, seeds=None):
     ut = _t_buffer(16 * G, M, dt, dev)
     drop = None
     p = specs[0].p
-    if p > 0:
-        # each adapter's own mask of x; slot g's lora_down writes u columns 16 g .. 16 g + 15
-        # and zeros after them, which the later slots overwrite
+    if p > 0 and K % 64 == 0:
+        # each adapter's own mask of x and its u, all adapters in one pass over x
+        xds, bitss = lora.dropout_down(x2, a16, p, seeds, u, ut)
+        drop = (p, a16, xds, bitss)
+    elif p > 0:
+        # one adapter at a time: slot g's lora_down writes u columns 16 g .. 16 g + 15 and
+        # zeros after them, which the later slots overwrite
         xds, bitss = [], []
         for g in range(G):
             xd, bits = lora.dropout_with_bits(x2, p, seeds[g])

@@ -165,6 +165,31 @@ def dropout_with_bits(x2, p, seed):
     return xd, bits
 
 
+def dropout_down(x2, a16, p, seeds, u, ut=None):
+    """Each adapter's dropped input and its down-projection in one pass over x2, for the G <= 4
+    adapters of a group (adapter g: rows 16 g .. 16 g + 15 of a16 [16 G, K], seed seeds[g]):
+    returns ([xd_g], [keep bits_g]) as dropout_with_bits(x2, p, seeds[g]) returns them, and
+    writes u[:, 16 g:16 g + 16] = xd_g a16_g^T (zeros in u's columns 16 G ..) and, when given,
+    ut [16 G, M] = its transpose (qlora_lora_dropout_down). K must be a multiple of 64."""
+    M, K = x2.shape
+    G = len(seeds)
+    if x2.data_ptr() % 16 or x2.stride(0) % 8:
+        x2 = x2.contiguous() if x2.stride(0) % 8 else x2.clone()
+    xds = [torch.empty((M, K), dtype=x2.dtype, device=x2.device) for _ in range(G)]
+    bitss = [torch.empty((M, K // 8), dtype=torch.uint8, device=x2.device) for _ in range(G)]
+    seed_arr = (ctypes.c_uint64 * G)(*[int(s) & 0xFFFF_FFFF_FFFF_FFFF for s in seeds])
+    xd_ptrs = (ctypes.c_void_p * G)(*[t.data_ptr() for t in xds])
+    bit_ptrs = (ctypes.c_void_p * G)(*[t.data_ptr() for t in bitss])
+    ws, ws_bytes = _lib.workspace("qlora_lora_dropout_down_workspace_size", M, K, G,
+                                  device=x2.device)
+    _lib.call("qlora_lora_dropout_down", x2.data_ptr(), x2.stride(0), a16.data_ptr(),
+              a16.stride(0), M, K, G, _lib.tag(x2.dtype), seed_arr, float(p), 1.0 / (1.0 - p),
+              xd_ptrs, K, bit_ptrs, K // 8, u.data_ptr(), u.stride(0), u.shape[1],
+              None if ut is None else ut.data_ptr(), 0 if ut is None else ut.stride(0),
+              _lib.ptr(ws), ws_bytes, _lib.stream_of(x2))
+    return xds, bitss
+
+
 def up_masked_add(dx, du, a16, bits, p):
     """dx += keep * (du a16) / (1 - p) in place: the input gradient of the adapter term of a
     dropped input (du [M, 16] and a16 [16, K] in dx's dtype, row strides >= 16 and >= K; bits
@@ -199,8 +224,8 @@ class LoraNF4Linear(torch.autograd.Function):
                   dB = s g^T u,  dA = du^T xd      qlora_lora_wgrad (reductions over tokens)
 
     with xd = x when p = 0. With dropout (p > 0, the reference's training regime) xd =
-    x * keep / (1 - p) comes from qlora_lora_dropout_scale_bits (the mask of DropoutCast with
-    the same seed, kept as bits), the dX GEMM runs on the base term alone and
+    x * keep / (1 - p) and u come from one pass of qlora_lora_dropout_down (the mask of
+    DropoutCast with the same seed, kept as bits), the dX GEMM runs on the base term alone and
     qlora_lora_up_masked_add adds keep * (du A) / (1 - p).
 
     The same sums as base_layer(x) + ScaledAdd(B(A(dropout(x)))) of solution/lora.py:157-173
@@ -218,10 +243,13 @@ class LoraNF4Linear(torch.autograd.Function):
         N = int(quant_state.shape[0])
         # A, A^T|0, s*B|0 and B^T in the compute dtype, one launch (kept for the backward)
         a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
-        xd, bits = dropout_with_bits(x2, p, seed) if p > 0 else (x2, None)
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
         ut = _gemm.lora_t_buffer(M, dt, x2.device)                     # u^T, for dB
-        _gemm.lora_down(xd, a16, u, out_t=ut)
+        if p > 0 and K % 64 == 0:  # the dropped input, its bits and u in one pass over x
+            (xd,), (bits,) = dropout_down(x2, a16, p, (seed,), u, ut)
+        else:
+            xd, bits = dropout_with_bits(x2, p, seed) if p > 0 else (x2, None)
+            _gemm.lora_down(xd, a16, u, out_t=ut)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
         b16 = None if bias is None else bias.to(dt)
         if nf4.use_fused_gemm(x2, quant_state, packed, a2=u):  # few rows: W dequantised in-GEMM

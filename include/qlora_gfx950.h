@@ -258,6 +258,31 @@ int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* 
                                    ql_stream_t stream);
 
 /*
+ * LoRA dropout fused with the adapters' down-projections, for 1 <= slots <= 4 adapters that
+ * read one input x [M, K] (K % 64 == 0), each with its own seed (host array seeds[slots]):
+ *   xd[g]   = x * keep_g * scale      in dtype, as qlora_lora_dropout_scale_bits(seeds[g]) writes it
+ *   bits[g] = keep_g                  bit layout of qlora_lora_dropout_scale_bits
+ *   u[m][16 g + c] = sum_k xd[g][m][k] * A[16 g + c][k]   fp32 sums, rounded once to dtype
+ * with u's columns 16 slots .. u_cols-1 set to zero and, when u_t is not null, u_t [16 slots,
+ * >= M] = its transpose. xd and bits are host arrays of `slots` device pointers sharing
+ * xd_row_stride / bits_row_stride. dtype QL_BF16 / QL_F16 for x, A, xd, u; 16-B aligned x, A
+ * and xd rows (QL_EALIGN); 0 < p < 1 and a null pointer QL_EINVAL; shapes QL_ESHAPE. A
+ * workspace of qlora_lora_dropout_down_workspace_size bytes (16-B aligned) lets the K range
+ * split over workgroups (fp32 partials summed in split order); without it the call runs
+ * unsplit, with the same xd and bits and u summed in another order.
+ * Replaces: solution/lora.py:29-46 + :84-89 (DropoutCast.forward) of each adapter of the group
+ * and the lora_A nn.Linear applied to its output (:172), in one pass over x.
+ */
+int64_t qlora_lora_dropout_down_workspace_size(int64_t M, int64_t K, int slots);
+int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, const void* A,
+                            int64_t a_row_stride, int64_t M, int64_t K, int slots, int dtype,
+                            const uint64_t* seeds, float p, float scale, void* const* xd,
+                            int64_t xd_row_stride, uint8_t* const* bits, int64_t bits_row_stride,
+                            void* u, int64_t u_row_stride, int u_cols, void* u_t,
+                            int64_t u_t_row_stride, void* workspace, int64_t workspace_bytes,
+                            ql_stream_t stream);
+
+/*
  * Measurement only (no counterpart in the reference; nothing in the step calls it): the
  * matrix-core rate under layers of the NT GEMM's pipeline. One workgroup of 4 waves per CU (one
  * wave per SIMD, as the GEMM runs) issues the GEMM's 4 x 4 grid of v_mfma_f32_32x32x16 on the

@@ -275,3 +275,26 @@ def test_dropout_keep_threshold_is_the_float_test(lib):
         assert np.array_equal(x >= t, want), p
     # the mask's own rate: at p = 0.05 the threshold sits at 5% of the range
     assert abs(int(lib.qlora_dropout_keep_threshold(0.05)) / 2**31 - 0.05) < 1e-6
+
+
+@needs_no_device
+def test_dropout_down_rejects_bad_arguments(lib):
+    """qlora_lora_dropout_down returns status codes before any launch: slots outside 1..4 and p
+    outside (0, 1) are QL_EINVAL, K not a multiple of 64 or a short stride QL_ESHAPE, a
+    misaligned row stride QL_EALIGN."""
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    seeds = (ctypes.c_uint64 * 4)(1, 2, 3, 4)
+    ptrs = (ctypes.c_void_p * 4)(0x1000, 0x2000, 0x3000, 0x4000)
+
+    def call(M=16, K=128, slots=1, p=0.05, ldx=128, u_cols=64, xd_rs=128):
+        return lib.qlora_lora_dropout_down(fake, ldx, fake, 128, M, K, slots, 2, seeds, p,
+                                           1.0 / (1.0 - p) if p < 1 else 1.0, ptrs, xd_rs, ptrs,
+                                           K // 8, fake, 64, u_cols, None, 0, None, 0, None)
+
+    assert call(slots=0) == -1 and call(slots=5) == -1
+    assert call(p=0.0) == -1 and call(p=1.0) == -1
+    assert call(K=96, ldx=96, xd_rs=96) == -4
+    assert call(ldx=64) == -4 and call(u_cols=16 * 1 - 8) == -4
+    assert call(ldx=132) == -3
+    assert call(M=0) == 0
