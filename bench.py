@@ -800,6 +800,57 @@ def bench_gemm_data(torch, res, reps=20, sets=3):
         res[f"mfma_probe_32x32x16_bf16_{name}"] = probe
 
 
+def bench_dropout(torch, res, replays=10):
+    """LoRA dropout at the 7B step's shapes (4096 rows, p = 0.05, bf16): per adapter group, the
+    dropout kernel plus lora_down for each adapter, the dropout kernel alone, and the one-pass
+    qlora_lora_dropout_down (with its workspace, which splits long K, and without it). Rates are
+    Philox draws per second (one per input element and adapter)."""
+    import ctypes
+
+    from hackathon_amd import _lib, gemm, lora
+
+    dt, p = torch.bfloat16, 0.05
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for M, K, G in ((4096, 3584, 3), (4096, 3584, 2), (4096, 3584, 1), (4096, 18944, 1)):
+        x = torch.randn(M, K, device="cuda", generator=g).to(dt)
+        a16 = (0.1 * torch.randn(16 * G, K, device="cuda", generator=g)).to(dt)
+        u = torch.empty(M, 64, device="cuda", dtype=dt)
+        ut = torch.empty(16 * G, M, device="cuda", dtype=dt)
+        seeds = [1234 + i for i in range(G)]
+        xds = [torch.empty(M, K, device="cuda", dtype=dt) for _ in range(G)]
+        bitss = [torch.empty(M, K // 8, device="cuda", dtype=torch.uint8) for _ in range(G)]
+        sa = (ctypes.c_uint64 * G)(*seeds)
+        xp = (ctypes.c_void_p * G)(*[t.data_ptr() for t in xds])
+        bp = (ctypes.c_void_p * G)(*[t.data_ptr() for t in bitss])
+        ws, ws_bytes = _lib.workspace("qlora_lora_dropout_down_workspace_size", M, K, G,
+                                      device="cuda")
+
+        def per_adapter(down=True):
+            for i in range(G):
+                _lib.call("qlora_lora_dropout_scale_bits", x.data_ptr(), K, xds[i].data_ptr(), K,
+                          bitss[i].data_ptr(), K // 8, M, K, _lib.tag(dt), seeds[i], p,
+                          1 / (1 - p), _lib.stream_of(x))
+                if down:
+                    gemm.lora_down(xds[i], a16[16 * i:16 * i + 16], u[:, 16 * i:],
+                                   out_t=ut[16 * i:16 * i + 16])
+
+        def one_pass(w=ws, nb=ws_bytes):
+            _lib.call("qlora_lora_dropout_down", x.data_ptr(), K, a16.data_ptr(), K, M, K, G,
+                      _lib.tag(dt), sa, p, 1 / (1 - p), xp, K, bp, K // 8, u.data_ptr(), 64, 64,
+                      ut.data_ptr(), M, _lib.ptr(w), nb, _lib.stream_of(x))
+
+        draws = G * M * K
+        entry = {}
+        for name, fn in (("dropout_and_lora_down_per_adapter", per_adapter),
+                         ("dropout_alone", lambda: per_adapter(False)),
+                         ("one_pass", one_pass),
+                         ("one_pass_unsplit", lambda: one_pass(None, 0))):
+            t = _graph_time([fn] * 4, torch, replays)
+            entry[name] = dict(us=round(t * 1e6, 1), gdraws_per_s=round(draws / t / 1e9, 1))
+        entry["splits"] = 1 if ws_bytes == 0 else ws_bytes // (M * 16 * G * 4)
+        res[f"dropout_down_{M}x{K}x{G}"] = entry
+
+
 WORKLOADS = {
     "gemm_data": lambda torch, res: bench_gemm_data(torch, res),
     "rmsnorm": lambda torch, res: bench_rmsnorm(torch, res),
@@ -810,6 +861,7 @@ WORKLOADS = {
     "mlp": lambda torch, res: res.update(qwen25_7b_mlp_lora_4096tok=bench_mlp(torch)),
     "nf4_small": lambda torch, res: res.update(nf4_4864x896=bench_nf4_small(torch)),
     "next": lambda torch, res: bench_next_rows(torch, res),
+    "dropout": lambda torch, res: bench_dropout(torch, res),
 }
 
 
