@@ -64,6 +64,9 @@ _SIGNATURES = {
                                 ctypes.POINTER(ctypes.c_void_p), _c_i64,
                                 ctypes.POINTER(ctypes.c_void_p), _c_i64, _c_ptr, _c_i64, _c_int,
                                 _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
+    "qlora_lora_wgrad_masked": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                ctypes.POINTER(ctypes.c_void_p), _c_i64, _c_f32, _c_ptr, _c_f32,
+                                _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_dropout_scale_bits": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64,
                                       _c_i64, _c_int, _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_up_masked_add": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,

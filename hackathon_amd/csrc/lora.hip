@@ -59,12 +59,13 @@ __global__ __launch_bounds__(kThreads) void dropout_scale_kernel(
 }
 
 // The dropout forward for the fused 4-bit LoRA layer: the same OUT = IN * keep * scale as
-// dropout_scale_kernel (vector rows only), plus the keep mask as bits, byte c / 8 of row `row`
-// holding columns c .. c + 7 (bit j = column c + j), so the backward needs no second Philox pass.
+// dropout_scale_kernel (vector rows only), plus the keep mask as bits in the 8 x 8 block layout
+// of ql_philox.h (bit j of a row's byte for columns c .. c + 7 is column c + j), so the backward
+// needs no second Philox pass.
 template <int IT, int OT>
 __global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
     const typename Elem<IT>::T* __restrict__ in, int64_t in_rs, typename Elem<OT>::T* __restrict__ out,
-    int64_t out_rs, uint8_t* __restrict__ bits, int64_t bits_rs, int64_t n_cols, uint64_t seed,
+    int64_t out_rs, uint8_t* __restrict__ bits, int64_t bits_gs, int64_t n_cols, uint64_t seed,
     uint32_t thr, float scale) {
   const int64_t row = blockIdx.x;
   const auto* src = in + row * in_rs;
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void dropout_bits_kernel(
       b |= (uint32_t)keep << j;
     }
     Vec8<OT>::store(dst + c, v);
-    bits[row * bits_rs + c / 8] = (uint8_t)b;
+    bits[ql_philox::keep_byte(row, c, bits_gs)] = (uint8_t)b;
   }
 }
 
@@ -122,7 +123,7 @@ template <> QL_DEV f32x4_t mfma16<QL_F16>(const uint2& a, const uint2& b) {
 }
 
 struct SlotBits {
-  const uint8_t* p[4];  // adapter g's keep bits [M, >= K / 8], one row stride for all
+  const uint8_t* p[4];  // adapter g's keep bits (8 x 8 blocks, ql_philox.h), one group stride
 };
 
 constexpr int kMaskedCols = 64;      // columns per wave (four 16-column blocks)
@@ -131,7 +132,7 @@ constexpr int kMaskedPitch = 64 + 4;  // floats per LDS row (padding spreads the
 template <int DT, int G>
 __device__ __forceinline__ void up_masked_add_body(
     uint16_t* __restrict__ dx, int64_t dx_rs, const uint16_t* __restrict__ du, int64_t du_rs,
-    const uint16_t* __restrict__ A, int64_t a_rs, const SlotBits& bits, int64_t bits_rs,
+    const uint16_t* __restrict__ A, int64_t a_rs, const SlotBits& bits, int64_t bits_gs,
     int64_t M, int64_t K, float scale, int row_blocks,
     float (*__restrict__ prod)[16 * kMaskedPitch]) {
 #pragma clang fp contract(off)
@@ -169,7 +170,7 @@ __device__ __forceinline__ void up_masked_add_body(
                      : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int g = 0; g < G; ++g)
-        bv[2 * g + h] = col_ok ? bits.p[g][m * bits_rs + (k0 + c8) / 8] : 0u;
+        bv[2 * g + h] = col_ok ? bits.p[g][ql_philox::keep_byte(m, k0 + c8, bits_gs)] : 0u;
     }
   };
   uint4 xv[2];
@@ -233,9 +234,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))
 void up_masked_add_kernel(uint16_t* __restrict__ dx, int64_t dx_rs,
                           const uint16_t* __restrict__ du, int64_t du_rs,
                           const uint16_t* __restrict__ A, int64_t a_rs, SlotBits bits,
-                          int64_t bits_rs, int64_t M, int64_t K, float scale, int row_blocks) {
+                          int64_t bits_gs, int64_t M, int64_t K, float scale, int row_blocks) {
   __shared__ __attribute__((aligned(16))) float prod[kThreads / 64][16 * kMaskedPitch];
-  up_masked_add_body<DT, G>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale,
+  up_masked_add_body<DT, G>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_gs, M, K, scale,
                             row_blocks, prod);
 }
 
@@ -244,9 +245,9 @@ __global__ __launch_bounds__(kThreads)
 void up_masked_add4_kernel(uint16_t* __restrict__ dx, int64_t dx_rs,
                            const uint16_t* __restrict__ du, int64_t du_rs,
                            const uint16_t* __restrict__ A, int64_t a_rs, SlotBits bits,
-                           int64_t bits_rs, int64_t M, int64_t K, float scale, int row_blocks) {
+                           int64_t bits_gs, int64_t M, int64_t K, float scale, int row_blocks) {
   __shared__ __attribute__((aligned(16))) float prod[kThreads / 64][16 * kMaskedPitch];
-  up_masked_add_body<DT, 4>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale,
+  up_masked_add_body<DT, 4>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_gs, M, K, scale,
                             row_blocks, prod);
 }
 
@@ -361,7 +362,7 @@ extern "C" uint32_t qlora_dropout_keep_threshold(float p) {
 
 extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* out,
                                              int64_t out_row_stride, uint8_t* bits,
-                                             int64_t bits_row_stride, int64_t n_rows,
+                                             int64_t bits_group_stride, int64_t n_rows,
                                              int64_t n_cols, int dtype, uint64_t seed, float p,
                                              float scale, ql_stream_t stream) {
   if (n_rows < 0 || n_cols < 0 || n_rows > UINT32_MAX || !(p > 0.0f) || !(p < 1.0f))
@@ -369,7 +370,7 @@ extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stri
   if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
   if (n_rows == 0 || n_cols == 0) return QL_OK;
   if (!in || !out || !bits) return QL_EINVAL;
-  if (n_cols % 8 || bits_row_stride < n_cols / 8) return QL_ESHAPE;
+  if (n_cols % 8 || bits_group_stride < n_cols || bits_group_stride % 8) return QL_ESHAPE;
   if (!rows_vec_ok(in, in_row_stride, dtype, n_cols) || !rows_vec_ok(out, out_row_stride, dtype, n_cols))
     return QL_EALIGN;
   const dim3 grid((unsigned)n_rows);
@@ -379,44 +380,44 @@ extern "C" int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stri
   if (dtype == QL_BF16)
     hipLaunchKernelGGL((dropout_bits_kernel<QL_BF16, QL_BF16>), grid, dim3(kThreads), 0, s,
                        (const B*)in, in_row_stride, (B*)out, out_row_stride, bits,
-                       bits_row_stride, n_cols, seed, thr, scale);
+                       bits_group_stride, n_cols, seed, thr, scale);
   else
     hipLaunchKernelGGL((dropout_bits_kernel<QL_F16, QL_F16>), grid, dim3(kThreads), 0, s,
                        (const B*)in, in_row_stride, (B*)out, out_row_stride, bits,
-                       bits_row_stride, n_cols, seed, thr, scale);
+                       bits_group_stride, n_cols, seed, thr, scale);
   return ql_launch_status();
 }
 
 template <int DT, int G>
 void launch_masked_add(void* dx, int64_t dx_rs, const void* du, int64_t du_rs, const void* A,
-                       int64_t a_rs, const SlotBits& bits, int64_t bits_rs, int64_t M, int64_t K,
+                       int64_t a_rs, const SlotBits& bits, int64_t bits_gs, int64_t M, int64_t K,
                        float scale, dim3 grid, int row_blocks, hipStream_t s) {
   if constexpr (G == 4)
     hipLaunchKernelGGL((up_masked_add4_kernel<DT>), grid, dim3(kThreads), 0, s, (uint16_t*)dx,
-                       dx_rs, (const uint16_t*)du, du_rs, (const uint16_t*)A, a_rs, bits, bits_rs,
+                       dx_rs, (const uint16_t*)du, du_rs, (const uint16_t*)A, a_rs, bits, bits_gs,
                        M, K, scale, row_blocks);
   else
     hipLaunchKernelGGL((up_masked_add_kernel<DT, G>), grid, dim3(kThreads), 0, s, (uint16_t*)dx,
-                       dx_rs, (const uint16_t*)du, du_rs, (const uint16_t*)A, a_rs, bits, bits_rs,
+                       dx_rs, (const uint16_t*)du, du_rs, (const uint16_t*)A, a_rs, bits, bits_gs,
                        M, K, scale, row_blocks);
 }
 
 template <int DT>
 void launch_masked_add_g(int slots, void* dx, int64_t dx_rs, const void* du, int64_t du_rs,
-                         const void* A, int64_t a_rs, const SlotBits& bits, int64_t bits_rs,
+                         const void* A, int64_t a_rs, const SlotBits& bits, int64_t bits_gs,
                          int64_t M, int64_t K, float scale, dim3 grid, int rows, hipStream_t s) {
   switch (slots) {
-    case 1: launch_masked_add<DT, 1>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
-    case 2: launch_masked_add<DT, 2>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
-    case 3: launch_masked_add<DT, 3>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
-    default: launch_masked_add<DT, 4>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_rs, M, K, scale, grid, rows, s); break;
+    case 1: launch_masked_add<DT, 1>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_gs, M, K, scale, grid, rows, s); break;
+    case 2: launch_masked_add<DT, 2>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_gs, M, K, scale, grid, rows, s); break;
+    case 3: launch_masked_add<DT, 3>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_gs, M, K, scale, grid, rows, s); break;
+    default: launch_masked_add<DT, 4>(dx, dx_rs, du, du_rs, A, a_rs, bits, bits_gs, M, K, scale, grid, rows, s); break;
   }
 }
 
 extern "C" int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* du,
                                               int64_t du_row_stride, const void* A,
                                               int64_t a_row_stride, const uint8_t* const* bits,
-                                              int64_t bits_row_stride, int slots, int64_t M,
+                                              int64_t bits_group_stride, int slots, int64_t M,
                                               int64_t K, int dtype, float scale,
                                               ql_stream_t stream) {
   if (M < 0 || K < 0 || slots < 1 || slots > 4) return QL_EINVAL;
@@ -428,7 +429,8 @@ extern "C" int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, c
     if (!bits[g]) return QL_EINVAL;
     sb.p[g] = bits[g];
   }
-  if (K % 8 || bits_row_stride < K / 8 || du_row_stride < 16 * slots || a_row_stride < K)
+  if (K % 8 || bits_group_stride < K || bits_group_stride % 8 || du_row_stride < 16 * slots ||
+      a_row_stride < K)
     return QL_ESHAPE;
   if (!rows_vec_ok(dx, dx_row_stride, dtype, K) || !rows_vec_ok(A, a_row_stride, dtype, K) ||
       !rows_vec_ok(du, du_row_stride, dtype, 16))
@@ -442,19 +444,19 @@ extern "C" int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, c
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == QL_BF16)
     launch_masked_add_g<QL_BF16>(slots, dx, dx_row_stride, du, du_row_stride, A, a_row_stride, sb,
-                                 bits_row_stride, M, K, scale, grid, rows, s);
+                                 bits_group_stride, M, K, scale, grid, rows, s);
   else
     launch_masked_add_g<QL_F16>(slots, dx, dx_row_stride, du, du_row_stride, A, a_row_stride, sb,
-                                bits_row_stride, M, K, scale, grid, rows, s);
+                                bits_group_stride, M, K, scale, grid, rows, s);
   return ql_launch_status();
 }
 
 extern "C" int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
                                         int64_t du_row_stride, const void* A, int64_t a_row_stride,
-                                        const uint8_t* bits, int64_t bits_row_stride, int64_t M,
+                                        const uint8_t* bits, int64_t bits_group_stride, int64_t M,
                                         int64_t K, int dtype, float scale, ql_stream_t stream) {
   if (!bits && M > 0 && K > 0) return QL_EINVAL;
   const uint8_t* one[1] = {bits};
   return qlora_lora_up_masked_add_slots(dx, dx_row_stride, du, du_row_stride, A, a_row_stride, one,
-                                        bits_row_stride, 1, M, K, dtype, scale, stream);
+                                        bits_group_stride, 1, M, K, dtype, scale, stream);
 }

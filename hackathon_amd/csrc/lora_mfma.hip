@@ -897,17 +897,85 @@ QL_DEV void store_wgrad4(float* __restrict__ out, bool out_t, int64_t N, int nc,
   }
 }
 
+// The lora_A gradients of adapters whose inputs are their own dropout masks of one shared Q
+// (dA_g^T = du_g^T xd_g with xd_g = keep_g * (Q * scale rounded to Q's type)): the kernel
+// reads Q once and each adapter's keep bits (8 x 8 blocks, ql_philox.h: one 8-byte word per
+// lane's 8 x 8 block of Q), scales the block as the dropout kernels do, and zeroes the dropped
+// rows of each transposed fragment before the adapter's products. The sums are those of
+// lora_wgrad over the stored xd_g, in the same order.
+typedef short s16x2_t __attribute__((ext_vector_type(2)));
+
+// Q's 8 x 8 block times the dropout scale, rounded to the input type (the dropped input's value
+// for a kept element).
+template <int IT> QL_DEV void scale_block(uint4 (&q)[8], float scale) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float v[8];
+    Vec8<IT>::unpack(q[i], v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * scale;
+    q[i] = Vec8<IT>::pack(v);
+  }
+}
+
+// The keep bytes of a block's rows (w: row i in byte i) spread for transposed fragments: word p
+// holds row 2p's byte in its low half and row 2p + 1's in its high half.
+QL_DEV void spread_rows(const uint2& w, uint32_t (&sp)[4]) {
+  sp[0] = __builtin_amdgcn_perm(w.x, w.x, 0x0C010C00u);
+  sp[1] = __builtin_amdgcn_perm(w.x, w.x, 0x0C030C02u);
+  sp[2] = __builtin_amdgcn_perm(w.y, w.y, 0x0C010C00u);
+  sp[3] = __builtin_amdgcn_perm(w.y, w.y, 0x0C030C02u);
+}
+
+// Fragment T (column T of the block, rows 2p and 2p + 1 in word p) with the dropped rows zeroed:
+// bit T of each half moves to the half's sign bit and an arithmetic shift makes it 0 or 0xFFFF.
+template <int T> QL_DEV uint4 mask_column(const uint4& f, const uint32_t (&sp)[4]) {
+  uint32_t m[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    s16x2_t v = __builtin_bit_cast(s16x2_t, sp[p]);
+    v = (v << (short)(15 - T)) >> (short)15;
+    m[p] = __builtin_bit_cast(uint32_t, v);
+  }
+  return make_uint4(f.x & m[0], f.y & m[1], f.z & m[2], f.w & m[3]);
+}
+
+// MFMAs of one 8 x 8 block (transposed fragments qt) with each adapter's P fragment, the
+// adapter's keep word applied when MASKED.
+template <int IT, int G, bool MASKED>
+QL_DEV void wgrad_block(f32x4_t (&acc)[G][8], const uint4 (&qt)[8], const uint4 (&pf)[G],
+                        const uint2 (&kw)[G]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if constexpr (MASKED) {
+      uint32_t sp[4];
+      spread_rows(kw[g], sp);
+      acc[g][0] = mfma<IT>(pf[g], mask_column<0>(qt[0], sp), acc[g][0]);
+      acc[g][1] = mfma<IT>(pf[g], mask_column<1>(qt[1], sp), acc[g][1]);
+      acc[g][2] = mfma<IT>(pf[g], mask_column<2>(qt[2], sp), acc[g][2]);
+      acc[g][3] = mfma<IT>(pf[g], mask_column<3>(qt[3], sp), acc[g][3]);
+      acc[g][4] = mfma<IT>(pf[g], mask_column<4>(qt[4], sp), acc[g][4]);
+      acc[g][5] = mfma<IT>(pf[g], mask_column<5>(qt[5], sp), acc[g][5]);
+      acc[g][6] = mfma<IT>(pf[g], mask_column<6>(qt[6], sp), acc[g][6]);
+      acc[g][7] = mfma<IT>(pf[g], mask_column<7>(qt[7], sp), acc[g][7]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[g], qt[t], acc[g][t]);
+    }
+  }
+}
+
 // PARTIAL: each split writes its fp32 [N, NC] partial to ws[split]; lora_wgrad_reduce sums
 // them in split order. (Summing inside this launch by the last workgroup of each column block
 // needs device-scope release/acquire fences per workgroup, whose L2 write-back and invalidate
 // cost more than the separate reduce launch.)
 // U: 32-row chunks per wave per step of the main loop (the host picks one that divides the
 // chunks of a split, so only a ragged last split reaches the single-chunk loops after it).
-template <int IT, bool PARTIAL, int G, int U>
+template <int IT, bool PARTIAL, int G, int U, bool MASKED>
 __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
     const uint16_t* __restrict__ PT, int64_t ldpt, const uint16_t* __restrict__ Q, int64_t ldq,
     int64_t M, int64_t N, int64_t m_per_split, float* __restrict__ ws, float* __restrict__ out,
-    float alpha, bool out_t) {
+    float alpha, bool out_t, WgradMask mk) {
   constexpr int NC = kRank * G;
   __shared__ f32x4_t red[4 * 8 * 64];
   const int lane = threadIdx.x & 63;
@@ -937,9 +1005,17 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
   // contiguous bytes) and the matching 8 rows of P, transposes the block in registers into
   // eight fragments that each hold 8 consecutive rows of one column, and multiplies them by
   // P's fragment: MFMA t accumulates column n0 + 8 (l % 16) + t.
+  // keep words: the 8-byte word of block (rows r .. r + 7, columns ncolc .. +7), r a multiple
+  // of 8, is at r / 8 * gs + ncolc
+  auto keep_words = [&](int64_t r, uint2 (&kw)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      kw[g] = *reinterpret_cast<const uint2*>(mk.p[g] + (r >> 3) * mk.gs + ncolc);
+  };
   int64_t m = mb + 32 * wave;
   for (; m + 128 * (U - 1) + 32 <= me; m += 128 * U) {  // U whole chunks: loads only
     uint4 q[U][8], pf[U][G];
+    uint2 kw[U][G];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const char* qb = reinterpret_cast<const char*>(Q + (m + 128 * u) * ldq);
@@ -948,32 +1024,33 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
       for (int g = 0; g < G; ++g) pf[u][g] = ld16(pb, po[g]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) q[u][i] = ld16(qb, qo + i * ldq2);
+      if constexpr (MASKED) keep_words(m + 128 * u + 8 * mq, kw[u]);
     }
     __builtin_amdgcn_sched_barrier(0);  // the step's loads all go out before the first wait
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if constexpr (MASKED) scale_block<IT>(q[u], mk.scale);
       uint4 qt[8];
       transpose8x8(q[u], qt);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[u][g], qt[t], acc[g][t]);
+      wgrad_block<IT, G, MASKED>(acc, qt, pf[u], kw[u]);
     }
   }
   for (; m + 32 <= me; m += 128) {  // whole chunks left (fewer than U), one at a time
     uint4 q[8], pf[G];
+    uint2 kw[G];
     const char* qb = reinterpret_cast<const char*>(Q + m * ldq);
     const char* pb = reinterpret_cast<const char*>(PT + m);
 #pragma unroll
     for (int g = 0; g < G; ++g) pf[g] = ld16(pb, po[g]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) q[i] = ld16(qb, qo + i * ldq2);
+    if constexpr (MASKED) {
+      keep_words(m + 8 * mq, kw);
+      scale_block<IT>(q, mk.scale);
+    }
     uint4 qt[8];
     transpose8x8(q, qt);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[g], qt[t], acc[g][t]);
+    wgrad_block<IT, G, MASKED>(acc, qt, pf, kw);
   }
   if (m < me) {  // a partial chunk: rows past me contribute zeros
     const int64_t r0 = m + 8 * mq;
@@ -1002,12 +1079,21 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
         q[i] = r0 + i < me ? *reinterpret_cast<const uint4*>(Q + (r0 + i) * ldq + ncolc)
                            : make_uint4(0, 0, 0, 0);
     }
+    uint2 kw[G];
+    if constexpr (MASKED) {
+      // rows past me hold zeros; a block that starts past M has no keep word (nor anything to
+      // mask)
+      if (r0 < M) {
+        keep_words(r0, kw);
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) kw[g] = make_uint2(0, 0);
+      }
+      scale_block<IT>(q, mk.scale);
+    }
     uint4 qt[8];
     transpose8x8(q, qt);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) acc[g][t] = mfma<IT>(pf[g], qt[t], acc[g][t]);
+    wgrad_block<IT, G, MASKED>(acc, qt, pf, kw);
   }
   // acc[g][t]: lane holds out[n = ncol + t][16 g + 4 (lane / 16) .. +3]. Per slot: every wave
   // writes its 8 accumulators, then wave w sums t = 2w, 2w + 1 over the waves in wave order.
@@ -1260,8 +1346,10 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
 // ---------------------------------------------------------------------------------------
 // LoRA dropout fused with the adapters' down-projections (the forward with p > 0) for the
 // G <= 4 adapters of a group that read one input, each with its own mask and seed:
-//   xd_g = x * keep_g * scale (rounded to the input type)   stored: lora_A's gradient reads it
-//   bits_g[m, k / 8] bit k % 8 = keep_g(m, k)                stored: the dx pass reads it
+//   xd_g = x * keep_g * scale (rounded to the input type)   stored when asked for (XD)
+//   keep_g                                                   stored as bits (8 x 8 blocks):
+//                                                            the backward's dx and lora_A
+//                                                            gradient passes read them with x
 //   u[m, 16 g + c] = sum_k xd_g[m, k] A[16 g + c, k]
 // in one pass over x. keep_g is the Philox test of ql_philox.h at flat index m * K + k with
 // seed_g, computed as the dropout kernels compute it, so xd_g and bits_g equal theirs bit for
@@ -1287,14 +1375,14 @@ QL_DEV uint4 from_fragments(const uint4& h0, const uint4& h1, int src_byte, bool
 struct DropDownSlots {
   uint64_t seed[kMaxSlots];
   uint16_t* xd[kMaxSlots];  // [M, >= K] with one row stride for all slots
-  uint8_t* bits[kMaxSlots]; // [M, >= K / 8] with one row stride for all slots
+  uint8_t* bits[kMaxSlots]; // 8 x 8 blocks (ql_philox.h), one group stride for all slots
 };
 
-template <int DT, int G, bool PARTIAL>
+template <int DT, int G, bool PARTIAL, bool XD>
 __global__ __launch_bounds__(64 * kDdWaves) void dropout_down_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ A, int64_t lda,
     int64_t M, int64_t K, int64_t chunks_per_split, DropDownSlots sl, int64_t xd_rs,
-    int64_t bits_rs, uint32_t thr, float scale, float* __restrict__ ws,
+    int64_t bits_gs, uint32_t thr, float scale, float* __restrict__ ws,
     uint16_t* __restrict__ out, int64_t ldo, int out_cols, uint16_t* __restrict__ out_t,
     int64_t ldt) {
   __shared__ f32x4_t red[G * kDdWaves * 64];
@@ -1379,11 +1467,13 @@ __global__ __launch_bounds__(64 * kDdWaves) void dropout_down_kernel(
       // each store instruction writes 8 whole 128-B row pieces instead of 16 half lines.
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint4 o = from_fragments(dv[0], dv[1], perm_src[t], perm_hi);
+        uint4 o{};
+        if constexpr (XD) o = from_fragments(dv[0], dv[1], perm_src[t], perm_hi);
         const uint32_t b0 = (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src[t], (int)bw[0]);
         const uint32_t b1 = (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src[t], (int)bw[1]);
-        *reinterpret_cast<uint4*>(sl.xd[g] + srow_t[t] * xd_rs + c) = o;
-        sl.bits[g][srow_t[t] * bits_rs + c / 8] = (uint8_t)(perm_hi ? b1 : b0);
+        if constexpr (XD) *reinterpret_cast<uint4*>(sl.xd[g] + srow_t[t] * xd_rs + c) = o;
+        // 8 x 8 block layout: the 64 lanes' bytes are 64 contiguous bytes
+        sl.bits[g][ql_philox::keep_byte(srow_t[t], c, bits_gs)] = (uint8_t)(perm_hi ? b1 : b0);
       }
     }
 #pragma unroll
@@ -1550,7 +1640,7 @@ int64_t ql_lora_wgrad_workspace_floats(int64_t M, int64_t N, int slots) {
 
 int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
                   int64_t M, int64_t N, int slots, float* out, int out_t, float alpha, float* ws,
-                  int64_t ws_floats, hipStream_t s) {
+                  int64_t ws_floats, hipStream_t s, const WgradMask* mask) {
   if (slots < 1 || slots > kMaxSlots) return QL_EINVAL;
   const int nc = kRank * slots;
   if (M <= 0 || N <= 0 || N % 8 || ldpt < M || ldq < N) return QL_EINVAL;
@@ -1569,19 +1659,25 @@ int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int
   // take the registers) that divides a split's mps / 128 chunks per wave
   const int64_t per_wave = mps / 128;
   const int unroll = (slots == 1 && per_wave % 4 == 0) ? 4 : (per_wave % 2 == 0 ? 2 : 1);
-#define QL_WGRAD_GU(IT, G, U)                                                                 \
+  const WgradMask mk = mask ? *mask : WgradMask{};
+#define QL_WGRAD_GUM(IT, G, U, MK)                                                            \
   do {                                                                                        \
     if (splits == 1) {                                                                        \
-      hipLaunchKernelGGL((lora_wgrad_kernel<IT, false, G, U>), grid, dim3(kThreads), 0, s,    \
+      hipLaunchKernelGGL((lora_wgrad_kernel<IT, false, G, U, MK>), grid, dim3(kThreads), 0, s, \
                          (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps,       \
-                         (float*)nullptr, out, alpha, out_t);                                 \
+                         (float*)nullptr, out, alpha, out_t, mk);                             \
     } else {                                                                                  \
-      hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U>), grid, dim3(kThreads), 0, s,     \
+      hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U, MK>), grid, dim3(kThreads), 0, s,  \
                          (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,   \
-                         out, alpha, out_t);                                                  \
+                         out, alpha, out_t, mk);                                              \
       hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(N * nc / 4)), dim3(256), 0, s, ws,    \
                          splits, N, nc, out, alpha, out_t);                                   \
     }                                                                                         \
+  } while (0)
+#define QL_WGRAD_GU(IT, G, U)                          \
+  do {                                                 \
+    if (mask) QL_WGRAD_GUM(IT, G, U, true);            \
+    else QL_WGRAD_GUM(IT, G, U, false);                \
   } while (0)
 #define QL_WGRAD_G(IT, G)                                          \
   do {                                                             \
@@ -1603,6 +1699,7 @@ int ql_lora_wgrad(int in_dtype, const void* PT, int64_t ldpt, const void* Q, int
 #undef QL_WGRAD
 #undef QL_WGRAD_G
 #undef QL_WGRAD_GU
+#undef QL_WGRAD_GUM
   return ql_launch_status();
 }
 
@@ -1951,7 +2048,7 @@ extern "C" int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, cons
                                        int64_t a_row_stride, int64_t M, int64_t K, int slots,
                                        int dtype, const uint64_t* seeds, float p, float scale,
                                        void* const* xd, int64_t xd_row_stride,
-                                       uint8_t* const* bits, int64_t bits_row_stride, void* u,
+                                       uint8_t* const* bits, int64_t bits_group_stride, void* u,
                                        int64_t u_row_stride, int u_cols, void* u_t,
                                        int64_t u_t_row_stride, void* workspace,
                                        int64_t workspace_bytes, ql_stream_t stream) {
@@ -1960,22 +2057,22 @@ extern "C" int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, cons
     return QL_EINVAL;
   if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
   if (M == 0 || K == 0) return QL_OK;
-  if (!x || !A || !seeds || !xd || !bits || !u) return QL_EINVAL;
+  if (!x || !A || !seeds || !bits || !u) return QL_EINVAL;
   if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
   DropDownSlots sl{};
   for (int g = 0; g < slots; ++g) {
-    if (!xd[g] || !bits[g]) return QL_EINVAL;
-    if (!ql_aligned(xd[g], 16)) return QL_EALIGN;
+    if ((xd && !xd[g]) || !bits[g]) return QL_EINVAL;
+    if (xd && !ql_aligned(xd[g], 16)) return QL_EALIGN;
     sl.seed[g] = seeds[g];
-    sl.xd[g] = static_cast<uint16_t*>(xd[g]);
+    sl.xd[g] = xd ? static_cast<uint16_t*>(xd[g]) : nullptr;
     sl.bits[g] = bits[g];
   }
   const int nc = kRank * slots;
-  if (K % 64 || x_row_stride < K || a_row_stride < K || xd_row_stride < K ||
-      bits_row_stride < K / 8 || u_cols < nc || u_row_stride < u_cols ||
+  if (K % 64 || x_row_stride < K || a_row_stride < K || (xd && xd_row_stride < K) ||
+      bits_group_stride < K || bits_group_stride % 8 || u_cols < nc || u_row_stride < u_cols ||
       (u_t && u_t_row_stride < M))
     return QL_ESHAPE;
-  if (x_row_stride % 8 || a_row_stride % 8 || xd_row_stride % 8 || !ql_aligned(x, 16) ||
+  if (x_row_stride % 8 || a_row_stride % 8 || (xd && xd_row_stride % 8) || !ql_aligned(x, 16) ||
       !ql_aligned(A, 16) || !ql_aligned(u, 2) || (u_t && !ql_aligned(u_t, 2)))
     return QL_EALIGN;
   const int64_t gx = (M + 15) / 16;
@@ -1989,18 +2086,23 @@ extern "C" int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, cons
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
   const dim3 grid((unsigned)gx, (unsigned)splits);
-#define QL_DD(DT, G)                                                                          \
+#define QL_DD(DT, G)                \
+  do {                              \
+    if (xd) QL_DDX(DT, G, true);    \
+    else QL_DDX(DT, G, false);      \
+  } while (0)
+#define QL_DDX(DT, G, XD)                                                                     \
   do {                                                                                        \
     if (splits == 1) {                                                                        \
-      hipLaunchKernelGGL((dropout_down_kernel<DT, G, false>), grid, dim3(64 * kDdWaves), 0, s, \
+      hipLaunchKernelGGL((dropout_down_kernel<DT, G, false, XD>), grid, dim3(64 * kDdWaves), 0, s, \
                          (const uint16_t*)x, x_row_stride, (const uint16_t*)A, a_row_stride,  \
-                         M, K, cps, sl, xd_row_stride, bits_row_stride, thr, scale,           \
+                         M, K, cps, sl, xd_row_stride, bits_group_stride, thr, scale,           \
                          (float*)nullptr, (uint16_t*)u, u_row_stride, u_cols,                 \
                          (uint16_t*)u_t, u_t_row_stride);                                     \
     } else {                                                                                  \
-      hipLaunchKernelGGL((dropout_down_kernel<DT, G, true>), grid, dim3(64 * kDdWaves), 0, s,  \
+      hipLaunchKernelGGL((dropout_down_kernel<DT, G, true, XD>), grid, dim3(64 * kDdWaves), 0, s, \
                          (const uint16_t*)x, x_row_stride, (const uint16_t*)A, a_row_stride,  \
-                         M, K, cps, sl, xd_row_stride, bits_row_stride, thr, scale, ws,       \
+                         M, K, cps, sl, xd_row_stride, bits_group_stride, thr, scale, ws,       \
                          (uint16_t*)u, u_row_stride, u_cols, (uint16_t*)u_t, u_t_row_stride); \
       hipLaunchKernelGGL((lora_down_reduce<DT, DT>), dim3(grid1d(M * u_cols)), dim3(256), 0,   \
                          s, ws, splits, M, nc, (typename Elem<DT>::T*)u, u_row_stride, u_cols, \
@@ -2021,6 +2123,7 @@ extern "C" int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, cons
   }
 #undef QL_DD_G
 #undef QL_DD
+#undef QL_DDX
   return ql_launch_status();
 }
 
@@ -2055,6 +2158,36 @@ extern "C" int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int
 // two per adapter.
 static int64_t wgrad_diag_floats(int64_t M, int64_t N, int slots) {
   return (int64_t)ql_lora_wgrad_splits(M, N, slots) * N * kRank * slots;
+}
+
+extern "C" int qlora_lora_wgrad_masked(const void* PT, int64_t ldpt, const void* Q, int64_t ldq,
+                                       int64_t M, int64_t N, int slots, int in_dtype,
+                                       const uint8_t* const* bits, int64_t bits_group_stride,
+                                       float scale, float* out, float alpha, void* workspace,
+                                       int64_t workspace_bytes, ql_stream_t stream) {
+  if (M < 0 || N < 0 || workspace_bytes < 0 || slots < 1 || slots > kMaxSlots) return QL_EINVAL;
+  if (N == 0) return QL_OK;
+  if (!PT || !Q || !out || !bits) return QL_EINVAL;
+  WgradMask mk{};
+  for (int g = 0; g < slots; ++g) {
+    if (!bits[g]) return QL_EINVAL;
+    if (!ql_aligned(bits[g], 8)) return QL_EALIGN;
+    mk.p[g] = bits[g];
+  }
+  if (N % 8 || bits_group_stride < N || bits_group_stride % 8) return QL_ESHAPE;
+  mk.gs = bits_group_stride;
+  mk.scale = scale;
+  if (M == 0) {  // an empty reduction: zeros (a fill kernel, not a memset node)
+    if (!ql_aligned(out, 16)) return QL_EALIGN;
+    hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(N * kRank * slots / 4)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), (const float*)nullptr, 0, N,
+                       kRank * slots, out, 0.f, true);
+    return ql_launch_status();
+  }
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  return ql_lora_wgrad(in_dtype, PT, ldpt, Q, ldq, M, N, slots, out, 1, alpha,
+                       static_cast<float*>(workspace), workspace_bytes / (int64_t)sizeof(float),
+                       static_cast<hipStream_t>(stream), &mk);
 }
 
 extern "C" int64_t qlora_lora_wgrad_diag_workspace_size(int64_t M, int64_t N, int slots) {
@@ -2095,9 +2228,9 @@ extern "C" int qlora_lora_wgrad_diag(const void* PT, int64_t ldpt, const void* Q
   const int64_t per_wave = mps / 128;
   const int unroll = (slots == 1 && per_wave % 4 == 0) ? 4 : (per_wave % 2 == 0 ? 2 : 1);
 #define QL_WD_GU(IT, G, U)                                                                     \
-  hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U>), grid, dim3(kThreads), 0, s,          \
+  hipLaunchKernelGGL((lora_wgrad_kernel<IT, true, G, U, false>), grid, dim3(kThreads), 0, s,   \
                      (const uint16_t*)PT, ldpt, (const uint16_t*)Q, ldq, M, N, mps, ws,         \
-                     (float*)nullptr, 0.f, false)
+                     (float*)nullptr, 0.f, false, WgradMask{})
 #define QL_WD_G(IT, G)                                     \
   do {                                                     \
     if (unroll == 4) QL_WD_GU(IT, G, (G == 1 ? 4 : 2));    \

@@ -56,4 +56,13 @@ inline uint32_t keep_threshold(float p) {
 
 QL_DEV bool keep_word(uint32_t w, uint32_t threshold) { return fold_word(w) >= threshold; }
 
+// The keep bits of an [M, K] input, in 8 x 8 blocks: the 8 rows 8 R .. 8 R + 7 take
+// `group_stride` (>= K) bytes from R * group_stride; in them, the 8 bytes of columns
+// 8 b .. 8 b + 7 sit at 8 b, one byte per row (row 8 R + i at 8 b + i), bit j for column
+// 8 b + j. An 8 x 8 block is one 8-byte word (the lora_A gradient's transposed reads take it in
+// one load), and a 16-row x 64-column tile is 128 contiguous bytes.
+QL_DEV int64_t keep_byte(int64_t row, int64_t col, int64_t group_stride) {
+  return (row >> 3) * group_stride + (col >> 3) * 8 + (row & 7);
+}
+
 }  // namespace ql_philox

@@ -139,7 +139,7 @@ def _column_blocks(specs):
 
 def group_forward(x2, specs, ab, seeds=None):
     """y [M, sum n_g] = x2 W_cat^T + u sB_cat^T + bias, the state the backward needs and, with
-    dropout (specs' p > 0, one seed per adapter), (p, a16, [xd_g], [keep bits_g]), else None."""
+    dropout (specs' p > 0, one seed per adapter), (p, a16, [keep bits_g]), else None."""
     dt = x2.dtype
     dev = x2.device
     M, K = x2.shape
@@ -152,20 +152,19 @@ def group_forward(x2, specs, ab, seeds=None):
     drop = None
     p = specs[0].p
     if p > 0 and K % 64 == 0:
-        # each adapter's own mask of x and its u, all adapters in one pass over x
-        xds, bitss = lora.dropout_down(x2, a16, p, seeds, u, ut)
-        drop = (p, a16, xds, bitss)
+        # each adapter's own mask of x (kept as bits) and its u, all adapters in one pass over x
+        _, bitss = lora.dropout_down(x2, a16, p, seeds, u, ut)
+        drop = (p, a16, bitss)
     elif p > 0:
         # one adapter at a time: slot g's lora_down writes u columns 16 g .. 16 g + 15 and
         # zeros after them, which the later slots overwrite
-        xds, bitss = [], []
+        bitss = []
         for g in range(G):
             xd, bits = lora.dropout_with_bits(x2, p, seeds[g])
             _gemm.lora_down(xd, a16[16 * g:16 * g + 16], u[:, 16 * g:],
                             out_t=ut[16 * g:16 * g + 16])
-            xds.append(xd)
             bitss.append(bits)
-        drop = (p, a16, xds, bitss)
+        drop = (p, a16, bitss)
     else:
         _gemm.lora_down(x2, a16, u, out_t=ut)  # every slot in one pass over x
     y = torch.empty((M, offs[-1]), dtype=dt, device=dev)
@@ -194,7 +193,7 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
     gradient g [M, sum n_g] (row stride a multiple of 8, unit column stride). `du_dut`, when
     given, holds the adapters' down-projections of g already (du [M, 64], du^T [16 G, M]);
     `db_given`, the lora_B gradients [dB_0, dB_1, ..] already computed; `drop`, group_forward's
-    dropout state (x2 is then not needed and may be None)."""
+    dropout state."""
     dt = g.dtype
     dev = g.device
     M = g.shape[0]
@@ -223,16 +222,18 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
         if drop is None:
             _gemm.gemm_nt_cat(g, wt, du, at, dx)
         else:
-            p, a16, _, bitss = drop
+            p, a16, bitss = drop
             _gemm.gemm_nt_cat(g, wt, None, None, dx)
             lora.up_masked_add_slots(dx, du, a16, bitss, p)  # every adapter in one pass
         del wt
     grads = []
     da_all = None
-    if drop is not None:  # dA_g^T = du_g^T xd_g, each adapter on its own dropped input
-        da_all = [_gemm.lora_wgrad(dut[16 * i:16 * i + 16], drop[2][i], transposed=True)
-                  if need_ab[2 * i] else None for i in range(G)]
-    elif any(need_ab[0::2]):  # dA_g^T for every slot in one pass over x: [16 G, K]
+    if drop is not None and any(need_ab[0::2]):
+        # dA_g^T = du_g^T xd_g, each adapter on its own dropped input, all in one pass over x
+        # (xd_g formed from x and adapter g's keep bits)
+        da_all = _gemm.lora_wgrad_masked(dut, x2, drop[2], drop[0])
+        da_all = [da_all[16 * i:16 * i + 16] for i in range(G)]
+    elif drop is None and any(need_ab[0::2]):  # dA_g^T for every slot in one pass over x
         da_all = _gemm.lora_wgrad(dut, x2, transposed=True)
         da_all = [da_all[16 * i:16 * i + 16] for i in range(G)]
     db_all = None
@@ -255,24 +256,24 @@ def group_backward(g, x2, at, bt, ut, specs, need_dx, need_ab, du_dut=None, db_g
 
 
 def _save(ctx, x2, drop, *tensors):
-    """save_for_backward of a group's state: x2 without dropout, else the dropout state (the
-    dropped inputs replace x2 for the lora_A gradients)."""
+    """save_for_backward of a group's state: x2, and with dropout a16 and every adapter's keep
+    bits (the lora_A gradients form the dropped inputs from x2 and the bits)."""
     if drop is None:
         ctx.save_for_backward(x2, *tensors)
         ctx.n_drop, ctx.p = 0, 0.0
     else:
-        p, a16, xds, bitss = drop
-        ctx.save_for_backward(a16, *xds, *bitss, *tensors)
-        ctx.n_drop, ctx.p = len(xds), p
+        p, a16, bitss = drop
+        ctx.save_for_backward(x2, a16, *bitss, *tensors)
+        ctx.n_drop, ctx.p = len(bitss), p
 
 
 def _saved(ctx):
-    """(x2 or None, dropout state or None, the other saved tensors) as _save stored them."""
+    """(x2, dropout state or None, the other saved tensors) as _save stored them."""
     t = ctx.saved_tensors
     G = ctx.n_drop
     if G == 0:
         return t[0], None, t[1:]
-    return None, (ctx.p, t[0], list(t[1:1 + G]), list(t[1 + G:1 + 2 * G])), t[1 + 2 * G:]
+    return t[0], (ctx.p, t[1], list(t[2:2 + G])), t[2 + G:]
 
 
 class QKVRoPE(torch.autograd.Function):

@@ -226,6 +226,29 @@ def lora_wgrad(pt: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
     return out
 
 
+def lora_wgrad_masked(pt: torch.Tensor, q: torch.Tensor, bitss, p: float,
+                      alpha: float = 1.0) -> torch.Tensor:
+    """fp32 [16 G, N]: rows 16 g .. 16 g + 15 = alpha * pt_g q_g, q_g = adapter g's dropout of
+    q [M, N] (keep bits bitss[g] from lora.dropout_with_bits / dropout_down, scale 1 / (1 - p)),
+    for G <= 4 adapters in one pass over q (qlora_lora_wgrad_masked): the lora_A gradients of a
+    group's adapters without their dropped inputs stored."""
+    import ctypes
+
+    _lib.require_rows(q.dtype, q=q, pt=pt)
+    M, N = q.shape
+    slots = _slots(pt.shape[0], "pt")
+    if len(bitss) != slots or len({b.stride(0) for b in bitss}) != 1:
+        raise ValueError("one keep-bit tensor per adapter, all with one group stride")
+    out = torch.empty((16 * slots, N), dtype=torch.float32, device=q.device)
+    ws, ws_bytes = _lib.workspace("qlora_lora_wgrad_workspace_size", M, N, slots,
+                                  device=q.device)
+    ptrs = (ctypes.c_void_p * slots)(*[b.data_ptr() for b in bitss])
+    _lib.call("qlora_lora_wgrad_masked", pt.data_ptr(), pt.stride(0), q.data_ptr(), q.stride(0),
+              M, N, slots, _lib.tag(q.dtype), ptrs, bitss[0].stride(0), 1.0 / (1.0 - p),
+              out.data_ptr(), float(alpha), _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+    return out
+
+
 def lora_pack(a: torch.Tensor, b: torch.Tensor, scaling: float, dtype, pad: int = 64):
     """(a16 [16,K], at_pad [K,pad], bs_pad [N,pad], bt [16,N]) in `dtype` from the fp32 adapter
     factors a [16, K] and b [N, 16] in one launch (qlora_lora_pack)."""

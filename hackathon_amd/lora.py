@@ -151,40 +151,49 @@ class LoRALinearFn(torch.autograd.Function):
 _PAD = 64  # rank-16 factors are zero-padded to one 64-wide K step of the NT GEMM
 
 
+def keep_bits_buffer(M, K, device):
+    """Keep bits of an [M, K] input in the kernels' 8 x 8 block layout: uint8 [ceil(M / 8), K],
+    row group R holding rows 8 R .. 8 R + 7, byte 8 (c / 8) + row % 8 the bits of columns
+    c .. c + 7 (bit j = column c + j)."""
+    return torch.empty(((M + 7) // 8, K), dtype=torch.uint8, device=device)
+
+
 def dropout_with_bits(x2, p, seed):
-    """(x2 * keep / (1 - p), keep bits [M, K / 8] uint8) in x2's dtype, the mask of
+    """(x2 * keep / (1 - p), keep bits in keep_bits_buffer's layout) in x2's dtype, the mask of
     DropoutCast(x2, p, seed) (qlora_lora_dropout_scale_bits)."""
     M, K = x2.shape
     if x2.data_ptr() % 16 or x2.stride(0) % 8:
         x2 = x2.contiguous() if x2.stride(0) % 8 else x2.clone()
     xd = torch.empty((M, K), dtype=x2.dtype, device=x2.device)
-    bits = torch.empty((M, K // 8), dtype=torch.uint8, device=x2.device)
+    bits = keep_bits_buffer(M, K, x2.device)
     _lib.call("qlora_lora_dropout_scale_bits", x2.data_ptr(), x2.stride(0), xd.data_ptr(),
               xd.stride(0), bits.data_ptr(), bits.stride(0), M, K, _lib.tag(x2.dtype),
               int(seed) & 0xFFFF_FFFF_FFFF_FFFF, float(p), 1.0 / (1.0 - p), _lib.stream_of(x2))
     return xd, bits
 
 
-def dropout_down(x2, a16, p, seeds, u, ut=None):
-    """Each adapter's dropped input and its down-projection in one pass over x2, for the G <= 4
-    adapters of a group (adapter g: rows 16 g .. 16 g + 15 of a16 [16 G, K], seed seeds[g]):
-    returns ([xd_g], [keep bits_g]) as dropout_with_bits(x2, p, seeds[g]) returns them, and
-    writes u[:, 16 g:16 g + 16] = xd_g a16_g^T (zeros in u's columns 16 G ..) and, when given,
-    ut [16 G, M] = its transpose (qlora_lora_dropout_down). K must be a multiple of 64."""
+def dropout_down(x2, a16, p, seeds, u, ut=None, keep_xd=False):
+    """Each adapter's keep mask and down-projection in one pass over x2, for the G <= 4 adapters
+    of a group (adapter g: rows 16 g .. 16 g + 15 of a16 [16 G, K], seed seeds[g]): returns
+    ([xd_g] if keep_xd else None, [keep bits_g]) as dropout_with_bits(x2, p, seeds[g]) returns
+    them, and writes u[:, 16 g:16 g + 16] = xd_g a16_g^T (zeros in u's columns 16 G ..) and,
+    when given, ut [16 G, M] = its transpose (qlora_lora_dropout_down). K must be a multiple
+    of 64."""
     M, K = x2.shape
     G = len(seeds)
     if x2.data_ptr() % 16 or x2.stride(0) % 8:
         x2 = x2.contiguous() if x2.stride(0) % 8 else x2.clone()
-    xds = [torch.empty((M, K), dtype=x2.dtype, device=x2.device) for _ in range(G)]
-    bitss = [torch.empty((M, K // 8), dtype=torch.uint8, device=x2.device) for _ in range(G)]
+    xds = ([torch.empty((M, K), dtype=x2.dtype, device=x2.device) for _ in range(G)]
+           if keep_xd else None)
+    bitss = [keep_bits_buffer(M, K, x2.device) for _ in range(G)]
     seed_arr = (ctypes.c_uint64 * G)(*[int(s) & 0xFFFF_FFFF_FFFF_FFFF for s in seeds])
-    xd_ptrs = (ctypes.c_void_p * G)(*[t.data_ptr() for t in xds])
+    xd_ptrs = (ctypes.c_void_p * G)(*[t.data_ptr() for t in xds]) if keep_xd else None
     bit_ptrs = (ctypes.c_void_p * G)(*[t.data_ptr() for t in bitss])
     ws, ws_bytes = _lib.workspace("qlora_lora_dropout_down_workspace_size", M, K, G,
                                   device=x2.device)
     _lib.call("qlora_lora_dropout_down", x2.data_ptr(), x2.stride(0), a16.data_ptr(),
               a16.stride(0), M, K, G, _lib.tag(x2.dtype), seed_arr, float(p), 1.0 / (1.0 - p),
-              xd_ptrs, K, bit_ptrs, K // 8, u.data_ptr(), u.stride(0), u.shape[1],
+              xd_ptrs, K, bit_ptrs, K, u.data_ptr(), u.stride(0), u.shape[1],
               None if ut is None else ut.data_ptr(), 0 if ut is None else ut.stride(0),
               _lib.ptr(ws), ws_bytes, _lib.stream_of(x2))
     return xds, bitss
@@ -224,9 +233,10 @@ class LoraNF4Linear(torch.autograd.Function):
                   dB = s g^T u,  dA = du^T xd      qlora_lora_wgrad (reductions over tokens)
 
     with xd = x when p = 0. With dropout (p > 0, the reference's training regime) xd =
-    x * keep / (1 - p) and u come from one pass of qlora_lora_dropout_down (the mask of
-    DropoutCast with the same seed, kept as bits), the dX GEMM runs on the base term alone and
-    qlora_lora_up_masked_add adds keep * (du A) / (1 - p).
+    x * keep / (1 - p) is never stored: one pass of qlora_lora_dropout_down draws the mask of
+    DropoutCast with the same seed (kept as bits) and forms u from xd on the way; the dX GEMM
+    runs on the base term alone and qlora_lora_up_masked_add adds keep * (du A) / (1 - p); dA
+    comes from x and the bits (qlora_lora_wgrad_masked).
 
     The same sums as base_layer(x) + ScaledAdd(B(A(dropout(x)))) of solution/lora.py:157-173
     with the adapter term accumulated in fp32 inside the base GEMM instead of rounded to the
@@ -245,11 +255,15 @@ class LoraNF4Linear(torch.autograd.Function):
         a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
         ut = _gemm.lora_t_buffer(M, dt, x2.device)                     # u^T, for dB
-        if p > 0 and K % 64 == 0:  # the dropped input, its bits and u in one pass over x
-            (xd,), (bits,) = dropout_down(x2, a16, p, (seed,), u, ut)
-        else:
-            xd, bits = dropout_with_bits(x2, p, seed) if p > 0 else (x2, None)
+        bits = None
+        if p > 0 and K % 64 == 0:  # the keep bits and u in one pass over x
+            _, (bits,) = dropout_down(x2, a16, p, (seed,), u, ut)
+        elif p > 0:
+            xd, bits = dropout_with_bits(x2, p, seed)
             _gemm.lora_down(xd, a16, u, out_t=ut)
+            del xd
+        else:
+            _gemm.lora_down(x2, a16, u, out_t=ut)
         y = torch.empty((M, N), dtype=dt, device=x2.device)
         b16 = None if bias is None else bias.to(dt)
         if nf4.use_fused_gemm(x2, quant_state, packed, a2=u):  # few rows: W dequantised in-GEMM
@@ -259,7 +273,7 @@ class LoraNF4Linear(torch.autograd.Function):
             _gemm.gemm_nt_cat(x2, w, u, bs, y, bias=b16)
             del w
         del u
-        ctx.save_for_backward(xd, ut, at, bt, a16 if p > 0 else None, bits)
+        ctx.save_for_backward(x2, ut, at, bt, a16 if p > 0 else None, bits)
         ctx.packed, ctx.quant_state, ctx.scaling = packed, quant_state, float(scaling)
         ctx.p = float(p)
         ctx.shape, ctx.wdtypes = x.shape, (a_weight.dtype, b_weight.dtype)
@@ -269,9 +283,9 @@ class LoraNF4Linear(torch.autograd.Function):
     def backward(ctx, g):
         from . import nf4
 
-        xd, ut, at, bt, a16, bits = ctx.saved_tensors
-        dt = xd.dtype
-        M, K = xd.shape
+        x2, ut, at, bt, a16, bits = ctx.saved_tensors
+        dt = x2.dtype
+        M, K = x2.shape
         g2 = _rows(g)
         if g2.dtype != dt:
             g2 = g2.to(dt)
@@ -291,8 +305,9 @@ class LoraNF4Linear(torch.autograd.Function):
                 up_masked_add(dx, du, a16, bits, ctx.p)
             del wt
             dx = dx.view(ctx.shape)
-        if ctx.needs_input_grad[1]:
-            da = _gemm.lora_wgrad(dut, xd, transposed=True)             # [16, K] = du^T xd
+        if ctx.needs_input_grad[1]:                                     # [16, K] = du^T xd
+            da = (_gemm.lora_wgrad(dut, x2, transposed=True) if bits is None
+                  else _gemm.lora_wgrad_masked(dut, x2, [bits], ctx.p))  # xd from x and bits
             if da.dtype != ctx.wdtypes[0]:
                 da = da.to(ctx.wdtypes[0])
         if ctx.needs_input_grad[2]:

@@ -202,16 +202,21 @@ int qlora_lora_scaled_add(const void* base, int base_dtype, int64_t base_row_str
 
 /*
  * LoRA dropout forward that also keeps the mask: out = in * keep * scale (the bits of
- * qlora_lora_dropout_scale with p > 0, the same Philox uniform), and bits[row][c / 8] bit
- * c % 8 = keep(row, c). in and out share dtype QL_BF16 or QL_F16; n_cols % 8 == 0 and 16-B
- * aligned rows (QL_ESHAPE / QL_EALIGN otherwise); 0 < p < 1 (QL_EINVAL otherwise).
+ * qlora_lora_dropout_scale with p > 0, the same Philox uniform), and the keep bits in 8 x 8
+ * blocks: rows 8 R .. 8 R + 7 take bits_group_stride bytes from R * bits_group_stride, and in
+ * them byte 8 (c / 8) + row % 8 holds keep(row, c .. c + 7), bit j for column c + j
+ * (c % 8 == 0). An 8 x 8 block is one 8-byte word; ceil(n_rows / 8) * bits_group_stride bytes
+ * in all (the bytes of rows past n_rows in the last group are not written). in and out share
+ * dtype QL_BF16 or QL_F16; n_cols % 8 == 0, bits_group_stride >= n_cols and a multiple of 8,
+ * 16-B aligned rows (QL_ESHAPE / QL_EALIGN otherwise); 0 < p < 1 (QL_EINVAL otherwise).
  * Replaces: solution/lora.py:29-46 + :84-89 (DropoutCast.forward) for the fused 4-bit LoRA
  * layer, whose backward reads the bits instead of regenerating the mask (:90-93).
  */
 int qlora_lora_dropout_scale_bits(const void* in, int64_t in_row_stride, void* out,
-                                  int64_t out_row_stride, uint8_t* bits, int64_t bits_row_stride,
-                                  int64_t n_rows, int64_t n_cols, int dtype, uint64_t seed,
-                                  float p, float scale, ql_stream_t stream);
+                                  int64_t out_row_stride, uint8_t* bits,
+                                  int64_t bits_group_stride, int64_t n_rows, int64_t n_cols,
+                                  int dtype, uint64_t seed, float p, float scale,
+                                  ql_stream_t stream);
 
 /*
  * The integer form of the dropout test, host only (no GPU call): with x the Philox word folded
@@ -227,15 +232,15 @@ uint32_t qlora_dropout_keep_threshold(float p);
  * The adapter's input gradient through the dropout, added to the base layer's:
  *   dx[m][k] += keep(m, k) ? scale * sum_{r<16} du[m][r] * A[r][k] : 0
  * du = s g B [M, >= 16], A [16, K] (rank 16), dx [M, K], all dtype (QL_BF16 / QL_F16); keep from
- * qlora_lora_dropout_scale_bits' bits. The rank-16 products run on the matrix cores (16-bit
- * operands, fp32 sums), dx is rounded once. K % 8 == 0 and 16-B aligned rows (QL_ESHAPE /
- * QL_EALIGN otherwise).
+ * qlora_lora_dropout_scale_bits' bits (its layout, bits_group_stride >= K and a multiple of 8).
+ * The rank-16 products run on the matrix cores (16-bit operands, fp32 sums), dx is rounded
+ * once. K % 8 == 0 and 16-B aligned rows (QL_ESHAPE / QL_EALIGN otherwise).
  * Replaces: solution/lora.py:90-93 (DropoutCast.backward) applied to lora_A's input gradient
  * (the autograd of :172), and autograd's sum with the base layer's gradient.
  */
 int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
                              int64_t du_row_stride, const void* A, int64_t a_row_stride,
-                             const uint8_t* bits, int64_t bits_row_stride, int64_t M, int64_t K,
+                             const uint8_t* bits, int64_t bits_group_stride, int64_t M, int64_t K,
                              int dtype, float scale, ql_stream_t stream);
 
 /*
@@ -243,8 +248,8 @@ int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
  * each with its own mask, in one pass over dx:
  *   dx[m][k] += scale * sum_{g < slots, keep_g(m, k)} sum_{r<16} du[m][16 g + r] * A[16 g + r][k]
  * du [M, >= 16 slots] (adapter g in columns 16 g ..), A [16 slots, K] (adapter g in rows 16 g ..),
- * bits: a host array of `slots` device pointers, adapter g's bits [M, >= K / 8] at bits[g], all
- * with bits_row_stride. The kept adapters' sums are added in fp32 in slot order and dx is
+ * bits: a host array of `slots` device pointers, adapter g's bits (the layout above) at
+ * bits[g], all with bits_group_stride. The kept adapters' sums are added in fp32 in slot order and dx is
  * rounded once (so slots = 1 is qlora_lora_up_masked_add, bit for bit). QL_EINVAL for slots
  * outside 1 .. 4 or a null pointer; shapes and alignment as above.
  * Replaces: solution/lora.py:90-93 (DropoutCast.backward) of each adapter of the group, applied
@@ -253,7 +258,7 @@ int qlora_lora_up_masked_add(void* dx, int64_t dx_row_stride, const void* du,
  */
 int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* du,
                                    int64_t du_row_stride, const void* A, int64_t a_row_stride,
-                                   const uint8_t* const* bits, int64_t bits_row_stride, int slots,
+                                   const uint8_t* const* bits, int64_t bits_group_stride, int slots,
                                    int64_t M, int64_t K, int dtype, float scale,
                                    ql_stream_t stream);
 
@@ -261,12 +266,13 @@ int qlora_lora_up_masked_add_slots(void* dx, int64_t dx_row_stride, const void* 
  * LoRA dropout fused with the adapters' down-projections, for 1 <= slots <= 4 adapters that
  * read one input x [M, K] (K % 64 == 0), each with its own seed (host array seeds[slots]):
  *   xd[g]   = x * keep_g * scale      in dtype, as qlora_lora_dropout_scale_bits(seeds[g]) writes it
- *   bits[g] = keep_g                  bit layout of qlora_lora_dropout_scale_bits
+ *   bits[g] = keep_g                  layout of qlora_lora_dropout_scale_bits
  *   u[m][16 g + c] = sum_k xd[g][m][k] * A[16 g + c][k]   fp32 sums, rounded once to dtype
  * with u's columns 16 slots .. u_cols-1 set to zero and, when u_t is not null, u_t [16 slots,
- * >= M] = its transpose. xd and bits are host arrays of `slots` device pointers sharing
- * xd_row_stride / bits_row_stride. dtype QL_BF16 / QL_F16 for x, A, xd, u; 16-B aligned x, A
- * and xd rows (QL_EALIGN); 0 < p < 1 and a null pointer QL_EINVAL; shapes QL_ESHAPE. A
+ * >= M] = its transpose. xd (may be null: the dropped inputs are then not stored) and bits are
+ * host arrays of `slots` device pointers sharing xd_row_stride / bits_group_stride. dtype
+ * QL_BF16 / QL_F16 for x, A, xd, u; 16-B aligned x, A and xd rows (QL_EALIGN); 0 < p < 1 and a
+ * null pointer QL_EINVAL; shapes QL_ESHAPE. A
  * workspace of qlora_lora_dropout_down_workspace_size bytes (16-B aligned) lets the K range
  * split over workgroups (fp32 partials summed in split order); without it the call runs
  * unsplit, with the same xd and bits and u summed in another order.
@@ -277,7 +283,7 @@ int64_t qlora_lora_dropout_down_workspace_size(int64_t M, int64_t K, int slots);
 int qlora_lora_dropout_down(const void* x, int64_t x_row_stride, const void* A,
                             int64_t a_row_stride, int64_t M, int64_t K, int slots, int dtype,
                             const uint64_t* seeds, float p, float scale, void* const* xd,
-                            int64_t xd_row_stride, uint8_t* const* bits, int64_t bits_row_stride,
+                            int64_t xd_row_stride, uint8_t* const* bits, int64_t bits_group_stride,
                             void* u, int64_t u_row_stride, int u_cols, void* u_t,
                             int64_t u_t_row_stride, void* workspace, int64_t workspace_bytes,
                             ql_stream_t stream);
@@ -499,6 +505,26 @@ int64_t qlora_lora_wgrad_workspace_size(int64_t M, int64_t N, int slots);
 int qlora_lora_wgrad(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M, int64_t N,
                      int slots, int in_dtype, float* out, int out_transposed, float alpha,
                      void* workspace, int64_t workspace_bytes, ql_stream_t stream);
+
+/*
+ * The lora_A gradients of 1 <= slots <= 4 adapters whose inputs are their own dropout masks of
+ * one input Q [M, N] (N % 8 == 0), in one pass over Q:
+ *   out[16 g + c][n] = alpha * sum_m PT[16 g + c][m] * xd_g[m][n]     fp32 [16 slots, N]
+ *   xd_g[m][n] = keep_g(m, n) ? (Q[m][n] * scale rounded to dtype) : 0
+ * i.e. qlora_lora_wgrad (transposed output) over each adapter's dropped input as
+ * qlora_lora_dropout_scale_bits / qlora_lora_dropout_down form it, without storing it. bits: a
+ * host array of `slots` device pointers to keep bits in the layout of
+ * qlora_lora_dropout_scale_bits (8-B aligned; bits_group_stride >= N, a multiple of 8). PT, Q,
+ * dtype, alignment and the workspace (qlora_lora_wgrad_workspace_size) as qlora_lora_wgrad;
+ * the sums run in the same order, so each adapter's result equals qlora_lora_wgrad over its
+ * stored dropped input bit for bit.
+ * Replaces: the autograd of solution/lora.py:172 for lora_A (du^T xd) on DropoutCast's output
+ * (:84-93), for the adapters of a group at once.
+ */
+int qlora_lora_wgrad_masked(const void* PT, int64_t ldpt, const void* Q, int64_t ldq, int64_t M,
+                            int64_t N, int slots, int dtype, const uint8_t* const* bits,
+                            int64_t bits_group_stride, float scale, float* out, float alpha,
+                            void* workspace, int64_t workspace_bytes, ql_stream_t stream);
 
 /*
  * The lora_B weight gradients of `slots` = G adapters whose outputs are concatenated (the

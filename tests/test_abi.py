@@ -290,7 +290,7 @@ def test_dropout_down_rejects_bad_arguments(lib):
     def call(M=16, K=128, slots=1, p=0.05, ldx=128, u_cols=64, xd_rs=128):
         return lib.qlora_lora_dropout_down(fake, ldx, fake, 128, M, K, slots, 2, seeds, p,
                                            1.0 / (1.0 - p) if p < 1 else 1.0, ptrs, xd_rs, ptrs,
-                                           K // 8, fake, 64, u_cols, None, 0, None, 0, None)
+                                           K, fake, 64, u_cols, None, 0, None, 0, None)
 
     assert call(slots=0) == -1 and call(slots=5) == -1
     assert call(p=0.0) == -1 and call(p=1.0) == -1
@@ -298,3 +298,22 @@ def test_dropout_down_rejects_bad_arguments(lib):
     assert call(ldx=64) == -4 and call(u_cols=16 * 1 - 8) == -4
     assert call(ldx=132) == -3
     assert call(M=0) == 0
+
+
+@needs_no_device
+def test_wgrad_masked_rejects_bad_arguments(lib):
+    """qlora_lora_wgrad_masked: a null or misaligned keep-bit pointer, a group stride below N or
+    not a multiple of 8 are rejected before any launch."""
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    ok = (ctypes.c_void_p * 2)(0x1000, 0x2000)
+    bad = (ctypes.c_void_p * 2)(0x1000, 0x2004)
+    null = (ctypes.c_void_p * 2)(0x1000, 0)
+
+    def call(bits=ok, gs=512, N=512, slots=2):
+        return lib.qlora_lora_wgrad_masked(fake, 64, fake, 512, 64, N, slots, 2, bits, gs,
+                                           1.0 / 0.95, fake, 1.0, None, 0, None)
+
+    assert call(bits=null) == -1 and call(slots=5) == -1
+    assert call(bits=bad) == -3
+    assert call(gs=504) == -4 and call(gs=516) == -4 and call(N=500, gs=512) == -4

@@ -9,6 +9,8 @@ from hackathon_amd import lora, nf4, quant
 from oracle import nf4 as onf4
 from oracle import ops
 
+from _util import keep_blocks, keep_rows
+
 pytestmark = pytest.mark.gpu
 TABLE = np.array(quant.NF4_CODE, dtype=np.float32)
 
@@ -240,7 +242,8 @@ def test_dropout_bits_match_the_reference_mask():
     want = ops.dropout_scale(x, p, seed, 1 / (1 - p), torch.bfloat16)
     assert torch.equal(xd.cpu().view(torch.int16), want.view(torch.int16))
     keep = philox.keep_mask(seed, M, K, p)
-    assert np.array_equal(bits.cpu().numpy(), np.packbits(keep, axis=1, bitorder="little"))
+    assert bits.shape == ((M + 7) // 8, K)  # the 8 x 8 block layout
+    assert np.array_equal(keep_rows(bits, M), np.packbits(keep, axis=1, bitorder="little"))
 
 
 def test_lora_layer_dropout_takes_the_fused_path_vs_fp64(monkeypatch):
@@ -308,7 +311,7 @@ def test_up_masked_add_vs_fp64(M, K, dtype):
     du[:, :16] = (torch.randn(M, 16, generator=g) * 0.5).to(dtype)
     A = (torch.randn(16, K, generator=g) * 0.25).to(dtype)
     keep = torch.rand(M, K, generator=g) > 0.05
-    bits = torch.from_numpy(np.packbits(keep.numpy(), axis=1, bitorder="little"))
+    bits = keep_blocks(keep)
     scale = 1 / 0.95
     dxg, dug, Ag, bitsg = dx.cuda(), du.cuda(), A.cuda(), bits.cuda()
     _lib.call("qlora_lora_up_masked_add", dxg.data_ptr(), dxg.stride(0), dug.data_ptr(),
@@ -343,8 +346,7 @@ def test_up_masked_add_slots_vs_fp64(M, K, slots, dtype):
     du[:, :16 * slots] = (torch.randn(M, 16 * slots, generator=g) * 0.5).to(dtype)
     A = (torch.randn(16 * slots, K, generator=g) * 0.25).to(dtype)
     keeps = [torch.rand(M, K, generator=g) > 0.3 for _ in range(slots)]
-    bitss = [torch.from_numpy(np.packbits(k.numpy(), axis=1, bitorder="little")).cuda()
-             for k in keeps]
+    bitss = [keep_blocks(k).cuda() for k in keeps]
     p = 0.05
     scale = 1 / (1 - p)
     dxg = dx.cuda()
@@ -392,14 +394,14 @@ def test_dropout_down_vs_dropout_kernel_and_fp64(M, K, slots, dtype, p):
     xg = x.cuda()
     u = torch.full((M, 64), 3.0, dtype=dtype, device="cuda")
     ut = torch.full((16 * slots, M + 8), 5.0, dtype=dtype, device="cuda")[:, :M]
-    xds, bitss = lora.dropout_down(xg, a16.cuda(), p, seeds, u, ut)
+    xds, bitss = lora.dropout_down(xg, a16.cuda(), p, seeds, u, ut, keep_xd=True)
     for i in range(slots):
         xd_ref, bits_ref = lora.dropout_with_bits(xg, p, seeds[i])
         assert torch.equal(xds[i].view(torch.int16), xd_ref.view(torch.int16)), i
-        assert torch.equal(bitss[i], bits_ref), i
+        assert np.array_equal(keep_rows(bitss[i], M), keep_rows(bits_ref, M)), i
     if M * K <= 1 << 20:
         keep = philox.keep_mask(seeds[-1], M, K, p)
-        assert np.array_equal(bitss[-1].cpu().numpy(), np.packbits(keep, axis=1, bitorder="little"))
+        assert np.array_equal(keep_rows(bitss[-1], M), np.packbits(keep, axis=1, bitorder="little"))
     rnd = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11  # one rounding to the output
     for i in range(slots):
         xd = xds[i].cpu().double()
@@ -421,16 +423,52 @@ def test_dropout_down_vs_dropout_kernel_and_fp64(M, K, slots, dtype, p):
     _lib.call("qlora_lora_dropout_down", xg.data_ptr(), xg.stride(0), a16g.data_ptr(), K,
               M, K, slots, _lib.tag(dtype), (ctypes.c_uint64 * slots)(*seeds), p, 1.0 / (1.0 - p),
               (ctypes.c_void_p * slots)(*[t.data_ptr() for t in xd2]), K,
-              (ctypes.c_void_p * slots)(*[t.data_ptr() for t in bits2]), K // 8, u2.data_ptr(),
+              (ctypes.c_void_p * slots)(*[t.data_ptr() for t in bits2]), K, u2.data_ptr(),
               64, 64, None, 0, None, 0, _lib.stream_of(xg))
     assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(xd2, xds))
-    assert all(torch.equal(a, b) for a, b in zip(bits2, bitss))
+    assert all(np.array_equal(keep_rows(a, M), keep_rows(b, M)) for a, b in zip(bits2, bitss))
+    # without the dropped inputs: the same bits and u
+    u3 = torch.full((M, 64), 3.0, dtype=dtype, device="cuda")
+    none, bits3 = lora.dropout_down(xg, a16g, p, seeds, u3)
+    assert none is None and torch.equal(u3, u)
+    assert all(np.array_equal(keep_rows(a, M), keep_rows(b, M)) for a, b in zip(bits3, bitss))
     for i in range(slots):
         ref = xds[i].cpu().double() @ a16[16 * i:16 * i + 16].double().t()
         bound = (2 * 4 * 2.0**-22 * K * xds[i].abs().max().item() * a16.abs().max().item()
                  + rnd * ref.abs())
         assert torch.all((u2[:, 16 * i:16 * i + 16].cpu().double() - ref).abs() <= bound), i
     assert torch.all(u2[:, 16 * slots:] == 0)
+
+
+@pytest.mark.parametrize("M,N,slots,dtype", [
+    (4096, 3584, 3, torch.bfloat16),   # the q/k/v group's lora_A gradients
+    (4096, 3584, 2, torch.float16),    # gate/up in fp16
+    (4096, 18944, 1, torch.bfloat16),  # the down projection's
+    (1000, 3584, 2, torch.bfloat16),   # ragged splits
+    (37, 264, 4, torch.float16),       # a partial 32-row chunk, rows past M in a bit group
+])
+def test_lora_wgrad_masked_equals_wgrad_on_the_dropped_inputs(M, N, slots, dtype):
+    """qlora_lora_wgrad_masked: the lora_A gradients du_g^T xd_g of a group's adapters from x
+    and each adapter's keep bits, bit for bit qlora_lora_wgrad over each stored dropped input
+    (same sums in the same order), and within the fp32-sum bound of fp64."""
+    from hackathon_amd import gemm
+
+    print(f"lora_wgrad_masked M={M} N={N} slots={slots} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M + N + slots)
+    p = 0.05
+    x = torch.randn(M, N, generator=g).to(dtype).cuda()
+    seeds = [int(v) for v in torch.randint(0, 2**31 - 1, (slots,), generator=g)]
+    pt = gemm.lora_t_buffer(M, dtype, "cuda", rows=16 * slots)
+    pt.copy_((torch.randn(16 * slots, M, generator=g) * 0.5).to(dtype))
+    drops = [lora.dropout_with_bits(x, p, s) for s in seeds]
+    got = gemm.lora_wgrad_masked(pt, x, [b for _, b in drops], p)
+    assert got.shape == (16 * slots, N) and got.dtype == torch.float32
+    for i, (xd, _) in enumerate(drops):
+        want = gemm.lora_wgrad(pt[16 * i:16 * i + 16], xd, transposed=True)
+        assert torch.equal(got[16 * i:16 * i + 16], want), i
+        ref = pt[16 * i:16 * i + 16].double().cpu() @ xd.double().cpu()
+        bound = 4 * 2.0**-22 * M * pt.abs().max().item() * xd.abs().max().item()
+        assert torch.all((got[16 * i:16 * i + 16].double().cpu() - ref).abs() <= bound), i
 
 
 def test_torch_dropout_rng_keeps_the_unfused_path(monkeypatch):
