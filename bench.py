@@ -801,10 +801,12 @@ def bench_gemm_data(torch, res, reps=20, sets=3):
 
 
 def bench_dropout(torch, res, replays=10):
-    """LoRA dropout at the 7B step's shapes (4096 rows, p = 0.05, bf16): per adapter group, the
-    dropout kernel plus lora_down for each adapter, the dropout kernel alone, and the one-pass
-    qlora_lora_dropout_down (with its workspace, which splits long K, and without it). Rates are
-    Philox draws per second (one per input element and adapter)."""
+    """LoRA dropout at the 7B step's shapes (4096 rows, p = 0.05, bf16), per adapter group:
+    forward, the dropout kernel plus lora_down for each adapter, the dropout kernel alone, and
+    the one-pass qlora_lora_dropout_down with the dropped inputs stored and without them (bits
+    and u only, as the step runs it; also without its K split); backward, the lora_A gradients
+    as lora_wgrad over each stored dropped input against qlora_lora_wgrad_masked over x and the
+    bits. Forward rates are Philox draws per second (one per input element and adapter)."""
     import ctypes
 
     from hackathon_amd import _lib, gemm, lora
@@ -815,10 +817,10 @@ def bench_dropout(torch, res, replays=10):
         x = torch.randn(M, K, device="cuda", generator=g).to(dt)
         a16 = (0.1 * torch.randn(16 * G, K, device="cuda", generator=g)).to(dt)
         u = torch.empty(M, 64, device="cuda", dtype=dt)
-        ut = torch.empty(16 * G, M, device="cuda", dtype=dt)
+        ut = gemm.lora_t_buffer(M, dt, "cuda", rows=16 * G)
         seeds = [1234 + i for i in range(G)]
         xds = [torch.empty(M, K, device="cuda", dtype=dt) for _ in range(G)]
-        bitss = [torch.empty(M, K // 8, device="cuda", dtype=torch.uint8) for _ in range(G)]
+        bitss = [lora.keep_bits_buffer(M, K, "cuda") for _ in range(G)]
         sa = (ctypes.c_uint64 * G)(*seeds)
         xp = (ctypes.c_void_p * G)(*[t.data_ptr() for t in xds])
         bp = (ctypes.c_void_p * G)(*[t.data_ptr() for t in bitss])
@@ -828,26 +830,38 @@ def bench_dropout(torch, res, replays=10):
         def per_adapter(down=True):
             for i in range(G):
                 _lib.call("qlora_lora_dropout_scale_bits", x.data_ptr(), K, xds[i].data_ptr(), K,
-                          bitss[i].data_ptr(), K // 8, M, K, _lib.tag(dt), seeds[i], p,
-                          1 / (1 - p), _lib.stream_of(x))
+                          bitss[i].data_ptr(), K, M, K, _lib.tag(dt), seeds[i], p, 1 / (1 - p),
+                          _lib.stream_of(x))
                 if down:
                     gemm.lora_down(xds[i], a16[16 * i:16 * i + 16], u[:, 16 * i:],
                                    out_t=ut[16 * i:16 * i + 16])
 
-        def one_pass(w=ws, nb=ws_bytes):
+        def one_pass(xdp=xp, w=ws, nb=ws_bytes):
             _lib.call("qlora_lora_dropout_down", x.data_ptr(), K, a16.data_ptr(), K, M, K, G,
-                      _lib.tag(dt), sa, p, 1 / (1 - p), xp, K, bp, K // 8, u.data_ptr(), 64, 64,
-                      ut.data_ptr(), M, _lib.ptr(w), nb, _lib.stream_of(x))
+                      _lib.tag(dt), sa, p, 1 / (1 - p), xdp, K, bp, K, u.data_ptr(), 64, 64,
+                      ut.data_ptr(), ut.stride(0), _lib.ptr(w), nb, _lib.stream_of(x))
+
+        def wgrad_per_adapter():
+            for i in range(G):
+                gemm.lora_wgrad(ut[16 * i:16 * i + 16], xds[i], transposed=True)
+
+        def wgrad_masked():
+            gemm.lora_wgrad_masked(ut, x, bitss, p)
 
         draws = G * M * K
         entry = {}
         for name, fn in (("dropout_and_lora_down_per_adapter", per_adapter),
                          ("dropout_alone", lambda: per_adapter(False)),
-                         ("one_pass", one_pass),
-                         ("one_pass_unsplit", lambda: one_pass(None, 0))):
+                         ("one_pass_with_xd", one_pass),
+                         ("one_pass", lambda: one_pass(None)),
+                         ("one_pass_unsplit", lambda: one_pass(None, None, 0))):
             t = _graph_time([fn] * 4, torch, replays)
             entry[name] = dict(us=round(t * 1e6, 1), gdraws_per_s=round(draws / t / 1e9, 1))
         entry["splits"] = 1 if ws_bytes == 0 else ws_bytes // (M * 16 * G * 4)
+        per_adapter()  # the stored dropped inputs and bits for the gradient timings
+        for name, fn in (("lora_a_grad_per_adapter_on_xd", wgrad_per_adapter),
+                         ("lora_a_grad_masked", wgrad_masked)):
+            entry[name] = dict(us=round(_graph_time([fn] * 4, torch, replays) * 1e6, 1))
         res[f"dropout_down_{M}x{K}x{G}"] = entry
 
 

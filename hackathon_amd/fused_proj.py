@@ -22,13 +22,13 @@ element-wise adds becomes one fp32 accumulation.
 With LoRA dropout (p > 0, the same p on every projection of the group) each adapter draws its
 own mask of x from its own seed, as the layers one by one do (solution/lora.py:29-46,157-173):
 
-  forward   xd_g = x * keep_g / (1 - p)                      qlora_lora_dropout_scale_bits per
-                                                            adapter (keep_g also kept as bits)
-            u_g = xd_g A_g^T                                 qlora_lora_down per adapter
+  forward   keep_g as bits, u_g = xd_g A_g^T                 qlora_lora_dropout_down, every
+            (xd_g = x * keep_g / (1 - p), never stored)      adapter in one pass over x
             y = [x | u] [W_cat | sB_cat]^T + b               as above
   backward  dx = dY_cat W_cat + sum_g keep_g (du_g A_g)/(1-p)  the GEMM on the base term, then
                                                             qlora_lora_up_masked_add_slots
-            dA_g = du_g^T xd_g                              qlora_lora_wgrad per adapter
+            dA_g = du_g^T xd_g                              qlora_lora_wgrad_masked, every
+                                                            adapter in one pass over x
 
 and du_g, dB_g as above (neither depends on the mask). The attention group also applies RoPE (the q
 and k slices of the output feed the rotation kernel directly and its backward writes the
