@@ -863,6 +863,27 @@ def bench_dropout(torch, res, replays=10):
                          ("lora_a_grad_masked", wgrad_masked)):
             entry[name] = dict(us=round(_graph_time([fn] * 4, torch, replays) * 1e6, 1))
         res[f"dropout_down_{M}x{K}x{G}"] = entry
+    # the down adapter's dropout inside the SwiGLU forward (h, its keep bits and u) against the
+    # dropout-free kernel and against the SwiGLU kernel plus the one-pass dropout of h
+    from hackathon_amd import swiglu
+
+    M, n = 4096, 18944
+    gu = torch.randn(M, 2 * n, device="cuda", generator=g).to(dt)
+    a = (0.05 * torch.randn(16, n, device="cuda", generator=g)).to(dt)
+    h = torch.empty(M, n, device="cuda", dtype=dt)
+    u = torch.empty(M, 64, device="cuda", dtype=dt)
+    ut = gemm.lora_t_buffer(M, dt, "cuda")
+    entry = {}
+    for name, fn in (
+            ("swiglu_fwd_lora_down", lambda: swiglu.swiglu_fwd_lora_down(
+                gu[:, :n], gu[:, n:], h, a, u, ut)),
+            ("swiglu_fwd_lora_down_dropout", lambda: swiglu.swiglu_fwd_lora_down(
+                gu[:, :n], gu[:, n:], h, a, u, ut, p=p, seed=99)),
+            ("swiglu_rows_then_one_pass_dropout", lambda: (
+                swiglu.swiglu_rows(gu[:, :n], gu[:, n:], h),
+                lora.dropout_down(h, a, p, (99,), u, ut)))):
+        entry[name] = dict(us=round(_graph_time([fn] * 4, torch, replays) * 1e6, 1))
+    res[f"swiglu_down_dropout_{M}x{n}"] = entry
 
 
 WORKLOADS = {

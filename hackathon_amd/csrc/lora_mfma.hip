@@ -329,6 +329,17 @@ __global__ __launch_bounds__(256) void lora_down_reduce(const float* __restrict_
 // fewer, longer row pieces), 16-row tiles and a software-pipelined variant (the next tile's
 // loads issued before this tile's arithmetic) all measured 1-15% slower; the per-tile test
 // costs 3 us against the fast reciprocal without it.
+// LoRA dropout on h = silu(gate) up, the input of the down projection's adapter (its own seed):
+// the forward draws keep and stores it as bits, and its u products take the dropped values; the
+// backward's recomputed h for that adapter's lora_A gradient is dropped with the same bits.
+struct SwDrop {
+  uint64_t seed;
+  uint32_t thr;     // ql_philox::keep_threshold(p)
+  float scale;      // 1 / (1 - p)
+  uint8_t* bits;    // 8 x 8 blocks (ql_philox.h)
+  int64_t gs;       // their group stride
+};
+
 constexpr int kSwRows = 32;                 // rows per workgroup (two 16-row MFMA groups)
 constexpr int kSwK = 256;                   // k per tile
 constexpr int kSwLdsRow = 2 * kSwK + 16;    // bytes per LDS row
@@ -537,7 +548,7 @@ constexpr int kSlLdsRow = 2 * kSlCols + 16;          // bytes per LDS row (16 B 
 constexpr int kSlLdsArr = kSlRows * kSlLdsRow;       // one gradient's tile
 constexpr int kSlLdsBuf = 2 * kSlLdsArr;             // dgate + dup
 
-template <int IT, bool DA>
+template <int IT, bool DA, bool DROP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void swiglu_bwd_lora_kernel(
     const uint16_t* __restrict__ GR, int64_t ldgr, const uint16_t* __restrict__ GA,
     int64_t ldga, const uint16_t* __restrict__ UP, int64_t ldup, uint16_t* __restrict__ DG,
@@ -545,7 +556,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     const uint16_t* __restrict__ YU, int64_t ldy, const uint16_t* __restrict__ UTG,
     const uint16_t* __restrict__ UTU, int64_t ldut, int64_t M, int64_t K,
     int64_t rows_per_split, float* __restrict__ ws_du, float* __restrict__ ws_db,
-    const uint16_t* __restrict__ UTD, float* __restrict__ ws_da) {
+    const uint16_t* __restrict__ UTD, float* __restrict__ ws_da, SwDrop dr) {
+  static_assert(DA || !DROP, "the mask applies to the recomputed h of the lora_A gradient");
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
   constexpr int NA = DA ? 3 : 2;          // LDS arrays per tile: dgate, dup (, h)
   constexpr int NBUF = DA ? 1 : 2;        // tiles in LDS
@@ -612,6 +624,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     char* dgb = reinterpret_cast<char*>(DG + m0 * lddg);
     char* dub = reinterpret_cast<char*>(DU + m0 * lddu);
     uint4 vgr[4], vga[4], vup[4], uq[NA];
+    uint32_t kbyte[4];  // DROP: the keep byte of each of this thread's rows at columns kx ..
+    if constexpr (DROP) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int64_t rowc = m0 + lr + 8 * h < M ? m0 + lr + 8 * h : M - 1;
+        kbyte[h] = dr.bits[ql_philox::keep_byte(rowc, kx, dr.gs)];
+      }
+    }
 #pragma unroll
     for (int h = 0; h < 4; ++h) vga[h] = ld16(gab, oga[h]);
 #pragma unroll
@@ -664,8 +684,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
         if constexpr (DA) {
           float h8[8];
           ql_swiglu_fwd8_as<decltype(fast_tag)::value>(ga8, up8, h8);
-          *reinterpret_cast<uint4*>(lb + 2 * kSlLdsArr + lds_w + 8 * h * kSlLdsRow) =
-              Vec8<IT>::pack(h8);
+          uint4 ph = Vec8<IT>::pack(h8);
+          if constexpr (DROP) {  // the forward's dropped value of h, from its keep bits
+            float hv[8];
+            Vec8<IT>::unpack(ph, hv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = (kbyte[h] >> e) & 1u ? hv[e] * dr.scale : 0.0f;
+            ph = Vec8<IT>::pack(hv);
+          }
+          *reinterpret_cast<uint4*>(lb + 2 * kSlLdsArr + lds_w + 8 * h * kSlLdsRow) = ph;
         }
       }
     };
@@ -739,13 +766,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
 // a K range, one LDS copy of each tile, one barrier per tile), with two inputs, one output and
 // one product: wave w multiplies k groups 2w and 2w + 1 of both row groups by Y's fragments
 // (from L2, each serving both row groups), and the waves' sums meet in LDS at the end.
-template <int IT, bool PARTIAL>
+template <int IT, bool PARTIAL, bool DROP>
 __global__ __launch_bounds__(256) void swiglu_fwd_down_kernel(
     const uint16_t* __restrict__ GA, int64_t ldga, const uint16_t* __restrict__ UP,
     int64_t ldup, uint16_t* __restrict__ HH, int64_t ldh, const uint16_t* __restrict__ Y,
     int64_t ldy, int64_t M, int64_t K, int64_t k_per_split, float* __restrict__ ws,
     uint16_t* __restrict__ out, int64_t ldo, int out_cols, float alpha,
-    uint16_t* __restrict__ out_t, int64_t ldt) {
+    uint16_t* __restrict__ out_t, int64_t ldt, SwDrop dr) {
   constexpr int RG = kSwRows / 16;
   constexpr int H = kSwRows / 8;
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
@@ -762,10 +789,12 @@ __global__ __launch_bounds__(256) void swiglu_fwd_down_kernel(
   const char* upb = reinterpret_cast<const char*>(UP + m0 * ldup);
   char* hb = reinterpret_cast<char*>(HH + m0 * ldh);
   uint32_t oga[H], oup[H], oh[H];
+  int64_t rowc[H];  // the row each of this thread's rows works on (row M - 1 past M)
 #pragma unroll
   for (int h = 0; h < H; ++h) {
     const int64_t row = m0 + lr + 8 * h;
     const int64_t rs = (row < M ? row : M - 1) - m0;
+    rowc[h] = m0 + rs;
     oga[h] = (uint32_t)(rs * ldga * 2);
     oup[h] = (uint32_t)(rs * ldup * 2);
     oh[h] = (uint32_t)(rs * ldh * 2);
@@ -810,7 +839,23 @@ __global__ __launch_bounds__(256) void swiglu_fwd_down_kernel(
         const uint4 ph = Vec8<IT>::pack(h8);
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, ph),
                                     reinterpret_cast<u32x4v*>(hb + oh[h] + kxb));
-        *reinterpret_cast<uint4*>(lb + lds_w + 8 * h * kSwLdsRow) = ph;
+        uint4 pl = ph;  // what the products read
+        if constexpr (DROP) {  // the dropout kernels' test and value on the stored h
+          float hv[8], v[8];
+          Vec8<IT>::unpack(ph, hv);
+          const uint32_t base = (uint32_t)((uint64_t)rowc[h] * (uint64_t)K) + (uint32_t)kx;
+          uint32_t b = 0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const bool keep =
+                ql_philox::keep_word(ql_philox::philox_word0(base + e, dr.seed), dr.thr);
+            v[e] = keep ? hv[e] * dr.scale : 0.0f;
+            b |= (uint32_t)keep << e;
+          }
+          pl = Vec8<IT>::pack(v);
+          dr.bits[ql_philox::keep_byte(rowc[h], kx, dr.gs)] = (uint8_t)b;
+        }
+        *reinterpret_cast<uint4*>(lb + lds_w + 8 * h * kSwLdsRow) = pl;
       }
     };
     if (__builtin_expect(fast, 1)) rows(std::true_type{});
@@ -1715,6 +1760,18 @@ int ql_swiglu_bwd_down_splits(int64_t M, int64_t K) {
   return s;
 }
 
+// The forward with the down adapter's dropout draws one Philox word per element of h: its
+// rounds are a dependent chain per element, so it wants more waves than the one a SIMD that
+// 256 workgroups give. Split K until about four workgroups a CU (1024), keeping a tile per
+// split.
+int ql_swiglu_fwd_down_splits(int64_t M, int64_t K, bool drop) {
+  if (!drop) return ql_swiglu_bwd_down_splits(M, K);
+  const int64_t blocks = (M + kSwRows - 1) / kSwRows;
+  int s = 1;
+  while (blocks * s < 1024 && K / (kSwK * 2 * s) >= 1 && s < 64) s *= 2;
+  return s;
+}
+
 static bool rows16_ok(const void* p, int64_t ld) { return ql_aligned(p, 16) && ld % 8 == 0; }
 
 int ql_swiglu_bwd_down(int dtype, const void* GR, int64_t ldgr, const void* GA, int64_t ldga,
@@ -1793,9 +1850,11 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
                        float alpha_g, float alpha_u, float beta_g, float beta_u, void* out,
                        int64_t ldo, int out_cols, void* out_t, int64_t ldt, float* dbg,
                        float* dbu, const void* UTD, float beta_d, float* dad, float* ws,
-                       int64_t ws_floats, hipStream_t s) {
+                       int64_t ws_floats, hipStream_t s, const SwDrop* drop = nullptr) {
   constexpr int NC = 2 * kRank;
   const bool da = UTD != nullptr;
+  if (drop && !da) return QL_EINVAL;
+  const SwDrop dr = drop ? *drop : SwDrop{};
   if (M <= 0 || K <= 0 || K % 32 || out_cols < NC || ldo < out_cols) return QL_EINVAL;
   if (out_t && ldt < M) return QL_EINVAL;
   if (ldgr < K || ldga < K || ldup < K || lddg < K || lddu < K || ldy < K || ldut < M)
@@ -1825,20 +1884,27 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
   const dim3 grid((unsigned)blocks, (unsigned)splits);
 #define QL_SWL(IT)                                                                            \
   do {                                                                                        \
-    if (da)                                                                                   \
-      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, true>), grid, dim3(256), 0, s,           \
+    if (da && drop)                                                                           \
+      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, true, true>), grid, dim3(256), 0, s,     \
                          (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                \
                          (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU,       \
                          lddu, (const uint16_t*)YG, (const uint16_t*)YU, ldy,                 \
                          (const uint16_t*)UTG, (const uint16_t*)UTU, ldut, M, K, rps, ws_du,  \
-                         ws_db, (const uint16_t*)UTD, ws_da);                                 \
+                         ws_db, (const uint16_t*)UTD, ws_da, dr);                             \
+    else if (da)                                                                              \
+      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, true, false>), grid, dim3(256), 0, s,    \
+                         (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                \
+                         (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU,       \
+                         lddu, (const uint16_t*)YG, (const uint16_t*)YU, ldy,                 \
+                         (const uint16_t*)UTG, (const uint16_t*)UTU, ldut, M, K, rps, ws_du,  \
+                         ws_db, (const uint16_t*)UTD, ws_da, dr);                             \
     else                                                                                      \
-      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, false>), grid, dim3(256), 0, s,          \
+      hipLaunchKernelGGL((swiglu_bwd_lora_kernel<IT, false, false>), grid, dim3(256), 0, s,   \
                          (const uint16_t*)GR, ldgr, (const uint16_t*)GA, ldga,                \
                          (const uint16_t*)UP, ldup, (uint16_t*)DG, lddg, (uint16_t*)DU,       \
                          lddu, (const uint16_t*)YG, (const uint16_t*)YU, ldy,                 \
                          (const uint16_t*)UTG, (const uint16_t*)UTU, ldut, M, K, rps, ws_du,  \
-                         ws_db, (const uint16_t*)nullptr, (float*)nullptr);                   \
+                         ws_db, (const uint16_t*)nullptr, (float*)nullptr, dr);               \
     int st = ql_launch_status();                                                              \
     if (st != QL_OK) return st;                                                               \
     hipLaunchKernelGGL((lora_down_reduce<IT, IT>), dim3(grid1d(M * out_cols)), dim3(256), 0,  \
@@ -1868,8 +1934,10 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
 int ql_swiglu_fwd_down(int dtype, const void* GA, int64_t ldga, const void* UP, int64_t ldup,
                        void* HH, int64_t ldh, int64_t M, int64_t K, const void* Y, int64_t ldy,
                        float alpha, void* out, int64_t ldo, int out_cols, void* out_t,
-                       int64_t ldt, float* ws, int64_t ws_floats, hipStream_t s) {
+                       int64_t ldt, float* ws, int64_t ws_floats, hipStream_t s,
+                       const SwDrop* drop = nullptr) {
   if (M <= 0 || K <= 0 || K % 32 || out_cols < kRank || ldo < out_cols) return QL_EINVAL;
+  const SwDrop dr = drop ? *drop : SwDrop{};
   if (out_t && ldt < M) return QL_EINVAL;
   if (ldga < K || ldup < K || ldh < K || ldy < K) return QL_EINVAL;
   const int64_t lim = int64_t(1) << 31;
@@ -1879,23 +1947,28 @@ int ql_swiglu_fwd_down(int dtype, const void* GA, int64_t ldga, const void* UP, 
   if (!rows16_ok(GA, ldga) || !rows16_ok(UP, ldup) || !rows16_ok(HH, ldh) || !rows16_ok(Y, ldy))
     return QL_EALIGN;
   if (dtype != QL_BF16 && dtype != QL_F16) return QL_EDTYPE;
-  int splits = ql_swiglu_bwd_down_splits(M, K);
+  int splits = ql_swiglu_fwd_down_splits(M, K, drop != nullptr);
   if (ws_floats < (int64_t)splits * M * kRank || !ws) splits = 1;
   int64_t kps = ((K + splits - 1) / splits + kSwK - 1) / kSwK * kSwK;
   splits = (int)((K + kps - 1) / kps);
   const dim3 grid((unsigned)((M + kSwRows - 1) / kSwRows), (unsigned)splits);
-#define QL_SWF(IT)                                                                            \
+#define QL_SWF(IT)                  \
+  do {                              \
+    if (drop) QL_SWFD(IT, true);    \
+    else QL_SWFD(IT, false);        \
+  } while (0)
+#define QL_SWFD(IT, DR)                                                                       \
   do {                                                                                        \
     if (splits == 1) {                                                                        \
-      hipLaunchKernelGGL((swiglu_fwd_down_kernel<IT, false>), grid, dim3(256), 0, s,          \
+      hipLaunchKernelGGL((swiglu_fwd_down_kernel<IT, false, DR>), grid, dim3(256), 0, s,      \
                          (const uint16_t*)GA, ldga, (const uint16_t*)UP, ldup, (uint16_t*)HH, \
                          ldh, (const uint16_t*)Y, ldy, M, K, kps, (float*)nullptr,            \
-                         (uint16_t*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt);        \
+                         (uint16_t*)out, ldo, out_cols, alpha, (uint16_t*)out_t, ldt, dr);    \
     } else {                                                                                  \
-      hipLaunchKernelGGL((swiglu_fwd_down_kernel<IT, true>), grid, dim3(256), 0, s,           \
+      hipLaunchKernelGGL((swiglu_fwd_down_kernel<IT, true, DR>), grid, dim3(256), 0, s,       \
                          (const uint16_t*)GA, ldga, (const uint16_t*)UP, ldup, (uint16_t*)HH, \
                          ldh, (const uint16_t*)Y, ldy, M, K, kps, ws, (uint16_t*)out, ldo,    \
-                         out_cols, alpha, (uint16_t*)out_t, ldt);                             \
+                         out_cols, alpha, (uint16_t*)out_t, ldt, dr);                         \
       hipLaunchKernelGGL((lora_down_reduce<IT, IT>), dim3(grid1d(M * out_cols)), dim3(256),   \
                          0, s, ws, splits, M, kRank, (uint16_t*)out, ldo, out_cols, alpha,    \
                          alpha, (uint16_t*)out_t, ldt);                                       \
@@ -1904,6 +1977,7 @@ int ql_swiglu_fwd_down(int dtype, const void* GA, int64_t ldga, const void* UP, 
   if (dtype == QL_BF16) QL_SWF(QL_BF16);
   else QL_SWF(QL_F16);
 #undef QL_SWF
+#undef QL_SWFD
   return ql_launch_status();
 }
 
@@ -1941,6 +2015,77 @@ extern "C" int qlora_swiglu_bwd_lora_down(
                             static_cast<hipStream_t>(stream));
 }
 
+
+// The dropout arguments of the two entries below: 0 < p < 1, bits 8-B aligned, group stride a
+// multiple of 8 and >= cols.
+static int swiglu_drop_args(uint64_t seed, float p, float scale, void* bits, int64_t gs,
+                            int64_t cols, bool draw, SwDrop* out) {
+  if (!(p > 0.0f) || !(p < 1.0f) || !bits) return QL_EINVAL;
+  if (!ql_aligned(bits, 8)) return QL_EALIGN;
+  if (gs < cols || gs % 8) return QL_ESHAPE;
+  out->seed = seed;
+  out->thr = draw ? ql_philox::keep_threshold(p) : 0u;
+  out->scale = scale;
+  out->bits = static_cast<uint8_t*>(bits);
+  out->gs = gs;
+  return QL_OK;
+}
+
+extern "C" int qlora_swiglu_fwd_lora_down_dropout(
+    const void* gate, int64_t ldg, const void* up, int64_t ldu, void* h, int64_t ldh,
+    int64_t rows, int64_t cols, const void* a, int64_t lda, float alpha, int dtype, void* u,
+    int64_t ldo, int out_cols, void* u_t, int64_t ldt, uint64_t seed, float p, float scale,
+    uint8_t* bits, int64_t bits_group_stride, void* workspace, int64_t workspace_bytes,
+    ql_stream_t stream) {
+  if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
+  SwDrop dr{};
+  const int st = swiglu_drop_args(seed, p, scale, bits, bits_group_stride, cols, true, &dr);
+  if (st != QL_OK) return st;
+  if (rows == 0) return QL_OK;
+  if (!gate || !up || !h || !a || !u) return QL_EINVAL;
+  if (ql_spans_overlap(h, ldh, gate, ldg, rows, cols, 2) ||
+      ql_spans_overlap(h, ldh, up, ldu, rows, cols, 2))
+    return QL_EINVAL;
+  if (workspace && !ql_aligned(workspace, 16)) return QL_EALIGN;
+  if (!ql_aligned(u, 2) || (u_t && !ql_aligned(u_t, 2))) return QL_EALIGN;
+  return ql_swiglu_fwd_down(dtype, gate, ldg, up, ldu, h, ldh, rows, cols, a, lda, alpha, u, ldo,
+                            out_cols, u_t, ldt, static_cast<float*>(workspace),
+                            workspace_bytes / (int64_t)sizeof(float),
+                            static_cast<hipStream_t>(stream), &dr);
+}
+
+extern "C" int qlora_swiglu_bwd_lora_dropout(
+    const void* grad, int64_t ldgr, const void* gate, int64_t ldg, const void* up, int64_t ldu,
+    void* dgate, int64_t lddg, void* dup, int64_t lddu, int64_t rows, int64_t cols,
+    const void* bt_gate, const void* bt_up, int64_t ldbt, const void* ut_gate,
+    const void* ut_up, int64_t ldut, float alpha_gate, float alpha_up, float beta_gate,
+    float beta_up, int dtype, void* du, int64_t ldo, int out_cols, void* du_t, int64_t ldt,
+    float* db_gate, float* db_up, const void* ud_t, float beta_down, float* da_down,
+    const uint8_t* bits, int64_t bits_group_stride, float p, float scale, void* workspace,
+    int64_t workspace_bytes, ql_stream_t stream) {
+  if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
+  SwDrop dr{};
+  int st = swiglu_drop_args(0, p, scale, const_cast<uint8_t*>(bits), bits_group_stride, cols,
+                            false, &dr);
+  if (st != QL_OK) return st;
+  if (rows == 0) return QL_OK;
+  if (!grad || !gate || !up || !dgate || !dup || !bt_gate || !bt_up || !ut_gate || !ut_up ||
+      !du || !db_gate || !db_up || !workspace || !ud_t || !da_down)
+    return QL_EINVAL;
+  const void* ins[3] = {grad, gate, up};
+  const int64_t in_ld[3] = {ldgr, ldg, ldu};
+  for (int i = 0; i < 3; ++i)
+    if (ql_spans_overlap(dgate, lddg, ins[i], in_ld[i], rows, cols, 2) ||
+        ql_spans_overlap(dup, lddu, ins[i], in_ld[i], rows, cols, 2))
+      return QL_EINVAL;
+  if (!ql_aligned(du, 2) || (du_t && !ql_aligned(du_t, 2))) return QL_EALIGN;
+  return ql_swiglu_bwd_lora(dtype, grad, ldgr, gate, ldg, up, ldu, dgate, lddg, dup, lddu, rows,
+                            cols, bt_gate, bt_up, ldbt, ut_gate, ut_up, ldut, alpha_gate,
+                            alpha_up, beta_gate, beta_up, du, ldo, out_cols, du_t, ldt, db_gate,
+                            db_up, ud_t, beta_down, da_down, static_cast<float*>(workspace),
+                            workspace_bytes / (int64_t)sizeof(float),
+                            static_cast<hipStream_t>(stream), &dr);
+}
 
 extern "C" int64_t qlora_swiglu_bwd_lora_workspace_size(int64_t rows, int64_t cols,
                                                         int with_da) {
@@ -1980,7 +2125,10 @@ extern "C" int qlora_swiglu_bwd_lora(
 
 extern "C" int64_t qlora_swiglu_fwd_lora_down_workspace_size(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  const int s = ql_swiglu_bwd_down_splits(rows, cols);
+  // enough for either form (the dropout form splits further)
+  const int s0 = ql_swiglu_fwd_down_splits(rows, cols, false);
+  const int s1 = ql_swiglu_fwd_down_splits(rows, cols, true);
+  const int s = s0 > s1 ? s0 : s1;
   return s > 1 ? (int64_t)s * rows * kRank * (int64_t)sizeof(float) : 0;
 }
 

@@ -407,23 +407,34 @@ class LoraMLP(torch.autograd.Function):
                 and dA_d = du_d^T h                         recomputes h on chip for dA_d
                 dx, dA_gate, dA_up                          as GateUpSwiGLU
 
-    h is not kept for the backward: it is neither read back for u_d nor stored for dA_d."""
+    h is not kept for the backward: it is neither read back for u_d nor stored for dA_d.
+
+    With LoRA dropout (`seeds`: the gate, up and down adapters' seeds, None where that p is 0)
+    the gate/up group drops x per adapter as GateUpSwiGLU does, and the down adapter's input is
+    its own mask of h: the forward kernel draws it and keeps it as bits
+    (qlora_swiglu_fwd_lora_down_dropout, u_d from the dropped h), dh takes the adapter term
+    through qlora_lora_up_masked_add instead of the GEMM's second K segment, and the backward
+    kernel drops its recomputed h with the same bits for dA_d
+    (qlora_swiglu_bwd_lora_dropout)."""
 
     @staticmethod
-    def forward(ctx, x, specs, dspec, *ab):
+    def forward(ctx, x, specs, dspec, seeds, *ab):
         K = x.shape[-1]
         x2 = x.reshape(-1, K)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
         dt, dev = x2.dtype, x2.device
         M = x2.shape[0]
-        y, (at, bt, ut), _ = group_forward(x2, specs, ab[:4])  # dropout off (fused_mlp)
+        seeds = seeds or (None, None, None)
+        y, (at, bt, ut), drop = group_forward(x2, specs, ab[:4],
+                                              seeds[:2] if specs[0].p > 0 else None)
         n, N = specs[0].n, dspec.n
         a16_d, at_d, bs_d, bt_d = _gemm.lora_pack(ab[4], ab[5], dspec.scaling, dt, _PAD)
         h = torch.empty((M, n), dtype=dt, device=dev)
         u_d = torch.empty((M, _PAD), dtype=dt, device=dev)
         ut_d = _gemm.lora_t_buffer(M, dt, dev)
-        swiglu.swiglu_fwd_lora_down(y[:, :n], y[:, n:], h, a16_d, u_d, ut_d)
+        bits_d = swiglu.swiglu_fwd_lora_down(y[:, :n], y[:, n:], h, a16_d, u_d, ut_d,
+                                             p=dspec.p, seed=seeds[2] or 0)
         out = torch.empty((M, N), dtype=dt, device=dev)
         bias = None if dspec.bias is None else dspec.bias.to(dt)
         if nf4.use_fused_gemm(h, dspec.qs, dspec.packed, a2=u_d):  # W_d dequantised in-GEMM
@@ -433,19 +444,35 @@ class LoraMLP(torch.autograd.Function):
             _gemm.gemm_nt_cat(h, w, u_d, bs_d, out, bias=bias)
             del w
         del h, u_d
-        ctx.save_for_backward(x2, y, at, bt, ut, at_d, bt_d, ut_d)
+        saved = [x2, y, at, bt, ut, at_d, bt_d, ut_d]
+        ctx.drop_d = bits_d is not None
+        if ctx.drop_d:
+            saved += [a16_d, bits_d]
+        ctx.n_drop = 0 if drop is None else len(drop[2])
+        if drop is not None:
+            saved += [drop[1], *drop[2]]
+            ctx.p = drop[0]
+        ctx.save_for_backward(*saved)
         ctx.specs, ctx.dspec, ctx.shape = specs, dspec, x.shape
         ctx.ab_dtypes = [t.dtype for t in ab]
         return out.view(*x.shape[:-1], N)
 
     @staticmethod
     def backward(ctx, dout):
-        x2, y, at, bt, ut, at_d, bt_d, ut_d = ctx.saved_tensors
+        t = list(ctx.saved_tensors)
+        x2, y, at, bt, ut, at_d, bt_d, ut_d = t[:8]
+        t = t[8:]
+        a16_d = bits_d = None
+        if ctx.drop_d:
+            a16_d, bits_d = t[:2]
+            t = t[2:]
+        drop = None if ctx.n_drop == 0 else (ctx.p, t[0], t[1:1 + ctx.n_drop])
         specs, dspec = ctx.specs, ctx.dspec
         dt, dev = x2.dtype, x2.device
         M = x2.shape[0]
         n, N = specs[0].n, dspec.n
-        need = ctx.needs_input_grad  # x, specs, dspec, A_gate, B_gate, A_up, B_up, A_d, B_d
+        # x, specs, dspec, seeds, A_gate, B_gate, A_up, B_up, A_d, B_d
+        need = ctx.needs_input_grad
         dy = dout.reshape(M, N)
         if dy.dtype != dt:
             dy = dy.to(dt)
@@ -457,22 +484,27 @@ class LoraMLP(torch.autograd.Function):
         _gemm.lora_down(dy, bt_d, du_d, alpha=s_d, out_t=dut_d)  # du_d = s_d dY B_d
         wt = nf4.dequantize_nf4_t(dspec.packed, dspec.qs, dt)    # W_d^T [n, N]
         dh = torch.empty((M, n), dtype=dt, device=dev)
-        _gemm.gemm_nt_cat(dy, wt, du_d, at_d, dh)
+        if bits_d is None:
+            _gemm.gemm_nt_cat(dy, wt, du_d, at_d, dh)
+        else:  # the adapter term through its mask of h
+            _gemm.gemm_nt_cat(dy, wt, None, None, dh)
+            lora.up_masked_add(dh, du_d, a16_d, bits_d, dspec.p)
         del wt, du_d
-        db_d = _gemm.lora_wgrad(ut_d, dy, alpha=s_d) if need[8] else None
+        db_d = _gemm.lora_wgrad(ut_d, dy, alpha=s_d) if need[9] else None
         g = torch.empty((M, 2 * n), dtype=dt, device=dev)
         du = torch.empty((M, _PAD), dtype=dt, device=dev)
         dut = _t_buffer(32, M, dt, dev)
         gate_s, up_s = specs
         db_g, db_u, da_d = swiglu.swiglu_bwd_lora(
             dh, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:16, :n], bt[16:32, n:], ut[:16], ut[16:32],
-            gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du, dut, ud_t=dut_d)
+            gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du, dut, ud_t=dut_d,
+            bits_down=bits_d, p_down=dspec.p)
         del dh
-        dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[3:7],
-                                   du_dut=(du, dut), db_given=[db_g, db_u])
-        grads = grads + [da_d if need[7] else None, db_d]
-        grads = [None if gr is None else gr.to(t) for gr, t in zip(grads, ctx.ab_dtypes)]
-        return (None if dx is None else dx.view(ctx.shape)), None, None, *grads
+        dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[4:8],
+                                   du_dut=(du, dut), db_given=[db_g, db_u], drop=drop)
+        grads = grads + [da_d if need[8] else None, db_d]
+        grads = [None if gr is None else gr.to(t_) for gr, t_ in zip(grads, ctx.ab_dtypes)]
+        return (None if dx is None else dx.view(ctx.shape)), None, None, None, *grads
 
 
 def _group(layers, x):
@@ -559,11 +591,15 @@ def fused_mlp(module, x):
     n = specs[0].n
     if specs[1].n != n or n % 8:
         return None
-    down = lora_spec(module.down_proj, x) if n % 32 == 0 and specs[0].p == 0 else None
-    if down is not None and down[0].p == 0 and int(down[0].qs.shape[1]) == n:
+    down = lora_spec(module.down_proj, x) if n % 32 == 0 else None
+    if down is not None and int(down[0].qs.shape[1]) == n:
         dspec, a_d, b_d = down
-        return LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
-    # with dropout the down adapter's input is its own mask of h: down_proj runs as its layer
+        # the layers one by one draw their seeds in this order: gate, up, down
+        seeds = _seeds(specs) or (None, None)
+        seeds = seeds + ((lora._Seeds.next() if dspec.p > 0 else None),)
+        if all(s_ is None for s_ in seeds):
+            seeds = None
+        return LoraMLP.apply(x, tuple(specs), dspec, seeds, *ab, a_d, b_d)
     return module.down_proj(GateUpSwiGLU.apply(x, tuple(specs), _seeds(specs), *ab))
 
 

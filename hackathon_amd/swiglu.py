@@ -85,14 +85,16 @@ def swiglu_bwd_lora_down(grad, gate, up, dgate, dup, bt_gate, bt_up, alpha_gate,
 
 
 def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, alpha_gate,
-                    alpha_up, beta_gate, beta_up, du, du_t=None, ud_t=None, beta_down=1.0):
+                    alpha_up, beta_gate, beta_up, du, du_t=None, ud_t=None, beta_down=1.0,
+                    bits_down=None, p_down=0.0):
     """swiglu_bwd_lora_down plus both adapters' lora_B gradients in the same pass
     (qlora_swiglu_bwd_lora): returns fp32 (db_gate, db_up) [cols, 16] with
     db_gate = beta_gate dgate^T ut_gate^T and db_up = beta_up dup^T ut_up^T, where ut_* [16, rows]
     are the adapters' down-projections of the forward input, transposed. With `ud_t` (the du^T
     [16, rows] of the adapter of the layer that reads h = silu(gate) up) also that adapter's
     lora_A gradient da_down = beta_down ud_t h [16, cols], h recomputed on chip: returns
-    (db_gate, db_up, da_down)."""
+    (db_gate, db_up, da_down). With `bits_down` (swiglu_fwd_lora_down's keep bits for dropout
+    p_down) h in that product is the adapter's dropped input (qlora_swiglu_bwd_lora_dropout)."""
     _lib.require_rows(gate.dtype, grad=grad, gate=gate, up=up, dgate=dgate, dup=dup,
                       bt_gate=bt_gate, bt_up=bt_up, ut_gate=ut_gate, ut_up=ut_up, du=du,
                       du_t=du_t, ud_t=ud_t)
@@ -108,31 +110,49 @@ def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, 
     da_down = None if ud_t is None else torch.empty((16, cols), dtype=torch.float32, device=dev)
     ws, ws_bytes = _lib.workspace("qlora_swiglu_bwd_lora_workspace_size", rows, cols,
                                   int(ud_t is not None), device=dev)
-    _lib.call("qlora_swiglu_bwd_lora", grad.data_ptr(), grad.stride(0), gate.data_ptr(),
-              gate.stride(0), up.data_ptr(), up.stride(0), dgate.data_ptr(), dgate.stride(0),
-              dup.data_ptr(), dup.stride(0), rows, cols, bt_gate.data_ptr(), bt_up.data_ptr(),
-              bt_gate.stride(0), ut_gate.data_ptr(), ut_up.data_ptr(), ut_gate.stride(0),
-              float(alpha_gate), float(alpha_up), float(beta_gate), float(beta_up),
-              _lib.tag(gate.dtype), du.data_ptr(), du.stride(0), du.shape[1], _lib.ptr(du_t),
-              du_t.stride(0) if du_t is not None else 0, db_gate.data_ptr(), db_up.data_ptr(),
-              _lib.ptr(ud_t), float(beta_down), _lib.ptr(da_down), _lib.ptr(ws), ws_bytes,
-              _lib.stream_of(gate))
+    args = (grad.data_ptr(), grad.stride(0), gate.data_ptr(), gate.stride(0), up.data_ptr(),
+            up.stride(0), dgate.data_ptr(), dgate.stride(0), dup.data_ptr(), dup.stride(0), rows,
+            cols, bt_gate.data_ptr(), bt_up.data_ptr(), bt_gate.stride(0), ut_gate.data_ptr(),
+            ut_up.data_ptr(), ut_gate.stride(0), float(alpha_gate), float(alpha_up),
+            float(beta_gate), float(beta_up), _lib.tag(gate.dtype), du.data_ptr(), du.stride(0),
+            du.shape[1], _lib.ptr(du_t), du_t.stride(0) if du_t is not None else 0,
+            db_gate.data_ptr(), db_up.data_ptr(), _lib.ptr(ud_t), float(beta_down),
+            _lib.ptr(da_down))
+    if bits_down is None:
+        _lib.call("qlora_swiglu_bwd_lora", *args, _lib.ptr(ws), ws_bytes, _lib.stream_of(gate))
+    else:
+        _lib.call("qlora_swiglu_bwd_lora_dropout", *args, bits_down.data_ptr(),
+                  bits_down.stride(0), float(p_down), 1.0 / (1.0 - p_down), _lib.ptr(ws),
+                  ws_bytes, _lib.stream_of(gate))
     return (db_gate, db_up) if ud_t is None else (db_gate, db_up, da_down)
 
 
-def swiglu_fwd_lora_down(gate, up, h, a, u, u_t=None, alpha=1.0):
+def swiglu_fwd_lora_down(gate, up, h, a, u, u_t=None, alpha=1.0, p=0.0, seed=0):
     """h = silu(gate) * up (as swiglu_rows) and, in the same pass, the down-projection of h by
     the next layer's adapter: u[:, :16] = alpha h a^T for a [16, cols] (that adapter's A in the
-    compute dtype), u[:, 16:] = 0, u_t = u[:, :16]^T when given (qlora_swiglu_fwd_lora_down)."""
+    compute dtype), u[:, 16:] = 0, u_t = u[:, :16]^T when given (qlora_swiglu_fwd_lora_down).
+    With dropout p > 0 that adapter's input is its own mask of h (Philox seed `seed`): u is
+    taken on the dropped h and the keep bits are returned (lora.keep_bits_buffer's layout;
+    qlora_swiglu_fwd_lora_down_dropout), else None."""
+    from . import lora
+
     _lib.require_rows(gate.dtype, gate=gate, up=up, h=h, a=a, u=u, u_t=u_t)
     rows, cols = gate.shape
     ws, ws_bytes = _lib.workspace("qlora_swiglu_fwd_lora_down_workspace_size", rows, cols,
                                   device=gate.device)
-    _lib.call("qlora_swiglu_fwd_lora_down", gate.data_ptr(), gate.stride(0), up.data_ptr(),
-              up.stride(0), h.data_ptr(), h.stride(0), rows, cols, a.data_ptr(), a.stride(0),
-              float(alpha), _lib.tag(gate.dtype), u.data_ptr(), u.stride(0), u.shape[1],
-              _lib.ptr(u_t), u_t.stride(0) if u_t is not None else 0, _lib.ptr(ws), ws_bytes,
+    args = (gate.data_ptr(), gate.stride(0), up.data_ptr(), up.stride(0), h.data_ptr(),
+            h.stride(0), rows, cols, a.data_ptr(), a.stride(0), float(alpha), _lib.tag(gate.dtype),
+            u.data_ptr(), u.stride(0), u.shape[1], _lib.ptr(u_t),
+            u_t.stride(0) if u_t is not None else 0)
+    if p == 0:
+        _lib.call("qlora_swiglu_fwd_lora_down", *args, _lib.ptr(ws), ws_bytes,
+                  _lib.stream_of(gate))
+        return None
+    bits = lora.keep_bits_buffer(rows, cols, gate.device)
+    _lib.call("qlora_swiglu_fwd_lora_down_dropout", *args, int(seed) & 0xFFFF_FFFF_FFFF_FFFF,
+              float(p), 1.0 / (1.0 - p), bits.data_ptr(), bits.stride(0), _lib.ptr(ws), ws_bytes,
               _lib.stream_of(gate))
+    return bits
 
 
 def patch_qwen2_mlp():

@@ -620,6 +620,28 @@ int qlora_swiglu_bwd_lora(const void* grad, int64_t ldgr, const void* gate, int6
                           int64_t workspace_bytes, ql_stream_t stream);
 
 /*
+ * qlora_swiglu_bwd_lora with the down projection's adapter under LoRA dropout: ud_t and da_down
+ * are required, and h recomputed on chip is that adapter's dropped input, keep(m, k) * (h[m, k]
+ * * scale rounded to dtype), keep from the bits qlora_swiglu_fwd_lora_down_dropout stored
+ * (0 < p < 1; bits 8-B aligned, bits_group_stride >= cols and a multiple of 8):
+ *   da_down[c, k] = beta_down * sum_m ud_t[c, m] * keep(m, k) * (h[m, k] * scale)
+ * Replaces: as qlora_swiglu_bwd_lora, with the lora_A gradient of the down projection taken on
+ * DropoutCast's output (solution/lora.py:84-93,172).
+ */
+int qlora_swiglu_bwd_lora_dropout(const void* grad, int64_t ldgr, const void* gate, int64_t ldg,
+                                  const void* up, int64_t ldu, void* dgate, int64_t lddg,
+                                  void* dup, int64_t lddu, int64_t rows, int64_t cols,
+                                  const void* bt_gate, const void* bt_up, int64_t ldbt,
+                                  const void* ut_gate, const void* ut_up, int64_t ldut,
+                                  float alpha_gate, float alpha_up, float beta_gate,
+                                  float beta_up, int dtype, void* du, int64_t ldo, int out_cols,
+                                  void* du_t, int64_t ldt, float* db_gate, float* db_up,
+                                  const void* ud_t, float beta_down, float* da_down,
+                                  const uint8_t* bits, int64_t bits_group_stride, float p,
+                                  float scale, void* workspace, int64_t workspace_bytes,
+                                  ql_stream_t stream);
+
+/*
  * SwiGLU forward fused with the down-projection of its output by the adapter of the layer
  * that reads it (the down projection of a LoRA MLP):
  *   h = silu(gate) * up                  the bits of qlora_swiglu_fwd_rows (row-strided)
@@ -639,6 +661,25 @@ int qlora_swiglu_fwd_lora_down(const void* gate, int64_t ldg, const void* up, in
                                int64_t lda, float alpha, int dtype, void* u, int64_t ldo,
                                int out_cols, void* u_t, int64_t ldt, void* workspace,
                                int64_t workspace_bytes, ql_stream_t stream);
+
+/*
+ * The same with LoRA dropout on h for the down projection's adapter (seed, 0 < p < 1, scale =
+ * 1 / (1 - p); the workspace size query above covers this form): h is stored as above, the
+ * adapter's keep mask of it (the Philox test of
+ * qlora_lora_dropout_scale_bits at flat index m * cols + k) goes to bits in that entry's 8 x 8
+ * block layout (8-B aligned, bits_group_stride >= cols and a multiple of 8), and
+ *   u[m, c] = alpha * sum_k keep(m, k) * (h[m, k] * scale rounded to dtype) * a[c, k].
+ * Replaces: solution/swiglu.py:15-22 together with DropoutCast.forward (solution/lora.py:29-46,
+ * 84-89) on its output and lora_A of the down projection (:172).
+ */
+int qlora_swiglu_fwd_lora_down_dropout(const void* gate, int64_t ldg, const void* up,
+                                       int64_t ldu, void* h, int64_t ldh, int64_t rows,
+                                       int64_t cols, const void* a, int64_t lda, float alpha,
+                                       int dtype, void* u, int64_t ldo, int out_cols, void* u_t,
+                                       int64_t ldt, uint64_t seed, float p, float scale,
+                                       uint8_t* bits, int64_t bits_group_stride,
+                                       void* workspace, int64_t workspace_bytes,
+                                       ql_stream_t stream);
 
 /*
  * The compute-dtype operands of one rank-16 adapter, from its fp32 factors A [16, K] and

@@ -135,7 +135,7 @@ def test_lora_mlp_matches_separate_layers(seq):
 
     specs, ab = fused_proj._group(layers[:2], x)
     dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
-    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
     (out2.float() * w).sum().backward()
     assert out2.shape == ref.shape and _rel(out2, ref) < 4e-3
     got_g = [x.grad] + [p.grad for p in params]
@@ -155,11 +155,11 @@ def test_lora_mlp_partial_grads_and_no_grad():
     w = torch.randn(2, 64, 512, device="cuda", generator=g).to(torch.bfloat16)
     specs, ab = fused_proj._group((mlp.gate_proj, mlp.up_proj), x)
     dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
-    out = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+    out = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
     (out.float() * w).sum().backward()
     ref = [x.grad.clone()] + [t.grad.clone() for t in ab]
     with torch.no_grad():
-        out0 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+        out0 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
     assert torch.equal(out0, out)
     x.grad = None
     for t in ab:
@@ -168,7 +168,7 @@ def test_lora_mlp_partial_grads_and_no_grad():
     a_d.requires_grad_(False)
     b_d.requires_grad_(False)
     try:
-        out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, *ab, a_d, b_d)
+        out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
         (out2.float() * w).sum().backward()
         assert a_d.grad is None and b_d.grad is None
         got = [x.grad] + [t.grad for t in ab]
@@ -258,9 +258,50 @@ def test_gate_up_swiglu_with_dropout_matches_separate_layers(seq):
         assert _rel(a, b) < 1e-2, (name, _rel(a, b))
 
 
+@pytest.mark.parametrize("seq", [96, 37])
+def test_lora_mlp_with_dropout_matches_separate_layers(seq):
+    """LoRA dropout 0.05 on gate, up and down: the fused LoRA MLP (the down adapter's mask of h
+    drawn in the SwiGLU forward kernel, kept as bits, applied again to the recomputed h in the
+    backward kernel) against gate, up and down run one by one with the same seeds: output,
+    input gradient and all six adapter gradients, at the tolerances without dropout."""
+    print(f"fused LoRA MLP with dropout seq={seq}", flush=True)
+    cfg, model = _model(dropout=0.05)
+    mlp = model.model.layers[0].mlp
+    layers = (mlp.gate_proj, mlp.up_proj, mlp.down_proj)
+    params = _params(layers)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16).requires_grad_()
+    w = torch.randn(2, seq, 512, device="cuda", generator=g).to(torch.bfloat16)
+
+    _reseed(5)
+    out = mlp.down_proj(swiglu.swiglu(mlp.gate_proj(x), mlp.up_proj(x)))
+    (out.float() * w).sum().backward()
+    ref = out.detach().clone()
+    ref_g = [x.grad.clone()] + [p.grad.clone() for p in params]
+    _zero(params, x)
+
+    specs, ab = fused_proj._group(layers[:2], x)
+    dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
+    assert specs[0].p == dspec.p == 0.05
+    _reseed(5)
+    seeds = fused_proj._seeds(specs) + (lora._Seeds.next(),)
+    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, seeds, *ab, a_d, b_d)
+    (out2.float() * w).sum().backward()
+    assert out2.shape == ref.shape and _rel(out2, ref) < 4e-3
+    got_g = [x.grad] + [p.grad for p in params]
+    for name, a, b in zip(["x", "Ag", "Bg", "Au", "Bu", "Ad", "Bd"], got_g, ref_g):
+        assert _rel(a, b) < 1e-2, (name, _rel(a, b))
+    # another down seed drops other elements of h: the output moves
+    _reseed(5)
+    seeds = fused_proj._seeds(specs) + (lora._Seeds.next() + 1,)
+    with torch.no_grad():
+        out3 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, seeds, *ab, a_d, b_d)
+    assert _rel(out3, ref) > 1e-4
+
+
 def test_decoder_layer_with_dropout_takes_the_groups(monkeypatch):
-    """With dropout the patched layer runs q/k/v and gate/up as groups and the down projection
-    as its own layer (its input is its own mask of h), not the fused LoRA MLP."""
+    """With dropout the patched layer runs q/k/v as a group and the MLP as the fused LoRA MLP
+    (gate/up as a group, the down adapter's mask of h in the SwiGLU kernels)."""
     print("fused routing with dropout", flush=True)
     cfg, model = _model(dropout=0.05)
     hackathon_amd.apply()
@@ -278,7 +319,7 @@ def test_decoder_layer_with_dropout_takes_the_groups(monkeypatch):
     ids = torch.randint(0, 1000, (2, 64), device="cuda")
     out = model(input_ids=ids, labels=ids, use_cache=False)
     out.loss.backward()
-    assert calls == {"qkv": 1, "gate_up": 1, "mlp": 0}
+    assert calls == {"qkv": 1, "gate_up": 0, "mlp": 1}
     assert all(p.grad is not None and torch.isfinite(p.grad).all()
                for p in qlora_step.lora_parameters(model))
 
@@ -522,3 +563,69 @@ def test_swiglu_bwd_lora(rows, cols, dtype):
         assert torch.all((db2.double() - exact_b).abs() <= bound_b), q
     assert torch.all(du[:, 32:] == 0)
     assert torch.equal(dut, du[:, :32].t())
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(4096, 18944, torch.bfloat16),
+                                             (37, 1024, torch.bfloat16),
+                                             (1000, 2048, torch.float16),
+                                             (300, 4832, torch.bfloat16)])
+def test_swiglu_lora_dropout_kernels(rows, cols, dtype):
+    """LoRA dropout of the down adapter inside the SwiGLU kernels: the forward stores h with the
+    bits of qlora_swiglu_fwd_rows and keep bits equal to qlora_lora_dropout_scale_bits' on that
+    h for the same seed (the oracle's Philox mask on small inputs), u = alpha xd a^T on the dropped
+    h (within the fp32 bound of fp64); the backward gives the SwiGLU gradients, du and both dB of
+    the dropout-free call bit for bit and da = beta ud^T xd from the same bits (fp32 bound)."""
+    print(f"swiglu lora dropout {rows}x{cols} {dtype}", flush=True)
+    import numpy as np
+
+    from hackathon_amd import gemm
+    from oracle import philox
+    from _util import keep_rows
+
+    p, seed = 0.05, 987654321
+    g = torch.Generator(device="cuda").manual_seed(7 * rows + cols)
+    y = torch.randn(rows, 2 * cols, device="cuda", generator=g).to(dtype)
+    gate, up = y[:, :cols], y[:, cols:]
+    a = (torch.randn(16, cols, device="cuda", generator=g) * 0.05).to(dtype)
+    h = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    u = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
+    ut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=16)
+    bits = swiglu.swiglu_fwd_lora_down(gate, up, h, a, u, ut, alpha=0.75, p=p, seed=seed)
+    ref_h = torch.empty_like(h)
+    swiglu.swiglu_rows(gate, up, ref_h)
+    assert torch.equal(h, ref_h)
+    xd, ref_bits = lora.dropout_with_bits(ref_h, p, seed)
+    assert np.array_equal(keep_rows(bits, rows), keep_rows(ref_bits, rows))
+    if rows * cols <= 1 << 20:
+        keep = philox.keep_mask(seed, rows, cols, p)
+        assert np.array_equal(keep_rows(bits, rows), np.packbits(keep, axis=1, bitorder="little"))
+    xdd, ad = xd.double(), a.double()
+    exact = 0.75 * (xdd @ ad.t())
+    rnd = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    bound = 0.75 * 4 * 2.0**-22 * cols * xdd.abs().max() * ad.abs().max() + rnd * exact.abs()
+    assert torch.all((u[:, :16].double() - exact).abs() <= bound)
+    assert torch.all(u[:, 16:] == 0) and torch.equal(ut, u[:, :16].t())
+
+    dh = torch.randn(rows, cols, device="cuda", generator=g).to(dtype)
+    bt = (torch.randn(16, 2 * cols, device="cuda", generator=g) * 0.1).to(dtype)
+    utg = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+    utg.copy_(torch.randn(32, rows, device="cuda", generator=g).to(dtype))
+    udt = gemm.lora_t_buffer(rows, dtype, "cuda", rows=16)
+    udt.copy_(torch.randn(16, rows, device="cuda", generator=g).to(dtype))
+    outs = []
+    for drop in (False, True):
+        buf = torch.empty(rows, 2 * cols, dtype=dtype, device="cuda")
+        du = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
+        dut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+        res = swiglu.swiglu_bwd_lora(dh, gate, up, buf[:, :cols], buf[:, cols:], bt[:, :cols],
+                                     bt[:, cols:], utg[:16], utg[16:32], 2.0, 0.5, 2.0, 0.5, du,
+                                     dut, ud_t=udt, beta_down=1.5,
+                                     bits_down=bits if drop else None, p_down=p)
+        outs.append((buf, du, dut) + tuple(res))
+    (b0, du0, dut0, dbg0, dbu0, _), (b1, du1, dut1, dbg1, dbu1, da1) = outs
+    assert torch.equal(b0, b1) and torch.equal(du0, du1) and torch.equal(dut0, dut1)
+    assert torch.equal(dbg0, dbg1) and torch.equal(dbu0, dbu1)
+    udd = udt.double()
+    exact_a = 1.5 * (udd @ xdd)
+    bound_a = 1.5 * 4 * 2.0**-22 * rows * xdd.abs().max() * udd.abs().max()
+    assert da1.shape == (16, cols) and torch.all((da1.double() - exact_a).abs() <= bound_a)
