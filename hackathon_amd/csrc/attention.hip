@@ -458,8 +458,11 @@ struct BwdShape {
 //   S = Q K^T, dP = dO V^T      Q, dO row fragments from LDS; K, V fragments in registers
 //   P = exp2(S scale log2e - lse log2e), dS = P (dP - Delta)
 //   dV^T += dO^T P, dK^T += Q^T dS    dO^T, Q^T by transposing reads; P, dS from registers
-// With several query heads per kv head, each head's dK, dV go to fp32 partials that
-// attn_bwd_reduce sums in head order; otherwise the kernel writes the 16-bit gradients itself.
+// With several query heads per kv head, each head's dK, dV go to partials in the input type
+// that attn_bwd_reduce sums in fp32 in head order; otherwise the kernel writes the 16-bit
+// gradients itself. (The reference's grouped-query path rounds each repeated head's gradient
+// to the input type too before the repeat's backward sums them: 16-bit partials add no rounding
+// it does not have, and halve the partials' traffic against fp32 ones.)
 constexpr int kBwdStage = 2 * kTileBytes + 512;  // Q tile, dO tile, lse2 [64], delta [64]
 
 template <int DT>
@@ -552,7 +555,8 @@ void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
                    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
                    const float* __restrict__ lse, const float* __restrict__ delta,
                    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
-                   float* __restrict__ pk, float* __restrict__ pv, BwdShape sh, int n_kblocks) {
+                   uint16_t* __restrict__ pk, uint16_t* __restrict__ pv, BwdShape sh,
+                   int n_kblocks) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kBwdStage];
   QL_DMA_BEGIN();
   const int64_t BH = sh.B * sh.HQ;
@@ -632,8 +636,9 @@ void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
     const int d = 16 * dt + 4 * fq;
     if (pk) {
       const int64_t row = (bh * S + key) * HD + d;
-      *reinterpret_cast<f32x4_t*>(pv + row) = v;
-      *reinterpret_cast<f32x4_t*>(pk + row) = k4;
+      *reinterpret_cast<uint2*>(pv + row) = make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
+      *reinterpret_cast<uint2*>(pk + row) =
+          make_uint2(pack2<DT>(k4[0], k4[1]), pack2<DT>(k4[2], k4[3]));
     } else {
       uint16_t* dvp = dV + b * sh.dk_b + hk * sh.dk_h + key * sh.dk_s + d;
       uint16_t* dkp = dK + b * sh.dk_b + hk * sh.dk_h + key * sh.dk_s + d;
@@ -643,10 +648,11 @@ void attn_bwd_dkdv(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
   }
 }
 
-// dK[b, s, hk] = sum_g pk[b, hk G + g, s], dV likewise, in head order (one thread per 8 d).
+// dK[b, s, hk] = sum_g pk[b, hk G + g, s], dV likewise, in fp32 in head order (one thread per
+// 8 d).
 template <int DT>
-__global__ __launch_bounds__(256) void attn_bwd_reduce(const float* __restrict__ pk,
-                                                        const float* __restrict__ pv,
+__global__ __launch_bounds__(256) void attn_bwd_reduce(const uint16_t* __restrict__ pk,
+                                                        const uint16_t* __restrict__ pv,
                                                         uint16_t* __restrict__ dK,
                                                         uint16_t* __restrict__ dV, BwdShape sh) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -660,14 +666,14 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce(const float* __restrict__
   float ak[8] = {}, av[8] = {};
   for (int64_t g = 0; g < G; ++g) {
     const int64_t off = ((b * sh.HQ + hk * G + g) * sh.S + s) * HD + 8 * part;
-    const float4 k0 = *reinterpret_cast<const float4*>(pk + off);
-    const float4 k1 = *reinterpret_cast<const float4*>(pk + off + 4);
-    const float4 v0 = *reinterpret_cast<const float4*>(pv + off);
-    const float4 v1 = *reinterpret_cast<const float4*>(pv + off + 4);
-    ak[0] += k0.x; ak[1] += k0.y; ak[2] += k0.z; ak[3] += k0.w;
-    ak[4] += k1.x; ak[5] += k1.y; ak[6] += k1.z; ak[7] += k1.w;
-    av[0] += v0.x; av[1] += v0.y; av[2] += v0.z; av[3] += v0.w;
-    av[4] += v1.x; av[5] += v1.y; av[6] += v1.z; av[7] += v1.w;
+    float k8[8], v8[8];
+    Vec8<DT>::load(pk + off, k8);
+    Vec8<DT>::load(pv + off, v8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ak[j] += k8[j];
+      av[j] += v8[j];
+    }
   }
   const int64_t o = b * sh.dk_b + hk * sh.dk_h + s * sh.dk_s + 8 * part;
   Vec8<DT>::store(dK + o, ak);
@@ -916,7 +922,7 @@ extern "C" int qlora_attn_fwd(const void* q, const void* k, const void* v, void*
 extern "C" int64_t qlora_attn_bwd_workspace_size(int64_t B, int64_t HQ, int64_t HK, int64_t S) {
   if (B <= 0 || HQ <= 0 || HK <= 0 || S <= 0 || HQ % HK) return 0;
   int64_t bytes = align256(B * HQ * S * (int64_t)sizeof(float));   // Delta
-  if (HQ != HK) bytes += 2 * align256(B * HQ * S * HD * (int64_t)sizeof(float));  // partials
+  if (HQ != HK) bytes += 2 * align256(B * HQ * S * HD * (int64_t)sizeof(uint16_t));  // partials
   return bytes;
 }
 
@@ -956,12 +962,12 @@ extern "C" int qlora_attn_bwd(const void* q, const void* k, const void* v, const
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   float* delta = reinterpret_cast<float*>(ws);
-  float* pk = nullptr;
-  float* pv = nullptr;
+  uint16_t* pk = nullptr;
+  uint16_t* pv = nullptr;
   if (HQ != HK) {
-    const int64_t part_bytes = align256(B * HQ * S * HD * (int64_t)sizeof(float));
-    pk = reinterpret_cast<float*>(ws + align256(B * HQ * S * (int64_t)sizeof(float)));
-    pv = reinterpret_cast<float*>(reinterpret_cast<char*>(pk) + part_bytes);
+    const int64_t part_bytes = align256(B * HQ * S * HD * (int64_t)sizeof(uint16_t));
+    pk = reinterpret_cast<uint16_t*>(ws + align256(B * HQ * S * (int64_t)sizeof(float)));
+    pv = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(pk) + part_bytes);
   }
   const int n_kblocks = (int)((S + kRows - 1) / kRows);
   const int n_qblocks = (int)((S + BQ - 1) / BQ);
