@@ -1173,11 +1173,9 @@ __global__ __launch_bounds__(kThreads) void lora_wgrad_kernel(
 // 64 float4 outputs per workgroup: wave w sums splits [w S / 4, (w + 1) S / 4) in split order
 // (all of its loads for an output in flight together, 4 at a time), and wave 0 adds the other
 // waves' sums in wave order, so the result does not depend on the launch shape.
-__global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
-                                                         int64_t N, int nc,
-                                                         float* __restrict__ out, float alpha,
-                                                         bool out_t) {
-  __shared__ float4 part[3][64];
+QL_DEV void wgrad_reduce_body(const float* __restrict__ ws, int splits, int64_t N, int nc,
+                              float* __restrict__ out, float alpha, bool out_t,
+                              float4 (*__restrict__ part)[64]) {
   const int64_t total4 = N * nc / 4;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int z0 = splits * w / 4, z1 = splits * (w + 1) / 4;
@@ -1215,6 +1213,31 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(256) void lora_wgrad_reduce(const float* __restrict__ ws, int splits,
+                                                         int64_t N, int nc,
+                                                         float* __restrict__ out, float alpha,
+                                                         bool out_t) {
+  __shared__ float4 part[3][64];
+  wgrad_reduce_body(ws, splits, N, nc, out, alpha, out_t, part);
+}
+
+// Up to three such reductions of one shape in one launch (blockIdx.y picks the product), each
+// summed exactly as lora_wgrad_reduce sums it: the weight gradients one fused kernel leaves as
+// partials (the SwiGLU backward's two lora_B and one lora_A), without a launch each.
+struct WgradReduceSet {
+  const float* ws[3];
+  float* out[3];
+  float alpha[3];
+  bool out_t[3];
+};
+
+__global__ __launch_bounds__(256) void lora_wgrad_reduce_set(WgradReduceSet set, int splits,
+                                                             int64_t N, int nc) {
+  __shared__ float4 part[3][64];
+  const int q = blockIdx.y;
+  wgrad_reduce_body(set.ws[q], splits, N, nc, set.out[q], set.alpha[q], set.out_t[q], part);
 }
 
 // The diagonal blocks of a multi-slot weight gradient: out[n, c] = alpha_q * sum over splits
@@ -1916,17 +1939,20 @@ int ql_swiglu_bwd_lora(int dtype, const void* GR, int64_t ldgr, const void* GA, 
 #undef QL_SWL
   int st = ql_launch_status();
   if (st != QL_OK) return st;
-  hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s, ws_db,
-                     splits, K, kRank, dbg, beta_g, false);
-  st = ql_launch_status();
-  if (st != QL_OK) return st;
-  hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s,
-                     ws_db + (int64_t)splits * K * kRank, splits, K, kRank, dbu, beta_u, false);
-  if (!da) return ql_launch_status();
-  st = ql_launch_status();
-  if (st != QL_OK) return st;
-  hipLaunchKernelGGL(lora_wgrad_reduce, dim3(grid64(K * kRank / 4)), dim3(256), 0, s, ws_da,
-                     splits, K, kRank, dad, beta_d, true);  // [16, K]: A's layout
+  // dB_gate, dB_up (and dA_down, [16, K]: A's layout) in one launch
+  WgradReduceSet set{};
+  set.ws[0] = ws_db;
+  set.out[0] = dbg;
+  set.alpha[0] = beta_g;
+  set.ws[1] = ws_db + (int64_t)splits * K * kRank;
+  set.out[1] = dbu;
+  set.alpha[1] = beta_u;
+  set.ws[2] = ws_da;
+  set.out[2] = dad;
+  set.alpha[2] = beta_d;
+  set.out_t[2] = true;
+  hipLaunchKernelGGL(lora_wgrad_reduce_set, dim3(grid64(K * kRank / 4), da ? 3 : 2), dim3(256),
+                     0, s, set, splits, K, kRank);
   return ql_launch_status();
 }
 
