@@ -1091,6 +1091,30 @@ def _short_kernel(name, width=64):
     return name if len(name) <= width else name[: width - 3] + "..."
 
 
+def pmc_summary(counter_csv):
+    """Per kernel of a rocprofv3 --pmc counter_collection.csv: dispatches and, for each counter,
+    the mean over dispatches of its value (summed over the counter's hardware instances by
+    rocprofv3), as a markdown table."""
+    import collections
+    import csv
+
+    sums = collections.defaultdict(lambda: collections.defaultdict(float))
+    dispatches = collections.defaultdict(set)
+    counters = set()
+    for r in csv.DictReader(open(counter_csv)):
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "")
+        name = name.split("(")[0][:48]
+        sums[name][r["Counter_Name"]] += float(r["Counter_Value"])
+        dispatches[name].add(r["Dispatch_Id"])
+        counters.add(r["Counter_Name"])
+    cols = sorted(counters)
+    print("| kernel | dispatches | " + " | ".join(cols) + " |")
+    print("|---|---|" + "---|" * len(cols))
+    for name in sorted(sums):
+        n = len(dispatches[name])
+        print(f"| `{name}` | {n} | " + " | ".join(f"{sums[name][c] / n:.4g}" for c in cols) + " |")
+
+
 def profile_summary(trace_csv, fetch_csv=None, write_csv=None, copy_mib=256):
     """Markdown table of a rocprofv3 run: per (kernel, grid size) the dispatch count and the
     average / min / max duration from the kernel trace; with the two PMC passes of the same
@@ -1184,7 +1208,13 @@ def main():
                     help="per-kernel table from a rocprofv3 kernel_trace.csv, optionally followed "
                          "by FETCH_SIZE and WRITE_SIZE counter_collection.csv files of the same "
                          "command (calibrated by its copy kernel); prints markdown and exits")
+    ap.add_argument("--pmc-summary", metavar="CSV",
+                    help="per-kernel mean of every counter in a rocprofv3 --pmc "
+                         "counter_collection.csv; prints markdown and exits")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.trace_summary:
         trace_summary(args.trace_summary)
         return
