@@ -131,6 +131,8 @@ _SIGNATURES = {
                        _c_i64p, _c_i64p, _c_i64p, _c_f32, _c_ptr, _c_i64, _c_ptr],
     "qlora_ce_rows": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                       _c_ptr, _c_int, _c_int, _c_f32, _c_ptr],
+    "qlora_ce_rows_scale_ptr": [_c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr,
+                                _c_ptr, _c_ptr, _c_int, _c_int, _c_ptr, _c_ptr],
 }
 
 # name -> argtypes; these return a byte count (int64)

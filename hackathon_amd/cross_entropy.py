@@ -40,6 +40,19 @@ MATMUL_DTYPES = (torch.float16, torch.bfloat16)
 entropy_from_logits = head_hooks.entropy_from_logits
 
 
+def _grad_scale(denominator, device):
+    """GRAD_GAIN / denominator, or 0 for a zero denominator, as the fp32 scale of dz
+    (solution/cross_entropy.py:105-106 forms it on the host from float(denominator)). A
+    denominator held on the GPU (the labelled-token count) stays there: the quotient is taken
+    in fp64 on the device and rounded to fp32 once, the value the host would pass, without
+    the host waiting for the forward to finish."""
+    if torch.is_tensor(denominator) and denominator.device == device and device.type == "cuda":
+        d = denominator.detach().reshape(()).to(torch.float64)
+        return torch.where(d != 0, GRAD_GAIN / d, torch.zeros_like(d)).to(torch.float32).reshape(1)
+    divisor = float(denominator)
+    return GRAD_GAIN / divisor if divisor else 0.0
+
+
 class FusedLinearCrossEntropy(torch.autograd.Function):
     """loss = sum over rows of CE(hidden @ W.T, target) / denominator, with per-token loss,
     entropy and argmax, never holding more than one group of rows' logits
@@ -57,7 +70,7 @@ class FusedLinearCrossEntropy(torch.autograd.Function):
         n = flat.shape[0]
         labels = target.reshape(-1).to(device=hidden.device, dtype=torch.int64).contiguous()
         rows = vocab_pass.RowResults(n, hidden.device, pred=True)
-        divisor = float(denominator)
+        grad_scale = _grad_scale(denominator, hidden.device)
         grad = None
         if ctx.needs_input_grad[0]:
             grad = torch.empty((n, width), dtype=torch.float32, device=hidden.device)
@@ -66,7 +79,7 @@ class FusedLinearCrossEntropy(torch.autograd.Function):
                            _gemm.frozen_as(weight, matmul_dtype), labels, rows,
                            ignore_mode=vocab_pass.IGNORE_MINUS_100, chunk_rows=chunk_rows,
                            grad=grad, grad_rows=n if grad is not None else 0,
-                           grad_scale=GRAD_GAIN / divisor if divisor else 0.0)
+                           grad_scale=grad_scale)
         ctx.save_for_backward(grad)
         ctx.lead, ctx.dtype = lead, hidden.dtype
         ctx.mark_non_differentiable(rows.loss, rows.entropy, rows.pred)

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     typename Elem<DT>::T* __restrict__ logits, int64_t row_stride, int64_t V,
     const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ entropy,
     int32_t* __restrict__ correct, int64_t* __restrict__ pred, int ignore_mode, int write_grad,
-    float grad_scale) {
+    float grad_scale, const float* __restrict__ grad_scale_dev) {
   extern __shared__ uint4 cache[];  // kCacheBytes when VW == 8
   __shared__ RowStat part[kWaves];
   __shared__ float lse_sh;
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   if (!write_grad) return;
   __syncthreads();
   const float lse = lse_sh;
-  const float gs = labelled ? grad_scale : 0.f;
+  const float gs = labelled ? (grad_scale_dev ? *grad_scale_dev : grad_scale) : 0.f;
   auto emit = [&](float* v, int64_t c) {
 #pragma unroll
     for (int j = 0; j < VW; ++j) {
@@ -185,27 +185,25 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
 template <int DT>
 int launch_ce(void* logits, int64_t rs, int64_t n_rows, int64_t V, const int64_t* target,
               float* loss, float* entropy, int32_t* correct, int64_t* pred, int ignore_mode,
-              int write_grad, float grad_scale, hipStream_t s) {
+              int write_grad, float grad_scale, const float* grad_scale_dev, hipStream_t s) {
   using T = typename Elem<DT>::T;
   const bool vec = (V % 8) == 0 && ql_aligned(logits, 16) && ((rs * ql_elem_size(DT)) % 16) == 0;
   if (vec)
     hipLaunchKernelGGL((ce_rows_kernel<DT, 8>), dim3((unsigned)n_rows), dim3(kThreads),
                        DT == QL_F32 ? 0 : kCacheBytes, s,
                        (T*)logits, rs, V, target, loss, entropy, correct, pred, ignore_mode,
-                       write_grad, grad_scale);
+                       write_grad, grad_scale, grad_scale_dev);
   else
     hipLaunchKernelGGL((ce_rows_kernel<DT, 1>), dim3((unsigned)n_rows), dim3(kThreads), 0, s,
                        (T*)logits, rs, V, target, loss, entropy, correct, pred, ignore_mode,
-                       write_grad, grad_scale);
+                       write_grad, grad_scale, grad_scale_dev);
   return ql_launch_status();
 }
 
-}  // namespace
-
-extern "C" int qlora_ce_rows(void* logits, int logits_dtype, int64_t row_stride, int64_t n_rows,
-                             int64_t vocab, const int64_t* target, float* loss, float* entropy,
-                             int32_t* correct, int64_t* pred, int ignore_mode, int write_grad,
-                             float grad_scale, ql_stream_t stream) {
+int ce_rows(void* logits, int logits_dtype, int64_t row_stride, int64_t n_rows, int64_t vocab,
+            const int64_t* target, float* loss, float* entropy, int32_t* correct, int64_t* pred,
+            int ignore_mode, int write_grad, float grad_scale, const float* grad_scale_dev,
+            ql_stream_t stream) {
   if (n_rows < 0 || vocab <= 0 || n_rows > UINT32_MAX) return QL_EINVAL;
   if (ignore_mode != 0 && ignore_mode != 1) return QL_EINVAL;
   if (!ql_valid_dtype(logits_dtype)) return QL_EDTYPE;
@@ -214,6 +212,26 @@ extern "C" int qlora_ce_rows(void* logits, int logits_dtype, int64_t row_stride,
   QL_DISPATCH_DTYPE(logits_dtype, DT,
                     return launch_ce<DT>(logits, row_stride, n_rows, vocab, target, loss, entropy,
                                          correct, pred, ignore_mode, write_grad, grad_scale,
-                                         static_cast<hipStream_t>(stream)));
+                                         grad_scale_dev, static_cast<hipStream_t>(stream)));
   return QL_EDTYPE;
+}
+
+}  // namespace
+
+extern "C" int qlora_ce_rows(void* logits, int logits_dtype, int64_t row_stride, int64_t n_rows,
+                             int64_t vocab, const int64_t* target, float* loss, float* entropy,
+                             int32_t* correct, int64_t* pred, int ignore_mode, int write_grad,
+                             float grad_scale, ql_stream_t stream) {
+  return ce_rows(logits, logits_dtype, row_stride, n_rows, vocab, target, loss, entropy, correct,
+                 pred, ignore_mode, write_grad, grad_scale, nullptr, stream);
+}
+
+extern "C" int qlora_ce_rows_scale_ptr(void* logits, int logits_dtype, int64_t row_stride,
+                                       int64_t n_rows, int64_t vocab, const int64_t* target,
+                                       float* loss, float* entropy, int32_t* correct,
+                                       int64_t* pred, int ignore_mode, int write_grad,
+                                       const float* grad_scale, ql_stream_t stream) {
+  if (write_grad && !grad_scale) return QL_EINVAL;
+  return ce_rows(logits, logits_dtype, row_stride, n_rows, vocab, target, loss, entropy, correct,
+                 pred, ignore_mode, write_grad, 0.f, write_grad ? grad_scale : nullptr, stream);
 }

@@ -102,11 +102,22 @@ def plan_groups(n_rows, vocab, chunk_rows, elem_bytes=2, budget=LOGITS_BUDGET):
 def row_statistics(logits, target, out, start, ignore_mode, write_grad, grad_scale):
     """qlora_ce_rows over one group's logits [rows, vocab] (16-bit or fp32, unit stride along
     the vocabulary), filling rows start.. of `out`; with write_grad the logits become
-    dz = (softmax - onehot) * (labelled ? grad_scale : 0) in place."""
+    dz = (softmax - onehot) * (labelled ? grad_scale : 0) in place. `grad_scale` is a number,
+    or a one-element fp32 tensor on the device that the kernel reads there
+    (qlora_ce_rows_scale_ptr), so a scale formed on the GPU costs the host no wait."""
     rows, vocab = logits.shape
     if rows == 0:
         return
     loss, entropy, correct, pred = out.pointers(start)
+    if torch.is_tensor(grad_scale):
+        if (grad_scale.dtype != torch.float32 or grad_scale.numel() != 1
+                or grad_scale.device != logits.device):
+            raise ValueError("a tensor grad_scale must be one fp32 value on the logits' device")
+        _lib.call("qlora_ce_rows_scale_ptr", logits.data_ptr(), _lib.tag(logits.dtype),
+                  logits.stride(0), rows, vocab, target.data_ptr(), loss, entropy, correct, pred,
+                  ignore_mode, int(bool(write_grad)), grad_scale.data_ptr(),
+                  _lib.stream_of(logits))
+        return
     _lib.call("qlora_ce_rows", logits.data_ptr(), _lib.tag(logits.dtype), logits.stride(0), rows,
               vocab, target.data_ptr(), loss, entropy, correct, pred, ignore_mode,
               int(bool(write_grad)), float(grad_scale), _lib.stream_of(logits))
@@ -118,6 +129,7 @@ def run(hidden, weight, target, out, *, ignore_mode, chunk_rows, grad=None, grad
     head `weight` [V, H] (same dtype): per-row statistics into `out` (a RowResults of n rows)
     and, when `grad` (fp32 [n, H]) is given, grad[r] = dz[r] @ W for the rows r < grad_rows;
     rows from grad_rows on are left untouched in `grad`. `target` is int64 [n] on the device.
+    `grad_scale` is a number or a one-element fp32 device tensor (row_statistics).
     `chunk_rows`: an EngineRows lets groups grow to LOGITS_BUDGET; a plain int is the bound on
     the rows of live logits."""
     n, vocab = hidden.shape[0], weight.shape[0]

@@ -323,6 +323,18 @@ int qlora_ce_rows(void* logits, int logits_dtype, int64_t row_stride, int64_t n_
                   float grad_scale, ql_stream_t stream);
 
 /*
+ * qlora_ce_rows with grad_scale read from device memory (one fp32; may be NULL when
+ * write_grad is 0). Replaces the same code as qlora_ce_rows: the reference computes
+ * GRAD_GAIN / float(denominator) on the host (solution/cross_entropy.py:105-106), which
+ * waits for the GPU when the denominator is a count still on the device. With the scale
+ * formed on the device the host never waits; the values are the same.
+ */
+int qlora_ce_rows_scale_ptr(void* logits, int logits_dtype, int64_t row_stride,
+                            int64_t n_rows, int64_t vocab, const int64_t* target, float* loss,
+                            float* entropy, int32_t* correct, int64_t* pred, int ignore_mode,
+                            int write_grad, const float* grad_scale, ql_stream_t stream);
+
+/*
  * Dense GEMM on bf16/fp16 matrix cores (fp32 accumulation):
  *   C[M,N] = alpha * sum_k A[m,k] * B[n,k]  + beta * C[M,N]  + bias[n]
  * a_km = 0: A is [M,K] with row stride lda (k contiguous); a_km = 1: A is stored [K,M].

@@ -135,6 +135,9 @@ def test_rejected_arguments_return_codes(lib):
     # ce_rows: unknown ignore mode
     assert lib.qlora_ce_rows(fake, 2, 8, 2, 8, fake, fake, fake, None, None, 2, 0, 1.0,
                              None) == -1
+    # ce_rows with the scale in device memory: a gradient asked for without the scale
+    assert lib.qlora_ce_rows_scale_ptr(fake, 2, 8, 2, 8, fake, fake, fake, None, None, 1, 1,
+                                       None, None) == -1
     # gemm: fp32 inputs are not a matrix-core type; an operand not element-aligned; a leading
     # dimension shorter than the row
     assert lib.qlora_gemm(0, 0, 4, 4, 8, fake, 8, fake, 8, 0, fake, 4, 0, None, 1.0, 0.0,

@@ -45,6 +45,71 @@ def test_ce_rows_vs_oracle(V, dtype, ignore_mode):
     torch.testing.assert_close(zg.cpu().double(), dz_r.to(dtype).double(), rtol=tol, atol=tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_ce_rows_scale_from_device_memory_is_bit_identical(dtype):
+    """qlora_ce_rows_scale_ptr reads the gradient scale from device memory: same statistics
+    and the same dz bits as qlora_ce_rows given the value on the host."""
+    from hackathon_amd import _lib
+
+    g = torch.Generator().manual_seed(5)
+    R, V = 16, 9000
+    z = (torch.randn(R, V, generator=g) * 3).to(dtype).cuda()
+    t = torch.randint(0, V, (R,), generator=g).cuda()
+    t[3] = -100
+    scale = 65536.0 / 3001.0
+    outs = []
+    for dev_scale in (False, True):
+        zz = z.clone()
+        res = [torch.empty(R, device="cuda"), torch.empty(R, device="cuda"),
+               torch.empty(R, dtype=torch.int32, device="cuda"),
+               torch.empty(R, dtype=torch.int64, device="cuda")]
+        ptrs = [r.data_ptr() for r in res]
+        if dev_scale:
+            st = torch.tensor([scale], dtype=torch.float32, device="cuda")
+            _lib.call("qlora_ce_rows_scale_ptr", zz.data_ptr(), _lib.tag(dtype), V, R, V,
+                      t.data_ptr(), *ptrs, 1, 1, st.data_ptr(), _lib.stream_of(zz))
+        else:
+            _lib.call("qlora_ce_rows", zz.data_ptr(), _lib.tag(dtype), V, R, V, t.data_ptr(),
+                      *ptrs, 1, 1, scale, _lib.stream_of(zz))
+        outs.append([zz] + res)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("denominator", ["count", "num_items", "zero"])
+def test_fused_loss_with_a_device_denominator_matches_the_host_value(denominator):
+    """A denominator left on the GPU (the labelled count, or num_items_in_batch as a device
+    tensor) gives the same loss and hidden gradient bits as the same value passed as a Python
+    number, which the kernel receives from the host; a zero denominator zeroes the gradient
+    (solution/cross_entropy.py:105-106)."""
+    g = torch.Generator().manual_seed(2)
+    B, T, H, V = 2, 256, 512, 3000
+    hidden = torch.randn(B, T, H, generator=g).to(torch.bfloat16).cuda()
+    weight = (0.05 * torch.randn(V, H, generator=g)).to(torch.bfloat16).cuda()
+    labels = torch.randint(0, V, (B, T), generator=g).cuda()
+    labels[:, :40] = -100
+    if denominator == "zero":
+        labels[:] = -100
+    count = int((labels[:, 1:] != -100).sum())
+    results = []
+    for on_device in (True, False):
+        hg = hidden.clone().requires_grad_()
+        if denominator == "num_items":
+            items = torch.tensor(count + 17, device="cuda") if on_device else count + 17
+        else:
+            items = None if on_device else count
+        loss, _ = cross_entropy.fused_causal_lm_loss(hg, weight, labels, num_items_in_batch=items)
+        (loss * 3.0).backward()
+        results.append((loss.detach(), hg.grad))
+    (l_dev, g_dev), (l_host, g_host) = results
+    assert torch.equal(g_dev, g_host)
+    if denominator == "zero":
+        assert not torch.any(g_dev)
+        assert torch.isnan(l_dev) and torch.isnan(l_host)
+    else:
+        assert torch.equal(l_dev, l_host)
+
+
 @pytest.mark.parametrize("vocab", [1000, 4096, 9001])
 @pytest.mark.parametrize("with_num_items", [True, False])
 @pytest.mark.parametrize("matmul_dtype", [torch.float16, torch.bfloat16])
