@@ -18,6 +18,7 @@ include/qlora_gfx950.h, bound through ctypes in `_lib`).
   residual.py       Qwen2DecoderLayer with the residual adds fused into its two RMSNorms
   optim.py          FusedAdamW: AdamW over the adapters in one launch
   fused_proj.py     q/k/v (+ RoPE) and gate/up (+ SwiGLU) of a decoder layer as one LoRA GEMM each
+  adapter_packs.py  every adapter group of a model packed in one launch per model forward
 """
 
 PATCHES = ("rmsnorm", "rope", "cross_entropy", "lora", "attention", "residual")
@@ -30,7 +31,8 @@ def apply(include_example=True):
     "residual" and "fused_proj" have no counterpart in the reference, which leaves attention to
     torch's SDPA, the decoder layer's residual adds to transformers and runs every projection
     as its own layer. "fused_proj" goes last: its forwards fall back to the ones installed
-    before them."""
+    before them. "adapter_packs" scopes each Qwen2Model forward so that the fused layers' adapter
+    operands are packed in one launch."""
     from importlib import import_module
 
     for name in PATCHES:
@@ -47,3 +49,8 @@ def apply(include_example=True):
 
         patch_fused_proj()
         _applied.add("fused_proj")
+    if "adapter_packs" not in _applied:
+        from .adapter_packs import patch as patch_adapter_packs
+
+        patch_adapter_packs()
+        _applied.add("adapter_packs")

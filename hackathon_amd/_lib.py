@@ -115,6 +115,7 @@ _SIGNATURES = {
                         _c_ptr, _c_int, _c_ptr],
     "qlora_lora_pack_group": [_c_ptr, _c_int, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                               _c_int, _c_ptr],
+    "qlora_lora_pack_jobs": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_int, _c_ptr],
     "qlora_nf4_quantize": [_c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
                            _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr],
     "qlora_add_rmsnorm_fwd": [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr,
@@ -263,6 +264,14 @@ def lora_factors(items) -> ctypes.Array:
     for i, (a, b, s) in enumerate(items):
         arr[i] = LoraFactor(a.data_ptr(), b.data_ptr(), b.shape[0], float(s))
     return arr
+
+
+class LoraPackJob(ctypes.Structure):
+    """ql_lora_pack_job: one group of qlora_lora_pack_jobs (outputs as byte offsets)."""
+    _fields_ = [("A", ctypes.c_void_p * 4), ("B", ctypes.c_void_p * 4), ("n", ctypes.c_int64 * 4),
+                ("scaling", ctypes.c_float * 4), ("K", ctypes.c_int64), ("a16", ctypes.c_int64),
+                ("at_pad", ctypes.c_int64), ("bs_pad", ctypes.c_int64), ("bt", ctypes.c_int64),
+                ("count", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class Nf4Weight(ctypes.Structure):

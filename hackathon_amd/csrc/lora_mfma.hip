@@ -1338,13 +1338,14 @@ struct PackGroupArgs {
   int G;
 };
 
-template <int OT>
-__global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, int64_t K,
-                                                              typename Elem<OT>::T* __restrict__ a16,
-                                                              typename Elem<OT>::T* __restrict__ at,
-                                                              typename Elem<OT>::T* __restrict__ bs,
-                                                              typename Elem<OT>::T* __restrict__ bt,
-                                                              int pad) {
+// The work items t0, t0 + stride, ... of one group's packing; `p` may live in the kernel
+// arguments or in LDS (indexed by the item's slot either way).
+template <int OT, typename Args>
+QL_DEV void pack_group_items(const Args& p, int64_t K, typename Elem<OT>::T* __restrict__ a16,
+                             typename Elem<OT>::T* __restrict__ at,
+                             typename Elem<OT>::T* __restrict__ bs,
+                             typename Elem<OT>::T* __restrict__ bt, int pad, int64_t t0,
+                             int64_t stride) {
   const int64_t N = p.off[p.G];
   const int ch = pad / 8;
   const int64_t n_at = K * ch, n_bs = N * ch;
@@ -1355,8 +1356,7 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
     while (g + 1 < p.G && n >= p.off[g + 1]) ++g;
     return g;
   };
-  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
-       t += (int64_t)gridDim.x * 256) {
+  for (int64_t t = t0; t < total; t += stride) {
     if (t < n_at) {
       // at [K, pad]: column 16 g + r of row k holds A_g[r][k]
       const int64_t k = t / ch;
@@ -1409,6 +1409,50 @@ __global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, i
       for (int e = 0; e < 8; ++e) a16[i + e] = Elem<OT>::from_f32(p.A[g][(int64_t)r * K + col + e]);
     }
   }
+}
+
+template <int OT>
+__global__ __launch_bounds__(256) void lora_pack_group_kernel(PackGroupArgs p, int64_t K,
+                                                              typename Elem<OT>::T* __restrict__ a16,
+                                                              typename Elem<OT>::T* __restrict__ at,
+                                                              typename Elem<OT>::T* __restrict__ bs,
+                                                              typename Elem<OT>::T* __restrict__ bt,
+                                                              int pad) {
+  pack_group_items<OT>(p, K, a16, at, bs, bt, pad, (int64_t)blockIdx.x * 256 + threadIdx.x,
+                       (int64_t)gridDim.x * 256);
+}
+
+static_assert(sizeof(ql_lora_pack_job) == 160, "ql_lora_pack_job layout");
+
+// Many groups' packings in one launch: blockIdx.y selects the job (a descriptor in device
+// memory, copied to LDS once per workgroup), blockIdx.x strides over its work items.
+template <int OT>
+__global__ __launch_bounds__(256) void lora_pack_jobs_kernel(const ql_lora_pack_job* __restrict__ jobs,
+                                                             char* __restrict__ base, int pad) {
+  using T = typename Elem<OT>::T;
+  __shared__ PackGroupArgs p;
+  __shared__ int64_t sK, so[4];
+  if (threadIdx.x == 0) {
+    const ql_lora_pack_job& j = jobs[blockIdx.y];
+    p.G = j.count;
+    p.off[0] = 0;
+    for (int g = 0; g < kMaxGroup; ++g) {
+      const bool in = g < j.count;
+      p.A[g] = in ? j.A[g] : nullptr;
+      p.B[g] = in ? j.B[g] : nullptr;
+      p.scale[g] = in ? j.scaling[g] : 0.f;
+      p.off[g + 1] = p.off[g] + (in ? j.n[g] : 0);
+    }
+    sK = j.K;
+    so[0] = j.a16;
+    so[1] = j.at_pad;
+    so[2] = j.bs_pad;
+    so[3] = j.bt;
+  }
+  __syncthreads();
+  pack_group_items<OT>(p, sK, reinterpret_cast<T*>(base + so[0]), reinterpret_cast<T*>(base + so[1]),
+                       reinterpret_cast<T*>(base + so[2]), reinterpret_cast<T*>(base + so[3]), pad,
+                       (int64_t)blockIdx.x * 256 + threadIdx.x, (int64_t)gridDim.x * 256);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2561,4 +2605,25 @@ extern "C" int qlora_lora_pack_group(const ql_lora_factor* factors, int count, i
   }
   return launch_pack_group(p, K, out_dtype, a16, at_pad, bs_pad, bt, pad,
                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qlora_lora_pack_jobs(const ql_lora_pack_job* jobs, int njobs, int64_t max_items,
+                                    void* out_base, int out_dtype, int pad, ql_stream_t stream) {
+  if (njobs < 0 || njobs > 65535 || max_items < 0 || pad < kRank || pad % 8) return QL_EINVAL;
+  if (njobs == 0 || max_items == 0) return QL_OK;
+  if (!jobs || !out_base) return QL_EINVAL;
+  if (!ql_aligned(out_base, 16)) return QL_EALIGN;
+  if (out_dtype != QL_BF16 && out_dtype != QL_F16) return QL_EDTYPE;
+  // about 8 items a thread for the largest job, at most 256 workgroups a job
+  int64_t gx = (max_items + 256 * 8 - 1) / (256 * 8);
+  gx = gx < 1 ? 1 : (gx > 256 ? 256 : gx);
+  const dim3 grid((unsigned)gx, (unsigned)njobs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (out_dtype == QL_BF16)
+    hipLaunchKernelGGL((lora_pack_jobs_kernel<QL_BF16>), grid, dim3(256), 0, s, jobs,
+                       (char*)out_base, pad);
+  else
+    hipLaunchKernelGGL((lora_pack_jobs_kernel<QL_F16>), grid, dim3(256), 0, s, jobs,
+                       (char*)out_base, pad);
+  return ql_launch_status();
 }

@@ -47,7 +47,7 @@ import math
 
 import torch
 
-from . import _common, _lib, attention, lora, nf4, rope, swiglu
+from . import _common, _lib, adapter_packs, attention, lora, nf4, rope, swiglu
 from . import gemm as _gemm
 
 _PAD = 64  # padded LoRA K segment: up to 4 adapters of rank 16
@@ -145,7 +145,7 @@ def group_forward(x2, specs, ab, seeds=None):
     M, K = x2.shape
     G = len(specs)
     offs = _offsets(specs)
-    a16, at, bs, bt = _gemm.lora_pack_group(
+    a16, at, bs, bt = adapter_packs.pack_group(
         [(ab[2 * g], ab[2 * g + 1], specs[g].scaling) for g in range(G)], dt, _PAD)
     u = torch.empty((M, _PAD), dtype=dt, device=dev)
     ut = _t_buffer(16 * G, M, dt, dev)
@@ -429,7 +429,7 @@ class LoraMLP(torch.autograd.Function):
         y, (at, bt, ut), drop = group_forward(x2, specs, ab[:4],
                                               seeds[:2] if specs[0].p > 0 else None)
         n, N = specs[0].n, dspec.n
-        a16_d, at_d, bs_d, bt_d = _gemm.lora_pack(ab[4], ab[5], dspec.scaling, dt, _PAD)
+        a16_d, at_d, bs_d, bt_d = adapter_packs.pack(ab[4], ab[5], dspec.scaling, dt, _PAD)
         h = torch.empty((M, n), dtype=dt, device=dev)
         u_d = torch.empty((M, _PAD), dtype=dt, device=dev)
         ut_d = _gemm.lora_t_buffer(M, dt, dev)

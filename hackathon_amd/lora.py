@@ -24,7 +24,7 @@ import math
 
 import torch
 
-from . import _common, _lib
+from . import _common, _lib, adapter_packs
 from . import gemm as _gemm
 
 TORCH_DROPOUT_RNG = False
@@ -252,7 +252,7 @@ class LoraNF4Linear(torch.autograd.Function):
         M, K = x2.shape
         N = int(quant_state.shape[0])
         # A, A^T|0, s*B|0 and B^T in the compute dtype, one launch (kept for the backward)
-        a16, at, bs, bt = _gemm.lora_pack(a_weight, b_weight, scaling, dt, _PAD)
+        a16, at, bs, bt = adapter_packs.pack(a_weight, b_weight, scaling, dt, _PAD)
         u = torch.empty((M, _PAD), dtype=dt, device=x2.device)
         ut = _gemm.lora_t_buffer(M, dt, x2.device)                     # u^T, for dB
         bits = None

@@ -731,6 +731,34 @@ int qlora_lora_pack_group(const ql_lora_factor* factors, int count, int64_t K, i
                           ql_stream_t stream);
 
 /*
+ * Many qlora_lora_pack_group calls in one launch: every adapter group of a model packed at
+ * once (the 112 per-projection packs of a 28-layer step become one launch).
+ * `jobs` is an array of `njobs` descriptors in DEVICE memory (the library reads it on the
+ * GPU only, so it cannot check it: the caller guarantees 1 <= count <= 4, pad >= 16 count,
+ * K % 8 == 0, A/B pointers as for qlora_lora_pack_group, and outputs 16-B aligned and
+ * disjoint). Job j writes its four outputs at out_base + its byte offsets, with the values
+ * qlora_lora_pack_group writes. `max_items` is the largest job's work-item count,
+ * (K + N) (pad / 8) + N + 2 count K with N = sum n; it sizes the grid.
+ * Replaces: the per-projection casts of solution/lora.py:172 (no reference counterpart for
+ * packing several layers at once).
+ */
+typedef struct ql_lora_pack_job {
+  const float* A[4];   /* lora_A weights [16, K], fp32 row-major; unused slots ignored */
+  const float* B[4];   /* lora_B weights [n_g, 16], fp32 row-major */
+  int64_t n[4];        /* output features of each adapter */
+  float scaling[4];
+  int64_t K;           /* input features, shared by the group */
+  int64_t a16;         /* byte offsets from out_base: a16 [16 count, K] */
+  int64_t at_pad;      /* [K, pad] */
+  int64_t bs_pad;      /* [N, pad] */
+  int64_t bt;          /* [16 count, N] */
+  int32_t count;       /* adapters in the group, 1..4 */
+  int32_t reserved;
+} ql_lora_pack_job;
+int qlora_lora_pack_jobs(const ql_lora_pack_job* jobs, int njobs, int64_t max_items,
+                         void* out_base, int out_dtype, int pad, ql_stream_t stream);
+
+/*
  * Causal flash attention forward with grouped-query heads (HQ % HK == 0), head_dim 128:
  *   o[b, hq, s, :] = sum_t softmax_t(scale * q[b,hq,s,:] . k[b,hk,t,:], t <= s) v[b,hk,t,:]
  *   lse[b, hq, s] = log sum_{t <= s} exp(scale * q . k)    (fp32 [B, HQ, S]; may be NULL)

@@ -135,6 +135,14 @@ def test_rejected_arguments_return_codes(lib):
     # ce_rows: unknown ignore mode
     assert lib.qlora_ce_rows(fake, 2, 8, 2, 8, fake, fake, fake, None, None, 2, 0, 1.0,
                              None) == -1
+    # pack jobs: negative count, a pad below one slot, no descriptors, a misaligned output
+    # base, an fp32 output; no jobs is a no-op
+    assert lib.qlora_lora_pack_jobs(fake, -1, 8, fake, 2, 64, None) == -1
+    assert lib.qlora_lora_pack_jobs(fake, 1, 8, fake, 2, 12, None) == -1
+    assert lib.qlora_lora_pack_jobs(None, 1, 8, fake, 2, 64, None) == -1
+    assert lib.qlora_lora_pack_jobs(fake, 1, 8, P(0x1008), 2, 64, None) == -3
+    assert lib.qlora_lora_pack_jobs(fake, 1, 8, fake, 0, 64, None) == -2
+    assert lib.qlora_lora_pack_jobs(None, 0, 0, None, 2, 64, None) == 0
     # ce_rows with the scale in device memory: a gradient asked for without the scale
     assert lib.qlora_ce_rows_scale_ptr(fake, 2, 8, 2, 8, fake, fake, fake, None, None, 1, 1,
                                        None, None) == -1
