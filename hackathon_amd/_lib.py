@@ -65,7 +65,8 @@ _SIGNATURES = {
                                       _c_i64, _c_ptr, _c_ptr, _c_i64, _c_f32, _c_f32, _c_f32,
                                       _c_f32, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64,
                                       _c_ptr, _c_ptr, _c_ptr, _c_f32, _c_ptr, _c_ptr, _c_i64,
-                                      _c_f32, _c_f32, _c_ptr, _c_i64, _c_ptr],
+                                      _c_f32, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr,
+                                      _c_i64, _c_ptr],
     "qlora_lora_dropout_scale": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64,
                                  _c_u64, _c_f32, _c_f32, _c_ptr],
     "qlora_lora_scaled_add": [_c_ptr, _c_int, _c_i64, _c_ptr, _c_int, _c_i64, _c_ptr, _c_int,

@@ -338,7 +338,29 @@ struct SwDrop {
   float scale;      // 1 / (1 - p)
   uint8_t* bits;    // 8 x 8 blocks (ql_philox.h)
   int64_t gs;       // their group stride
+  // backward only: the down adapter's masked rank-16 term added to the incoming gradient,
+  // grad + scale * keep (du[:, :16] a) (a [16, K]); du null: none
+  const uint16_t* add_du;
+  int64_t add_ldu;
+  const uint16_t* add_a;
+  int64_t add_lda;
 };
+
+// v_mfma_f32_16x16x16 (one rank-16 product per output), the instruction of the masked adds in
+// lora.hip: D[i][j] = sum_r a[i][r] b[r][j], lane l supplying a[l % 16][4 (l / 16) .. +3] and
+// b[4 (l / 16) .. +3][l % 16] and holding D[4 (l / 16) + e][l % 16] in element e.
+template <int DT> QL_DEV f32x4_t mfma_k16(const uint2& a, const uint2& b);
+template <> QL_DEV f32x4_t mfma_k16<QL_BF16>(const uint2& a, const uint2& b) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4i16, a),
+                                                  __builtin_bit_cast(v4i16, b),
+                                                  f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+}
+template <> QL_DEV f32x4_t mfma_k16<QL_F16>(const uint2& a, const uint2& b) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b),
+                                              f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+}
 
 constexpr int kSwRows = 32;                 // rows per workgroup (two 16-row MFMA groups)
 constexpr int kSwK = 256;                   // k per tile
@@ -531,6 +553,13 @@ __global__ __launch_bounds__(256) void swiglu_bwd_down_kernel(
 // transposed like the gradients. The three arrays take one LDS buffer (with a second barrier
 // per tile before it is refilled) and the Y fragments move from registers to LDS, so two
 // workgroups (at most 256 registers a lane) still fit on a CU.
+// DROP with dr.add_du: the incoming gradient first gets the down adapter's term through its
+// dropout mask, grad + scale * keep (du a), rounded to the input type: the sum
+// qlora_lora_up_masked_add writes, from the same products (one v_mfma_f32_16x16x16 per 16 x 16
+// block, C = 0, the a fragments staged in LDS once per workgroup) and the same fp32 steps, so
+// the gradients are those of the separate add followed by this kernel, bit for bit. The
+// products of a tile go through the (not yet written) gradient arrays of the LDS buffer,
+// with two more barriers a tile.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
@@ -565,7 +594,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
   // DA: the Y fragments live in LDS (16 rows of 256 columns per adapter, rows padded like the
   // tiles), not in registers, which keeps the kernel at two waves per SIMD
   constexpr int YBYTES = DA ? 2 * 16 * kSlLdsRow : 0;
-  __shared__ __attribute__((aligned(16))) char lds[NBUF * BUF + YBYTES];
+  // DROP: the a fragments of the fused masked add, [16-column block][lane], 8 B each
+  constexpr int AFBYTES = DROP ? (kSlCols / 16) * 64 * 8 : 0;
+  constexpr int kTermRow = 4 * kSlCols + 16;  // bytes per row of a tile's fp32 products
+  static_assert(!DROP || kSlRows * kTermRow <= 2 * kSlLdsArr, "products fit the gradient arrays");
+  __shared__ __attribute__((aligned(16))) char lds[NBUF * BUF + YBYTES + AFBYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t k0 = (int64_t)blockIdx.x * kSlCols;
@@ -596,6 +629,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
       yv[g] = ld16(reinterpret_cast<const char*>(yq + (kg < K ? kg : k0)), oy);
     }
   }
+  char* const aflds = lds + NBUF * BUF + YBYTES;
+  const bool madd = DROP && dr.add_du != nullptr;  // uniform
+  if constexpr (DROP) {
+    if (madd) {  // lane (r, q) of block t: a[4 q + e][k0 + 16 t + r], e = 0 .. 3 (zero past K)
+#pragma unroll
+      for (int j = 0; j < (kSlCols / 16) * 64 / 256; ++j) {
+        const int e8 = tid + 256 * j;
+        const int t = e8 >> 6, l = e8 & 63;
+        const int64_t col = k0 + 16 * t + (l & 15);
+        uint16_t hv[4] = {0, 0, 0, 0};
+        if (col < K) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) hv[e] = dr.add_a[(int64_t)(4 * (l >> 4) + e) * dr.add_lda + col];
+        }
+        *reinterpret_cast<uint2*>(aflds + 8 * e8) =
+            make_uint2(hv[0] | (uint32_t)hv[1] << 16, hv[2] | (uint32_t)hv[3] << 16);
+      }
+      __syncthreads();
+    }
+  }
   f32x4_t acc_db[4][NA];  // [column block 4 wave + i][adapter (, dA)]
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -605,18 +658,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
   const int lds_r = (lane & 15) * kSlLdsRow + 16 * (lane >> 4);         // + 16 rg rows + 64 g
   const int lds_t = (8 * (lane >> 4) + ((lane >> 2) & 3)) * kSlLdsRow + 8 * (lane & 3);
   int buf = 0;
+  // DROP with the masked add: lane's row 16 rg + lane % 16 of the tile at row m, columns
+  // 4 (lane / 16) .. +3 of du (the second operand of the products)
+  auto load_dv = [&](int64_t m) {
+    const int64_t rd = m + 16 * rg + (lane & 15) < M ? m + 16 * rg + (lane & 15) : M - 1;
+    return *reinterpret_cast<const uint2*>(dr.add_du + rd * dr.add_ldu + 4 * (lane >> 4));
+  };
+  uint2 dv_next = make_uint2(0, 0);
+  if constexpr (DROP) {
+    if (madd && r0 < r1) dv_next = load_dv(r0);
+  }
   for (int64_t m0 = r0; m0 < r1; m0 += kSlRows) {
     // rows m0 + lr + 8 h; a row past M (the last tile) works on row M - 1 and stores the
     // bits row M - 1's owner stores, and is left out of both products
-    uint32_t ogr[4], oga[4], oup[4], odg[4], odu[4];
+    uint32_t ogr[4], oga[4], oup[4];
+    auto row_of = [&](int h) { return m0 + lr + 8 * h < M ? lr + 8 * h : (int)(M - 1 - m0); };
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const int64_t rs = m0 + lr + 8 * h < M ? lr + 8 * h : M - 1 - m0;
+      const int64_t rs = row_of(h);
       ogr[h] = (uint32_t)((rs * ldgr + kx) * 2);
       oga[h] = (uint32_t)((rs * ldga + kx) * 2);
       oup[h] = (uint32_t)((rs * ldup + kx) * 2);
-      odg[h] = (uint32_t)((rs * lddg + kx) * 2);
-      odu[h] = (uint32_t)((rs * lddu + kx) * 2);
     }
     const char* grb = reinterpret_cast<const char*>(GR + m0 * ldgr);
     const char* gab = reinterpret_cast<const char*>(GA + m0 * ldga);
@@ -625,7 +687,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     char* dub = reinterpret_cast<char*>(DU + m0 * lddu);
     uint4 vgr[4], vga[4], vup[4], uq[NA];
     uint32_t kbyte[4];  // DROP: the keep byte of each of this thread's rows at columns kx ..
+    const uint2 dv = dv_next;  // the masked add's du operand, loaded a tile ahead
     if constexpr (DROP) {
+      if (madd && m0 + kSlRows < r1) dv_next = load_dv(m0 + kSlRows);
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
         const int64_t rowc = m0 + lr + 8 * h < M ? m0 + lr + 8 * h : M - 1;
@@ -658,6 +722,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     }
     char* lb = lds + buf * BUF;
     if (NBUF == 1 && m0 != r0) __syncthreads();  // the previous tile's reads are done
+    if constexpr (DROP) {
+      if (madd) {
+        // wave w: rows 16 rg .. +15, column blocks 8 qd .. +7 of the tile's products
+#pragma unroll
+        for (int tt = 0; tt < kSlCols / 32; ++tt) {
+          const int t = (kSlCols / 32) * qd + tt;
+          const uint2 af = *reinterpret_cast<const uint2*>(aflds + 8 * (t * 64 + lane));
+          const f32x4_t pr = mfma_k16<IT>(af, dv);
+          *reinterpret_cast<f32x4_t*>(lb + (16 * rg + (lane & 15)) * kTermRow +
+                                      4 * (16 * t + 4 * (lane >> 4))) = pr;
+        }
+        __syncthreads();
+        {
+#pragma clang fp contract(off)  // scale * kept, then the add: two roundings, as the masked add
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const float* tp =
+              reinterpret_cast<const float*>(lb + row_of(h) * kTermRow + 4 * (kx - k0));
+          const f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(tp);
+          const f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(tp + 4);
+          const float pv[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+          float v[8];
+          Vec8<IT>::unpack(vgr[h], v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float kept = -0.0f + ((kbyte[h] >> e) & 1u ? pv[e] : -0.0f);
+            v[e] = v[e] + dr.scale * kept;
+          }
+          vgr[h] = Vec8<IT>::pack(v);
+        }
+        }
+        __syncthreads();  // every product is read before the gradients overwrite them
+      }
+    }
     bool fast = true;  // one test of the tile's gate values (ql_swiglu.h)
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -675,10 +773,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
         ql_swiglu_bwd8_as<decltype(fast_tag)::value>(gr8, ga8, up8, dg8, du8);
         const uint4 pdg = Vec8<IT>::pack(dg8);
         const uint4 pdu = Vec8<IT>::pack(du8);
+        // the store offsets are formed here, not kept from the loads (registers)
+        const uint32_t rsu = (uint32_t)row_of(h), kxu = (uint32_t)kx;
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, pdg),
-                                    reinterpret_cast<u32x4v*>(dgb + odg[h]));
+                                    reinterpret_cast<u32x4v*>(dgb + 2u * (rsu * (uint32_t)lddg + kxu)));
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4v, pdu),
-                                    reinterpret_cast<u32x4v*>(dub + odu[h]));
+                                    reinterpret_cast<u32x4v*>(dub + 2u * (rsu * (uint32_t)lddu + kxu)));
         *reinterpret_cast<uint4*>(lb + lds_w + 8 * h * kSlLdsRow) = pdg;
         *reinterpret_cast<uint4*>(lb + kSlLdsArr + lds_w + 8 * h * kSlLdsRow) = pdu;
         if constexpr (DA) {
@@ -2131,13 +2231,22 @@ extern "C" int qlora_swiglu_bwd_lora_dropout(
     const void* ut_up, int64_t ldut, float alpha_gate, float alpha_up, float beta_gate,
     float beta_up, int dtype, void* du, int64_t ldo, int out_cols, void* du_t, int64_t ldt,
     float* db_gate, float* db_up, const void* ud_t, float beta_down, float* da_down,
-    const uint8_t* bits, int64_t bits_group_stride, float p, float scale, void* workspace,
+    const uint8_t* bits, int64_t bits_group_stride, float p, float scale, const void* du_add,
+    int64_t ld_du_add, const void* a_add, int64_t ld_a_add, void* workspace,
     int64_t workspace_bytes, ql_stream_t stream) {
   if (rows < 0 || cols < 0 || workspace_bytes < 0) return QL_EINVAL;
   SwDrop dr{};
   int st = swiglu_drop_args(0, p, scale, const_cast<uint8_t*>(bits), bits_group_stride, cols,
                             false, &dr);
   if (st != QL_OK) return st;
+  if (du_add) {
+    if (!a_add || ld_du_add < kRank || ld_a_add < cols) return QL_EINVAL;
+    if (!ql_aligned(du_add, 8) || ld_du_add % 4) return QL_EALIGN;
+    dr.add_du = static_cast<const uint16_t*>(du_add);
+    dr.add_ldu = ld_du_add;
+    dr.add_a = static_cast<const uint16_t*>(a_add);
+    dr.add_lda = ld_a_add;
+  }
   if (rows == 0) return QL_OK;
   if (!grad || !gate || !up || !dgate || !dup || !bt_gate || !bt_up || !ut_gate || !ut_up ||
       !du || !db_gate || !db_up || !workspace || !ud_t || !da_down)

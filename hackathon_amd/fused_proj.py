@@ -412,10 +412,10 @@ class LoraMLP(torch.autograd.Function):
     With LoRA dropout (`seeds`: the gate, up and down adapters' seeds, None where that p is 0)
     the gate/up group drops x per adapter as GateUpSwiGLU does, and the down adapter's input is
     its own mask of h: the forward kernel draws it and keeps it as bits
-    (qlora_swiglu_fwd_lora_down_dropout, u_d from the dropped h), dh takes the adapter term
-    through qlora_lora_up_masked_add instead of the GEMM's second K segment, and the backward
-    kernel drops its recomputed h with the same bits for dA_d
-    (qlora_swiglu_bwd_lora_dropout)."""
+    (qlora_swiglu_fwd_lora_down_dropout, u_d from the dropped h); in the backward the adapter
+    term of dh goes through that mask inside the SwiGLU kernel instead of the GEMM's second K
+    segment (the sum qlora_lora_up_masked_add would write, bit for bit), and the kernel drops its
+    recomputed h with the same bits for dA_d (qlora_swiglu_bwd_lora_dropout)."""
 
     @staticmethod
     def forward(ctx, x, specs, dspec, seeds, *ab):
@@ -486,10 +486,9 @@ class LoraMLP(torch.autograd.Function):
         dh = torch.empty((M, n), dtype=dt, device=dev)
         if bits_d is None:
             _gemm.gemm_nt_cat(dy, wt, du_d, at_d, dh)
-        else:  # the adapter term through its mask of h
+        else:  # the adapter term goes through its mask of h inside the SwiGLU backward
             _gemm.gemm_nt_cat(dy, wt, None, None, dh)
-            lora.up_masked_add(dh, du_d, a16_d, bits_d, dspec.p)
-        del wt, du_d
+        del wt
         db_d = _gemm.lora_wgrad(ut_d, dy, alpha=s_d) if need[9] else None
         g = torch.empty((M, 2 * n), dtype=dt, device=dev)
         du = torch.empty((M, _PAD), dtype=dt, device=dev)
@@ -498,8 +497,9 @@ class LoraMLP(torch.autograd.Function):
         db_g, db_u, da_d = swiglu.swiglu_bwd_lora(
             dh, y[:, :n], y[:, n:], g[:, :n], g[:, n:], bt[:16, :n], bt[16:32, n:], ut[:16], ut[16:32],
             gate_s.scaling, up_s.scaling, gate_s.scaling, up_s.scaling, du, dut, ud_t=dut_d,
-            bits_down=bits_d, p_down=dspec.p)
-        del dh
+            bits_down=bits_d, p_down=dspec.p,
+            du_add=None if bits_d is None else du_d, a_add=None if bits_d is None else a16_d)
+        del dh, du_d
         dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[4:8],
                                    du_dut=(du, dut), db_given=[db_g, db_u], drop=drop)
         grads = grads + [da_d if need[8] else None, db_d]

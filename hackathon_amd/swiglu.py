@@ -86,7 +86,7 @@ def swiglu_bwd_lora_down(grad, gate, up, dgate, dup, bt_gate, bt_up, alpha_gate,
 
 def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, alpha_gate,
                     alpha_up, beta_gate, beta_up, du, du_t=None, ud_t=None, beta_down=1.0,
-                    bits_down=None, p_down=0.0):
+                    bits_down=None, p_down=0.0, du_add=None, a_add=None):
     """swiglu_bwd_lora_down plus both adapters' lora_B gradients in the same pass
     (qlora_swiglu_bwd_lora): returns fp32 (db_gate, db_up) [cols, 16] with
     db_gate = beta_gate dgate^T ut_gate^T and db_up = beta_up dup^T ut_up^T, where ut_* [16, rows]
@@ -94,7 +94,10 @@ def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, 
     [16, rows] of the adapter of the layer that reads h = silu(gate) up) also that adapter's
     lora_A gradient da_down = beta_down ud_t h [16, cols], h recomputed on chip: returns
     (db_gate, db_up, da_down). With `bits_down` (swiglu_fwd_lora_down's keep bits for dropout
-    p_down) h in that product is the adapter's dropped input (qlora_swiglu_bwd_lora_dropout)."""
+    p_down) h in that product is the adapter's dropped input (qlora_swiglu_bwd_lora_dropout),
+    and with `du_add` [rows, >= 16] and `a_add` [16, cols] (that adapter's du and A) the
+    gradient differentiated is grad plus that adapter's masked input gradient, the sum
+    lora.up_masked_add would leave in grad (grad itself is not written)."""
     _lib.require_rows(gate.dtype, grad=grad, gate=gate, up=up, dgate=dgate, dup=dup,
                       bt_gate=bt_gate, bt_up=bt_up, ut_gate=ut_gate, ut_up=ut_up, du=du,
                       du_t=du_t, ud_t=ud_t)
@@ -121,9 +124,13 @@ def swiglu_bwd_lora(grad, gate, up, dgate, dup, bt_gate, bt_up, ut_gate, ut_up, 
     if bits_down is None:
         _lib.call("qlora_swiglu_bwd_lora", *args, _lib.ptr(ws), ws_bytes, _lib.stream_of(gate))
     else:
+        if du_add is not None:
+            _lib.require_rows(gate.dtype, du_add=du_add, a_add=a_add)
         _lib.call("qlora_swiglu_bwd_lora_dropout", *args, bits_down.data_ptr(),
-                  bits_down.stride(0), float(p_down), 1.0 / (1.0 - p_down), _lib.ptr(ws),
-                  ws_bytes, _lib.stream_of(gate))
+                  bits_down.stride(0), float(p_down), 1.0 / (1.0 - p_down), _lib.ptr(du_add),
+                  du_add.stride(0) if du_add is not None else 0, _lib.ptr(a_add),
+                  a_add.stride(0) if a_add is not None else 0, _lib.ptr(ws), ws_bytes,
+                  _lib.stream_of(gate))
     return (db_gate, db_up) if ud_t is None else (db_gate, db_up, da_down)
 
 

@@ -637,8 +637,15 @@ int qlora_swiglu_bwd_lora(const void* grad, int64_t ldgr, const void* gate, int6
  * * scale rounded to dtype), keep from the bits qlora_swiglu_fwd_lora_down_dropout stored
  * (0 < p < 1; bits 8-B aligned, bits_group_stride >= cols and a multiple of 8):
  *   da_down[c, k] = beta_down * sum_m ud_t[c, m] * keep(m, k) * (h[m, k] * scale)
+ * With du_add (may be NULL), the gradient the SwiGLU backward differentiates is first
+ *   grad[m, k] + scale * keep(m, k) * sum_r du_add[m, r] * a_add[r, k]      (r < 16)
+ * rounded to dtype: the down adapter's input gradient through its dropout mask, what
+ * qlora_lora_up_masked_add adds to grad in place (the same bits), taken on chip instead; grad
+ * itself is not written. du_add [rows, >= 16] (8-B aligned, ld_du_add % 4 == 0), a_add
+ * [16, cols] (ld_a_add >= cols) in dtype.
  * Replaces: as qlora_swiglu_bwd_lora, with the lora_A gradient of the down projection taken on
- * DropoutCast's output (solution/lora.py:84-93,172).
+ * DropoutCast's output (solution/lora.py:84-93,172) and, with du_add, DropoutCast.backward on
+ * that adapter's input gradient summed into grad (solution/lora.py:90-93).
  */
 int qlora_swiglu_bwd_lora_dropout(const void* grad, int64_t ldgr, const void* gate, int64_t ldg,
                                   const void* up, int64_t ldu, void* dgate, int64_t lddg,
@@ -650,8 +657,9 @@ int qlora_swiglu_bwd_lora_dropout(const void* grad, int64_t ldgr, const void* ga
                                   void* du_t, int64_t ldt, float* db_gate, float* db_up,
                                   const void* ud_t, float beta_down, float* da_down,
                                   const uint8_t* bits, int64_t bits_group_stride, float p,
-                                  float scale, void* workspace, int64_t workspace_bytes,
-                                  ql_stream_t stream);
+                                  float scale, const void* du_add, int64_t ld_du_add,
+                                  const void* a_add, int64_t ld_a_add, void* workspace,
+                                  int64_t workspace_bytes, ql_stream_t stream);
 
 /*
  * SwiGLU forward fused with the down-projection of its output by the adapter of the layer

@@ -629,3 +629,24 @@ def test_swiglu_lora_dropout_kernels(rows, cols, dtype):
     exact_a = 1.5 * (udd @ xdd)
     bound_a = 1.5 * 4 * 2.0**-22 * rows * xdd.abs().max() * udd.abs().max()
     assert da1.shape == (16, cols) and torch.all((da1.double() - exact_a).abs() <= bound_a)
+
+    # the down adapter's input gradient through its mask, added on chip: every result equals the
+    # separate masked add (lora.up_masked_add on a copy of dh) followed by the same call
+    dud = (torch.randn(rows, 64, device="cuda", generator=g) * 0.5).to(dtype)
+    dh_sum = dh.clone()
+    lora.up_masked_add(dh_sum, dud, a, bits, p)
+    dh_before = dh.clone()
+    outs = []
+    for fused in (False, True):
+        buf = torch.empty(rows, 2 * cols, dtype=dtype, device="cuda")
+        du = torch.full((rows, 64), 5.0, dtype=dtype, device="cuda")
+        dut = gemm.lora_t_buffer(rows, dtype, "cuda", rows=32)
+        res = swiglu.swiglu_bwd_lora(dh if fused else dh_sum, gate, up, buf[:, :cols],
+                                     buf[:, cols:], bt[:, :cols], bt[:, cols:], utg[:16],
+                                     utg[16:32], 2.0, 0.5, 2.0, 0.5, du, dut, ud_t=udt,
+                                     beta_down=1.5, bits_down=bits, p_down=p,
+                                     du_add=dud if fused else None, a_add=a if fused else None)
+        outs.append((buf, du, dut) + tuple(res))
+    for x0, x1 in zip(*outs):
+        assert torch.equal(x0, x1)
+    assert torch.equal(dh, dh_before)  # the sum is taken on chip, dh is not written
