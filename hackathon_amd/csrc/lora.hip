@@ -129,6 +129,11 @@ struct SlotBits {
 constexpr int kMaskedCols = 64;      // columns per wave (four 16-column blocks)
 constexpr int kMaskedPitch = 64 + 4;  // floats per LDS row (padding spreads the 16-B stores)
 
+// Each wave stages its products in its own LDS area, and the LDS accesses of one wave execute
+// in program order, so the exchange between its lanes needs no workgroup barrier, only that the
+// compiler keeps the reads after the writes (and the next writes after the reads).
+QL_DEV void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+
 template <int DT, int G>
 __device__ __forceinline__ void up_masked_add_body(
     uint16_t* __restrict__ dx, int64_t dx_rs, const uint16_t* __restrict__ du, int64_t du_rs,
@@ -140,7 +145,7 @@ __device__ __forceinline__ void up_masked_add_body(
   const int wave = threadIdx.x >> 6;
   const int fr = lane & 15, fq = lane >> 4;
   const int64_t k0 = ((int64_t)blockIdx.x * (kThreads / 64) + wave) * kMaskedCols;
-  const bool wave_on = k0 < K;  // wave-uniform; every wave still meets the barriers
+  const bool wave_on = k0 < K;  // wave-uniform
   // A^T fragments of block t, adapter g: A[16 g + 4 fq + i][k0 + 16 t + fr], i = 0 .. 3 (zero
   // past K: those products are never added)
   uint2 af[G][4];
@@ -198,7 +203,7 @@ __device__ __forceinline__ void up_masked_add_body(
         const f32x4_t p = mfma16<DT>(af[g][t], dv);
         *reinterpret_cast<f32x4_t*>(&prod[wave][fr * kMaskedPitch + 16 * t + 4 * fq]) = p;
       }
-      __syncthreads();  // the products are in LDS
+      wave_lds_order();  // the products are in this wave's LDS area
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const float* pr = &prod[wave][(hr + 8 * h) * kMaskedPitch + c8];
@@ -209,7 +214,7 @@ __device__ __forceinline__ void up_masked_add_body(
 #pragma unroll
         for (int j = 0; j < 8; ++j) sum[h][j] = sum[h][j] + ((b >> j) & 1u ? pv[j] : -0.0f);
       }
-      __syncthreads();  // every read of these products is done before the next writes
+      wave_lds_order();  // every read of these products is done before the next writes
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
