@@ -99,6 +99,9 @@ _SIGNATURES = {
     "qlora_gemm_nt_cat": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr,
                           _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr, _c_i64, _c_int, _c_ptr, _c_f32,
                           _c_ptr, _c_i64, _c_ptr],
+    "qlora_gemm_nt_cat_residual": [_c_i64, _c_i64, _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64,
+                                   _c_i64, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_int, _c_ptr,
+                                   _c_i64, _c_int, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_lora_down": [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr,
                         _c_i64, _c_int, _c_int, _c_f32, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr],
     "qlora_mfma_probe": [_c_ptr, _c_int, _c_int, _c_i64, _c_int, _c_ptr, _c_ptr, _c_ptr],

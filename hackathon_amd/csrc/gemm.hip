@@ -352,11 +352,12 @@ extern "C" int64_t qlora_gemm_nt_cat_workspace_size(int64_t M, int64_t N, int64_
          (int64_t)sizeof(float);
 }
 
-extern "C" int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
-                                 const void* B, int64_t ldb, int64_t K2, const void* A2,
-                                 int64_t lda2, const void* B2, int64_t ldb2, int in_dtype, void* C,
-                                 int64_t ldc, int c_dtype, const void* bias, float alpha,
-                                 void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
+static int gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                       const void* B, int64_t ldb, int64_t K2, const void* A2, int64_t lda2,
+                       const void* B2, int64_t ldb2, int in_dtype, void* C, int64_t ldc,
+                       int c_dtype, const void* bias, float alpha, const void* residual,
+                       int64_t ld_residual, void* workspace, int64_t workspace_bytes,
+                       ql_stream_t stream) {
   if (M < 0 || N < 0 || K < 0 || K2 < 0 || workspace_bytes < 0) return QL_EINVAL;
   if (in_dtype != QL_BF16 && in_dtype != QL_F16) return QL_EDTYPE;
   if (!ql_valid_dtype(c_dtype)) return QL_EDTYPE;
@@ -373,7 +374,38 @@ extern "C" int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A,
   int splits = ql_gemm_nt_auto_splits(M, N, K);
   const int64_t need = ql_gemm_nt_workspace_floats(M, N, splits) * (int64_t)sizeof(float);
   if (need > workspace_bytes || !workspace || !ql_aligned(workspace, 16)) splits = 1;
+  if (residual) {
+    if (c_dtype == QL_F32) return QL_EDTYPE;
+    if (ld_residual < N) return QL_ESHAPE;
+    if (!ql_aligned(residual, 16) || ld_residual % 8) return QL_EALIGN;
+    // the residual is read while the output is written: no overlap
+    const char* r0 = static_cast<const char*>(residual);
+    const char* c0 = static_cast<const char*>(C);
+    const int64_t rbytes = ((M - 1) * ld_residual + N) * 2, cbytes = ((M - 1) * ldc + N) * 2;
+    if (r0 < c0 + cbytes && c0 < r0 + rbytes) return QL_EINVAL;
+  }
   return ql_gemm_nt2(in_dtype, c_dtype, M, N, K, A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc,
                      bias, alpha, 0.f, splits, static_cast<float*>(workspace),
-                     static_cast<hipStream_t>(stream));
+                     static_cast<hipStream_t>(stream), residual, ld_residual);
+}
+
+extern "C" int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                                 const void* B, int64_t ldb, int64_t K2, const void* A2,
+                                 int64_t lda2, const void* B2, int64_t ldb2, int in_dtype, void* C,
+                                 int64_t ldc, int c_dtype, const void* bias, float alpha,
+                                 void* workspace, int64_t workspace_bytes, ql_stream_t stream) {
+  return gemm_nt_cat(M, N, K, A, lda, B, ldb, K2, A2, lda2, B2, ldb2, in_dtype, C, ldc, c_dtype,
+                     bias, alpha, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int qlora_gemm_nt_cat_residual(int64_t M, int64_t N, int64_t K, const void* A,
+                                          int64_t lda, const void* B, int64_t ldb, int64_t K2,
+                                          const void* A2, int64_t lda2, const void* B2,
+                                          int64_t ldb2, int in_dtype, void* C, int64_t ldc,
+                                          int c_dtype, const void* residual, int64_t ld_residual,
+                                          void* workspace, int64_t workspace_bytes,
+                                          ql_stream_t stream) {
+  if (!residual) return QL_EINVAL;
+  return gemm_nt_cat(M, N, K, A, lda, B, ldb, K2, A2, lda2, B2, ldb2, in_dtype, C, ldc, c_dtype,
+                     nullptr, 1.0f, residual, ld_residual, workspace, workspace_bytes, stream);
 }

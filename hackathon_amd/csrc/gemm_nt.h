@@ -23,8 +23,11 @@ int ql_gemm_nt(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const
                float alpha, float beta, int splits, float* ws, hipStream_t s);
 
 // C = alpha * (A @ B^T + A2 @ B2^T) (+ beta C) (+ bias): a second k-contiguous segment with
-// K2 % 64 == 0 columns (A2 [M, K2], B2 [N, K2], same alignment rules; K2 = 0: none).
+// K2 % 64 == 0 columns (A2 [M, K2], B2 [N, K2], same alignment rules; K2 = 0: none). With
+// `residual` (16-bit C only, beta 0; [M, N] in C's type, 16-B aligned rows, ld % 8 == 0) the
+// rounded result plus the residual, rounded again.
 int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
                 int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
                 const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
-                float alpha, float beta, int splits, float* ws, hipStream_t s);
+                float alpha, float beta, int splits, float* ws, hipStream_t s,
+                const void* residual = nullptr, int64_t ld_residual = 0);

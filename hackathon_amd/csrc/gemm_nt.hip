@@ -568,12 +568,24 @@ QL_DEV void mma_step_pipe_nf4(f32x16_t (&acc)[4][4], Frags<8>& f0, char* __restr
 // r % 4, against bank conflicts), then the threads store whole rows, 16 B per lane (a wave
 // covers two rows of a 256-wide tile: 1 KiB of full 128-B lines per instruction). The arithmetic is the
 // direct path's: alpha * acc, plus the bias, rounded once.
+// An optional residual R added to the finished output: out = round(round(alpha * acc
+// (+ bias)) + R), R [M, N] in the 16-bit output type, the two roundings of the product's own
+// store followed by a separate `R + out` (a decoder layer's `residual + mlp(x)`).
+struct Residual {
+  const uint16_t* p;  // null: none
+  int64_t ld;
+};
+
+template <int OT> QL_DEV float add_residual(float v, uint16_t r) {
+  return Elem<OT>::to_f32(Elem<OT>::from_f32(v)) + Elem<OT>::to_f32(r);
+}
+
 template <int IT, int OT, int NB>
 QL_DEV void tile_store_via_lds(const f32x16_t (&acc)[Layout<NB>::BI][Layout<NB>::BJ],
                                char* __restrict__ smem, typename Elem<OT>::T* __restrict__ C,
                                int64_t ldc, const uint16_t* __restrict__ bias, int64_t m0,
                                int64_t n0, int64_t M, int64_t N, float alpha, int wm, int wn,
-                               int lane) {
+                               int lane, const Residual& res) {
 #pragma clang fp contract(off)  // alpha * acc, then + bias: two roundings, as the direct path
   using L = Layout<NB>;
   using T = typename Elem<OT>::T;
@@ -610,13 +622,26 @@ QL_DEV void tile_store_via_lds(const f32x16_t (&acc)[Layout<NB>::BI][Layout<NB>:
     const int r = idx / kChunks, q = idx % kChunks;
     const int64_t row = m0 + r, col = n0 + 8 * q;
     if (row >= M || col >= N) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(smem + r * kRow + ((q ^ (r & kSwz)) * 16));
+    uint4 v = *reinterpret_cast<const uint4*>(smem + r * kRow + ((q ^ (r & kSwz)) * 16));
     T* cp = C + row * ldc + col;
     if (col + 8 <= N) {
+      if (res.p) {  // the rounded product plus the residual, rounded again
+        float pv[8], rv[8];
+        Vec8<OT>::unpack(v, pv);
+        Vec8<OT>::unpack(*reinterpret_cast<const uint4*>(res.p + row * res.ld + col), rv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = pv[e] + rv[e];
+        v = Vec8<OT>::pack(pv);
+      }
       *reinterpret_cast<uint4*>(cp) = v;
     } else {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-      for (int e = 0; e < 8 && col + e < N; ++e) cp[e] = (T)(w[e >> 1] >> (16 * (e & 1)));
+      for (int e = 0; e < 8 && col + e < N; ++e) {
+        T o = (T)(w[e >> 1] >> (16 * (e & 1)));
+        if (res.p)
+          o = Elem<OT>::from_f32(Elem<OT>::to_f32(o) + Elem<OT>::to_f32(res.p[row * res.ld + col + e]));
+        cp[e] = o;
+      }
     }
   }
 }
@@ -634,7 +659,7 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
                     typename Elem<OT>::T* __restrict__ C, int64_t ldc,
                     float* __restrict__ ws, const uint16_t* __restrict__ bias, int64_t M,
                     int64_t N, int64_t K, int64_t k_per_split, float alpha, float beta,
-                    bool vec_out, Nf4Operand nf4op) {
+                    bool vec_out, Nf4Operand nf4op, Residual res) {
   using L = Layout<NB>;
   constexpr bool kNf4 = BQ != kBDense;
   static_assert(!kNf4 || NB == 8, "the NF4 B operand takes 256-row tiles: one row per thread");
@@ -762,7 +787,8 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
   // a time (see tile_store_via_lds); the values are those of the direct path below.
   if constexpr (!PARTIAL && OT != QL_F32) {
     if (beta == 0.f && ((uintptr_t)C & 15) == 0 && (ldc & 7) == 0) {
-      tile_store_via_lds<IT, OT, NB>(acc, smem, C, ldc, bias, m0, n0, M, N, alpha, wm, wn, lane);
+      tile_store_via_lds<IT, OT, NB>(acc, smem, C, ldc, bias, m0, n0, M, N, alpha, wm, wn, lane,
+                                     res);
       return;
     }
   }
@@ -801,6 +827,11 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
           if (bias)
             for (int e = 0; e < 4; ++e)
               if (col + e < N) v[e] += Elem<IT>::to_f32(bias[col + e]);
+          if constexpr (OT != QL_F32) {
+            if (res.p)
+              for (int e = 0; e < 4; ++e)
+                if (col + e < N) v[e] = add_residual<OT>(v[e], res.p[row * res.ld + col + e]);
+          }
           const bool vec = vec_out && col + 3 < N;
           if (vec) {
             if constexpr (OT == QL_F32) {
@@ -821,12 +852,14 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
   }
 }
 
-// out[m, n] = alpha * sum_s ws[s][m][n] (+ beta * out) (+ bias[n]), summed in split order.
+// out[m, n] = alpha * sum_s ws[s][m][n] (+ beta * out) (+ bias[n]), summed in split order
+// (+ the residual, after rounding).
 template <int IT, int OT>
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, int splits,
                                                      typename Elem<OT>::T* __restrict__ C,
                                                      int64_t ldc, const uint16_t* __restrict__ bias,
-                                                     int64_t M, int64_t N, float alpha, float beta) {
+                                                     int64_t M, int64_t N, float alpha, float beta,
+                                                     Residual res) {
   const int64_t total = M * N;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
@@ -846,6 +879,9 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ w
     auto* cp = C + row * ldc + col;
     if (beta != 0.f) v += beta * Elem<OT>::to_f32(*cp);
     if (bias) v += Elem<IT>::to_f32(bias[col]);
+    if constexpr (OT != QL_F32) {
+      if (res.p) v = add_residual<OT>(v, res.p[row * res.ld + col]);
+    }
     *cp = Elem<OT>::from_f32(v);
   }
 }
@@ -854,7 +890,7 @@ template <int IT, int OT, int NB, int BQ = kBDense>
 int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
            const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
            int64_t M, int64_t N, int64_t K, float alpha, float beta, int splits, float* ws,
-           hipStream_t s, const Nf4Operand& nf4op = Nf4Operand{}) {
+           hipStream_t s, const Nf4Operand& nf4op = Nf4Operand{}, Residual res = Residual{}) {
   using T = typename Elem<OT>::T;
   constexpr int BN = bn_of<NB>();
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
@@ -869,12 +905,14 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
       hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, true, BQ>), dim3((unsigned)tiles, 1),
                          dim3(kThreads), 0, s, (const uint16_t*)A, lda, (const uint16_t*)B, ldb,
                          (const uint16_t*)A2, lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc,
-                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out, nf4op);
+                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out, nf4op,
+                         res);
     else
       hipLaunchKernelGGL((gemm_nt_kernel<IT, OT, false, NB, false, BQ>), dim3((unsigned)tiles, 1),
                          dim3(kThreads), 0, s, (const uint16_t*)A, lda, (const uint16_t*)B, ldb,
                          (const uint16_t*)A2, lda2, (const uint16_t*)B2, ldb2, K2, (T*)C, ldc,
-                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out, nf4op);
+                         nullptr, (const uint16_t*)bias, M, N, K, K, alpha, beta, vec_out, nf4op,
+                         res);
     return ql_launch_status();
   }
   if (al8)
@@ -882,20 +920,22 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
                        dim3((unsigned)tiles, (unsigned)nsplit), dim3(kThreads), 0, s,
                        (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
                        (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0, ws,
-                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false, nf4op);
+                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false, nf4op,
+                       Residual{});
   else
     hipLaunchKernelGGL((gemm_nt_kernel<IT, QL_F32, true, NB, false, BQ>),
                        dim3((unsigned)tiles, (unsigned)nsplit), dim3(kThreads), 0, s,
                        (const uint16_t*)A, lda, (const uint16_t*)B, ldb, (const uint16_t*)A2, lda2,
                        (const uint16_t*)B2, ldb2, K2, (float*)nullptr, (int64_t)0, ws,
-                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false, nf4op);
+                       (const uint16_t*)nullptr, M, N, K, kps, 1.0f, 0.0f, false, nf4op,
+                       Residual{});
   int st = ql_launch_status();
   if (st != QL_OK) return st;
   const int64_t total = M * N;
   int64_t grid = (total + 255) / 256;
   if (grid > 256 * 16) grid = 256 * 16;
   hipLaunchKernelGGL((splitk_reduce<IT, OT>), dim3((unsigned)grid), dim3(256), 0, s, ws, nsplit,
-                     (T*)C, ldc, (const uint16_t*)bias, M, N, alpha, beta);
+                     (T*)C, ldc, (const uint16_t*)bias, M, N, alpha, beta, res);
   return ql_launch_status();
 }
 
@@ -973,8 +1013,13 @@ int ql_gemm_nf4_auto_splits(int64_t M, int64_t N, int64_t K) {
 int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, const void* A,
                 int64_t lda, const void* B, int64_t ldb, const void* A2, int64_t lda2,
                 const void* B2, int64_t ldb2, int64_t K2, void* C, int64_t ldc, const void* bias,
-                float alpha, float beta, int splits, float* ws, hipStream_t s) {
+                float alpha, float beta, int splits, float* ws, hipStream_t s,
+                const void* residual, int64_t ld_residual) {
   if (splits > 1 && !ws) return QL_EINVAL;
+  if (residual && (c_dtype == QL_F32 || beta != 0.f || ((uintptr_t)residual & 15) ||
+                   (ld_residual & 7) || ld_residual < N))
+    return QL_EINVAL;
+  const Residual res{static_cast<const uint16_t*>(residual), ld_residual};
   if (K2 < 0 || K2 % BK || K <= 0 || K % BK) return QL_EINVAL;
   // the kernel loads the second segment in its prologue: at most kPrologueSteps steps; the
   // sum is symmetric in the two segments, so a short first segment may take that place
@@ -991,7 +1036,8 @@ int ql_gemm_nt2(int in_dtype, int c_dtype, int64_t M, int64_t N, int64_t K, cons
 #define QL_GEMM_NT_LAUNCH(ITC, NBC)                                                            \
   QL_DISPATCH_DTYPE(c_dtype, OT,                                                               \
                     return (launch<ITC, OT, NBC>(A, lda, B, ldb, A2, lda2, B2, ldb2, K2, C, ldc, \
-                                                 bias, M, N, K, alpha, beta, splits, ws, s)))
+                                                 bias, M, N, K, alpha, beta, splits, ws, s,     \
+                                                 Nf4Operand{}, res)))
   if (in_dtype == QL_BF16) {
     if (narrow) {
       QL_GEMM_NT_LAUNCH(QL_BF16, 7);

@@ -409,6 +409,11 @@ class LoraMLP(torch.autograd.Function):
 
     h is not kept for the backward: it is neither read back for u_d nor stored for dA_d.
 
+    `residual` (None, or [..., N] in x's dtype, contiguous, 16-B aligned) is the decoder
+    layer's stream the output is added to (`residual + mlp(x)`, modeling_qwen2.py:297): the
+    down GEMM adds it in its store (qlora_gemm_nt_cat_residual, the same two roundings), and
+    its gradient is dY itself.
+
     With LoRA dropout (`seeds`: the gate, up and down adapters' seeds, None where that p is 0)
     the gate/up group drops x per adapter as GateUpSwiGLU does, and the down adapter's input is
     its own mask of h: the forward kernel draws it and keeps it as bits
@@ -418,7 +423,7 @@ class LoraMLP(torch.autograd.Function):
     recomputed h with the same bits for dA_d (qlora_swiglu_bwd_lora_dropout)."""
 
     @staticmethod
-    def forward(ctx, x, specs, dspec, seeds, *ab):
+    def forward(ctx, x, specs, dspec, seeds, residual, *ab):
         K = x.shape[-1]
         x2 = x.reshape(-1, K)
         if not x2.is_contiguous():
@@ -437,11 +442,19 @@ class LoraMLP(torch.autograd.Function):
                                              p=dspec.p, seed=seeds[2] or 0)
         out = torch.empty((M, N), dtype=dt, device=dev)
         bias = None if dspec.bias is None else dspec.bias.to(dt)
+        res2 = None if residual is None else residual.view(M, N)
         if nf4.use_fused_gemm(h, dspec.qs, dspec.packed, a2=u_d):  # W_d dequantised in-GEMM
             nf4.gemm_nf4(h, dspec.packed, dspec.qs, out=out, a2=u_d, b2=bs_d, bias=bias)
+            if res2 is not None:
+                out = res2 + out
         else:
             w = nf4.dequantize_nf4(dspec.packed, dspec.qs, dt)
-            _gemm.gemm_nt_cat(h, w, u_d, bs_d, out, bias=bias)
+            if res2 is not None and bias is None:
+                _gemm.gemm_nt_cat(h, w, u_d, bs_d, out, residual=res2)
+            else:
+                _gemm.gemm_nt_cat(h, w, u_d, bs_d, out, bias=bias)
+                if res2 is not None:
+                    out = res2 + out
             del w
         del h, u_d
         saved = [x2, y, at, bt, ut, at_d, bt_d, ut_d]
@@ -471,8 +484,9 @@ class LoraMLP(torch.autograd.Function):
         dt, dev = x2.dtype, x2.device
         M = x2.shape[0]
         n, N = specs[0].n, dspec.n
-        # x, specs, dspec, seeds, A_gate, B_gate, A_up, B_up, A_d, B_d
+        # x, specs, dspec, seeds, residual, A_gate, B_gate, A_up, B_up, A_d, B_d
         need = ctx.needs_input_grad
+        dres = dout if need[4] else None
         dy = dout.reshape(M, N)
         if dy.dtype != dt:
             dy = dy.to(dt)
@@ -489,7 +503,7 @@ class LoraMLP(torch.autograd.Function):
         else:  # the adapter term goes through its mask of h inside the SwiGLU backward
             _gemm.gemm_nt_cat(dy, wt, None, None, dh)
         del wt
-        db_d = _gemm.lora_wgrad(ut_d, dy, alpha=s_d) if need[9] else None
+        db_d = _gemm.lora_wgrad(ut_d, dy, alpha=s_d) if need[10] else None
         g = torch.empty((M, 2 * n), dtype=dt, device=dev)
         du = torch.empty((M, _PAD), dtype=dt, device=dev)
         dut = _t_buffer(32, M, dt, dev)
@@ -500,11 +514,11 @@ class LoraMLP(torch.autograd.Function):
             bits_down=bits_d, p_down=dspec.p,
             du_add=None if bits_d is None else du_d, a_add=None if bits_d is None else a16_d)
         del dh, du_d
-        dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[4:8],
+        dx, grads = group_backward(g, x2, at, bt, ut, specs, need[0], need[5:9],
                                    du_dut=(du, dut), db_given=[db_g, db_u], drop=drop)
-        grads = grads + [da_d if need[8] else None, db_d]
+        grads = grads + [da_d if need[9] else None, db_d]
         grads = [None if gr is None else gr.to(t_) for gr, t_ in zip(grads, ctx.ab_dtypes)]
-        return (None if dx is None else dx.view(ctx.shape)), None, None, None, *grads
+        return (None if dx is None else dx.view(ctx.shape)), None, None, None, dres, *grads
 
 
 def _group(layers, x):
@@ -576,9 +590,17 @@ def fused_attention(module, hidden_states, position_embeddings, attention_mask,
     return module.o_proj(attn.reshape(B, S, -1)), None
 
 
-def fused_mlp(module, x):
+def _residual_ok(residual, x, N):
+    return (residual.dtype == x.dtype and residual.shape == (*x.shape[:-1], N)
+            and residual.is_contiguous() and residual.data_ptr() % 16 == 0 and N % 8 == 0
+            and residual.device == x.device)
+
+
+def fused_mlp(module, x, residual=None):
     """Qwen2MLP.forward as LoraMLP(x) when the down projection is a fused-kernel 4-bit LoRA
-    layer too, else down_proj(GateUpSwiGLU(x)); None when the gate/up group does not fit."""
+    layer too, else down_proj(GateUpSwiGLU(x)); None when the gate/up group does not fit.
+    With `residual`: residual + that output (the decoder layer's last add), taken into the
+    down GEMM when LoraMLP can."""
     if getattr(getattr(module, "config", None), "hidden_act", "silu") != "silu":
         return None
     if not (_common.on_gpu(x) and x.dtype in (torch.bfloat16, torch.float16)
@@ -599,8 +621,11 @@ def fused_mlp(module, x):
         seeds = seeds + ((lora._Seeds.next() if dspec.p > 0 else None),)
         if all(s_ is None for s_ in seeds):
             seeds = None
-        return LoraMLP.apply(x, tuple(specs), dspec, seeds, *ab, a_d, b_d)
-    return module.down_proj(GateUpSwiGLU.apply(x, tuple(specs), _seeds(specs), *ab))
+        if residual is not None and not _residual_ok(residual, x, dspec.n):
+            return residual + LoraMLP.apply(x, tuple(specs), dspec, seeds, None, *ab, a_d, b_d)
+        return LoraMLP.apply(x, tuple(specs), dspec, seeds, residual, *ab, a_d, b_d)
+    out = module.down_proj(GateUpSwiGLU.apply(x, tuple(specs), _seeds(specs), *ab))
+    return out if residual is None else residual + out
 
 
 def patch():

@@ -143,13 +143,27 @@ def frozen_as(w: torch.Tensor, dtype) -> torch.Tensor:
 
 def gemm_nt_cat(a: torch.Tensor, b: torch.Tensor, a2: torch.Tensor | None,
                 b2: torch.Tensor | None, out: torch.Tensor, bias: torch.Tensor | None = None,
-                alpha: float = 1.0) -> torch.Tensor:
+                alpha: float = 1.0, residual: torch.Tensor | None = None) -> torch.Tensor:
     """out = alpha * (a @ b^T + a2 @ b2^T) (+ bias) in one NT GEMM over the concatenated K
-    (qlora_gemm_nt_cat). All operands 2-D, unit stride along K, K and K2 multiples of 64."""
+    (qlora_gemm_nt_cat). All operands 2-D, unit stride along K, K and K2 multiples of 64.
+    With `residual` ([M, N], out's 16-bit dtype; no bias, alpha 1) out = residual + the
+    product, each rounded as `residual + (a @ b^T + a2 @ b2^T)` rounds them
+    (qlora_gemm_nt_cat_residual)."""
     M, K = a.shape
     N = b.shape[0]
     K2 = 0 if a2 is None else a2.shape[1]
     ws, ws_bytes = _lib.workspace("qlora_gemm_nt_cat_workspace_size", M, N, K, device=out.device)
+    if residual is not None:
+        if bias is not None or alpha != 1.0 or residual.dtype != out.dtype:
+            raise ValueError("a residual takes no bias, alpha 1 and out's dtype")
+        if residual.shape != (M, N) or residual.stride(-1) != 1:
+            raise ValueError(f"residual must be [{M}, {N}] with unit column stride")
+        _lib.call("qlora_gemm_nt_cat_residual", M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(),
+                  b.stride(0), K2, _lib.ptr(a2), a2.stride(0) if a2 is not None else 0,
+                  _lib.ptr(b2), b2.stride(0) if b2 is not None else 0, _lib.tag(a.dtype),
+                  out.data_ptr(), out.stride(0), _lib.tag(out.dtype), residual.data_ptr(),
+                  residual.stride(0), _lib.ptr(ws), ws_bytes, _lib.stream_of(out))
+        return out
     _lib.call("qlora_gemm_nt_cat", M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
               K2, _lib.ptr(a2), a2.stride(0) if a2 is not None else 0, _lib.ptr(b2),
               b2.stride(0) if b2 is not None else 0, _lib.tag(a.dtype), out.data_ptr(),

@@ -11,8 +11,10 @@ forward with the same computation on two fused operations:
                                                                      x's dtype as torch's add
 whose backward is one kernel: dh = rmsnorm_bwd(dy) + d(residual output), the gradient of the
 stream's two uses summed in fp32 and rounded once (autograd rounds each term, then adds).
-The final `h + mlp` stays a plain add. The reference leaves the layer to transformers; this
-is the "RMSNorm + residual-add" fusion around modeling_qwen2.py:280-297.
+The final `h + mlp` is added in the MLP's down-projection GEMM when the MLP takes the fused
+LoRA path (fused_proj.LoraMLP with a residual, the same roundings as the add), else it stays
+a plain add. The reference leaves the layer to transformers; this is the "RMSNorm +
+residual-add" fusion around modeling_qwen2.py:280-297.
 """
 
 from __future__ import annotations
@@ -108,6 +110,29 @@ def supported(layer, hidden_states):
             and layer.post_attention_layernorm.weight.dtype == hidden_states.dtype)
 
 
+def _plain_call(module):
+    """Whether calling `module` runs its class's forward and nothing else: no hooks of its own
+    or global ones, no forward set on the instance, the stock Module.__call__."""
+    from torch.nn.modules import module as mm
+
+    hooks = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")
+    glob = ("_global_forward_hooks", "_global_forward_pre_hooks", "_global_backward_hooks",
+            "_global_backward_pre_hooks")
+    return (type(module).__call__ is torch.nn.Module.__call__ and "forward" not in vars(module)
+            and not any(getattr(module, h, None) for h in hooks)
+            and not any(getattr(mm, g, None) for g in glob))
+
+
+def _mlp_with_residual(mlp, x, h):
+    """h + mlp(x) with the add taken into the MLP's last GEMM (fused_proj.fused_mlp with a
+    residual), or None when the MLP's call is not the fused forward alone."""
+    if not (getattr(type(mlp).forward, "_solution_fused_proj", False) and _plain_call(mlp)):
+        return None
+    from . import fused_proj
+
+    return fused_proj.fused_mlp(mlp, x, residual=h)
+
+
 def patch():
     """Install the fused-norm Qwen2DecoderLayer.forward (unsupported calls run the original)."""
     from transformers.models.qwen2 import modeling_qwen2 as m
@@ -134,7 +159,8 @@ def patch():
             x = ln2(h)
         else:
             h, x = residual_rmsnorm(residual, attn, ln2.weight, ln2.variance_epsilon)
-        return h + self.mlp(x)
+        out = _mlp_with_residual(self.mlp, x, h)
+        return h + self.mlp(x) if out is None else out
 
     forward._solution_patch = True
     forward._original = original

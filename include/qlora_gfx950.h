@@ -458,6 +458,23 @@ int qlora_gemm_nt_cat(int64_t M, int64_t N, int64_t K, const void* A, int64_t ld
                       ql_stream_t stream);
 
 /*
+ * qlora_gemm_nt_cat (no bias, alpha 1) with a residual added to the output in the GEMM's
+ * store: C = R + (A B^T + A2 B2^T), the product rounded to c_dtype and the sum rounded again,
+ * so C equals qlora_gemm_nt_cat followed by `R + C` bit for bit. R [M, N] in c_dtype (bf16 or
+ * fp16; QL_EDTYPE for fp32), 16-B aligned, ld_residual >= N a multiple of 8 (QL_EALIGN
+ * otherwise); R must not overlap C (QL_EINVAL).
+ * Replaces: the decoder layer's final `residual + mlp(x)` (transformers
+ * modeling_qwen2.py:297, the Qwen2 layer the reference's patched modules run in) taken into
+ * the down projection's GEMM (solution/nf4.py:102 with solution/lora.py:172).
+ */
+int qlora_gemm_nt_cat_residual(int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                               const void* B, int64_t ldb, int64_t K2, const void* A2,
+                               int64_t lda2, const void* B2, int64_t ldb2, int in_dtype, void* C,
+                               int64_t ldc, int c_dtype, const void* residual,
+                               int64_t ld_residual, void* workspace, int64_t workspace_bytes,
+                               ql_stream_t stream);
+
+/*
  * The 4-bit base GEMM with its NF4 weight dequantised inside the GEMM, on the way into LDS:
  *   C[M,N] = alpha * (A[M,K] W[N,K]^T + A2[M,K2] B2[N,K2]^T) (+ bias[n]),  C in in_dtype,
  * where W is the weight qlora_nf4_dequant produces from (packed, absmax, nested, code2,

@@ -157,6 +157,17 @@ def test_rejected_arguments_return_codes(lib):
     # cat gemm: the two K segments may not both exceed 128 (the short one is loaded up front)
     assert lib.qlora_gemm_nt_cat(256, 256, 256, fake, 256, fake, 256, 192, fake, 192, fake, 192,
                                  2, fake, 256, 2, None, 1.0, None, 0, None) == -4
+    # cat gemm with a residual: none given; an fp32 output; a misaligned residual; a residual
+    # row shorter than N; a residual overlapping the output
+    other = P(0x100000)
+    args = (256, 256, 256, fake, 256, fake, 256, 0, None, 0, None, 0, 2)
+    assert lib.qlora_gemm_nt_cat_residual(*args, fake, 256, 2, None, 256, None, 0, None) == -1
+    assert lib.qlora_gemm_nt_cat_residual(*args, fake, 256, 0, other, 256, None, 0, None) == -2
+    assert lib.qlora_gemm_nt_cat_residual(*args, fake, 256, 2, P(0x100008), 256, None, 0,
+                                          None) == -3
+    assert lib.qlora_gemm_nt_cat_residual(*args, fake, 256, 2, other, 128, None, 0, None) == -4
+    assert lib.qlora_gemm_nt_cat_residual(*args, fake, 256, 2, P(0x1000 + 512), 256, None, 0,
+                                          None) == -1
     # rank-16 LoRA kernels: 1 to 4 adapters per call; the workspace query is 0 outside that
     assert lib.qlora_lora_down(fake, 64, fake, 64, 16, 64, 0, 2, fake, 64, 64, 2, 1.0, None, 0,
                                None, 0, None) == -1

@@ -135,7 +135,7 @@ def test_lora_mlp_matches_separate_layers(seq):
 
     specs, ab = fused_proj._group(layers[:2], x)
     dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
-    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
+    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, None, *ab, a_d, b_d)
     (out2.float() * w).sum().backward()
     assert out2.shape == ref.shape and _rel(out2, ref) < 4e-3
     got_g = [x.grad] + [p.grad for p in params]
@@ -155,11 +155,11 @@ def test_lora_mlp_partial_grads_and_no_grad():
     w = torch.randn(2, 64, 512, device="cuda", generator=g).to(torch.bfloat16)
     specs, ab = fused_proj._group((mlp.gate_proj, mlp.up_proj), x)
     dspec, a_d, b_d = fused_proj.lora_spec(mlp.down_proj, x)
-    out = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
+    out = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, None, *ab, a_d, b_d)
     (out.float() * w).sum().backward()
     ref = [x.grad.clone()] + [t.grad.clone() for t in ab]
     with torch.no_grad():
-        out0 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
+        out0 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, None, *ab, a_d, b_d)
     assert torch.equal(out0, out)
     x.grad = None
     for t in ab:
@@ -168,7 +168,7 @@ def test_lora_mlp_partial_grads_and_no_grad():
     a_d.requires_grad_(False)
     b_d.requires_grad_(False)
     try:
-        out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, *ab, a_d, b_d)
+        out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, None, None, *ab, a_d, b_d)
         (out2.float() * w).sum().backward()
         assert a_d.grad is None and b_d.grad is None
         got = [x.grad] + [t.grad for t in ab]
@@ -285,7 +285,7 @@ def test_lora_mlp_with_dropout_matches_separate_layers(seq):
     assert specs[0].p == dspec.p == 0.05
     _reseed(5)
     seeds = fused_proj._seeds(specs) + (lora._Seeds.next(),)
-    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, seeds, *ab, a_d, b_d)
+    out2 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, seeds, None, *ab, a_d, b_d)
     (out2.float() * w).sum().backward()
     assert out2.shape == ref.shape and _rel(out2, ref) < 4e-3
     got_g = [x.grad] + [p.grad for p in params]
@@ -295,7 +295,7 @@ def test_lora_mlp_with_dropout_matches_separate_layers(seq):
     _reseed(5)
     seeds = fused_proj._seeds(specs) + (lora._Seeds.next() + 1,)
     with torch.no_grad():
-        out3 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, seeds, *ab, a_d, b_d)
+        out3 = fused_proj.LoraMLP.apply(x, tuple(specs), dspec, seeds, None, *ab, a_d, b_d)
     assert _rel(out3, ref) > 1e-4
 
 
