@@ -853,13 +853,70 @@ void gemm_nt_kernel(const uint16_t* __restrict__ A, int64_t lda, const uint16_t*
 }
 
 // out[m, n] = alpha * sum_s ws[s][m][n] (+ beta * out) (+ bias[n]), summed in split order
-// (+ the residual, after rounding).
+// (+ the residual, after rounding); each step rounded to fp32, no contraction, as the GEMM's
+// own epilogue. VW = 4: four consecutive elements of a row per thread (16-bit outputs, N and
+// ldc multiples of 4, C 8-B aligned), loaded as float4 from the 16-B aligned workspace.
+template <int IT, int OT>
+QL_DEV uint16_t splitk_out(float s, float alpha, float beta, const uint16_t* cp,
+                           const uint16_t* bias_col, const uint16_t* res_el) {
+#pragma clang fp contract(off)
+  float v = alpha * s;
+  if (beta != 0.f) v += beta * Elem<OT>::to_f32(*cp);
+  if (bias_col) v += Elem<IT>::to_f32(*bias_col);
+  if (res_el) v = add_residual<OT>(v, *res_el);
+  return Elem<OT>::from_f32(v);
+}
+
+template <int IT, int OT>
+__global__ __launch_bounds__(256) void splitk_reduce4(const float* __restrict__ ws, int splits,
+                                                      uint16_t* __restrict__ C, int64_t ldc,
+                                                      const uint16_t* __restrict__ bias,
+                                                      int64_t M, int64_t N, float alpha,
+                                                      float beta, Residual res) {
+  const int64_t total = M * N, groups = total / 4;
+  for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < groups;
+       g += (int64_t)gridDim.x * 256) {
+    const int64_t i = 4 * g;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    int z = 0;
+    for (; z + 4 <= splits; z += 4) {  // four partial vectors in flight, added in split order
+      float4 w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const float4*>(ws + (z + j) * total + i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s[0] += w[j].x;
+        s[1] += w[j].y;
+        s[2] += w[j].z;
+        s[3] += w[j].w;
+      }
+    }
+    for (; z < splits; ++z) {
+      const float4 w = *reinterpret_cast<const float4*>(ws + z * total + i);
+      s[0] += w.x;
+      s[1] += w.y;
+      s[2] += w.z;
+      s[3] += w.w;
+    }
+    const int64_t row = i / N, col = i - row * N;
+    uint16_t* cp = C + row * ldc + col;
+    uint16_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = splitk_out<IT, OT>(s[e], alpha, beta, cp + e, bias ? bias + col + e : nullptr,
+                                res.p ? res.p + row * res.ld + col + e : nullptr);
+    *reinterpret_cast<uint2*>(cp) =
+        make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+  }
+}
+
 template <int IT, int OT>
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, int splits,
                                                      typename Elem<OT>::T* __restrict__ C,
                                                      int64_t ldc, const uint16_t* __restrict__ bias,
                                                      int64_t M, int64_t N, float alpha, float beta,
                                                      Residual res) {
+#pragma clang fp contract(off)
   const int64_t total = M * N;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
@@ -932,6 +989,16 @@ int launch(const void* A, int64_t lda, const void* B, int64_t ldb, const void* A
   int st = ql_launch_status();
   if (st != QL_OK) return st;
   const int64_t total = M * N;
+  if constexpr (OT != QL_F32) {
+    if (N % 4 == 0 && ldc % 4 == 0 && ((uintptr_t)C & 7) == 0) {
+      int64_t grid = (total / 4 + 255) / 256;
+      if (grid > 256 * 16) grid = 256 * 16;
+      hipLaunchKernelGGL((splitk_reduce4<IT, OT>), dim3((unsigned)grid), dim3(256), 0, s, ws,
+                         nsplit, (uint16_t*)C, ldc, (const uint16_t*)bias, M, N, alpha, beta,
+                         res);
+      return ql_launch_status();
+    }
+  }
   int64_t grid = (total + 255) / 256;
   if (grid > 256 * 16) grid = 256 * 16;
   hipLaunchKernelGGL((splitk_reduce<IT, OT>), dim3((unsigned)grid), dim3(256), 0, s, ws, nsplit,
